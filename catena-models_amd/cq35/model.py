@@ -1,0 +1,254 @@
+"""Host-side mirror of catena-models' Model / Session API (src/model.rs) over
+the cq35 C ABI. Method names, argument meaning and error behaviour follow the
+reference:
+
+  Model.session(capacity)                 src/model.rs:192-206
+  Session.prefill_next_token(tokens)      src/model.rs:484-492
+  Session.decode_next_token(token)        src/model.rs:494-502
+  Session.append_next_token(tokens)       src/model.rs:449-456
+  Session.{prefill,decode,append}_logits  src/model.rs:458-482
+  Session.into_checkpoint()               src/model.rs:431-446
+  Model.resume_checkpoint(checkpoint)     src/model.rs:209-246
+  Model.logits / Model.next_token         src/model.rs:187-190
+
+A failed step leaves the session unusable, like the reference's `state.take()`
+(src/model.rs:711-730).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import CQ35Error, check
+from .config import CConfig, preset, to_c
+
+
+class Model:
+    def __init__(self, handle: int, cfg: dict):
+        self._h = ctypes.c_void_p(handle)
+        self.cfg = dict(cfg)
+
+    # -- construction ---------------------------------------------------
+    @classmethod
+    def synthetic(cls, cfg, seed: int = 0) -> "Model":
+        """Weights generated on the device by the library's seeded generator."""
+        cfg = preset(cfg) if isinstance(cfg, str) else dict(cfg)
+        lib = _lib.load()
+        out = ctypes.c_void_p()
+        c = to_c(cfg)
+        check(lib.cq35_model_create_synthetic(ctypes.byref(c), seed, ctypes.byref(out)))
+        return cls(out.value, cfg)
+
+    @classmethod
+    def from_arrays(cls, cfg: dict, arrays: Sequence[np.ndarray]) -> "Model":
+        """Upload host tensors given in weight_specs order (src/spec.rs:443-712)."""
+        lib = _lib.load()
+        c = to_c(cfg)
+        ptrs = (ctypes.c_void_p * len(arrays))(*[a.ctypes.data for a in arrays])
+        out = ctypes.c_void_p()
+        check(lib.cq35_model_create(ctypes.byref(c), ptrs, 0, ctypes.byref(out)))
+        m = cls(out.value, cfg)
+        m._keep = arrays
+        return m
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.load().cq35_model_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- queries ----------------------------------------------------------
+    @property
+    def vocabulary_size(self) -> int:
+        return self.cfg["vocab"]
+
+    def weight_bytes(self) -> int:
+        b = ctypes.c_int64()
+        check(_lib.load().cq35_model_weight_bytes(self._h, ctypes.byref(b)))
+        return b.value
+
+    def read_weight(self, index: int) -> np.ndarray:
+        info = weight_info(self.cfg, index)
+        dtype = np.uint16 if info.dtype == 0 else np.float32
+        a = np.empty(info.rows * info.cols, dtype=dtype)
+        check(_lib.load().cq35_model_read_weight(self._h, index, a.ctypes.data, info.bytes))
+        return a
+
+    # -- sessions ---------------------------------------------------------
+    def session(self, capacity: int) -> "Session":
+        if capacity <= 0:
+            raise ValueError("cache capacity must be non-zero")
+        out = ctypes.c_void_p()
+        check(_lib.load().cq35_session_init(self._h, capacity, ctypes.byref(out)))
+        return Session(self, out.value, capacity, 0)
+
+    def resume_checkpoint(self, checkpoint: "SessionCheckpoint") -> "Session":
+        if checkpoint.model is not self:
+            raise ValueError("session checkpoint belongs to another loaded model")
+        out = ctypes.c_void_p()
+        check(_lib.load().cq35_session_copy(checkpoint._h, ctypes.byref(out)))
+        return Session(self, out.value, checkpoint.capacity, checkpoint.position)
+
+    def logits(self, tokens: Sequence[int]) -> np.ndarray:
+        return self.session(len(tokens)).prefill_logits(tokens)
+
+    def next_token(self, tokens: Sequence[int]) -> int:
+        return self.session(len(tokens)).prefill_next_token(tokens)
+
+
+def weight_info(cfg: dict, index: int):
+    info = _lib.TensorInfo()
+    c = to_c(cfg)
+    check(_lib.load().cq35_weight_info(ctypes.byref(c), index, ctypes.byref(info)))
+    return info
+
+
+def weight_count(cfg: dict) -> int:
+    n = ctypes.c_int64()
+    c = to_c(cfg)
+    check(_lib.load().cq35_weight_count(ctypes.byref(c), ctypes.byref(n)))
+    return n.value
+
+
+class Session:
+    def __init__(self, model: Model, handle: int, capacity: int, position: int):
+        self.model = model
+        self._h = ctypes.c_void_p(handle)
+        self.capacity = capacity
+        self.position = position
+        self._alive = True
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.load().cq35_session_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- the forward call (src/model.rs:692-731) --------------------------
+    def _forward(self, tokens: Sequence[int], want_logits: bool):
+        if not self._alive:
+            raise RuntimeError("session state unavailable after failed execution")
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint64).reshape(-1))
+        if len(toks) == 0 or self.position + len(toks) > self.capacity:
+            raise ValueError("token range exceeds cache capacity")
+        if np.any(toks >= self.model.vocabulary_size):
+            raise ValueError("token ID outside vocabulary")
+        nxt = ctypes.c_uint64()
+        logits = np.empty(self.model.vocabulary_size, dtype=np.uint16) if want_logits else None
+        rc = _lib.load().cq35_step(self._h, toks.ctypes.data, len(toks), self.position,
+                                   self.capacity, ctypes.byref(nxt),
+                                   logits.ctypes.data if want_logits else None)
+        if rc != 0:
+            if rc in (-3, -5):
+                self._alive = False
+            check(rc)
+        self.position += len(toks)
+        return logits, int(nxt.value)
+
+    def append_next_token(self, tokens: Sequence[int]) -> int:
+        return self._forward(tokens, False)[1]
+
+    def append_logits(self, tokens: Sequence[int]) -> np.ndarray:
+        return read_logits(self._forward(tokens, True)[0])
+
+    def prefill_logits(self, tokens: Sequence[int]) -> np.ndarray:
+        if self.position != 0:
+            raise ValueError("a session can only be prefilled once")
+        return read_logits(self._forward(tokens, True)[0])
+
+    def decode_logits(self, token: int) -> np.ndarray:
+        if self.position <= 0:
+            raise ValueError("decode requires a completed prefill")
+        return read_logits(self._forward([token], True)[0])
+
+    def prefill_next_token(self, tokens: Sequence[int]) -> int:
+        if self.position != 0:
+            raise ValueError("a session can only be prefilled once")
+        return self._forward(tokens, False)[1]
+
+    def decode_next_token(self, token: int) -> int:
+        if self.position <= 0:
+            raise ValueError("decode requires a completed prefill")
+        return self._forward([token], False)[1]
+
+    def step_raw(self, tokens: Sequence[int], want_logits: bool = True):
+        """(BF16 logits bits, next token) of one call, without the checks."""
+        return self._forward(tokens, want_logits)
+
+    # -- state ------------------------------------------------------------
+    def state_bytes(self, which: int) -> int:
+        b = ctypes.c_int64()
+        check(_lib.load().cq35_session_state_bytes(self._h, which, ctypes.byref(b)))
+        return b.value
+
+    def export_state(self, which: int = 0) -> np.ndarray:
+        n = self.state_bytes(which)
+        a = np.empty(n // (2 if which == 0 else 4), dtype=np.uint16 if which == 0 else np.float32)
+        check(_lib.load().cq35_session_export_state(self._h, which, a.ctypes.data, n))
+        return a
+
+    def import_state(self, which: int, data: np.ndarray) -> None:
+        a = np.ascontiguousarray(data)
+        check(_lib.load().cq35_session_import_state(self._h, which, a.ctypes.data, a.nbytes))
+
+    def into_checkpoint(self) -> "SessionCheckpoint":
+        if not self._alive:
+            raise RuntimeError("session state is unavailable after an inference error")
+        cp = SessionCheckpoint(self.model, self._h, self.capacity, self.position)
+        self._h = ctypes.c_void_p()
+        self._alive = False
+        return cp
+
+    def set_graph(self, enabled: bool) -> None:
+        check(_lib.load().cq35_session_set_graph(self._h, 1 if enabled else 0))
+
+    def time_kernel(self, kernel_class: int) -> None:
+        check(_lib.load().cq35_session_time_kernel(self._h, kernel_class))
+
+    def kernel_time(self):
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        check(_lib.load().cq35_session_kernel_time(self._h, ctypes.byref(ms), ctypes.byref(n)))
+        return ms.value, n.value
+
+
+class SessionCheckpoint:
+    """Immutable frozen state; resumable only by its own model."""
+
+    def __init__(self, model: Model, handle, capacity: int, position: int):
+        self.model = model
+        self._h = handle
+        self.capacity = capacity
+        self.position = position
+
+    def __del__(self):
+        try:
+            if self._h and self._h.value:
+                _lib.load().cq35_session_free(self._h)
+        except Exception:
+            pass
+
+
+def read_logits(bits: np.ndarray) -> np.ndarray:
+    """BF16 bits -> F32 logits; non-finite logits are an error (src/model.rs:734-750)."""
+    f = (bits.astype(np.uint32) << 16).view(np.float32)
+    if not np.all(np.isfinite(f)):
+        raise ValueError("qwen3 returned non-finite logits")
+    return f
+
+
+def kernel_classes() -> list[str]:
+    lib = _lib.load()
+    return [lib.cq35_kernel_class_name(i).decode() for i in range(lib.cq35_kernel_class_count())]

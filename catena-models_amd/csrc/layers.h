@@ -1,0 +1,486 @@
+// Per-layer kernels of the decode step other than the GEMVs: embedding and
+// RoPE table, RMSNorm, convolution + L2 prepare, the Gated DeltaNet step,
+// gated RMSNorm, full-attention prepare, decode attention (online and staged
+// variants), MoE top-k selection, shadow import/persist and the synthetic
+// weight generator. Each keeps the reference's reduction order.
+#pragma once
+
+#include "gemv.h"
+
+namespace cq35 {
+
+// Step parameters in device memory so a captured graph replays unchanged:
+// params[0] = start position, params[1 + t] = token t.
+__device__ __forceinline__ int64_t step_position(const uint64_t* params, int t) {
+  return (int64_t)params[0] + t;
+}
+
+// Embedding row gather (embedding.hex:5-14) and the F32 RoPE table
+// [cos x R/2 | sin x R/2] for this position (rope.hex:5-17); block 0 also
+// clears the argmax key of the step.
+__global__ __launch_bounds__(kBlock) void k_embed(const uint64_t* __restrict__ params, int t,
+                                                   const uint16_t* __restrict__ table, int hidden,
+                                                   uint16_t* __restrict__ h,
+                                                   const float* __restrict__ freq, int half,
+                                                   float* __restrict__ rope,
+                                                   unsigned long long* __restrict__ best) {
+  const uint64_t token = params[1 + t];
+  const uint16_t* row = table + token * (uint64_t)hidden;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+    h[i] = row[i];
+  if (blockIdx.x == 0) {
+    const float position = (float)(uint32_t)step_position(params, t);
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+      float s, c;
+      sincos_q(position * freq[i], &s, &c);
+      rope[i] = c;
+      rope[half + i] = s;
+    }
+    if (threadIdx.x == 0 && best) *best = 0ull;
+  }
+}
+
+// Adjacent-pair tree of squares over the padded power-of-two width held in
+// LDS (qwen35.hex:834-900): stage d combines (k*2d, k*2d + d). Block-wide.
+__device__ __forceinline__ float ap_tree(float* buf, int pad) {
+  __syncthreads();
+  for (int d = 1; d < pad; d <<= 1) {
+    for (int k = threadIdx.x; (k * 2 + 1) * d < pad; k += blockDim.x) buf[k * 2 * d] += buf[k * 2 * d + d];
+    __syncthreads();
+  }
+  return buf[0];
+}
+
+// qwen35.normalize (qwen35.hex:912-977): one block per row,
+// y = bf16(x * inv) (x) bf16(w), inv = 1 / sqrt(sum/cols + eps).
+__global__ __launch_bounds__(kBlock) void k_rmsnorm(const uint16_t* __restrict__ x,
+                                                     const float* __restrict__ w, int cols, int pad,
+                                                     float eps, uint16_t* __restrict__ out) {
+  extern __shared__ float buf[];
+  const uint16_t* xr = x + (size_t)blockIdx.x * cols;
+  for (int i = threadIdx.x; i < pad; i += blockDim.x) {
+    const float v = i < cols ? bf2f(xr[i]) : 0.0f;
+    buf[i] = i < cols ? v * v : 0.0f;
+  }
+  const float sum = ap_tree(buf, pad);
+  const float inverse = 1.0f / nsqrt(sum / (float)cols + eps);
+  for (int i = threadIdx.x; i < cols; i += blockDim.x)
+    out[(size_t)blockIdx.x * cols + i] = bf_mul(f2bf(bf2f(xr[i]) * inverse), f2bf(w[i]));
+}
+
+// Four-tap causal convolution with its 3-slot history in the cache, then the
+// per-head L2 norm of the Q and K heads with a serial sum
+// (linear_prepare.hex:2-131; qwen35.hex:278-436). One block per KD-channel
+// chunk of the QKV vector.
+__global__ __launch_bounds__(kBlock) void k_linear_prepare(
+    const uint16_t* __restrict__ qkv, uint16_t* __restrict__ cache, int64_t conv_base,
+    const uint64_t* __restrict__ params, int t, const float* __restrict__ conv_w, int qkv_size,
+    int key_dim, int key_heads, uint16_t* __restrict__ conv_out, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out) {
+  __shared__ float squares[256];
+  __shared__ float total;
+  const int64_t position = step_position(params, t);
+  const int chunk = blockIdx.x, tid = threadIdx.x;
+  const int ch = chunk * key_dim + tid;
+  const bool active = tid < key_dim && ch < qkv_size;
+  float value = 0.0f;
+  if (active) {
+    float taps[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int64_t p = position + k;
+      const float hist = bf2f(cache[conv_base + (p % 3) * qkv_size + ch]);
+      taps[k] = (p < 3 ? 0.0f : hist) * conv_w[(size_t)ch * 4 + k];
+    }
+    const uint16_t current = qkv[ch];
+    const float tap3 = bf2f(current) * conv_w[(size_t)ch * 4 + 3];
+    const float sum = (taps[0] + taps[2]) + (taps[1] + tap3);
+    const uint16_t result = f2bf(silu(rbf(sum)));
+    conv_out[ch] = result;
+    cache[conv_base + (position % 3) * qkv_size + ch] = current;
+    value = bf2f(result);
+  }
+  if (chunk >= 2 * key_heads) return;  // value heads: convolution only
+  if (tid < key_dim) squares[tid] = value * value;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.0f;
+    for (int i = 0; i < key_dim; ++i) s += squares[i];
+    total = s;
+  }
+  __syncthreads();
+  if (tid < key_dim) {
+    const float norm = nsqrt(total + bitsf(0x358637bdu));
+    uint16_t* dst = chunk < key_heads ? q_out : k_out;
+    dst[(chunk % key_heads) * key_dim + tid] = f2bf(value / norm);
+  }
+}
+
+// Gated DeltaNet single step (cached_delta.hex:69-135,
+// register_delta.hex:5-124, gates fused_delta.hex:1-20). 32 lanes per value
+// channel, 8 channels per block: lane l owns key elements l, l+32, ...
+// (serial from 0.0, then a 32-wide halving tree). The state row is BF16 in
+// the cache (decode) or F32 in the shadow (inside a multi-token call); the
+// output always uses the unrounded F32 update.
+template <bool kF32State>
+__global__ __launch_bounds__(kBlock) void k_delta(
+    const uint16_t* __restrict__ conv, const uint16_t* __restrict__ q,
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ alpha,
+    const uint16_t* __restrict__ beta, const float* __restrict__ dt, const float* __restrict__ a,
+    uint16_t* __restrict__ state16, float* __restrict__ state32, int value_size, int value_dim,
+    int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out) {
+  const int c = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int lane = threadIdx.x & 31;
+  const bool valid = c < value_size;
+  const int cc = valid ? c : 0;
+  const int head = cc / value_dim;
+  const int kbase = (head % key_heads) * key_dim;
+  const float time_step = softplus(bf2f(alpha[head]) + dt[head]);
+  const float decay = hexp(rbf(time_step * a[head]));
+  const float rate = rbf(sigmoid(bf2f(beta[head])));
+  float old[8], kv[8];
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = lane + 32 * j;
+    if (i < key_dim) {
+      old[j] = kF32State ? state32[(size_t)cc * key_dim + i] : bf2f(state16[(size_t)cc * key_dim + i]);
+      kv[j] = bf2f(k[kbase + i]);
+      acc += old[j] * kv[j];
+    }
+  }
+#pragma unroll
+  for (int s = 16; s >= 1; s >>= 1) acc += __shfl_down(acc, s, 32);
+  const float total = __shfl(acc, 0, 32);
+  const float value = bf2f(conv[2 * key_size + cc]);
+  const float delta = (value - total * decay) * rate;
+  float acc2 = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = lane + 32 * j;
+    if (i < key_dim) {
+      const float next = old[j] * decay + kv[j] * delta;
+      if (valid) {
+        if (kF32State) state32[(size_t)cc * key_dim + i] = next;
+        else state16[(size_t)cc * key_dim + i] = f2bf(next);
+      }
+      acc2 += next * bf2f(q[kbase + i]);
+    }
+  }
+#pragma unroll
+  for (int s = 16; s >= 1; s >>= 1) acc2 += __shfl_down(acc2, s, 32);
+  if (lane == 0 && valid) out[c] = f2bf(acc2 * scale);
+}
+
+// Gated RMSNorm x SiLU(z) per value head with a serial sum of squares
+// (cooperative_norm.hex:139-182; qwen35.hex:753-778).
+__global__ __launch_bounds__(kBlock) void k_gated_norm(const uint16_t* __restrict__ core,
+                                                        const uint16_t* __restrict__ z,
+                                                        const float* __restrict__ w, int value_dim,
+                                                        float eps, uint16_t* __restrict__ out) {
+  __shared__ float squares[256];
+  __shared__ float total;
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const float v = tid < value_dim ? bf2f(core[h * value_dim + tid]) : 0.0f;
+  if (tid < value_dim) squares[tid] = v * v;
+  __syncthreads();
+  if (tid == 0) {
+    float s = 0.0f;
+    for (int i = 0; i < value_dim; ++i) s += squares[i];
+    total = s;
+  }
+  __syncthreads();
+  if (tid < value_dim) {
+    const float rms = nsqrt(total / (float)value_dim + eps);
+    const float normalized = v / rms;
+    const float gate = silu(bf2f(z[h * value_dim + tid]));
+    out[h * value_dim + tid] = f2bf((normalized * w[tid]) * gate);
+  }
+}
+
+// Full-attention prepare (full_prepare.hex:3-82): per Q or KV head, head RMS
+// with the adjacent-pair tree, neox RoPE on the first R channels, Q to
+// `qout`, K rotated into the cache and V copied into the cache.
+__global__ __launch_bounds__(kBlock) void k_full_prepare(
+    const uint16_t* __restrict__ qg, const uint16_t* __restrict__ key,
+    const uint16_t* __restrict__ value, const float* __restrict__ rope,
+    const float* __restrict__ qw, const float* __restrict__ kw, uint16_t* __restrict__ cache,
+    int64_t key_base, int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs,
+    int q_heads, int head_dim, int pad, int rope_dim, float eps, uint16_t* __restrict__ qout) {
+  __shared__ float buf[256];
+  __shared__ float normed[256];
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const bool is_q = head < q_heads;
+  const int local = is_q ? head : head - q_heads;
+  const uint16_t* src = is_q ? qg + (size_t)local * 2 * head_dim : key + (size_t)local * head_dim;
+  const float x = tid < head_dim ? bf2f(src[tid]) : 0.0f;
+  if (tid < pad) buf[tid] = tid < head_dim ? x * x : 0.0f;
+  const float sum = ap_tree(buf, pad);
+  const float inverse = 1.0f / nsqrt(sum / (float)head_dim + eps);
+  const float* w = is_q ? qw : kw;
+  const float nf = tid < head_dim ? bf2f(bf_mul(f2bf(x * inverse), f2bf(w[tid]))) : 0.0f;
+  normed[tid] = nf;
+  __syncthreads();
+  if (tid >= head_dim) return;
+  float result = nf;
+  if (tid < rope_dim) {
+    const int half = rope_dim / 2;
+    const int pair = tid % half;
+    const bool first = tid < half;
+    const float partner = normed[first ? pair + half : pair];
+    const float ac = nf * rope[pair];
+    const float bs = partner * rope[pair + half];
+    result = first ? ac - bs : ac + bs;
+  }
+  const uint16_t rb = f2bf(result);
+  if (is_q) {
+    qout[local * head_dim + tid] = rb;
+  } else {
+    const int64_t pos = step_position(params, t);
+    cache[key_base + pos * kvs + local * head_dim + tid] = rb;
+    cache[value_base + pos * kvs + local * head_dim + tid] = value[local * head_dim + tid];
+  }
+}
+
+constexpr int kAttnBlock = 512;
+
+// Online decode attention in the reference's exact order (online.hex:4-331)
+// with the work reorganised across the block: all scores in parallel
+// (32-lane dots, 32-wide tree, x 1/sqrt(HD)); per 8-key tile the running
+// maximum is a prefix maximum (max is exact), alpha and p in parallel; then
+// each channel runs its own serial acc = acc*alpha + sum p*v chain while one
+// extra lane runs the denominator chain. One block per query head.
+__global__ __launch_bounds__(kAttnBlock) void k_attention_online(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
+    int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
+    int heads_per_kv, float scale, const uint16_t* __restrict__ qg, float* __restrict__ scratch,
+    int scratch_stride, uint16_t* __restrict__ out) {
+  __shared__ float den_shared;
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const int64_t keys = step_position(params, t) + 1;
+  const int tiles = (int)((keys + 7) / 8);
+  const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
+  float* p = scratch + (size_t)head * scratch_stride;  // scores, then weights
+  float* mx = p + (size_t)tiles * 8;                    // running maximum per tile
+  float* alpha = mx + tiles;                            // exp(m_{t-1} - m_t)
+  // scores
+  const int lane = tid & 31, group = tid >> 5, groups = kAttnBlock / 32;
+  float qv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int ch = lane + 32 * j;
+    qv[j] = ch < head_dim ? bf2f(q[head * head_dim + ch]) : 0.0f;
+  }
+  for (int64_t kk = group; kk < (int64_t)tiles * 8; kk += groups) {
+    float acc = 0.0f;
+    if (kk < keys) {
+      const uint16_t* kr = cache + key_base + kk * kvs + off;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ch = lane + 32 * j;
+        if (ch < head_dim) acc += qv[j] * bf2f(kr[ch]);
+      }
+    }
+#pragma unroll
+    for (int s = 16; s >= 1; s >>= 1) acc += __shfl_down(acc, s, 32);
+    if (lane == 0) p[kk] = kk < keys ? acc * scale : bitsf(0xff800000u);
+  }
+  __syncthreads();
+  // running maximum per tile = prefix maximum of the tile maxima
+  for (int i = tid; i < tiles; i += kAttnBlock) {
+    float m = p[i * 8];
+    for (int j = 1; j < 8; ++j) m = fmaxf(m, p[i * 8 + j]);
+    mx[i] = m;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float m = bitsf(0xff800000u);
+    for (int i = 0; i < tiles; ++i) { m = fmaxf(m, mx[i]); mx[i] = m; }
+  }
+  __syncthreads();
+  for (int i = tid; i < tiles * 8; i += kAttnBlock) p[i] = hexp(p[i] - mx[i / 8]);
+  for (int i = tid; i < tiles; i += kAttnBlock)
+    alpha[i] = hexp((i > 0 ? mx[i - 1] : bitsf(0xff800000u)) - mx[i]);
+  __syncthreads();
+  if (tid == head_dim) {
+    float den = 0.0f;
+    for (int i = 0; i < tiles; ++i) {
+      den = den * alpha[i];
+      for (int j = 0; j < 8; ++j) den = den + p[i * 8 + j];
+    }
+    den_shared = den;
+  }
+  float acc = 0.0f;
+  if (tid < head_dim) {
+    const uint16_t* vb = cache + value_base + off + tid;
+    for (int i = 0; i < tiles; ++i) {
+      acc = acc * alpha[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t kk = (int64_t)i * 8 + j;
+        const int64_t safe = kk < keys ? kk : 0;
+        acc = acc + p[kk] * bf2f(vb[safe * kvs]);
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < head_dim) {
+    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + tid]));
+    out[head * head_dim + tid] = f2bf(rbf(acc / den_shared) * gate);
+  }
+}
+
+// Staged dense attention (configs without MoE): scalar-order scores
+// (qwen35.rs:722-790 over attention.hex:71-92), softmax with a 256-partial
+// maximum and an adjacent-pair sum over the keys (qwen35_attention.hex:
+// 258-393), 8 interleaved context partials combined
+// ((s0+s4)+(s2+s6))+((s1+s5)+(s3+s7)) (qwen35_attention.hex:2-177) and the
+// sigmoid gate (qwen35.hex:207-222). One block per query head.
+__global__ __launch_bounds__(kBlock) void k_attention_staged(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
+    int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
+    int heads_per_kv, float scale, const uint16_t* __restrict__ qg, float* __restrict__ scratch,
+    int scratch_stride, uint16_t* __restrict__ out) {
+  __shared__ float partial[kBlock];
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const int64_t keys = step_position(params, t) + 1;
+  const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
+  float* s = scratch + (size_t)head * scratch_stride;
+  float* e = s + keys;
+  uint16_t* pb = reinterpret_cast<uint16_t*>(e + keys);
+  for (int64_t kk = tid; kk < keys; kk += kBlock) {
+    const uint16_t* kr = cache + key_base + kk * kvs + off;
+    float acc = 0.0f;
+    for (int i = 0; i < head_dim; ++i) acc += bf2f(q[head * head_dim + i]) * bf2f(kr[i]);
+    s[kk] = rbf(acc * scale);
+  }
+  __syncthreads();
+  float m = bitsf(0xff800000u);
+  for (int64_t kk = tid; kk < keys; kk += kBlock) m = fmaxf(m, s[kk]);
+  partial[tid] = m;
+  __syncthreads();
+  for (int st = kBlock / 2; st >= 1; st >>= 1) {
+    if (tid < st) partial[tid] = fmaxf(partial[tid], partial[tid + st]);
+    __syncthreads();
+  }
+  const float maximum = partial[0];
+  for (int64_t kk = tid; kk < keys; kk += kBlock) e[kk] = hexp(s[kk] - maximum);
+  __syncthreads();
+  for (int64_t d = 1; d < keys; d <<= 1) {
+    for (int64_t k2 = tid; k2 * 2 * d + d < keys; k2 += kBlock) e[k2 * 2 * d] += e[k2 * 2 * d + d];
+    __syncthreads();
+  }
+  const float den = e[0];
+  for (int64_t kk = tid; kk < keys; kk += kBlock) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
+  __syncthreads();
+  if (tid < head_dim) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    const uint16_t* vb = cache + value_base + off + tid;
+    for (int64_t start = 0; start < keys; start += 8) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int64_t kk = start + r;
+        acc[r] = acc[r] + (kk < keys ? bf2f(pb[kk]) * bf2f(vb[kk * kvs]) : 0.0f);
+      }
+    }
+    const float sum = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + tid]));
+    out[head * head_dim + tid] = f2bf(rbf(sum) * gate);
+  }
+}
+
+// MoE top-k (moe.hex:86-252): stable rank with ties to the lower index,
+// ids in rank order, softmax over the selected logits with a serial
+// left-to-right denominator. One block.
+__global__ __launch_bounds__(kBlock) void k_moe_select(const float* __restrict__ logits,
+                                                        int experts, int top_k,
+                                                        int* __restrict__ ids,
+                                                        float* __restrict__ probs) {
+  __shared__ float chosen[64];
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    const float v = logits[e];
+    int rank = 0;
+    for (int i = 0; i < experts; ++i) {
+      const float o = logits[i];
+      rank += (o > v) ? 1 : ((i < e && !(v > o)) ? 1 : 0);
+    }
+    if (rank < top_k) {
+      ids[rank] = e;
+      chosen[rank] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ex[64];
+    float den = 0.0f;
+    for (int j = 0; j < top_k; ++j) ex[j] = hexp(chosen[j] - chosen[0]);
+    for (int j = 0; j < top_k; ++j) den = den + ex[j];
+    for (int j = 0; j < top_k; ++j) probs[j] = ex[j] / den;
+  }
+}
+
+// BF16 cache state <-> F32 shadow for every layer (qwen35.hex:2-141).
+__global__ void k_import(const uint16_t* __restrict__ cache, int64_t base, int64_t layer_stride,
+                         int64_t conv, int64_t rec, int layers, float* __restrict__ shadow) {
+  const int64_t n = rec * layers;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t l = i / rec, w = i % rec;
+    shadow[i] = bf2f(cache[base + l * layer_stride + conv + w]);
+  }
+}
+__global__ void k_persist(uint16_t* __restrict__ cache, int64_t base, int64_t layer_stride,
+                          int64_t conv, int64_t rec, int layers, const float* __restrict__ shadow) {
+  const int64_t n = rec * layers;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t l = i / rec, w = i % rec;
+    cache[base + l * layer_stride + conv + w] = f2bf(shadow[i]);
+  }
+}
+
+// Synthetic weights: element i of a tensor keyed by `key`.
+enum WeightKind { kEmbed = 0, kMatrix, kNorm, kDt, kA, kConv, kRouter, kSharedGate };
+
+__global__ void k_fill(void* __restrict__ dst, int64_t count, uint64_t key, int kind,
+                       float scale) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const uint64_t h = mix64(key + (uint64_t)i * 0x9e3779b97f4a7c15ull);
+    const float z = (float)irwin_hall4(h);
+    switch (kind) {
+      case kEmbed:
+      case kMatrix: static_cast<uint16_t*>(dst)[i] = f2bf(z * scale); break;
+      case kNorm: static_cast<float*>(dst)[i] = 1.0f + z * scale; break;
+      case kDt: static_cast<float*>(dst)[i] = 1.0f; break;
+      case kA: {
+        const float u = (float)(uint32_t)(h >> 40) * 0x1p-24f;
+        static_cast<float*>(dst)[i] = -(1.0f + 15.0f * u);
+        break;
+      }
+      default: static_cast<float*>(dst)[i] = z * scale; break;
+    }
+  }
+}
+
+// Elementwise numerics for device/host bit checks.
+__global__ void k_numeric(int op, const float* __restrict__ in, float* __restrict__ out,
+                          int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float x = in[i];
+    float y = 0.0f, s, c;
+    switch (op) {
+      case 0: y = hexp(x); break;
+      case 1: y = silu(x); break;
+      case 2: y = sigmoid(x); break;
+      case 3: y = softplus(x); break;
+      case 4: y = nsqrt(x); break;
+      case 5: sincos_q(x, &s, &c); y = s; break;
+      default: sincos_q(x, &s, &c); y = c; break;
+    }
+    out[i] = y;
+  }
+}
+
+}  // namespace cq35

@@ -1,0 +1,950 @@
+// Host side of the cq35 C ABI: configuration and weight ABI, device weight
+// placement, sessions with the reference's opaque state layout, and the
+// per-token launch sequence (captured once into a hipGraph for decode).
+//
+// Reference call path replaced: src/model.rs:260-328 (Model::cached_outputs
+// -> Artifact::exec_values("qwen3")), src/qwen/qwen35.rs:1374-1650 (the
+// generated token fold), src/model.rs:248-258 (qwen3.init).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/cq35.h"
+#include "layers.h"
+
+using namespace cq35;
+
+// ----------------------------------------------------------------- errors
+
+static thread_local std::string g_error;
+
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                     \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess)                                                                 \
+      return fail(CQ35_EDEVICE, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),     \
+                  __FILE__, __LINE__);                                                    \
+  } while (0)
+
+extern "C" const char* cq35_last_error(void) { return g_error.c_str(); }
+extern "C" int cq35_abi_version(void) { return CQ35_ABI_VERSION; }
+
+// ----------------------------------------------------------- configuration
+
+namespace {
+
+struct Dims {
+  int64_t H, V, L, Q, KVH, HD, R, KS, VS, QKV, REC, CONV, LIN, KVS, QS, KV_STRIDE, E, K, I, SI;
+  int pad_h, pad_hd;
+};
+
+int64_t next_pow2(int64_t v) {
+  int64_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+Dims dims_of(const cq35_config& c) {
+  Dims d{};
+  d.H = c.hidden; d.V = c.vocab; d.L = c.layers; d.Q = c.q_heads; d.KVH = c.kv_heads;
+  d.HD = c.head_dim; d.R = c.rope_dim;
+  d.KS = (int64_t)c.key_heads * c.key_dim;
+  d.VS = (int64_t)c.value_heads * c.value_dim;
+  d.QKV = 2 * d.KS + d.VS;
+  d.REC = d.VS * c.key_dim;
+  d.CONV = 3 * d.QKV;
+  d.LIN = d.CONV + d.REC;
+  d.KVS = d.KVH * d.HD;
+  d.QS = d.Q * d.HD;
+  d.KV_STRIDE = d.L * 2 * d.KVS;
+  d.E = c.experts; d.K = c.top_k; d.I = c.intermediate; d.SI = c.shared_intermediate;
+  d.pad_h = (int)next_pow2(d.H);
+  d.pad_hd = (int)next_pow2(d.HD);
+  return d;
+}
+
+bool is_full(const cq35_config& c, int64_t l) { return ((l + 1) % c.full_interval) == 0; }
+int layer_tensors(const cq35_config& c, int64_t l) {
+  return is_full(c, l) ? (c.moe ? 16 : 11) : (c.moe ? 19 : 14);
+}
+
+// Kinds drive the synthetic generator (shared specification with the CPU
+// restatement): BF16 matrices ~N(0, 0.02); norm weights 1 + N(0, 0.02);
+// dt bias 1; A = -(1 + 15u); conv taps N(0, 0.3); router N(0, 0.04);
+// shared-expert gate row N(0, 0.02).
+struct TensorDesc {
+  int32_t dtype;
+  int64_t rows, cols;
+  int kind;
+};
+
+int64_t weight_count(const cq35_config& c) {
+  int64_t n = 1;
+  for (int64_t l = 0; l < c.layers; ++l) n += layer_tensors(c, l);
+  return n + 2;
+}
+
+// src/spec.rs:443-712, in order.
+bool describe(const cq35_config& c, int64_t index, TensorDesc* t) {
+  const Dims d = dims_of(c);
+  const int64_t total = weight_count(c);
+  auto set = [&](int32_t dt, int64_t r, int64_t co, int kind) {
+    *t = TensorDesc{dt, r, co, kind};
+    return true;
+  };
+  if (index < 0 || index >= total) return false;
+  if (index == 0) return set(CQ35_BF16, d.V, d.H, kEmbed);
+  if (index == total - 2) return set(CQ35_F32, d.H, 1, kNorm);
+  if (index == total - 1) return set(CQ35_BF16, d.V, d.H, kEmbed);
+  int64_t base = 1;
+  for (int64_t l = 0; l < c.layers; ++l) {
+    const int n = layer_tensors(c, l);
+    if (index < base + n) {
+      const int s = (int)(index - base);
+      if (s == 0) return set(CQ35_F32, d.H, 1, kNorm);
+      int ffn;
+      if (is_full(c, l)) {
+        switch (s) {
+          case 1: return set(CQ35_BF16, 2 * d.QS, d.H, kMatrix);
+          case 2: return set(CQ35_BF16, d.KVS, d.H, kMatrix);
+          case 3: return set(CQ35_BF16, d.KVS, d.H, kMatrix);
+          case 4: return set(CQ35_BF16, d.H, d.QS, kMatrix);
+          case 5: return set(CQ35_F32, d.HD, 1, kNorm);
+          case 6: return set(CQ35_F32, d.HD, 1, kNorm);
+          case 7: return set(CQ35_F32, d.H, 1, kNorm);
+          default: break;
+        }
+        ffn = s - 8;
+      } else {
+        switch (s) {
+          case 1: return set(CQ35_BF16, d.QKV, d.H, kMatrix);
+          case 2: return set(CQ35_BF16, d.VS, d.H, kMatrix);
+          case 3: return set(CQ35_BF16, c.value_heads, d.H, kMatrix);
+          case 4: return set(CQ35_BF16, c.value_heads, d.H, kMatrix);
+          case 5: return set(CQ35_F32, c.value_heads, 1, kDt);
+          case 6: return set(CQ35_F32, c.value_heads, 1, kA);
+          case 7: return set(CQ35_F32, c.value_dim, 1, kNorm);
+          case 8: return set(CQ35_BF16, d.H, d.VS, kMatrix);
+          case 9: return set(CQ35_F32, d.QKV, 4, kConv);
+          case 10: return set(CQ35_F32, d.H, 1, kNorm);
+          default: break;
+        }
+        ffn = s - 11;
+      }
+      if (!c.moe) {
+        switch (ffn) {
+          case 0: return set(CQ35_BF16, d.I, d.H, kMatrix);
+          case 1: return set(CQ35_BF16, d.I, d.H, kMatrix);
+          case 2: return set(CQ35_BF16, d.H, d.I, kMatrix);
+          default: return false;
+        }
+      }
+      switch (ffn) {
+        case 0: return set(CQ35_F32, d.E, d.H, kRouter);
+        case 1: return set(CQ35_BF16, d.E * d.I, d.H, kMatrix);
+        case 2: return set(CQ35_BF16, d.E * d.I, d.H, kMatrix);
+        case 3: return set(CQ35_BF16, d.E * d.H, d.I, kMatrix);
+        case 4: return set(CQ35_F32, 1, d.H, kSharedGate);
+        case 5: return set(CQ35_BF16, d.SI, d.H, kMatrix);
+        case 6: return set(CQ35_BF16, d.SI, d.H, kMatrix);
+        case 7: return set(CQ35_BF16, d.H, d.SI, kMatrix);
+        default: return false;
+      }
+    }
+    base += n;
+  }
+  return false;
+}
+
+int64_t tensor_bytes(const TensorDesc& t) { return t.rows * t.cols * (t.dtype == CQ35_BF16 ? 2 : 4); }
+
+int64_t cache_elements(const cq35_config& c, int64_t capacity) {
+  // src/spec.rs:321-362 = state_layout.hex:26-27
+  const Dims d = dims_of(c);
+  return capacity * d.KV_STRIDE + d.L * d.LIN;
+}
+
+}  // namespace
+
+extern "C" int cq35_config_validate(const cq35_config* cfg) {
+  if (!cfg) return fail(CQ35_EINVAL, "null configuration");
+  const cq35_config& c = *cfg;
+  // ModelConfig::validate (src/spec.rs:185-275).
+  if (c.vocab <= 0 || c.hidden <= 0 || c.intermediate <= 0 || c.layers <= 0 || c.q_heads <= 0 ||
+      c.kv_heads <= 0 || c.head_dim <= 0)
+    return fail(CQ35_EINVAL, "model dimensions must be non-zero");
+  if (c.q_heads % c.kv_heads != 0)
+    return fail(CQ35_EINVAL, "attention head count must be divisible by KV head count");
+  if (c.moe) {
+    if (c.experts <= 0 || c.top_k <= 0) return fail(CQ35_EINVAL, "expert counts must be non-zero");
+    if (c.top_k > c.experts) return fail(CQ35_EINVAL, "experts used exceeds expert count");
+    if (c.shared_intermediate <= 0) return fail(CQ35_EINVAL, "missing shared expert size");
+  } else if (c.experts != 0 || c.top_k != 0) {
+    return fail(CQ35_EINVAL, "dense model metadata must not define routed experts");
+  }
+  if (c.rope_dim <= 0 || c.rope_dim > c.head_dim)
+    return fail(CQ35_EINVAL, "rotary dimension must be within the attention head");
+  if (c.full_interval <= 0 || c.key_heads <= 0 || c.key_dim <= 0 || c.value_heads <= 0 ||
+      c.value_dim <= 0)
+    return fail(CQ35_EINVAL, "hybrid layer metadata must be non-zero");
+  bool has_full = false, has_linear = false;
+  for (int l = 0; l < c.layers; ++l) (is_full(c, l) ? has_full : has_linear) = true;
+  if (!has_full || !has_linear)
+    return fail(CQ35_EINVAL, "Qwen3.5 requires both full and linear layers");
+  // Limits of this build's kernels.
+  if (c.hidden % 8 || c.intermediate % 8 || (c.moe && c.shared_intermediate % 8) ||
+      (c.q_heads * c.head_dim) % 8 || (c.value_heads * c.value_dim) % 8)
+    return fail(CQ35_EINVAL, "widths must be multiples of 8 elements (128-bit GEMV loads)");
+  if (c.head_dim > 256 || c.key_dim > 256 || c.value_dim > 256 || c.key_dim % 32)
+    return fail(CQ35_EINVAL, "head_dim/value_dim <= 256 and key_dim a multiple of 32 up to 256");
+  if (c.rope_dim % 2) return fail(CQ35_EINVAL, "rotary dimension must be even");
+  if (c.moe && (c.experts > 4096 || c.top_k > 64))
+    return fail(CQ35_EINVAL, "at most 4096 experts and top-k 64");
+  if (c.value_dim % 8) return fail(CQ35_EINVAL, "value head width must be a multiple of 8");
+  return CQ35_OK;
+}
+
+extern "C" int cq35_weight_count(const cq35_config* cfg, int64_t* count) {
+  int rc = cq35_config_validate(cfg);
+  if (rc) return rc;
+  if (!count) return fail(CQ35_EINVAL, "null output");
+  *count = weight_count(*cfg);
+  return CQ35_OK;
+}
+
+extern "C" int cq35_weight_info(const cq35_config* cfg, int64_t index, cq35_tensor_info* info) {
+  int rc = cq35_config_validate(cfg);
+  if (rc) return rc;
+  TensorDesc t;
+  if (!info || !describe(*cfg, index, &t)) return fail(CQ35_EINVAL, "bad weight index %lld", (long long)index);
+  info->dtype = t.dtype;
+  info->rows = t.rows;
+  info->cols = t.cols;
+  info->bytes = tensor_bytes(t);
+  return CQ35_OK;
+}
+
+// ------------------------------------------------------------------ model
+
+struct cq35_model {
+  cq35_config cfg;
+  Dims d;
+  int device = 0;
+  std::vector<void*> w;       // device pointers in weight ABI order
+  std::vector<void*> owned;   // allocations to free
+  float* freq = nullptr;      // F32 theta^(-2i/R) (src/catena.rs:185-232)
+  int64_t weight_bytes = 0;
+};
+
+namespace {
+
+int finish_model(cq35_model* m) {
+  const int half = (int)(m->cfg.rope_dim / 2);
+  std::vector<float> f(std::max(half, 1));
+  for (int i = 0; i < half; ++i)
+    f[i] = powf(m->cfg.theta, -((float)(2 * i) / (float)m->cfg.rope_dim));
+  HIP_TRY(hipMalloc(&m->freq, f.size() * sizeof(float)));
+  HIP_TRY(hipMemcpy(m->freq, f.data(), f.size() * sizeof(float), hipMemcpyHostToDevice));
+  return CQ35_OK;
+}
+
+float normal_scale(double sd) { return (float)(sd / std::sqrt(1431655765.0)); }
+
+}  // namespace
+
+extern "C" int cq35_model_free(cq35_model* m) {
+  if (!m) return CQ35_OK;
+  hipSetDevice(m->device);
+  for (void* p : m->owned) hipFree(p);
+  if (m->freq) hipFree(m->freq);
+  delete m;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_model_create(const cq35_config* cfg, const void* const* weights, int on_device,
+                                 cq35_model** out) {
+  int rc = cq35_config_validate(cfg);
+  if (rc) return rc;
+  if (!weights || !out) return fail(CQ35_EINVAL, "null argument");
+  cq35_model* m = new (std::nothrow) cq35_model();
+  if (!m) return fail(CQ35_EINVAL, "out of host memory");
+  m->cfg = *cfg;
+  m->d = dims_of(*cfg);
+  hipGetDevice(&m->device);
+  const int64_t n = weight_count(*cfg);
+  m->w.assign(n, nullptr);
+  for (int64_t i = 0; i < n; ++i) {
+    TensorDesc t;
+    describe(*cfg, i, &t);
+    if (!weights[i]) { cq35_model_free(m); return fail(CQ35_EINVAL, "weight %lld is null", (long long)i); }
+    const int64_t bytes = tensor_bytes(t);
+    if (on_device) {
+      m->w[i] = const_cast<void*>(weights[i]);
+    } else {
+      if (i == n - 1 && weights[i] == weights[0]) { m->w[i] = m->w[0]; continue; }  // tied head
+      void* p = nullptr;
+      hipError_t e = hipMalloc(&p, bytes);
+      if (e == hipSuccess) e = hipMemcpy(p, weights[i], bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) {
+        if (p) hipFree(p);
+        cq35_model_free(m);
+        return fail(CQ35_EDEVICE, "uploading weight %lld: %s", (long long)i, hipGetErrorString(e));
+      }
+      m->owned.push_back(p);
+      m->w[i] = p;
+      m->weight_bytes += bytes;
+    }
+  }
+  rc = finish_model(m);
+  if (rc) { cq35_model_free(m); return rc; }
+  *out = m;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_model_create_synthetic(const cq35_config* cfg, uint64_t seed, cq35_model** out) {
+  int rc = cq35_config_validate(cfg);
+  if (rc) return rc;
+  if (!out) return fail(CQ35_EINVAL, "null argument");
+  cq35_model* m = new (std::nothrow) cq35_model();
+  if (!m) return fail(CQ35_EINVAL, "out of host memory");
+  m->cfg = *cfg;
+  m->d = dims_of(*cfg);
+  hipGetDevice(&m->device);
+  const int64_t n = weight_count(*cfg);
+  m->w.assign(n, nullptr);
+  for (int64_t i = 0; i < n; ++i) {
+    TensorDesc t;
+    describe(*cfg, i, &t);
+    if (cfg->tied && i == n - 1) { m->w[i] = m->w[0]; continue; }  // lm_head = token_embd
+    const int64_t bytes = tensor_bytes(t);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+      cq35_model_free(m);
+      return fail(CQ35_EDEVICE, "allocating weight %lld (%lld bytes): %s", (long long)i,
+                  (long long)bytes, hipGetErrorString(e));
+    }
+    m->owned.push_back(p);
+    m->w[i] = p;
+    m->weight_bytes += bytes;
+    const uint64_t key = mix64(seed ^ mix64((uint64_t)i + 1));
+    float scale = normal_scale(0.02);
+    if (t.kind == kConv) scale = normal_scale(0.3);
+    if (t.kind == kRouter) scale = normal_scale(0.04);
+    const int64_t count = t.rows * t.cols;
+    const int blocks = (int)std::min<int64_t>((count + 255) / 256, 65536);
+    k_fill<<<blocks, 256>>>(p, count, key, t.kind, scale);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      cq35_model_free(m);
+      return fail(CQ35_EDEVICE, "synthetic fill of weight %lld: %s", (long long)i, hipGetErrorString(e));
+    }
+  }
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    cq35_model_free(m);
+    return fail(CQ35_EDEVICE, "synthetic fill: %s", hipGetErrorString(e));
+  }
+  rc = finish_model(m);
+  if (rc) { cq35_model_free(m); return rc; }
+  *out = m;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_model_config(const cq35_model* m, cq35_config* out) {
+  if (!m || !out) return fail(CQ35_EINVAL, "null argument");
+  *out = m->cfg;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_model_weight_bytes(const cq35_model* m, int64_t* bytes) {
+  if (!m || !bytes) return fail(CQ35_EINVAL, "null argument");
+  *bytes = m->weight_bytes;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_model_read_weight(const cq35_model* m, int64_t index, void* dst, int64_t bytes) {
+  if (!m || !dst) return fail(CQ35_EINVAL, "null argument");
+  TensorDesc t;
+  if (!describe(m->cfg, index, &t)) return fail(CQ35_EINVAL, "bad weight index");
+  if (bytes != tensor_bytes(t)) return fail(CQ35_EINVAL, "size mismatch: tensor has %lld bytes", (long long)tensor_bytes(t));
+  HIP_TRY(hipSetDevice(m->device));
+  HIP_TRY(hipMemcpy(dst, m->w[index], bytes, hipMemcpyDeviceToHost));
+  return CQ35_OK;
+}
+
+// ---------------------------------------------------------------- session
+
+namespace {
+
+enum KernelClass {
+  KC_EMBED = 0, KC_NORM, KC_PROJECT, KC_PREPARE_LINEAR, KC_DELTA, KC_GATED_NORM, KC_RESIDUAL,
+  KC_PREPARE_FULL, KC_ATTENTION, KC_ROUTER, KC_SELECT, KC_MOE_GATE, KC_MOE_DOWN, KC_SWIGLU,
+  KC_LOGITS, KC_SHADOW, KC_COUNT
+};
+const char* kClassNames[KC_COUNT] = {
+    "embed_rope", "rmsnorm", "project", "linear_prepare", "delta", "gated_norm", "residual_project",
+    "full_prepare", "attention", "moe_router", "moe_select", "moe_gate_up", "moe_down", "swiglu",
+    "logits_argmax", "shadow_copy"};
+
+constexpr int kMaxTimedEvents = 512;
+
+}  // namespace
+
+struct cq35_session {
+  cq35_model* model = nullptr;
+  int64_t capacity = 0;
+  bool poisoned = false;
+  hipStream_t stream = nullptr;
+  // opaque state (reference layout)
+  uint16_t* cache = nullptr;
+  float* shadow = nullptr;
+  // step parameters
+  uint64_t* d_params = nullptr;
+  uint64_t* h_params = nullptr;   // pinned
+  unsigned long long* d_best = nullptr;
+  unsigned long long* h_best = nullptr;  // pinned
+  // activations
+  uint16_t *h = nullptr, *attn = nullptr, *xn = nullptr;
+  uint16_t *qkv = nullptr, *conv = nullptr, *z = nullptr, *alpha = nullptr, *beta = nullptr;
+  uint16_t *qn = nullptr, *kn = nullptr, *core = nullptr, *gated = nullptr;
+  uint16_t *qg = nullptr, *kraw = nullptr, *vraw = nullptr, *qr = nullptr, *ctx = nullptr;
+  float* router = nullptr;
+  int* ids = nullptr;
+  float* probs = nullptr;
+  uint16_t* active = nullptr;
+  uint16_t* act = nullptr;
+  uint16_t* logits = nullptr;
+  float* rope = nullptr;
+  float* attn_scratch = nullptr;
+  int attn_stride = 0;
+  std::vector<void*> allocations;
+  // decode graph
+  bool graph_enabled = true;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  // kernel timing
+  int timed_class = -1;
+  hipEvent_t ev[2 * kMaxTimedEvents] = {};
+  int ev_used = 0;
+  double timed_ms = 0.0;
+  int64_t timed_launches = 0;
+};
+
+namespace {
+
+template <typename T>
+int dalloc(cq35_session* s, T** p, int64_t count) {
+  void* q = nullptr;
+  HIP_TRY(hipMalloc(&q, std::max<int64_t>(count, 1) * sizeof(T)));
+  s->allocations.push_back(q);
+  *p = static_cast<T*>(q);
+  return CQ35_OK;
+}
+
+void destroy_session(cq35_session* s) {
+  if (!s) return;
+  hipSetDevice(s->model->device);
+  if (s->stream) hipStreamSynchronize(s->stream);
+  if (s->graph_exec) hipGraphExecDestroy(s->graph_exec);
+  if (s->graph) hipGraphDestroy(s->graph);
+  for (auto& e : s->ev) if (e) hipEventDestroy(e);
+  for (void* p : s->allocations) hipFree(p);
+  if (s->h_params) hipHostFree(s->h_params);
+  if (s->h_best) hipHostFree(s->h_best);
+  if (s->stream) hipStreamDestroy(s->stream);
+  delete s;
+}
+
+int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
+  cq35_session* s = new (std::nothrow) cq35_session();
+  if (!s) return fail(CQ35_EINVAL, "out of host memory");
+  s->model = m;
+  s->capacity = capacity;
+  const Dims& d = m->d;
+  const cq35_config& c = m->cfg;
+  int rc = CQ35_OK;
+  auto check = [&](int r) { if (r && !rc) rc = r; };
+  hipError_t e = hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) { destroy_session(s); return fail(CQ35_EDEVICE, "stream: %s", hipGetErrorString(e)); }
+  const int64_t cache_n = cache_elements(c, capacity);
+  check(dalloc(s, &s->cache, cache_n));
+  check(dalloc(s, &s->shadow, d.L * d.REC));
+  check(dalloc(s, &s->d_params, capacity + 1));
+  check(dalloc(s, &s->d_best, 1));
+  check(dalloc(s, &s->h, d.H));
+  check(dalloc(s, &s->attn, d.H));
+  check(dalloc(s, &s->xn, d.H));
+  check(dalloc(s, &s->qkv, d.QKV));
+  check(dalloc(s, &s->conv, d.QKV));
+  check(dalloc(s, &s->z, d.VS));
+  check(dalloc(s, &s->alpha, c.value_heads));
+  check(dalloc(s, &s->beta, c.value_heads));
+  check(dalloc(s, &s->qn, d.KS));
+  check(dalloc(s, &s->kn, d.KS));
+  check(dalloc(s, &s->core, d.VS));
+  check(dalloc(s, &s->gated, d.VS));
+  check(dalloc(s, &s->qg, 2 * d.QS));
+  check(dalloc(s, &s->kraw, d.KVS));
+  check(dalloc(s, &s->vraw, d.KVS));
+  check(dalloc(s, &s->qr, d.QS));
+  check(dalloc(s, &s->ctx, d.QS));
+  check(dalloc(s, &s->router, d.E + 1));
+  check(dalloc(s, &s->ids, std::max<int64_t>(d.K, 1)));
+  check(dalloc(s, &s->probs, std::max<int64_t>(d.K, 1)));
+  check(dalloc(s, &s->active, d.K * d.I + d.SI));
+  check(dalloc(s, &s->act, d.I));
+  check(dalloc(s, &s->logits, d.V));
+  check(dalloc(s, &s->rope, std::max<int64_t>(d.R, 2)));
+  // online: scores/weights (tiles*8) + running max + alpha (tiles each);
+  // staged: scores + exponentials (keys each) + BF16 weights.
+  const int64_t tiles = (capacity + 7) / 8;
+  s->attn_stride = (int)std::max<int64_t>(tiles * 8 + 2 * tiles + 16, 3 * capacity + 16);
+  check(dalloc(s, &s->attn_scratch, d.Q * (int64_t)s->attn_stride));
+  if (rc) { destroy_session(s); return rc; }
+  e = hipHostMalloc((void**)&s->h_params, (capacity + 1) * sizeof(uint64_t), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_best, sizeof(unsigned long long), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipMemset(s->cache, 0, cache_n * sizeof(uint16_t));
+  if (e == hipSuccess) e = hipMemset(s->shadow, 0, d.L * d.REC * sizeof(float));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) { destroy_session(s); return fail(CQ35_EDEVICE, "session init: %s", hipGetErrorString(e)); }
+  *out = s;
+  return CQ35_OK;
+}
+
+// ---------------------------------------------------------- launch helpers
+
+struct Launcher {
+  cq35_session* s;
+  template <typename Kernel, typename... Args>
+  void operator()(int kc, Kernel kernel, dim3 grid, dim3 block, size_t lds, Args... args) {
+    const bool timed = s->timed_class == kc && s->ev_used < kMaxTimedEvents;
+    if (timed) hipEventRecord(s->ev[2 * s->ev_used], s->stream);
+    kernel<<<grid, block, lds, s->stream>>>(args...);
+    if (timed) {
+      hipEventRecord(s->ev[2 * s->ev_used + 1], s->stream);
+      ++s->ev_used;
+    }
+  }
+};
+
+int grid_for(int64_t groups, int64_t cap) { return (int)std::max<int64_t>(1, std::min(groups, cap)); }
+constexpr int64_t kGridCap = 2048;
+
+template <int W, int EPI>
+void project(Launcher& L, int kc, const uint16_t* x, const Segments& seg, int64_t cols,
+             const uint16_t* res) {
+  const int64_t rows = (int64_t)seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  constexpr int RPB = 4 * (64 / (W / 4));
+  L(kc, k_project<W, EPI>, dim3(grid_for((rows + RPB - 1) / RPB, kGridCap)), dim3(kBlock),
+    (size_t)cols * 2, x, seg, (int)(cols / 2), res);
+}
+
+Segments segments(std::initializer_list<std::pair<const void*, std::pair<uint16_t*, int64_t>>> list) {
+  Segments s{};
+  int i = 0;
+  for (auto& e : list) {
+    s.w[i] = static_cast<const uint16_t*>(e.first);
+    s.out[i] = e.second.first;
+    s.rows[i] = (int)e.second.second;
+    ++i;
+  }
+  s.count = i;
+  return s;
+}
+
+// Enqueue token t of the call: embedding, every layer, and (for the last
+// token) the head. f32_state selects the F32 shadow DeltaNet state used
+// inside a multi-token call (cached_delta.hex:230-261).
+void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
+  const cq35_model& m = *s->model;
+  const cq35_config& c = m.cfg;
+  const Dims& d = m.d;
+  Launcher L{s};
+  auto Wt = [&](int64_t index) { return m.w[index]; };
+  const int64_t cap = s->capacity;
+  L(KC_EMBED, k_embed, dim3(grid_for((d.H + kBlock - 1) / kBlock, 64)), dim3(kBlock), 0,
+    (const uint64_t*)s->d_params, t, (const uint16_t*)Wt(0), (int)d.H, s->h, (const float*)m.freq,
+    (int)(d.R / 2), s->rope, last ? s->d_best : (unsigned long long*)nullptr);
+  int64_t base = 1;
+  for (int64_t l = 0; l < d.L; ++l) {
+    auto W = [&](int slot) { return Wt(base + slot); };
+    const int64_t key_base = l * 2 * cap * d.KVS;
+    const int64_t value_base = key_base + cap * d.KVS;
+    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->h,
+      (const float*)W(0), (int)d.H, d.pad_h, c.eps, s->xn);
+    int ffn;
+    const float* post_norm;
+    if (is_full(c, l)) {
+      Segments seg = segments({{W(1), {s->qg, 2 * d.QS}}, {W(2), {s->kraw, d.KVS}}, {W(3), {s->vraw, d.KVS}}});
+      if (c.moe) project<256, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      else project<32, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      L(KC_PREPARE_FULL, k_full_prepare, dim3((unsigned)(d.Q + d.KVH)), dim3(kBlock), 0,
+        (const uint16_t*)s->qg, (const uint16_t*)s->kraw, (const uint16_t*)s->vraw,
+        (const float*)s->rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
+        value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd,
+        (int)d.R, c.eps, s->qr);
+      const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
+      if (c.moe)
+        L(KC_ATTENTION, k_attention_online, dim3((unsigned)d.Q), dim3(kAttnBlock), 0,
+          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, value_base,
+          (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
+          (const uint16_t*)s->qg, s->attn_scratch, s->attn_stride, s->ctx);
+      else
+        L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
+          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, value_base,
+          (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
+          (const uint16_t*)s->qg, s->attn_scratch, s->attn_stride, s->ctx);
+      project<64, kResidual>(L, KC_RESIDUAL, s->ctx, segments({{W(4), {s->attn, d.H}}}), d.QS, s->h);
+      post_norm = (const float*)W(7);
+      ffn = 8;
+    } else {
+      Segments seg = segments({{W(1), {s->qkv, d.QKV}}, {W(2), {s->z, d.VS}},
+                               {W(3), {s->alpha, c.value_heads}}, {W(4), {s->beta, c.value_heads}}});
+      if (c.moe) project<256, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      else project<32, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
+      L(KC_PREPARE_LINEAR, k_linear_prepare, dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim)),
+        dim3(kBlock), 0, (const uint16_t*)s->qkv, s->cache, conv_base, (const uint64_t*)s->d_params,
+        t, (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, s->conv, s->qn, s->kn);
+      const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
+      const dim3 dgrid((unsigned)((d.VS + 7) / 8));
+      if (f32_state)
+        L(KC_DELTA, k_delta<true>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
+          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
+          (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr,
+          s->shadow + l * d.REC, (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale,
+          s->core);
+      else
+        L(KC_DELTA, k_delta<false>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
+          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
+          (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6),
+          s->cache + conv_base + d.CONV, (float*)nullptr, (int)d.VS, c.value_dim, c.key_dim,
+          c.key_heads, (int)d.KS, scale, s->core);
+      L(KC_GATED_NORM, k_gated_norm, dim3((unsigned)c.value_heads), dim3(kBlock), 0,
+        (const uint16_t*)s->core, (const uint16_t*)s->z, (const float*)W(7), c.value_dim, c.eps,
+        s->gated);
+      project<64, kResidual>(L, KC_RESIDUAL, s->gated, segments({{W(8), {s->attn, d.H}}}), d.VS, s->h);
+      post_norm = (const float*)W(10);
+      ffn = 11;
+    }
+    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->attn,
+      post_norm, (int)d.H, d.pad_h, c.eps, s->xn);
+    if (c.moe) {
+      L(KC_ROUTER, k_router, dim3(grid_for((d.E + 1 + 31) / 32, kGridCap)), dim3(kBlock),
+        (size_t)d.H * 2, (const uint16_t*)s->xn, (const float*)W(ffn), (const float*)W(ffn + 4),
+        (int)d.E, (int)(d.H / 2), s->router);
+      L(KC_SELECT, k_moe_select, dim3(1), dim3(kBlock), 0, (const float*)s->router, (int)d.E,
+        (int)d.K, s->ids, s->probs);
+      const int64_t rows = d.K * d.I + d.SI;
+      L(KC_MOE_GATE, k_moe_gate, dim3(grid_for((rows + 3) / 4, kGridCap)), dim3(kBlock),
+        (size_t)d.H * 2, (const uint16_t*)s->xn, (const uint16_t*)W(ffn + 1),
+        (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6),
+        (const int*)s->ids, (const float*)s->probs, (const float*)s->router, (int)d.E, (int)d.K,
+        (int)d.I, (int)d.SI, (int)(d.H / 2), s->active);
+      L(KC_MOE_DOWN, k_moe_down, dim3(grid_for((d.H + 31) / 32, kGridCap)), dim3(kBlock),
+        (size_t)(d.K * d.I + d.SI) * 2, (const uint16_t*)s->active, (const uint16_t*)W(ffn + 3),
+        (const uint16_t*)W(ffn + 7), (const int*)s->ids, (const uint16_t*)s->attn, (int)d.H,
+        (int)d.K, (int)d.I, (int)d.SI, s->h);
+    } else {
+      L(KC_SWIGLU, k_swiglu, dim3(grid_for((d.I + 3) / 4, kGridCap)), dim3(kBlock), (size_t)d.H * 2,
+        (const uint16_t*)s->xn, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1), (int)d.I,
+        (int)(d.H / 2), s->act);
+      project<64, kResidual>(L, KC_RESIDUAL, s->act, segments({{W(ffn + 2), {s->h, d.H}}}), d.I, s->attn);
+    }
+    base += layer_tensors(c, l);
+  }
+  if (last) {
+    const int64_t total = weight_count(c);
+    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->h,
+      (const float*)Wt(total - 2), (int)d.H, d.pad_h, c.eps, s->xn);
+    L(KC_LOGITS, k_logits, dim3(grid_for((d.V + 31) / 32, kGridCap)), dim3(kBlock), (size_t)d.H * 2,
+      (const uint16_t*)s->xn, (const uint16_t*)Wt(total - 1), (int)d.V, (int)(d.H / 2), s->logits,
+      s->d_best);
+  }
+}
+
+void enqueue_shadow(cq35_session* s, bool import) {
+  const Dims& d = s->model->d;
+  Launcher L{s};
+  const int64_t base = s->capacity * d.KV_STRIDE;
+  const int blocks = grid_for((d.L * d.REC + kBlock - 1) / kBlock, 8192);
+  if (import)
+    L(KC_SHADOW, k_import, dim3(blocks), dim3(kBlock), 0, (const uint16_t*)s->cache, base, d.LIN,
+      d.CONV, d.REC, (int)d.L, s->shadow);
+  else
+    L(KC_SHADOW, k_persist, dim3(blocks), dim3(kBlock), 0, s->cache, base, d.LIN, d.CONV, d.REC,
+      (int)d.L, (const float*)s->shadow);
+}
+
+uint64_t decode_key(unsigned long long key) {
+  if (key == 0) return 0;
+  return (uint64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+}
+
+int collect_timing(cq35_session* s) {
+  for (int i = 0; i < s->ev_used; ++i) {
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, s->ev[2 * i], s->ev[2 * i + 1]));
+    s->timed_ms += ms;
+    ++s->timed_launches;
+  }
+  s->ev_used = 0;
+  return CQ35_OK;
+}
+
+}  // namespace
+
+extern "C" int cq35_session_init(cq35_model* m, int64_t capacity, cq35_session** out) {
+  if (!m || !out) return fail(CQ35_EINVAL, "null argument");
+  if (capacity <= 0) return fail(CQ35_EINVAL, "cache capacity must be non-zero");
+  if (capacity > 262144) return fail(CQ35_ERANGE, "cache capacity %lld exceeds the model maximum 262144", (long long)capacity);
+  HIP_TRY(hipSetDevice(m->device));
+  return create_session(m, capacity, out);
+}
+
+extern "C" int cq35_session_free(cq35_session* s) {
+  destroy_session(s);
+  return CQ35_OK;
+}
+
+extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int64_t start,
+                         int64_t capacity, uint64_t* next_token, uint16_t* logits) {
+  if (!s || !tokens || !next_token) return fail(CQ35_EINVAL, "null argument");
+  if (s->poisoned) return fail(CQ35_EPOISONED, "session state unavailable after failed execution");
+  const cq35_config& c = s->model->cfg;
+  // Validation before any work (src/model.rs:267-281, 697-709).
+  if (n <= 0) return fail(CQ35_EINVAL, "the token prefix must not be empty");
+  if (capacity != s->capacity)
+    return fail(CQ35_EINVAL, "capacity %lld does not match the session's %lld", (long long)capacity,
+                (long long)s->capacity);
+  if (start < 0 || start + n > capacity)
+    return fail(CQ35_ERANGE, "token range %lld..%lld exceeds cache capacity %lld", (long long)start,
+                (long long)(start + n), (long long)capacity);
+  for (int64_t i = 0; i < n; ++i)
+    if (tokens[i] >= (uint64_t)c.vocab)
+      return fail(CQ35_ERANGE, "token prefix contains an ID outside the %d-token vocabulary", c.vocab);
+  if (n >= 2 && c.key_dim == 128)
+    return fail(CQ35_EUNSUPPORTED,
+                "multi-token calls with key_dim 128 take the reference's batched prefill path "
+                "(prefill.rs:623-652), which this build does not provide; append tokens one at a time");
+  hipError_t e = hipSetDevice(s->model->device);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+  s->h_params[0] = (uint64_t)start;
+  for (int64_t i = 0; i < n; ++i) s->h_params[1 + i] = tokens[i];
+  s->poisoned = true;  // cleared on success
+  e = hipMemcpyAsync(s->d_params, s->h_params, (n + 1) * sizeof(uint64_t), hipMemcpyHostToDevice,
+                     s->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "parameter upload: %s", hipGetErrorString(e));
+  // Dense calls import the BF16 recurrent state into the F32 shadow and
+  // persist it afterwards; MoE only for multi-token calls
+  // (qwen35.rs:1536-1545, 1591-1610). A single-token call is identical with
+  // the state kept in BF16, which the decode path does directly.
+  const bool shadow = n >= 2;
+  const bool use_graph = n == 1 && s->graph_enabled && s->timed_class < 0;
+  if (use_graph) {
+    if (!s->graph_exec) {
+      e = hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal);
+      if (e != hipSuccess) return fail(CQ35_EDEVICE, "graph capture: %s", hipGetErrorString(e));
+      enqueue_token(s, 0, true, false);
+      hipGraph_t graph = nullptr;
+      e = hipStreamEndCapture(s->stream, &graph);
+      if (e == hipSuccess) e = hipGraphInstantiate(&s->graph_exec, graph, nullptr, nullptr, 0);
+      if (e != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return fail(CQ35_EDEVICE, "graph instantiate: %s", hipGetErrorString(e));
+      }
+      s->graph = graph;
+    }
+    e = hipGraphLaunch(s->graph_exec, s->stream);
+    if (e != hipSuccess) return fail(CQ35_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+  } else {
+    if (shadow) enqueue_shadow(s, true);
+    for (int64_t t = 0; t < n; ++t) enqueue_token(s, (int)t, t == n - 1, shadow);
+    if (shadow) enqueue_shadow(s, false);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(CQ35_EDEVICE, "kernel launch: %s", hipGetErrorString(e));
+  }
+  e = hipMemcpyAsync(s->h_best, s->d_best, sizeof(unsigned long long), hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess && logits)
+    e = hipMemcpyAsync(logits, s->logits, (size_t)c.vocab * 2, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "step: %s", hipGetErrorString(e));
+  if (s->timed_class >= 0) {
+    int rc = collect_timing(s);
+    if (rc) return rc;
+  }
+  const uint64_t token = decode_key(*s->h_best);
+  if (token >= (uint64_t)c.vocab)
+    return fail(CQ35_EDEVICE, "qwen3 returned next-token ID %llu outside the vocabulary",
+                (unsigned long long)token);
+  *next_token = token;
+  s->poisoned = false;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_copy(const cq35_session* src, cq35_session** out) {
+  if (!src || !out) return fail(CQ35_EINVAL, "null argument");
+  if (src->poisoned) return fail(CQ35_EPOISONED, "session state unavailable after failed execution");
+  HIP_TRY(hipSetDevice(src->model->device));
+  cq35_session* s = nullptr;
+  int rc = create_session(src->model, src->capacity, &s);
+  if (rc) return rc;
+  const Dims& d = src->model->d;
+  hipError_t e = hipMemcpy(s->cache, src->cache, cache_elements(src->model->cfg, src->capacity) * 2,
+                           hipMemcpyDeviceToDevice);
+  if (e == hipSuccess) e = hipMemcpy(s->shadow, src->shadow, d.L * d.REC * 4, hipMemcpyDeviceToDevice);
+  if (e != hipSuccess) {
+    destroy_session(s);
+    return fail(CQ35_EDEVICE, "session copy: %s", hipGetErrorString(e));
+  }
+  s->graph_enabled = src->graph_enabled;
+  *out = s;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_state_bytes(const cq35_session* s, int which, int64_t* bytes) {
+  if (!s || !bytes) return fail(CQ35_EINVAL, "null argument");
+  if (which == 0) *bytes = cache_elements(s->model->cfg, s->capacity) * 2;
+  else if (which == 1) *bytes = s->model->d.L * s->model->d.REC * 4;
+  else return fail(CQ35_EINVAL, "state buffer %d does not exist", which);
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_export_state(const cq35_session* s, int which, void* dst, int64_t bytes) {
+  int64_t expect = 0;
+  int rc = cq35_session_state_bytes(s, which, &expect);
+  if (rc) return rc;
+  if (!dst || bytes != expect) return fail(CQ35_EINVAL, "state buffer %d has %lld bytes", which, (long long)expect);
+  HIP_TRY(hipSetDevice(s->model->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipMemcpy(dst, which == 0 ? (void*)s->cache : (void*)s->shadow, bytes, hipMemcpyDeviceToHost));
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_import_state(cq35_session* s, int which, const void* src, int64_t bytes) {
+  int64_t expect = 0;
+  int rc = cq35_session_state_bytes(s, which, &expect);
+  if (rc) return rc;
+  if (!src || bytes != expect) return fail(CQ35_EINVAL, "state buffer %d has %lld bytes", which, (long long)expect);
+  HIP_TRY(hipSetDevice(s->model->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipMemcpy(which == 0 ? (void*)s->cache : (void*)s->shadow, src, bytes, hipMemcpyHostToDevice));
+  s->poisoned = false;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_time_kernel(cq35_session* s, int kernel_class) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  if (kernel_class >= KC_COUNT) return fail(CQ35_EINVAL, "unknown kernel class %d", kernel_class);
+  HIP_TRY(hipSetDevice(s->model->device));
+  if (kernel_class >= 0 && !s->ev[0])
+    for (auto& e : s->ev) HIP_TRY(hipEventCreate(&e));
+  s->timed_class = kernel_class < 0 ? -1 : kernel_class;
+  s->timed_ms = 0.0;
+  s->timed_launches = 0;
+  s->ev_used = 0;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_kernel_time(cq35_session* s, double* total_ms, int64_t* launches) {
+  if (!s || !total_ms || !launches) return fail(CQ35_EINVAL, "null argument");
+  *total_ms = s->timed_ms;
+  *launches = s->timed_launches;
+  return CQ35_OK;
+}
+
+extern "C" const char* cq35_kernel_class_name(int kc) {
+  return kc >= 0 && kc < KC_COUNT ? kClassNames[kc] : "";
+}
+extern "C" int cq35_kernel_class_count(void) { return KC_COUNT; }
+
+extern "C" int cq35_session_set_graph(cq35_session* s, int enabled) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  s->graph_enabled = enabled != 0;
+  return CQ35_OK;
+}
+
+// ------------------------------------------------------ numeric test hooks
+
+extern "C" float cq35_numeric_exp(float x) { return hexp(x); }
+extern "C" float cq35_numeric_sqrt(float x) { return nsqrt(x); }
+extern "C" float cq35_numeric_softplus(float x) { return softplus(x); }
+extern "C" void cq35_numeric_sincos(float angle, float* sine, float* cosine) {
+  sincos_q(angle, sine, cosine);
+}
+
+extern "C" int cq35_device_numeric(int op, const float* input, float* output, int64_t count) {
+  if (!input || !output || count < 0 || op < 0 || op > 6) return fail(CQ35_EINVAL, "bad argument");
+  if (count == 0) return CQ35_OK;
+  float *din = nullptr, *dout = nullptr;
+  HIP_TRY(hipMalloc(&din, count * 4));
+  hipError_t e = hipMalloc(&dout, count * 4);
+  if (e == hipSuccess) e = hipMemcpy(din, input, count * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    k_numeric<<<grid_for((count + 255) / 256, 16384), 256>>>(op, din, dout, count);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(output, dout, count * 4, hipMemcpyDeviceToHost);
+  hipFree(din);
+  if (dout) hipFree(dout);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "device numeric: %s", hipGetErrorString(e));
+  return CQ35_OK;
+}
+
+extern "C" int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
+                                int width, uint16_t* out) {
+  if (!x || !w || !out || rows <= 0 || cols <= 0 || cols % 2 || rows > (1 << 30))
+    return fail(CQ35_EINVAL, "bad GEMV shape");
+  if (width != 32 && width != 64 && width != 256) return fail(CQ35_EINVAL, "tree width must be 32, 64 or 256");
+  // Zero-pad the pairs to a multiple of 4: extra pairs add +-0 to a lane
+  // accumulator that is never -0, so every row's value is unchanged.
+  const int64_t padded = (cols + 7) / 8 * 8;
+  std::vector<uint16_t> xp(padded, 0), wp((size_t)(rows * padded), 0);
+  std::copy(x, x + cols, xp.begin());
+  for (int64_t r = 0; r < rows; ++r) std::copy(w + r * cols, w + (r + 1) * cols, wp.begin() + r * padded);
+  uint16_t *dx = nullptr, *dw = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&dx, padded * 2);
+  if (e == hipSuccess) e = hipMalloc(&dw, rows * padded * 2);
+  if (e == hipSuccess) e = hipMalloc(&dout, rows * 2);
+  if (e == hipSuccess) e = hipMemcpy(dx, xp.data(), padded * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dw, wp.data(), rows * padded * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    Segments seg{};
+    seg.w[0] = dw;
+    seg.out[0] = dout;
+    seg.rows[0] = (int)rows;
+    seg.count = 1;
+    const int pairs = (int)(padded / 2);
+    const size_t lds = (size_t)padded * 2;
+    const int rpb = 4 * (64 / (width / 4));
+    const int grid = grid_for((rows + rpb - 1) / rpb, kGridCap);
+    if (width == 32) k_project<32, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
+    else if (width == 64) k_project<64, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
+    else k_project<256, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(out, dout, rows * 2, hipMemcpyDeviceToHost);
+  if (dx) hipFree(dx);
+  if (dw) hipFree(dw);
+  if (dout) hipFree(dout);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "device GEMV: %s", hipGetErrorString(e));
+  return CQ35_OK;
+}

@@ -1,0 +1,164 @@
+/*
+ * cq35 — MI355X-native Qwen3.5/3.6 token loop behind a plain C ABI.
+ *
+ * The entry points replace the compiled catena artifact's session ABI that
+ * hellas-ai/catena-models' Rust runtime binds (src/model.rs):
+ *
+ *   qwen3.init(capacity) -> state          src/model.rs:248-258,
+ *                                          src/catena/state_init_moe.hex:2-13,
+ *                                          src/catena/state_init_hybrid.hex:2-7
+ *   qwen3(tokens, state, capacity, start,  src/model.rs:260-328,
+ *         weights...) -> state, logits,    src/qwen/qwen35.rs:1466-1650
+ *         token
+ *   qwen3.copy-buffer(-16)(buffer, n)      src/model.rs:209-246,
+ *                                          src/catena/session_copy.hex:131-135
+ *   weights placed once in device memory   src/checkpoint.rs:197-231, 822-880
+ *   weight ABI order                       src/spec.rs:443-712 (weight_specs)
+ *
+ * Conventions: every call returns 0 on success or a negative CQ35_E* code;
+ * cq35_last_error() describes the last failure of the calling thread. No
+ * signature carries framework types: only plain pointers, sizes and scalars.
+ * One caller per session at a time; distinct sessions may be used from
+ * distinct threads.
+ */
+#ifndef CQ35_H
+#define CQ35_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CQ35_ABI_VERSION 1
+
+enum {
+  CQ35_OK = 0,
+  CQ35_EINVAL = -1,        /* malformed argument or configuration */
+  CQ35_ERANGE = -2,        /* token id / position / capacity out of range */
+  CQ35_EDEVICE = -3,       /* HIP runtime failure */
+  CQ35_EUNSUPPORTED = -4,  /* path not provided by this build */
+  CQ35_EPOISONED = -5      /* session state unusable after a failed step */
+};
+
+/* The fields of ModelConfig (src/spec.rs:33-62) the token loop reads.
+ * moe != 0 selects ModelArchitecture::Qwen35Moe. */
+typedef struct cq35_config {
+  int32_t moe;
+  int32_t vocab;
+  int32_t hidden;
+  int32_t intermediate;      /* dense FFN width, or per-expert width (MoE) */
+  int32_t layers;
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t rope_dim;
+  float eps;
+  float theta;
+  int32_t experts;
+  int32_t top_k;
+  int32_t shared_intermediate;
+  int32_t full_interval;
+  int32_t key_heads;         /* linear_group_count */
+  int32_t key_dim;           /* linear_state_size */
+  int32_t value_heads;       /* linear_time_step_rank */
+  int32_t value_dim;         /* linear_inner_size / linear_time_step_rank */
+  int32_t tied;              /* output_weight_tied */
+} cq35_config;
+
+enum { CQ35_BF16 = 0, CQ35_F32 = 1 };
+
+typedef struct cq35_tensor_info {
+  int32_t dtype;      /* CQ35_BF16 or CQ35_F32 */
+  int64_t rows;       /* leading dimensions folded: [E,I,H] -> rows=E*I, cols=H */
+  int64_t cols;
+  int64_t bytes;
+} cq35_tensor_info;
+
+typedef struct cq35_model cq35_model;
+typedef struct cq35_session cq35_session;
+
+const char* cq35_last_error(void);
+int cq35_abi_version(void);
+
+/* ModelConfig::validate (src/spec.rs:185-275) plus the limits of this build. */
+int cq35_config_validate(const cq35_config* cfg);
+
+/* weight_specs (src/spec.rs:443-712): tensor count and per-tensor shape. */
+int cq35_weight_count(const cq35_config* cfg, int64_t* count);
+int cq35_weight_info(const cq35_config* cfg, int64_t index, cq35_tensor_info* info);
+
+/* Place the weights in device memory once (replacing the reference's
+ * hipHostRegister zero-copy mapping, src/checkpoint.rs:916-986).
+ * weights[i] points at tensor i in weight_specs order; on_device != 0 means
+ * the pointers are already device allocations that the caller keeps alive
+ * for the model's lifetime (they are borrowed, not copied). */
+int cq35_model_create(const cq35_config* cfg, const void* const* weights, int on_device,
+                      cq35_model** out);
+
+/* Same, with weights produced on the device by the library's counter-based
+ * synthetic generator (seeded BF16 ~N(0, 0.02) matrices; see DESIGN).
+ * Used for benchmarks and parity tests without a checkpoint. */
+int cq35_model_create_synthetic(const cq35_config* cfg, uint64_t seed, cq35_model** out);
+int cq35_model_free(cq35_model* model);
+int cq35_model_config(const cq35_model* model, cq35_config* out);
+/* Device bytes held by the model's weights. */
+int cq35_model_weight_bytes(const cq35_model* model, int64_t* bytes);
+/* Copy tensor `index` back to host memory (for checks). */
+int cq35_model_read_weight(const cq35_model* model, int64_t index, void* dst, int64_t bytes);
+
+/* qwen3.init: zero-initialised opaque state for `capacity` positions. */
+int cq35_session_init(cq35_model* model, int64_t capacity, cq35_session** out);
+int cq35_session_free(cq35_session* session);
+
+/* qwen3: process tokens[0..n) at positions start..start+n (n == 1 is the
+ * decode step), write the greedy next token and, when logits != NULL, the
+ * final position's BF16 logits (vocab entries) to host memory.
+ * `capacity` must equal the session's. A failure after work was enqueued
+ * poisons the session (the reference drops its state on a failed exec,
+ * src/model.rs:711-730). */
+int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t start,
+              int64_t capacity, uint64_t* next_token, uint16_t* logits);
+
+/* qwen3.copy-buffer: an independent bitwise copy of a session's state. */
+int cq35_session_copy(const cq35_session* src, cq35_session** out);
+
+/* Canonical state for parity checks, in the reference layout
+ * (state_layout.hex, decoder.hex:16-23, qwen35.hex:2-16):
+ *   which = 0: BF16 cache [KV: layer, K|V, capacity, kv_heads*head_dim]
+ *              [per layer: conv history 3*QKV, recurrent VH*VD*KD]
+ *   which = 1: F32 DeltaNet shadow [layer, VH*VD*KD]
+ * `bytes` must equal cq35_session_state_bytes(session, which). */
+int cq35_session_state_bytes(const cq35_session* session, int which, int64_t* bytes);
+int cq35_session_export_state(const cq35_session* session, int which, void* dst, int64_t bytes);
+int cq35_session_import_state(cq35_session* session, int which, const void* src, int64_t bytes);
+
+/* Measurement hooks: bracket every launch of one kernel class with HIP
+ * events on the session stream (class ids: see cq35_kernel_class_name);
+ * -1 disables. Results accumulate until read. Decode-step graph replay is
+ * suspended while timing is on. */
+int cq35_session_time_kernel(cq35_session* session, int kernel_class);
+int cq35_session_kernel_time(cq35_session* session, double* total_ms, int64_t* launches);
+const char* cq35_kernel_class_name(int kernel_class);
+int cq35_kernel_class_count(void);
+/* Disable (0) or enable (1, default) hipGraph replay of the decode step. */
+int cq35_session_set_graph(cq35_session* session, int enabled);
+
+/* Host-side builds of the device numerics (same source), for CPU checks. */
+float cq35_numeric_exp(float x);
+float cq35_numeric_sqrt(float x);
+float cq35_numeric_softplus(float x);
+void cq35_numeric_sincos(float angle, float* sine, float* cosine);
+/* Device evaluation of the same numerics over an array (op 0 exp, 1 silu,
+ * 2 sigmoid, 3 softplus, 4 sqrt, 5 sin, 6 cos); host in/out arrays. */
+int cq35_device_numeric(int op, const float* input, float* output, int64_t count);
+/* Device split-pair GEMV with tree width W (32, 64 or 256) over a row-major
+ * BF16 matrix: out[r] = bf16(tree_W(x . w_r)). Host arrays. */
+int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
+                     int width, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,120 @@
+/*
+ * CPU restatement of catena-models' Qwen3.5/3.6 token loop, used ONLY as the
+ * parity checker and the CPU baseline. This is test infrastructure: nothing in
+ * the shipped library links, loads or calls it.
+ *
+ * Every function restates the operation order and rounding points of the
+ * reference Hex kernels (file:line citations are into hellas-ai/catena-models).
+ * Arithmetic is plain IEEE binary32 with FMA contraction disabled
+ * (build with -ffp-contract=off), matching numeric.hex:10.
+ */
+#ifndef CQ35_ORACLE_H
+#define CQ35_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Field-for-field the subset of ModelConfig (src/spec.rs:33-62) the token loop
+ * reads. moe != 0 selects ModelArchitecture::Qwen35Moe. */
+typedef struct ox_config {
+  int32_t moe;
+  int32_t vocab;
+  int32_t hidden;
+  int32_t intermediate;     /* dense FFN width, or per-expert width (MoE) */
+  int32_t layers;
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t rope_dim;
+  float eps;
+  float theta;
+  int32_t experts;
+  int32_t top_k;
+  int32_t shared_intermediate;
+  int32_t full_interval;
+  int32_t key_heads;        /* linear_group_count */
+  int32_t key_dim;          /* linear_state_size */
+  int32_t value_heads;      /* linear_time_step_rank */
+  int32_t value_dim;        /* linear_inner_size / value_heads */
+  int32_t tied;
+} ox_config;
+
+enum { OX_BF16 = 0, OX_F32 = 1 };
+
+/* Weight ABI: the ordered list of src/spec.rs:443-712 (weight_specs). */
+int64_t ox_weight_count(const ox_config* c);
+/* dtype (OX_BF16/OX_F32), rows, cols (cols==1 for vectors), kind (see oracle.c). */
+int ox_weight_info(const ox_config* c, int64_t index, int32_t* dtype, int64_t* rows,
+                   int64_t* cols, int32_t* kind);
+
+/* Numerics (numeric.hex). */
+float ox_exp(float x);
+float ox_silu(float x);
+float ox_sigmoid(float x);
+float ox_softplus(float x);
+float ox_sqrt(float x);
+void ox_sincos(float angle, float* sine, float* cosine);
+uint16_t ox_f2bf(float x);
+float ox_bf2f(uint16_t b);
+
+/* Split-pair dot with a halving tree of the given width (tests/qwen35_simt.rs:99-116). */
+float ox_dot_width(const uint16_t* x, const uint16_t* w, int64_t pairs, int width);
+float ox_dot_width_f32w(const uint16_t* x, const float* w, int64_t pairs, int width);
+
+/* Synthetic weights: the deterministic generator shared (as a specification)
+ * with the GPU library. Fills one tensor of the weight ABI. */
+void ox_fill_tensor(const ox_config* c, uint64_t seed, int64_t index, void* dst);
+uint64_t ox_mix64(uint64_t x);
+
+/* Model (weights held by reference; the caller owns them). */
+typedef struct ox_model ox_model;
+ox_model* ox_model_create(const ox_config* c, void* const* weights);
+void ox_model_free(ox_model* m);
+
+/* Session = the reference's opaque state (state_init_*.hex) in the reference
+ * layout: cache BF16 [KV | per-layer conv history + recurrent], workspace F32
+ * shadow [layers * recurrent]. */
+typedef struct ox_session ox_session;
+ox_session* ox_session_create(const ox_model* m, int64_t capacity);
+void ox_session_free(ox_session* s);
+int64_t ox_cache_elements(const ox_config* c, int64_t capacity);
+uint16_t* ox_session_cache(ox_session* s);
+float* ox_session_shadow(ox_session* s);
+
+/* One `qwen3` call (src/qwen/qwen35.rs:1466-1650): processes tokens at
+ * positions start..start+n and returns the greedy token of the last one.
+ * Returns 0 on success, <0 on invalid input, -9 for the batched (n>=2,
+ * key_dim==128) prefill path, which this restatement does not cover. */
+int ox_step(ox_session* s, const uint64_t* tokens, int64_t n, int64_t start,
+            uint64_t* next_token, uint16_t* logits);
+
+/* Router diagnostics of the last MoE step: ids[layer*top_k + j]. */
+const int64_t* ox_session_last_ids(const ox_session* s);
+
+void ox_set_threads(int n);
+
+/* Kernel-level entry points for the known-answer tests. */
+void ox_project(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols, int width,
+                uint16_t* out);
+void ox_residual_project(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
+                         const uint16_t* residual, uint16_t* out);
+void ox_swiglu_project(const uint16_t* x, const uint16_t* wg, const uint16_t* wu, int64_t rows,
+                       int64_t cols, uint16_t* out);
+void ox_moe_gate_rows(const uint16_t* x, const uint16_t* gate, const uint16_t* up,
+                      const uint16_t* sgate, const uint16_t* sup, const int64_t* ids,
+                      const float* probs, float shared_logit, int64_t H, int64_t K, int64_t I,
+                      int64_t SI, uint16_t* active);
+void ox_moe_down_rows(const uint16_t* active, const uint16_t* down, const uint16_t* sdown,
+                      const int64_t* ids, const uint16_t* residual, int64_t H, int64_t K,
+                      int64_t I, int64_t SI, uint16_t* out);
+void ox_moe_route(const uint16_t* x, const float* router, const float* shared_router, int64_t H,
+                  int64_t E, int64_t K, float* logits, int64_t* ids, float* probs);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
