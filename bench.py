@@ -1,0 +1,257 @@
+#!/usr/bin/env python3
+"""Batch-1 decode benchmark of the Qwen3.5/3.6 token loop on one MI355X.
+
+Mirrors the reference's `--bench --tg K --tg-context C` protocol
+(src/main.rs:393-445): a fresh session, the C-token synthetic prompt
+(LCG ids, src/main.rs:447-457) appended one token per call, W untimed decode
+steps, then K timed greedy `decode_next_token` steps, each ending with the
+8-byte token readback and a stream synchronisation. Defaults are the 35B-A3B
+configuration: 512-token prompt, 512 greedy decode steps (context 512-1024). Weights are random-init BF16
+generated on the device (no checkpoint). One JSON line on stdout.
+
+The CPU baseline is the C restatement (oracle/) on the same shape, timed on
+the host's cores over a bounded sample, with its greedy tokens compared to
+the GPU's on the same prompt.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "catena-models_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def synthetic_tokens(count: int, vocab: int) -> list[int]:
+    """src/main.rs:447-457."""
+    state = 0x9E3779B97F4A7C15
+    out = []
+    for _ in range(count):
+        state = (state * 6364136223846793005 + 1442695040888963407) & 0xFFFFFFFFFFFFFFFF
+        out.append(state % vocab)
+    return out
+
+
+def device_sync():
+    try:
+        ctypes.CDLL("libamdhip64.so").hipDeviceSynchronize()
+    except OSError:
+        pass
+
+
+def kernel_bytes(cfg: dict, context: int) -> dict:
+    """Algorithmic HBM bytes per launch of each streaming kernel class."""
+    import cq35
+    d = cq35.derived(cfg)
+    H, V = cfg["hidden"], cfg["vocab"]
+    full = len(d["full_layers"])
+    lin = cfg["layers"] - full
+    lin_rows = d["qkv"] + d["value_size"] + 2 * cfg["value_heads"]
+    full_rows = 2 * d["query_size"] + 2 * d["kvs"]
+    out = {
+        "project": ((lin * lin_rows + full * full_rows) * H * 2 / cfg["layers"], cfg["layers"]),
+        "residual_project": ((lin * H * d["value_size"] + full * H * d["query_size"]) * 2 / cfg["layers"]
+                             + (0 if cfg["moe"] else H * cfg["intermediate"] * 2) / 2,
+                             cfg["layers"] * (1 if cfg["moe"] else 2)),
+        "logits_argmax": (V * H * 2, 1),
+        "attention": ((context + 1) * 2 * d["kvs"] * 2, full),
+        "delta": (2 * d["recurrent"] * 2, lin),
+    }
+    if cfg["moe"]:
+        K, I, SI, E = cfg["top_k"], cfg["intermediate"], cfg["shared_intermediate"], cfg["experts"]
+        out["moe_gate_up"] = ((K * I + SI) * H * 2 * 2, cfg["layers"])
+        out["moe_down"] = ((K * I + SI) * H * 2, cfg["layers"])
+        out["moe_router"] = ((E + 1) * H * 4, cfg["layers"])
+    else:
+        out["swiglu"] = (2 * cfg["intermediate"] * H * 2, cfg["layers"])
+    return out
+
+
+def measure_kernels(session, tokens, classes, steps_each):
+    """Average launch duration of each kernel class from HIP events on the
+    session stream (graph replay suspended while timing)."""
+    import cq35
+    names = cq35.kernel_classes()
+    res = {}
+    i = 0
+    for name in classes:
+        kc = names.index(name)
+        session.time_kernel(kc)
+        for _ in range(steps_each):
+            session.decode_next_token(tokens[i])
+            i += 1
+        ms, n = session.kernel_time()
+        res[name] = (ms, n)
+        session.time_kernel(-1)
+    return res, i
+
+
+def cpu_baseline(cfg, seed, prompt_len, max_steps, budget_s, gpu_model, threads):
+    import numpy as np
+
+    import oracle
+    oracle.build()
+    oracle.lib().ox_set_threads(threads)
+    t0 = time.time()
+    weights = oracle.synthetic_weights(cfg, seed)
+    gen_s = time.time() - t0
+    model = oracle.Model(cfg, weights)
+    toks = synthetic_tokens(prompt_len + max_steps + 1, cfg["vocab"])
+    cs = model.session(prompt_len + max_steps + 1)
+    gs = gpu_model.session(prompt_len + max_steps + 1)
+    for i, t in enumerate(toks[:prompt_len]):
+        ct, cl = cs.step([t], i)
+        gl, gt = gs.step_raw([t])
+    equal_tokens = ct == gt
+    equal_logits = bool(np.array_equal(cl, gl))
+    steps = 0
+    elapsed = 0.0
+    pos = prompt_len
+    while steps < max_steps and elapsed < budget_s:
+        t1 = time.time()
+        ct, cl = cs.step([ct], pos)
+        elapsed += time.time() - t1
+        gl, gt = gs.step_raw([gt])
+        equal_tokens &= ct == gt
+        equal_logits &= bool(np.array_equal(cl, gl))
+        pos += 1
+        steps += 1
+    return dict(tokens_per_s=steps / elapsed if elapsed else 0.0, steps=steps, seconds=elapsed,
+                weight_gen_s=gen_s, prompt=prompt_len, tokens_equal=bool(equal_tokens),
+                logits_equal=equal_logits)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", default="qwen36-35b-a3b")
+    ap.add_argument("--context", type=int, default=512)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--cpu-budget", type=float, default=25.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "see DESIGN.md for how the token loop would shard.", file=sys.stderr)
+        return 2
+
+    import cq35
+    cfg = cq35.preset(args.config)
+    t0 = time.time()
+    model = cq35.Model.synthetic(cfg, seed=args.seed)
+    log(f"weights: {model.weight_bytes() / 1e9:.2f} GB generated on device in {time.time() - t0:.1f}s")
+    timing_classes = [] if args.no_kernel_timing else (
+        ["project", "moe_gate_up", "moe_down", "residual_project", "logits_argmax", "attention",
+         "delta", "moe_router"] if cfg["moe"] else
+        ["project", "swiglu", "residual_project", "logits_argmax", "attention", "delta"])
+    timing_steps = 3
+    capacity = args.context + args.warmup + args.steps + len(timing_classes) * timing_steps + 1
+    tokens = synthetic_tokens(capacity, cfg["vocab"])
+    session = model.session(capacity)
+    t0 = time.time()
+    for t in tokens[:args.context]:
+        session.append_next_token([t])
+    prefill_s = time.time() - t0
+    log(f"prompt of {args.context} appended one token per call in {prefill_s:.2f}s")
+    base = args.context
+    nxt = tokens[base]
+    for _ in range(args.warmup):
+        nxt = session.decode_next_token(nxt)
+    base += args.warmup
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):  # greedy: each step feeds back the previous token
+        nxt = session.decode_next_token(nxt)
+    device_sync()
+    elapsed = time.perf_counter() - t0
+    base += args.steps
+    ms = elapsed / args.steps * 1e3
+    value = args.steps / elapsed
+    ctx_avg = args.context + args.warmup + args.steps // 2
+    bpt = cq35.bytes_per_token(cfg, ctx_avg)
+    step_gbs = bpt["total"] / (ms / 1e3) / 1e9
+    log(f"decode: {value:.1f} tok/s, {ms:.3f} ms/token, {step_gbs:.0f} GB/s of {bpt['total'] / 1e9:.3f} GB/token")
+
+    roofline = None
+    kernels = {}
+    if timing_classes:
+        kb = kernel_bytes(cfg, ctx_avg)
+        res, used = measure_kernels(session, tokens[base:], timing_classes, timing_steps)
+        base += used
+        for name, (kms, n) in res.items():
+            if n == 0:
+                continue
+            per_launch = kms / n
+            by = kb.get(name, (None, None))[0]
+            kernels[name] = dict(ms_per_step=kms / timing_steps, avg_launch_us=per_launch * 1e3,
+                                 launches_per_step=n / timing_steps,
+                                 gbs=(by / (per_launch / 1e3) / 1e9) if by else None)
+        dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+        by, _ = kb[dom]
+        avg_s = kernels[dom]["avg_launch_us"] / 1e6
+        achieved = by / avg_s / 1e9
+        roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS,
+                        unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                        bytes_per_launch=int(by), avg_launch_us=round(kernels[dom]["avg_launch_us"], 2))
+        for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
+            log(f"  {k:18s} {v['ms_per_step']:.3f} ms/step  {v['avg_launch_us']:.1f} us/launch"
+                + (f"  {v['gbs']:.0f} GB/s" if v["gbs"] else ""))
+
+    cpu = None
+    if not args.no_cpu:
+        need = model.weight_bytes()
+        try:
+            import psutil
+            avail = psutil.virtual_memory().available
+        except Exception:
+            avail = need * 4
+        if avail > need * 1.3:
+            log(f"CPU baseline: restatement on {args.cpu_threads} threads ...")
+            c = cpu_baseline(cfg, args.seed, 4, args.cpu_steps, args.cpu_budget, model, args.cpu_threads)
+            cpu = dict(value=round(c["tokens_per_s"], 4), unit="tokens/s", cores=args.cpu_threads,
+                       kind="port",
+                       sample=(f"{args.config} shape, same synthetic weights; 4-token prompt then "
+                               f"{c['steps']} timed batch-1 decode steps ({c['seconds']:.1f}s; weight "
+                               f"generation {c['weight_gen_s']:.1f}s not timed)"),
+                       gpu_parity=dict(greedy_tokens_equal=c["tokens_equal"],
+                                       bf16_logits_equal=c["logits_equal"], steps=c["steps"] + 4))
+            log(f"CPU: {c['tokens_per_s']:.3f} tok/s; GPU/CPU greedy equal={c['tokens_equal']} "
+                f"logits equal={c['logits_equal']}")
+        else:
+            log(f"CPU baseline skipped: {avail / 1e9:.0f} GB host memory available, need {need / 1e9:.0f} GB")
+
+    line = dict(
+        metric="decode tokens/sec at batch 1 (35B-A3B-shape MoE) + % of HBM roofline",
+        value=round(value, 3), unit="tokens/s", n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 4), higher_is_better=True, scaling="weak", vs_baseline=None,
+        dtype="bf16", data="synthetic (seeded random-init weights, LCG prompt ids)",
+        config=dict(workload=f"{args.config} batch-1 greedy decode", model=args.config,
+                    global_batch=1, seq_len=args.context, context_avg=ctx_avg, parallelism="none"),
+        step_roofline=dict(bytes_per_token=bpt["total"], achieved_gbs=round(step_gbs, 1),
+                           frac=round(step_gbs / HBM_PEAK_GBS, 4)),
+        roofline=roofline, kernels=kernels, cpu_baseline=cpu,
+        prefill_one_token_calls_s=round(prefill_s, 3),
+    )
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
