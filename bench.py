@@ -107,6 +107,7 @@ def cpu_baseline(cfg, seed, prompt_len, max_steps, budget_s, gpu_model, threads)
     t0 = time.time()
     weights = oracle.synthetic_weights(cfg, seed)
     gen_s = time.time() - t0
+    log(f"  CPU weights generated in {gen_s:.1f}s")
     model = oracle.Model(cfg, weights)
     toks = synthetic_tokens(prompt_len + max_steps + 1, cfg["vocab"])
     cs = model.session(prompt_len + max_steps + 1)
@@ -128,6 +129,7 @@ def cpu_baseline(cfg, seed, prompt_len, max_steps, budget_s, gpu_model, threads)
         equal_logits &= bool(np.array_equal(cl, gl))
         pos += 1
         steps += 1
+        log(f"  CPU decode step {steps}: {elapsed:.1f}s so far, tokens equal {equal_tokens}")
     return dict(tokens_per_s=steps / elapsed if elapsed else 0.0, steps=steps, seconds=elapsed,
                 weight_gen_s=gen_s, prompt=prompt_len, tokens_equal=bool(equal_tokens),
                 logits_equal=equal_logits)

@@ -4,15 +4,28 @@
 // BF16 pairs r, r+W, r+2W, ... in order, keeping separate low/high F32
 // accumulators, and the W lane values (low + high) are combined by a halving
 // tree (tests/qwen35_simt.rs:99-116; qwen35_simt.hex:4-120, 240-346). W is 32
-// (project, router, MoE down), 64 (residual) or 256 (grouped projections,
-// SwiGLU, MoE gate/up).
+// (project, router, MoE down, vocabulary head), 64 (residual) or 256
+// (grouped projections, SwiGLU, MoE gate/up).
 //
 // Mapping onto wave64 with 128-bit loads: a physical lane q owns reference
-// lanes 4q..4q+3, so one 16-byte load per chunk hands it exactly the four
-// pairs those lanes read in that chunk, and the per-lane order is preserved.
-// A row therefore occupies LPR = W/4 physical lanes (8, 16 or 64) and a wave
-// streams 64/LPR rows at once. The tree runs with cross-lane shuffles for
-// reference strides >= 4 and finishes inside the lane (strides 2, 1).
+// lanes 4q..4q+3, so one 16-byte load ("quad", four pairs) hands it exactly
+// the four pairs those lanes read in that chunk, and the per-lane order is
+// preserved. A row occupies LPR = W/4 physical lanes (8, 16 or 64). The tree
+// runs with cross-lane shuffles for reference strides >= 4 and finishes
+// inside the lane (strides 2, 1).
+//
+// Memory-level parallelism is the whole game at batch 1. Every kernel
+//  1. issues the loads of its input row (and norm weights) first,
+//  2. then all the weight loads of its tile into a statically indexed
+//     register array (clamped addresses, no branches between the loads),
+//  3. and only then waits, for the input alone (the vector-memory counter
+//     retires in order), stages it in LDS and consumes the weights,
+// so each lane keeps 16-32 loads in flight instead of one.
+//
+// Inputs that the reference normalises first (qwen35.normalize before every
+// projection) are normalised inside the consuming kernel: each block
+// recomputes the RMS norm of the hidden row while its weight loads are in
+// flight, so no launch is spent on it.
 //
 // Requires pairs % 4 == 0 (hidden, expert and head widths are multiples of
 // 8 elements in every Qwen3.5/3.6 shape; validated on the host).
@@ -46,16 +59,6 @@ __device__ __forceinline__ void quad_acc(Quad& a, const u32x4& x, const u32x4& w
   a.lo[3] += lo2f(x.w) * lo2f(w.w); a.hi[3] += hi2f(x.w) * hi2f(w.w);
 }
 
-// F32 weights (the MoE router, qwen35_simt.hex:122-239): a quad of pairs is
-// eight floats.
-__device__ __forceinline__ void quad_acc_f32(Quad& a, const u32x4& x, const f32x4& w0,
-                                             const f32x4& w1) {
-  a.lo[0] += lo2f(x.x) * w0.x; a.hi[0] += hi2f(x.x) * w0.y;
-  a.lo[1] += lo2f(x.y) * w0.z; a.hi[1] += hi2f(x.y) * w0.w;
-  a.lo[2] += lo2f(x.z) * w1.x; a.hi[2] += hi2f(x.z) * w1.y;
-  a.lo[3] += lo2f(x.w) * w1.z; a.hi[3] += hi2f(x.w) * w1.w;
-}
-
 // Halving tree of width W = 4*LPR over the reference lanes held by the LPR
 // physical lanes of a row group. Must be reached by every lane of the wave.
 // The result is valid in the group's first lane.
@@ -77,31 +80,144 @@ __device__ __forceinline__ float quad_tree(const Quad& a) {
   return v0 + v1;
 }
 
-// Copy a BF16 vector of `pairs` pairs into LDS (as packed u32 pairs).
-__device__ __forceinline__ void stage_pairs(uint32_t* lds, const uint16_t* x, int pairs) {
-  const u32x4* src = reinterpret_cast<const u32x4*>(x);
-  u32x4* dst = reinterpret_cast<u32x4*>(lds);
-  for (int i = threadIdx.x; i < pairs / 4; i += blockDim.x) dst[i] = src[i];
+__device__ __forceinline__ u32x4 ldq(const void* base, int64_t quad) {
+  return reinterpret_cast<const u32x4*>(base)[quad];
+}
+
+__device__ __forceinline__ uint32_t pack_bf(uint16_t lo, uint16_t hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+// ------------------------------------------------------------ input staging
+
+// qwen35.normalize (qwen35.hex:912-977) of one row of `cols` BF16 values into
+// LDS as packed BF16 quads: y_i = bf16(bf16(x_i * inv) * bf16(w_i)),
+// inv = 1 / sqrt(S / cols + eps), S the adjacent-pair tree sum of the squares
+// over the next power of two `pad` >= cols (zero padded).
+//
+// cols <= 2048 (every preset): thread t owns octet t (8 values), loaded by
+// norm_prefetch before the caller's weight loads. An in-register tree over
+// the octet, a shuffle tree over the 64 lanes of a wave and
+// ((w0 + w1) + (w2 + w3)) over the waves; threads past pad/8 hold +0, and
+// joining a subtotal with a zero subtree is exact, so the result equals the
+// tree over pad. Wider rows (up to 16384) take a generic path in which thread
+// t owns pad/2048 consecutive octets. Requires blockDim.x == 256.
+struct NormIn {
+  u32x4 x;
+  f32x4 w0, w1;
+};
+
+__device__ __forceinline__ void norm_prefetch(NormIn& in, const uint16_t* __restrict__ x,
+                                              const float* __restrict__ w, int cols) {
+  const int o = min((int)threadIdx.x, (cols >> 3) - 1);
+  in.x = ldq(x, o);
+  in.w0 = reinterpret_cast<const f32x4*>(w)[2 * o];
+  in.w1 = reinterpret_cast<const f32x4*>(w)[2 * o + 1];
+}
+
+__device__ __forceinline__ float octet_squares(const u32x4& v) {
+  const float s0 = lo2f(v.x) * lo2f(v.x), s1 = hi2f(v.x) * hi2f(v.x);
+  const float s2 = lo2f(v.y) * lo2f(v.y), s3 = hi2f(v.y) * hi2f(v.y);
+  const float s4 = lo2f(v.z) * lo2f(v.z), s5 = hi2f(v.z) * hi2f(v.z);
+  const float s6 = lo2f(v.w) * lo2f(v.w), s7 = hi2f(v.w) * hi2f(v.w);
+  return ((s0 + s1) + (s2 + s3)) + ((s4 + s5) + (s6 + s7));
+}
+
+__device__ __forceinline__ u32x4 octet_scale(const u32x4& v, float inverse, const f32x4& w0,
+                                             const f32x4& w1) {
+  u32x4 y;
+  y.x = pack_bf(bf_mul(f2bf(lo2f(v.x) * inverse), f2bf(w0.x)),
+                bf_mul(f2bf(hi2f(v.x) * inverse), f2bf(w0.y)));
+  y.y = pack_bf(bf_mul(f2bf(lo2f(v.y) * inverse), f2bf(w0.z)),
+                bf_mul(f2bf(hi2f(v.y) * inverse), f2bf(w0.w)));
+  y.z = pack_bf(bf_mul(f2bf(lo2f(v.z) * inverse), f2bf(w1.x)),
+                bf_mul(f2bf(hi2f(v.z) * inverse), f2bf(w1.y)));
+  y.w = pack_bf(bf_mul(f2bf(lo2f(v.w) * inverse), f2bf(w1.z)),
+                bf_mul(f2bf(hi2f(v.w) * inverse), f2bf(w1.w)));
+  return y;
+}
+
+// Thread-total -> block-total: shuffle tree over the wave, then the waves.
+__device__ __forceinline__ float block_ap_sum(float t, float* red) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) t = t + __shfl_down(t, s, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__device__ __noinline__ void norm_wide(u32x4* xs, const uint16_t* __restrict__ x,
+                                       const float* __restrict__ w, int cols, float eps,
+                                       float* red) {
+  const int tid = threadIdx.x, octs = cols >> 3;
+  int pad = 8;
+  while (pad < cols) pad <<= 1;
+  const int m = pad >> 11;  // 2..8 octets per thread
+  float part[8];
+  for (int j = 0; j < 8; ++j) {
+    const int o = tid * m + j;
+    part[j] = (j < m && o < octs) ? octet_squares(ldq(x, o)) : 0.0f;
+  }
+  for (int d = 1; d < m; d <<= 1)
+    for (int j = 0; j + d < m; j += 2 * d) part[j] = part[j] + part[j + d];
+  const float sum = block_ap_sum(part[0], red);
+  const float inverse = 1.0f / nsqrt(sum / (float)cols + eps);
+  for (int j = 0; j < m; ++j) {
+    const int o = tid * m + j;
+    if (o < octs)
+      xs[o] = octet_scale(ldq(x, o), inverse, reinterpret_cast<const f32x4*>(w)[2 * o],
+                          reinterpret_cast<const f32x4*>(w)[2 * o + 1]);
+  }
   __syncthreads();
 }
 
-// Accumulate one row against the staged input: physical lane q reads quads
-// j*LPR + q (pairs 4(j*LPR+q) .. +3 = chunk j, reference lanes 4q..4q+3).
-template <int LPR>
-__device__ __forceinline__ void row_accumulate(Quad& acc, const uint32_t* xs, const uint16_t* wrow,
-                                               int pairs, int q) {
-  const u32x4* w4 = reinterpret_cast<const u32x4*>(wrow);
-  const u32x4* x4 = reinterpret_cast<const u32x4*>(xs);
-  const int quads = pairs >> 2;
-#pragma unroll 8
-  for (int i = q; i < quads; i += LPR) quad_acc(acc, x4[i], w4[i]);
+__device__ __forceinline__ void norm_finish(const NormIn& in, u32x4* xs,
+                                            const uint16_t* __restrict__ x,
+                                            const float* __restrict__ w, int cols, float eps,
+                                            float* red) {
+  if (cols > 2048) {
+    norm_wide(xs, x, w, cols, eps, red);
+    return;
+  }
+  const bool own = (int)threadIdx.x < (cols >> 3);
+  const float sum = block_ap_sum(own ? octet_squares(in.x) : 0.0f, red);
+  const float inverse = 1.0f / nsqrt(sum / (float)cols + eps);
+  if (own) xs[threadIdx.x] = octet_scale(in.x, inverse, in.w0, in.w1);
+  __syncthreads();
 }
 
-// ---------------------------------------------------------------- kernels
+// Plain copy of a BF16 row (already in its final form) into LDS: kXQ quads
+// per thread prefetched into registers, any remainder copied afterwards.
+template <int kXQ>
+struct CopyIn {
+  u32x4 v[kXQ];
+};
+
+template <int kXQ>
+__device__ __forceinline__ void copy_prefetch(CopyIn<kXQ>& in, const uint16_t* __restrict__ x,
+                                              int cols) {
+  const int quads = cols >> 3;
+#pragma unroll
+  for (int j = 0; j < kXQ; ++j) in.v[j] = ldq(x, min((int)(threadIdx.x + blockDim.x * j), quads - 1));
+}
+
+template <int kXQ>
+__device__ __forceinline__ void copy_finish(const CopyIn<kXQ>& in, u32x4* xs,
+                                            const uint16_t* __restrict__ x, int cols) {
+  const int quads = cols >> 3;
+#pragma unroll
+  for (int j = 0; j < kXQ; ++j) {
+    const int i = threadIdx.x + blockDim.x * j;
+    if (i < quads) xs[i] = in.v[j];
+  }
+  for (int i = threadIdx.x + blockDim.x * kXQ; i < quads; i += blockDim.x) xs[i] = ldq(x, i);
+  __syncthreads();
+}
+
+// ---------------------------------------------------------- S256 projection
 
 // Up to four row-major matrices sharing one input (group-project,
-// group_projection.hex:3-97, and the consecutive fused.project launches of
-// the dense graph). Rows are numbered across segments.
+// group_projection.hex:3-97). Rows are numbered across segments.
 struct Segments {
   const uint16_t* w[4];
   uint16_t* out[4];
@@ -109,37 +225,98 @@ struct Segments {
   int count;
 };
 
-enum Epilogue { kStoreBf16 = 0, kResidual = 1 };
+// Segment of a row and its row within the segment; selects rather than an
+// indexed kernel-argument load, so the weight address is ready at once.
+__device__ __forceinline__ int segment_of(const Segments& seg, int row, int* local) {
+  const int e0 = seg.rows[0], e1 = e0 + seg.rows[1], e2 = e1 + seg.rows[2];
+  const int s = row < e0 ? 0 : row < e1 ? 1 : row < e2 ? 2 : 3;
+  *local = row - (s == 0 ? 0 : s == 1 ? e0 : s == 2 ? e1 : e2);
+  return s;
+}
+__device__ __forceinline__ const uint16_t* segment_w(const Segments& seg, int s) {
+  return s == 0 ? seg.w[0] : s == 1 ? seg.w[1] : s == 2 ? seg.w[2] : seg.w[3];
+}
+__device__ __forceinline__ uint16_t* segment_out(const Segments& seg, int s) {
+  return s == 0 ? seg.out[0] : s == 1 ? seg.out[1] : s == 2 ? seg.out[2] : seg.out[3];
+}
 
-template <int W, int EPI>
-__global__ __launch_bounds__(kBlock) void k_project(const uint16_t* __restrict__ x, Segments seg,
-                                                     int pairs, const uint16_t* __restrict__ res) {
-  constexpr int LPR = W / 4, RPW = 64 / LPR, RPB = 4 * RPW;
-  extern __shared__ __align__(16) uint32_t xs[];
-  stage_pairs(xs, x, pairs);
-  const int total = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+// S256 (64 lanes per row): each wave streams kRows256 rows, each lane four
+// quads of each per batch (cols <= 2048 is one batch). Output bf16 of the
+// tree (simt.hex:400-410). kNorm: the input is the hidden row normalised in
+// the prologue; otherwise it is used as given.
+constexpr int kRows256 = 4;
+
+template <bool kNorm>
+__global__ __launch_bounds__(kBlock) void k_project256(const uint16_t* __restrict__ x,
+                                                        const float* __restrict__ norm_w, float eps,
+                                                        Segments seg, int cols) {
+  constexpr int RW = kRows256, NQ = 4;
+  extern __shared__ __align__(16) u32x4 xs[];
+  __shared__ float red[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane % LPR, g = lane / LPR;
-  for (int base = blockIdx.x * RPB; base < total; base += gridDim.x * RPB) {
-    const int row = base + wave * RPW + g;
-    int s = 0, local = row;
-    while (s < 3 && local >= seg.rows[s]) { local -= seg.rows[s]; ++s; }
-    Quad acc;
-    quad_zero(acc);
-    if (row < total) row_accumulate<LPR>(acc, xs, seg.w[s] + (size_t)local * (2 * pairs), pairs, q);
-    const float v = quad_tree<LPR>(acc);
-    if (q == 0 && row < total) {
-      if (EPI == kResidual)
-        seg.out[s][local] = bf_add(f2bf(v), res[local]);  // simt.hex:442-454
-      else
-        seg.out[s][local] = f2bf(v);                      // simt.hex:400-410
+  const int quads = cols >> 3;
+  const int total = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  const int row0 = (blockIdx.x * 4 + wave) * RW;
+  NormIn nin;
+  CopyIn<1> cin;
+  if (kNorm) norm_prefetch(nin, x, norm_w, cols);
+  else copy_prefetch(cin, x, cols);
+  const uint16_t* wr[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    int local;
+    const int s = segment_of(seg, min(row0 + r, total - 1), &local);
+    wr[r] = segment_w(seg, s) + (size_t)local * cols;
+  }
+  u32x4 wv[RW][NQ];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) wv[r][j] = ldq(wr[r], min(lane + 64 * j, quads - 1));
+  if (kNorm) norm_finish(nin, xs, x, norm_w, cols, eps, red);
+  else copy_finish(cin, xs, x, cols);
+  Quad acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) quad_zero(acc[r]);
+  for (int b = 0; b * 64 * NQ < quads; ++b) {
+    if (b > 0) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int j = 0; j < NQ; ++j)
+          wv[r][j] = ldq(wr[r], min(lane + 64 * (NQ * b + j), quads - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int qi = lane + 64 * (NQ * b + j);
+      if (qi < quads) {
+        const u32x4 xq = xs[qi];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) quad_acc(acc[r], xq, wv[r][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float v = quad_tree<64>(acc[r]);
+    if (lane == 0 && row0 + r < total) {
+      int local;
+      const int s = segment_of(seg, row0 + r, &local);
+      segment_out(seg, s)[local] = f2bf(v);
     }
   }
 }
 
+// ------------------------------------------------------------ S32 projection
+
+// S32 (8 lanes per row, 8 rows per wave, 32 per block): dense projections
+// (simt.hex:400-410) and, with kArgmax, the vocabulary head fused with the
+// greedy argmax (simt.hex:348-441 + fused_argmax.hex:1-104). kNQ quads per
+// lane per batch; cols <= 64 * kNQ is one batch.
+
 // Orderable key of a BF16 logit for a (value, first index) maximum: larger
 // value wins, equal values prefer the lower index; -0 equals +0; NaN never
-// wins. key 0 means "no candidate" (fused_argmax.hex:1-104 semantics).
+// wins. key 0 means "no candidate".
 __device__ __forceinline__ unsigned long long logit_key(uint16_t b, uint32_t index) {
   float v = bf2f(b);
   if (v != v) return 0ull;
@@ -148,188 +325,382 @@ __device__ __forceinline__ unsigned long long logit_key(uint16_t b, uint32_t ind
   return ((unsigned long long)ordered << 32) | (unsigned long long)(0xffffffffu - index);
 }
 
-// Vocabulary head: S32 projection to BF16 logits fused with the greedy
-// argmax (simt.hex:348-441 + fused_argmax.hex), reduced through one 64-bit
-// atomic max per block.
-__global__ __launch_bounds__(kBlock) void k_logits(const uint16_t* __restrict__ x,
-                                                    const uint16_t* __restrict__ w, int rows,
-                                                    int pairs, uint16_t* __restrict__ logits,
-                                                    unsigned long long* __restrict__ best) {
-  constexpr int LPR = 8, RPW = 8, RPB = 32;
-  extern __shared__ __align__(16) uint32_t xs[];
-  __shared__ unsigned long long wave_best[kBlock / 64];
-  stage_pairs(xs, x, pairs);
+template <bool kNorm, bool kArgmax, int kNQ>
+__global__ __launch_bounds__(kBlock) void k_project32(const uint16_t* __restrict__ x,
+                                                       const float* __restrict__ norm_w, float eps,
+                                                       Segments seg, int cols,
+                                                       unsigned long long* __restrict__ best) {
+  constexpr int NQ = kNQ;
+  extern __shared__ __align__(16) u32x4 xs[];
+  __shared__ float red[4];
+  __shared__ unsigned long long wave_best[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane % LPR, g = lane / LPR;
-  unsigned long long mine = 0ull;
-  for (int base = blockIdx.x * RPB; base < rows; base += gridDim.x * RPB) {
-    const int row = base + wave * RPW + g;
-    Quad acc;
-    quad_zero(acc);
-    if (row < rows) row_accumulate<LPR>(acc, xs, w + (size_t)row * (2 * pairs), pairs, q);
-    const float v = quad_tree<LPR>(acc);
-    if (q == 0 && row < rows) {
-      const uint16_t b = f2bf(v);
-      logits[row] = b;
-      const unsigned long long k = logit_key(b, (uint32_t)row);
-      mine = k > mine ? k : mine;
+  const int q = lane & 7, g = lane >> 3;
+  const int quads = cols >> 3;
+  const int total = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  const int row = (blockIdx.x * 4 + wave) * 8 + g;
+  NormIn nin;
+  CopyIn<1> cin;
+  if (kNorm) norm_prefetch(nin, x, norm_w, cols);
+  else copy_prefetch(cin, x, cols);
+  int local;
+  const int s = segment_of(seg, min(row, total - 1), &local);
+  const uint16_t* wr = segment_w(seg, s) + (size_t)local * cols;
+  u32x4 wv[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) wv[j] = ldq(wr, min(q + 8 * j, quads - 1));
+  if (kNorm) norm_finish(nin, xs, x, norm_w, cols, eps, red);
+  else copy_finish(cin, xs, x, cols);
+  Quad acc;
+  quad_zero(acc);
+  for (int b = 0; b * 8 * NQ < quads; ++b) {
+    if (b > 0) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) wv[j] = ldq(wr, min(q + 8 * (NQ * b + j), quads - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int qi = q + 8 * (NQ * b + j);
+      if (qi < quads) quad_acc(acc, xs[qi], wv[j]);
     }
   }
-  for (int s = 32; s >= 1; s >>= 1) {
-    const unsigned long long o = __shfl_down(mine, s, 64);
-    mine = o > mine ? o : mine;
+  const float v = quad_tree<8>(acc);
+  unsigned long long mine = 0ull;
+  if (q == 0 && row < total) {
+    const uint16_t b = f2bf(v);
+    segment_out(seg, s)[local] = b;
+    if (kArgmax) mine = logit_key(b, (uint32_t)row);
   }
-  if (lane == 0) wave_best[wave] = mine;
+  if (kArgmax) {
+#pragma unroll
+    for (int d = 32; d >= 8; d >>= 1) {
+      const unsigned long long o = __shfl_down(mine, d, 64);
+      mine = o > mine ? o : mine;
+    }
+    if (lane == 0) wave_best[wave] = mine;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      unsigned long long b = wave_best[0];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) b = wave_best[i] > b ? wave_best[i] : b;
+      if (b) atomicMax(best, b);
+    }
+  }
+}
+
+// ------------------------------------------------------- S64 residual output
+
+// bf16(bf16(tree64(x . w_r)) (+) res_r) (qwen3.fused.residual,
+// simt.hex:442-538), or bf16(tree64) when res is null. One wave per block,
+// four rows per wave (16 lanes per row); kNQ quads per lane per batch
+// (cols <= 128 * kNQ is one batch, and then the input fits the prefetch).
+template <int kNQ>
+__global__ __launch_bounds__(64) void k_residual(const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w, int rows,
+                                                  int cols, const uint16_t* __restrict__ res,
+                                                  uint16_t* __restrict__ out) {
+  constexpr int NQ = kNQ;
+  extern __shared__ __align__(16) u32x4 xs[];
+  const int lane = threadIdx.x, q = lane & 15, g = lane >> 4;
+  const int quads = cols >> 3;
+  const int row = blockIdx.x * 4 + g;
+  CopyIn<NQ / 4> cin;
+  copy_prefetch(cin, x, cols);
+  const uint16_t* wr = w + (size_t)min(row, rows - 1) * cols;
+  u32x4 wv[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) wv[j] = ldq(wr, min(q + 16 * j, quads - 1));
+  const uint16_t rv = (q == 0 && res) ? res[min(row, rows - 1)] : (uint16_t)0;
+  copy_finish(cin, xs, x, cols);
+  Quad acc;
+  quad_zero(acc);
+  for (int b = 0; b * 16 * NQ < quads; ++b) {
+    if (b > 0) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) wv[j] = ldq(wr, min(q + 16 * (NQ * b + j), quads - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int qi = q + 16 * (NQ * b + j);
+      if (qi < quads) quad_acc(acc, xs[qi], wv[j]);
+    }
+  }
+  const float v = quad_tree<16>(acc);
+  if (q == 0 && row < rows) out[row] = res ? bf_add(f2bf(v), rv) : f2bf(v);
+}
+
+// ------------------------------------------------------------- MoE router
+
+// Router (moe.hex:4-84) over the normalised hidden row with F32 weights:
+// rows [0, E) routed, row E the shared-expert gate; S32, F32 logits. One
+// wave per row; physical lane l = 2r + h runs reference lane r's low (h = 0)
+// or high (h = 1) accumulator over floats 64k + l, k = 0, 1, ... (64
+// coalesced dwords per step), then lo + hi and the halving tree.
+//
+// The last block to finish (atomic ticket after a device-scope fence) ranks
+// the routed logits, rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)},
+// and writes the top-k ids in rank order with their softmax weights
+// p_j = exp(l_j - l_0) / sum exp (moe.hex:86-252), then resets the ticket.
+template <int kND>
+__global__ __launch_bounds__(kBlock) void k_router_select(
+    const uint16_t* __restrict__ x, const float* __restrict__ norm_w, float eps, int cols,
+    const float* __restrict__ w, const float* __restrict__ shared_w, int experts, int top_k,
+    float* __restrict__ logits, int* __restrict__ ids, float* __restrict__ probs,
+    unsigned* __restrict__ ticket) {
+  constexpr int ND = kND;
+  extern __shared__ __align__(16) u32x4 xs[];
+  __shared__ float red[4];
+  __shared__ float chosen[64];
+  __shared__ int last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = experts + 1;
+  const int row = blockIdx.x * 4 + wave;
+  const int rc = min(row, rows - 1);
+  NormIn nin;
+  norm_prefetch(nin, x, norm_w, cols);
+  const float* wr = rc < experts ? w + (size_t)rc * cols : shared_w;
+  float wv[ND];
+#pragma unroll
+  for (int j = 0; j < ND; ++j) wv[j] = wr[min(64 * j + lane, cols - 1)];
+  norm_finish(nin, xs, x, norm_w, cols, eps, red);
+  const uint16_t* xe = reinterpret_cast<const uint16_t*>(xs);
+  float acc = 0.0f;
+  for (int b = 0; b * 64 * ND < cols; ++b) {
+    if (b > 0) {
+#pragma unroll
+      for (int j = 0; j < ND; ++j) wv[j] = wr[min(64 * (ND * b + j) + lane, cols - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+      const int i = 64 * (ND * b + j) + lane;
+      if (i < cols) acc += bf2f(xe[i]) * wv[j];
+    }
+  }
+  float v = acc + __shfl_down(acc, 1, 64);
+#pragma unroll
+  for (int s = 16; s >= 1; s >>= 1) v += __shfl_down(v, 2 * s, 64);
+  if (lane == 0 && row < rows) logits[row] = v;
+
+  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned long long b = wave_best[0];
-    for (int i = 1; i < kBlock / 64; ++i) b = wave_best[i] > b ? wave_best[i] : b;
-    if (b) atomicMax(best, b);
+    __threadfence();
+    last = atomicAdd(ticket, 1u) == gridDim.x - 1;
   }
-}
-
-// MoE router: S32 over BF16 input x F32 weights, E routed rows then the
-// shared-expert gate row, F32 logits (moe.hex:4-84).
-__global__ __launch_bounds__(kBlock) void k_router(const uint16_t* __restrict__ x,
-                                                    const float* __restrict__ w,
-                                                    const float* __restrict__ shared_w, int experts,
-                                                    int pairs, float* __restrict__ logits) {
-  constexpr int LPR = 8, RPW = 8, RPB = 32;
-  extern __shared__ __align__(16) uint32_t xs[];
-  stage_pairs(xs, x, pairs);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane % LPR, g = lane / LPR;
-  const int rows = experts + 1;
-  for (int base = blockIdx.x * RPB; base < rows; base += gridDim.x * RPB) {
-    const int row = base + wave * RPW + g;
-    Quad acc;
-    quad_zero(acc);
-    if (row < rows) {
-      const float* wr = row < experts ? w + (size_t)row * (2 * pairs) : shared_w;
-      const f32x4* w4 = reinterpret_cast<const f32x4*>(wr);
-      const u32x4* x4 = reinterpret_cast<const u32x4*>(xs);
-      for (int i = q; i < pairs / 4; i += LPR) quad_acc_f32(acc, x4[i], w4[2 * i], w4[2 * i + 1]);
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  float* lg = reinterpret_cast<float*>(xs);  // the staged row is no longer needed
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += blockDim.x)
+    lg[e] = __hip_atomic_load(logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+    const float le = lg[e];
+    int rank = 0;
+    for (int i = 0; i < experts; ++i) {
+      const float o = lg[i];
+      rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
     }
-    const float v = quad_tree<LPR>(acc);
-    if (q == 0 && row < rows) logits[row] = v;
-  }
-}
-
-// Dense SwiGLU: dual S256 over gate and up rows, bf16(silu(bf16 g)) (x)
-// bf16(u) (qwen3.fused.gate, simt.hex:539-646).
-__global__ __launch_bounds__(kBlock) void k_swiglu(const uint16_t* __restrict__ x,
-                                                    const uint16_t* __restrict__ wg,
-                                                    const uint16_t* __restrict__ wu, int rows,
-                                                    int pairs, uint16_t* __restrict__ out) {
-  extern __shared__ __align__(16) uint32_t xs[];
-  stage_pairs(xs, x, pairs);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
-    Quad g, u;
-    quad_zero(g);
-    quad_zero(u);
-    if (row < rows) {
-      row_accumulate<64>(g, xs, wg + (size_t)row * (2 * pairs), pairs, lane);
-      row_accumulate<64>(u, xs, wu + (size_t)row * (2 * pairs), pairs, lane);
+    if (rank < top_k) {
+      ids[rank] = e;
+      chosen[rank] = le;
     }
-    const float gv = quad_tree<64>(g);
-    const float uv = quad_tree<64>(u);
-    if (lane == 0 && row < rows) out[row] = bf_mul(f2bf(silu(rbf(gv))), f2bf(uv));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float den = 0.0f;
+    for (int j = 0; j < top_k; ++j) den = den + hexp(chosen[j] - chosen[0]);
+    for (int j = 0; j < top_k; ++j) probs[j] = hexp(chosen[j] - chosen[0]) / den;
+    *ticket = 0u;
   }
 }
 
-// Routed + shared expert gate/up (moe.hex:254-333): rows [0, K*I) belong to
-// the selected experts in rank order, rows [K*I, K*I+SI) to the shared
-// expert. Routed: bf16(silu(g) * u * p_slot); shared:
-// bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)).
-__global__ __launch_bounds__(kBlock) void k_moe_gate(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate,
-    const uint16_t* __restrict__ up, const uint16_t* __restrict__ sgate,
-    const uint16_t* __restrict__ sup, const int* __restrict__ ids, const float* __restrict__ probs,
+inline size_t router_lds_bytes(int cols, int experts) {
+  return (size_t)(cols * 2 > experts * 4 ? cols * 2 : experts * 4);
+}
+
+// ------------------------------------------------------ dual S256 (SwiGLU)
+
+// Routed + shared expert gate/up (moe.hex:254-333) or the dense SwiGLU
+// (qwen3.fused.gate, simt.hex:539-646) over the normalised hidden row.
+// MoE rows [0, K*I) belong to the selected experts in rank order, rows
+// [K*I, K*I+SI) to the shared expert. Routed: bf16(silu(g) * u * p_slot);
+// shared: bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)); dense:
+// bf16(bf16(silu(bf16 g)) * bf16(u)). kRowsGate rows per wave.
+constexpr int kRowsGate = 2;
+
+template <bool kMoE>
+__global__ __launch_bounds__(kBlock) void k_gate_up(
+    const uint16_t* __restrict__ x, const float* __restrict__ norm_w, float eps, int cols,
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+    const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ sup,
+    const int* __restrict__ ids, const float* __restrict__ probs,
     const float* __restrict__ router, int experts, int top_k, int inter, int shared_inter,
-    int pairs, uint16_t* __restrict__ active) {
-  extern __shared__ __align__(16) uint32_t xs[];
-  stage_pairs(xs, x, pairs);
+    uint16_t* __restrict__ active) {
+  constexpr int RW = kRowsGate, NQ = 4;
+  extern __shared__ __align__(16) u32x4 xs[];
+  __shared__ float red[4];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int routed_rows = top_k * inter, rows = routed_rows + shared_inter;
-  const float shared_prob = sigmoid(router[experts]);
-  for (int row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
-    Quad g, u;
-    quad_zero(g);
-    quad_zero(u);
-    const bool routed = row < routed_rows;
-    int slot = 0;
-    if (row < rows) {
-      const uint16_t *wg, *wu;
-      if (routed) {
-        slot = row / inter;
-        const size_t r = (size_t)ids[slot] * inter + (row % inter);
-        wg = gate + r * (2 * pairs);
-        wu = up + r * (2 * pairs);
-      } else {
-        wg = sgate + (size_t)(row - routed_rows) * (2 * pairs);
-        wu = sup + (size_t)(row - routed_rows) * (2 * pairs);
-      }
-      row_accumulate<64>(g, xs, wg, pairs, lane);
-      row_accumulate<64>(u, xs, wu, pairs, lane);
+  const int quads = cols >> 3;
+  const int routed_rows = kMoE ? top_k * inter : inter;
+  const int rows = kMoE ? routed_rows + shared_inter : inter;
+  const int row0 = (blockIdx.x * 4 + wave) * RW;
+  NormIn nin;
+  norm_prefetch(nin, x, norm_w, cols);
+  const uint16_t *wg[RW], *wu[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int row = min(row0 + r, rows - 1);
+    if (!kMoE) {
+      wg[r] = gate + (size_t)row * cols;
+      wu[r] = up + (size_t)row * cols;
+    } else if (row < routed_rows) {
+      const int slot = row / inter;
+      const size_t e = (size_t)ids[slot] * inter + (row - slot * inter);
+      wg[r] = gate + e * cols;
+      wu[r] = up + e * cols;
+    } else {
+      wg[r] = sgate + (size_t)(row - routed_rows) * cols;
+      wu[r] = sup + (size_t)(row - routed_rows) * cols;
     }
-    const float gv = quad_tree<64>(g);
-    const float uv = quad_tree<64>(u);
+  }
+  u32x4 gv[RW][NQ], uv[RW][NQ];
+#pragma unroll
+  for (int r = 0; r < RW; ++r)
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      gv[r][j] = ldq(wg[r], min(lane + 64 * j, quads - 1));
+      uv[r][j] = ldq(wu[r], min(lane + 64 * j, quads - 1));
+    }
+  norm_finish(nin, xs, x, norm_w, cols, eps, red);
+  Quad ga[RW], ua[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    quad_zero(ga[r]);
+    quad_zero(ua[r]);
+  }
+  for (int b = 0; b * 64 * NQ < quads; ++b) {
+    if (b > 0) {
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+          gv[r][j] = ldq(wg[r], min(lane + 64 * (NQ * b + j), quads - 1));
+          uv[r][j] = ldq(wu[r], min(lane + 64 * (NQ * b + j), quads - 1));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int qi = lane + 64 * (NQ * b + j);
+      if (qi < quads) {
+        const u32x4 xq = xs[qi];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+          quad_acc(ga[r], xq, gv[r][j]);
+          quad_acc(ua[r], xq, uv[r][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const float gsum = quad_tree<64>(ga[r]);
+    const float usum = quad_tree<64>(ua[r]);
+    const int row = row0 + r;
     if (lane == 0 && row < rows) {
-      const float gb = rbf(gv), ub = rbf(uv);
-      const float activated = silu(gb);
-      float y;
-      if (routed) y = (activated * ub) * probs[slot];
-      else y = rbf(rbf(activated) * ub) * shared_prob;
-      active[row] = f2bf(y);
+      if (!kMoE) {
+        active[row] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
+      } else {
+        const float gb = rbf(gsum), ub = rbf(usum);
+        const float activated = silu(gb);
+        float y;
+        if (row < routed_rows) y = (activated * ub) * probs[row / inter];
+        else y = rbf(rbf(activated) * ub) * sigmoid(router[experts]);
+        active[row] = f2bf(y);
+      }
     }
   }
 }
+
+// ----------------------------------------------------- MoE down projection
 
 // Expert down projection (moe.hex:371-434, simt_moe.hex:36-287): per hidden
 // row, S32 over the concatenated routed activations (pair p reads expert
 // ids[p / (I/2)]) and a separate S32 over the shared activations;
 // out = bf16(bf16(routed + residual) (+) bf16(shared)).
+//
+// A row's chains (72 quads per reference-lane group at the 35B shape) are
+// too long to stream from registers, so the block stages kDownRows rows in
+// LDS: wave w loads row row0 + w with all 64 lanes (kNQ quads each, all in
+// flight; a row is at most 64 * kNQ quads), then wave 0 reduces the rows from
+// LDS in the reference order (8 lanes per row).
+constexpr int kDownRows = 4;
+
+template <int kNQ>
 __global__ __launch_bounds__(kBlock) void k_moe_down(
     const uint16_t* __restrict__ active, const uint16_t* __restrict__ down,
     const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
     const uint16_t* __restrict__ residual, int hidden, int top_k, int inter, int shared_inter,
     uint16_t* __restrict__ out) {
-  constexpr int LPR = 8, RPW = 8, RPB = 32;
-  extern __shared__ __align__(16) uint32_t xs[];
-  const int routed_pairs = top_k * inter / 2, shared_pairs = shared_inter / 2;
-  stage_pairs(xs, active, routed_pairs + shared_pairs);
+  constexpr int NQ = kNQ;
+  extern __shared__ __align__(16) u32x4 sm[];
+  const int rq = top_k * inter / 8, sq = shared_inter / 8, per_row = rq + sq;
+  const int iq = inter / 8;
+  const int per_row_cols = per_row * 8;
+  u32x4* xs = sm;
+  u32x4* ws = sm + per_row;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int q = lane % LPR, g = lane / LPR;
-  const int ip = inter / 2;
-  const u32x4* x4 = reinterpret_cast<const u32x4*>(xs);
-  for (int base = blockIdx.x * RPB; base < hidden; base += gridDim.x * RPB) {
-    const int row = base + wave * RPW + g;
+  const int row0 = blockIdx.x * kDownRows;
+  const int row = min(row0 + wave, hidden - 1);
+  CopyIn<NQ / 4> cin;
+  copy_prefetch(cin, active, per_row_cols);
+  int slot_id[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int k = min(lane + 64 * j, rq - 1);
+    slot_id[j] = ids[k / iq];
+  }
+  u32x4 wv[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int k = min(lane + 64 * j, per_row - 1);
+    const int slot = min(k, rq - 1) / iq;
+    const u32x4* src =
+        k < rq ? reinterpret_cast<const u32x4*>(down + ((size_t)slot_id[j] * hidden + row) * inter) +
+                     (k - slot * iq)
+               : reinterpret_cast<const u32x4*>(sdown + (size_t)row * shared_inter) + (k - rq);
+    wv[j] = *src;
+  }
+  copy_finish(cin, xs, active, per_row_cols);
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int k = lane + 64 * j;
+    if (k < per_row) ws[wave * per_row + k] = wv[j];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int g = lane >> 3, q = lane & 7;
+    const int nrows = min(kDownRows, hidden - row0);
     Quad r, s;
     quad_zero(r);
     quad_zero(s);
-    if (row < hidden) {
-#pragma unroll 4
-      for (int i = q; i < routed_pairs / 4; i += LPR) {
-        const int p = 4 * i;
-        const int slot = p / ip;
-        const u32x4* w4 = reinterpret_cast<const u32x4*>(
-            down + ((size_t)ids[slot] * hidden + row) * inter + 2 * (p - slot * ip));
-        quad_acc(r, x4[i], *w4);
-      }
-      const u32x4* s4 = reinterpret_cast<const u32x4*>(sdown + (size_t)row * shared_inter);
-      const u32x4* xs4 = x4 + routed_pairs / 4;
-#pragma unroll 4
-      for (int i = q; i < shared_pairs / 4; i += LPR)
-        quad_acc(s, xs4[i], s4[i]);
+    if (g < nrows) {
+      const u32x4* wr = ws + g * per_row;
+      for (int i = q; i < rq; i += 8) quad_acc(r, xs[i], wr[i]);
+      for (int i = q; i < sq; i += 8) quad_acc(s, xs[rq + i], wr[rq + i]);
     }
-    const float rv = quad_tree<LPR>(r);
-    const float sv = quad_tree<LPR>(s);
-    if (q == 0 && row < hidden) {
-      const uint16_t routed_bf = f2bf(rv + bf2f(residual[row]));
-      out[row] = bf_add(routed_bf, f2bf(sv));
+    const float rv = quad_tree<8>(r);
+    const float sv = quad_tree<8>(s);
+    if (q == 0 && g < nrows) {
+      const int o = row0 + g;
+      out[o] = bf_add(f2bf(rv + bf2f(residual[o])), f2bf(sv));
     }
   }
+}
+
+inline size_t moe_down_lds_bytes(int per_row_quads) {
+  return (size_t)(1 + kDownRows) * per_row_quads * 16;
 }
 
 }  // namespace cq35

@@ -51,23 +51,6 @@ __device__ __forceinline__ float ap_tree(float* buf, int pad) {
   return buf[0];
 }
 
-// qwen35.normalize (qwen35.hex:912-977): one block per row,
-// y = bf16(x * inv) (x) bf16(w), inv = 1 / sqrt(sum/cols + eps).
-__global__ __launch_bounds__(kBlock) void k_rmsnorm(const uint16_t* __restrict__ x,
-                                                     const float* __restrict__ w, int cols, int pad,
-                                                     float eps, uint16_t* __restrict__ out) {
-  extern __shared__ float buf[];
-  const uint16_t* xr = x + (size_t)blockIdx.x * cols;
-  for (int i = threadIdx.x; i < pad; i += blockDim.x) {
-    const float v = i < cols ? bf2f(xr[i]) : 0.0f;
-    buf[i] = i < cols ? v * v : 0.0f;
-  }
-  const float sum = ap_tree(buf, pad);
-  const float inverse = 1.0f / nsqrt(sum / (float)cols + eps);
-  for (int i = threadIdx.x; i < cols; i += blockDim.x)
-    out[(size_t)blockIdx.x * cols + i] = bf_mul(f2bf(bf2f(xr[i]) * inverse), f2bf(w[i]));
-}
-
 // Four-tap causal convolution with its 3-slot history in the cache, then the
 // per-head L2 norm of the Q and K heads with a serial sum
 // (linear_prepare.hex:2-131; qwen35.hex:278-436). One block per KD-channel
@@ -242,94 +225,6 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
   }
 }
 
-constexpr int kAttnBlock = 512;
-
-// Online decode attention in the reference's exact order (online.hex:4-331)
-// with the work reorganised across the block: all scores in parallel
-// (32-lane dots, 32-wide tree, x 1/sqrt(HD)); per 8-key tile the running
-// maximum is a prefix maximum (max is exact), alpha and p in parallel; then
-// each channel runs its own serial acc = acc*alpha + sum p*v chain while one
-// extra lane runs the denominator chain. One block per query head.
-__global__ __launch_bounds__(kAttnBlock) void k_attention_online(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
-    int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
-    int heads_per_kv, float scale, const uint16_t* __restrict__ qg, float* __restrict__ scratch,
-    int scratch_stride, uint16_t* __restrict__ out) {
-  __shared__ float den_shared;
-  const int head = blockIdx.x, tid = threadIdx.x;
-  const int64_t keys = step_position(params, t) + 1;
-  const int tiles = (int)((keys + 7) / 8);
-  const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
-  float* p = scratch + (size_t)head * scratch_stride;  // scores, then weights
-  float* mx = p + (size_t)tiles * 8;                    // running maximum per tile
-  float* alpha = mx + tiles;                            // exp(m_{t-1} - m_t)
-  // scores
-  const int lane = tid & 31, group = tid >> 5, groups = kAttnBlock / 32;
-  float qv[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int ch = lane + 32 * j;
-    qv[j] = ch < head_dim ? bf2f(q[head * head_dim + ch]) : 0.0f;
-  }
-  for (int64_t kk = group; kk < (int64_t)tiles * 8; kk += groups) {
-    float acc = 0.0f;
-    if (kk < keys) {
-      const uint16_t* kr = cache + key_base + kk * kvs + off;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int ch = lane + 32 * j;
-        if (ch < head_dim) acc += qv[j] * bf2f(kr[ch]);
-      }
-    }
-#pragma unroll
-    for (int s = 16; s >= 1; s >>= 1) acc += __shfl_down(acc, s, 32);
-    if (lane == 0) p[kk] = kk < keys ? acc * scale : bitsf(0xff800000u);
-  }
-  __syncthreads();
-  // running maximum per tile = prefix maximum of the tile maxima
-  for (int i = tid; i < tiles; i += kAttnBlock) {
-    float m = p[i * 8];
-    for (int j = 1; j < 8; ++j) m = fmaxf(m, p[i * 8 + j]);
-    mx[i] = m;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float m = bitsf(0xff800000u);
-    for (int i = 0; i < tiles; ++i) { m = fmaxf(m, mx[i]); mx[i] = m; }
-  }
-  __syncthreads();
-  for (int i = tid; i < tiles * 8; i += kAttnBlock) p[i] = hexp(p[i] - mx[i / 8]);
-  for (int i = tid; i < tiles; i += kAttnBlock)
-    alpha[i] = hexp((i > 0 ? mx[i - 1] : bitsf(0xff800000u)) - mx[i]);
-  __syncthreads();
-  if (tid == head_dim) {
-    float den = 0.0f;
-    for (int i = 0; i < tiles; ++i) {
-      den = den * alpha[i];
-      for (int j = 0; j < 8; ++j) den = den + p[i * 8 + j];
-    }
-    den_shared = den;
-  }
-  float acc = 0.0f;
-  if (tid < head_dim) {
-    const uint16_t* vb = cache + value_base + off + tid;
-    for (int i = 0; i < tiles; ++i) {
-      acc = acc * alpha[i];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t kk = (int64_t)i * 8 + j;
-        const int64_t safe = kk < keys ? kk : 0;
-        acc = acc + p[kk] * bf2f(vb[safe * kvs]);
-      }
-    }
-  }
-  __syncthreads();
-  if (tid < head_dim) {
-    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + tid]));
-    out[head * head_dim + tid] = f2bf(rbf(acc / den_shared) * gate);
-  }
-}
-
 // Staged dense attention (configs without MoE): scalar-order scores
 // (qwen35.rs:722-790 over attention.hex:71-92), softmax with a 256-partial
 // maximum and an adjacent-pair sum over the keys (qwen35_attention.hex:
@@ -386,36 +281,6 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
     const float sum = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
     const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + tid]));
     out[head * head_dim + tid] = f2bf(rbf(sum) * gate);
-  }
-}
-
-// MoE top-k (moe.hex:86-252): stable rank with ties to the lower index,
-// ids in rank order, softmax over the selected logits with a serial
-// left-to-right denominator. One block.
-__global__ __launch_bounds__(kBlock) void k_moe_select(const float* __restrict__ logits,
-                                                        int experts, int top_k,
-                                                        int* __restrict__ ids,
-                                                        float* __restrict__ probs) {
-  __shared__ float chosen[64];
-  for (int e = threadIdx.x; e < experts; e += blockDim.x) {
-    const float v = logits[e];
-    int rank = 0;
-    for (int i = 0; i < experts; ++i) {
-      const float o = logits[i];
-      rank += (o > v) ? 1 : ((i < e && !(v > o)) ? 1 : 0);
-    }
-    if (rank < top_k) {
-      ids[rank] = e;
-      chosen[rank] = v;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float ex[64];
-    float den = 0.0f;
-    for (int j = 0; j < top_k; ++j) ex[j] = hexp(chosen[j] - chosen[0]);
-    for (int j = 0; j < top_k; ++j) den = den + ex[j];
-    for (int j = 0; j < top_k; ++j) probs[j] = ex[j] / den;
   }
 }
 

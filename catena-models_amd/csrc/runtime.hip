@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "../../include/cq35.h"
+#include "attention.h"
 #include "layers.h"
 
 using namespace cq35;
@@ -212,12 +213,20 @@ extern "C" int cq35_config_validate(const cq35_config* cfg) {
   if (c.hidden % 8 || c.intermediate % 8 || (c.moe && c.shared_intermediate % 8) ||
       (c.q_heads * c.head_dim) % 8 || (c.value_heads * c.value_dim) % 8)
     return fail(CQ35_EINVAL, "widths must be multiples of 8 elements (128-bit GEMV loads)");
-  if (c.head_dim > 256 || c.key_dim > 256 || c.value_dim > 256 || c.key_dim % 32)
-    return fail(CQ35_EINVAL, "head_dim/value_dim <= 256 and key_dim a multiple of 32 up to 256");
+  if (c.head_dim > 256 || c.key_dim > 256 || c.value_dim > 256 || c.key_dim % 32 || c.head_dim % 32)
+    return fail(CQ35_EINVAL, "head_dim/key_dim multiples of 32 up to 256, value_dim <= 256");
+  if ((c.q_heads / c.kv_heads) * c.head_dim > 16 * 256)
+    return fail(CQ35_EINVAL, "at most 16 query heads of 256 channels per KV head");
   if (c.rope_dim % 2) return fail(CQ35_EINVAL, "rotary dimension must be even");
   if (c.moe && (c.experts > 4096 || c.top_k > 64))
     return fail(CQ35_EINVAL, "at most 4096 experts and top-k 64");
   if (c.value_dim % 8) return fail(CQ35_EINVAL, "value head width must be a multiple of 8");
+  if (c.hidden > 16384) return fail(CQ35_EINVAL, "hidden width above 16384");
+  if ((int64_t)c.q_heads * c.head_dim > 32768 || (int64_t)c.value_heads * c.value_dim > 32768 ||
+      (!c.moe && c.intermediate > 32768))
+    return fail(CQ35_EINVAL, "residual projection inputs above 32768 values");
+  if (c.moe && (int64_t)c.top_k * c.intermediate + c.shared_intermediate > 12288)
+    return fail(CQ35_EINVAL, "top_k * intermediate + shared_intermediate above 12288");
   return CQ35_OK;
 }
 
@@ -394,15 +403,17 @@ extern "C" int cq35_model_read_weight(const cq35_model* m, int64_t index, void* 
 
 namespace {
 
+// Launch classes for per-class event timing. RMSNorm is fused into the
+// consuming GEMVs and top-k selection into the router, so neither has a class.
 enum KernelClass {
-  KC_EMBED = 0, KC_NORM, KC_PROJECT, KC_PREPARE_LINEAR, KC_DELTA, KC_GATED_NORM, KC_RESIDUAL,
-  KC_PREPARE_FULL, KC_ATTENTION, KC_ROUTER, KC_SELECT, KC_MOE_GATE, KC_MOE_DOWN, KC_SWIGLU,
-  KC_LOGITS, KC_SHADOW, KC_COUNT
+  KC_EMBED = 0, KC_PROJECT, KC_PREPARE_LINEAR, KC_DELTA, KC_GATED_NORM, KC_RESIDUAL,
+  KC_PREPARE_FULL, KC_ATTENTION, KC_ATTENTION_VALUES, KC_ROUTER, KC_MOE_GATE, KC_MOE_DOWN,
+  KC_SWIGLU, KC_LOGITS, KC_SHADOW, KC_COUNT
 };
 const char* kClassNames[KC_COUNT] = {
-    "embed_rope", "rmsnorm", "project", "linear_prepare", "delta", "gated_norm", "residual_project",
-    "full_prepare", "attention", "moe_router", "moe_select", "moe_gate_up", "moe_down", "swiglu",
-    "logits_argmax", "shadow_copy"};
+    "embed_rope", "project", "linear_prepare", "delta", "gated_norm", "residual_project",
+    "full_prepare", "attention", "attention_values", "moe_router", "moe_gate_up", "moe_down",
+    "swiglu", "logits_argmax", "shadow_copy"};
 
 constexpr int kMaxTimedEvents = 512;
 
@@ -422,13 +433,14 @@ struct cq35_session {
   unsigned long long* d_best = nullptr;
   unsigned long long* h_best = nullptr;  // pinned
   // activations
-  uint16_t *h = nullptr, *attn = nullptr, *xn = nullptr;
+  uint16_t *h = nullptr, *attn = nullptr;
   uint16_t *qkv = nullptr, *conv = nullptr, *z = nullptr, *alpha = nullptr, *beta = nullptr;
   uint16_t *qn = nullptr, *kn = nullptr, *core = nullptr, *gated = nullptr;
   uint16_t *qg = nullptr, *kraw = nullptr, *vraw = nullptr, *qr = nullptr, *ctx = nullptr;
   float* router = nullptr;
   int* ids = nullptr;
   float* probs = nullptr;
+  unsigned* ticket = nullptr;  // router blocks finished (reset by the last one)
   uint16_t* active = nullptr;
   uint16_t* act = nullptr;
   uint16_t* logits = nullptr;
@@ -491,7 +503,6 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   check(dalloc(s, &s->d_best, 1));
   check(dalloc(s, &s->h, d.H));
   check(dalloc(s, &s->attn, d.H));
-  check(dalloc(s, &s->xn, d.H));
   check(dalloc(s, &s->qkv, d.QKV));
   check(dalloc(s, &s->conv, d.QKV));
   check(dalloc(s, &s->z, d.VS));
@@ -509,6 +520,7 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   check(dalloc(s, &s->router, d.E + 1));
   check(dalloc(s, &s->ids, std::max<int64_t>(d.K, 1)));
   check(dalloc(s, &s->probs, std::max<int64_t>(d.K, 1)));
+  check(dalloc(s, &s->ticket, 1));
   check(dalloc(s, &s->active, d.K * d.I + d.SI));
   check(dalloc(s, &s->act, d.I));
   check(dalloc(s, &s->logits, d.V));
@@ -519,10 +531,12 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   s->attn_stride = (int)std::max<int64_t>(tiles * 8 + 2 * tiles + 16, 3 * capacity + 16);
   check(dalloc(s, &s->attn_scratch, d.Q * (int64_t)s->attn_stride));
   if (rc) { destroy_session(s); return rc; }
+  if (const char* g = getenv("CQ35_GRAPH")) s->graph_enabled = atoi(g) != 0;
   e = hipHostMalloc((void**)&s->h_params, (capacity + 1) * sizeof(uint64_t), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_best, sizeof(unsigned long long), hipHostMallocDefault);
   if (e == hipSuccess) e = hipMemset(s->cache, 0, cache_n * sizeof(uint16_t));
   if (e == hipSuccess) e = hipMemset(s->shadow, 0, d.L * d.REC * sizeof(float));
+  if (e == hipSuccess) e = hipMemset(s->ticket, 0, sizeof(unsigned));
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) { destroy_session(s); return fail(CQ35_EDEVICE, "session init: %s", hipGetErrorString(e)); }
   *out = s;
@@ -546,15 +560,106 @@ struct Launcher {
 };
 
 int grid_for(int64_t groups, int64_t cap) { return (int)std::max<int64_t>(1, std::min(groups, cap)); }
-constexpr int64_t kGridCap = 2048;
 
-template <int W, int EPI>
-void project(Launcher& L, int kc, const uint16_t* x, const Segments& seg, int64_t cols,
-             const uint16_t* res) {
-  const int64_t rows = (int64_t)seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
-  constexpr int RPB = 4 * (64 / (W / 4));
-  L(kc, k_project<W, EPI>, dim3(grid_for((rows + RPB - 1) / RPB, kGridCap)), dim3(kBlock),
-    (size_t)cols * 2, x, seg, (int)(cols / 2), res);
+int64_t seg_rows(const Segments& seg) {
+  return (int64_t)seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+}
+
+// Register batch (quads, or dwords for the router) per lane: the smallest
+// instantiated size that covers `per_lane`, capped at the largest.
+int batch_of(int64_t per_lane, std::initializer_list<int> sizes) {
+  int pick = 0;
+  for (int n : sizes) {
+    pick = n;
+    if (per_lane <= n) break;
+  }
+  return pick;
+}
+
+// S256 grouped projection of the normalised hidden row (MoE models).
+void project256(Launcher& L, int kc, const uint16_t* x, const float* norm_w, float eps,
+                const Segments& seg, int64_t cols) {
+  const int64_t per_block = 4 * kRows256;
+  L(kc, k_project256<true>, dim3((unsigned)((seg_rows(seg) + per_block - 1) / per_block)),
+    dim3(kBlock), (size_t)cols * 2, x, norm_w, eps, seg, (int)cols);
+}
+
+// S32 projection of the normalised hidden row (dense models) and, with
+// kArgmax, the vocabulary head with the fused greedy argmax.
+template <bool kArgmax>
+void project32(Launcher& L, int kc, const uint16_t* x, const float* norm_w, float eps,
+               const Segments& seg, int64_t cols, unsigned long long* best) {
+  const dim3 grid((unsigned)((seg_rows(seg) + 31) / 32)), block(kBlock);
+  const size_t lds = (size_t)cols * 2;
+  switch (batch_of((cols / 8 + 7) / 8, {8, 16, 32})) {
+    case 8: L(kc, k_project32<true, kArgmax, 8>, grid, block, lds, x, norm_w, eps, seg, (int)cols, best); break;
+    case 16: L(kc, k_project32<true, kArgmax, 16>, grid, block, lds, x, norm_w, eps, seg, (int)cols, best); break;
+    default: L(kc, k_project32<true, kArgmax, 32>, grid, block, lds, x, norm_w, eps, seg, (int)cols, best); break;
+  }
+}
+
+// bf16(bf16(tree64(x . w_r)) (+) res_r) for the hidden-width outputs
+// (qwen3.fused.residual, simt.hex:442-538).
+void residual(Launcher& L, const uint16_t* x, const void* w, int64_t rows, int64_t cols,
+              const uint16_t* res, uint16_t* out) {
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(64);
+  const size_t lds = (size_t)cols * 2;
+  const uint16_t* wq = static_cast<const uint16_t*>(w);
+  switch (batch_of((cols / 8 + 15) / 16, {8, 16, 32})) {
+    case 8: L(KC_RESIDUAL, k_residual<8>, grid, block, lds, x, wq, (int)rows, (int)cols, res, out); break;
+    case 16: L(KC_RESIDUAL, k_residual<16>, grid, block, lds, x, wq, (int)rows, (int)cols, res, out); break;
+    default: L(KC_RESIDUAL, k_residual<32>, grid, block, lds, x, wq, (int)rows, (int)cols, res, out); break;
+  }
+}
+
+// MoE router + top-k selection (one launch; the last block selects).
+void router_select(Launcher& L, cq35_session* s, const uint16_t* x, const float* norm_w,
+                   const float* w, const float* shared_w) {
+  const Dims& d = s->model->d;
+  const float eps = s->model->cfg.eps;
+  const dim3 grid((unsigned)((d.E + 1 + 3) / 4)), block(kBlock);
+  const size_t lds = router_lds_bytes((int)d.H, (int)d.E);
+  switch (batch_of((d.H + 63) / 64, {8, 16, 32})) {
+    case 8: L(KC_ROUTER, k_router_select<8>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
+    case 16: L(KC_ROUTER, k_router_select<16>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
+    default: L(KC_ROUTER, k_router_select<32>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
+  }
+}
+
+int down_batch(const Dims& d) { return batch_of(((d.K * d.I + d.SI) / 8 + 63) / 64, {4, 8, 12, 16, 24}); }
+
+// Expert down projection + residual + shared expert.
+void moe_down(Launcher& L, cq35_session* s, const void* down, const void* sdown) {
+  const Dims& d = s->model->d;
+  const int per_row = (int)((d.K * d.I + d.SI) / 8);
+  const dim3 grid((unsigned)((d.H + kDownRows - 1) / kDownRows)), block(kBlock);
+  const size_t lds = moe_down_lds_bytes(per_row);
+  const uint16_t* dw = static_cast<const uint16_t*>(down);
+  const uint16_t* sw = static_cast<const uint16_t*>(sdown);
+  const int H = (int)d.H, K = (int)d.K, I = (int)d.I, SI = (int)d.SI;
+  switch (down_batch(d)) {
+    case 4: L(KC_MOE_DOWN, k_moe_down<4>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 8: L(KC_MOE_DOWN, k_moe_down<8>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 12: L(KC_MOE_DOWN, k_moe_down<12>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 16: L(KC_MOE_DOWN, k_moe_down<16>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    default: L(KC_MOE_DOWN, k_moe_down<24>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+  }
+}
+
+// Largest dynamic LDS of the MoE down kernel; above 64 KiB the kernel must
+// be opted in.
+hipError_t moe_down_lds_optin(const Dims& d) {
+  const size_t lds = moe_down_lds_bytes((int)((d.K * d.I + d.SI) / 8));
+  if (lds <= 65536) return hipSuccess;
+  const void* f = nullptr;
+  switch (down_batch(d)) {
+    case 4: f = (const void*)k_moe_down<4>; break;
+    case 8: f = (const void*)k_moe_down<8>; break;
+    case 12: f = (const void*)k_moe_down<12>; break;
+    case 16: f = (const void*)k_moe_down<16>; break;
+    default: f = (const void*)k_moe_down<24>; break;
+  }
+  return hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
 Segments segments(std::initializer_list<std::pair<const void*, std::pair<uint16_t*, int64_t>>> list) {
@@ -588,38 +693,44 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
     auto W = [&](int slot) { return Wt(base + slot); };
     const int64_t key_base = l * 2 * cap * d.KVS;
     const int64_t value_base = key_base + cap * d.KVS;
-    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->h,
-      (const float*)W(0), (int)d.H, d.pad_h, c.eps, s->xn);
+    const float* in_norm = (const float*)W(0);
+    auto project = [&](const Segments& seg) {
+      if (c.moe) project256(L, KC_PROJECT, s->h, in_norm, c.eps, seg, d.H);
+      else project32<false>(L, KC_PROJECT, s->h, in_norm, c.eps, seg, d.H, nullptr);
+    };
     int ffn;
     const float* post_norm;
     if (is_full(c, l)) {
-      Segments seg = segments({{W(1), {s->qg, 2 * d.QS}}, {W(2), {s->kraw, d.KVS}}, {W(3), {s->vraw, d.KVS}}});
-      if (c.moe) project<256, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
-      else project<32, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      project(segments({{W(1), {s->qg, 2 * d.QS}}, {W(2), {s->kraw, d.KVS}}, {W(3), {s->vraw, d.KVS}}}));
       L(KC_PREPARE_FULL, k_full_prepare, dim3((unsigned)(d.Q + d.KVH)), dim3(kBlock), 0,
         (const uint16_t*)s->qg, (const uint16_t*)s->kraw, (const uint16_t*)s->vraw,
         (const float*)s->rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
         value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd,
         (int)d.R, c.eps, s->qr);
       const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
-      if (c.moe)
-        L(KC_ATTENTION, k_attention_online, dim3((unsigned)d.Q), dim3(kAttnBlock), 0,
-          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, value_base,
-          (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
-          (const uint16_t*)s->qg, s->attn_scratch, s->attn_stride, s->ctx);
-      else
+      if (c.moe) {
+        L(KC_ATTENTION, k_attn_scores,
+          dim3((unsigned)std::min<int64_t>((cap + 7) / 8, 512), (unsigned)d.KVH), dim3(kScoreBlock),
+          (size_t)(d.Q / d.KVH) * d.HD * 4, (const uint16_t*)s->qr, (const uint16_t*)s->cache,
+          key_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH),
+          scale, s->attn_scratch, s->attn_stride);
+        L(KC_ATTENTION_VALUES, k_attn_values,
+          dim3((unsigned)d.Q, (unsigned)((d.HD + kValueChannels - 1) / kValueChannels)), dim3(64),
+          attn_values_lds_bytes(cap), (const float*)s->attn_scratch,
+          s->attn_stride, (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t,
+          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->ctx);
+      } else {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, value_base,
           (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
           (const uint16_t*)s->qg, s->attn_scratch, s->attn_stride, s->ctx);
-      project<64, kResidual>(L, KC_RESIDUAL, s->ctx, segments({{W(4), {s->attn, d.H}}}), d.QS, s->h);
+      }
+      residual(L, s->ctx, W(4), d.H, d.QS, s->h, s->attn);
       post_norm = (const float*)W(7);
       ffn = 8;
     } else {
-      Segments seg = segments({{W(1), {s->qkv, d.QKV}}, {W(2), {s->z, d.VS}},
-                               {W(3), {s->alpha, c.value_heads}}, {W(4), {s->beta, c.value_heads}}});
-      if (c.moe) project<256, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
-      else project<32, kStoreBf16>(L, KC_PROJECT, s->xn, seg, d.H, nullptr);
+      project(segments({{W(1), {s->qkv, d.QKV}}, {W(2), {s->z, d.VS}},
+                        {W(3), {s->alpha, c.value_heads}}, {W(4), {s->beta, c.value_heads}}}));
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       L(KC_PREPARE_LINEAR, k_linear_prepare, dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim)),
         dim3(kBlock), 0, (const uint16_t*)s->qkv, s->cache, conv_base, (const uint64_t*)s->d_params,
@@ -641,43 +752,33 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       L(KC_GATED_NORM, k_gated_norm, dim3((unsigned)c.value_heads), dim3(kBlock), 0,
         (const uint16_t*)s->core, (const uint16_t*)s->z, (const float*)W(7), c.value_dim, c.eps,
         s->gated);
-      project<64, kResidual>(L, KC_RESIDUAL, s->gated, segments({{W(8), {s->attn, d.H}}}), d.VS, s->h);
+      residual(L, s->gated, W(8), d.H, d.VS, s->h, s->attn);
       post_norm = (const float*)W(10);
       ffn = 11;
     }
-    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->attn,
-      post_norm, (int)d.H, d.pad_h, c.eps, s->xn);
     if (c.moe) {
-      L(KC_ROUTER, k_router, dim3(grid_for((d.E + 1 + 31) / 32, kGridCap)), dim3(kBlock),
-        (size_t)d.H * 2, (const uint16_t*)s->xn, (const float*)W(ffn), (const float*)W(ffn + 4),
-        (int)d.E, (int)(d.H / 2), s->router);
-      L(KC_SELECT, k_moe_select, dim3(1), dim3(kBlock), 0, (const float*)s->router, (int)d.E,
-        (int)d.K, s->ids, s->probs);
+      router_select(L, s, s->attn, post_norm, (const float*)W(ffn), (const float*)W(ffn + 4));
       const int64_t rows = d.K * d.I + d.SI;
-      L(KC_MOE_GATE, k_moe_gate, dim3(grid_for((rows + 3) / 4, kGridCap)), dim3(kBlock),
-        (size_t)d.H * 2, (const uint16_t*)s->xn, (const uint16_t*)W(ffn + 1),
-        (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6),
-        (const int*)s->ids, (const float*)s->probs, (const float*)s->router, (int)d.E, (int)d.K,
-        (int)d.I, (int)d.SI, (int)(d.H / 2), s->active);
-      L(KC_MOE_DOWN, k_moe_down, dim3(grid_for((d.H + 31) / 32, kGridCap)), dim3(kBlock),
-        (size_t)(d.K * d.I + d.SI) * 2, (const uint16_t*)s->active, (const uint16_t*)W(ffn + 3),
-        (const uint16_t*)W(ffn + 7), (const int*)s->ids, (const uint16_t*)s->attn, (int)d.H,
-        (int)d.K, (int)d.I, (int)d.SI, s->h);
+      L(KC_MOE_GATE, k_gate_up<true>, dim3((unsigned)((rows + 4 * kRowsGate - 1) / (4 * kRowsGate))),
+        dim3(kBlock), (size_t)d.H * 2, (const uint16_t*)s->attn, post_norm, c.eps, (int)d.H,
+        (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
+        (const uint16_t*)W(ffn + 6), (const int*)s->ids, (const float*)s->probs,
+        (const float*)s->router, (int)d.E, (int)d.K, (int)d.I, (int)d.SI, s->active);
+      moe_down(L, s, W(ffn + 3), W(ffn + 7));
     } else {
-      L(KC_SWIGLU, k_swiglu, dim3(grid_for((d.I + 3) / 4, kGridCap)), dim3(kBlock), (size_t)d.H * 2,
-        (const uint16_t*)s->xn, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1), (int)d.I,
-        (int)(d.H / 2), s->act);
-      project<64, kResidual>(L, KC_RESIDUAL, s->act, segments({{W(ffn + 2), {s->h, d.H}}}), d.I, s->attn);
+      L(KC_SWIGLU, k_gate_up<false>, dim3((unsigned)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate))),
+        dim3(kBlock), (size_t)d.H * 2, (const uint16_t*)s->attn, post_norm, c.eps, (int)d.H,
+        (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1), (const uint16_t*)nullptr,
+        (const uint16_t*)nullptr, (const int*)nullptr, (const float*)nullptr, (const float*)nullptr,
+        0, 0, (int)d.I, 0, s->act);
+      residual(L, s->act, W(ffn + 2), d.H, d.I, s->attn, s->h);
     }
     base += layer_tensors(c, l);
   }
   if (last) {
     const int64_t total = weight_count(c);
-    L(KC_NORM, k_rmsnorm, dim3(1), dim3(kBlock), (size_t)d.pad_h * 4, (const uint16_t*)s->h,
-      (const float*)Wt(total - 2), (int)d.H, d.pad_h, c.eps, s->xn);
-    L(KC_LOGITS, k_logits, dim3(grid_for((d.V + 31) / 32, kGridCap)), dim3(kBlock), (size_t)d.H * 2,
-      (const uint16_t*)s->xn, (const uint16_t*)Wt(total - 1), (int)d.V, (int)(d.H / 2), s->logits,
-      s->d_best);
+    project32<true>(L, KC_LOGITS, s->h, (const float*)Wt(total - 2), c.eps,
+                    segments({{Wt(total - 1), {s->logits, d.V}}}), d.H, s->d_best);
   }
 }
 
@@ -717,6 +818,17 @@ extern "C" int cq35_session_init(cq35_model* m, int64_t capacity, cq35_session**
   if (capacity <= 0) return fail(CQ35_EINVAL, "cache capacity must be non-zero");
   if (capacity > 262144) return fail(CQ35_ERANGE, "cache capacity %lld exceeds the model maximum 262144", (long long)capacity);
   HIP_TRY(hipSetDevice(m->device));
+  if (m->cfg.moe) {
+    // The exact-order attention keeps every key's weight of a head in LDS.
+    const size_t lds = attn_values_lds_bytes(capacity);
+    if (lds > 65536 &&
+        hipFuncSetAttribute((const void*)k_attn_values, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return fail(CQ35_EUNSUPPORTED, "capacity %lld needs %zu bytes of LDS for exact-order attention",
+                  (long long)capacity, lds);
+    if (moe_down_lds_optin(m->d) != hipSuccess)
+      return fail(CQ35_EUNSUPPORTED, "expert widths need more LDS than the device grants");
+  }
   return create_session(m, capacity, out);
 }
 
@@ -911,7 +1023,7 @@ extern "C" int cq35_device_numeric(int op, const float* input, float* output, in
 
 extern "C" int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
                                 int width, uint16_t* out) {
-  if (!x || !w || !out || rows <= 0 || cols <= 0 || cols % 2 || rows > (1 << 30))
+  if (!x || !w || !out || rows <= 0 || cols <= 0 || cols % 2 || rows > (1 << 30) || cols > 32768)
     return fail(CQ35_EINVAL, "bad GEMV shape");
   if (width != 32 && width != 64 && width != 256) return fail(CQ35_EINVAL, "tree width must be 32, 64 or 256");
   // Zero-pad the pairs to a multiple of 4: extra pairs add +-0 to a lane
@@ -932,13 +1044,26 @@ extern "C" int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t ro
     seg.out[0] = dout;
     seg.rows[0] = (int)rows;
     seg.count = 1;
-    const int pairs = (int)(padded / 2);
+    const int n = (int)padded;
     const size_t lds = (size_t)padded * 2;
-    const int rpb = 4 * (64 / (width / 4));
-    const int grid = grid_for((rows + rpb - 1) / rpb, kGridCap);
-    if (width == 32) k_project<32, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
-    else if (width == 64) k_project<64, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
-    else k_project<256, kStoreBf16><<<grid, kBlock, lds>>>(dx, seg, pairs, nullptr);
+    if (width == 32) {
+      const unsigned grid = (unsigned)((rows + 31) / 32);
+      switch (batch_of((n / 8 + 7) / 8, {8, 16, 32})) {
+        case 8: k_project32<false, false, 8><<<grid, kBlock, lds>>>(dx, nullptr, 0.0f, seg, n, nullptr); break;
+        case 16: k_project32<false, false, 16><<<grid, kBlock, lds>>>(dx, nullptr, 0.0f, seg, n, nullptr); break;
+        default: k_project32<false, false, 32><<<grid, kBlock, lds>>>(dx, nullptr, 0.0f, seg, n, nullptr); break;
+      }
+    } else if (width == 64) {
+      const unsigned grid = (unsigned)((rows + 3) / 4);
+      switch (batch_of((n / 8 + 15) / 16, {8, 16, 32})) {
+        case 8: k_residual<8><<<grid, 64, lds>>>(dx, dw, (int)rows, n, nullptr, dout); break;
+        case 16: k_residual<16><<<grid, 64, lds>>>(dx, dw, (int)rows, n, nullptr, dout); break;
+        default: k_residual<32><<<grid, 64, lds>>>(dx, dw, (int)rows, n, nullptr, dout); break;
+      }
+    } else {
+      const unsigned grid = (unsigned)((rows + 4 * kRows256 - 1) / (4 * kRows256));
+      k_project256<false><<<grid, kBlock, lds>>>(dx, nullptr, 0.0f, seg, n);
+    }
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipMemcpy(out, dout, rows * 2, hipMemcpyDeviceToHost);
