@@ -51,6 +51,22 @@ def device_sync():
         pass
 
 
+def copy_probe(megabytes: int) -> None:
+    """One device-to-device copy of a known size (the runtime's copy kernel),
+    so hardware-counter passes can scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = megabytes << 20
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(n)) or hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(n)):
+        raise RuntimeError("hipMalloc failed for the copy probe")
+    hip.hipMemset(src, 0x3C, ctypes.c_size_t(n))
+    hip.hipMemcpy(dst, src, ctypes.c_size_t(n), 3)  # hipMemcpyDeviceToDevice
+    hip.hipDeviceSynchronize()
+    hip.hipFree(src)
+    hip.hipFree(dst)
+    log(f"copy probe: {megabytes} MiB device-to-device")
+
+
 def kernel_bytes(cfg: dict, context: int) -> dict:
     """Algorithmic HBM bytes per launch of each streaming kernel class."""
     import cq35
@@ -77,6 +93,19 @@ def kernel_bytes(cfg: dict, context: int) -> dict:
     else:
         out["swiglu"] = (2 * cfg["intermediate"] * H * 2, cfg["layers"])
     return out
+
+
+def measured_traffic(config: str) -> dict:
+    """HBM bytes per dispatch by kernel class from the committed counter
+    summary (two rocprofv3 --pmc passes, FETCH_SIZE then WRITE_SIZE, scaled
+    by a copy of known size); empty when none exists for this config."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{config.replace('qwen36-', '').replace('-', '_')}.md")
+    try:
+        text = open(path).read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(block)
+    except (OSError, IndexError, ValueError):
+        return {}
 
 
 def measure_kernels(session, tokens, classes, steps_each):
@@ -146,16 +175,21 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernel-timing", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
-    ap.add_argument("--cpu-steps", type=int, default=6)
+    ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=25.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="first run one device copy of this size (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "see DESIGN.md for how the token loop would shard.", file=sys.stderr)
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The token loop would shard by placing whole sessions per GPU, with no communication.",
+              file=sys.stderr)
         return 2
 
     import cq35
     cfg = cq35.preset(args.config)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
     t0 = time.time()
     model = cq35.Model.synthetic(cfg, seed=args.seed)
     log(f"weights: {model.weight_bytes() / 1e9:.2f} GB generated on device in {time.time() - t0:.1f}s")
@@ -209,8 +243,10 @@ def main() -> int:
         by, _ = kb[dom]
         avg_s = kernels[dom]["avg_launch_us"] / 1e6
         achieved = by / avg_s / 1e9
+        tr = measured_traffic(args.config).get(dom)
+        traffic = tr["fetch_bytes"] + tr["write_bytes"] if tr else None
         roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS,
-                        unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                        unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
                         bytes_per_launch=int(by), avg_launch_us=round(kernels[dom]["avg_launch_us"], 2))
         for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
             log(f"  {k:18s} {v['ms_per_step']:.3f} ms/step  {v['avg_launch_us']:.1f} us/launch"

@@ -42,7 +42,7 @@ def _moe(**kw):
 
 
 PRESETS = {
-    # 4 layers (3 DeltaNet + 1 gated attention), hidden
+    # The benchmark's CPU-runnable tiny case: 4 layers (3 DeltaNet + 1 gated attention), hidden
     # 256, DeltaNet 4 QK / 8 V heads of dim 32, attention 4 Q / 1 KV heads of
     # dim 64 (rotary 16 = head_dim/4, the Qwen3.5 partial-rotary ratio), FFN
     # 768, vocab 4096.
@@ -53,7 +53,7 @@ PRESETS = {
     "qwen35-0.8b": _dense(vocab=248_320, hidden=1024, intermediate=3584, layers=24,
                           q_heads=8, kv_heads=2, head_dim=256, rope_dim=64, key_heads=16,
                           key_dim=128, value_heads=16, value_dim=128, tied=1),
-    # BASELINE configs[2]
+    # The benchmark's 2B-shaped dense case
     "qwen35-2b": _dense(vocab=248_320, hidden=2048, intermediate=6144, layers=24,
                         q_heads=8, kv_heads=2, head_dim=256, rope_dim=64, key_heads=16,
                         key_dim=128, value_heads=32, value_dim=128, tied=1),

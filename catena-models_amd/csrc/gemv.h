@@ -59,22 +59,45 @@ __device__ __forceinline__ void quad_acc(Quad& a, const u32x4& x, const u32x4& w
   a.lo[3] += lo2f(x.w) * lo2f(w.w); a.hi[3] += hi2f(x.w) * hi2f(w.w);
 }
 
+// Value of lane i + S as seen from lane i, for the lanes a tree level uses:
+// S <= 8 within a 16-lane row (DPP row shift; lanes past the row end read
+// +0 and are never used), S = 16 for rows 0 and 2 (permlane16 swap), S = 32
+// for lanes 0-31 (permlane32 swap). No LDS traffic, unlike a bpermute.
+template <int S>
+__device__ __forceinline__ float lane_down(float v) {
+  const int b = __builtin_bit_cast(int, v);
+  if constexpr (S == 32) {
+    return __builtin_bit_cast(float, (int)__builtin_amdgcn_permlane32_swap(b, b, false, false)[1]);
+  } else if constexpr (S == 16) {
+    return __builtin_bit_cast(float, (int)__builtin_amdgcn_permlane16_swap(b, b, false, false)[1]);
+  } else {
+    static_assert(S == 1 || S == 2 || S == 4 || S == 8, "DPP row shift");
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x100 + S, 0xf, 0xf, true));
+  }
+}
+
 // Halving tree of width W = 4*LPR over the reference lanes held by the LPR
-// physical lanes of a row group. Must be reached by every lane of the wave.
-// The result is valid in the group's first lane.
+// physical lanes of a row group (reference stride 4s = physical stride s,
+// then strides 2 and 1 inside the lane). Must be reached by every lane of
+// the wave. The result is valid in the group's first lane.
+template <int LPR, int S = LPR / 2>
+__device__ __forceinline__ void tree_levels(float& v0, float& v1, float& v2, float& v3) {
+  if constexpr (S >= 1) {
+    v0 += lane_down<S>(v0);
+    v1 += lane_down<S>(v1);
+    v2 += lane_down<S>(v2);
+    v3 += lane_down<S>(v3);
+    tree_levels<LPR, S / 2>(v0, v1, v2, v3);
+  }
+}
+
 template <int LPR>
 __device__ __forceinline__ float quad_tree(const Quad& a) {
   float v0 = a.lo[0] + a.hi[0];
   float v1 = a.lo[1] + a.hi[1];
   float v2 = a.lo[2] + a.hi[2];
   float v3 = a.lo[3] + a.hi[3];
-#pragma unroll
-  for (int s = LPR / 2; s >= 1; s >>= 1) {
-    v0 += __shfl_down(v0, s, 64);
-    v1 += __shfl_down(v1, s, 64);
-    v2 += __shfl_down(v2, s, 64);
-    v3 += __shfl_down(v3, s, 64);
-  }
+  tree_levels<LPR>(v0, v1, v2, v3);
   v0 += v2;
   v1 += v3;
   return v0 + v1;
@@ -139,8 +162,12 @@ __device__ __forceinline__ u32x4 octet_scale(const u32x4& v, float inverse, cons
 
 // Thread-total -> block-total: shuffle tree over the wave, then the waves.
 __device__ __forceinline__ float block_ap_sum(float t, float* red) {
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) t = t + __shfl_down(t, s, 64);
+  t = t + lane_down<1>(t);
+  t = t + lane_down<2>(t);
+  t = t + lane_down<4>(t);
+  t = t + lane_down<8>(t);
+  t = t + lane_down<16>(t);
+  t = t + lane_down<32>(t);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
   __syncthreads();
   return (red[0] + red[1]) + (red[2] + red[3]);
@@ -243,11 +270,12 @@ __device__ __forceinline__ uint16_t* segment_out(const Segments& seg, int s) {
 // S256 (64 lanes per row): each wave streams kRows256 rows, each lane four
 // quads of each per batch (cols <= 2048 is one batch). Output bf16 of the
 // tree (simt.hex:400-410). kNorm: the input is the hidden row normalised in
-// the prologue; otherwise it is used as given.
+// the prologue; otherwise it is used as given. Held to 128 VGPRs so four
+// blocks fit per CU and a 12352-row DeltaNet projection runs in one round.
 constexpr int kRows256 = 4;
 
 template <bool kNorm>
-__global__ __launch_bounds__(kBlock) void k_project256(const uint16_t* __restrict__ x,
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void k_project256(const uint16_t* __restrict__ x,
                                                         const float* __restrict__ norm_w, float eps,
                                                         Segments seg, int cols) {
   constexpr int RW = kRows256, NQ = 4;
@@ -261,44 +289,44 @@ __global__ __launch_bounds__(kBlock) void k_project256(const uint16_t* __restric
   CopyIn<1> cin;
   if (kNorm) norm_prefetch(nin, x, norm_w, cols);
   else copy_prefetch(cin, x, cols);
-  const uint16_t* wr[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
+  // Row r's weights; recomputed for later batches so no pointer stays live.
+  auto row_w = [&](int r) {
     int local;
     const int s = segment_of(seg, min(row0 + r, total - 1), &local);
-    wr[r] = segment_w(seg, s) + (size_t)local * cols;
-  }
+    return segment_w(seg, s) + (size_t)local * cols;
+  };
   u32x4 wv[RW][NQ];
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+  for (int r = 0; r < RW; ++r) {
+    const uint16_t* wr = row_w(r);
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) wv[r][j] = ldq(wr[r], min(lane + 64 * j, quads - 1));
+    for (int j = 0; j < NQ; ++j) wv[r][j] = ldq(wr, min(lane + 64 * j, quads - 1));
+  }
   if (kNorm) norm_finish(nin, xs, x, norm_w, cols, eps, red);
   else copy_finish(cin, xs, x, cols);
-  Quad acc[RW];
+  u32x4 xq[NQ];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) quad_zero(acc[r]);
-  for (int b = 0; b * 64 * NQ < quads; ++b) {
-    if (b > 0) {
-#pragma unroll
-      for (int r = 0; r < RW; ++r)
-#pragma unroll
-        for (int j = 0; j < NQ; ++j)
-          wv[r][j] = ldq(wr[r], min(lane + 64 * (NQ * b + j), quads - 1));
-    }
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const int qi = lane + 64 * (NQ * b + j);
-      if (qi < quads) {
-        const u32x4 xq = xs[qi];
-#pragma unroll
-        for (int r = 0; r < RW; ++r) quad_acc(acc[r], xq, wv[r][j]);
-      }
-    }
-  }
+  for (int j = 0; j < NQ; ++j) xq[j] = xs[min(lane + 64 * j, quads - 1)];
+  // One row at a time: row r's tree overlaps the arrival of row r+1.
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    const float v = quad_tree<64>(acc[r]);
+    Quad acc;
+    quad_zero(acc);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+      if (lane + 64 * j < quads) quad_acc(acc, xq[j], wv[r][j]);
+    // Rows wider than 64 * NQ quads (hidden > 2048): remaining batches.
+    for (int b = 1; b * 64 * NQ < quads; ++b) {
+      const uint16_t* wr = row_w(r);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) wv[r][j] = ldq(wr, min(lane + 64 * (NQ * b + j), quads - 1));
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int qi = lane + 64 * (NQ * b + j);
+        if (qi < quads) quad_acc(acc, xs[qi], wv[r][j]);
+      }
+    }
+    const float v = quad_tree<64>(acc);
     if (lane == 0 && row0 + r < total) {
       int local;
       const int s = segment_of(seg, row0 + r, &local);
@@ -476,43 +504,89 @@ __global__ __launch_bounds__(kBlock) void k_router_select(
       if (i < cols) acc += bf2f(xe[i]) * wv[j];
     }
   }
-  float v = acc + __shfl_down(acc, 1, 64);
-#pragma unroll
-  for (int s = 16; s >= 1; s >>= 1) v += __shfl_down(v, 2 * s, 64);
-  if (lane == 0 && row < rows) logits[row] = v;
+  // lane 2r: lo_r + hi_r, then reference strides 16..1 = physical 32..2
+  float v = acc + lane_down<1>(acc);
+  v += lane_down<32>(v);
+  v += lane_down<16>(v);
+  v += lane_down<8>(v);
+  v += lane_down<4>(v);
+  v += lane_down<2>(v);
+  if (lane == 0 && row < rows)
+    __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  __threadfence();
+  // The logits went out as device-coherent stores; once every wave's stores
+  // have completed, one ticket per block tells the last block it may read
+  // them all.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    last = atomicAdd(ticket, 1u) == gridDim.x - 1;
-  }
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           gridDim.x - 1;
   __syncthreads();
   if (!last) return;
-  __threadfence();
   float* lg = reinterpret_cast<float*>(xs);  // the staged row is no longer needed
-  __syncthreads();
-  for (int e = threadIdx.x; e < experts; e += blockDim.x)
-    lg[e] = __hip_atomic_load(logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __shared__ int any_nan;
+  if (threadIdx.x == 0) any_nan = 0;
   __syncthreads();
   for (int e = threadIdx.x; e < experts; e += blockDim.x) {
-    const float le = lg[e];
-    int rank = 0;
-    for (int i = 0; i < experts; ++i) {
-      const float o = lg[i];
-      rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+    const float le = __hip_atomic_load(logits + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lg[e] = le;
+    if (le != le) any_nan = 1;
+  }
+  __syncthreads();
+  if (!any_nan) {
+    // Without NaNs the rank order is the stable descending order: top_k
+    // rounds of a wave-wide maximum of (value, lowest index) keys.
+    if (wave == 0) {
+      unsigned long long taken = 0;  // bit j: lane's j-th candidate chosen (experts <= 4096)
+      for (int k = 0; k < top_k; ++k) {
+        unsigned long long mine = 0ull;
+        for (int j = 0, e = lane; e < experts; ++j, e += 64) {
+          if ((taken >> j) & 1ull) continue;
+          const float le = lg[e];
+          const uint32_t u = le == 0.0f ? 0u : fbits(le);
+          const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+          const unsigned long long key =
+              ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
+          mine = key > mine ? key : mine;
+        }
+        unsigned long long best = mine;
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) {
+          const unsigned long long o = __shfl_xor(best, s, 64);
+          best = o > best ? o : best;
+        }
+        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+        if ((e & 63) == lane) taken |= 1ull << (e >> 6);
+        if (lane == 0) {
+          ids[k] = e;
+          chosen[k] = lg[e];
+        }
+      }
     }
-    if (rank < top_k) {
-      ids[rank] = e;
-      chosen[rank] = le;
+  } else {
+    // rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}
+    for (int e = threadIdx.x; e < experts; e += blockDim.x) {
+      const float le = lg[e];
+      int rank = 0;
+      for (int i = 0; i < experts; ++i) {
+        const float o = lg[i];
+        rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+      }
+      if (rank < top_k) {
+        ids[rank] = e;
+        chosen[rank] = le;
+      }
     }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (wave == 0) {
+    // p_j = exp(l_j - l_0) / den, den summed left to right from 0.
+    const float ex = lane < top_k ? hexp(chosen[lane] - chosen[0]) : 0.0f;
     float den = 0.0f;
-    for (int j = 0; j < top_k; ++j) den = den + hexp(chosen[j] - chosen[0]);
-    for (int j = 0; j < top_k; ++j) probs[j] = hexp(chosen[j] - chosen[0]) / den;
-    *ticket = 0u;
+    for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
+    if (lane < top_k) probs[lane] = ex / den;
+    if (lane == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -527,11 +601,12 @@ inline size_t router_lds_bytes(int cols, int experts) {
 // MoE rows [0, K*I) belong to the selected experts in rank order, rows
 // [K*I, K*I+SI) to the shared expert. Routed: bf16(silu(g) * u * p_slot);
 // shared: bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)); dense:
-// bf16(bf16(silu(bf16 g)) * bf16(u)). kRowsGate rows per wave.
-constexpr int kRowsGate = 2;
+// bf16(bf16(silu(bf16 g)) * bf16(u)). kRowsGate rows per wave (at the
+// 35B-A3B shape 9216 rows = 768 blocks, one per resident slot).
+constexpr int kRowsGate = 3;
 
 template <bool kMoE>
-__global__ __launch_bounds__(kBlock) void k_gate_up(
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) void k_gate_up(
     const uint16_t* __restrict__ x, const float* __restrict__ norm_w, float eps, int cols,
     const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
     const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ sup,
@@ -548,65 +623,66 @@ __global__ __launch_bounds__(kBlock) void k_gate_up(
   const int row0 = (blockIdx.x * 4 + wave) * RW;
   NormIn nin;
   norm_prefetch(nin, x, norm_w, cols);
-  const uint16_t *wg[RW], *wu[RW];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
+  // Gate and up rows of row r (recomputed for later batches so no pointer
+  // stays live).
+  auto row_ptrs = [&](int r, const uint16_t*& g, const uint16_t*& u) {
     const int row = min(row0 + r, rows - 1);
     if (!kMoE) {
-      wg[r] = gate + (size_t)row * cols;
-      wu[r] = up + (size_t)row * cols;
+      g = gate + (size_t)row * cols;
+      u = up + (size_t)row * cols;
     } else if (row < routed_rows) {
       const int slot = row / inter;
       const size_t e = (size_t)ids[slot] * inter + (row - slot * inter);
-      wg[r] = gate + e * cols;
-      wu[r] = up + e * cols;
+      g = gate + e * cols;
+      u = up + e * cols;
     } else {
-      wg[r] = sgate + (size_t)(row - routed_rows) * cols;
-      wu[r] = sup + (size_t)(row - routed_rows) * cols;
+      g = sgate + (size_t)(row - routed_rows) * cols;
+      u = sup + (size_t)(row - routed_rows) * cols;
     }
-  }
+  };
   u32x4 gv[RW][NQ], uv[RW][NQ];
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
+  for (int r = 0; r < RW; ++r) {
+    const uint16_t *wg, *wu;
+    row_ptrs(r, wg, wu);
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
-      gv[r][j] = ldq(wg[r], min(lane + 64 * j, quads - 1));
-      uv[r][j] = ldq(wu[r], min(lane + 64 * j, quads - 1));
+      gv[r][j] = ldq(wg, min(lane + 64 * j, quads - 1));
+      uv[r][j] = ldq(wu, min(lane + 64 * j, quads - 1));
     }
+  }
   norm_finish(nin, xs, x, norm_w, cols, eps, red);
-  Quad ga[RW], ua[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
-    quad_zero(ga[r]);
-    quad_zero(ua[r]);
-  }
-  for (int b = 0; b * 64 * NQ < quads; ++b) {
-    if (b > 0) {
+    Quad ga, ua;
+    quad_zero(ga);
+    quad_zero(ua);
 #pragma unroll
-      for (int r = 0; r < RW; ++r)
+    for (int j = 0; j < NQ; ++j)
+      if (lane + 64 * j < quads) {
+        const u32x4 xq = xs[lane + 64 * j];
+        quad_acc(ga, xq, gv[r][j]);
+        quad_acc(ua, xq, uv[r][j]);
+      }
+    for (int b = 1; b * 64 * NQ < quads; ++b) {  // hidden > 2048
+      const uint16_t *wg, *wu;
+      row_ptrs(r, wg, wu);
 #pragma unroll
-        for (int j = 0; j < NQ; ++j) {
-          gv[r][j] = ldq(wg[r], min(lane + 64 * (NQ * b + j), quads - 1));
-          uv[r][j] = ldq(wu[r], min(lane + 64 * (NQ * b + j), quads - 1));
-        }
-    }
+      for (int j = 0; j < NQ; ++j) {
+        gv[r][j] = ldq(wg, min(lane + 64 * (NQ * b + j), quads - 1));
+        uv[r][j] = ldq(wu, min(lane + 64 * (NQ * b + j), quads - 1));
+      }
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const int qi = lane + 64 * (NQ * b + j);
-      if (qi < quads) {
-        const u32x4 xq = xs[qi];
-#pragma unroll
-        for (int r = 0; r < RW; ++r) {
-          quad_acc(ga[r], xq, gv[r][j]);
-          quad_acc(ua[r], xq, uv[r][j]);
+      for (int j = 0; j < NQ; ++j) {
+        const int qi = lane + 64 * (NQ * b + j);
+        if (qi < quads) {
+          quad_acc(ga, xs[qi], gv[r][j]);
+          quad_acc(ua, xs[qi], uv[r][j]);
         }
       }
     }
-  }
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const float gsum = quad_tree<64>(ga[r]);
-    const float usum = quad_tree<64>(ua[r]);
+    const float gsum = quad_tree<64>(ga);
+    const float usum = quad_tree<64>(ua);
     const int row = row0 + r;
     if (lane == 0 && row < rows) {
       if (!kMoE) {

@@ -6,6 +6,7 @@
 // -> Artifact::exec_values("qwen3")), src/qwen/qwen35.rs:1374-1650 (the
 // generated token fold), src/model.rs:248-258 (qwen3.init).
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <algorithm>
 #include <cmath>
@@ -550,11 +551,14 @@ struct Launcher {
   template <typename Kernel, typename... Args>
   void operator()(int kc, Kernel kernel, dim3 grid, dim3 block, size_t lds, Args... args) {
     const bool timed = s->timed_class == kc && s->ev_used < kMaxTimedEvents;
-    if (timed) hipEventRecord(s->ev[2 * s->ev_used], s->stream);
-    kernel<<<grid, block, lds, s->stream>>>(args...);
     if (timed) {
-      hipEventRecord(s->ev[2 * s->ev_used + 1], s->stream);
+      // Events stamped by the dispatch packet itself, so the interval is the
+      // kernel's execution as a profiler sees it, without event-record gaps.
+      hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s->stream, s->ev[2 * s->ev_used],
+                            s->ev[2 * s->ev_used + 1], 0, args...);
       ++s->ev_used;
+    } else {
+      kernel<<<grid, block, lds, s->stream>>>(args...);
     }
   }
 };

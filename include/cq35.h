@@ -98,8 +98,12 @@ int cq35_model_create(const cq35_config* cfg, const void* const* weights, int on
                       cq35_model** out);
 
 /* Same, with weights produced on the device by the library's counter-based
- * synthetic generator (seeded BF16 ~N(0, 0.02) matrices; see DESIGN).
- * Used for benchmarks and parity tests without a checkpoint. */
+ * synthetic generator: per tensor t and element i, SplitMix64 finaliser of
+ * mix64(seed ^ mix64(t + 1)) + i * 0x9E3779B97F4A7C15, Irwin-Hall(4)
+ * normals; BF16 matrices ~N(0, 0.02), norms 1 + N(0, 0.02), dt 1,
+ * A = -(1 + 15u), conv N(0, 0.3), router N(0, 0.04), shared gate N(0, 0.02).
+ * No reference counterpart: for benchmarks and parity tests without a
+ * checkpoint. */
 int cq35_model_create_synthetic(const cq35_config* cfg, uint64_t seed, cq35_model** out);
 int cq35_model_free(cq35_model* model);
 int cq35_model_config(const cq35_model* model, cq35_config* out);
@@ -134,10 +138,11 @@ int cq35_session_state_bytes(const cq35_session* session, int which, int64_t* by
 int cq35_session_export_state(const cq35_session* session, int which, void* dst, int64_t bytes);
 int cq35_session_import_state(cq35_session* session, int which, const void* src, int64_t bytes);
 
-/* Measurement hooks: bracket every launch of one kernel class with HIP
- * events on the session stream (class ids: see cq35_kernel_class_name);
- * -1 disables. Results accumulate until read. Decode-step graph replay is
- * suspended while timing is on. */
+/* Measurement hooks (no reference counterpart): time every launch of one
+ * kernel class with start/stop events stamped by its dispatch packet on the
+ * session stream (class ids: see cq35_kernel_class_name); -1 disables.
+ * Results accumulate until read. Decode-step graph replay is suspended while
+ * timing is on. */
 int cq35_session_time_kernel(cq35_session* session, int kernel_class);
 int cq35_session_kernel_time(cq35_session* session, double* total_ms, int64_t* launches);
 const char* cq35_kernel_class_name(int kernel_class);

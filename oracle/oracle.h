@@ -7,6 +7,32 @@
  * reference Hex kernels (file:line citations are into hellas-ai/catena-models).
  * Arithmetic is plain IEEE binary32 with FMA contraction disabled
  * (build with -ffp-contract=off), matching numeric.hex:10.
+ *
+ * How each part is pinned (the reference itself cannot run here: its compiler
+ * crate catena-lang is not in the tree and there is no Rust toolchain):
+ *  - ox_f2bf / BF16 add and mul: RNE closed form over all exponent classes,
+ *    and the bit-exact epilogues of the known-answer fixtures.
+ *  - ox_exp: the reference's accuracy contract (tests/support/
+ *    portable_exp.cpp:26-102: <= 1 ULP against float64, exact specials,
+ *    NaN -> 0x7fc00000), with a planted-mistake check.
+ *  - ox_sqrt / ox_softplus / ox_sincos: closed forms (Newton limit, log1p(e^x),
+ *    sin/cos) at their documented accuracy.
+ *  - ox_project, ox_residual_project, grouped projections, router, MoE down
+ *    (S32 / S64 / S256 trees, split lo/hi accumulators, BF16 epilogues):
+ *    bit-exact known answers from the generators of tests/qwen35_simt.rs
+ *    (129-436), plus F32 random-dot fixtures that a wrong tree width fails.
+ *  - ox_moe_gate_rows: within the reference test's own 1% bar
+ *    (tests/qwen35_simt.rs:309-389).
+ *  - ox_step (conv, L2 norms, gated delta rule, gated RMSNorm, online and
+ *    staged attention, top-k, argmax, F32 multi-token fold): against a float64
+ *    textbook formulation (relative RMS of logits < 0.15, a planted
+ *    key-head-mapping mistake > 0.6). The exact orders inside these (D32, AP,
+ *    SER, dense-staged, CONV) are therefore pinned only to tolerance:
+ *    "parity partial".
+ *  - parity unpinned: stdlib.math.round_to_u32 at exact .5 ties (taken as
+ *    ties away from zero), f32.max with NaN operands, bf16x2 low/high order
+ *    (taken as little-endian), core.fold.bounded order (taken as ascending).
+ *    Their definitions live in catena-lang, which is absent.
  */
 #ifndef CQ35_ORACLE_H
 #define CQ35_ORACLE_H
