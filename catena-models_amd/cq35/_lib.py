@@ -59,6 +59,8 @@ def load():
         "cq35_kernel_class_name": ([ctypes.c_int], ctypes.c_char_p),
         "cq35_kernel_class_count": ([], ctypes.c_int),
         "cq35_session_set_graph": ([P, ctypes.c_int], ctypes.c_int),
+        "cq35_session_set_persistent": ([P, ctypes.c_int], ctypes.c_int),
+        "cq35_session_persistent": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "cq35_numeric_exp": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_sqrt": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_softplus": ([ctypes.c_float], ctypes.c_float),
@@ -87,6 +89,7 @@ EXPORTED = [
     "cq35_session_free", "cq35_step", "cq35_session_copy", "cq35_session_state_bytes",
     "cq35_session_export_state", "cq35_session_import_state", "cq35_session_time_kernel",
     "cq35_session_kernel_time", "cq35_kernel_class_name", "cq35_kernel_class_count",
-    "cq35_session_set_graph", "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
+    "cq35_session_set_graph", "cq35_session_set_persistent", "cq35_session_persistent",
+    "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
     "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv",
 ]

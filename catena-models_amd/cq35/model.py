@@ -215,6 +215,17 @@ class Session:
     def set_graph(self, enabled: bool) -> None:
         check(_lib.load().cq35_session_set_graph(self._h, 1 if enabled else 0))
 
+    def set_persistent(self, enabled: bool) -> None:
+        """Decode steps through the persistent one-launch kernel (MoE shapes
+        it covers; the default there) or the per-kernel launch sequence."""
+        check(_lib.load().cq35_session_set_persistent(self._h, 1 if enabled else 0))
+
+    @property
+    def persistent(self) -> bool:
+        v = ctypes.c_int()
+        check(_lib.load().cq35_session_persistent(self._h, ctypes.byref(v)))
+        return bool(v.value)
+
     def time_kernel(self, kernel_class: int) -> None:
         check(_lib.load().cq35_session_time_kernel(self._h, kernel_class))
 

@@ -20,6 +20,7 @@
 #include "../../include/cq35.h"
 #include "attention.h"
 #include "layers.h"
+#include "mega.h"
 
 using namespace cq35;
 
@@ -409,12 +410,12 @@ namespace {
 enum KernelClass {
   KC_EMBED = 0, KC_PROJECT, KC_PREPARE_LINEAR, KC_DELTA, KC_GATED_NORM, KC_RESIDUAL,
   KC_PREPARE_FULL, KC_ATTENTION, KC_ATTENTION_VALUES, KC_ROUTER, KC_MOE_GATE, KC_MOE_DOWN,
-  KC_SWIGLU, KC_LOGITS, KC_SHADOW, KC_COUNT
+  KC_SWIGLU, KC_LOGITS, KC_SHADOW, KC_DECODE_STEP, KC_COUNT
 };
 const char* kClassNames[KC_COUNT] = {
     "embed_rope", "project", "linear_prepare", "delta", "gated_norm", "residual_project",
     "full_prepare", "attention", "attention_values", "moe_router", "moe_gate_up", "moe_down",
-    "swiglu", "logits_argmax", "shadow_copy"};
+    "swiglu", "logits_argmax", "shadow_copy", "decode_step"};
 
 constexpr int kMaxTimedEvents = 512;
 
@@ -453,6 +454,15 @@ struct cq35_session {
   bool graph_enabled = true;
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
+  // persistent decode step (MoE): tagged exchange words, layer table, args
+  bool mega_ok = false;       // the shape fits the persistent kernel
+  bool mega_on = false;       // n == 1 steps use it
+  uint64_t* words = nullptr;
+  MegaLayer* d_layers = nullptr;
+  MegaArgs margs{};
+  MegaArgs* d_margs = nullptr;
+  int mega_grid = 0;
+  uint32_t seq = 0;
   // kernel timing
   int timed_class = -1;
   hipEvent_t ev[2 * kMaxTimedEvents] = {};
@@ -486,6 +496,172 @@ void destroy_session(cq35_session* s) {
   delete s;
 }
 
+// Shapes the persistent decode kernel covers (its static per-wave maxima and
+// LDS carve-up); other shapes use the per-kernel path. `why` names the first
+// limit a shape exceeds.
+bool mega_fits(const cq35_config& c, const Dims& d, int grid, int64_t cap, const char** why) {
+  const int64_t nw = (int64_t)grid * kMW;
+  auto no = [&](const char* r) { *why = r; return false; };
+  if (!c.moe) return no("dense model");
+  if (d.H > 2048 || d.H % 8) return no("hidden width above 2048");
+  if (d.VS > 4096 || d.QS > 4096) return no("mixer width above 4096");
+  if (c.key_dim > 128 || c.value_dim > 128 || c.key_dim % 32 || c.value_dim % 2)
+    return no("DeltaNet head dims");
+  if (c.value_heads < c.key_heads || c.value_heads > grid) return no("DeltaNet head counts");
+  if (d.QKV % 2 || d.VS % 2 || c.value_heads % 2 || d.KVS % 2) return no("odd projection segment");
+  if (d.HD != 64 && d.HD != 128 && d.HD != 256) return no("attention head dim");
+  if (d.QS > 4096 || d.KVS > 512 || d.R > 256) return no("attention widths");
+  if (d.QS / 2 + d.KVS > 5 * kMT) return no("attention projection words");
+  const int64_t rows_lin = d.QKV + d.VS + 2LL * c.value_heads, rows_full = 2 * d.QS + 2 * d.KVS;
+  if (std::max(rows_lin, rows_full) / 2 > kPairsA * nw) return no("projection rows per wave");
+  if (d.E + 1 > 1025 || d.K > 64) return no("expert counts");
+  if (d.I % 64 || d.SI % 2) return no("expert width (routed width a multiple of 64)");
+  const int64_t act = d.K * d.I + d.SI;
+  if (act / 2 > kPairsG * nw || act / 2 > 5 * kMT) return no("expert rows");
+  if (d.K * d.I / 2 > 32 * kDownJ || d.SI / 2 > 32 * kDownSJ) return no("down projection widths");
+  if (d.H / 2 > nw || d.E + 1 > nw) return no("rows per wave");
+  if ((cap + 7) / 8 > kValueMxMax) return no("cache capacity above the LDS tile maxima");
+  if ((int64_t)(d.V + 7) / 8 > (int64_t)1 << 30) return no("vocabulary");
+  *why = "";
+  return true;
+}
+
+// Tagged exchange buffers per layer (each region 128-byte aligned), the
+// device layer table and the kernel arguments of the persistent step.
+int setup_mega(cq35_session* s) {
+  const cq35_model& m = *s->model;
+  const cq35_config& c = m.cfg;
+  const Dims& d = m.d;
+  int grid = 0;
+  HIP_TRY(hipDeviceGetAttribute(&grid, hipDeviceAttributeMultiprocessorCount, m.device));
+  const char* why = "";
+  if (!mega_fits(c, d, grid, s->capacity, &why)) return CQ35_OK;
+  if (hipFuncSetAttribute((const void*)k_decode_step, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kMegaLds) != hipSuccess)
+    return CQ35_OK;
+  int occupancy = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, k_decode_step, kMT, kMegaLds) != hipSuccess ||
+      occupancy < 1)
+    return CQ35_OK;
+  auto region = [](int64_t words) { return (words + 15) / 16 * 16; };
+  const int64_t hw = region(d.H / 2);
+  std::vector<int64_t> offs;  // per layer: h, proj, mix, attn, router, active, scores
+  int64_t total = 0;
+  for (int64_t l = 0; l < d.L; ++l) {
+    const bool full = is_full(c, l);
+    const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS + 2LL * c.value_heads;
+    const int64_t sizes[7] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
+                              region(d.E + 1), region((d.K * d.I + d.SI) / 2),
+                              full ? region(d.Q * s->capacity) : 0};
+    for (int64_t z : sizes) {
+      offs.push_back(total);
+      total += z;
+    }
+  }
+  const int64_t final_off = total;
+  total += hw;
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, total * sizeof(uint64_t)));
+  s->allocations.push_back(p);
+  s->words = static_cast<uint64_t*>(p);
+  HIP_TRY(hipMemset(s->words, 0, total * sizeof(uint64_t)));
+  std::vector<MegaLayer> layers(d.L);
+  int64_t base = 1;
+  const int64_t cap = s->capacity;
+  for (int64_t l = 0; l < d.L; ++l) {
+    auto W = [&](int slot) { return m.w[base + slot]; };
+    MegaLayer& Ly = layers[l];
+    Ly = MegaLayer{};
+    const int64_t* o = &offs[7 * l];
+    Ly.full = is_full(c, l) ? 1 : 0;
+    Ly.in_norm = (const float*)W(0);
+    Ly.x_h = s->words + o[0];
+    Ly.x_proj = s->words + o[1];
+    Ly.x_mix = s->words + o[2];
+    Ly.x_attn = s->words + o[3];
+    Ly.x_router = s->words + o[4];
+    Ly.x_active = s->words + o[5];
+    Ly.x_scores = s->words + o[6];
+    Ly.x_out = l + 1 < d.L ? s->words + offs[7 * (l + 1)] : s->words + final_off;
+    int ffn;
+    if (Ly.full) {
+      Ly.seg_w[0] = (const uint16_t*)W(1); Ly.seg_rows[0] = (int)(2 * d.QS);
+      Ly.seg_w[1] = (const uint16_t*)W(2); Ly.seg_rows[1] = (int)d.KVS;
+      Ly.seg_w[2] = (const uint16_t*)W(3); Ly.seg_rows[2] = (int)d.KVS;
+      Ly.out_w = (const uint16_t*)W(4);
+      Ly.qnorm = (const float*)W(5);
+      Ly.knorm = (const float*)W(6);
+      Ly.post_norm = (const float*)W(7);
+      Ly.key_base = l * 2 * cap * d.KVS;
+      Ly.value_base = Ly.key_base + cap * d.KVS;
+      ffn = 8;
+    } else {
+      Ly.seg_w[0] = (const uint16_t*)W(1); Ly.seg_rows[0] = (int)d.QKV;
+      Ly.seg_w[1] = (const uint16_t*)W(2); Ly.seg_rows[1] = (int)d.VS;
+      Ly.seg_w[2] = (const uint16_t*)W(3); Ly.seg_rows[2] = c.value_heads;
+      Ly.seg_w[3] = (const uint16_t*)W(4); Ly.seg_rows[3] = c.value_heads;
+      Ly.dt = (const float*)W(5);
+      Ly.a = (const float*)W(6);
+      Ly.gnorm = (const float*)W(7);
+      Ly.out_w = (const uint16_t*)W(8);
+      Ly.conv_w = (const float*)W(9);
+      Ly.post_norm = (const float*)W(10);
+      Ly.conv_base = cap * d.KV_STRIDE + l * d.LIN;
+      Ly.state_base = Ly.conv_base + d.CONV;
+      ffn = 11;
+    }
+    Ly.router = (const float*)W(ffn);
+    Ly.gate_exps = (const uint16_t*)W(ffn + 1);
+    Ly.up_exps = (const uint16_t*)W(ffn + 2);
+    Ly.down_exps = (const uint16_t*)W(ffn + 3);
+    Ly.shared_gate = (const float*)W(ffn + 4);
+    Ly.sgate = (const uint16_t*)W(ffn + 5);
+    Ly.sup = (const uint16_t*)W(ffn + 6);
+    Ly.sdown = (const uint16_t*)W(ffn + 7);
+    base += layer_tensors(c, l);
+  }
+  p = nullptr;
+  HIP_TRY(hipMalloc(&p, layers.size() * sizeof(MegaLayer)));
+  s->allocations.push_back(p);
+  s->d_layers = static_cast<MegaLayer*>(p);
+  HIP_TRY(hipMemcpy(s->d_layers, layers.data(), layers.size() * sizeof(MegaLayer), hipMemcpyHostToDevice));
+  MegaArgs& a = s->margs;
+  a = MegaArgs{};
+  a.layers = s->d_layers;
+  a.L = (int)d.L;
+  a.H = (int)d.H; a.V = (int)d.V; a.Q = (int)d.Q; a.KVH = (int)d.KVH; a.HD = (int)d.HD;
+  a.R = (int)d.R; a.KH = c.key_heads; a.KD = c.key_dim; a.VH = c.value_heads; a.VD = c.value_dim;
+  a.KS = (int)d.KS; a.VS = (int)d.VS; a.QKV = (int)d.QKV; a.QS = (int)d.QS; a.KVS = (int)d.KVS;
+  a.E = (int)d.E; a.K = (int)d.K; a.I = (int)d.I; a.SI = (int)d.SI;
+  a.eps = c.eps;
+  a.attn_scale = 1.0f / sqrtf((float)d.HD);        // SCALE_BITS, qwen35.rs:701
+  a.delta_scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
+  a.cap = cap;
+  const int64_t nweights = weight_count(c);
+  a.embed = (const uint16_t*)m.w[0];
+  a.out_norm = (const float*)m.w[nweights - 2];
+  a.head = (const uint16_t*)m.w[nweights - 1];
+  a.freq = m.freq;
+  a.cache = s->cache;
+  a.params = s->d_params;
+  a.x_final = s->words + final_off;
+  a.logits = s->logits;
+  a.best = s->d_best;
+  a.error = reinterpret_cast<unsigned*>(s->d_best + 1);
+  a.spin_limit = 1u << 21;
+  if (const char* lim = getenv("CQ35_SPIN_LIMIT")) a.spin_limit = (unsigned)strtoul(lim, nullptr, 10);
+  p = nullptr;
+  HIP_TRY(hipMalloc(&p, sizeof(MegaArgs)));
+  s->allocations.push_back(p);
+  s->d_margs = static_cast<MegaArgs*>(p);
+  HIP_TRY(hipMemcpy(s->d_margs, &a, sizeof(MegaArgs), hipMemcpyHostToDevice));
+  s->mega_grid = grid;
+  s->mega_ok = true;
+  s->mega_on = true;
+  if (const char* g = getenv("CQ35_PERSISTENT")) s->mega_on = atoi(g) != 0;
+  return CQ35_OK;
+}
+
 int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   cq35_session* s = new (std::nothrow) cq35_session();
   if (!s) return fail(CQ35_EINVAL, "out of host memory");
@@ -500,8 +676,8 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   const int64_t cache_n = cache_elements(c, capacity);
   check(dalloc(s, &s->cache, cache_n));
   check(dalloc(s, &s->shadow, d.L * d.REC));
-  check(dalloc(s, &s->d_params, capacity + 1));
-  check(dalloc(s, &s->d_best, 1));
+  check(dalloc(s, &s->d_params, capacity + 2));
+  check(dalloc(s, &s->d_best, 2));  // [0] argmax key, [1] persistent-kernel error word
   check(dalloc(s, &s->h, d.H));
   check(dalloc(s, &s->attn, d.H));
   check(dalloc(s, &s->qkv, d.QKV));
@@ -533,13 +709,16 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   check(dalloc(s, &s->attn_scratch, d.Q * (int64_t)s->attn_stride));
   if (rc) { destroy_session(s); return rc; }
   if (const char* g = getenv("CQ35_GRAPH")) s->graph_enabled = atoi(g) != 0;
-  e = hipHostMalloc((void**)&s->h_params, (capacity + 1) * sizeof(uint64_t), hipHostMallocDefault);
-  if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_best, sizeof(unsigned long long), hipHostMallocDefault);
+  e = hipHostMalloc((void**)&s->h_params, (capacity + 2) * sizeof(uint64_t), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_best, 2 * sizeof(unsigned long long), hipHostMallocDefault);
   if (e == hipSuccess) e = hipMemset(s->cache, 0, cache_n * sizeof(uint16_t));
   if (e == hipSuccess) e = hipMemset(s->shadow, 0, d.L * d.REC * sizeof(float));
   if (e == hipSuccess) e = hipMemset(s->ticket, 0, sizeof(unsigned));
+  if (e == hipSuccess) e = hipMemset(s->d_best, 0, 2 * sizeof(unsigned long long));
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) { destroy_session(s); return fail(CQ35_EDEVICE, "session init: %s", hipGetErrorString(e)); }
+  rc = setup_mega(s);
+  if (rc) { destroy_session(s); return rc; }
   *out = s;
   return CQ35_OK;
 }
@@ -817,6 +996,61 @@ int collect_timing(cq35_session* s) {
 
 }  // namespace
 
+namespace {
+
+// One decode step through the persistent kernel: upload (position, token,
+// step tag), one launch, read back the argmax key and the kernel's error word.
+int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* next_token,
+                    uint16_t* logits) {
+  const cq35_config& c = s->model->cfg;
+  if (++s->seq == 0) s->seq = 1;  // tag 0 marks never-written words
+  s->h_params[0] = (uint64_t)start;
+  s->h_params[1] = token;
+  s->h_params[2] = s->seq;
+  s->poisoned = true;  // cleared on success
+  hipError_t e = hipMemcpyAsync(s->d_params, s->h_params, 3 * sizeof(uint64_t), hipMemcpyHostToDevice,
+                                s->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "parameter upload: %s", hipGetErrorString(e));
+  Launcher L{s};
+  L(KC_DECODE_STEP, k_decode_step, dim3((unsigned)s->mega_grid), dim3(kMT), (size_t)kMegaLds,
+    (const MegaArgs*)s->d_margs);
+  e = hipGetLastError();
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(s->h_best, s->d_best, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess && logits)
+    e = hipMemcpyAsync(logits, s->logits, (size_t)c.vocab * 2, hipMemcpyDeviceToHost, s->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "persistent step: %s", hipGetErrorString(e));
+  if (s->timed_class >= 0) {
+    int rc = collect_timing(s);
+    if (rc) return rc;
+  }
+  if (s->h_best[1] != 0)
+    return fail(CQ35_EDEVICE, "persistent step: an exchange wait exceeded its spin limit");
+  const uint64_t t = decode_key(s->h_best[0]);
+  if (t >= (uint64_t)c.vocab)
+    return fail(CQ35_EDEVICE, "qwen3 returned next-token ID %llu outside the vocabulary", (unsigned long long)t);
+  *next_token = t;
+  s->poisoned = false;
+  return CQ35_OK;
+}
+
+}  // namespace
+
+extern "C" int cq35_session_set_persistent(cq35_session* s, int enabled) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  if (enabled && !s->mega_ok)
+    return fail(CQ35_EUNSUPPORTED, "this model shape or capacity is outside the persistent decode kernel");
+  s->mega_on = enabled != 0;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_persistent(const cq35_session* s, int* enabled) {
+  if (!s || !enabled) return fail(CQ35_EINVAL, "null argument");
+  *enabled = s->mega_on ? 1 : 0;
+  return CQ35_OK;
+}
+
 extern "C" int cq35_session_init(cq35_model* m, int64_t capacity, cq35_session** out) {
   if (!m || !out) return fail(CQ35_EINVAL, "null argument");
   if (capacity <= 0) return fail(CQ35_EINVAL, "cache capacity must be non-zero");
@@ -863,6 +1097,8 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
                 "(prefill.rs:623-652), which this build does not provide; append tokens one at a time");
   hipError_t e = hipSetDevice(s->model->device);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+  if (n == 1 && s->mega_on && (s->timed_class < 0 || s->timed_class == KC_DECODE_STEP))
+    return step_persistent(s, tokens[0], start, next_token, logits);
   s->h_params[0] = (uint64_t)start;
   for (int64_t i = 0; i < n; ++i) s->h_params[1 + i] = tokens[i];
   s->poisoned = true;  // cleared on success

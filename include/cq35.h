@@ -150,6 +150,14 @@ int cq35_kernel_class_count(void);
 /* Disable (0) or enable (1, default) hipGraph replay of the decode step. */
 int cq35_session_set_graph(cq35_session* session, int enabled);
 
+/* Decode steps (n == 1) of MoE models run as one persistent launch per token
+ * by default, where the shape and capacity fit its limits; 0 selects the
+ * per-kernel launch sequence, 1 the persistent kernel (CQ35_EUNSUPPORTED
+ * when the session's shape is outside it). Same arithmetic either way. No
+ * reference counterpart (the reference launches ~1,316 kernels per token). */
+int cq35_session_set_persistent(cq35_session* session, int enabled);
+int cq35_session_persistent(const cq35_session* session, int* enabled);
+
 /* Host-side builds of the device numerics (same source), for CPU checks. */
 float cq35_numeric_exp(float x);
 float cq35_numeric_sqrt(float x);
