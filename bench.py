@@ -85,6 +85,9 @@ def kernel_bytes(cfg: dict, context: int) -> dict:
         "attention": ((context + 1) * 2 * d["kvs"] * 2, full),
         "delta": (2 * d["recurrent"] * 2, lin),
     }
+    # the persistent step is one launch per token: its algorithmic bytes are
+    # the whole token's (weights touched + KV read + state read/write)
+    out["decode_step"] = (cq35.bytes_per_token(cfg, context)["total"], 1)
     if cfg["moe"]:
         K, I, SI, E = cfg["top_k"], cfg["intermediate"], cfg["shared_intermediate"], cfg["experts"]
         out["moe_gate_up"] = ((K * I + SI) * H * 2 * 2, cfg["layers"])
@@ -117,6 +120,8 @@ def measure_kernels(session, tokens, classes, steps_each):
     i = 0
     for name in classes:
         kc = names.index(name)
+        if name != "decode_step" and session.persistent:
+            session.set_persistent(False)  # per-kernel classes exist only on that path
         session.time_kernel(kc)
         for _ in range(steps_each):
             session.decode_next_token(tokens[i])
@@ -174,6 +179,10 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--per-kernel-timing", action="store_true",
+                    help="also time each kernel class of the per-kernel launch sequence")
+    ap.add_argument("--per-kernel", action="store_true",
+                    help="decode through the per-kernel launch sequence instead of the persistent step")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--cpu-steps", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=25.0)
@@ -193,14 +202,23 @@ def main() -> int:
     t0 = time.time()
     model = cq35.Model.synthetic(cfg, seed=args.seed)
     log(f"weights: {model.weight_bytes() / 1e9:.2f} GB generated on device in {time.time() - t0:.1f}s")
-    timing_classes = [] if args.no_kernel_timing else (
+    per_kernel_classes = (
         ["project", "moe_gate_up", "moe_down", "residual_project", "logits_argmax", "attention",
          "delta", "moe_router"] if cfg["moe"] else
         ["project", "swiglu", "residual_project", "logits_argmax", "attention", "delta"])
     timing_steps = 3
-    capacity = args.context + args.warmup + args.steps + len(timing_classes) * timing_steps + 1
+    capacity = args.context + args.warmup + args.steps + (len(per_kernel_classes) + 1) * timing_steps + 1
     tokens = synthetic_tokens(capacity, cfg["vocab"])
     session = model.session(capacity)
+    if args.per_kernel and session.persistent:
+        session.set_persistent(False)
+    persistent = session.persistent
+    if args.no_kernel_timing:
+        timing_classes = []
+    elif persistent:
+        timing_classes = ["decode_step"] + (per_kernel_classes if args.per_kernel_timing else [])
+    else:
+        timing_classes = per_kernel_classes
     t0 = time.time()
     for t in tokens[:args.context]:
         session.append_next_token([t])
@@ -239,7 +257,7 @@ def main() -> int:
             kernels[name] = dict(ms_per_step=kms / timing_steps, avg_launch_us=per_launch * 1e3,
                                  launches_per_step=n / timing_steps,
                                  gbs=(by / (per_launch / 1e3) / 1e9) if by else None)
-        dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+        dom = "decode_step" if "decode_step" in kernels else max(kernels, key=lambda k: kernels[k]["ms_per_step"])
         by, _ = kb[dom]
         avg_s = kernels[dom]["avg_launch_us"] / 1e6
         achieved = by / avg_s / 1e9
@@ -281,7 +299,8 @@ def main() -> int:
         ms_per_step=round(ms, 4), higher_is_better=True, scaling="weak", vs_baseline=None,
         dtype="bf16", data="synthetic (seeded random-init weights, LCG prompt ids)",
         config=dict(workload=f"{args.config} batch-1 greedy decode", model=args.config,
-                    global_batch=1, seq_len=args.context, context_avg=ctx_avg, parallelism="none"),
+                    global_batch=1, seq_len=args.context, context_avg=ctx_avg, parallelism="none",
+                    decode_path="persistent one-launch step" if persistent else "per-kernel launch sequence"),
         step_roofline=dict(bytes_per_token=bpt["total"], achieved_gbs=round(step_gbs, 1),
                            frac=round(step_gbs / HBM_PEAK_GBS, 4)),
         roofline=roofline, kernels=kernels, cpu_baseline=cpu,

@@ -20,6 +20,12 @@
 // raises the block's abort flag and the global error word, after which every
 // wait of every block returns at once, so the grid always drains.
 //
+// Code size is a first-order cost here: the layer loop runs every phase once
+// per layer, so the loop body must stay within the instruction cache. The
+// kernel is therefore a template over the model shape (all widths
+// compile-time constants, so loops have exact trip counts and no per-element
+// guards), and the per-lane loads of a phase are straight-line code.
+//
 // Arithmetic and reduction orders are those of the per-kernel path
 // (gemv.h, layers.h, attention.h), bit for bit.
 #pragma once
@@ -32,14 +38,34 @@ namespace cq35 {
 constexpr int kMT = 512;       // threads per block
 constexpr int kMW = kMT / 64;  // waves per block
 
-// Static per-wave work maxima (checked on the host for every shape).
-constexpr int kPairsA = 4;     // projection row pairs per wave
-constexpr int kPairsG = 2;     // gate/up row pairs per wave
-constexpr int kDownJ = 64;     // routed dwords per lane in the down projection
-constexpr int kDownSJ = 16;    // shared dwords per lane
-constexpr int kOutJ = 32;      // dwords per lane per row of the output projections
-constexpr int kRouterJ = 32;   // router floats per lane
-constexpr int kChunkKeys = 512;  // attention keys staged per chunk
+// Per-wave work maxima.
+constexpr int kPairsA = 4;       // projection row pairs per wave
+constexpr int kPairsG = 2;       // gate/up row pairs per wave
+
+// Model shapes the persistent step is compiled for. Widths follow
+// ModelConfig (src/spec.rs:33-62); derived sizes as in spec.rs:293-362.
+template <int H_, int V_, int Q_, int KVH_, int HD_, int R_, int KH_, int KD_, int VH_, int VD_,
+          int E_, int K_, int I_, int SI_>
+struct MegaShape {
+  static constexpr int H = H_, V = V_, Q = Q_, KVH = KVH_, HD = HD_, R = R_, KH = KH_, KD = KD_,
+                       VH = VH_, VD = VD_, E = E_, K = K_, I = I_, SI = SI_;
+  static constexpr int KS = KH * KD, VS = VH * VD, QKV = 2 * KS + VS, QS = Q * HD, KVS = KVH * HD;
+  static constexpr int QH = H / 8;            // BF16 quads per hidden row
+  static constexpr int NQA = (QH + 63) / 64;  // S256 quads per lane per row
+  static_assert(H % 8 == 0 && H <= 2048, "hidden width");
+  static_assert(KD % 32 == 0 && KD <= 128 && VD <= 128 && VD % 4 == 0, "DeltaNet head dims");
+  static_assert(VH >= KH, "value heads");
+  static_assert(HD == 64 || HD == 128 || HD == 256, "attention head dim");
+  static_assert(QS <= 4096 && VS <= 4096 && KVS <= 512 && R <= 256 && R % 2 == 0, "attention widths");
+  static_assert(QS / 2 + KVS <= 5 * kMT, "attention projection words");
+  static_assert(E + 1 <= 1025 && K <= 64 && I % 64 == 0 && SI % 64 == 0, "expert shapes");
+  static_assert((K * I + SI) / 2 <= 5 * kMT, "expert rows");
+  static_assert(V % 8 == 0, "vocabulary in groups of 8 rows");
+};
+// qwen36-35b-a3b (src/spec.rs:153-183) and the two reduced MoE test shapes.
+using Shape35BA3B = MegaShape<2048, 248320, 16, 2, 256, 64, 16, 128, 32, 128, 256, 8, 512, 512>;
+using ShapeMiniMoE = MegaShape<512, 8192, 4, 2, 256, 64, 2, 128, 4, 128, 32, 8, 128, 256>;
+using ShapeTinyMoE = MegaShape<256, 4096, 4, 1, 64, 16, 4, 32, 8, 32, 16, 4, 64, 128>;
 
 struct MegaLayer {
   int full;
@@ -77,7 +103,6 @@ struct MegaLayer {
 struct MegaArgs {
   const MegaLayer* layers;
   int L;
-  int H, V, Q, KVH, HD, R, KH, KD, VH, VD, KS, VS, QKV, QS, KVS, E, K, I, SI;
   float eps, attn_scale, delta_scale;
   int64_t cap;
   const uint16_t* embed;
@@ -132,11 +157,24 @@ __device__ __forceinline__ const CQ35_GLOBAL T* G(const T* p) {
   return (const CQ35_GLOBAL T*)p;
 }
 
+// An opaque copy of a uniform pointer, kept in scalar registers: loads
+// through it cannot be hoisted out of the phase that makes the copy, which
+// keeps every phase's scalar state local to the phase. The tables are written
+// by the host before the launch and never by the kernel, so they are read
+// through the constant address space (scalar loads).
+template <typename T>
+__device__ __forceinline__ const CQ35_CONST T* phase_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  asm volatile("" : "+s"(lo), "+s"(hi));
+  return (const CQ35_CONST T*)(((uint64_t)hi << 32) | lo);
+}
 
-// Per-thread view of one phase: the arguments (device memory, read through
-// the scalar cache), the step tag, thread coordinates and the LDS carve-up.
-// Phases are separate functions that rebuild it, so nothing of it lives in
-// private memory across calls.
+// Per-thread view of one phase: the arguments, the step tag, thread
+// coordinates and the LDS carve-up. Per-lane arithmetic is rebuilt in every
+// phase instead of being hoisted out of the layer loop and held in registers
+// across all phases.
 struct Mega {
   const CQ35_CONST MegaArgs& a;
   uint32_t tag;
@@ -149,28 +187,12 @@ struct Mega {
   unsigned char* big;
 };
 
-// An opaque copy of a uniform pointer, kept in scalar registers: loads
-// through it cannot be hoisted out of the phase that makes the copy, which
-// keeps every phase's scalar state local to the phase.
-// The tables are written by the host before the launch and never by the
-// kernel, so they are read through the constant address space (scalar loads).
-template <typename T>
-__device__ __forceinline__ const CQ35_CONST T* phase_ptr(const T* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  asm volatile("" : "+s"(lo), "+s"(hi));
-  return (const CQ35_CONST T*)(((uint64_t)hi << 32) | lo);
-}
-
 __device__ __forceinline__ Mega make_mega(const MegaArgs* pa, uint32_t tag) {
   const CQ35_CONST MegaArgs* a = phase_ptr(pa);
-  // per-lane arithmetic is recomputed in every phase instead of being hoisted
-  // out of the layer loop and held in registers across all phases
   int tid = threadIdx.x;
   asm volatile("" : "+v"(tid));
-  // wave-level indices are uniform: keep them in scalar registers so weight
-  // rows get scalar base addresses (one 32-bit lane offset per load)
+  // wave-level indices are uniform: scalar registers, so weight rows get
+  // scalar base addresses (one 32-bit lane offset per load)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gw = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kMW + wave);
   const int nw = __builtin_amdgcn_readfirstlane((int)gridDim.x * kMW);
@@ -205,14 +227,14 @@ __device__ __forceinline__ bool word_ready(uint64_t w, uint32_t tag) {
 __device__ __forceinline__ volatile CQ35_LDS int* abort_flag(const Mega& m) {
   return (volatile CQ35_LDS int*)&m.misc->abort;
 }
-__device__ __forceinline__ bool mega_aborted(const Mega& m) { return *abort_flag(m) != 0; }
 
-// Spin bookkeeping of one polling loop: true when the wait must stop.
-__device__ __forceinline__ bool spin_exhausted(const Mega& m, unsigned& spins) {
-  if (mega_aborted(m)) return true;
-  ++spins;
-  if ((spins & 255u) == 0 &&
-      __hip_atomic_load(G(m.a.error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+// Spin bookkeeping of one polling loop: true when the wait must stop. The
+// block's abort flag is checked every spin, the global error word and the
+// spin limit every 256 spins.
+__device__ __forceinline__ bool spin_stop(const Mega& m, unsigned spins) {
+  if (*abort_flag(m)) return true;
+  if ((spins & 255u) != 0) return false;
+  if (__hip_atomic_load(G(m.a.error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
     *abort_flag(m) = 1;
     return true;
   }
@@ -233,18 +255,18 @@ __device__ __forceinline__ void poll_words(const Mega& m, const uint64_t* src, i
   uint64_t v[MAXW];
 #pragma unroll
   for (int j = 0; j < MAXW; ++j) {
-    const int i = m.tid + kMT * j;
-    v[j] = i < n ? word_load(src + src_index(i)) : ((uint64_t)m.tag << 32);
+    const int i = min(m.tid + kMT * j, n - 1);
+    v[j] = word_load(src + src_index(i));
   }
   unsigned spins = 0;
   while (true) {
     bool ready = true;
 #pragma unroll
     for (int j = 0; j < MAXW; ++j) ready &= word_ready(v[j], m.tag);
-    if (ready || spin_exhausted(m, spins)) break;
+    if (ready || spin_stop(m, ++spins)) break;
 #pragma unroll
     for (int j = 0; j < MAXW; ++j) {
-      const int i = m.tid + kMT * j;
+      const int i = min(m.tid + kMT * j, n - 1);
       if (!word_ready(v[j], m.tag)) v[j] = word_load(src + src_index(i));
     }
   }
@@ -264,20 +286,40 @@ struct Identity {
 __device__ __forceinline__ uint32_t poll_one(const Mega& m, const uint64_t* p) {
   uint64_t v = word_load(p);
   unsigned spins = 0;
-  while (!word_ready(v, m.tag) && !spin_exhausted(m, spins)) v = word_load(p);
+  while (!word_ready(v, m.tag) && !spin_stop(m, ++spins)) v = word_load(p);
   return (uint32_t)v;
+}
+
+// In-order sum of n floats in LDS (n a multiple of 4): every read is issued
+// before the dependent adds, which keep the serial order.
+template <int N>
+__device__ __forceinline__ float serial_sum(const float* v) {
+  static_assert(N % 4 == 0, "serial sum width");
+  f32x4 x[N / 4];
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) x[i] = reinterpret_cast<const f32x4*>(v)[i];
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < N / 4; ++i) {
+    total += x[i].x;
+    total += x[i].y;
+    total += x[i].z;
+    total += x[i].w;
+  }
+  return total;
 }
 
 // ------------------------------------------------------- normalised input
 
-// qwen35.normalize (qwen35.hex:912-977) of the raw row in `raw` (H <= 2048)
-// into m.xn, with the norm weights prefetched by thread t < 256 for octet t.
-// The adjacent-pair tree over the padded width equals the octet tree, the
-// 64-lane shuffle tree and ((w0 + w1) + (w2 + w3)) over waves 0-3 (threads
-// past H/8 hold +0, and joining a zero subtree is exact).
-__device__ __forceinline__ void norm_row(const Mega& m, const uint16_t* raw, f32x4 w0, f32x4 w1) {
-  const int H = m.a.H;
-  const bool own = m.tid < (H >> 3);
+// qwen35.normalize (qwen35.hex:912-977) of the raw row in `raw` into m.xn,
+// with the norm weights prefetched by thread t < H/8 for octet t. The
+// adjacent-pair tree over the padded width equals the octet tree, the 64-lane
+// shuffle tree and ((w0 + w1) + (w2 + w3)) over waves 0-3 (threads past H/8
+// hold +0, and joining a zero subtree is exact).
+template <class S>
+__device__ __forceinline__ void norm_row(const Mega& m, const uint16_t* raw, f32x4 w0, f32x4 w1,
+                                         float eps) {
+  const bool own = m.tid < S::QH;
   u32x4 x = {0u, 0u, 0u, 0u};
   if (own) x = reinterpret_cast<const u32x4*>(raw)[m.tid];
   float t = own ? octet_squares(x) : 0.0f;
@@ -290,29 +332,30 @@ __device__ __forceinline__ void norm_row(const Mega& m, const uint16_t* raw, f32
   if (m.lane == 0 && m.wave < 4) m.misc->red[m.wave] = t;
   __syncthreads();
   const float sum = (m.misc->red[0] + m.misc->red[1]) + (m.misc->red[2] + m.misc->red[3]);
-  const float inverse = 1.0f / nsqrt(sum / (float)H + m.a.eps);
+  const float inverse = 1.0f / nsqrt(sum / (float)S::H + eps);
   if (own) m.xn[m.tid] = octet_scale(x, inverse, w0, w1);
   __syncthreads();
 }
 
+template <class S>
 __device__ __forceinline__ void norm_weights(const Mega& m, const float* w, f32x4& w0, f32x4& w1) {
-  const int o = min(m.tid, (m.a.H >> 3) - 1);
+  const int o = min(m.tid, S::QH - 1);
   w0 = G(reinterpret_cast<const f32x4*>(w))[2 * o];
   w1 = G(reinterpret_cast<const f32x4*>(w))[2 * o + 1];
 }
 
 // Raw hidden row of layer l into `raw`: the embedding row for layer 0,
 // otherwise the previous layer's output words.
+template <class S>
 __device__ __forceinline__ void load_hidden(const Mega& m, const uint64_t* words, uint16_t* raw,
                                             bool embedding) {
-  const int H = m.a.H;
   if (embedding) {
     const uint64_t token = G(m.a.params)[1];
-    const u32x4* row = reinterpret_cast<const u32x4*>(m.a.embed + token * (uint64_t)H);
-    if (m.tid < (H >> 3)) reinterpret_cast<u32x4*>(raw)[m.tid] = G(row)[m.tid];
+    const u32x4* row = reinterpret_cast<const u32x4*>(m.a.embed + token * (uint64_t)S::H);
+    if (m.tid < S::QH) reinterpret_cast<u32x4*>(raw)[m.tid] = G(row)[m.tid];
     __syncthreads();
   } else {
-    poll_words<2>(m, words, H >> 1, Identity{}, reinterpret_cast<uint32_t*>(raw));
+    poll_words<(S::H / 2 + kMT - 1) / kMT>(m, words, S::H / 2, Identity{}, reinterpret_cast<uint32_t*>(raw));
   }
 }
 
@@ -370,29 +413,30 @@ __device__ __forceinline__ const uint16_t* seg_row(const CQ35_CONST MegaLayer& L
 // Normalised hidden row x grouped BF16 matrices (group-project,
 // group_projection.hex:3-97): S256 split pairs, a physical lane holding
 // reference lanes 4q..4q+3; row pairs (2p, 2p+1) per output word.
+template <class S>
 __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int l) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const int H = m.a.H, quads = H >> 3;
+  constexpr int NQ = S::NQA;
   const int total = Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3];
   const int pairs = total >> 1;
-  u32x4 wv[kPairsA][2][4];
+  u32x4 wv[kPairsA][2][NQ];
 #pragma unroll
   for (int k = 0; k < kPairsA; ++k) {
     const int p = m.gw + m.nw * k;
     if (p < pairs) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const uint16_t* w = seg_row(Ly, 2 * p + r, H);
+        const uint16_t* w = seg_row(Ly, 2 * p + r, S::H);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wv[k][r][j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, quads - 1) * 16u);
+        for (int j = 0; j < NQ; ++j) wv[k][r][j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
       }
     }
   }
   f32x4 w0, w1;
-  norm_weights(m, Ly.in_norm, w0, w1);
-  load_hidden(m, Ly.x_h, m.xr, l == 0);
-  norm_row(m, m.xr, w0, w1);
+  norm_weights<S>(m, Ly.in_norm, w0, w1);
+  load_hidden<S>(m, Ly.x_h, m.xr, l == 0);
+  norm_row<S>(m, m.xr, w0, w1, m.a.eps);
 #pragma unroll
   for (int k = 0; k < kPairsA; ++k) {
     const int p = m.gw + m.nw * k;
@@ -403,8 +447,8 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
         Quad acc;
         quad_zero(acc);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (m.lane + 64 * j < quads) quad_acc(acc, m.xn[m.lane + 64 * j], wv[k][r][j]);
+        for (int j = 0; j < NQ; ++j)
+          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], wv[k][r][j]);
         v[r] = quad_tree<64>(acc);
       }
       if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
@@ -430,61 +474,62 @@ struct DeltaLds {
   uint16_t khat[128];
   uint16_t core[128];
   uint16_t raw_qk[256]; // raw q | k of the key head (history written next phase)
-  float gates[4];       // decay, rate
+  float gates[4];       // decay, rate, norms
 };
 constexpr int kDeltaState = 8192;  // offset of the state rows in the big area
 static_assert(sizeof(DeltaLds) <= kDeltaState, "delta LDS");
 
+template <class S>
 __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
   const int h = blockIdx.x;
-  if (h >= a.VH) return;  // uniform per block
-  const int KD = a.KD, VD = a.VD, kh = h % a.KH;
-  const int nch = 2 * KD + VD;
+  if (h >= S::VH) return;  // uniform per block
+  constexpr int KD = S::KD, VD = S::VD, NCH = 2 * KD + VD;
+  constexpr int SQUADS = VD * KD / 8, SPT = (SQUADS + kMT - 1) / kMT;
+  static_assert(SQUADS * 16 <= kLdsBigBytes - kDeltaState && NCH <= kMT, "delta shape");
+  const int kh = h % S::KH;
   DeltaLds* d = reinterpret_cast<DeltaLds*>(m.big);
   uint16_t* state = reinterpret_cast<uint16_t*>(m.big + kDeltaState);
   uint16_t* st_g = a.cache + Ly.state_base + (size_t)h * VD * KD;
   // prefetch: state rows, conv taps, history, gate parameters
-  const int squads = (VD * KD) >> 3;
-  u32x4 sv[4];
+  u32x4 sv[SPT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    sv[j] = ldq_at(st_g, (uint32_t)min(m.tid + kMT * j, squads - 1) * 16u);
+  for (int j = 0; j < SPT; ++j) sv[j] = ldq_at(st_g, (uint32_t)min(m.tid + kMT * j, SQUADS - 1) * 16u);
   const int64_t position = (int64_t)G(a.params)[0];
   int ch = 0;
   if (m.tid < KD) ch = kh * KD + m.tid;
-  else if (m.tid < 2 * KD) ch = a.KS + kh * KD + (m.tid - KD);
-  else ch = 2 * a.KS + h * VD + (m.tid - 2 * KD);
-  const bool conv_thread = m.tid < nch;
+  else if (m.tid < 2 * KD) ch = S::KS + kh * KD + (m.tid - KD);
+  else ch = 2 * S::KS + h * VD + (m.tid - 2 * KD);
+  const bool conv_thread = m.tid < NCH;
   f32x4 taps_w = {0.f, 0.f, 0.f, 0.f};
   float hist[3] = {0.f, 0.f, 0.f};
   const uint16_t* history = a.cache + Ly.conv_base;
   if (conv_thread) {
     taps_w = G(reinterpret_cast<const f32x4*>(Ly.conv_w))[ch];
 #pragma unroll
-    for (int k = 0; k < 3; ++k) hist[k] = bf2f(G(history)[((position + k) % 3) * a.QKV + ch]);
+    for (int k = 0; k < 3; ++k) hist[k] = bf2f(G(history)[((position + k) % 3) * S::QKV + ch]);
   }
   const float dt = G(Ly.dt)[h], aa = G(Ly.a)[h];
   const float gw = m.tid < VD ? G(Ly.gnorm)[m.tid] : 0.0f;
   // inputs: q | k | v of this head, z, alpha, beta (projection words)
-  const int qw = KD >> 1, vw = VD >> 1;
-  const int zbase = a.QKV, abase = a.QKV + a.VS, bbase = abase + a.VH;
-  const int nwords = 2 * qw + 2 * vw + 2;
+  constexpr int qw = KD / 2, vw = VD / 2;
+  constexpr int zbase = S::QKV, abase = S::QKV + S::VS, bbase = abase + S::VH;
+  constexpr int nwords = 2 * qw + 2 * vw + 2;
   auto index = [&](int i) -> int {
     if (i < qw) return ((kh * KD) >> 1) + i;
-    if (i < 2 * qw) return ((a.KS + kh * KD) >> 1) + (i - qw);
-    if (i < 2 * qw + vw) return ((2 * a.KS + h * VD) >> 1) + (i - 2 * qw);
+    if (i < 2 * qw) return ((S::KS + kh * KD) >> 1) + (i - qw);
+    if (i < 2 * qw + vw) return ((2 * S::KS + h * VD) >> 1) + (i - 2 * qw);
     if (i < 2 * qw + 2 * vw) return ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
     if (i == 2 * qw + 2 * vw) return (abase + h) >> 1;
     return (bbase + h) >> 1;
   };
-  poll_words<1>(m, Ly.x_proj, nwords, index, m.vec);
+  poll_words<(nwords + kMT - 1) / kMT>(m, Ly.x_proj, nwords, index, m.vec);
   const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (m.tid + kMT * j < squads) reinterpret_cast<u32x4*>(state)[m.tid + kMT * j] = sv[j];
+  for (int j = 0; j < SPT; ++j)
+    if (m.tid + kMT * j < SQUADS) reinterpret_cast<u32x4*>(state)[m.tid + kMT * j] = sv[j];
   // convolution (linear_prepare.hex:2-64)
   if (conv_thread) {
     const uint16_t current = in16[m.tid];
@@ -504,15 +549,13 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
       d->raw_qk[m.tid] = current;
     } else {
       // v history: read by this block only
-      G(a.cache)[Ly.conv_base + (position % 3) * a.QKV + ch] = current;
+      G(a.cache)[Ly.conv_base + (position % 3) * S::QKV + ch] = current;
     }
   }
   __syncthreads();
   // serial L2 sums (q: thread 0, k: thread 64) and the gates (thread 128)
   if (m.tid == 0 || m.tid == 64) {
-    const float* s = d->sq + (m.tid == 0 ? 0 : KD);
-    float total = 0.0f;
-    for (int i = 0; i < KD; ++i) total += s[i];
+    const float total = serial_sum<KD>(d->sq + (m.tid == 0 ? 0 : KD));
     d->gates[2 + (m.tid == 0 ? 0 : 1)] = nsqrt(total + bitsf(0x358637bdu));
   } else if (m.tid == 128) {
     const uint16_t alpha = in16[2 * (2 * qw + 2 * vw) + ((abase + h) & 1)];
@@ -529,48 +572,70 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     else d->khat[m.tid - KD] = r;
   }
   __syncthreads();
-  // delta step: 16 channels per pass, 32 lanes per channel
+  // delta step: 64 channels per pass, 8 lanes per channel; lane q holds the
+  // D32 reference lanes 4q..4q+3, i.e. key elements 4q + i + 32j (i, j < 4):
+  // per i a serial chain over j from 0.0, then the 32-lane halving tree
+  // (strides 16, 8, 4 across lanes, 2 and 1 in-lane; tree_levels order).
   const float decay = d->gates[0], rate = d->gates[1];
-  const int sub = m.tid >> 5, l32 = m.tid & 31, kj = KD >> 5;
-  for (int c0 = 0; c0 < VD; c0 += kMT / 32) {
+  constexpr int KJ = KD / 32, CPP = kMT / 8;  // key chunks; channels per pass
+  const int q = m.lane & 7, sub = m.tid >> 3;
+  float kv[KJ][4], qv[KJ][4];
+#pragma unroll
+  for (int j = 0; j < KJ; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[j][i] = bf2f(d->khat[4 * q + i + 32 * j]);
+      qv[j][i] = bf2f(d->qhat[4 * q + i + 32 * j]);
+    }
+#pragma unroll 1
+  for (int c0 = 0; c0 < VD; c0 += CPP) {
     const int c = c0 + sub;
     const bool valid = c < VD;
     const int cc = valid ? c : 0;
-    float old[4], kv[4];
-    float acc = 0.0f;
+    uint16_t* row = state + cc * KD + 4 * q;
+    float old[KJ][4];
+    float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < kj) {
-        const int i = l32 + 32 * j;
-        old[j] = bf2f(state[cc * KD + i]);
-        kv[j] = bf2f(d->khat[i]);
-        acc += old[j] * kv[j];
-      }
+    for (int j = 0; j < KJ; ++j) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(row + 32 * j);
+      old[j][0] = lo2f(raw.x); old[j][1] = hi2f(raw.x);
+      old[j][2] = lo2f(raw.y); old[j][3] = hi2f(raw.y);
     }
 #pragma unroll
-    for (int s = 16; s >= 1; s >>= 1) acc += __shfl_down(acc, s, 32);
-    const float total = __shfl(acc, 0, 32);
+    for (int i = 0; i < 4; ++i) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) acc += old[j][i] * kv[j][i];
+      v[i] = acc;
+    }
+    tree_levels<8>(v[0], v[1], v[2], v[3]);
+    float total = (v[0] + v[2]) + (v[1] + v[3]);
+    // the group's first lane holds the tree value: broadcast within the 8 lanes
+    total = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, total), 0x18));
     const float value = d->conv[2 * KD + cc];
     const float delta = (value - total * decay) * rate;
-    float acc2 = 0.0f;
+    float w[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j < kj) {
-        const int i = l32 + 32 * j;
-        const float next = old[j] * decay + kv[j] * delta;
-        if (valid) state[cc * KD + i] = f2bf(next);
-        acc2 += next * bf2f(d->qhat[i]);
+    for (int j = 0; j < KJ; ++j) {
+      float nx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        nx[i] = old[j][i] * decay + kv[j][i] * delta;
+        w[i] += nx[i] * qv[j][i];
       }
+      if (valid)
+        *reinterpret_cast<uint2*>(row + 32 * j) =
+            uint2{pack_bf(f2bf(nx[0]), f2bf(nx[1])), pack_bf(f2bf(nx[2]), f2bf(nx[3]))};
     }
-#pragma unroll
-    for (int s = 16; s >= 1; s >>= 1) acc2 += __shfl_down(acc2, s, 32);
-    if (l32 == 0 && valid) d->core[c] = f2bf(acc2 * a.delta_scale);
+    tree_levels<8>(w[0], w[1], w[2], w[3]);
+    const float out = (w[0] + w[2]) + (w[1] + w[3]);
+    if (q == 0 && valid) d->core[c] = f2bf(out * a.delta_scale);
   }
   __syncthreads();
   // state write-back (this block's head only; read again next step)
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (m.tid + kMT * j < squads)
+  for (int j = 0; j < SPT; ++j)
+    if (m.tid + kMT * j < SQUADS)
       G(reinterpret_cast<u32x4*>(st_g))[m.tid + kMT * j] = reinterpret_cast<const u32x4*>(state)[m.tid + kMT * j];
   // gated RMSNorm with a serial sum (cooperative_norm.hex:139-182)
   if (m.tid < VD) {
@@ -578,11 +643,7 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     d->sq[m.tid] = v * v;
   }
   __syncthreads();
-  if (m.tid == 0) {
-    float total = 0.0f;
-    for (int i = 0; i < VD; ++i) total += d->sq[i];
-    d->gates[2] = total;
-  }
+  if (m.tid == 0) d->gates[2] = serial_sum<VD>(d->sq);
   __syncthreads();
   if (m.tid < VD) {
     const float rms = nsqrt(d->gates[2] / (float)VD + a.eps);
@@ -598,47 +659,46 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
 // -------------------------------- phase: output projection + residual (S64)
 
 // bf16(bf16(tree64(x . w_r)) (+) residual_r) (qwen3.fused.residual,
-// simt.hex:442-538) over the polled mixer output `x_mix` (cols BF16), one
-// reference lane per physical lane, two rows per wave. Blocks kh < KH of a
-// linear layer also write the q and k conv history of key head kh.
-__device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int cols) {
+// simt.hex:442-538) over the polled mixer output (COLS BF16), one reference
+// lane per physical lane, two rows per wave. Blocks kh < KH of a linear layer
+// also write the q and k conv history of key head kh.
+template <class S, int COLS>
+__device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  const int H = a.H, np = cols >> 1, nj = (np + 63) >> 6;
+  constexpr int NP = COLS / 2, NJ = (NP + 63) / 64;
   const int prow = m.gw;  // row pair
-  uint32_t wv[2][kOutJ];
-  if (prow < (H >> 1)) {
+  const bool has_rows = prow < S::H / 2;
+  uint32_t wv[2][NJ];
+  if (has_rows) {
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const uint16_t* w = Ly.out_w + (size_t)(2 * prow + r) * cols;
+      const uint16_t* w = Ly.out_w + (size_t)(2 * prow + r) * COLS;
 #pragma unroll
-      for (int j = 0; j < kOutJ; ++j)
-        if (j < nj) wv[r][j] = ldd_at(w, (uint32_t)min(m.lane + 64 * j, np - 1) * 4u);
+      for (int j = 0; j < NJ; ++j) wv[r][j] = ldd_at(w, (uint32_t)min(m.lane + 64 * j, NP - 1) * 4u);
     }
   }
-  poll_words<4>(m, Ly.x_mix, np, Identity{}, m.vec);
-  if (!Ly.full && (int)blockIdx.x < a.KH && blockIdx.x < (unsigned)a.VH) {
+  poll_words<(NP + kMT - 1) / kMT>(m, Ly.x_mix, NP, Identity{}, m.vec);
+  if (!Ly.full && (int)blockIdx.x < S::KH) {
     // q and k history of key head kh = blockIdx.x (its raw values are still in
     // this block's LDS from the previous phase).
     const DeltaLds* d = reinterpret_cast<const DeltaLds*>(m.big);
-    const int kh = blockIdx.x, KD = a.KD;
-    const int64_t slot = ((int64_t)G(a.params)[0] % 3) * a.QKV;
-    if (m.tid < 2 * KD) {
-      const int ch = m.tid < KD ? kh * KD + m.tid : a.KS + kh * KD + (m.tid - KD);
+    const int kh = blockIdx.x;
+    const int64_t slot = ((int64_t)G(a.params)[0] % 3) * S::QKV;
+    if (m.tid < 2 * S::KD) {
+      const int ch = m.tid < S::KD ? kh * S::KD + m.tid : S::KS + kh * S::KD + (m.tid - S::KD);
       G(a.cache)[Ly.conv_base + slot + ch] = d->raw_qk[m.tid];
     }
   }
-  if (prow < (H >> 1)) {
+  if (has_rows) {
     float v[2];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kOutJ; ++j) {
-        const int p = m.lane + 64 * j;
-        if (j < nj && p < np) pair_acc(lo, hi, m.vec[p], wv[r][j]);
-      }
+      for (int j = 0; j < NJ; ++j)
+        if (NP % 64 == 0 || m.lane + 64 * j < NP) pair_acc(lo, hi, m.vec[m.lane + 64 * j], wv[r][j]);
       v[r] = tree64_lanes(lo + hi);
     }
     if (m.lane == 0) {
@@ -657,31 +717,28 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
 // residual. Waves gw <= E compute router row gw (moe.hex:4-84): physical lane
 // 2r + h runs reference lane r's low (h = 0) or high (h = 1) accumulator over
 // floats 64k + lane.
+template <class S>
 __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const CQ35_CONST MegaArgs& a = m.a;
-  const int H = a.H, rows = a.E + 1, nj = (H + 63) >> 6;
-  float wv[kRouterJ];
-  const bool has_row = m.gw < rows;
+  constexpr int H = S::H, ROWS = S::E + 1, NJ = (H + 63) / 64;
+  float wv[NJ];
+  const bool has_row = m.gw < ROWS;
   if (has_row) {
-    const float* w = m.gw < a.E ? Ly.router + (size_t)m.gw * H : Ly.shared_gate;
+    const float* w = m.gw < S::E ? Ly.router + (size_t)m.gw * H : Ly.shared_gate;
 #pragma unroll
-    for (int j = 0; j < kRouterJ; ++j)
-      if (j < nj) wv[j] = ldf_at(w, (uint32_t)min(64 * j + m.lane, H - 1) * 4u);
+    for (int j = 0; j < NJ; ++j) wv[j] = ldf_at(w, (uint32_t)min(64 * j + m.lane, H - 1) * 4u);
   }
   f32x4 w0, w1;
-  norm_weights(m, Ly.post_norm, w0, w1);
-  poll_words<2>(m, Ly.x_attn, H >> 1, Identity{}, reinterpret_cast<uint32_t*>(m.xa));
-  norm_row(m, m.xa, w0, w1);
+  norm_weights<S>(m, Ly.post_norm, w0, w1);
+  poll_words<(H / 2 + kMT - 1) / kMT>(m, Ly.x_attn, H / 2, Identity{}, reinterpret_cast<uint32_t*>(m.xa));
+  norm_row<S>(m, m.xa, w0, w1, m.a.eps);
   if (has_row) {
     const uint16_t* xe = reinterpret_cast<const uint16_t*>(m.xn);
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kRouterJ; ++j) {
-      const int i = 64 * j + m.lane;
-      if (j < nj && i < H) acc += bf2f(xe[i]) * wv[j];
-    }
+    for (int j = 0; j < NJ; ++j)
+      if (H % 64 == 0 || 64 * j + m.lane < H) acc += bf2f(xe[64 * j + m.lane]) * wv[j];
     float v = acc + lane_down<1>(acc);
     v += lane_down<32>(v);
     v += lane_down<16>(v);
@@ -694,127 +751,90 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
 
 // ----------------------------------------- phase: top-k select + gate / up
 
-// Every block ranks the experts itself (moe.hex:86-252): without NaNs, top-k
-// rounds of a wave-wide (value, lowest index) maximum; otherwise the
-// reference's rank formula. Then dual S256 gate/up rows over the selected
-// and shared experts (moe.hex:254-333): routed bf16(silu(g) * u * p_slot),
-// shared bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)).
+// Every block ranks the experts itself with the reference's formula
+// (moe.hex:86-252), one thread per expert:
+// rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}, ids[rank] = e for
+// rank < K; then p_j = exp(l_j - l_0) / den with den summed left to right.
+// Two threads per expert (adjacent lanes) each count over half of the others.
+template <class S>
 __device__ __forceinline__ void select_experts(const Mega& m) {
-  const CQ35_CONST MegaArgs& a = m.a;
   MegaMisc* s = m.misc;
-  const int E = a.E, K = a.K;
-  if (m.tid == 0) s->any_nan = 0;
-  __syncthreads();
-  for (int e = m.tid; e < E; e += kMT)
-    if (s->logits[e] != s->logits[e]) s->any_nan = 1;
-  __syncthreads();
-  if (!s->any_nan) {
-    if (m.wave == 0) {
-      unsigned long long taken = 0;  // bit j: lane's j-th candidate chosen (E <= 4096)
-      for (int k = 0; k < K; ++k) {
-        unsigned long long mine = 0ull;
-        for (int j = 0, e = m.lane; e < E; ++j, e += 64) {
-          if ((taken >> j) & 1ull) continue;
-          const float le = s->logits[e];
-          const uint32_t u = le == 0.0f ? 0u : fbits(le);
-          const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-          const unsigned long long key =
-              ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
-          mine = key > mine ? key : mine;
-        }
-        unsigned long long best = mine;
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-          const unsigned long long o = __shfl_xor(best, sh, 64);
-          best = o > best ? o : best;
-        }
-        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-        if ((e & 63) == m.lane) taken |= 1ull << (e >> 6);
-        if (m.lane == 0) {
-          s->ids[k] = e;
-          s->chosen[k] = s->logits[e];
-        }
-      }
+  constexpr int HALF = (S::E + 1) / 2;
+  static_assert(S::E % 8 == 0, "expert count");
+  for (int e0 = 0; e0 < S::E; e0 += kMT / 2) {
+    const int e = e0 + (m.tid >> 1), part = m.tid & 1;
+    const float le = e < S::E ? s->logits[e] : 0.0f;
+    int rank = 0;
+    const float* lg = s->logits + part * HALF;
+#pragma unroll 8
+    for (int i = 0; i < HALF; ++i) {
+      const int ii = part * HALF + i;
+      const float o = lg[i];
+      rank += (ii < S::E && (o > le || (ii < e && !(le > o)))) ? 1 : 0;
     }
-  } else {
-    for (int e = m.tid; e < E; e += kMT) {
-      const float le = s->logits[e];
-      int rank = 0;
-      for (int i = 0; i < E; ++i) {
-        const float o = s->logits[i];
-        rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
-      }
-      if (rank < K) {
-        s->ids[rank] = e;
-        s->chosen[rank] = le;
-      }
+    rank += __shfl_xor(rank, 1, 64);
+    if (e < S::E && part == 0 && rank < S::K) {
+      s->ids[rank] = e;
+      s->chosen[rank] = le;
     }
   }
   __syncthreads();
   if (m.wave == 0) {
-    const float ex = m.lane < K ? hexp(s->chosen[m.lane] - s->chosen[0]) : 0.0f;
+    const float ex = m.lane < S::K ? hexp(s->chosen[m.lane] - s->chosen[0]) : 0.0f;
     float den = 0.0f;
-    for (int j = 0; j < K; ++j) den = den + __shfl(ex, j, 64);
-    if (m.lane < K) s->probs[m.lane] = ex / den;
-    if (m.lane == 0) s->scalars[0] = sigmoid(s->logits[E]);
+    for (int j = 0; j < S::K; ++j) den = den + __shfl(ex, j, 64);
+    if (m.lane < S::K) s->probs[m.lane] = ex / den;
+    if (m.lane == 0) s->scalars[0] = sigmoid(s->logits[S::E]);
   }
   __syncthreads();
 }
 
-__device__ __forceinline__ void gate_rows(const Mega& m, const CQ35_CONST MegaLayer& Ly, int row,
-                                          const uint16_t*& g, const uint16_t*& u) {
-  const CQ35_CONST MegaArgs& a = m.a;
-  const int routed = a.K * a.I;
-  if (row < routed) {
-    const int slot = row / a.I;
-    const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
-    const size_t e = (size_t)id * a.I + (row - slot * a.I);
-    g = Ly.gate_exps + e * a.H;
-    u = Ly.up_exps + e * a.H;
-  } else {
-    g = Ly.sgate + (size_t)(row - routed) * a.H;
-    u = Ly.sup + (size_t)(row - routed) * a.H;
-  }
-}
-
+// Dual S256 gate/up rows over the selected and shared experts
+// (moe.hex:254-333): routed bf16(silu(g) * u * p_slot), shared
+// bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)).
+template <class S>
 __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const CQ35_CONST MegaArgs& a = m.a;
-  const int H = a.H, quads = H >> 3;
-  const int routed = a.K * a.I, pairs = (routed + a.SI) >> 1;
-  u32x4 gv[kPairsG][2][4], uv[kPairsG][2][4];
+  constexpr int H = S::H, QH = S::QH, NQ = S::NQA;
+  constexpr int ROUTED = S::K * S::I, PAIRS = (ROUTED + S::SI) / 2;
+  u32x4 gv[kPairsG][2][NQ], uv[kPairsG][2][NQ];
   // the shared expert's rows do not depend on the routing: load them first
 #pragma unroll
   for (int k = 0; k < kPairsG; ++k) {
     const int p = m.gw + m.nw * k;
-    if (p < pairs && 2 * p >= routed) {
+    if (p < PAIRS && 2 * p >= ROUTED) {
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const uint16_t* g = Ly.sgate + (size_t)(2 * p + r - routed) * H;
-        const uint16_t* u = Ly.sup + (size_t)(2 * p + r - routed) * H;
+        const uint16_t* g = Ly.sgate + (size_t)(2 * p + r - ROUTED) * H;
+        const uint16_t* u = Ly.sup + (size_t)(2 * p + r - ROUTED) * H;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t off = (uint32_t)min(m.lane + 64 * j, quads - 1) * 16u;
+        for (int j = 0; j < NQ; ++j) {
+          const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
           gv[k][r][j] = ldq_at(g, off);
           uv[k][r][j] = ldq_at(u, off);
         }
       }
     }
   }
-  poll_words<3>(m, Ly.x_router, a.E + 1, Identity{}, reinterpret_cast<uint32_t*>(m.misc->logits));
-  select_experts(m);
+  poll_words<(S::E + 1 + kMT - 1) / kMT>(m, Ly.x_router, S::E + 1, Identity{},
+                                          reinterpret_cast<uint32_t*>(m.misc->logits));
+  select_experts<S>(m);
 #pragma unroll
   for (int k = 0; k < kPairsG; ++k) {
     const int p = m.gw + m.nw * k;
-    if (p < pairs && 2 * p < routed) {
+    if (p < PAIRS && 2 * p < ROUTED) {
+      // both rows of a pair lie in one expert slot (I is even)
+      const int slot = (2 * p) / S::I;
+      const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
-        const uint16_t *g, *u;
-        gate_rows(m, Ly, 2 * p + r, g, u);
+        const size_t e = (size_t)id * S::I + (2 * p + r - slot * S::I);
+        const uint16_t* g = Ly.gate_exps + e * H;
+        const uint16_t* u = Ly.up_exps + e * H;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t off = (uint32_t)min(m.lane + 64 * j, quads - 1) * 16u;
+        for (int j = 0; j < NQ; ++j) {
+          const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
           gv[k][r][j] = ldq_at(g, off);
           uv[k][r][j] = ldq_at(u, off);
         }
@@ -825,7 +845,7 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
 #pragma unroll
   for (int k = 0; k < kPairsG; ++k) {
     const int p = m.gw + m.nw * k;
-    if (p < pairs) {
+    if (p < PAIRS) {
       uint16_t y[2];
 #pragma unroll
       for (int r = 0; r < 2; ++r) {
@@ -833,8 +853,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
         quad_zero(ga);
         quad_zero(ua);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (m.lane + 64 * j < quads) {
+        for (int j = 0; j < NQ; ++j)
+          if (QH % 64 == 0 || m.lane + 64 * j < QH) {
             const u32x4 xq = m.xn[m.lane + 64 * j];
             quad_acc(ga, xq, gv[k][r][j]);
             quad_acc(ua, xq, uv[k][r][j]);
@@ -845,7 +865,7 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
         const float gb = rbf(gsum), ub = rbf(usum);
         const float activated = silu(gb);
         float out;
-        if (row < routed) out = (activated * ub) * m.misc->probs[row / a.I];
+        if (row < ROUTED) out = (activated * ub) * m.misc->probs[row / S::I];
         else out = rbf(rbf(activated) * ub) * shared_p;
         y[r] = f2bf(out);
       }
@@ -861,51 +881,42 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
 // separate S32 over the shared activations, one reference lane per physical
 // lane (lanes 0-31 row 2w, lanes 32-63 row 2w+1);
 // out = bf16(bf16(routed + residual) (+) bf16(shared)).
+template <class S>
 __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const CQ35_CONST MegaArgs& a = m.a;
-  const int H = a.H, half = m.lane >> 5, r32 = m.lane & 31;
-  const int ip = a.I >> 1, rp = (a.K * a.I) >> 1, sp = a.SI >> 1;
-  const int nj = (rp + 31) >> 5, nsj = (sp + 31) >> 5;
+  constexpr int H = S::H, IP = S::I / 2, RP = S::K * IP, SP = S::SI / 2;
+  constexpr int NJ = RP / 32, NSJ = SP / 32, JPS = IP / 32;  // dwords per lane; per expert slot
+  const int half = m.lane >> 5, r32 = m.lane & 31;
   const int prow = m.gw;
-  const int row = 2 * prow + half;
-  const bool has_rows = prow < (H >> 1);
-  uint32_t wr[kDownJ], ws[kDownSJ];
+  const bool has_rows = prow < H / 2;
+  uint32_t wr[NJ], ws[NSJ];
   if (has_rows) {
-    // pair p = r32 + 32j of the routed row lies in expert slot (32j) / ip when
-    // ip is a multiple of 32 (host-checked), so the expert row base is
-    // uniform per j; the lane offset selects the row (half) and the pair
+    // pair r32 + 32j lies in expert slot j / JPS: the row base is uniform per
+    // slot, the lane offset selects the row (half) and the pair
+    const uint32_t base = (uint32_t)(half * IP + r32) * 4u;
 #pragma unroll
-    for (int j = 0; j < kDownJ; ++j) {
-      if (j < nj) {
-        const int slot = (32 * j) / ip;
-        const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
-        const uint16_t* w = Ly.down_exps + ((size_t)id * H + 2 * prow) * a.I;
-        wr[j] = ldd_at(w, (uint32_t)(half * ip + min(r32 + 32 * j, rp - 1) - slot * ip) * 4u);
-      }
+    for (int slot = 0; slot < S::K; ++slot) {
+      const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
+      const uint16_t* w = Ly.down_exps + ((size_t)id * H + 2 * prow) * S::I;
+#pragma unroll
+      for (int jj = 0; jj < JPS; ++jj) wr[slot * JPS + jj] = ldd_at(w, base + jj * 128u);
     }
-    const uint16_t* sw = Ly.sdown + (size_t)(2 * prow) * a.SI;
+    const uint16_t* sw = Ly.sdown + (size_t)(2 * prow) * S::SI;
 #pragma unroll
-    for (int j = 0; j < kDownSJ; ++j)
-      if (j < nsj) ws[j] = ldd_at(sw, (uint32_t)(half * sp + min(r32 + 32 * j, sp - 1)) * 4u);
+    for (int j = 0; j < NSJ; ++j) ws[j] = ldd_at(sw, (uint32_t)(half * SP + r32 + 32 * j) * 4u);
   }
-  poll_words<5>(m, Ly.x_active, rp + sp, Identity{}, m.vec);
+  poll_words<(RP + SP + kMT - 1) / kMT>(m, Ly.x_active, RP + SP, Identity{}, m.vec);
   if (has_rows) {
     float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kDownJ; ++j) {
-      const int p = r32 + 32 * j;
-      if (j < nj && p < rp) pair_acc(lo, hi, m.vec[p], wr[j]);
-    }
+    for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[r32 + 32 * j], wr[j]);
     const float routed_v = tree32_lanes(lo + hi);
     float slo = 0.0f, shi = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kDownSJ; ++j) {
-      const int p = r32 + 32 * j;
-      if (j < nsj && p < sp) pair_acc(slo, shi, m.vec[rp + p], ws[j]);
-    }
+    for (int j = 0; j < NSJ; ++j) pair_acc(slo, shi, m.vec[RP + r32 + 32 * j], ws[j]);
     const float shared_v = tree32_lanes(slo + shi);
+    const int row = 2 * prow + half;
     const uint16_t out = bf_add(f2bf(routed_v + bf2f(m.xa[row])), f2bf(shared_v));
     const uint16_t other = (uint16_t)__shfl_down((int)out, 32, 64);
     if (m.lane == 0) word_store(Ly.x_out + prow, pack_bf(out, other), m.tag);
@@ -931,70 +942,78 @@ struct ScoreLds {
 };
 static_assert(sizeof(ScoreLds) <= kLdsBigBytes, "score LDS");
 
+template <class S>
 __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  const int HD = a.HD, Q = a.Q, KVH = a.KVH, hpk = Q / KVH;
+  constexpr int HD = S::HD, Q = S::Q, KVH = S::KVH, HPK = Q / KVH, KJ = HD / 32, RH = S::R / 2;
+  static_assert(Q * HD <= 16 * 256 && KVH * HD <= 2 * 256, "score shape");
   const int64_t position = (int64_t)G(a.params)[0];
   const int64_t keys = position + 1;
   const int64_t items = keys * KVH;
   ScoreLds* s = reinterpret_cast<ScoreLds*>(m.big);
-  const int l32 = m.lane & 31, half = m.lane >> 5, kj = HD >> 5;
-  // prefetch the cached keys of this block's first items
+  const int l32 = m.lane & 31, half = m.lane >> 5;
+  // prefetch the cached keys of this wave's first items
   const int64_t item0 = (int64_t)m.gw * 2 + half;
-  float kv0[8];
+  float kv0[KJ];
   if (item0 < items) {
     const int kvh = (int)(item0 / keys);
     const int64_t key = item0 - (int64_t)kvh * keys;
     if (key < position) {
-      const uint16_t* kr = a.cache + Ly.key_base + key * a.KVS + (int64_t)kvh * HD + l32;
+      const uint16_t* kr = a.cache + Ly.key_base + key * S::KVS + (int64_t)kvh * HD + l32;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < kj) kv0[j] = bf2f(G(kr)[32 * j]);
+      for (int j = 0; j < KJ; ++j) kv0[j] = bf2f(G(kr)[32 * j]);
     }
   }
+  // norm weights (shared by all query heads / all key heads) and the RoPE
+  // frequencies do not depend on the projection: load them first
+  constexpr int VPL = HD / 64;  // values per lane
+  float qw_[VPL], kw_[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    qw_[i] = G(Ly.qnorm)[VPL * m.lane + i];
+    kw_[i] = G(Ly.knorm)[VPL * m.lane + i];
+  }
+  const float freq = G(a.freq)[min(m.tid, RH - 1)];
   // query parts of every head, then the raw key and value heads
-  const int qwords = Q * (HD >> 1), kvwords = a.KVS >> 1;
+  constexpr int QWORDS = Q * (HD / 2), KVWORDS = S::KVS / 2;
   auto index = [&](int i) -> int {
-    if (i < qwords) {
-      const int hq = i / (HD >> 1), c = i - hq * (HD >> 1);
+    if (i < QWORDS) {
+      const int hq = i / (HD / 2), c = i - hq * (HD / 2);
       return hq * HD + c;  // words of [q(HD) | gate(HD)] per head
     }
-    return a.QS + (i - qwords);  // k words then v words
+    return S::QS + (i - QWORDS);  // k words then v words
   };
-  poll_words<5>(m, Ly.x_proj, qwords + 2 * kvwords, index, m.vec);
+  poll_words<(QWORDS + 2 * KVWORDS + kMT - 1) / kMT>(m, Ly.x_proj, QWORDS + 2 * KVWORDS, index, m.vec);
   const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
   const uint16_t* kraw = in16 + Q * HD;
-  const uint16_t* vraw = kraw + a.KVS;
+  const uint16_t* vraw = kraw + S::KVS;
   // RoPE table for this position (rope.hex:5-17)
-  const int rh = a.R >> 1;
-  if (m.tid < rh) {
+  if (m.tid < RH) {
     float sn, cs;
-    sincos_q((float)(uint32_t)position * G(a.freq)[m.tid], &sn, &cs);
+    sincos_q((float)(uint32_t)position * freq, &sn, &cs);
     s->rope[m.tid] = cs;
-    s->rope[rh + m.tid] = sn;
+    s->rope[RH + m.tid] = sn;
   }
   __syncthreads();
   // one wave per head: Q query heads then KVH key heads
-  const int vpl = HD >> 6;  // values per lane (HD in {64, 128, 256})
+#pragma unroll 1
   for (int h0 = 0; h0 < Q + KVH; h0 += kMW) {
     const int hh = h0 + m.wave;
     const bool is_q = hh < Q;
-    float x[4], w[4];
+    float x[VPL], w[VPL];
     float t = 0.0f;
     if (hh < Q + KVH) {
       const uint16_t* src = is_q ? in16 + hh * HD : kraw + (hh - Q) * HD;
-      const float* nw = is_q ? Ly.qnorm : Ly.knorm;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i < vpl) {
-          x[i] = bf2f(src[vpl * m.lane + i]);
-          w[i] = G(nw)[vpl * m.lane + i];
-        }
+      for (int i = 0; i < VPL; ++i) {
+        x[i] = bf2f(src[VPL * m.lane + i]);
+        w[i] = is_q ? qw_[i] : kw_[i];
+      }
       // adjacent-pair tree: in-lane pairs first, then the lanes
-      if (vpl == 1) t = x[0] * x[0];
-      else if (vpl == 2) t = x[0] * x[0] + x[1] * x[1];
+      if constexpr (VPL == 1) t = x[0] * x[0];
+      else if constexpr (VPL == 2) t = x[0] * x[0] + x[1] * x[1];
       else t = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
     }
     t = t + lane_down<1>(t);
@@ -1007,20 +1026,22 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
     if (hh < Q + KVH) {
       const float inverse = 1.0f / nsqrt(sum / (float)HD + a.eps);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (i < vpl) s->normed[m.wave][vpl * m.lane + i] = bf2f(bf_mul(f2bf(x[i] * inverse), f2bf(w[i])));
+      for (int i = 0; i < VPL; ++i)
+        s->normed[m.wave][VPL * m.lane + i] = bf2f(bf_mul(f2bf(x[i] * inverse), f2bf(w[i])));
     }
     __syncthreads();
     if (hh < Q + KVH) {
-      for (int c = m.lane; c < HD; c += 64) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = m.lane + 64 * i;
         const float nf = s->normed[m.wave][c];
         float result = nf;
-        if (c < a.R) {
-          const int pair = c % rh;
-          const bool first = c < rh;
-          const float partner = s->normed[m.wave][first ? pair + rh : pair];
+        if (c < S::R) {
+          const int pair = c % RH;
+          const bool first = c < RH;
+          const float partner = s->normed[m.wave][first ? pair + RH : pair];
           const float ac = nf * s->rope[pair];
-          const float bs = partner * s->rope[pair + rh];
+          const float bs = partner * s->rope[pair + RH];
           result = first ? ac - bs : ac + bs;
         }
         const uint16_t rb = f2bf(result);
@@ -1035,35 +1056,35 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   for (int64_t it = item0; it < items; it += 2 * (int64_t)m.nw, ++round) {
     const int kvh = (int)(it / keys);
     const int64_t key = it - (int64_t)kvh * keys;
-    float kv[8];
+    float kv[KJ];
     if (key == position) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < kj) kv[j] = bf2f(s->khat[kvh * HD + l32 + 32 * j]);
+      for (int j = 0; j < KJ; ++j) kv[j] = bf2f(s->khat[kvh * HD + l32 + 32 * j]);
       // K and V of the new position into the cache (V device-coherent)
-      uint16_t* kdst = a.cache + Ly.key_base + position * a.KVS + (int64_t)kvh * HD;
-      uint16_t* vdst = a.cache + Ly.value_base + position * a.KVS + (int64_t)kvh * HD;
-      for (int c = l32; c < HD; c += 32) {
+      uint16_t* kdst = a.cache + Ly.key_base + position * S::KVS + (int64_t)kvh * HD;
+      uint16_t* vdst = a.cache + Ly.value_base + position * S::KVS + (int64_t)kvh * HD;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        const int c = l32 + 32 * j;
         G(kdst)[c] = s->khat[kvh * HD + c];
         __hip_atomic_store(G(vdst) + c, vraw[kvh * HD + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else if (round == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kv[j] = kv0[j];
+      for (int j = 0; j < KJ; ++j) kv[j] = kv0[j];
     } else {
-      const uint16_t* kr = a.cache + Ly.key_base + key * a.KVS + (int64_t)kvh * HD + l32;
+      const uint16_t* kr = a.cache + Ly.key_base + key * S::KVS + (int64_t)kvh * HD + l32;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < kj) kv[j] = bf2f(G(kr)[32 * j]);
+      for (int j = 0; j < KJ; ++j) kv[j] = bf2f(G(kr)[32 * j]);
     }
-    for (int hq = 0; hq < hpk; ++hq) {
-      const int head = kvh * hpk + hq;
+#pragma unroll
+    for (int hq = 0; hq < HPK; ++hq) {
+      const int head = kvh * HPK + hq;
       const uint16_t* qh = s->qhat + head * HD + l32;
       float acc = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (j < kj) acc += bf2f(qh[32 * j]) * kv[j];
+      for (int j = 0; j < KJ; ++j) acc += bf2f(qh[32 * j]) * kv[j];
 #pragma unroll
       for (int sh = 16; sh >= 1; sh >>= 1) acc += __shfl_down(acc, sh, 32);
       if (l32 == 0) word_store(Ly.x_scores + (size_t)head * a.cap + key, fbits(acc * a.attn_scale), m.tag);
@@ -1075,47 +1096,64 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
 // ------------------------------------- phase: attention values (full layers)
 
 // Per (query head, 16-channel chunk) item, the reference's online softmax in
-// 8-key tiles (online.hex:272-331; per-kernel version attention.h): running
-// maximum per tile as a prefix maximum of the tile maxima, alpha_t and
-// p = exp(s - m_t) in parallel, then each channel's serial chain
-// acc = acc * alpha_t + p_0 v_0 + ... + p_7 v_7 while lane 16 runs the
-// denominator; out = bf16(bf16(acc / den) * sigmoid(gate)).
+// 8-key tiles (online.hex:272-331; per-kernel version attention.h):
+//  - tile maxima, and their running maximum as a parallel prefix maximum
+//    (max is exact, so any association gives the reference's values);
+//  - p_k = exp(s_k - m_t) and alpha_t = exp(m_{t-1} - m_t) in parallel;
+//  - every product p_k * v_{k,c} in parallel (each rounds on its own in the
+//    reference too: contraction is off);
+//  - then each channel's chain acc = acc * alpha_t + prod_0 + ... + prod_7 in
+//    order (lanes 0-15), with lane 16 running den = den * alpha_t + p_0 + ...;
+// out = bf16(bf16(acc / den) * sigmoid(gate)). Invalid keys of the last tile
+// contribute p = 0 against key 0's value, as in the reference.
+constexpr int kMegaValueChunk = 256;  // keys per chunk
 struct ValueLds {
-  float p[kChunkKeys];
-  float alpha[kChunkKeys / 8];
-  u32x4 vs[kChunkKeys * 2];  // [key][16 channels] BF16
-  float mx[1];               // tiles (the rest of the big area)
+  float p[kMegaValueChunk];
+  float alpha[kMegaValueChunk / 8];
+  float prod[kMegaValueChunk * kValueChannels];
+  float mx[1];  // tile maxima, then running maxima (the rest of the big area)
 };
 constexpr int kValueMxMax = (kLdsBigBytes - (int)offsetof(ValueLds, mx)) / 4;
 
+template <class S>
 __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  const int HD = a.HD, hpk = a.Q / a.KVH;
-  const int chunks = HD / kValueChannels, items = a.Q * chunks;
+  constexpr int HD = S::HD, HPK = S::Q / S::KVH, CHUNKS = HD / kValueChannels, ITEMS = S::Q * CHUNKS;
+  static_assert(2 * kMegaValueChunk <= kMT, "one V quad per thread per chunk");
   const int64_t position = (int64_t)G(a.params)[0];
   const int64_t keys = position + 1;
   const int tiles = (int)((keys + 7) >> 3);
   ValueLds* s = reinterpret_cast<ValueLds*>(m.big);
   const float ninf = bitsf(0xff800000u);
-  for (int item = blockIdx.x; item < items; item += gridDim.x) {
-    const int head = item / chunks, c0 = (item - head * chunks) * kValueChannels;
-    const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / hpk) * HD + c0;
+  // thread i < 2n stages key i >> 1, channels 8 (i & 1) .. 8 (i & 1) + 7 of a chunk
+  const int vk = m.tid >> 1, vh = m.tid & 1;
+#pragma unroll 1
+  for (int item = blockIdx.x; item < ITEMS; item += gridDim.x) {
+    const int head = item / CHUNKS, c0 = (item - head * CHUNKS) * kValueChannels;
+    const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0;
+    // V quad of key k (key 0 past the end; the new position device-coherently)
+    auto load_v = [&](int64_t k) -> u32x4 {
+      const int64_t safe = k < keys ? k : 0;
+      const uint16_t* src = vbase + safe * S::KVS + 8 * vh;
+      if (safe != position) return G(reinterpret_cast<const u32x4*>(src))[0];
+      const uint64_t lo = __hip_atomic_load(G(reinterpret_cast<const uint64_t*>(src)), __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+      const uint64_t hi = __hip_atomic_load(G(reinterpret_cast<const uint64_t*>(src)) + 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+      return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+    };
     // prefetch the first chunk's V rows (positions before the new one)
-    u32x4 vpre[2];
-    const int n0 = (int)min<int64_t>(kChunkKeys, (int64_t)tiles * 8);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = m.tid + kMT * j;
-      const int64_t k = i >> 1;
-      const int64_t safe = (k < keys && k != position) ? k : 0;
-      if (i < 2 * n0) vpre[j] = G(reinterpret_cast<const u32x4*>(vbase + safe * a.KVS))[i & 1];
+    const int n0 = (int)min<int64_t>(kMegaValueChunk, (int64_t)tiles * 8);
+    u32x4 vq = {0u, 0u, 0u, 0u};
+    if (vk < n0 && (int64_t)vk != position) {
+      const int64_t safe = vk < keys ? vk : 0;
+      vq = G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
     }
     // scores of this head: poll every tile, keep the tile maxima
     const uint64_t* sc = Ly.x_scores + (size_t)head * a.cap;
     for (int t = m.tid; t < tiles; t += kMT) {
-      float mt = ninf;
       uint64_t v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -1127,17 +1165,18 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
         bool ready = true;
 #pragma unroll
         for (int j = 0; j < 8; ++j) ready &= word_ready(v[j], m.tag);
-        if (ready || spin_exhausted(m, spins)) break;
+        if (ready || spin_stop(m, ++spins)) break;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
           if (!word_ready(v[j], m.tag)) v[j] = word_load(sc + (int64_t)t * 8 + j);
       }
+      float mt = ninf;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int64_t k = (int64_t)t * 8 + j;
         const float sk = bitsf((uint32_t)v[j]);
         mt = fmaxf(mt, k < keys ? sk : ninf);
-        if (k < kChunkKeys) s->p[k] = sk;  // first chunk's scores, kept for the weights
+        if (k < kMegaValueChunk) s->p[k] = sk;  // first chunk's scores, kept for the weights
       }
       s->mx[t] = mt;
     }
@@ -1146,61 +1185,73 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
     if (m.tid < kValueChannels / 2)
       gate_word = poll_one(m, Ly.x_proj + ((head * 2 * HD + HD + c0) >> 1) + m.tid);
     __syncthreads();
-    if (m.tid == 0) {
+    if (m.wave == 0) {
+      // running maximum: serial within a lane's segment, then an inclusive
+      // scan of the segment maxima across the wave
+      const int seg = (tiles + 63) >> 6, t0 = m.lane * seg, t1 = min(t0 + seg, tiles);
       float mm = ninf;
-      for (int i = 0; i < tiles; ++i) {
-        mm = fmaxf(mm, s->mx[i]);
-        s->mx[i] = mm;
+      for (int i = t0; i < t1; ++i) mm = fmaxf(mm, s->mx[i]);
+      float inc = mm;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const float o = __shfl_up(inc, d, 64);
+        if (m.lane >= d) inc = fmaxf(inc, o);
+      }
+      float run = __shfl_up(inc, 1, 64);
+      if (m.lane == 0) run = ninf;
+      for (int i = t0; i < t1; ++i) {
+        run = fmaxf(run, s->mx[i]);
+        s->mx[i] = run;
       }
     }
     __syncthreads();
     float acc = 0.0f, den = 0.0f;
-    for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kChunkKeys) {
-      const int n = (int)min<int64_t>(kChunkKeys, (int64_t)tiles * 8 - k0);  // multiple of 8
-      // the new position's row is filled below by threads 0..15 (not staged here)
-      if (k0 == 0) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int i = m.tid + kMT * j;
-          if (i < 2 * n && (int64_t)(i >> 1) != position) s->vs[i] = vpre[j];
-        }
-      } else {
-        for (int i = m.tid; i < 2 * n; i += kMT) {
-          const int64_t k = k0 + (i >> 1);
-          if (k == position) continue;
-          const int64_t safe = k < keys ? k : 0;
-          s->vs[i] = G(reinterpret_cast<const u32x4*>(vbase + safe * a.KVS))[i & 1];
-        }
+    for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kMegaValueChunk) {
+      const int n = (int)min<int64_t>(kMegaValueChunk, (int64_t)tiles * 8 - k0);  // multiple of 8
+      if (m.tid < n) {
+        const int64_t k = k0 + m.tid;
+        const float sk = k0 == 0 ? s->p[m.tid] : bitsf((uint32_t)word_load(sc + k));
+        s->p[m.tid] = k < keys ? hexp(sk - s->mx[k >> 3]) : 0.0f;
       }
-      // the new position's V row was written in the previous phase
-      if (position >= k0 && position < k0 + n && m.tid < kValueChannels) {
-        const uint16_t v = __hip_atomic_load(G(vbase) + position * a.KVS + m.tid, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-        reinterpret_cast<uint16_t*>(s->vs)[(position - k0) * kValueChannels + m.tid] = v;
+      if (m.tid < n / 8) {
+        const int tile = (int)(k0 / 8) + m.tid;
+        s->alpha[m.tid] = hexp((tile > 0 ? s->mx[tile - 1] : ninf) - s->mx[tile]);
       }
-      for (int i = m.tid; i < n; i += kMT) {
-        const int64_t k = k0 + i;
-        const float sk = k0 == 0 ? s->p[i] : bitsf((uint32_t)word_load(sc + k));
-        s->p[i] = k < keys ? hexp(sk - s->mx[k >> 3]) : 0.0f;
-      }
-      for (int i = m.tid; i < n / 8; i += kMT) {
-        const int tile = (int)(k0 / 8) + i;
-        s->alpha[i] = hexp((tile > 0 ? s->mx[tile - 1] : ninf) - s->mx[tile]);
+      u32x4 vcur = vq;
+      if (vk < n && (k0 > 0 || (int64_t)vk == position)) vcur = load_v(k0 + vk);
+      __syncthreads();
+      if (vk < n) {
+        const float pk = s->p[vk];
+        f32x4 o0, o1;
+        o0.x = pk * lo2f(vcur.x); o0.y = pk * hi2f(vcur.x);
+        o0.z = pk * lo2f(vcur.y); o0.w = pk * hi2f(vcur.y);
+        o1.x = pk * lo2f(vcur.z); o1.y = pk * hi2f(vcur.z);
+        o1.z = pk * lo2f(vcur.w); o1.w = pk * hi2f(vcur.w);
+        f32x4* dst = reinterpret_cast<f32x4*>(s->prod + vk * kValueChannels + 8 * vh);
+        dst[0] = o0;
+        dst[1] = o1;
       }
       __syncthreads();
       if (m.wave == 0) {
         if (m.lane < kValueChannels) {
-          const uint16_t* vh = reinterpret_cast<const uint16_t*>(s->vs) + m.lane;
+          const float* pr = s->prod + m.lane;
+#pragma unroll 2
           for (int i = 0; i < n / 8; ++i) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = pr[(i * 8 + j) * kValueChannels];
             acc = acc * s->alpha[i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc = acc + s->p[i * 8 + j] * bf2f(vh[(i * 8 + j) * kValueChannels]);
+            for (int j = 0; j < 8; ++j) acc = acc + x[j];
           }
         } else if (m.lane == kValueChannels) {
+#pragma unroll 2
           for (int i = 0; i < n / 8; ++i) {
+            const f32x4 p0 = reinterpret_cast<const f32x4*>(s->p)[2 * i];
+            const f32x4 p1 = reinterpret_cast<const f32x4*>(s->p)[2 * i + 1];
             den = den * s->alpha[i];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) den = den + s->p[i * 8 + j];
+            den = den + p0.x; den = den + p0.y; den = den + p0.z; den = den + p0.w;
+            den = den + p1.x; den = den + p1.y; den = den + p1.z; den = den + p1.w;
           }
         }
       }
@@ -1225,54 +1276,46 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
 // output_norm, the S32 vocabulary GEMV (simt.hex:348-441) and the greedy
 // first-index argmax (fused_argmax.hex) as a (value, lowest index) maximum.
 // Eight lanes per row (lane q holds reference lanes 4q..4q+3), eight rows per
-// wave per batch; a row streams in pieces of kVocabPiece quads per lane,
+// wave per batch; a row streams in pieces of PIECE quads per lane,
 // double-buffered, so the accumulation stays in reference order.
-constexpr int kVocabPiece = 8;
-
+template <class S>
 __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaArgs& a = m.a;
-  const int H = a.H, quads = H >> 3, V = a.V;
+  constexpr int H = S::H, V = S::V, PER_LANE = (S::QH + 7) / 8;
+  constexpr int PIECE = PER_LANE < 8 ? PER_LANE : 8, PIECES = (PER_LANE + PIECE - 1) / PIECE;
+  static_assert(PIECES * PIECE == PER_LANE && S::QH % 8 == 0, "vocabulary pieces");
+  constexpr int GROUPS = V / 8;  // 8-row groups; group gw + nw*b is this wave's batch b
   const int q = m.lane & 7, g = m.lane >> 3;
-  const int per_lane = quads >> 3;                                // quads per lane per row
-  const int pieces = (per_lane + kVocabPiece - 1) / kVocabPiece;  // per row
-  const int groups = (V + 7) / 8;  // 8-row groups; group gw + nw*b is this wave's batch b
-  const int nbatches = m.gw < groups ? (groups - 1 - m.gw) / m.nw + 1 : 0;
-  const int steps = nbatches * pieces;
-  // piece t = (batch t / pieces, piece t % pieces); group base address is uniform
+  const int nbatches = m.gw < GROUPS ? (GROUPS - 1 - m.gw) / m.nw + 1 : 0;
+  const int steps = nbatches * PIECES;
+  const uint32_t lane_off = (uint32_t)g * (uint32_t)H * 2u + (uint32_t)q * 16u;
+  // piece t = (batch t / PIECES, piece t % PIECES); the group base address is
+  // uniform, quad q + 8(pc*PIECE + j) of the lane's row is at byte 16q + 128(pc*PIECE + j)
   auto load_piece = [&](u32x4* buf, int t) {
-    const int b = t / pieces, pc = t - b * pieces;
-    const int row0 = (m.gw + m.nw * b) * 8;
-    const uint16_t* w = a.head + (size_t)row0 * H;
-    const bool row_ok = row0 + g < V;
+    const int b = t / PIECES, pc = t - b * PIECES;
+    const uint16_t* w = a.head + (size_t)((m.gw + m.nw * b) * 8) * H + pc * PIECE * 64;
 #pragma unroll
-    for (int j = 0; j < kVocabPiece; ++j) {
-      const int qi = q + 8 * (pc * kVocabPiece + j);
-      if (row_ok && pc * kVocabPiece + j < per_lane)
-        buf[j] = ldq_at(w, (uint32_t)g * (uint32_t)H * 2u + (uint32_t)qi * 16u);
-    }
+    for (int j = 0; j < PIECE; ++j) buf[j] = ldq_at(w, lane_off + (uint32_t)j * 128u);
   };
-  u32x4 b0[kVocabPiece], b1[kVocabPiece];
+  u32x4 b0[PIECE], b1[PIECE];
   if (steps > 0) load_piece(b0, 0);
   f32x4 w0, w1;
-  norm_weights(m, a.out_norm, w0, w1);
-  poll_words<2>(m, a.x_final, H >> 1, Identity{}, reinterpret_cast<uint32_t*>(m.xr));
-  norm_row(m, m.xr, w0, w1);
+  norm_weights<S>(m, a.out_norm, w0, w1);
+  poll_words<(H / 2 + kMT - 1) / kMT>(m, a.x_final, H / 2, Identity{}, reinterpret_cast<uint32_t*>(m.xr));
+  norm_row<S>(m, m.xr, w0, w1, a.eps);
   unsigned long long mine = 0ull;
   Quad acc;
   quad_zero(acc);
   auto consume = [&](const u32x4* buf, int t) {
-    const int b = t / pieces, pc = t - b * pieces;
+    const int b = t / PIECES, pc = t - b * PIECES;
 #pragma unroll
-    for (int j = 0; j < kVocabPiece; ++j) {
-      const int qi = q + 8 * (pc * kVocabPiece + j);
-      if (pc * kVocabPiece + j < per_lane) quad_acc(acc, m.xn[qi], buf[j]);
-    }
-    if (pc == pieces - 1) {
+    for (int j = 0; j < PIECE; ++j) quad_acc(acc, m.xn[q + 8 * (pc * PIECE + j)], buf[j]);
+    if (pc == PIECES - 1) {
       const float v = quad_tree<8>(acc);
       quad_zero(acc);
       const int row = (m.gw + m.nw * b) * 8 + g;
-      if (q == 0 && row < V) {
+      if (q == 0) {
         const uint16_t bb = f2bf(v);
         G(a.logits)[row] = bb;
         const unsigned long long key = logit_key(bb, (uint32_t)row);
@@ -1305,6 +1348,7 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
 
 // ------------------------------------------------------------- the kernel
 
+template <class S>
 __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict__ pa) {
   const uint32_t tag = (uint32_t)G(pa->params)[2];
   MegaMisc* misc = reinterpret_cast<MegaMisc*>(mega_lds + kLdsMisc);
@@ -1322,21 +1366,21 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
   const MegaLayer* layers = pa->layers;
   for (int l = 0; l < L; ++l) {
     const MegaLayer* ly = layers + l;
-    phase_project(pa, tag, ly, l);
-    const bool full = phase_ptr(ly)->full != 0;
-    if (full) {
-      phase_scores(pa, tag, ly);
-      phase_values(pa, tag, ly);
+    phase_project<S>(pa, tag, ly, l);
+    if (phase_ptr(ly)->full != 0) {
+      phase_scores<S>(pa, tag, ly);
+      phase_values<S>(pa, tag, ly);
+      phase_outproj<S, S::QS>(pa, tag, ly);
     } else {
-      phase_delta(pa, tag, ly);
+      phase_delta<S>(pa, tag, ly);
       __syncthreads();
+      phase_outproj<S, S::VS>(pa, tag, ly);
     }
-    phase_outproj(pa, tag, ly, full ? phase_ptr(pa)->QS : phase_ptr(pa)->VS);
-    phase_router(pa, tag, ly);
-    phase_gate_up(pa, tag, ly);
-    phase_down(pa, tag, ly);
+    phase_router<S>(pa, tag, ly);
+    phase_gate_up<S>(pa, tag, ly);
+    phase_down<S>(pa, tag, ly);
   }
-  phase_head(pa, tag);
+  phase_head<S>(pa, tag);
 }
 
 }  // namespace cq35

@@ -462,6 +462,7 @@ struct cq35_session {
   MegaArgs margs{};
   MegaArgs* d_margs = nullptr;
   int mega_grid = 0;
+  const void* mega_kernel = nullptr;  // k_decode_step<shape> for this model
   uint32_t seq = 0;
   // kernel timing
   int timed_class = -1;
@@ -496,34 +497,42 @@ void destroy_session(cq35_session* s) {
   delete s;
 }
 
-// Shapes the persistent decode kernel covers (its static per-wave maxima and
-// LDS carve-up); other shapes use the per-kernel path. `why` names the first
-// limit a shape exceeds.
-bool mega_fits(const cq35_config& c, const Dims& d, int grid, int64_t cap, const char** why) {
+// Model shapes the persistent decode kernel is compiled for (mega.h) and the
+// per-grid limits of its work split; other shapes and capacities use the
+// per-kernel path. Returns the shape index (0 = none).
+enum MegaKind { kMegaNone = 0, kMega35B, kMegaMini, kMegaTiny };
+
+template <class S>
+bool shape_is(const cq35_config& c) {
+  return c.moe && c.hidden == S::H && c.vocab == S::V && c.q_heads == S::Q && c.kv_heads == S::KVH &&
+         c.head_dim == S::HD && c.rope_dim == S::R && c.key_heads == S::KH && c.key_dim == S::KD &&
+         c.value_heads == S::VH && c.value_dim == S::VD && c.experts == S::E && c.top_k == S::K &&
+         c.intermediate == S::I && c.shared_intermediate == S::SI;
+}
+
+template <class S>
+bool grid_fits(int grid, int64_t cap) {
   const int64_t nw = (int64_t)grid * kMW;
-  auto no = [&](const char* r) { *why = r; return false; };
-  if (!c.moe) return no("dense model");
-  if (d.H > 2048 || d.H % 8) return no("hidden width above 2048");
-  if (d.VS > 4096 || d.QS > 4096) return no("mixer width above 4096");
-  if (c.key_dim > 128 || c.value_dim > 128 || c.key_dim % 32 || c.value_dim % 2)
-    return no("DeltaNet head dims");
-  if (c.value_heads < c.key_heads || c.value_heads > grid) return no("DeltaNet head counts");
-  if (d.QKV % 2 || d.VS % 2 || c.value_heads % 2 || d.KVS % 2) return no("odd projection segment");
-  if (d.HD != 64 && d.HD != 128 && d.HD != 256) return no("attention head dim");
-  if (d.QS > 4096 || d.KVS > 512 || d.R > 256) return no("attention widths");
-  if (d.QS / 2 + d.KVS > 5 * kMT) return no("attention projection words");
-  const int64_t rows_lin = d.QKV + d.VS + 2LL * c.value_heads, rows_full = 2 * d.QS + 2 * d.KVS;
-  if (std::max(rows_lin, rows_full) / 2 > kPairsA * nw) return no("projection rows per wave");
-  if (d.E + 1 > 1025 || d.K > 64) return no("expert counts");
-  if (d.I % 64 || d.SI % 2) return no("expert width (routed width a multiple of 64)");
-  const int64_t act = d.K * d.I + d.SI;
-  if (act / 2 > kPairsG * nw || act / 2 > 5 * kMT) return no("expert rows");
-  if (d.K * d.I / 2 > 32 * kDownJ || d.SI / 2 > 32 * kDownSJ) return no("down projection widths");
-  if (d.H / 2 > nw || d.E + 1 > nw) return no("rows per wave");
-  if ((cap + 7) / 8 > kValueMxMax) return no("cache capacity above the LDS tile maxima");
-  if ((int64_t)(d.V + 7) / 8 > (int64_t)1 << 30) return no("vocabulary");
-  *why = "";
-  return true;
+  const int64_t rows_lin = S::QKV + S::VS + 2LL * S::VH, rows_full = 2LL * S::QS + 2LL * S::KVS;
+  return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw &&
+         (S::K * S::I + S::SI) / 2 <= kPairsG * nw && S::H / 2 <= nw && S::E + 1 <= nw &&
+         (cap + 7) / 8 <= kValueMxMax;
+}
+
+int mega_kind(const cq35_config& c, int grid, int64_t cap) {
+  if (shape_is<Shape35BA3B>(c)) return grid_fits<Shape35BA3B>(grid, cap) ? kMega35B : kMegaNone;
+  if (shape_is<ShapeMiniMoE>(c)) return grid_fits<ShapeMiniMoE>(grid, cap) ? kMegaMini : kMegaNone;
+  if (shape_is<ShapeTinyMoE>(c)) return grid_fits<ShapeTinyMoE>(grid, cap) ? kMegaTiny : kMegaNone;
+  return kMegaNone;
+}
+
+const void* mega_kernel(int kind) {
+  switch (kind) {
+    case kMega35B: return (const void*)k_decode_step<Shape35BA3B>;
+    case kMegaMini: return (const void*)k_decode_step<ShapeMiniMoE>;
+    case kMegaTiny: return (const void*)k_decode_step<ShapeTinyMoE>;
+    default: return nullptr;
+  }
 }
 
 // Tagged exchange buffers per layer (each region 128-byte aligned), the
@@ -534,13 +543,13 @@ int setup_mega(cq35_session* s) {
   const Dims& d = m.d;
   int grid = 0;
   HIP_TRY(hipDeviceGetAttribute(&grid, hipDeviceAttributeMultiprocessorCount, m.device));
-  const char* why = "";
-  if (!mega_fits(c, d, grid, s->capacity, &why)) return CQ35_OK;
-  if (hipFuncSetAttribute((const void*)k_decode_step, hipFuncAttributeMaxDynamicSharedMemorySize,
-                          kMegaLds) != hipSuccess)
+  const int kind = mega_kind(c, grid, s->capacity);
+  const void* kernel = mega_kernel(kind);
+  if (!kernel) return CQ35_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMegaLds) != hipSuccess)
     return CQ35_OK;
   int occupancy = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, k_decode_step, kMT, kMegaLds) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, kernel, kMT, kMegaLds) != hipSuccess ||
       occupancy < 1)
     return CQ35_OK;
   auto region = [](int64_t words) { return (words + 15) / 16 * 16; };
@@ -629,10 +638,6 @@ int setup_mega(cq35_session* s) {
   a = MegaArgs{};
   a.layers = s->d_layers;
   a.L = (int)d.L;
-  a.H = (int)d.H; a.V = (int)d.V; a.Q = (int)d.Q; a.KVH = (int)d.KVH; a.HD = (int)d.HD;
-  a.R = (int)d.R; a.KH = c.key_heads; a.KD = c.key_dim; a.VH = c.value_heads; a.VD = c.value_dim;
-  a.KS = (int)d.KS; a.VS = (int)d.VS; a.QKV = (int)d.QKV; a.QS = (int)d.QS; a.KVS = (int)d.KVS;
-  a.E = (int)d.E; a.K = (int)d.K; a.I = (int)d.I; a.SI = (int)d.SI;
   a.eps = c.eps;
   a.attn_scale = 1.0f / sqrtf((float)d.HD);        // SCALE_BITS, qwen35.rs:701
   a.delta_scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
@@ -656,6 +661,7 @@ int setup_mega(cq35_session* s) {
   s->d_margs = static_cast<MegaArgs*>(p);
   HIP_TRY(hipMemcpy(s->d_margs, &a, sizeof(MegaArgs), hipMemcpyHostToDevice));
   s->mega_grid = grid;
+  s->mega_kernel = kernel;
   s->mega_ok = true;
   s->mega_on = true;
   if (const char* g = getenv("CQ35_PERSISTENT")) s->mega_on = atoi(g) != 0;
@@ -1011,10 +1017,18 @@ int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* ne
   hipError_t e = hipMemcpyAsync(s->d_params, s->h_params, 3 * sizeof(uint64_t), hipMemcpyHostToDevice,
                                 s->stream);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "parameter upload: %s", hipGetErrorString(e));
-  Launcher L{s};
-  L(KC_DECODE_STEP, k_decode_step, dim3((unsigned)s->mega_grid), dim3(kMT), (size_t)kMegaLds,
-    (const MegaArgs*)s->d_margs);
-  e = hipGetLastError();
+  const MegaArgs* args = s->d_margs;
+  void* kargs[] = {(void*)&args};
+  if (s->timed_class == KC_DECODE_STEP && s->ev_used < kMaxTimedEvents) {
+    // events stamped by the dispatch packet, as for the per-kernel classes
+    e = hipExtLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)kMegaLds,
+                           s->stream, s->ev[2 * s->ev_used], s->ev[2 * s->ev_used + 1], 0);
+    ++s->ev_used;
+  } else {
+    e = hipLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)kMegaLds,
+                        s->stream);
+  }
+  if (e == hipSuccess) e = hipGetLastError();
   if (e == hipSuccess)
     e = hipMemcpyAsync(s->h_best, s->d_best, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost, s->stream);
   if (e == hipSuccess && logits)
