@@ -39,8 +39,7 @@ constexpr int kMT = 512;       // threads per block
 constexpr int kMW = kMT / 64;  // waves per block
 
 // Per-wave work maxima.
-constexpr int kPairsA = 4;       // projection row pairs per wave
-constexpr int kPairsG = 2;       // gate/up row pairs per wave
+constexpr int kPairsA = 3;       // projection row pairs per wave
 
 // Model shapes the persistent step is compiled for. Widths follow
 // ModelConfig (src/spec.rs:33-62); derived sizes as in spec.rs:293-362.
@@ -59,7 +58,7 @@ struct MegaShape {
   static_assert(QS <= 4096 && VS <= 4096 && KVS <= 512 && R <= 256 && R % 2 == 0, "attention widths");
   static_assert(QS / 2 + KVS <= 5 * kMT, "attention projection words");
   static_assert(E + 1 <= 1025 && K <= 64 && I % 64 == 0 && SI % 64 == 0, "expert shapes");
-  static_assert((K * I + SI) / 2 <= 5 * kMT, "expert rows");
+  static_assert((K * I + SI) / 2 + 1 <= 5 * kMT, "expert rows");
   static_assert(V % 8 == 0, "vocabulary in groups of 8 rows");
 };
 // qwen36-35b-a3b (src/spec.rs:153-183) and the two reduced MoE test shapes.
@@ -73,6 +72,8 @@ struct MegaLayer {
   const uint16_t* seg_w[4];
   int seg_rows[4];
   // linear (Gated DeltaNet)
+  const uint16_t* alpha_w;  // ssm_alpha [VH, H]
+  const uint16_t* beta_w;   // ssm_beta [VH, H]
   const float* dt;
   const float* a;
   const float* gnorm;
@@ -95,7 +96,8 @@ struct MegaLayer {
   uint64_t* x_mix;     // gated core (VS/2) or gated attention context (QS/2)
   uint64_t* x_attn;    // residual after the mixer (H/2)
   uint64_t* x_router;  // E+1 F32 logits
-  uint64_t* x_active;  // (K*I+SI)/2
+  uint64_t* x_active;  // routed activations (K*I/2)
+  uint64_t* x_shared;  // shared-expert bf16(bf16(silu(g)) * u), before the gate (SI/2)
   uint64_t* x_scores;  // Q * capacity F32 scores (full layers)
   uint64_t* x_out;     // output hidden row (H/2) = next layer's x_h
 };
@@ -126,7 +128,7 @@ constexpr int kLdsVec = 12288;     // polled words (4096)
 constexpr int kLdsMisc = 28672;    // logits, ids, probs, reductions
 constexpr int kLdsBig = 36864;
 constexpr int kLdsBigBytes = 53248;
-constexpr int kMegaLds = kLdsBig + kLdsBigBytes;
+constexpr int kMegaLdsBase = kLdsBig + kLdsBigBytes;
 
 struct MegaMisc {
   float logits[1025];
@@ -137,6 +139,7 @@ struct MegaMisc {
   float scalars[8];
   int abort;
   int any_nan;
+  int bid, grid;  // block index and grid size, re-read by every phase
 };
 static_assert(sizeof(MegaMisc) <= kLdsBig - kLdsMisc, "misc LDS");
 
@@ -145,6 +148,7 @@ extern __shared__ __align__(16) unsigned char mega_lds[];
 // Pointers read from the argument tables are generic; every HBM access goes
 // through the global address space so it compiles to global (not flat)
 // memory instructions.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #define CQ35_GLOBAL __attribute__((address_space(1)))
 #define CQ35_CONST __attribute__((address_space(4)))
 #define CQ35_LDS __attribute__((address_space(3)))
@@ -178,7 +182,7 @@ __device__ __forceinline__ const CQ35_CONST T* phase_ptr(const T* p) {
 struct Mega {
   const CQ35_CONST MegaArgs& a;
   uint32_t tag;
-  int tid, lane, wave, gw, nw;
+  int tid, lane, wave, gw, nw, bid, grid;
   u32x4* xn;
   uint16_t* xr;
   uint16_t* xa;
@@ -193,9 +197,14 @@ __device__ __forceinline__ Mega make_mega(const MegaArgs* pa, uint32_t tag) {
   asm volatile("" : "+v"(tid));
   // wave-level indices are uniform: scalar registers, so weight rows get
   // scalar base addresses (one 32-bit lane offset per load)
+  // read from LDS (written once by the kernel), so values derived from the
+  // block index are recomputed per phase rather than held across the loop
+  const MegaMisc* mm = reinterpret_cast<const MegaMisc*>(mega_lds + kLdsMisc);
+  const int bid = __builtin_amdgcn_readfirstlane(mm->bid);
+  const int grid = __builtin_amdgcn_readfirstlane(mm->grid);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int gw = __builtin_amdgcn_readfirstlane((int)blockIdx.x * kMW + wave);
-  const int nw = __builtin_amdgcn_readfirstlane((int)gridDim.x * kMW);
+  const int gw = bid * kMW + wave;
+  const int nw = grid * kMW;
   return Mega{*a,
               tag,
               tid,
@@ -203,6 +212,8 @@ __device__ __forceinline__ Mega make_mega(const MegaArgs* pa, uint32_t tag) {
               wave,
               gw,
               nw,
+              bid,
+              grid,
               reinterpret_cast<u32x4*>(mega_lds + kLdsXn),
               reinterpret_cast<uint16_t*>(mega_lds + kLdsXr),
               reinterpret_cast<uint16_t*>(mega_lds + kLdsXa),
@@ -246,17 +257,16 @@ __device__ __forceinline__ bool spin_stop(const Mega& m, unsigned spins) {
   return false;
 }
 
-// Poll n words (word i = src_index(i)) until every tag matches, then write
-// the payloads to dst[i]. Up to MAXW words per thread; block-wide; ends with
-// a barrier.
-template <int MAXW, typename Index>
-__device__ __forceinline__ void poll_words(const Mega& m, const uint64_t* src, int n, Index src_index,
-                                           uint32_t* dst) {
+// Poll n words (word i at addr(i)) until every tag matches, then write the
+// payloads to dst[i]. Up to MAXW words per thread; block-wide; ends with a
+// barrier.
+template <int MAXW, typename Addr>
+__device__ __forceinline__ void poll_words(const Mega& m, int n, Addr addr, uint32_t* dst) {
   uint64_t v[MAXW];
 #pragma unroll
   for (int j = 0; j < MAXW; ++j) {
     const int i = min(m.tid + kMT * j, n - 1);
-    v[j] = word_load(src + src_index(i));
+    v[j] = word_load(addr(i));
   }
   unsigned spins = 0;
   while (true) {
@@ -267,7 +277,7 @@ __device__ __forceinline__ void poll_words(const Mega& m, const uint64_t* src, i
 #pragma unroll
     for (int j = 0; j < MAXW; ++j) {
       const int i = min(m.tid + kMT * j, n - 1);
-      if (!word_ready(v[j], m.tag)) v[j] = word_load(src + src_index(i));
+      if (!word_ready(v[j], m.tag)) v[j] = word_load(addr(i));
     }
   }
 #pragma unroll
@@ -278,8 +288,10 @@ __device__ __forceinline__ void poll_words(const Mega& m, const uint64_t* src, i
   __syncthreads();
 }
 
-struct Identity {
-  __device__ __forceinline__ int operator()(int i) const { return i; }
+// Words i of one buffer.
+struct Span {
+  const uint64_t* base;
+  __device__ __forceinline__ const uint64_t* operator()(int i) const { return base + i; }
 };
 
 // Poll one word per calling thread (any subset of threads); returns the payload.
@@ -355,7 +367,7 @@ __device__ __forceinline__ void load_hidden(const Mega& m, const uint64_t* words
     if (m.tid < S::QH) reinterpret_cast<u32x4*>(raw)[m.tid] = G(row)[m.tid];
     __syncthreads();
   } else {
-    poll_words<(S::H / 2 + kMT - 1) / kMT>(m, words, S::H / 2, Identity{}, reinterpret_cast<uint32_t*>(raw));
+    poll_words<(S::H / 2 + kMT - 1) / kMT>(m, S::H / 2, Span{words}, reinterpret_cast<uint32_t*>(raw));
   }
 }
 
@@ -412,27 +424,51 @@ __device__ __forceinline__ const uint16_t* seg_row(const CQ35_CONST MegaLayer& L
 
 // Normalised hidden row x grouped BF16 matrices (group-project,
 // group_projection.hex:3-97): S256 split pairs, a physical lane holding
-// reference lanes 4q..4q+3; row pairs (2p, 2p+1) per output word.
+// reference lanes 4q..4q+3; row pairs (2p, 2p+1) per output word. The
+// weights are issued by the previous phase (the last phase of the previous
+// layer), so they stream while that phase computes.
+// Pairs k < kPairsEarly are issued one phase early (before the previous
+// layer's down projection waits); the rest at the start of the projection.
+constexpr int kPairsEarly = 2;
 template <class S>
-__device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int l) {
-  const Mega m = make_mega(pa, tag);
+struct ProjRegs {
+  u32x4 w[kPairsA][2][S::NQA];
+};
+
+template <class S, int K0, int K1>
+__device__ __forceinline__ void issue_project(const MegaArgs* pa, const MegaLayer* ly, ProjRegs<S>& r) {
+  const Mega m = make_mega(pa, 0);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  constexpr int NQ = S::NQA;
-  const int total = Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3];
-  const int pairs = total >> 1;
-  u32x4 wv[kPairsA][2][NQ];
+  const int pairs = (Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3]) >> 1;
 #pragma unroll
-  for (int k = 0; k < kPairsA; ++k) {
+  for (int k = K0; k < K1; ++k) {
     const int p = m.gw + m.nw * k;
     if (p < pairs) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const uint16_t* w = seg_row(Ly, 2 * p + r, S::H);
+      for (int rr = 0; rr < 2; ++rr) {
+        const uint16_t* w = seg_row(Ly, 2 * p + rr, S::H);
 #pragma unroll
-        for (int j = 0; j < NQ; ++j) wv[k][r][j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
+        for (int j = 0; j < S::NQA; ++j)
+          r.w[k][rr][j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
       }
+    } else {
+      // defined on every path, so the registers are not carried across phases
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+        for (int j = 0; j < S::NQA; ++j) r.w[k][rr][j] = u32x4{0u, 0u, 0u, 0u};
     }
   }
+}
+
+template <class S>
+__device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int l,
+                                              ProjRegs<S>& r) {
+  issue_project<S, kPairsEarly, kPairsA>(pa, ly, r);
+  const Mega m = make_mega(pa, tag);
+  const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
+  constexpr int NQ = S::NQA;
+  const int pairs = (Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3]) >> 1;
   f32x4 w0, w1;
   norm_weights<S>(m, Ly.in_norm, w0, w1);
   load_hidden<S>(m, Ly.x_h, m.xr, l == 0);
@@ -443,13 +479,13 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
     if (p < pairs) {
       float v[2];
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int rr = 0; rr < 2; ++rr) {
         Quad acc;
         quad_zero(acc);
 #pragma unroll
         for (int j = 0; j < NQ; ++j)
-          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], wv[k][r][j]);
-        v[r] = quad_tree<64>(acc);
+          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], r.w[k][rr][j]);
+        v[rr] = quad_tree<64>(acc);
       }
       if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
     }
@@ -463,7 +499,9 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
 // and k (linear_prepare.hex:84-131), the gates (fused_delta.hex:1-20), the
 // delta step of the head's VD channels with the state staged in LDS
 // (cached_delta.hex:69-168, D32 trees) and the gated RMSNorm x SiLU(z)
-// (cooperative_norm.hex:139-182). The v channels' conv history is written
+// (cooperative_norm.hex:139-182). The head's alpha and beta rows of the
+// grouped projection (S256 over the normalised row the block already holds)
+// are computed here by waves 0 and 1. The v channels' conv history is written
 // here; the q and k channels' history is shared with the other value heads
 // of the key head and is written by block kh in the next phase, after every
 // reader has finished.
@@ -475,28 +513,34 @@ struct DeltaLds {
   uint16_t core[128];
   uint16_t raw_qk[256]; // raw q | k of the key head (history written next phase)
   float gates[4];       // decay, rate, norms
+  uint16_t ab[2];       // alpha, beta of the head
 };
-constexpr int kDeltaState = 8192;  // offset of the state rows in the big area
-static_assert(sizeof(DeltaLds) <= kDeltaState, "delta LDS");
+static_assert(sizeof(DeltaLds) <= kLdsBigBytes, "delta LDS");
 
 template <class S>
 __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  const int h = blockIdx.x;
+  const int h = m.bid;
   if (h >= S::VH) return;  // uniform per block
   constexpr int KD = S::KD, VD = S::VD, NCH = 2 * KD + VD;
-  constexpr int SQUADS = VD * KD / 8, SPT = (SQUADS + kMT - 1) / kMT;
-  static_assert(SQUADS * 16 <= kLdsBigBytes - kDeltaState && NCH <= kMT, "delta shape");
+  constexpr int KJ = KD / 32, CPP = kMT / 8, PASSES = (VD + CPP - 1) / CPP;
+  static_assert(NCH <= kMT, "delta shape");
   const int kh = h % S::KH;
   DeltaLds* d = reinterpret_cast<DeltaLds*>(m.big);
-  uint16_t* state = reinterpret_cast<uint16_t*>(m.big + kDeltaState);
   uint16_t* st_g = a.cache + Ly.state_base + (size_t)h * VD * KD;
-  // prefetch: state rows, conv taps, history, gate parameters
-  u32x4 sv[SPT];
+  // prefetch: this thread's state slices (channel c = pass * CPP + tid / 8,
+  // key elements 4q + i + 32j, 8 bytes per j), conv taps, history, gates
+  const int q = m.lane & 7, sub = m.tid >> 3;
+  u32x2 sv[PASSES][KJ];
 #pragma unroll
-  for (int j = 0; j < SPT; ++j) sv[j] = ldq_at(st_g, (uint32_t)min(m.tid + kMT * j, SQUADS - 1) * 16u);
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int cc = min(ps * CPP + sub, VD - 1);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+      sv[ps][j] = *G(reinterpret_cast<const u32x2*>(st_g + (size_t)cc * KD + 4 * q + 32 * j));
+  }
   const int64_t position = (int64_t)G(a.params)[0];
   int ch = 0;
   if (m.tid < KD) ch = kh * KD + m.tid;
@@ -513,23 +557,35 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   }
   const float dt = G(Ly.dt)[h], aa = G(Ly.a)[h];
   const float gw = m.tid < VD ? G(Ly.gnorm)[m.tid] : 0.0f;
-  // inputs: q | k | v of this head, z, alpha, beta (projection words)
-  constexpr int qw = KD / 2, vw = VD / 2;
-  constexpr int zbase = S::QKV, abase = S::QKV + S::VS, bbase = abase + S::VH;
-  constexpr int nwords = 2 * qw + 2 * vw + 2;
-  auto index = [&](int i) -> int {
-    if (i < qw) return ((kh * KD) >> 1) + i;
-    if (i < 2 * qw) return ((S::KS + kh * KD) >> 1) + (i - qw);
-    if (i < 2 * qw + vw) return ((2 * S::KS + h * VD) >> 1) + (i - 2 * qw);
-    if (i < 2 * qw + 2 * vw) return ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
-    if (i == 2 * qw + 2 * vw) return (abase + h) >> 1;
-    return (bbase + h) >> 1;
-  };
-  poll_words<(nwords + kMT - 1) / kMT>(m, Ly.x_proj, nwords, index, m.vec);
-  const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
+  // alpha (wave 0) and beta (wave 1) rows of head h
+  u32x4 abw[S::NQA];
+  if (m.wave < 2) {
+    const uint16_t* w = (m.wave == 0 ? Ly.alpha_w : Ly.beta_w) + (size_t)h * S::H;
 #pragma unroll
-  for (int j = 0; j < SPT; ++j)
-    if (m.tid + kMT * j < SQUADS) reinterpret_cast<u32x4*>(state)[m.tid + kMT * j] = sv[j];
+    for (int j = 0; j < S::NQA; ++j) abw[j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
+  }
+  // inputs: q | k | v of this head, z (projection words)
+  constexpr int qw = KD / 2, vw = VD / 2;
+  constexpr int zbase = S::QKV;
+  constexpr int nwords = 2 * qw + 2 * vw;
+  const uint64_t* proj = Ly.x_proj;
+  auto addr = [&](int i) -> const uint64_t* {
+    if (i < qw) return proj + ((kh * KD) >> 1) + i;
+    if (i < 2 * qw) return proj + ((S::KS + kh * KD) >> 1) + (i - qw);
+    if (i < 2 * qw + vw) return proj + ((2 * S::KS + h * VD) >> 1) + (i - 2 * qw);
+    return proj + ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
+  };
+  poll_words<(nwords + kMT - 1) / kMT>(m, nwords, addr, m.vec);
+  if (m.wave < 2) {
+    Quad acc;
+    quad_zero(acc);
+#pragma unroll
+    for (int j = 0; j < S::NQA; ++j)
+      if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], abw[j]);
+    const float v = quad_tree<64>(acc);
+    if (m.lane == 0) d->ab[m.wave] = f2bf(v);
+  }
+  const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
   // convolution (linear_prepare.hex:2-64)
   if (conv_thread) {
     const uint16_t current = in16[m.tid];
@@ -558,8 +614,8 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     const float total = serial_sum<KD>(d->sq + (m.tid == 0 ? 0 : KD));
     d->gates[2 + (m.tid == 0 ? 0 : 1)] = nsqrt(total + bitsf(0x358637bdu));
   } else if (m.tid == 128) {
-    const uint16_t alpha = in16[2 * (2 * qw + 2 * vw) + ((abase + h) & 1)];
-    const uint16_t beta = in16[2 * (2 * qw + 2 * vw + 1) + ((bbase + h) & 1)];
+    const uint16_t alpha = d->ab[0];
+    const uint16_t beta = d->ab[1];
     const float time_step = softplus(bf2f(alpha) + dt);
     d->gates[0] = hexp(rbf(time_step * aa));
     d->gates[1] = rbf(sigmoid(bf2f(beta)));
@@ -576,9 +632,8 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   // D32 reference lanes 4q..4q+3, i.e. key elements 4q + i + 32j (i, j < 4):
   // per i a serial chain over j from 0.0, then the 32-lane halving tree
   // (strides 16, 8, 4 across lanes, 2 and 1 in-lane; tree_levels order).
+  // The state stays in registers and is written back from them.
   const float decay = d->gates[0], rate = d->gates[1];
-  constexpr int KJ = KD / 32, CPP = kMT / 8;  // key chunks; channels per pass
-  const int q = m.lane & 7, sub = m.tid >> 3;
   float kv[KJ][4], qv[KJ][4];
 #pragma unroll
   for (int j = 0; j < KJ; ++j)
@@ -587,19 +642,17 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
       kv[j][i] = bf2f(d->khat[4 * q + i + 32 * j]);
       qv[j][i] = bf2f(d->qhat[4 * q + i + 32 * j]);
     }
-#pragma unroll 1
-  for (int c0 = 0; c0 < VD; c0 += CPP) {
-    const int c = c0 + sub;
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int c = ps * CPP + sub;
     const bool valid = c < VD;
     const int cc = valid ? c : 0;
-    uint16_t* row = state + cc * KD + 4 * q;
     float old[KJ][4];
     float v[4];
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
-      const uint2 raw = *reinterpret_cast<const uint2*>(row + 32 * j);
-      old[j][0] = lo2f(raw.x); old[j][1] = hi2f(raw.x);
-      old[j][2] = lo2f(raw.y); old[j][3] = hi2f(raw.y);
+      old[j][0] = lo2f(sv[ps][j].x); old[j][1] = hi2f(sv[ps][j].x);
+      old[j][2] = lo2f(sv[ps][j].y); old[j][3] = hi2f(sv[ps][j].y);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -624,19 +677,14 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
         w[i] += nx[i] * qv[j][i];
       }
       if (valid)
-        *reinterpret_cast<uint2*>(row + 32 * j) =
-            uint2{pack_bf(f2bf(nx[0]), f2bf(nx[1])), pack_bf(f2bf(nx[2]), f2bf(nx[3]))};
+        *G(reinterpret_cast<u32x2*>(st_g + (size_t)c * KD + 4 * q + 32 * j)) =
+            u32x2{pack_bf(f2bf(nx[0]), f2bf(nx[1])), pack_bf(f2bf(nx[2]), f2bf(nx[3]))};
     }
     tree_levels<8>(w[0], w[1], w[2], w[3]);
     const float out = (w[0] + w[2]) + (w[1] + w[3]);
     if (q == 0 && valid) d->core[c] = f2bf(out * a.delta_scale);
   }
   __syncthreads();
-  // state write-back (this block's head only; read again next step)
-#pragma unroll
-  for (int j = 0; j < SPT; ++j)
-    if (m.tid + kMT * j < SQUADS)
-      G(reinterpret_cast<u32x4*>(st_g))[m.tid + kMT * j] = reinterpret_cast<const u32x4*>(state)[m.tid + kMT * j];
   // gated RMSNorm with a serial sum (cooperative_norm.hex:139-182)
   if (m.tid < VD) {
     const float v = bf2f(d->core[m.tid]);
@@ -659,32 +707,33 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
 // -------------------------------- phase: output projection + residual (S64)
 
 // bf16(bf16(tree64(x . w_r)) (+) residual_r) (qwen3.fused.residual,
-// simt.hex:442-538) over the polled mixer output (COLS BF16), one reference
-// lane per physical lane, two rows per wave. Blocks kh < KH of a linear layer
-// also write the q and k conv history of key head kh.
+// simt.hex:442-538) over the polled mixer output (COLS BF16): 16 lanes per
+// row (lane q holds reference lanes 4q..4q+3, one 16-byte load per chunk of
+// 64 pairs), four rows per wave, waves 0 and 1 of every block. Blocks kh < KH
+// of a linear layer also write the q and k conv history of key head kh.
 template <class S, int COLS>
 __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  constexpr int NP = COLS / 2, NJ = (NP + 63) / 64;
-  const int prow = m.gw;  // row pair
-  const bool has_rows = prow < S::H / 2;
-  uint32_t wv[2][NJ];
+  constexpr int NP = COLS / 2, QP = NP / 4, NJ = QP / 16;
+  static_assert(QP % 16 == 0, "output projection width");
+  const int q = m.lane & 15, g = m.lane >> 4;
+  const int rq = m.bid + m.grid * m.wave;  // row quad of this wave
+  const bool has_rows = m.wave < 2 && rq < S::H / 4;
+  u32x4 wv[NJ];
   if (has_rows) {
+    const uint16_t* w = Ly.out_w + (size_t)(4 * rq) * COLS;
+    const uint32_t off = (uint32_t)g * (uint32_t)COLS * 2u + (uint32_t)q * 16u;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const uint16_t* w = Ly.out_w + (size_t)(2 * prow + r) * COLS;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) wv[r][j] = ldd_at(w, (uint32_t)min(m.lane + 64 * j, NP - 1) * 4u);
-    }
+    for (int j = 0; j < NJ; ++j) wv[j] = ldq_at(w, off + (uint32_t)j * 256u);
   }
-  poll_words<(NP + kMT - 1) / kMT>(m, Ly.x_mix, NP, Identity{}, m.vec);
-  if (!Ly.full && (int)blockIdx.x < S::KH) {
-    // q and k history of key head kh = blockIdx.x (its raw values are still in
-    // this block's LDS from the previous phase).
+  poll_words<(NP + kMT - 1) / kMT>(m, NP, Span{Ly.x_mix}, m.vec);
+  if (!Ly.full && m.bid < S::KH) {
+    // q and k history of key head kh = the block index (its raw values are
+    // still in this block's LDS from the previous phase).
     const DeltaLds* d = reinterpret_cast<const DeltaLds*>(m.big);
-    const int kh = blockIdx.x;
+    const int kh = m.bid;
     const int64_t slot = ((int64_t)G(a.params)[0] % 3) * S::QKV;
     if (m.tid < 2 * S::KD) {
       const int ch = m.tid < S::KD ? kh * S::KD + m.tid : S::KS + kh * S::KD + (m.tid - S::KD);
@@ -692,20 +741,16 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
     }
   }
   if (has_rows) {
-    float v[2];
+    const u32x4* xq = reinterpret_cast<const u32x4*>(m.vec);
+    Quad acc;
+    quad_zero(acc);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-        if (NP % 64 == 0 || m.lane + 64 * j < NP) pair_acc(lo, hi, m.vec[m.lane + 64 * j], wv[r][j]);
-      v[r] = tree64_lanes(lo + hi);
-    }
-    if (m.lane == 0) {
-      const uint16_t o0 = bf_add(f2bf(v[0]), m.xr[2 * prow]);
-      const uint16_t o1 = bf_add(f2bf(v[1]), m.xr[2 * prow + 1]);
-      word_store(Ly.x_attn + prow, pack_bf(o0, o1), m.tag);
-    }
+    for (int j = 0; j < NJ; ++j) quad_acc(acc, xq[q + 16 * j], wv[j]);
+    const float v = quad_tree<16>(acc);
+    const int row = 4 * rq + g;
+    const uint16_t o = bf_add(f2bf(v), m.xr[row]);
+    const uint16_t other = (uint16_t)__shfl_down((int)o, 16, 64);
+    if (m.lane == 0 || m.lane == 32) word_store(Ly.x_attn + 2 * rq + (m.lane >> 5), pack_bf(o, other), m.tag);
   }
   __syncthreads();
 }
@@ -716,24 +761,42 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
 // for the router and the gate/up phase and keeps the raw row for the FFN
 // residual. Waves gw <= E compute router row gw (moe.hex:4-84): physical lane
 // 2r + h runs reference lane r's low (h = 0) or high (h = 1) accumulator over
-// floats 64k + lane.
+// floats 64k + lane. Waves E+1 .. E+SI/2 compute the shared expert's gate/up
+// row pairs (dual S256, moe.hex:254-333) up to the routing-dependent factor:
+// t = bf16(bf16(silu(bf16 g)) * bf16 u); the down phase applies
+// bf16(t * sigmoid(shared logit)), the same roundings as the reference.
 template <class S>
 __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  constexpr int H = S::H, ROWS = S::E + 1, NJ = (H + 63) / 64;
+  constexpr int H = S::H, QH = S::QH, NQ = S::NQA, ROWS = S::E + 1, NJ = (H + 63) / 64;
   float wv[NJ];
-  const bool has_row = m.gw < ROWS;
-  if (has_row) {
+  u32x4 gv[2][NQ], uv[2][NQ];
+  const bool router_wave = m.gw < ROWS;
+  const int sp = m.gw - ROWS;  // shared pair of this wave
+  const bool shared_wave = sp >= 0 && sp < S::SI / 2;
+  if (router_wave) {
     const float* w = m.gw < S::E ? Ly.router + (size_t)m.gw * H : Ly.shared_gate;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) wv[j] = ldf_at(w, (uint32_t)min(64 * j + m.lane, H - 1) * 4u);
+  } else if (shared_wave) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint16_t* g = Ly.sgate + (size_t)(2 * sp + r) * H;
+      const uint16_t* u = Ly.sup + (size_t)(2 * sp + r) * H;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
+        gv[r][j] = ldq_at(g, off);
+        uv[r][j] = ldq_at(u, off);
+      }
+    }
   }
   f32x4 w0, w1;
   norm_weights<S>(m, Ly.post_norm, w0, w1);
-  poll_words<(H / 2 + kMT - 1) / kMT>(m, Ly.x_attn, H / 2, Identity{}, reinterpret_cast<uint32_t*>(m.xa));
+  poll_words<(H / 2 + kMT - 1) / kMT>(m, H / 2, Span{Ly.x_attn}, reinterpret_cast<uint32_t*>(m.xa));
   norm_row<S>(m, m.xa, w0, w1, m.a.eps);
-  if (has_row) {
+  if (router_wave) {
     const uint16_t* xe = reinterpret_cast<const uint16_t*>(m.xn);
     float acc = 0.0f;
 #pragma unroll
@@ -746,131 +809,218 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
     v += lane_down<4>(v);
     v += lane_down<2>(v);
     if (m.lane == 0) word_store(Ly.x_router + m.gw, fbits(v), m.tag);
+  } else if (shared_wave) {
+    uint16_t t[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      Quad ga, ua;
+      quad_zero(ga);
+      quad_zero(ua);
+#pragma unroll
+      for (int j = 0; j < NQ; ++j)
+        if (QH % 64 == 0 || m.lane + 64 * j < QH) {
+          const u32x4 xq = m.xn[m.lane + 64 * j];
+          quad_acc(ga, xq, gv[r][j]);
+          quad_acc(ua, xq, uv[r][j]);
+        }
+      const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
+      t[r] = f2bf(rbf(silu(gb)) * ub);
+    }
+    if (m.lane == 0) word_store(Ly.x_shared + sp, pack_bf(t[0], t[1]), m.tag);
   }
 }
 
 // ----------------------------------------- phase: top-k select + gate / up
 
-// Every block ranks the experts itself with the reference's formula
-// (moe.hex:86-252), one thread per expert:
-// rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}, ids[rank] = e for
-// rank < K; then p_j = exp(l_j - l_0) / den with den summed left to right.
-// Two threads per expert (adjacent lanes) each count over half of the others.
+// Every block ranks the experts itself (moe.hex:86-252). The reference's
+// rank is rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}, ids[rank] = e
+// for rank < K. Without NaNs this is the descending order with ties to the
+// lower index, so wave 0 takes K rounds of a wave-wide maximum of
+// (ordered value, lowest index) keys; with a NaN the formula is evaluated
+// directly. Then p_j = exp(l_j - l_0) / den with den summed left to right.
+__device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+// Value of lane i + S for a 64-bit key (the halving-tree shifts of lane_down).
+template <int S>
+__device__ __forceinline__ unsigned long long key_down(unsigned long long v) {
+  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  const uint32_t l2 = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, lo)));
+  const uint32_t h2 = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, hi)));
+  return ((unsigned long long)h2 << 32) | l2;
+}
+
 template <class S>
 __device__ __forceinline__ void select_experts(const Mega& m) {
   MegaMisc* s = m.misc;
-  constexpr int HALF = (S::E + 1) / 2;
-  static_assert(S::E % 8 == 0, "expert count");
-  for (int e0 = 0; e0 < S::E; e0 += kMT / 2) {
-    const int e = e0 + (m.tid >> 1), part = m.tid & 1;
-    const float le = e < S::E ? s->logits[e] : 0.0f;
-    int rank = 0;
-    const float* lg = s->logits + part * HALF;
-#pragma unroll 8
-    for (int i = 0; i < HALF; ++i) {
-      const int ii = part * HALF + i;
-      const float o = lg[i];
-      rank += (ii < S::E && (o > le || (ii < e && !(le > o)))) ? 1 : 0;
+  static_assert(S::E <= 64 * 64, "expert count");
+  constexpr int PER = (S::E + 63) / 64;  // candidates per lane
+  if (m.wave == 0) {
+    // keys of this lane's experts e = lane + 64c; NaN -> fallback
+    unsigned long long key[PER];
+    bool nan = false;
+#pragma unroll
+    for (int c = 0; c < PER; ++c) {
+      const int e = m.lane + 64 * c;
+      key[c] = 0ull;
+      if (e < S::E) {
+        const float le = s->logits[e];
+        nan |= le != le;
+        const uint32_t u = le == 0.0f ? 0u : fbits(le);
+        const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        key[c] = ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
+      }
     }
-    rank += __shfl_xor(rank, 1, 64);
-    if (e < S::E && part == 0 && rank < S::K) {
-      s->ids[rank] = e;
-      s->chosen[rank] = le;
+    const bool any_nan = __any(nan);
+    if (!any_nan) {
+      for (int k = 0; k < S::K; ++k) {
+        unsigned long long best = key[0];
+#pragma unroll
+        for (int c = 1; c < PER; ++c) best = key_max(best, key[c]);
+        best = key_max(best, key_down<32>(best));
+        best = key_max(best, key_down<16>(best));
+        best = key_max(best, key_down<8>(best));
+        best = key_max(best, key_down<4>(best));
+        best = key_max(best, key_down<2>(best));
+        best = key_max(best, key_down<1>(best));
+        const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)best);
+        const uint32_t bhi = __builtin_amdgcn_readfirstlane((uint32_t)(best >> 32));
+        const unsigned long long win = ((unsigned long long)bhi << 32) | blo;
+        const int e = (int)(0xffffffffu - blo);
+#pragma unroll
+        for (int c = 0; c < PER; ++c)
+          if (key[c] == win) key[c] = 0ull;  // taken
+        if (m.lane == 0) {
+          s->ids[k] = e;
+          s->chosen[k] = s->logits[e];
+        }
+      }
     }
+    if (m.lane == 0) s->any_nan = any_nan ? 1 : 0;
   }
   __syncthreads();
+  if (s->any_nan) {
+    for (int e = m.tid; e < S::E; e += kMT) {
+      const float le = s->logits[e];
+      int rank = 0;
+      for (int i = 0; i < S::E; ++i) {
+        const float o = s->logits[i];
+        rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+      }
+      if (rank < S::K) {
+        s->ids[rank] = e;
+        s->chosen[rank] = le;
+      }
+    }
+    __syncthreads();
+  }
   if (m.wave == 0) {
     const float ex = m.lane < S::K ? hexp(s->chosen[m.lane] - s->chosen[0]) : 0.0f;
     float den = 0.0f;
     for (int j = 0; j < S::K; ++j) den = den + __shfl(ex, j, 64);
     if (m.lane < S::K) s->probs[m.lane] = ex / den;
-    if (m.lane == 0) s->scalars[0] = sigmoid(s->logits[S::E]);
   }
   __syncthreads();
 }
 
-// Dual S256 gate/up rows over the selected and shared experts
-// (moe.hex:254-333): routed bf16(silu(g) * u * p_slot), shared
-// bf16(bf16(bf16(silu(g)) * u) * sigmoid(shared logit)).
+// Down-projection weights, staged in LDS by DMA (global_load_lds, 16 bytes
+// per lane) as soon as the experts are known, so no registers hold them and
+// one instruction moves 1 KB. Waves 0-3 of every block own one row pair
+// each, prow = block + grid * wave; per wave the staging is
+//   [row A routed RP][32][row B routed RP][row A shared SP][32][row B shared SP]
+// dwords (the pads keep the two rows on different LDS banks).
+template <class S>
+struct DownLayout {
+  static constexpr int RP = S::K * S::I / 2, SP = S::SI / 2, IP = S::I / 2;
+  static constexpr int A_R = 0, B_R = RP + 32, A_S = 2 * RP + 32, B_S = 2 * RP + SP + 64;
+  static constexpr int DWORDS = 2 * RP + 2 * SP + 64;
+  static constexpr int WAVES = 4;
+  static constexpr int BYTES = WAVES * DWORDS * 4;
+};
+
+template <class S>
+__device__ __forceinline__ CQ35_LDS uint32_t* down_stage(const Mega& m, int fw) {
+  return (CQ35_LDS uint32_t*)(m.big + (size_t)fw * DownLayout<S>::DWORDS * 4);
+}
+
+// DMA one BF16 row of `elems` (a multiple of 8) into LDS at dst.
+__device__ __forceinline__ void dma_row(const Mega& m, const uint16_t* src, CQ35_LDS uint32_t* dst, int elems) {
+  const int pieces = elems / 8;  // 16-byte pieces
+  for (int c = 0; c * 64 < pieces; ++c)
+    if (m.lane + 64 * c < pieces)
+      __builtin_amdgcn_global_load_lds(
+          (const CQ35_GLOBAL void*)(src + (size_t)(m.lane + 64 * c) * 8), (CQ35_LDS void*)(dst + 256 * c), 16, 0, 0);
+}
+
+template <class S>
+__device__ __forceinline__ void issue_down(const Mega& m, const CQ35_CONST MegaLayer& Ly) {
+  using D = DownLayout<S>;
+  const int fw = m.wave;
+  const int prow = m.bid + m.grid * fw;
+  if (fw >= D::WAVES || prow >= S::H / 2) return;
+  CQ35_LDS uint32_t* st = down_stage<S>(m, fw);
+#pragma unroll 1
+  for (int slot = 0; slot < S::K; ++slot) {
+    const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
+    const uint16_t* w = Ly.down_exps + ((size_t)id * S::H + 2 * prow) * S::I;
+    dma_row(m, w, st + D::A_R + slot * D::IP, S::I);
+    dma_row(m, w + S::I, st + D::B_R + slot * D::IP, S::I);
+  }
+  const uint16_t* sw = Ly.sdown + (size_t)(2 * prow) * S::SI;
+  dma_row(m, sw, st + D::A_S, S::SI);
+  dma_row(m, sw + S::SI, st + D::B_S, S::SI);
+}
+
+// Dual S256 gate/up rows of the selected experts (moe.hex:254-333):
+// bf16(silu(g) * u * p_slot), one row pair per wave.
 template <class S>
 __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   constexpr int H = S::H, QH = S::QH, NQ = S::NQA;
-  constexpr int ROUTED = S::K * S::I, PAIRS = (ROUTED + S::SI) / 2;
-  u32x4 gv[kPairsG][2][NQ], uv[kPairsG][2][NQ];
-  // the shared expert's rows do not depend on the routing: load them first
-#pragma unroll
-  for (int k = 0; k < kPairsG; ++k) {
-    const int p = m.gw + m.nw * k;
-    if (p < PAIRS && 2 * p >= ROUTED) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const uint16_t* g = Ly.sgate + (size_t)(2 * p + r - ROUTED) * H;
-        const uint16_t* u = Ly.sup + (size_t)(2 * p + r - ROUTED) * H;
-#pragma unroll
-        for (int j = 0; j < NQ; ++j) {
-          const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
-          gv[k][r][j] = ldq_at(g, off);
-          uv[k][r][j] = ldq_at(u, off);
-        }
-      }
-    }
-  }
-  poll_words<(S::E + 1 + kMT - 1) / kMT>(m, Ly.x_router, S::E + 1, Identity{},
+  constexpr int PAIRS = S::K * S::I / 2;
+  u32x4 gv[2][NQ], uv[2][NQ];
+  poll_words<(S::E + 1 + kMT - 1) / kMT>(m, S::E + 1, Span{Ly.x_router},
                                           reinterpret_cast<uint32_t*>(m.misc->logits));
   select_experts<S>(m);
+  const int p = m.gw;
+  const bool has_pair = p < PAIRS;
+  if (has_pair) {
+    // both rows of a pair lie in one expert slot (I is even)
+    const int slot = (2 * p) / S::I;
+    const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
 #pragma unroll
-  for (int k = 0; k < kPairsG; ++k) {
-    const int p = m.gw + m.nw * k;
-    if (p < PAIRS && 2 * p < ROUTED) {
-      // both rows of a pair lie in one expert slot (I is even)
-      const int slot = (2 * p) / S::I;
-      const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
+    for (int r = 0; r < 2; ++r) {
+      const size_t e = (size_t)id * S::I + (2 * p + r - slot * S::I);
+      const uint16_t* g = Ly.gate_exps + e * H;
+      const uint16_t* u = Ly.up_exps + e * H;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const size_t e = (size_t)id * S::I + (2 * p + r - slot * S::I);
-        const uint16_t* g = Ly.gate_exps + e * H;
-        const uint16_t* u = Ly.up_exps + e * H;
-#pragma unroll
-        for (int j = 0; j < NQ; ++j) {
-          const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
-          gv[k][r][j] = ldq_at(g, off);
-          uv[k][r][j] = ldq_at(u, off);
-        }
+      for (int j = 0; j < NQ; ++j) {
+        const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
+        gv[r][j] = ldq_at(g, off);
+        uv[r][j] = ldq_at(u, off);
       }
     }
   }
-  const float shared_p = m.misc->scalars[0];
+  issue_down<S>(m, Ly);
+  if (has_pair) {
+    uint16_t y[2];
 #pragma unroll
-  for (int k = 0; k < kPairsG; ++k) {
-    const int p = m.gw + m.nw * k;
-    if (p < PAIRS) {
-      uint16_t y[2];
+    for (int r = 0; r < 2; ++r) {
+      Quad ga, ua;
+      quad_zero(ga);
+      quad_zero(ua);
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        Quad ga, ua;
-        quad_zero(ga);
-        quad_zero(ua);
-#pragma unroll
-        for (int j = 0; j < NQ; ++j)
-          if (QH % 64 == 0 || m.lane + 64 * j < QH) {
-            const u32x4 xq = m.xn[m.lane + 64 * j];
-            quad_acc(ga, xq, gv[k][r][j]);
-            quad_acc(ua, xq, uv[k][r][j]);
-          }
-        const float gsum = quad_tree<64>(ga);
-        const float usum = quad_tree<64>(ua);
-        const int row = 2 * p + r;
-        const float gb = rbf(gsum), ub = rbf(usum);
-        const float activated = silu(gb);
-        float out;
-        if (row < ROUTED) out = (activated * ub) * m.misc->probs[row / S::I];
-        else out = rbf(rbf(activated) * ub) * shared_p;
-        y[r] = f2bf(out);
-      }
-      if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
+      for (int j = 0; j < NQ; ++j)
+        if (QH % 64 == 0 || m.lane + 64 * j < QH) {
+          const u32x4 xq = m.xn[m.lane + 64 * j];
+          quad_acc(ga, xq, gv[r][j]);
+          quad_acc(ua, xq, uv[r][j]);
+        }
+      const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
+      y[r] = f2bf((silu(gb) * ub) * m.misc->probs[(2 * p + r) / S::I]);
     }
+    if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
   }
 }
 
@@ -879,42 +1029,59 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
 // Per hidden row (moe.hex:371-434, simt_moe.hex:36-287): S32 over the
 // concatenated routed activations (pair p reads expert ids[p / (I/2)]) and a
 // separate S32 over the shared activations, one reference lane per physical
-// lane (lanes 0-31 row 2w, lanes 32-63 row 2w+1);
-// out = bf16(bf16(routed + residual) (+) bf16(shared)).
+// lane (lanes 0-31 row A, lanes 32-63 row B) reading the staged weights;
+// out = bf16(bf16(routed + residual) (+) bf16(shared)). The shared
+// activations are completed here: bf16(t * sigmoid(shared logit)). Once its
+// inputs are in, the block issues the next layer's first projection weights.
 template <class S>
-__device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
+__device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly,
+                                           const MegaLayer* next, ProjRegs<S>& pr) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  constexpr int H = S::H, IP = S::I / 2, RP = S::K * IP, SP = S::SI / 2;
-  constexpr int NJ = RP / 32, NSJ = SP / 32, JPS = IP / 32;  // dwords per lane; per expert slot
-  const int half = m.lane >> 5, r32 = m.lane & 31;
-  const int prow = m.gw;
-  const bool has_rows = prow < H / 2;
-  uint32_t wr[NJ], ws[NSJ];
-  if (has_rows) {
-    // pair r32 + 32j lies in expert slot j / JPS: the row base is uniform per
-    // slot, the lane offset selects the row (half) and the pair
-    const uint32_t base = (uint32_t)(half * IP + r32) * 4u;
+  using D = DownLayout<S>;
+  constexpr int H = S::H, RP = D::RP, SP = D::SP;
+  constexpr int NJ = RP / 32, NSJ = SP / 32;
+  const uint64_t* act = Ly.x_active;
+  const uint64_t* shr = Ly.x_shared;
+  const uint64_t* lge = Ly.x_router + S::E;
+  poll_words<(RP + SP + 1 + kMT - 1) / kMT>(
+      m, RP + SP + 1, [&](int i) { return i < RP ? act + i : i < RP + SP ? shr + (i - RP) : lge; }, m.vec);
+  // the staged weights were issued before the poll: complete in issue order
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // the next layer's first projection pairs: issued after the poll (a wave's
+  // loads complete in issue order), so they stream during this phase's
+  // compute and the next exchange without delaying the inputs above
+  if (next) {
+    issue_project<S, 0, kPairsEarly>(pa, next, pr);
+  } else {
+    // defined on every path, so the registers are not carried across phases
 #pragma unroll
-    for (int slot = 0; slot < S::K; ++slot) {
-      const int id = __builtin_amdgcn_readfirstlane(m.misc->ids[slot]);
-      const uint16_t* w = Ly.down_exps + ((size_t)id * H + 2 * prow) * S::I;
+    for (int k = 0; k < kPairsEarly; ++k)
 #pragma unroll
-      for (int jj = 0; jj < JPS; ++jj) wr[slot * JPS + jj] = ldd_at(w, base + jj * 128u);
-    }
-    const uint16_t* sw = Ly.sdown + (size_t)(2 * prow) * S::SI;
+      for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
-    for (int j = 0; j < NSJ; ++j) ws[j] = ldd_at(sw, (uint32_t)(half * SP + r32 + 32 * j) * 4u);
+        for (int j = 0; j < S::NQA; ++j) pr.w[k][rr][j] = u32x4{0u, 0u, 0u, 0u};
   }
-  poll_words<(RP + SP + kMT - 1) / kMT>(m, Ly.x_active, RP + SP, Identity{}, m.vec);
-  if (has_rows) {
+  if (m.tid < SP) {
+    const float gate = sigmoid(bitsf(m.vec[RP + SP]));
+    const uint32_t t = m.vec[RP + m.tid];
+    m.vec[RP + m.tid] = pack_bf(f2bf(lo2f(t) * gate), f2bf(hi2f(t) * gate));
+  }
+  __syncthreads();
+  const int half = m.lane >> 5, r32 = m.lane & 31;
+  const int fw = m.wave;
+  const int prow = m.bid + m.grid * fw;
+  if (fw < D::WAVES && prow < H / 2) {
+    const CQ35_LDS uint32_t* st = down_stage<S>(m, fw);
+    const CQ35_LDS uint32_t* wr = st + (half ? D::B_R : D::A_R) + r32;
+    const CQ35_LDS uint32_t* ws = st + (half ? D::B_S : D::A_S) + r32;
     float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[r32 + 32 * j], wr[j]);
+    for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[r32 + 32 * j], wr[32 * j]);
     const float routed_v = tree32_lanes(lo + hi);
     float slo = 0.0f, shi = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NSJ; ++j) pair_acc(slo, shi, m.vec[RP + r32 + 32 * j], ws[j]);
+    for (int j = 0; j < NSJ; ++j) pair_acc(slo, shi, m.vec[RP + r32 + 32 * j], ws[32 * j]);
     const float shared_v = tree32_lanes(slo + shi);
     const int row = 2 * prow + half;
     const uint16_t out = bf_add(f2bf(routed_v + bf2f(m.xa[row])), f2bf(shared_v));
@@ -939,6 +1106,8 @@ struct ScoreLds {
   float normed[kMW][256];
   uint16_t qhat[16 * 256];
   uint16_t khat[2 * 256];
+  int heads[32];  // heads this block normalises: query heads, then Q + key head
+  int nheads;
 };
 static_assert(sizeof(ScoreLds) <= kLdsBigBytes, "score LDS");
 
@@ -954,6 +1123,10 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   const int64_t items = keys * KVH;
   ScoreLds* s = reinterpret_cast<ScoreLds*>(m.big);
   const int l32 = m.lane & 31, half = m.lane >> 5;
+  // the block's items are 16 consecutive ones per round; without any it has
+  // nothing to do in this phase
+  const int64_t first = (int64_t)m.bid * 2 * kMW;
+  if (first >= items) return;  // uniform per block
   // prefetch the cached keys of this wave's first items
   const int64_t item0 = (int64_t)m.gw * 2 + half;
   float kv0[KJ];
@@ -985,10 +1158,27 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
     }
     return S::QS + (i - QWORDS);  // k words then v words
   };
-  poll_words<(QWORDS + 2 * KVWORDS + kMT - 1) / kMT>(m, Ly.x_proj, QWORDS + 2 * KVWORDS, index, m.vec);
+  const uint64_t* proj = Ly.x_proj;
+  poll_words<(QWORDS + 2 * KVWORDS + kMT - 1) / kMT>(m, QWORDS + 2 * KVWORDS,
+                                                     [&](int i) { return proj + index(i); }, m.vec);
   const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
   const uint16_t* kraw = in16 + Q * HD;
   const uint16_t* vraw = kraw + S::KVS;
+  // KV groups touched by the block's items -> heads to normalise
+  if (m.tid == 0) {
+    unsigned mask = 0;
+    for (int64_t i0 = first; i0 < items; i0 += 2 * (int64_t)m.nw) {
+      const int64_t i1 = min<int64_t>(i0 + 2 * kMW, items) - 1;
+      for (int g = (int)(i0 / keys); g <= (int)(i1 / keys); ++g) mask |= 1u << g;
+    }
+    int n = 0;
+    for (int g = 0; g < KVH; ++g)
+      if (mask & (1u << g)) {
+        for (int hq = 0; hq < HPK; ++hq) s->heads[n++] = g * HPK + hq;
+        s->heads[n++] = Q + g;
+      }
+    s->nheads = n;
+  }
   // RoPE table for this position (rope.hex:5-17)
   if (m.tid < RH) {
     float sn, cs;
@@ -997,10 +1187,12 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
     s->rope[RH + m.tid] = sn;
   }
   __syncthreads();
-  // one wave per head: Q query heads then KVH key heads
+  // one wave per head of the list
+  const int nheads = s->nheads;
 #pragma unroll 1
-  for (int h0 = 0; h0 < Q + KVH; h0 += kMW) {
-    const int hh = h0 + m.wave;
+  for (int h0 = 0; h0 < nheads; h0 += kMW) {
+    const bool live = h0 + m.wave < nheads;
+    const int hh = live ? s->heads[h0 + m.wave] : Q + KVH;
     const bool is_q = hh < Q;
     float x[VPL], w[VPL];
     float t = 0.0f;
@@ -1107,10 +1299,12 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
 // out = bf16(bf16(acc / den) * sigmoid(gate)). Invalid keys of the last tile
 // contribute p = 0 against key 0's value, as in the reference.
 constexpr int kMegaValueChunk = 256;  // keys per chunk
+constexpr int kValuePre = 4;          // chunks whose V rows and scores are fetched up front
 struct ValueLds {
   float p[kMegaValueChunk];
   float alpha[kMegaValueChunk / 8];
   float prod[kMegaValueChunk * kValueChannels];
+  float sc[kValuePre * kMegaValueChunk];  // scores of the first chunks
   float mx[1];  // tile maxima, then running maxima (the rest of the big area)
 };
 constexpr int kValueMxMax = (kLdsBigBytes - (int)offsetof(ValueLds, mx)) / 4;
@@ -1130,7 +1324,7 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   // thread i < 2n stages key i >> 1, channels 8 (i & 1) .. 8 (i & 1) + 7 of a chunk
   const int vk = m.tid >> 1, vh = m.tid & 1;
 #pragma unroll 1
-  for (int item = blockIdx.x; item < ITEMS; item += gridDim.x) {
+  for (int item = m.bid; item < ITEMS; item += m.grid) {
     const int head = item / CHUNKS, c0 = (item - head * CHUNKS) * kValueChannels;
     const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0;
     // V quad of key k (key 0 past the end; the new position device-coherently)
@@ -1144,12 +1338,16 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
                                             __HIP_MEMORY_SCOPE_AGENT);
       return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
     };
-    // prefetch the first chunk's V rows (positions before the new one)
-    const int n0 = (int)min<int64_t>(kMegaValueChunk, (int64_t)tiles * 8);
-    u32x4 vq = {0u, 0u, 0u, 0u};
-    if (vk < n0 && (int64_t)vk != position) {
-      const int64_t safe = vk < keys ? vk : 0;
-      vq = G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
+    // prefetch the first chunks' V rows (positions before the new one)
+    u32x4 vq[kValuePre];
+#pragma unroll
+    for (int c = 0; c < kValuePre; ++c) {
+      const int64_t k = vk + (int64_t)kMegaValueChunk * c;
+      vq[c] = u32x4{0u, 0u, 0u, 0u};
+      if (k < (int64_t)tiles * 8 && k != position) {
+        const int64_t safe = k < keys ? k : 0;
+        vq[c] = G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
+      }
     }
     // scores of this head: poll every tile, keep the tile maxima
     const uint64_t* sc = Ly.x_scores + (size_t)head * a.cap;
@@ -1176,7 +1374,7 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
         const int64_t k = (int64_t)t * 8 + j;
         const float sk = bitsf((uint32_t)v[j]);
         mt = fmaxf(mt, k < keys ? sk : ninf);
-        if (k < kMegaValueChunk) s->p[k] = sk;  // first chunk's scores, kept for the weights
+        if (k < kValuePre * kMegaValueChunk) s->sc[k] = sk;  // kept for the weights
       }
       s->mx[t] = mt;
     }
@@ -1206,19 +1404,20 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
     }
     __syncthreads();
     float acc = 0.0f, den = 0.0f;
-    for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kMegaValueChunk) {
+    int chunk = 0;
+    for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kMegaValueChunk, ++chunk) {
       const int n = (int)min<int64_t>(kMegaValueChunk, (int64_t)tiles * 8 - k0);  // multiple of 8
       if (m.tid < n) {
         const int64_t k = k0 + m.tid;
-        const float sk = k0 == 0 ? s->p[m.tid] : bitsf((uint32_t)word_load(sc + k));
+        const float sk = chunk < kValuePre ? s->sc[k] : bitsf((uint32_t)word_load(sc + k));
         s->p[m.tid] = k < keys ? hexp(sk - s->mx[k >> 3]) : 0.0f;
       }
       if (m.tid < n / 8) {
         const int tile = (int)(k0 / 8) + m.tid;
         s->alpha[m.tid] = hexp((tile > 0 ? s->mx[tile - 1] : ninf) - s->mx[tile]);
       }
-      u32x4 vcur = vq;
-      if (vk < n && (k0 > 0 || (int64_t)vk == position)) vcur = load_v(k0 + vk);
+      u32x4 vcur = chunk == 0 ? vq[0] : chunk == 1 ? vq[1 % kValuePre] : chunk == 2 ? vq[2 % kValuePre] : vq[3 % kValuePre];
+      if (vk < n && (chunk >= kValuePre || k0 + vk == position)) vcur = load_v(k0 + vk);
       __syncthreads();
       if (vk < n) {
         const float pk = s->p[vk];
@@ -1302,7 +1501,7 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
   if (steps > 0) load_piece(b0, 0);
   f32x4 w0, w1;
   norm_weights<S>(m, a.out_norm, w0, w1);
-  poll_words<(H / 2 + kMT - 1) / kMT>(m, a.x_final, H / 2, Identity{}, reinterpret_cast<uint32_t*>(m.xr));
+  poll_words<(H / 2 + kMT - 1) / kMT>(m, H / 2, Span{a.x_final}, reinterpret_cast<uint32_t*>(m.xr));
   norm_row<S>(m, m.xr, w0, w1, a.eps);
   unsigned long long mine = 0ull;
   Quad acc;
@@ -1348,12 +1547,21 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
 
 // ------------------------------------------------------------- the kernel
 
+// Dynamic LDS of the step for shape S: the big area must also hold the
+// down-projection staging.
+template <class S>
+constexpr int mega_lds_bytes() {
+  return kLdsBig + (DownLayout<S>::BYTES > kLdsBigBytes ? DownLayout<S>::BYTES : kLdsBigBytes);
+}
+
 template <class S>
 __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict__ pa) {
   const uint32_t tag = (uint32_t)G(pa->params)[2];
   MegaMisc* misc = reinterpret_cast<MegaMisc*>(mega_lds + kLdsMisc);
   if (threadIdx.x == 0) {
     misc->abort = 0;
+    misc->bid = blockIdx.x;
+    misc->grid = gridDim.x;
     if (blockIdx.x == 0) {
       // cleared before any output of this block exists, so before any block
       // can reach the head
@@ -1364,9 +1572,11 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
   __syncthreads();
   const int L = pa->L;
   const MegaLayer* layers = pa->layers;
+  ProjRegs<S> pr;
+  issue_project<S, 0, kPairsEarly>(pa, layers, pr);
   for (int l = 0; l < L; ++l) {
     const MegaLayer* ly = layers + l;
-    phase_project<S>(pa, tag, ly, l);
+    phase_project<S>(pa, tag, ly, l, pr);
     if (phase_ptr(ly)->full != 0) {
       phase_scores<S>(pa, tag, ly);
       phase_values<S>(pa, tag, ly);
@@ -1378,7 +1588,7 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
     }
     phase_router<S>(pa, tag, ly);
     phase_gate_up<S>(pa, tag, ly);
-    phase_down<S>(pa, tag, ly);
+    phase_down<S>(pa, tag, ly, l + 1 < L ? ly + 1 : nullptr, pr);
   }
   phase_head<S>(pa, tag);
 }

@@ -463,6 +463,7 @@ struct cq35_session {
   MegaArgs* d_margs = nullptr;
   int mega_grid = 0;
   const void* mega_kernel = nullptr;  // k_decode_step<shape> for this model
+  int mega_lds = 0;                   // its dynamic LDS bytes
   uint32_t seq = 0;
   // kernel timing
   int timed_class = -1;
@@ -513,9 +514,10 @@ bool shape_is(const cq35_config& c) {
 template <class S>
 bool grid_fits(int grid, int64_t cap) {
   const int64_t nw = (int64_t)grid * kMW;
-  const int64_t rows_lin = S::QKV + S::VS + 2LL * S::VH, rows_full = 2LL * S::QS + 2LL * S::KVS;
-  return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw &&
-         (S::K * S::I + S::SI) / 2 <= kPairsG * nw && S::H / 2 <= nw && S::E + 1 <= nw &&
+  const int64_t rows_lin = S::QKV + S::VS, rows_full = 2LL * S::QS + 2LL * S::KVS;
+  return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw && S::H / 4 <= 2LL * grid &&
+         S::H / 2 <= (int64_t)DownLayout<S>::WAVES * grid &&
+         S::K * S::I / 2 <= nw && S::E + 1 + S::SI / 2 <= nw && S::H / 2 <= nw &&
          (cap + 7) / 8 <= kValueMxMax;
 }
 
@@ -524,6 +526,15 @@ int mega_kind(const cq35_config& c, int grid, int64_t cap) {
   if (shape_is<ShapeMiniMoE>(c)) return grid_fits<ShapeMiniMoE>(grid, cap) ? kMegaMini : kMegaNone;
   if (shape_is<ShapeTinyMoE>(c)) return grid_fits<ShapeTinyMoE>(grid, cap) ? kMegaTiny : kMegaNone;
   return kMegaNone;
+}
+
+int mega_lds(int kind) {
+  switch (kind) {
+    case kMega35B: return mega_lds_bytes<Shape35BA3B>();
+    case kMegaMini: return mega_lds_bytes<ShapeMiniMoE>();
+    case kMegaTiny: return mega_lds_bytes<ShapeTinyMoE>();
+    default: return 0;
+  }
 }
 
 const void* mega_kernel(int kind) {
@@ -546,22 +557,23 @@ int setup_mega(cq35_session* s) {
   const int kind = mega_kind(c, grid, s->capacity);
   const void* kernel = mega_kernel(kind);
   if (!kernel) return CQ35_OK;
-  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMegaLds) != hipSuccess)
+  const int lds = mega_lds(kind);
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
     return CQ35_OK;
   int occupancy = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, kernel, kMT, kMegaLds) != hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occupancy, kernel, kMT, lds) != hipSuccess ||
       occupancy < 1)
     return CQ35_OK;
   auto region = [](int64_t words) { return (words + 15) / 16 * 16; };
   const int64_t hw = region(d.H / 2);
-  std::vector<int64_t> offs;  // per layer: h, proj, mix, attn, router, active, scores
+  std::vector<int64_t> offs;  // per layer: h, proj, mix, attn, router, active, scores, shared
   int64_t total = 0;
   for (int64_t l = 0; l < d.L; ++l) {
     const bool full = is_full(c, l);
-    const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS + 2LL * c.value_heads;
-    const int64_t sizes[7] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
-                              region(d.E + 1), region((d.K * d.I + d.SI) / 2),
-                              full ? region(d.Q * s->capacity) : 0};
+    const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS;
+    const int64_t sizes[8] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
+                              region(d.E + 1), region(d.K * d.I / 2),
+                              full ? region(d.Q * s->capacity) : 0, region(d.SI / 2)};
     for (int64_t z : sizes) {
       offs.push_back(total);
       total += z;
@@ -581,7 +593,7 @@ int setup_mega(cq35_session* s) {
     auto W = [&](int slot) { return m.w[base + slot]; };
     MegaLayer& Ly = layers[l];
     Ly = MegaLayer{};
-    const int64_t* o = &offs[7 * l];
+    const int64_t* o = &offs[8 * l];
     Ly.full = is_full(c, l) ? 1 : 0;
     Ly.in_norm = (const float*)W(0);
     Ly.x_h = s->words + o[0];
@@ -591,7 +603,8 @@ int setup_mega(cq35_session* s) {
     Ly.x_router = s->words + o[4];
     Ly.x_active = s->words + o[5];
     Ly.x_scores = s->words + o[6];
-    Ly.x_out = l + 1 < d.L ? s->words + offs[7 * (l + 1)] : s->words + final_off;
+    Ly.x_shared = s->words + o[7];
+    Ly.x_out = l + 1 < d.L ? s->words + offs[8 * (l + 1)] : s->words + final_off;
     int ffn;
     if (Ly.full) {
       Ly.seg_w[0] = (const uint16_t*)W(1); Ly.seg_rows[0] = (int)(2 * d.QS);
@@ -607,8 +620,8 @@ int setup_mega(cq35_session* s) {
     } else {
       Ly.seg_w[0] = (const uint16_t*)W(1); Ly.seg_rows[0] = (int)d.QKV;
       Ly.seg_w[1] = (const uint16_t*)W(2); Ly.seg_rows[1] = (int)d.VS;
-      Ly.seg_w[2] = (const uint16_t*)W(3); Ly.seg_rows[2] = c.value_heads;
-      Ly.seg_w[3] = (const uint16_t*)W(4); Ly.seg_rows[3] = c.value_heads;
+      Ly.alpha_w = (const uint16_t*)W(3);
+      Ly.beta_w = (const uint16_t*)W(4);
       Ly.dt = (const float*)W(5);
       Ly.a = (const float*)W(6);
       Ly.gnorm = (const float*)W(7);
@@ -662,6 +675,7 @@ int setup_mega(cq35_session* s) {
   HIP_TRY(hipMemcpy(s->d_margs, &a, sizeof(MegaArgs), hipMemcpyHostToDevice));
   s->mega_grid = grid;
   s->mega_kernel = kernel;
+  s->mega_lds = lds;
   s->mega_ok = true;
   s->mega_on = true;
   if (const char* g = getenv("CQ35_PERSISTENT")) s->mega_on = atoi(g) != 0;
@@ -1021,11 +1035,11 @@ int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* ne
   void* kargs[] = {(void*)&args};
   if (s->timed_class == KC_DECODE_STEP && s->ev_used < kMaxTimedEvents) {
     // events stamped by the dispatch packet, as for the per-kernel classes
-    e = hipExtLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)kMegaLds,
+    e = hipExtLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)s->mega_lds,
                            s->stream, s->ev[2 * s->ev_used], s->ev[2 * s->ev_used + 1], 0);
     ++s->ev_used;
   } else {
-    e = hipLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)kMegaLds,
+    e = hipLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)s->mega_lds,
                         s->stream);
   }
   if (e == hipSuccess) e = hipGetLastError();
