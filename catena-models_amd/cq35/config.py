@@ -62,6 +62,11 @@ PRESETS = {
                            q_heads=16, kv_heads=2, head_dim=256, rope_dim=64, experts=256,
                            top_k=8, shared_intermediate=512, key_heads=16, key_dim=128,
                            value_heads=32, value_dim=128),
+    # Reduced dense shape on the key_dim-128 paths (batched prefill); the FFN
+    # width leaves a partial last round of 256-lane pairs.
+    "mini": _dense(vocab=8192, hidden=512, intermediate=1408, layers=4, q_heads=4,
+                   kv_heads=2, head_dim=256, rope_dim=64, key_heads=2, key_dim=128,
+                   value_heads=4, value_dim=128),
     # Reduced shapes on the MoE code paths.
     "mini-moe": _moe(vocab=8192, hidden=512, intermediate=128, layers=4, q_heads=4,
                      kv_heads=2, head_dim=256, rope_dim=64, experts=32, top_k=8,

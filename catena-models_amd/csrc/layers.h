@@ -183,7 +183,9 @@ __global__ __launch_bounds__(kBlock) void k_gated_norm(const uint16_t* __restric
 
 // Full-attention prepare (full_prepare.hex:3-82): per Q or KV head, head RMS
 // with the adjacent-pair tree, neox RoPE on the first R channels, Q to
-// `qout`, K rotated into the cache and V copied into the cache.
+// `qout`, K rotated into the cache and V copied into the cache. blockIdx.y
+// selects token t + y of the call, its rows of qg/key/value/qout and its RoPE
+// table (the batched prefill's per-token prepare, batch_full_prepare.hex:3-97).
 __global__ __launch_bounds__(kBlock) void k_full_prepare(
     const uint16_t* __restrict__ qg, const uint16_t* __restrict__ key,
     const uint16_t* __restrict__ value, const float* __restrict__ rope,
@@ -193,6 +195,13 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
   __shared__ float buf[256];
   __shared__ float normed[256];
   const int head = blockIdx.x, tid = threadIdx.x;
+  const int y = blockIdx.y;
+  qg += (size_t)y * 2 * q_heads * head_dim;
+  key += (size_t)y * kvs;
+  value += (size_t)y * kvs;
+  rope += (size_t)y * rope_dim;
+  qout += (size_t)y * q_heads * head_dim;
+  t += y;
   const bool is_q = head < q_heads;
   const int local = is_q ? head : head - q_heads;
   const uint16_t* src = is_q ? qg + (size_t)local * 2 * head_dim : key + (size_t)local * head_dim;
@@ -230,7 +239,9 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
 // maximum and an adjacent-pair sum over the keys (qwen35_attention.hex:
 // 258-393), 8 interleaved context partials combined
 // ((s0+s4)+(s2+s6))+((s1+s5)+(s3+s7)) (qwen35_attention.hex:2-177) and the
-// sigmoid gate (qwen35.hex:207-222). One block per query head.
+// sigmoid gate (qwen35.hex:207-222). One block per query head; blockIdx.y
+// selects token t + y of the call (the batched prefill's per-query staged
+// attention, batch_staged_attention.hex:10-47) with its own rows and scratch.
 __global__ __launch_bounds__(kBlock) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
     int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
@@ -238,7 +249,13 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
     int scratch_stride, uint16_t* __restrict__ out) {
   __shared__ float partial[kBlock];
   const int head = blockIdx.x, tid = threadIdx.x;
-  const int64_t keys = step_position(params, t) + 1;
+  const int y = blockIdx.y;
+  const size_t qs = (size_t)gridDim.x * head_dim;
+  q += y * qs;
+  qg += y * 2 * qs;
+  out += y * qs;
+  scratch += (size_t)y * gridDim.x * scratch_stride;
+  const int64_t keys = step_position(params, t + y) + 1;
   const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
   float* s = scratch + (size_t)head * scratch_stride;
   float* e = s + keys;

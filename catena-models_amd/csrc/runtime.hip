@@ -21,6 +21,7 @@
 #include "attention.h"
 #include "layers.h"
 #include "mega.h"
+#include "prefill.h"
 
 using namespace cq35;
 
@@ -410,12 +411,12 @@ namespace {
 enum KernelClass {
   KC_EMBED = 0, KC_PROJECT, KC_PREPARE_LINEAR, KC_DELTA, KC_GATED_NORM, KC_RESIDUAL,
   KC_PREPARE_FULL, KC_ATTENTION, KC_ATTENTION_VALUES, KC_ROUTER, KC_MOE_GATE, KC_MOE_DOWN,
-  KC_SWIGLU, KC_LOGITS, KC_SHADOW, KC_DECODE_STEP, KC_COUNT
+  KC_SWIGLU, KC_LOGITS, KC_SHADOW, KC_DECODE_STEP, KC_PREFILL_PROJECT, KC_COUNT
 };
 const char* kClassNames[KC_COUNT] = {
     "embed_rope", "project", "linear_prepare", "delta", "gated_norm", "residual_project",
     "full_prepare", "attention", "attention_values", "moe_router", "moe_gate_up", "moe_down",
-    "swiglu", "logits_argmax", "shadow_copy", "decode_step"};
+    "swiglu", "logits_argmax", "shadow_copy", "decode_step", "prefill_project"};
 
 constexpr int kMaxTimedEvents = 512;
 
@@ -465,6 +466,15 @@ struct cq35_session {
   const void* mega_kernel = nullptr;  // k_decode_step<shape> for this model
   int mega_lds = 0;                   // its dynamic LDS bytes
   uint32_t seq = 0;
+  // batched prefill: chunk buffers of kBChunk token rows, allocated on the
+  // first multi-token call at key_dim 128
+  bool pf_ready = false;
+  uint16_t *pf_h = nullptr, *pf_x = nullptr, *pf_attn = nullptr;
+  uint16_t *pf_a = nullptr, *pf_b = nullptr, *pf_c = nullptr, *pf_d = nullptr;
+  uint16_t *pf_e = nullptr, *pf_f = nullptr, *pf_g = nullptr, *pf_act = nullptr;
+  float *pf_rope = nullptr, *pf_logits = nullptr, *pf_probs = nullptr, *pf_scratch = nullptr;
+  int* pf_ids = nullptr;
+  int pf_attn_tokens = 0;  // tokens per staged-attention launch (scratch rows)
   // kernel timing
   int timed_class = -1;
   hipEvent_t ev[2 * kMaxTimedEvents] = {};
@@ -998,6 +1008,179 @@ void enqueue_shadow(cq35_session* s, bool import) {
       (int)d.L, (const float*)s->shadow);
 }
 
+// Shapes the batched prefill kernels accept (quad loads, scan width, the
+// shared-expert lanes inside the routed loop); empty when supported.
+const char* prefill_unsupported(const cq35_model& m) {
+  const Dims& d = m.d;
+  const cq35_config& c = m.cfg;
+  if (d.H % 8 || d.QS % 8 || d.VS % 8) return "hidden, query and value widths must be multiples of 8";
+  if (c.key_dim > 256) return "key_dim above 256";
+  if (d.I % 8) return "intermediate width must be a multiple of 8";
+  if (c.moe && (d.SI % 8 || d.SI > d.K * d.I))
+    return "shared-expert width must be a multiple of 8 and at most top_k * intermediate";
+  if (c.moe && d.K > 64) return "top_k above 64";
+  return nullptr;
+}
+
+// Chunk buffers of the batched prefill (kBChunk token rows each).
+int setup_prefill(cq35_session* s) {
+  if (s->pf_ready) return CQ35_OK;
+  const Dims& d = s->model->d;
+  const cq35_config& c = s->model->cfg;
+  const int64_t m = kBChunk, VH = c.value_heads;
+  int rc = CQ35_OK;
+  auto check = [&](int r) { if (r && !rc) rc = r; };
+  check(dalloc(s, &s->pf_h, m * d.H));
+  check(dalloc(s, &s->pf_x, m * d.H));
+  check(dalloc(s, &s->pf_attn, m * d.H));
+  check(dalloc(s, &s->pf_a, m * std::max(d.QKV, 2 * d.QS)));  // qkv | qg
+  check(dalloc(s, &s->pf_b, m * std::max(d.VS, d.KVS)));      // z | k
+  check(dalloc(s, &s->pf_c, m * std::max(2 * VH, d.KVS)));    // alpha, beta | v
+  check(dalloc(s, &s->pf_d, m * std::max(d.QKV, d.QS)));      // conv | rotated q
+  check(dalloc(s, &s->pf_e, m * 2 * d.KS));                   // l2 q, k
+  check(dalloc(s, &s->pf_f, m * std::max(d.VS, d.QS)));       // core | context
+  check(dalloc(s, &s->pf_g, m * d.VS));                       // gated
+  check(dalloc(s, &s->pf_act, m * std::max(d.I, d.K * d.I + d.SI)));
+  check(dalloc(s, &s->pf_rope, m * std::max<int64_t>(d.R, 2)));
+  if (c.moe) {
+    check(dalloc(s, &s->pf_logits, m * (d.E + 1)));
+    check(dalloc(s, &s->pf_ids, m * d.K));
+    check(dalloc(s, &s->pf_probs, m * d.K));
+  }
+  // staged attention scratch rows, at most 64 MiB
+  const int64_t per_token = d.Q * (int64_t)s->attn_stride;
+  s->pf_attn_tokens = (int)std::max<int64_t>(1, std::min<int64_t>(m, (64ll << 20) / 4 / per_token));
+  check(dalloc(s, &s->pf_scratch, s->pf_attn_tokens * per_token));
+  if (rc) return rc;
+  s->pf_ready = true;
+  return CQ35_OK;
+}
+
+// The batched prefill of an n-token call (text-batch, prefill.rs:523-618):
+// shadow import, then per chunk of kBChunk tokens the embedding rows and the
+// layer fold over all rows (batch.full / batch.linear, prefill.rs:92-456),
+// shadow persist, and the head on the call's last row (prefill.row).
+void enqueue_prefill(cq35_session* s, int64_t n) {
+  const cq35_model& m = *s->model;
+  const cq35_config& c = m.cfg;
+  const Dims& d = m.d;
+  Launcher L{s};
+  auto Wt = [&](int64_t index) { return m.w[index]; };
+  const int64_t cap = s->capacity;
+  const int H = (int)d.H, VH = c.value_heads;
+  const uint64_t* params = s->d_params;
+  enqueue_shadow(s, true);
+  int last_rows = 1;
+  for (int64_t c0 = 0; c0 < n; c0 += kBChunk) {
+    const int rows_n = (int)std::min<int64_t>(kBChunk, n - c0);
+    const int first = (int)c0;
+    const unsigned tiles = (unsigned)((rows_n + 4 * kBTokens - 1) / (4 * kBTokens));
+    L(KC_EMBED, k_bembed, dim3(rows_n), dim3(kBlock), 0, params, first, (const uint16_t*)Wt(0), H,
+      s->pf_h, c0 + rows_n == n ? s->d_best : (unsigned long long*)nullptr);
+    auto project = [&](const uint16_t* x, int cols, const void* w, int rows, uint16_t* out) {
+      L(KC_PREFILL_PROJECT, k_bproject<kBPlain>, dim3((unsigned)rows, tiles), dim3(kBlock), 0, x,
+        rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr,
+        out);
+    };
+    auto residual_rows = [&](const uint16_t* x, int cols, const void* w, const uint16_t* res,
+                             uint16_t* out) {
+      L(KC_PREFILL_PROJECT, k_bproject<kBResidual>, dim3((unsigned)H, tiles), dim3(kBlock), 0, x,
+        rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
+    };
+    auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
+      L(KC_PROJECT, k_bnorm, dim3(rows_n), dim3(kBlock), (size_t)H * 2, x, (const float*)w, H,
+        c.eps, out);
+    };
+    int64_t base = 1;
+    for (int64_t l = 0; l < d.L; ++l) {
+      auto W = [&](int slot) { return Wt(base + slot); };
+      const int64_t key_base = l * 2 * cap * d.KVS;
+      const int64_t value_base = key_base + cap * d.KVS;
+      norm(s->pf_h, W(0), s->pf_x);
+      int ffn;
+      const void* post_norm;
+      if (is_full(c, l)) {
+        uint16_t *qg = s->pf_a, *kraw = s->pf_b, *vraw = s->pf_c, *qr = s->pf_d, *ctx = s->pf_f;
+        project(s->pf_x, H, W(1), (int)(2 * d.QS), qg);
+        project(s->pf_x, H, W(2), (int)d.KVS, kraw);
+        project(s->pf_x, H, W(3), (int)d.KVS, vraw);
+        L(KC_EMBED, k_brope, dim3(rows_n), dim3(kBlock), 0, params, first, (const float*)m.freq,
+          (int)(d.R / 2), s->pf_rope);
+        L(KC_PREPARE_FULL, k_full_prepare, dim3((unsigned)(d.Q + d.KVH), rows_n), dim3(kBlock), 0,
+          (const uint16_t*)qg, (const uint16_t*)kraw, (const uint16_t*)vraw,
+          (const float*)s->pf_rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
+          value_base, params, first, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, qr);
+        const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
+        for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
+          const int am = std::min(s->pf_attn_tokens, rows_n - a0);
+          L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kBlock), 0,
+            (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base,
+            value_base, params, first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
+            (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS), s->pf_scratch, s->attn_stride,
+            ctx + (size_t)a0 * d.QS);
+        }
+        residual_rows(ctx, (int)d.QS, W(4), s->pf_h, s->pf_attn);
+        post_norm = W(7);
+        ffn = 8;
+      } else {
+        uint16_t *qkv = s->pf_a, *z = s->pf_b, *alpha = s->pf_c, *beta = s->pf_c + (size_t)kBChunk * VH;
+        uint16_t *conv = s->pf_d, *qn = s->pf_e, *kn = s->pf_e + (size_t)kBChunk * d.KS;
+        uint16_t *core = s->pf_f, *gated = s->pf_g;
+        project(s->pf_x, H, W(1), (int)d.QKV, qkv);
+        project(s->pf_x, H, W(2), (int)d.VS, z);
+        project(s->pf_x, H, W(3), VH, alpha);
+        project(s->pf_x, H, W(4), VH, beta);
+        const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
+        L(KC_PREPARE_LINEAR, k_bprepare,
+          dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), rows_n), dim3(kBlock), 0,
+          (const uint16_t*)qkv, (const uint16_t*)s->cache, conv_base, params, first,
+          (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, conv, qn, kn);
+        L(KC_PREPARE_LINEAR, k_bhistory, dim3(grid_for((3 * d.QKV + kBlock - 1) / kBlock, 1024)),
+          dim3(kBlock), 0, (const uint16_t*)qkv, rows_n, s->cache, conv_base, params, first,
+          (int)d.QKV);
+        const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
+        L(KC_DELTA, k_bscan, dim3((unsigned)((d.VS + 7) / 8)), dim3(kBlock), 0,
+          (const uint16_t*)conv, (const uint16_t*)qn, (const uint16_t*)kn, (const uint16_t*)alpha,
+          (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), s->shadow + l * d.REC,
+          rows_n, (int)d.VS, c.value_dim, VH, c.key_dim, c.key_heads, (int)d.QKV, scale, core);
+        L(KC_GATED_NORM, k_gated_norm, dim3((unsigned)(VH * rows_n)), dim3(kBlock), 0,
+          (const uint16_t*)core, (const uint16_t*)z, (const float*)W(7), c.value_dim, c.eps, gated);
+        residual_rows(gated, (int)d.VS, W(8), s->pf_h, s->pf_attn);
+        post_norm = W(10);
+        ffn = 11;
+      }
+      norm(s->pf_attn, post_norm, s->pf_x);
+      if (c.moe) {
+        const int E = (int)d.E, K = (int)d.K, I = (int)d.I, SI = (int)d.SI;
+        L(KC_ROUTER, k_brouter, dim3((unsigned)((E + 1 + 3) / 4), rows_n), dim3(kBlock), 0,
+          (const uint16_t*)s->pf_x, H, (const float*)W(ffn), (const float*)W(ffn + 4), E,
+          s->pf_logits);
+        L(KC_ROUTER, k_bselect, dim3(rows_n), dim3(kBlock), (size_t)E * 4,
+          (const float*)s->pf_logits, E, K, s->pf_ids, s->pf_probs);
+        const int rows = K * I + SI;
+        L(KC_MOE_GATE, k_bmoe_gate, dim3((unsigned)((rows + 3) / 4), rows_n), dim3(kBlock), 0,
+          (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
+          (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
+          (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
+        L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)((H + 3) / 4), rows_n), dim3(kBlock), 0,
+          (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
+          (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, s->pf_h);
+      } else {
+        L(KC_PREFILL_PROJECT, k_bproject<kBGate>, dim3((unsigned)d.I, tiles), dim3(kBlock), 0,
+          (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
+          (int)d.I, (const uint16_t*)nullptr, s->pf_act);
+        residual_rows(s->pf_act, (int)d.I, W(ffn + 2), s->pf_attn, s->pf_h);
+      }
+      base += layer_tensors(c, l);
+    }
+    last_rows = rows_n;
+  }
+  enqueue_shadow(s, false);
+  const int64_t total = weight_count(c);
+  project32<true>(L, KC_LOGITS, s->pf_h + (size_t)(last_rows - 1) * d.H, (const float*)Wt(total - 2),
+                  c.eps, segments({{Wt(total - 1), {s->logits, d.V}}}), d.H, s->d_best);
+}
+
 uint64_t decode_key(unsigned long long key) {
   if (key == 0) return 0;
   return (uint64_t)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
@@ -1119,12 +1302,19 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
   for (int64_t i = 0; i < n; ++i)
     if (tokens[i] >= (uint64_t)c.vocab)
       return fail(CQ35_ERANGE, "token prefix contains an ID outside the %d-token vocabulary", c.vocab);
-  if (n >= 2 && c.key_dim == 128)
-    return fail(CQ35_EUNSUPPORTED,
-                "multi-token calls with key_dim 128 take the reference's batched prefill path "
-                "(prefill.rs:623-652), which this build does not provide; append tokens one at a time");
+  // Multi-token calls at key_dim 128 take the batched prefill
+  // (text-dispatch, prefill.rs:623-652); smaller key dims fold token by token.
+  const bool batched = n >= 2 && c.key_dim == 128;
+  if (batched) {
+    if (const char* why = prefill_unsupported(*s->model))
+      return fail(CQ35_EUNSUPPORTED, "batched prefill: %s", why);
+  }
   hipError_t e = hipSetDevice(s->model->device);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+  if (batched) {
+    const int rc = setup_prefill(s);
+    if (rc) return rc;
+  }
   if (n == 1 && s->mega_on && (s->timed_class < 0 || s->timed_class == KC_DECODE_STEP))
     return step_persistent(s, tokens[0], start, next_token, logits);
   s->h_params[0] = (uint64_t)start;
@@ -1155,6 +1345,10 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
     }
     e = hipGraphLaunch(s->graph_exec, s->stream);
     if (e != hipSuccess) return fail(CQ35_EDEVICE, "graph launch: %s", hipGetErrorString(e));
+  } else if (batched) {
+    enqueue_prefill(s, n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail(CQ35_EDEVICE, "kernel launch: %s", hipGetErrorString(e));
   } else {
     if (shadow) enqueue_shadow(s, true);
     for (int64_t t = 0; t < n; ++t) enqueue_token(s, (int)t, t == n - 1, shadow);

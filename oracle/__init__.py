@@ -63,6 +63,8 @@ def lib():
         l.ox_dot_width.restype = ctypes.c_float
         l.ox_dot_width_f32w.argtypes = [P, P, I64, ctypes.c_int]
         l.ox_dot_width_f32w.restype = ctypes.c_float
+        l.ox_dot_b256.argtypes = [P, P, I64]
+        l.ox_dot_b256.restype = ctypes.c_float
         l.ox_fill_tensor.argtypes = [ctypes.POINTER(OxConfig), U64, I64, P]
         l.ox_mix64.argtypes = [U64]
         l.ox_mix64.restype = U64
@@ -121,6 +123,12 @@ def dot_width(x: np.ndarray, w: np.ndarray, width: int) -> float:
         return lib().ox_dot_width_f32w(x.ctypes.data, w.ctypes.data, len(x) // 2, width)
     w = np.ascontiguousarray(w, dtype=np.uint16)
     return lib().ox_dot_width(x.ctypes.data, w.ctypes.data, len(x) // 2, width)
+
+
+def dot_b256(x: np.ndarray, w: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    return lib().ox_dot_b256(x.ctypes.data, w.ctypes.data, len(x) // 2)
 
 
 # ------------------------------------------------------------- weights/model

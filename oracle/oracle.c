@@ -225,6 +225,43 @@ static void dot_dual(const uint16_t* x, const uint16_t* w1, const uint16_t* w2, 
   *r2 = tree(b, width);
 }
 
+/* B256, the batched-prefill projections: lane l visits pairs l, l+256, ...
+ * with ONE accumulator, acc = (acc + x.lo*w.lo) + x.hi*w.hi (bf16x2.dot-f32,
+ * numeric.hex:17-28), then the 256-wide halving tree (batch_projection.hex:
+ * 4-18 and 855-941; cooperative.hex:285-335). Lanes without pairs hold +0. */
+float ox_dot_b256(const uint16_t* x, const uint16_t* w, int64_t pairs) {
+  float sums[256];
+  for (int lane = 0; lane < 256; ++lane) {
+    float acc = 0.0f;
+    for (int64_t p = lane; p < pairs; p += 256) {
+      acc = acc + ox_bf2f(x[2 * p]) * ox_bf2f(w[2 * p]);
+      acc = acc + ox_bf2f(x[2 * p + 1]) * ox_bf2f(w[2 * p + 1]);
+    }
+    sums[lane] = acc;
+  }
+  return tree(sums, 256);
+}
+
+/* Dual B256 sharing the input (batch.dot-dual, batch_projection.hex:4-18). */
+static void dot_b256_dual(const uint16_t* x, const uint16_t* w1, const uint16_t* w2, int64_t pairs,
+                          float* r1, float* r2) {
+  float a[256], b[256];
+  for (int lane = 0; lane < 256; ++lane) {
+    float g = 0.0f, u = 0.0f;
+    for (int64_t p = lane; p < pairs; p += 256) {
+      float xl = ox_bf2f(x[2 * p]), xh = ox_bf2f(x[2 * p + 1]);
+      g = g + xl * ox_bf2f(w1[2 * p]);
+      g = g + xh * ox_bf2f(w1[2 * p + 1]);
+      u = u + xl * ox_bf2f(w2[2 * p]);
+      u = u + xh * ox_bf2f(w2[2 * p + 1]);
+    }
+    a[lane] = g;
+    b[lane] = u;
+  }
+  *r1 = tree(a, 256);
+  *r2 = tree(b, 256);
+}
+
 static int64_t next_pow2(int64_t v) { int64_t p = 1; while (p < v) p <<= 1; return p; }
 
 /* Adjacent-pair tree of x^2 over the padded power-of-two width
@@ -745,28 +782,18 @@ static void attention_staged(const ox_model* m, const uint16_t* q, const uint16_
   free(s); free(p); free(buf);
 }
 
-/* Routed MoE FFN (qwen35_moe.hex; graph qwen35.rs:124-167). */
-static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uint16_t* x,
-                    const uint16_t* residual, uint16_t* out) {
-  const int64_t H = m->c.hidden, E = m->c.experts, K = m->c.top_k, I = m->c.intermediate,
-                SI = m->c.shared_intermediate;
-  const float* router = WF(m, l, ffn + 0);
-  const uint16_t* gate = WB(m, l, ffn + 1);
-  const uint16_t* up = WB(m, l, ffn + 2);
-  const uint16_t* down = WB(m, l, ffn + 3);
-  const float* shared_router = WF(m, l, ffn + 4);
-  const uint16_t* sgate = WB(m, l, ffn + 5);
-  const uint16_t* sup = WB(m, l, ffn + 6);
-  const uint16_t* sdown = WB(m, l, ffn + 7);
-  /* router: S32 over BF16 input x F32 weights, E routed rows + the shared gate
-   * row (moe.hex:4-84). */
+/* Router logits (E routed rows + the shared-expert gate row, S32 over BF16
+ * input x F32 weights, moe.hex:4-84; the batched router runs the same stage
+ * per token, batch_moe.hex:45-96) and the top-k selection: stable rank,
+ * softmax over the selected logits with a serial denominator
+ * (moe.hex:86-252; batch_moe.hex:136-281). */
+static void moe_route(const ox_model* m, const uint16_t* x, const float* router,
+                      const float* shared_router, int64_t* ids, float* prob, float* shared_prob) {
+  const int64_t H = m->c.hidden, E = m->c.experts, K = m->c.top_k;
   float* logit = (float*)malloc(sizeof(float) * (size_t)(E + 1));
 #pragma omp parallel for schedule(static)
   for (int64_t e = 0; e <= E; ++e)
     logit[e] = ox_dot_width_f32w(x, e < E ? router + e * H : shared_router, H / 2, 32);
-  /* select: stable rank, softmax over the selected logits with a serial
-   * denominator (moe.hex:86-252). */
-  int64_t ids[64];
   float sel[64];
   for (int64_t e = 0; e < E; ++e) {
     int64_t rank = 0;
@@ -777,16 +804,27 @@ static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uin
     }
     if (rank < K) { ids[rank] = e; sel[rank] = logit[e]; }
   }
-  float ex[64], den = 0.0f, prob[64];
+  float ex[64], den = 0.0f;
   for (int64_t j = 0; j < K; ++j) ex[j] = ox_exp(sel[j] - sel[0]);
   for (int64_t j = 0; j < K; ++j) den = den + ex[j];
   for (int64_t j = 0; j < K; ++j) prob[j] = ex[j] / den;
-  for (int64_t j = 0; j < K; ++j) se->last_ids[l * K + j] = ids[j];
-  float shared_prob = ox_sigmoid(logit[E]);
-  /* gate/up: S256 dual rows; routed bf16(silu(g)*u*p), shared
-   * bf16(bf16(bf16(silu(g))*u)*sigmoid) (moe.hex:254-333). */
+  *shared_prob = ox_sigmoid(logit[E]);
+  free(logit);
+}
+
+/* Expert gate/up rows: routed bf16(silu(g)*u*p), shared
+ * bf16(bf16(bf16(silu(g))*u)*sigmoid) with g, u = bf16 of the dual dot:
+ * S256 split pair in decode (moe.hex:254-333), B256 single accumulator in
+ * the batched prefill (batch_moe.hex:339-411). */
+static void moe_gate(const ox_model* m, int l, int ffn, const uint16_t* x, const int64_t* ids,
+                     const float* prob, float shared_prob, int b256, uint16_t* active) {
+  const int64_t H = m->c.hidden, K = m->c.top_k, I = m->c.intermediate,
+                SI = m->c.shared_intermediate;
+  const uint16_t* gate = WB(m, l, ffn + 1);
+  const uint16_t* up = WB(m, l, ffn + 2);
+  const uint16_t* sgate = WB(m, l, ffn + 5);
+  const uint16_t* sup = WB(m, l, ffn + 6);
   const int64_t rows = K * I + SI;
-  uint16_t* active = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)rows);
 #pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < rows; ++r) {
     int routed = r < K * I;
@@ -800,7 +838,8 @@ static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uin
       wg = sgate + (r - K * I) * H; wu = sup + (r - K * I) * H;
     }
     float g, u;
-    dot_dual(x, wg, wu, H / 2, 256, &g, &u);
+    if (b256) dot_b256_dual(x, wg, wu, H / 2, &g, &u);
+    else dot_dual(x, wg, wu, H / 2, 256, &g, &u);
     float gb = rbf(g), ub = rbf(u);
     float activated = ox_silu(gb);
     float y;
@@ -808,29 +847,74 @@ static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uin
     else y = rbf(rbf(activated) * ub) * shared_prob;
     active[r] = ox_f2bf(y);
   }
-  /* down: routed S32 over the concatenated expert rows, shared S32, then
-   * bf16(bf16(routed + residual) (+) bf16(shared)) (moe.hex:371-434,
-   * simt_moe.hex:36-287). */
+}
+
+/* Expert down: routed tree over the concatenated expert rows, shared tree,
+ * then bf16(bf16(routed + residual) (+) bf16(shared)). Decode: S32 split
+ * pair (moe.hex:371-434, simt_moe.hex:36-287); batched prefill: B256 single
+ * accumulators, the shared terms gated to p < SI/2 inside the routed loop
+ * (batch_moe.hex:453-563). */
+static void moe_down(const ox_model* m, int l, int ffn, const uint16_t* active, const int64_t* ids,
+                     const uint16_t* residual, int b256, uint16_t* out) {
+  const int64_t H = m->c.hidden, K = m->c.top_k, I = m->c.intermediate,
+                SI = m->c.shared_intermediate;
+  const uint16_t* down = WB(m, l, ffn + 3);
+  const uint16_t* sdown = WB(m, l, ffn + 7);
   const int64_t ip = I / 2, ap = K * I / 2, sp = SI / 2;
 #pragma omp parallel for schedule(static)
   for (int64_t o = 0; o < H; ++o) {
-    float lanes[32];
-    for (int lane = 0; lane < 32; ++lane) {
-      float lo = 0.0f, hi = 0.0f;
-      for (int64_t p = lane; p < ap; p += 32) {
-        const uint16_t* w = down + (ids[p / ip] * H + o) * I + 2 * (p % ip);
-        lo += ox_bf2f(active[2 * p]) * ox_bf2f(w[0]);
-        hi += ox_bf2f(active[2 * p + 1]) * ox_bf2f(w[1]);
+    float routed, shared;
+    if (b256) {
+      float rl[256], sl[256];
+      for (int lane = 0; lane < 256; ++lane) {
+        float r = 0.0f, sh = 0.0f;
+        for (int64_t p = lane; p < ap; p += 256) {
+          const uint16_t* w = down + (ids[p / ip] * H + o) * I + 2 * (p % ip);
+          r = r + ox_bf2f(active[2 * p]) * ox_bf2f(w[0]);
+          r = r + ox_bf2f(active[2 * p + 1]) * ox_bf2f(w[1]);
+          if (p < sp) {
+            const uint16_t* sw = sdown + o * SI + 2 * p;
+            const uint16_t* sx = active + K * I + 2 * p;
+            sh = sh + ox_bf2f(sx[0]) * ox_bf2f(sw[0]);
+            sh = sh + ox_bf2f(sx[1]) * ox_bf2f(sw[1]);
+          }
+        }
+        rl[lane] = r;
+        sl[lane] = sh;
       }
-      lanes[lane] = lo + hi;
+      routed = tree(rl, 256);
+      shared = tree(sl, 256);
+    } else {
+      float lanes[32];
+      for (int lane = 0; lane < 32; ++lane) {
+        float lo = 0.0f, hi = 0.0f;
+        for (int64_t p = lane; p < ap; p += 32) {
+          const uint16_t* w = down + (ids[p / ip] * H + o) * I + 2 * (p % ip);
+          lo += ox_bf2f(active[2 * p]) * ox_bf2f(w[0]);
+          hi += ox_bf2f(active[2 * p + 1]) * ox_bf2f(w[1]);
+        }
+        lanes[lane] = lo + hi;
+      }
+      routed = tree(lanes, 32);
+      shared = ox_dot_width(active + K * I, sdown + o * SI, sp, 32);
     }
-    float routed = tree(lanes, 32);
-    float shared = ox_dot_width(active + K * I, sdown + o * SI, sp, 32);
     uint16_t routed_bf = ox_f2bf(routed + ox_bf2f(residual[o]));
     out[o] = bf_add(routed_bf, ox_f2bf(shared));
   }
+}
+
+/* Routed MoE FFN of one token (qwen35_moe.hex; graph qwen35.rs:124-167). */
+static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uint16_t* x,
+                    const uint16_t* residual, int b256, uint16_t* out) {
+  const int64_t K = m->c.top_k, I = m->c.intermediate, SI = m->c.shared_intermediate;
+  int64_t ids[64];
+  float prob[64], shared_prob;
+  moe_route(m, x, WF(m, l, ffn + 0), WF(m, l, ffn + 4), ids, prob, &shared_prob);
+  for (int64_t j = 0; j < K; ++j) se->last_ids[l * K + j] = ids[j];
+  uint16_t* active = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(K * I + SI));
+  moe_gate(m, l, ffn, x, ids, prob, shared_prob, b256, active);
+  moe_down(m, l, ffn, active, ids, residual, b256, out);
   free(active);
-  free(logit);
 }
 
 static int argmax_bf16(const uint16_t* logits, int64_t vocab, uint64_t* token) {
@@ -855,6 +939,160 @@ static int argmax_bf16(const uint16_t* logits, int64_t vocab, uint64_t* token) {
 
 static int64_t attention_interval_ok(const ox_config* c) { return c->full_interval > 0; }
 
+/* ------------------------------------------------- batched prefill (K8) */
+
+/* Token-major batched projections (batch.project / residual / gate,
+ * batch_projection.hex:30-279, 280-530, 531-854): row r of token t is a B256
+ * dot; epilogues bf16(total), bf16(bf16(total) (+) res), and
+ * bf16(bf16(silu(bf16 g))) (x) bf16(u). */
+static void bproject(const uint16_t* x, int64_t n, const uint16_t* w, int64_t rows, int64_t cols,
+                     uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n * rows; ++i) {
+    const int64_t t = i / rows, r = i % rows;
+    out[i] = ox_f2bf(ox_dot_b256(x + t * cols, w + r * cols, cols / 2));
+  }
+}
+static void bresidual(const uint16_t* x, int64_t n, const uint16_t* w, int64_t rows, int64_t cols,
+                      const uint16_t* res, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n * rows; ++i) {
+    const int64_t t = i / rows, r = i % rows;
+    out[i] = bf_add(ox_f2bf(ox_dot_b256(x + t * cols, w + r * cols, cols / 2)), res[i]);
+  }
+}
+static void bgate(const uint16_t* x, int64_t n, const uint16_t* wg, const uint16_t* wu,
+                  int64_t rows, int64_t cols, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n * rows; ++i) {
+    const int64_t t = i / rows, r = i % rows;
+    float g, u;
+    dot_b256_dual(x + t * cols, wg + r * cols, wu + r * cols, cols / 2, &g, &u);
+    out[i] = bf_mul(ox_f2bf(ox_silu(rbf(g))), ox_f2bf(u));
+  }
+}
+
+/* A call with n >= 2 tokens at key_dim 128 (text-dispatch -> text-batch,
+ * prefill.rs:36-653): every layer runs over all tokens before the next
+ * (batch.layer.fold), with the per-token operations of the decode step
+ * where the batched kernels keep them (RMSNorm per row, qwen35.hex:912-977;
+ * conv + L2 with history reads before the history commit,
+ * batch_prepare.hex:3-292; the DeltaNet scan with the F32 state,
+ * batch_scan.hex:1-200; gated norm, batch_gated.hex; head norm + RoPE + KV
+ * append, batch_full_prepare.hex:3-97; staged attention per query,
+ * batch_staged_attention.hex:10-47; router + select per token) and B256
+ * projections for the rest. The recurrent state is imported into the F32
+ * shadow before and persisted after (qwen35.hex:2-141); the head runs on the
+ * last row (prefill.row). */
+static int step_batch(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
+                      uint64_t* next_token, uint16_t* logits_out) {
+  const ox_model* m = se->m;
+  const ox_config* c = &m->c;
+  const int64_t H = c->hidden, HD = c->head_dim, KVS = m->KVS, QS = m->QS;
+  const int64_t KV_STRIDE = (int64_t)c->layers * 2 * KVS;
+  const int64_t kv_end = se->capacity * KV_STRIDE;
+  for (int l = 0; l < c->layers; ++l)
+    for (int64_t i = 0; i < m->REC; ++i)
+      se->shadow[l * m->REC + i] = ox_bf2f(se->cache[kv_end + l * m->LIN + m->CONV + i]);
+  int64_t wide = m->QKV > 2 * QS ? m->QKV : 2 * QS;
+  if (m->VS > wide) wide = m->VS;
+  if (c->intermediate > wide) wide = c->intermediate;
+  if (H > wide) wide = H;
+  uint16_t* h = (uint16_t*)malloc(2 * (size_t)(n * H));
+  uint16_t* x = (uint16_t*)malloc(2 * (size_t)(n * H));
+  uint16_t* attn = (uint16_t*)malloc(2 * (size_t)(n * H));
+  uint16_t* b1 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* b2 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* b3 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* b4 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* b5 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* b6 = (uint16_t*)malloc(2 * (size_t)(n * wide));
+  uint16_t* row = (uint16_t*)malloc(2 * (size_t)wide);
+  float rope[1024];
+  for (int64_t t = 0; t < n; ++t)
+    memcpy(h + t * H, (const uint16_t*)m->w[0] + tokens[t] * H, 2 * (size_t)H);  /* prefill.embed */
+  for (int l = 0; l < c->layers; ++l) {
+    const int64_t key_off = (int64_t)l * 2 * se->capacity * KVS;
+    const int64_t value_off = key_off + se->capacity * KVS;
+    normalize_rows(h, WF(m, l, 0), H, n, c->eps, x);
+    int ffn;
+    const float* post_norm;
+    if (is_full(c, l)) {
+      uint16_t *qg = b1, *kraw = b2, *vraw = b3, *qn = b4, *qr = b5, *ctx = b6;
+      bproject(x, n, WB(m, l, 1), 2 * QS, H, qg);
+      bproject(x, n, WB(m, l, 2), KVS, H, kraw);
+      bproject(x, n, WB(m, l, 3), KVS, H, vraw);
+      for (int64_t t = 0; t < n; ++t) {
+        const int64_t position = start + t;
+        uint16_t* qgt = qg + t * 2 * QS;
+        uint16_t* kt = kraw + t * KVS;
+        for (int hh = 0; hh < c->q_heads; ++hh)
+          memcpy(qn + hh * HD, qgt + 2 * hh * HD, 2 * (size_t)HD);
+        normalize_rows(qn, WF(m, l, 5), HD, c->q_heads, c->eps, qn);
+        normalize_rows(kt, WF(m, l, 6), HD, c->kv_heads, c->eps, kt);
+        rope_table(m, position, rope);
+        for (int hh = 0; hh < c->q_heads; ++hh)
+          rotate_head(qn + hh * HD, rope, (int)HD, c->rope_dim, qr + t * QS + hh * HD);
+        for (int hh = 0; hh < c->kv_heads; ++hh)
+          rotate_head(kt + hh * HD, rope, (int)HD, c->rope_dim,
+                      se->cache + key_off + position * KVS + hh * HD);
+        memcpy(se->cache + value_off + position * KVS, vraw + t * KVS, 2 * (size_t)KVS);
+      }
+      for (int64_t t = 0; t < n; ++t)
+        attention_staged(m, qr + t * QS, se->cache, key_off, value_off, start + t + 1,
+                         qg + t * 2 * QS, ctx + t * QS);
+      bresidual(ctx, n, WB(m, l, 4), H, QS, h, attn);
+      post_norm = WF(m, l, 7);
+      ffn = 8;
+    } else {
+      uint16_t *qkv = b1, *z = b2, *ab = b3, *conv = b4, *core = b5, *gated = b6;
+      const int64_t VH = c->value_heads;
+      uint16_t* alpha = ab;
+      uint16_t* beta = ab + n * VH;
+      bproject(x, n, WB(m, l, 1), m->QKV, H, qkv);
+      bproject(x, n, WB(m, l, 2), m->VS, H, z);
+      bproject(x, n, WB(m, l, 3), VH, H, alpha);
+      bproject(x, n, WB(m, l, 4), VH, H, beta);
+      const int64_t conv_base = kv_end + l * m->LIN;
+      for (int64_t t = 0; t < n; ++t) {
+        uint16_t* ct = conv + t * m->QKV;
+        conv_step(m, se->cache, conv_base, start + t, WF(m, l, 9), qkv + t * m->QKV, ct);
+        uint16_t* q = row;
+        uint16_t* k = row + m->KS;
+        l2_heads(ct, c->key_heads, c->key_dim, q);
+        l2_heads(ct + m->KS, c->key_heads, c->key_dim, k);
+        delta_step(m, ct, q, k, alpha + t * VH, beta + t * VH, WF(m, l, 5), WF(m, l, 6), NULL,
+                   se->shadow + l * m->REC, core + t * m->VS);
+        gated_norm(m, core + t * m->VS, z + t * m->VS, WF(m, l, 7), gated + t * m->VS);
+      }
+      bresidual(gated, n, WB(m, l, 8), H, m->VS, h, attn);
+      post_norm = WF(m, l, 10);
+      ffn = 11;
+    }
+    normalize_rows(attn, post_norm, H, n, c->eps, x);
+    if (c->moe) {
+      for (int64_t t = 0; t < n; ++t)
+        moe_ffn(m, se, l, ffn, x + t * H, attn + t * H, 1, h + t * H);
+    } else {
+      uint16_t* act = b1;
+      bgate(x, n, WB(m, l, ffn + 0), WB(m, l, ffn + 1), c->intermediate, H, act);
+      bresidual(act, n, WB(m, l, ffn + 2), H, c->intermediate, attn, h);
+    }
+  }
+  for (int l = 0; l < c->layers; ++l)
+    for (int64_t i = 0; i < m->REC; ++i)
+      se->cache[kv_end + l * m->LIN + m->CONV + i] = ox_f2bf(se->shadow[l * m->REC + i]);
+  int64_t total = ox_weight_count(c);
+  normalize_rows(h + (n - 1) * H, (const float*)m->w[total - 2], H, 1, c->eps, x);
+  uint16_t* logits = logits_out ? logits_out : (uint16_t*)malloc(2 * (size_t)c->vocab);
+  project(x, (const uint16_t*)m->w[total - 1], c->vocab, H, 32, logits);
+  argmax_bf16(logits, c->vocab, next_token);
+  if (!logits_out) free(logits);
+  free(h); free(x); free(attn); free(b1); free(b2); free(b3); free(b4); free(b5); free(b6);
+  free(row);
+  return 0;
+}
+
 int ox_step(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
             uint64_t* next_token, uint16_t* logits_out) {
   const ox_model* m = se->m;
@@ -862,7 +1100,8 @@ int ox_step(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
   if (n < 1 || start < 0 || start + n > se->capacity || !attention_interval_ok(c)) return -1;
   for (int64_t t = 0; t < n; ++t)
     if (tokens[t] >= (uint64_t)c->vocab) return -2;
-  if (n >= 2 && c->key_dim == 128) return -9;  /* batched prefill, prefill.rs:623-652 */
+  if (n >= 2 && c->key_dim == 128)  /* text-dispatch, prefill.rs:623-652 */
+    return step_batch(se, tokens, n, start, next_token, logits_out);
   const int64_t H = c->hidden, HD = c->head_dim, KVS = m->KVS, QS = m->QS;
   const int64_t KV_STRIDE = (int64_t)c->layers * 2 * KVS;
   const int64_t kv_end = se->capacity * KV_STRIDE;
@@ -950,7 +1189,7 @@ int ox_step(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
       }
       normalize_rows(attn, post_norm, H, 1, c->eps, x);
       if (c->moe) {
-        moe_ffn(m, se, l, ffn, x, attn, h);
+        moe_ffn(m, se, l, ffn, x, attn, 0, h);
       } else {
         uint16_t* act = b1;
         swiglu_project(x, WB(m, l, ffn + 0), WB(m, l, ffn + 1), c->intermediate, H, act);

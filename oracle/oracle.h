@@ -90,6 +90,8 @@ float ox_bf2f(uint16_t b);
 /* Split-pair dot with a halving tree of the given width (tests/qwen35_simt.rs:99-116). */
 float ox_dot_width(const uint16_t* x, const uint16_t* w, int64_t pairs, int width);
 float ox_dot_width_f32w(const uint16_t* x, const float* w, int64_t pairs, int width);
+/* B256 single-accumulator dot of the batched prefill (batch_projection.hex:4-18). */
+float ox_dot_b256(const uint16_t* x, const uint16_t* w, int64_t pairs);
 
 /* Synthetic weights: the deterministic generator shared (as a specification)
  * with the GPU library. Fills one tensor of the weight ABI. */

@@ -152,3 +152,62 @@ def merged(a, b, width):
             sums[lane] = F(sums[lane] + sums[lane + s])
         s //= 2
     return sums[0]
+
+
+# ------------------------------------------------ B256 (batched prefill order)
+# The reference holds no known answers for batch_projection.hex; these pin the
+# order by values derived by hand, each chosen so that a plausible mistake
+# (split low/high accumulators, high-before-low, another tree) gives a
+# different number.
+
+def _bf(v):
+    return np.array([np.float32(v)], dtype=np.float32).view(np.uint32)[0] >> 16
+
+
+def _pairs(n_pairs, entries):
+    """x, w BF16 vectors of n_pairs pairs with x*w = value at (pair, half)."""
+    x = np.zeros(2 * n_pairs, dtype=np.uint16)
+    w = np.zeros(2 * n_pairs, dtype=np.uint16)
+    for (p, half), (xv, wv) in entries.items():
+        x[2 * p + half] = _bf(xv)
+        w[2 * p + half] = _bf(wv)
+    return x, w
+
+
+def test_b256_single_accumulator_low_then_high(oracle):
+    # lane 0 visits pairs 0 and 256: products lo 2^24, hi 1, then lo -2^24, hi 1.
+    # one accumulator, low then high: ((((0 + 2^24) + 1) - 2^24) + 1) = 1
+    # (2^24 + 1 rounds to 2^24); split accumulators give 0 + 2 = 2; high
+    # before low gives 0.
+    x, w = _pairs(512, {(0, 0): (4096.0, 4096.0), (0, 1): (1.0, 1.0),
+                        (256, 0): (-4096.0, 4096.0), (256, 1): (1.0, 1.0)})
+    assert oracle.dot_b256(x, w) == 1.0
+    assert oracle.dot_width(x, w, 256) == 2.0  # the decode S256 on the same input
+
+
+def test_b256_halving_tree(oracle):
+    # lanes 0, 1, 2 hold 2^24, 1, -2^24: the halving tree adds lane 2 to lane 0
+    # first (stride 2), then lane 1: (2^24 - 2^24) + 1 = 1. Adjacent pairs or
+    # a serial sum lose the 1 to rounding: 0.
+    x, w = _pairs(256, {(0, 0): (4096.0, 4096.0), (1, 0): (1.0, 1.0), (2, 0): (-4096.0, 4096.0)})
+    assert oracle.dot_b256(x, w) == 1.0
+    # a lane with several pairs and the tree's wide strides: exact small integers
+    rng = np.random.default_rng(3)
+    xv = rng.integers(-8, 9, 2 * 700).astype(np.float32)
+    wv = rng.integers(-8, 9, 2 * 700).astype(np.float32)
+    x = (xv.view(np.uint32) >> 16).astype(np.uint16)
+    w = (wv.view(np.uint32) >> 16).astype(np.uint16)
+    assert oracle.dot_b256(x, w) == float(np.dot(xv.astype(np.float64), wv.astype(np.float64)))
+
+
+def test_b256_random_within_rounding(oracle):
+    rng = np.random.default_rng(5)
+    for pairs in (128, 256, 704, 1024):
+        xv = rng.standard_normal(2 * pairs).astype(np.float32)
+        wv = rng.standard_normal(2 * pairs).astype(np.float32) * 0.02
+        x = oracle.bf16_round(xv)
+        w = oracle.bf16_round(wv)
+        exact = float(np.dot(oracle.bf16_to_f32(x).astype(np.float64),
+                             oracle.bf16_to_f32(w).astype(np.float64)))
+        got = oracle.dot_b256(x, w)
+        assert abs(got - exact) <= 1e-5 * (1 + abs(exact)), (pairs, got, exact)

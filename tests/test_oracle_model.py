@@ -133,3 +133,33 @@ def test_multi_token_call_keeps_f32_state(oracle):
     tl = textbook_logits(cfg, w, tokens, 0, multi)
     assert discrepancy(multi, tl) < 0.15
     assert discrepancy(single, tl) < 0.15
+
+
+@pytest.mark.parametrize("name", ["mini", "mini-moe"])
+def test_batched_prefill_matches_textbook(oracle, name):
+    """A multi-token call at key_dim 128 takes the batched prefill (layer-major,
+    B256 projections, F32 scan state); its logits and the decode steps after
+    it stay within BF16 noise of the textbook, and a planted key-head mistake
+    in the textbook is detected."""
+    cfg = cc.preset(name)
+    tokens = np.random.default_rng(4).integers(0, cfg["vocab"], 12).tolist()
+    w, batched, s = run_oracle(oracle, cfg, 7, tokens, 3, multi=True)
+    tl = textbook_logits(cfg, w, tokens, 3, batched)
+    assert discrepancy(batched, tl) < 0.15
+    r = cfg["value_heads"] // cfg["key_heads"]
+    bad = textbook_logits(cfg, w, tokens, 3, batched, key_head=lambda h, KH, VH: h // r)
+    assert discrepancy(batched, bad) > 0.6
+
+
+def test_batched_prefill_differs_from_token_fold_only_by_order(oracle):
+    """The batched path's B256 projections round differently from the decode
+    S256/S32 ones, so a batched prompt and the same prompt appended token by
+    token agree to BF16 noise but not bit for bit."""
+    cfg = cc.preset("mini-moe")
+    tokens = np.random.default_rng(8).integers(0, cfg["vocab"], 10).tolist()
+    _, batched, sb = run_oracle(oracle, cfg, 3, tokens, 0, multi=True)
+    _, single, ss = run_oracle(oracle, cfg, 3, tokens, 0, multi=False)
+    fb = oracle.bf16_to_f32(batched[0]).astype(np.float64)
+    fs = oracle.bf16_to_f32(single[0]).astype(np.float64)
+    rel = float(np.sqrt(np.mean((fb - fs) ** 2)) / np.std(fs))
+    assert 0 < rel < 0.1, rel
