@@ -59,6 +59,23 @@ __device__ __forceinline__ void quad_acc(Quad& a, const u32x4& x, const u32x4& w
   a.lo[3] += lo2f(x.w) * lo2f(w.w); a.hi[3] += hi2f(x.w) * hi2f(w.w);
 }
 
+// The same products with the input quad already unpacked to F32 (an input
+// reused across rows is then unpacked once, not once per row).
+__device__ __forceinline__ void quad_acc_f(Quad& a, const float (&xl)[4], const float (&xh)[4],
+                                           const u32x4& w) {
+  a.lo[0] += xl[0] * lo2f(w.x); a.hi[0] += xh[0] * hi2f(w.x);
+  a.lo[1] += xl[1] * lo2f(w.y); a.hi[1] += xh[1] * hi2f(w.y);
+  a.lo[2] += xl[2] * lo2f(w.z); a.hi[2] += xh[2] * hi2f(w.z);
+  a.lo[3] += xl[3] * lo2f(w.w); a.hi[3] += xh[3] * hi2f(w.w);
+}
+
+__device__ __forceinline__ void quad_unpack(const u32x4& x, float (&xl)[4], float (&xh)[4]) {
+  xl[0] = lo2f(x.x); xh[0] = hi2f(x.x);
+  xl[1] = lo2f(x.y); xh[1] = hi2f(x.y);
+  xl[2] = lo2f(x.z); xh[2] = hi2f(x.z);
+  xl[3] = lo2f(x.w); xh[3] = hi2f(x.w);
+}
+
 // Value of lane i + S as seen from lane i, for the lanes a tree level uses:
 // S <= 8 within a 16-lane row (DPP row shift; lanes past the row end read
 // +0 and are never used), S = 16 for rows 0 and 2 (permlane16 swap), S = 32

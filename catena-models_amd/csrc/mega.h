@@ -473,6 +473,13 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
   norm_weights<S>(m, Ly.in_norm, w0, w1);
   load_hidden<S>(m, Ly.x_h, m.xr, l == 0);
   norm_row<S>(m, m.xr, w0, w1, m.a.eps);
+  // this lane's input quads, unpacked once for all its rows
+  float xl[NQ][4], xh[NQ][4];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const u32x4 xq = (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) ? m.xn[m.lane + 64 * j] : u32x4{0u, 0u, 0u, 0u};
+    quad_unpack(xq, xl[j], xh[j]);
+  }
 #pragma unroll
   for (int k = 0; k < kPairsA; ++k) {
     const int p = m.gw + m.nw * k;
@@ -484,7 +491,7 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
         quad_zero(acc);
 #pragma unroll
         for (int j = 0; j < NQ; ++j)
-          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], r.w[k][rr][j]);
+          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc, xl[j], xh[j], r.w[k][rr][j]);
         v[rr] = quad_tree<64>(acc);
       }
       if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
@@ -707,26 +714,27 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
 // -------------------------------- phase: output projection + residual (S64)
 
 // bf16(bf16(tree64(x . w_r)) (+) residual_r) (qwen3.fused.residual,
-// simt.hex:442-538) over the polled mixer output (COLS BF16): 16 lanes per
-// row (lane q holds reference lanes 4q..4q+3, one 16-byte load per chunk of
-// 64 pairs), four rows per wave, waves 0 and 1 of every block. Blocks kh < KH
-// of a linear layer also write the q and k conv history of key head kh.
+// simt.hex:442-538) over the polled mixer output (COLS BF16): one row per
+// wave and all waves of every block; physical lane = reference lane l, which
+// visits pairs l, l+64, ... (one dword each, 256 contiguous bytes per wave),
+// then the 64-lane tree. Waves 2i and 2i+1 take rows 2p and 2p+1,
+// p = block + grid * i, and the even wave stores the word. Blocks kh < KH of a
+// linear layer also write the q and k conv history of key head kh.
 template <class S, int COLS>
 __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  constexpr int NP = COLS / 2, QP = NP / 4, NJ = QP / 16;
-  static_assert(QP % 16 == 0, "output projection width");
-  const int q = m.lane & 15, g = m.lane >> 4;
-  const int rq = m.bid + m.grid * m.wave;  // row quad of this wave
-  const bool has_rows = m.wave < 2 && rq < S::H / 4;
-  u32x4 wv[NJ];
-  if (has_rows) {
-    const uint16_t* w = Ly.out_w + (size_t)(4 * rq) * COLS;
-    const uint32_t off = (uint32_t)g * (uint32_t)COLS * 2u + (uint32_t)q * 16u;
+  constexpr int NP = COLS / 2, NJ = NP / 64;
+  static_assert(NP % 64 == 0, "output projection width");
+  const int p = m.bid + m.grid * (m.wave >> 1);
+  const int row = 2 * p + (m.wave & 1);
+  const bool has_row = p < S::H / 2;
+  uint32_t wv[NJ];
+  if (has_row) {
+    const uint16_t* w = Ly.out_w + (size_t)row * COLS;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) wv[j] = ldq_at(w, off + (uint32_t)j * 256u);
+    for (int j = 0; j < NJ; ++j) wv[j] = ldd_at(w, (uint32_t)(m.lane + 64 * j) * 4u);
   }
   poll_words<(NP + kMT - 1) / kMT>(m, NP, Span{Ly.x_mix}, m.vec);
   if (!Ly.full && m.bid < S::KH) {
@@ -740,19 +748,20 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
       G(a.cache)[Ly.conv_base + slot + ch] = d->raw_qk[m.tid];
     }
   }
-  if (has_rows) {
-    const u32x4* xq = reinterpret_cast<const u32x4*>(m.vec);
-    Quad acc;
-    quad_zero(acc);
+  uint16_t o = 0;
+  if (has_row) {
+    float lo = 0.0f, hi = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) quad_acc(acc, xq[q + 16 * j], wv[j]);
-    const float v = quad_tree<16>(acc);
-    const int row = 4 * rq + g;
-    const uint16_t o = bf_add(f2bf(v), m.xr[row]);
-    const uint16_t other = (uint16_t)__shfl_down((int)o, 16, 64);
-    if (m.lane == 0 || m.lane == 32) word_store(Ly.x_attn + 2 * rq + (m.lane >> 5), pack_bf(o, other), m.tag);
+    for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[m.lane + 64 * j], wv[j]);
+    const float v = tree64_lanes(lo + hi);
+    o = bf_add(f2bf(v), m.xr[row]);
+    if (m.lane == 0 && (m.wave & 1)) m.misc->red[4 + (m.wave >> 1)] = __builtin_bit_cast(float, (uint32_t)o);
   }
   __syncthreads();
+  if (has_row && m.lane == 0 && !(m.wave & 1)) {
+    const uint16_t other = (uint16_t)__builtin_bit_cast(uint32_t, m.misc->red[4 + (m.wave >> 1)]);
+    word_store(Ly.x_attn + p, pack_bf(o, other), m.tag);
+  }
 }
 
 // ----------------------------------------------- phase: MoE router (S32 F32)
@@ -811,6 +820,12 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
     if (m.lane == 0) word_store(Ly.x_router + m.gw, fbits(v), m.tag);
   } else if (shared_wave) {
     uint16_t t[2];
+    float xl[NQ][4], xh[NQ][4];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const u32x4 xq = (QH % 64 == 0 || m.lane + 64 * j < QH) ? m.xn[m.lane + 64 * j] : u32x4{0u, 0u, 0u, 0u};
+      quad_unpack(xq, xl[j], xh[j]);
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       Quad ga, ua;
@@ -819,9 +834,8 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
 #pragma unroll
       for (int j = 0; j < NQ; ++j)
         if (QH % 64 == 0 || m.lane + 64 * j < QH) {
-          const u32x4 xq = m.xn[m.lane + 64 * j];
-          quad_acc(ga, xq, gv[r][j]);
-          quad_acc(ua, xq, uv[r][j]);
+          quad_acc_f(ga, xl[j], xh[j], gv[r][j]);
+          quad_acc_f(ua, xl[j], xh[j], uv[r][j]);
         }
       const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
       t[r] = f2bf(rbf(silu(gb)) * ub);
@@ -1005,6 +1019,12 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
   issue_down<S>(m, Ly);
   if (has_pair) {
     uint16_t y[2];
+    float xl[NQ][4], xh[NQ][4];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const u32x4 xq = (QH % 64 == 0 || m.lane + 64 * j < QH) ? m.xn[m.lane + 64 * j] : u32x4{0u, 0u, 0u, 0u};
+      quad_unpack(xq, xl[j], xh[j]);
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       Quad ga, ua;
@@ -1013,9 +1033,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
 #pragma unroll
       for (int j = 0; j < NQ; ++j)
         if (QH % 64 == 0 || m.lane + 64 * j < QH) {
-          const u32x4 xq = m.xn[m.lane + 64 * j];
-          quad_acc(ga, xq, gv[r][j]);
-          quad_acc(ua, xq, uv[r][j]);
+          quad_acc_f(ga, xl[j], xh[j], gv[r][j]);
+          quad_acc_f(ua, xl[j], xh[j], uv[r][j]);
         }
       const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
       y[r] = f2bf((silu(gb) * ub) * m.misc->probs[(2 * p + r) / S::I]);
@@ -1032,7 +1051,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
 // lane (lanes 0-31 row A, lanes 32-63 row B) reading the staged weights;
 // out = bf16(bf16(routed + residual) (+) bf16(shared)). The shared
 // activations are completed here: bf16(t * sigmoid(shared logit)). Once its
-// inputs are in, the block issues the next layer's first projection weights.
+// outputs are stored, the block issues the next layer's first projection
+// weights.
 template <class S>
 __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly,
                                            const MegaLayer* next, ProjRegs<S>& pr) {
@@ -1048,20 +1068,6 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
       m, RP + SP + 1, [&](int i) { return i < RP ? act + i : i < RP + SP ? shr + (i - RP) : lge; }, m.vec);
   // the staged weights were issued before the poll: complete in issue order
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  // the next layer's first projection pairs: issued after the poll (a wave's
-  // loads complete in issue order), so they stream during this phase's
-  // compute and the next exchange without delaying the inputs above
-  if (next) {
-    issue_project<S, 0, kPairsEarly>(pa, next, pr);
-  } else {
-    // defined on every path, so the registers are not carried across phases
-#pragma unroll
-    for (int k = 0; k < kPairsEarly; ++k)
-#pragma unroll
-      for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int j = 0; j < S::NQA; ++j) pr.w[k][rr][j] = u32x4{0u, 0u, 0u, 0u};
-  }
   if (m.tid < SP) {
     const float gate = sigmoid(bitsf(m.vec[RP + SP]));
     const uint32_t t = m.vec[RP + m.tid];
@@ -1087,6 +1093,20 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
     const uint16_t out = bf_add(f2bf(routed_v + bf2f(m.xa[row])), f2bf(shared_v));
     const uint16_t other = (uint16_t)__shfl_down((int)out, 32, 64);
     if (m.lane == 0) word_store(Ly.x_out + prow, pack_bf(out, other), m.tag);
+  }
+  // the next layer's first projection pairs, once this block's outputs are
+  // out (issuing them earlier stalls the compute above behind the memory
+  // queue): they stream during the next exchange
+  if (next) {
+    issue_project<S, 0, kPairsEarly>(pa, next, pr);
+  } else {
+    // defined on every path, so the registers are not carried across phases
+#pragma unroll
+    for (int k = 0; k < kPairsEarly; ++k)
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+        for (int j = 0; j < S::NQA; ++j) pr.w[k][rr][j] = u32x4{0u, 0u, 0u, 0u};
   }
   __syncthreads();
 }
