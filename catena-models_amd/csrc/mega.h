@@ -564,10 +564,13 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   }
   const float dt = G(Ly.dt)[h], aa = G(Ly.a)[h];
   const float gw = m.tid < VD ? G(Ly.gnorm)[m.tid] : 0.0f;
-  // alpha (wave 0) and beta (wave 1) rows of head h
+  // alpha (wave kMW - 2) and beta (wave kMW - 1) rows of head h, on the
+  // waves that have no convolution channel
+  static_assert(NCH <= kMT - 128, "alpha/beta waves");
+  constexpr int kAB = kMW - 2;
   u32x4 abw[S::NQA];
-  if (m.wave < 2) {
-    const uint16_t* w = (m.wave == 0 ? Ly.alpha_w : Ly.beta_w) + (size_t)h * S::H;
+  if (m.wave >= kAB) {
+    const uint16_t* w = (m.wave == kAB ? Ly.alpha_w : Ly.beta_w) + (size_t)h * S::H;
 #pragma unroll
     for (int j = 0; j < S::NQA; ++j) abw[j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
   }
@@ -583,14 +586,14 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     return proj + ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
   };
   poll_words<(nwords + kMT - 1) / kMT>(m, nwords, addr, m.vec);
-  if (m.wave < 2) {
+  if (m.wave >= kAB) {
     Quad acc;
     quad_zero(acc);
 #pragma unroll
     for (int j = 0; j < S::NQA; ++j)
       if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc(acc, m.xn[m.lane + 64 * j], abw[j]);
     const float v = quad_tree<64>(acc);
-    if (m.lane == 0) d->ab[m.wave] = f2bf(v);
+    if (m.lane == 0) d->ab[m.wave - kAB] = f2bf(v);
   }
   const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
   // convolution (linear_prepare.hex:2-64)
@@ -849,66 +852,73 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
 // Every block ranks the experts itself (moe.hex:86-252). The reference's
 // rank is rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}, ids[rank] = e
 // for rank < K. Without NaNs this is the descending order with ties to the
-// lower index, so wave 0 takes K rounds of a wave-wide maximum of
-// (ordered value, lowest index) keys; with a NaN the formula is evaluated
+// lower index, so wave 0 takes K rounds: the wave-wide maximum of the
+// order-preserving integer images of the logits (+0 and -0 equal), then the
+// lowest expert index holding it (ballots over the lanes' candidate groups,
+// lane l holding experts l + 64c). With a NaN the formula is evaluated
 // directly. Then p_j = exp(l_j - l_0) / den with den summed left to right.
-__device__ __forceinline__ unsigned long long key_max(unsigned long long a, unsigned long long b) {
-  return a > b ? a : b;
+__device__ __forceinline__ uint32_t logit_order(float le) {
+  const uint32_t u = le == 0.0f ? 0u : fbits(le);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // >= 0x00800000 for non-NaN
 }
-// Value of lane i + S for a 64-bit key (the halving-tree shifts of lane_down).
+
 template <int S>
-__device__ __forceinline__ unsigned long long key_down(unsigned long long v) {
-  const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  const uint32_t l2 = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, lo)));
-  const uint32_t h2 = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, hi)));
-  return ((unsigned long long)h2 << 32) | l2;
+__device__ __forceinline__ uint32_t umax_down(uint32_t v) {
+  const uint32_t o = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, v)));
+  return o > v ? o : v;
 }
 
 template <class S>
 __device__ __forceinline__ void select_experts(const Mega& m) {
   MegaMisc* s = m.misc;
-  static_assert(S::E <= 64 * 64, "expert count");
+  static_assert(S::E <= 64 * 64 && S::K <= 64, "expert count");
   constexpr int PER = (S::E + 63) / 64;  // candidates per lane
   if (m.wave == 0) {
-    // keys of this lane's experts e = lane + 64c; NaN -> fallback
-    unsigned long long key[PER];
+    uint32_t ov[PER];  // 0: absent or taken (below every non-NaN image)
     bool nan = false;
 #pragma unroll
     for (int c = 0; c < PER; ++c) {
       const int e = m.lane + 64 * c;
-      key[c] = 0ull;
+      ov[c] = 0u;
       if (e < S::E) {
         const float le = s->logits[e];
         nan |= le != le;
-        const uint32_t u = le == 0.0f ? 0u : fbits(le);
-        const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-        key[c] = ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
+        ov[c] = logit_order(le);
       }
     }
     const bool any_nan = __any(nan);
     if (!any_nan) {
       for (int k = 0; k < S::K; ++k) {
-        unsigned long long best = key[0];
+        uint32_t best = ov[0];
 #pragma unroll
-        for (int c = 1; c < PER; ++c) best = key_max(best, key[c]);
-        best = key_max(best, key_down<32>(best));
-        best = key_max(best, key_down<16>(best));
-        best = key_max(best, key_down<8>(best));
-        best = key_max(best, key_down<4>(best));
-        best = key_max(best, key_down<2>(best));
-        best = key_max(best, key_down<1>(best));
-        const uint32_t blo = __builtin_amdgcn_readfirstlane((uint32_t)best);
-        const uint32_t bhi = __builtin_amdgcn_readfirstlane((uint32_t)(best >> 32));
-        const unsigned long long win = ((unsigned long long)bhi << 32) | blo;
-        const int e = (int)(0xffffffffu - blo);
+        for (int c = 1; c < PER; ++c) best = ov[c] > best ? ov[c] : best;
+        best = umax_down<32>(best);
+        best = umax_down<16>(best);
+        best = umax_down<8>(best);
+        best = umax_down<4>(best);
+        best = umax_down<2>(best);
+        best = umax_down<1>(best);
+        const uint32_t win = __builtin_amdgcn_readfirstlane(best);
+        int e = S::E;
+#pragma unroll
+        for (int c = PER - 1; c >= 0; --c) {
+          const unsigned long long hit = __ballot(ov[c] == win);
+          if (hit) e = 64 * c + __builtin_ctzll(hit);
+        }
 #pragma unroll
         for (int c = 0; c < PER; ++c)
-          if (key[c] == win) key[c] = 0ull;  // taken
-        if (m.lane == 0) {
-          s->ids[k] = e;
-          s->chosen[k] = s->logits[e];
-        }
+          if (64 * c + m.lane == e) ov[c] = 0u;  // taken
+        if (m.lane == 0) s->ids[k] = e;
       }
+      // probabilities right here: lane j < K holds l_j
+      const float lj = m.lane < S::K ? s->logits[s->ids[m.lane]] : 0.0f;
+      const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lj)));
+      const float ex = m.lane < S::K ? hexp(lj - l0) : 0.0f;
+      float den = 0.0f;
+#pragma unroll
+      for (int j = 0; j < S::K; ++j)
+        den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j));
+      if (m.lane < S::K) s->probs[m.lane] = ex / den;
     }
     if (m.lane == 0) s->any_nan = any_nan ? 1 : 0;
   }
@@ -927,14 +937,14 @@ __device__ __forceinline__ void select_experts(const Mega& m) {
       }
     }
     __syncthreads();
+    if (m.wave == 0) {
+      const float ex = m.lane < S::K ? hexp(s->chosen[m.lane] - s->chosen[0]) : 0.0f;
+      float den = 0.0f;
+      for (int j = 0; j < S::K; ++j) den = den + __shfl(ex, j, 64);
+      if (m.lane < S::K) s->probs[m.lane] = ex / den;
+    }
+    __syncthreads();
   }
-  if (m.wave == 0) {
-    const float ex = m.lane < S::K ? hexp(s->chosen[m.lane] - s->chosen[0]) : 0.0f;
-    float den = 0.0f;
-    for (int j = 0; j < S::K; ++j) den = den + __shfl(ex, j, 64);
-    if (m.lane < S::K) s->probs[m.lane] = ex / den;
-  }
-  __syncthreads();
 }
 
 // Down-projection weights, staged in LDS by DMA (global_load_lds, 16 bytes
