@@ -1026,7 +1026,6 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
       }
     }
   }
-  issue_down<S>(m, Ly);
   if (has_pair) {
     uint16_t y[2];
     float xl[NQ][4], xh[NQ][4];
@@ -1051,6 +1050,10 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
     }
     if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
   }
+  // the down-projection rows of the selected experts, once this wave's
+  // outputs are out (issued earlier, they hold the compute above behind the
+  // memory queue); they land during the exchange into the down phase
+  issue_down<S>(m, Ly);
 }
 
 // ------------------------------------------ phase: MoE down + residual (S32)
