@@ -771,10 +771,12 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
 
 // Every block normalises the post-mixer row (post_attention_norm) into m.xn
 // for the router and the gate/up phase and keeps the raw row for the FFN
-// residual. Waves gw <= E compute router row gw (moe.hex:4-84): physical lane
-// 2r + h runs reference lane r's low (h = 0) or high (h = 1) accumulator over
-// floats 64k + lane. Waves E+1 .. E+SI/2 compute the shared expert's gate/up
-// row pairs (dual S256, moe.hex:254-333) up to the routing-dependent factor:
+// residual. Even waves 2i compute router row block + grid * i (rows
+// [0, E] spread one per block; moe.hex:4-84): physical lane 2r + h runs
+// reference lane r's low (h = 0) or high (h = 1) accumulator over floats
+// 64k + lane. Odd waves 2i+1 compute the shared expert's gate/up row pair
+// block + grid * i (dual S256, moe.hex:254-333) up to the routing-dependent
+// factor:
 // t = bf16(bf16(silu(bf16 g)) * bf16 u); the down phase applies
 // bf16(t * sigmoid(shared logit)), the same roundings as the reference.
 template <class S>
@@ -784,11 +786,13 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
   constexpr int H = S::H, QH = S::QH, NQ = S::NQA, ROWS = S::E + 1, NJ = (H + 63) / 64;
   float wv[NJ];
   u32x4 gv[2][NQ], uv[2][NQ];
-  const bool router_wave = m.gw < ROWS;
-  const int sp = m.gw - ROWS;  // shared pair of this wave
-  const bool shared_wave = sp >= 0 && sp < S::SI / 2;
+  const int slot = m.bid + m.grid * (m.wave >> 1);
+  const int rrow = slot;  // router row of an even wave
+  const int sp = slot;    // shared pair of an odd wave
+  const bool router_wave = !(m.wave & 1) && rrow < ROWS;
+  const bool shared_wave = (m.wave & 1) && sp < S::SI / 2;
   if (router_wave) {
-    const float* w = m.gw < S::E ? Ly.router + (size_t)m.gw * H : Ly.shared_gate;
+    const float* w = rrow < S::E ? Ly.router + (size_t)rrow * H : Ly.shared_gate;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) wv[j] = ldf_at(w, (uint32_t)min(64 * j + m.lane, H - 1) * 4u);
   } else if (shared_wave) {
@@ -820,7 +824,7 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
     v += lane_down<8>(v);
     v += lane_down<4>(v);
     v += lane_down<2>(v);
-    if (m.lane == 0) word_store(Ly.x_router + m.gw, fbits(v), m.tag);
+    if (m.lane == 0) word_store(Ly.x_router + rrow, fbits(v), m.tag);
   } else if (shared_wave) {
     uint16_t t[2];
     float xl[NQ][4], xh[NQ][4];

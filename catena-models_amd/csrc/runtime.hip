@@ -527,7 +527,8 @@ bool grid_fits(int grid, int64_t cap) {
   const int64_t rows_lin = S::QKV + S::VS, rows_full = 2LL * S::QS + 2LL * S::KVS;
   return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw && S::H / 2 <= (int64_t)(kMW / 2) * grid &&
          S::H / 2 <= (int64_t)DownLayout<S>::WAVES * grid &&
-         S::K * S::I / 2 <= nw && S::E + 1 + S::SI / 2 <= nw && S::H / 2 <= nw &&
+         S::K * S::I / 2 <= nw && S::E + 1 <= (int64_t)(kMW / 2) * grid &&
+         S::SI / 2 <= (int64_t)(kMW / 2) * grid && S::H / 2 <= nw &&
          (cap + 7) / 8 <= kValueMxMax;
 }
 
