@@ -1136,8 +1136,7 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
 // (lane l owns channels l, l+32, ..., serial from 0.0, then a 32-wide
 // halving tree) for every query head of the group, x 1/sqrt(HD)
 // (online.hex:4-18). The block that scores the new position writes K and V
-// of that position into the cache; V is device-coherent and complete before
-// that position's scores are published.
+// of that position into the cache for later steps.
 struct ScoreLds {
   float rope[256];
   float normed[kMW][256];
@@ -1251,7 +1250,7 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
     t = t + lane_down<8>(t);
     t = t + lane_down<16>(t);
     t = t + lane_down<32>(t);
-    const float sum = __shfl(t, 0, 64);
+    const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
     if (hh < Q + KVH) {
       const float inverse = 1.0f / nsqrt(sum / (float)HD + a.eps);
 #pragma unroll
@@ -1289,16 +1288,16 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
     if (key == position) {
 #pragma unroll
       for (int j = 0; j < KJ; ++j) kv[j] = bf2f(s->khat[kvh * HD + l32 + 32 * j]);
-      // K and V of the new position into the cache (V device-coherent)
+      // K and V of the new position into the cache, for later steps (this
+      // step's values phase takes V from the projection words)
       uint16_t* kdst = a.cache + Ly.key_base + position * S::KVS + (int64_t)kvh * HD;
       uint16_t* vdst = a.cache + Ly.value_base + position * S::KVS + (int64_t)kvh * HD;
 #pragma unroll
       for (int j = 0; j < KJ; ++j) {
         const int c = l32 + 32 * j;
         G(kdst)[c] = s->khat[kvh * HD + c];
-        __hip_atomic_store(G(vdst) + c, vraw[kvh * HD + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        G(vdst)[c] = vraw[kvh * HD + c];
       }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     } else if (round == 0) {
 #pragma unroll
       for (int j = 0; j < KJ; ++j) kv[j] = kv0[j];
@@ -1314,8 +1313,7 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < KJ; ++j) acc += bf2f(qh[32 * j]) * kv[j];
-#pragma unroll
-      for (int sh = 16; sh >= 1; sh >>= 1) acc += __shfl_down(acc, sh, 32);
+      acc = tree32_lanes(acc);  // halving strides 16 .. 1 in each half wave
       if (l32 == 0) word_store(Ly.x_scores + (size_t)head * a.cap + key, fbits(acc * a.attn_scale), m.tag);
     }
   }
@@ -1334,7 +1332,9 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
 //  - then each channel's chain acc = acc * alpha_t + prod_0 + ... + prod_7 in
 //    order (lanes 0-15), with lane 16 running den = den * alpha_t + p_0 + ...;
 // out = bf16(bf16(acc / den) * sigmoid(gate)). Invalid keys of the last tile
-// contribute p = 0 against key 0's value, as in the reference.
+// contribute p = 0 against key 0's value, as in the reference. The new
+// position's V comes from the projection words (the cache copy is written by
+// the scores phase for later steps).
 constexpr int kMegaValueChunk = 256;  // keys per chunk
 constexpr int kValuePre = 4;          // chunks whose V rows and scores are fetched up front
 struct ValueLds {
@@ -1344,7 +1344,10 @@ struct ValueLds {
   float sc[kValuePre * kMegaValueChunk];  // scores of the first chunks
   float mx[1];  // tile maxima, then running maxima (the rest of the big area)
 };
-constexpr int kValueMxMax = (kLdsBigBytes - (int)offsetof(ValueLds, mx)) / 4;
+// Tile maxima the big LDS area of shape S holds (it is sized for the MoE
+// down staging as well).
+template <class S>
+constexpr int value_mx_max();
 
 template <class S>
 __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
@@ -1364,17 +1367,13 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   for (int item = m.bid; item < ITEMS; item += m.grid) {
     const int head = item / CHUNKS, c0 = (item - head * CHUNKS) * kValueChannels;
     const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0;
-    // V quad of key k (key 0 past the end; the new position device-coherently)
+    // V quad of key k (key 0 past the end); the new position's quad comes
+    // from the projection words polled into LDS
     auto load_v = [&](int64_t k) -> u32x4 {
       const int64_t safe = k < keys ? k : 0;
-      const uint16_t* src = vbase + safe * S::KVS + 8 * vh;
-      if (safe != position) return G(reinterpret_cast<const u32x4*>(src))[0];
-      const uint64_t lo = __hip_atomic_load(G(reinterpret_cast<const uint64_t*>(src)), __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-      const uint64_t hi = __hip_atomic_load(G(reinterpret_cast<const uint64_t*>(src)) + 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-      return u32x4{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+      return G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
     };
+    const uint64_t* vwords = Ly.x_proj + (S::QS + S::KVS / 2 + ((head / HPK * HD + c0) >> 1));
     // prefetch the first chunks' V rows (positions before the new one)
     u32x4 vq[kValuePre];
 #pragma unroll
@@ -1415,11 +1414,19 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
       }
       s->mx[t] = mt;
     }
-    // gate of this item's channels (word pairs)
+    // gate of this item's channels and the new position's V (word pairs)
     uint32_t gate_word = 0;
     if (m.tid < kValueChannels / 2)
       gate_word = poll_one(m, Ly.x_proj + ((head * 2 * HD + HD + c0) >> 1) + m.tid);
+    else if (m.tid < kValueChannels)
+      reinterpret_cast<uint32_t*>(s->alpha)[m.tid - kValueChannels / 2] =
+          poll_one(m, vwords + (m.tid - kValueChannels / 2));
     __syncthreads();
+    u32x4 vnew;
+    {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(s->alpha) + 4 * vh;
+      vnew = u32x4{w[0], w[1], w[2], w[3]};
+    }
     if (m.wave == 0) {
       // running maximum: serial within a lane's segment, then an inclusive
       // scan of the segment maxima across the wave
@@ -1454,7 +1461,8 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
         s->alpha[m.tid] = hexp((tile > 0 ? s->mx[tile - 1] : ninf) - s->mx[tile]);
       }
       u32x4 vcur = chunk == 0 ? vq[0] : chunk == 1 ? vq[1 % kValuePre] : chunk == 2 ? vq[2 % kValuePre] : vq[3 % kValuePre];
-      if (vk < n && (chunk >= kValuePre || k0 + vk == position)) vcur = load_v(k0 + vk);
+      if (k0 + vk == position) vcur = vnew;
+      else if (vk < n && chunk >= kValuePre) vcur = load_v(k0 + vk);
       __syncthreads();
       if (vk < n) {
         const float pk = s->p[vk];
@@ -1587,8 +1595,16 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
 // Dynamic LDS of the step for shape S: the big area must also hold the
 // down-projection staging.
 template <class S>
+constexpr int mega_big_bytes() {
+  return DownLayout<S>::BYTES > kLdsBigBytes ? DownLayout<S>::BYTES : kLdsBigBytes;
+}
+template <class S>
 constexpr int mega_lds_bytes() {
-  return kLdsBig + (DownLayout<S>::BYTES > kLdsBigBytes ? DownLayout<S>::BYTES : kLdsBigBytes);
+  return kLdsBig + mega_big_bytes<S>();
+}
+template <class S>
+constexpr int value_mx_max() {
+  return (mega_big_bytes<S>() - (int)offsetof(ValueLds, mx)) / 4;
 }
 
 template <class S>

@@ -529,7 +529,7 @@ bool grid_fits(int grid, int64_t cap) {
          S::H / 2 <= (int64_t)DownLayout<S>::WAVES * grid &&
          S::K * S::I / 2 <= nw && S::E + 1 <= (int64_t)(kMW / 2) * grid &&
          S::SI / 2 <= (int64_t)(kMW / 2) * grid && S::H / 2 <= nw &&
-         (cap + 7) / 8 <= kValueMxMax;
+         (cap + 7) / 8 <= value_mx_max<S>();
 }
 
 int mega_kind(const cq35_config& c, int grid, int64_t cap) {
