@@ -1330,7 +1330,8 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
 //  - every product p_k * v_{k,c} in parallel (each rounds on its own in the
 //    reference too: contraction is off);
 //  - then each channel's chain acc = acc * alpha_t + prod_0 + ... + prod_7 in
-//    order (lanes 0-15), with lane 16 running den = den * alpha_t + p_0 + ...;
+//    order (wave 0, lanes 0-15), with wave 1 running den = den * alpha_t +
+//    p_0 + ... beside them;
 // out = bf16(bf16(acc / den) * sigmoid(gate)). Invalid keys of the last tile
 // contribute p = 0 against key 0's value, as in the reference. The new
 // position's V comes from the projection words (the cache copy is written by
@@ -1340,7 +1341,7 @@ constexpr int kValuePre = 4;          // chunks whose V rows and scores are fetc
 struct ValueLds {
   float p[kMegaValueChunk];
   float alpha[kMegaValueChunk / 8];
-  float prod[kMegaValueChunk * kValueChannels];
+  float prod[kValueChannels * kMegaValueChunk];  // [channel][key]
   float sc[kValuePre * kMegaValueChunk];  // scores of the first chunks
   float mx[1];  // tile maxima, then running maxima (the rest of the big area)
 };
@@ -1471,25 +1472,28 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
         o0.z = pk * lo2f(vcur.y); o0.w = pk * hi2f(vcur.y);
         o1.x = pk * lo2f(vcur.z); o1.y = pk * hi2f(vcur.z);
         o1.z = pk * lo2f(vcur.w); o1.w = pk * hi2f(vcur.w);
-        f32x4* dst = reinterpret_cast<f32x4*>(s->prod + vk * kValueChannels + 8 * vh);
-        dst[0] = o0;
-        dst[1] = o1;
+        float* dst = s->prod + (8 * vh) * kMegaValueChunk + vk;
+        dst[0 * kMegaValueChunk] = o0.x; dst[1 * kMegaValueChunk] = o0.y;
+        dst[2 * kMegaValueChunk] = o0.z; dst[3 * kMegaValueChunk] = o0.w;
+        dst[4 * kMegaValueChunk] = o1.x; dst[5 * kMegaValueChunk] = o1.y;
+        dst[6 * kMegaValueChunk] = o1.z; dst[7 * kMegaValueChunk] = o1.w;
       }
       __syncthreads();
       if (m.wave == 0) {
         if (m.lane < kValueChannels) {
-          const float* pr = s->prod + m.lane;
-#pragma unroll 2
+          const f32x4* pr = reinterpret_cast<const f32x4*>(s->prod + m.lane * kMegaValueChunk);
+#pragma unroll 4
           for (int i = 0; i < n / 8; ++i) {
-            float x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = pr[(i * 8 + j) * kValueChannels];
+            const f32x4 x0 = pr[2 * i], x1 = pr[2 * i + 1];
             acc = acc * s->alpha[i];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc = acc + x[j];
+            acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
+            acc = acc + x1.x; acc = acc + x1.y; acc = acc + x1.z; acc = acc + x1.w;
           }
-        } else if (m.lane == kValueChannels) {
-#pragma unroll 2
+        }
+      } else if (m.wave == 1) {
+        // the denominator chain beside the channel chains (its own SIMD)
+        if (m.lane == 0) {
+#pragma unroll 4
           for (int i = 0; i < n / 8; ++i) {
             const f32x4 p0 = reinterpret_cast<const f32x4*>(s->p)[2 * i];
             const f32x4 p1 = reinterpret_cast<const f32x4*>(s->p)[2 * i + 1];
@@ -1501,8 +1505,10 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
       }
       __syncthreads();
     }
+    if (m.wave == 1 && m.lane == 0) s->alpha[0] = den;  // the chunks are done with alpha
+    __syncthreads();
     if (m.wave == 0) {
-      den = __shfl(den, kValueChannels, 64);
+      den = s->alpha[0];
       const uint32_t gw = __shfl((int)gate_word, m.lane >> 1, 64);
       const uint16_t gb = (m.lane & 1) ? (uint16_t)(gw >> 16) : (uint16_t)(gw & 0xffffu);
       uint16_t y = 0;
