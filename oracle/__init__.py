@@ -205,6 +205,14 @@ class Session:
         n = lib().ox_cache_elements(ctypes.byref(self.model._c), self.capacity)
         return np.ctypeslib.as_array(lib().ox_session_cache(self._h), shape=(n,)).copy()
 
+    def import_cache(self, data: np.ndarray) -> None:
+        """Overwrite the BF16 session state (same layout as ``cache()``)."""
+        n = lib().ox_cache_elements(ctypes.byref(self.model._c), self.capacity)
+        src = np.ascontiguousarray(data, dtype=np.uint16).reshape(-1)
+        if src.size != n:
+            raise ValueError(f"state has {src.size} elements, expected {n}")
+        np.ctypeslib.as_array(lib().ox_session_cache(self._h), shape=(n,))[:] = src
+
     def last_ids(self) -> np.ndarray:
         c = self.model.cfg
         n = c["layers"] * max(c["top_k"], 1)
