@@ -169,6 +169,66 @@ def cpu_baseline(cfg, seed, prompt_len, max_steps, budget_s, gpu_model, threads)
                 logits_equal=equal_logits)
 
 
+def seeded_state(cfg: dict, capacity: int, position: int, seed: int):
+    """BF16 session state of the long-context configuration: key and value
+    rows of positions < `position` ~ N(0,1) x 0.1, conv history ~ N(0,1) x 0.1
+    and DeltaNet recurrent state ~ N(0,1), seeded; generated on the host
+    (torch's CPU generator, so no second GPU runtime joins the process).
+    Layout (src/spec.rs:321-362): [layer][key|value][capacity][kv_heads*head_dim],
+    then per layer [conv history | recurrent state]."""
+    import numpy as np
+    import torch
+    kvs = cfg["kv_heads"] * cfg["head_dim"]
+    ks, vs = cfg["key_heads"] * cfg["key_dim"], cfg["value_heads"] * cfg["value_dim"]
+    conv = 3 * (2 * ks + vs)
+    lin = conv + vs * cfg["key_dim"]
+    kv = capacity * cfg["layers"] * 2 * kvs
+    g = torch.Generator()
+    g.manual_seed(seed)
+    out = torch.zeros(kv + cfg["layers"] * lin, dtype=torch.bfloat16)
+    rows = out[:kv].view(cfg["layers"] * 2, capacity, kvs)
+    for r in range(cfg["layers"] * 2):
+        rows[r, :position] = (torch.randn(position, kvs, generator=g) * 0.1).to(torch.bfloat16)
+    tail = out[kv:].view(cfg["layers"], lin)
+    tail[:, :conv] = (torch.randn(cfg["layers"], conv, generator=g) * 0.1).to(torch.bfloat16)
+    tail[:, conv:] = torch.randn(cfg["layers"], lin - conv, generator=g).to(torch.bfloat16)
+    return out.view(torch.int16).numpy().view(np.uint16)
+
+
+def long_context_decode(model, cfg: dict, context: int, steps: int, seed: int) -> dict:
+    """Batch-1 greedy decode from a seeded state holding `context` cached
+    positions (the long-context configuration's per-session work)."""
+    import cq35
+    warm = 2
+    capacity = context + warm + steps
+    t0 = time.time()
+    state = seeded_state(cfg, capacity, context, seed + 101)
+    s = model.session(capacity)
+    s.import_state(0, state)
+    s.position = context
+    del state
+    log(f"long context: {context}-position state generated and imported in {time.time() - t0:.1f}s")
+    nxt = 1
+    for _ in range(warm):
+        nxt = s.decode_next_token(nxt)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        nxt = s.decode_next_token(nxt)
+    device_sync()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / steps * 1e3
+    bpt = cq35.bytes_per_token(cfg, context + warm + steps // 2)
+    gbs = bpt["total"] / (ms / 1e3) / 1e9
+    log(f"long context {context}: {steps / elapsed:.1f} tok/s, {ms:.3f} ms/token, {gbs:.0f} GB/s "
+        f"of {bpt['total'] / 1e9:.3f} GB/token")
+    return dict(context=context, steps=steps, warmup=warm, tokens_per_s=round(steps / elapsed, 2),
+                ms_per_token=round(ms, 4), bytes_per_token=bpt["total"], achieved_gbs=round(gbs, 1),
+                frac=round(gbs / HBM_PEAK_GBS, 4),
+                decode_path="persistent one-launch step" if s.persistent else "per-kernel launch sequence",
+                state="seeded: KV N(0,1) x 0.1, conv history N(0,1) x 0.1, DeltaNet state N(0,1)")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -188,6 +248,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--prompt-per-token", action="store_true",
                     help="append the prompt one token per call instead of one batched call")
+    ap.add_argument("--long-context", type=int, default=32768,
+                    help="cached positions of the long-context decode leg (0 skips it)")
+    ap.add_argument("--long-steps", type=int, default=128)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -283,6 +346,11 @@ def main() -> int:
             log(f"  {k:18s} {v['ms_per_step']:.3f} ms/step  {v['avg_launch_us']:.1f} us/launch"
                 + (f"  {v['gbs']:.0f} GB/s" if v["gbs"] else ""))
 
+    long_ctx = None
+    if args.long_context > 0:
+        del session
+        long_ctx = long_context_decode(model, cfg, args.long_context, args.long_steps, args.seed)
+
     cpu = None
     if not args.no_cpu:
         need = model.weight_bytes()
@@ -317,7 +385,7 @@ def main() -> int:
         step_roofline=dict(bytes_per_token=bpt["total"], achieved_gbs=round(step_gbs, 1),
                            frac=round(step_gbs / HBM_PEAK_GBS, 4)),
         roofline=roofline, kernels=kernels, cpu_baseline=cpu,
-        prefill=prefill,
+        prefill=prefill, long_context=long_ctx,
     )
     print(json.dumps(line))
     return 0

@@ -30,6 +30,8 @@
 // (gemv.h, layers.h, attention.h), bit for bit.
 #pragma once
 
+#include <type_traits>
+
 #include "attention.h"
 #include "layers.h"
 
@@ -1323,32 +1325,98 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
 // ------------------------------------- phase: attention values (full layers)
 
 // Per (query head, 16-channel chunk) item, the reference's online softmax in
-// 8-key tiles (online.hex:272-331; per-kernel version attention.h):
-//  - tile maxima, and their running maximum as a parallel prefix maximum
-//    (max is exact, so any association gives the reference's values);
-//  - p_k = exp(s_k - m_t) and alpha_t = exp(m_{t-1} - m_t) in parallel;
-//  - every product p_k * v_{k,c} in parallel (each rounds on its own in the
-//    reference too: contraction is off);
-//  - then each channel's chain acc = acc * alpha_t + prod_0 + ... + prod_7 in
-//    order (wave 0, lanes 0-15), with wave 1 running den = den * alpha_t +
-//    p_0 + ... beside them;
+// 8-key tiles (online.hex:272-331; per-kernel version attention.h). Every
+// channel's accumulator is one serial chain acc = acc * alpha_t + prod_0 +
+// ... + prod_7 over the tiles (contraction off), so the phase is bound by
+// that chain's dependent-op latency. A three-stage pipeline over chunks of
+// kMegaValueChunk keys keeps everything else off it, one barrier a chunk:
+//  - scan (wave 2), chunk i: polls the chunk's score words (fetched two
+//    chunks ahead), keeps the scores in LDS, takes the tile maxima and their
+//    running maximum (a prefix maximum across the wave carried from the
+//    previous chunk: max is exact, so any association gives the reference's
+//    values) and alpha_t = exp(m_{t-1} - m_t);
+//  - products (waves 4-7), chunk i-1: p_k = exp(s_k - m_t) and every product
+//    p_k * v_{k,c} (each rounds on its own in the reference too), V rows
+//    fetched three chunks ahead;
+//  - chains, chunk i-2: wave 0 runs the 16 channel chains, wave 1 the
+//    denominator chain den = den * alpha_t + p_0 + ... + p_7. A chunk whose
+//    alphas are all exactly 1 skips the multiplications (x * 1 == x).
 // out = bf16(bf16(acc / den) * sigmoid(gate)). Invalid keys of the last tile
 // contribute p = 0 against key 0's value, as in the reference. The new
 // position's V comes from the projection words (the cache copy is written by
 // the scores phase for later steps).
-constexpr int kMegaValueChunk = 256;  // keys per chunk
-constexpr int kValuePre = 4;          // chunks whose V rows and scores are fetched up front
+constexpr int kMegaValueChunk = 256;              // keys per chunk
+constexpr int kValueTiles = kMegaValueChunk / 8;  // tiles per chunk
+constexpr int kProdStride = kMegaValueChunk + 4;  // padded channel rows of the products
+constexpr int kValueRing = 3;                     // chunks of V rows in flight per producer
+constexpr int kScoreRing = 3;                     // chunks of score words in flight on the scan wave
+static_assert(kValueRing == 3 && kScoreRing == 3, "the role loops unroll by the ring depth");
 struct ValueLds {
-  float p[kMegaValueChunk];
-  float alpha[kMegaValueChunk / 8];
-  float prod[kValueChannels * kMegaValueChunk];  // [channel][key]
-  float sc[kValuePre * kMegaValueChunk];  // scores of the first chunks
-  float mx[1];  // tile maxima, then running maxima (the rest of the big area)
+  float prod[2][kValueChannels * kProdStride];  // [buffer][channel][key]
+  float p[2][kMegaValueChunk];
+  float sc[3][kMegaValueChunk];
+  float alpha[3][kValueTiles];
+  float mx[3][kValueTiles];
+  int one[3];
+  uint32_t vnew[kValueChannels / 2];
+  float den;
 };
-// Tile maxima the big LDS area of shape S holds (it is sized for the MoE
-// down staging as well).
-template <class S>
-constexpr int value_mx_max();
+static_assert(sizeof(ValueLds) <= kLdsBigBytes, "value LDS");
+static_assert(kProdStride % 4 == 0 && offsetof(ValueLds, p) % 16 == 0 && offsetof(ValueLds, sc) % 16 == 0 &&
+                  offsetof(ValueLds, alpha) % 16 == 0 && sizeof(ValueLds::alpha[0]) % 16 == 0,
+              "16-byte reads of the value stages");
+static_assert(kMegaValueChunk == 4 * 64 && kMegaValueChunk == 2 * 128, "lane mapping of the value stages");
+
+// One channel chain (or the denominator chain) over nt tiles: row holds the
+// tiles' eight addends in key order, alpha the tiles' rescale factors. Four
+// tiles make a group; two register sets alternate, so the next group's
+// addends are read while the current group is summed, with no copies on
+// the chain's wave (the last read is clamped to a valid group).
+template <bool SCALE>
+__device__ __forceinline__ float chain_group(float acc, const f32x4 (&x)[8], const f32x4& al) {
+  const float a4[4] = {al.x, al.y, al.z, al.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (SCALE) acc = acc * a4[t];
+    const f32x4 x0 = x[2 * t], x1 = x[2 * t + 1];
+    acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
+    acc = acc + x1.x; acc = acc + x1.y; acc = acc + x1.z; acc = acc + x1.w;
+  }
+  return acc;
+}
+
+template <bool SCALE>
+__device__ __forceinline__ float value_chain(float acc, const f32x4* row, const float* alpha, int nt) {
+  const int groups = nt >> 2;
+  const f32x4* al4 = reinterpret_cast<const f32x4*>(alpha);
+  f32x4 xa[8], xb[8], aa, ab;
+  // the scheduler would sink the reads next to their first use; the
+  // barrier keeps them issued ahead of the group being summed
+  auto load = [&](f32x4 (&x)[8], f32x4& al, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = row[8 * g + j];
+    if (SCALE) al = al4[g];
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (groups > 0) load(xa, aa, 0);
+  int g = 0;
+#pragma unroll 1
+  for (; g + 1 < groups; g += 2) {
+    load(xb, ab, g + 1);
+    acc = chain_group<SCALE>(acc, xa, aa);
+    load(xa, aa, min(g + 2, groups - 1));
+    acc = chain_group<SCALE>(acc, xb, ab);
+  }
+  if (g < groups) acc = chain_group<SCALE>(acc, xa, aa);
+#pragma unroll 1
+  for (int t = 4 * groups; t < nt; ++t) {
+    if (SCALE) acc = acc * alpha[t];
+    const f32x4 x0 = row[2 * t], x1 = row[2 * t + 1];
+    acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
+    acc = acc + x1.x; acc = acc + x1.y; acc = acc + x1.z; acc = acc + x1.w;
+  }
+  return acc;
+}
 
 template <class S>
 __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
@@ -1356,159 +1424,190 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
   constexpr int HD = S::HD, HPK = S::Q / S::KVH, CHUNKS = HD / kValueChannels, ITEMS = S::Q * CHUNKS;
-  static_assert(2 * kMegaValueChunk <= kMT, "one V quad per thread per chunk");
   const int64_t position = (int64_t)G(a.params)[0];
   const int64_t keys = position + 1;
   const int tiles = (int)((keys + 7) >> 3);
+  const int64_t padded = (int64_t)tiles * 8;
+  const int nch = (int)((padded + kMegaValueChunk - 1) / kMegaValueChunk);
   ValueLds* s = reinterpret_cast<ValueLds*>(m.big);
   const float ninf = bitsf(0xff800000u);
-  // thread i < 2n stages key i >> 1, channels 8 (i & 1) .. 8 (i & 1) + 7 of a chunk
-  const int vk = m.tid >> 1, vh = m.tid & 1;
+  const int pj = m.tid - 4 * 64;  // producer thread (waves 4-7)
+  const int ph = pj & 1;          // channels 8 ph .. 8 ph + 7
 #pragma unroll 1
   for (int item = m.bid; item < ITEMS; item += m.grid) {
     const int head = item / CHUNKS, c0 = (item - head * CHUNKS) * kValueChannels;
-    const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0;
-    // V quad of key k (key 0 past the end); the new position's quad comes
-    // from the projection words polled into LDS
-    auto load_v = [&](int64_t k) -> u32x4 {
-      const int64_t safe = k < keys ? k : 0;
-      return G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
-    };
-    const uint64_t* vwords = Ly.x_proj + (S::QS + S::KVS / 2 + ((head / HPK * HD + c0) >> 1));
-    // prefetch the first chunks' V rows (positions before the new one)
-    u32x4 vq[kValuePre];
-#pragma unroll
-    for (int c = 0; c < kValuePre; ++c) {
-      const int64_t k = vk + (int64_t)kMegaValueChunk * c;
-      vq[c] = u32x4{0u, 0u, 0u, 0u};
-      if (k < (int64_t)tiles * 8 && k != position) {
-        const int64_t safe = k < keys ? k : 0;
-        vq[c] = G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS + 8 * vh))[0];
-      }
-    }
-    // scores of this head: poll every tile, keep the tile maxima
+    const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0 + 8 * ph;
     const uint64_t* sc = Ly.x_scores + (size_t)head * a.cap;
-    for (int t = m.tid; t < tiles; t += kMT) {
-      uint64_t v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t k = (int64_t)t * 8 + j;
-        v[j] = k < keys ? word_load(sc + k) : ((uint64_t)m.tag << 32);
-      }
-      unsigned spins = 0;
-      while (true) {
-        bool ready = true;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ready &= word_ready(v[j], m.tag);
-        if (ready || spin_stop(m, ++spins)) break;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (!word_ready(v[j], m.tag)) v[j] = word_load(sc + (int64_t)t * 8 + j);
-      }
-      float mt = ninf;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t k = (int64_t)t * 8 + j;
-        const float sk = bitsf((uint32_t)v[j]);
-        mt = fmaxf(mt, k < keys ? sk : ninf);
-        if (k < kValuePre * kMegaValueChunk) s->sc[k] = sk;  // kept for the weights
-      }
-      s->mx[t] = mt;
-    }
-    // gate of this item's channels and the new position's V (word pairs)
+    // V quad of key k (key 0 past the end); nothing past the last tile
+    auto load_v = [&](int64_t k) -> u32x4 {
+      if (k >= padded) return u32x4{0u, 0u, 0u, 0u};
+      const int64_t safe = k < keys ? k : 0;
+      return G(reinterpret_cast<const u32x4*>(vbase + safe * S::KVS))[0];
+    };
+    // score word of key k (a ready placeholder past the last key)
+    auto load_s = [&](int64_t k) -> uint64_t {
+      return k < keys ? word_load(sc + k) : ((uint64_t)m.tag << 32);
+    };
+    // Each role runs its own loop of n_iter iterations with one barrier each
+    // (every wave passes the same barriers); the prefetch rings are indexed
+    // by chunk mod 3 through unrolling, so a ring slot is only waited on
+    // three chunks after its reads were issued.
+    const int n_iter = nch + 2;
+    using R0 = std::integral_constant<int, 0>;
+    using R1 = std::integral_constant<int, 1>;
+    using R2 = std::integral_constant<int, 2>;
     uint32_t gate_word = 0;
-    if (m.tid < kValueChannels / 2)
-      gate_word = poll_one(m, Ly.x_proj + ((head * 2 * HD + HD + c0) >> 1) + m.tid);
-    else if (m.tid < kValueChannels)
-      reinterpret_cast<uint32_t*>(s->alpha)[m.tid - kValueChannels / 2] =
-          poll_one(m, vwords + (m.tid - kValueChannels / 2));
-    __syncthreads();
-    u32x4 vnew;
-    {
-      const uint32_t* w = reinterpret_cast<const uint32_t*>(s->alpha) + 4 * vh;
-      vnew = u32x4{w[0], w[1], w[2], w[3]};
-    }
-    if (m.wave == 0) {
-      // running maximum: serial within a lane's segment, then an inclusive
-      // scan of the segment maxima across the wave
-      const int seg = (tiles + 63) >> 6, t0 = m.lane * seg, t1 = min(t0 + seg, tiles);
-      float mm = ninf;
-      for (int i = t0; i < t1; ++i) mm = fmaxf(mm, s->mx[i]);
-      float inc = mm;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float o = __shfl_up(inc, d, 64);
-        if (m.lane >= d) inc = fmaxf(inc, o);
-      }
-      float run = __shfl_up(inc, 1, 64);
-      if (m.lane == 0) run = ninf;
-      for (int i = t0; i < t1; ++i) {
-        run = fmaxf(run, s->mx[i]);
-        s->mx[i] = run;
-      }
-    }
-    __syncthreads();
     float acc = 0.0f, den = 0.0f;
-    int chunk = 0;
-    for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kMegaValueChunk, ++chunk) {
-      const int n = (int)min<int64_t>(kMegaValueChunk, (int64_t)tiles * 8 - k0);  // multiple of 8
-      if (m.tid < n) {
-        const int64_t k = k0 + m.tid;
-        const float sk = chunk < kValuePre ? s->sc[k] : bitsf((uint32_t)word_load(sc + k));
-        s->p[m.tid] = k < keys ? hexp(sk - s->mx[k >> 3]) : 0.0f;
-      }
-      if (m.tid < n / 8) {
-        const int tile = (int)(k0 / 8) + m.tid;
-        s->alpha[m.tid] = hexp((tile > 0 ? s->mx[tile - 1] : ninf) - s->mx[tile]);
-      }
-      u32x4 vcur = chunk == 0 ? vq[0] : chunk == 1 ? vq[1 % kValuePre] : chunk == 2 ? vq[2 % kValuePre] : vq[3 % kValuePre];
-      if (k0 + vk == position) vcur = vnew;
-      else if (vk < n && chunk >= kValuePre) vcur = load_v(k0 + vk);
-      __syncthreads();
-      if (vk < n) {
-        const float pk = s->p[vk];
-        f32x4 o0, o1;
-        o0.x = pk * lo2f(vcur.x); o0.y = pk * hi2f(vcur.x);
-        o0.z = pk * lo2f(vcur.y); o0.w = pk * hi2f(vcur.y);
-        o1.x = pk * lo2f(vcur.z); o1.y = pk * hi2f(vcur.z);
-        o1.z = pk * lo2f(vcur.w); o1.w = pk * hi2f(vcur.w);
-        float* dst = s->prod + (8 * vh) * kMegaValueChunk + vk;
-        dst[0 * kMegaValueChunk] = o0.x; dst[1 * kMegaValueChunk] = o0.y;
-        dst[2 * kMegaValueChunk] = o0.z; dst[3 * kMegaValueChunk] = o0.w;
-        dst[4 * kMegaValueChunk] = o1.x; dst[5 * kMegaValueChunk] = o1.y;
-        dst[6 * kMegaValueChunk] = o1.z; dst[7 * kMegaValueChunk] = o1.w;
-      }
-      __syncthreads();
+    if (m.wave <= 1) {
       if (m.wave == 0) {
-        if (m.lane < kValueChannels) {
-          const f32x4* pr = reinterpret_cast<const f32x4*>(s->prod + m.lane * kMegaValueChunk);
-#pragma unroll 4
-          for (int i = 0; i < n / 8; ++i) {
-            const f32x4 x0 = pr[2 * i], x1 = pr[2 * i + 1];
-            acc = acc * s->alpha[i];
-            acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
-            acc = acc + x1.x; acc = acc + x1.y; acc = acc + x1.z; acc = acc + x1.w;
-          }
-        }
-      } else if (m.wave == 1) {
-        // the denominator chain beside the channel chains (its own SIMD)
-        if (m.lane == 0) {
-#pragma unroll 4
-          for (int i = 0; i < n / 8; ++i) {
-            const f32x4 p0 = reinterpret_cast<const f32x4*>(s->p)[2 * i];
-            const f32x4 p1 = reinterpret_cast<const f32x4*>(s->p)[2 * i + 1];
-            den = den * s->alpha[i];
-            den = den + p0.x; den = den + p0.y; den = den + p0.z; den = den + p0.w;
-            den = den + p1.x; den = den + p1.y; den = den + p1.z; den = den + p1.w;
-          }
-        }
+        if (m.lane < kValueChannels / 2)
+          gate_word = poll_one(m, Ly.x_proj + ((head * 2 * HD + HD + c0) >> 1) + m.lane);
+      } else if (m.lane < kValueChannels / 2) {
+        // the new position's V (word pairs of the projection)
+        s->vnew[m.lane] = poll_one(m, Ly.x_proj + (S::QS + S::KVS / 2 + ((head / HPK * HD + c0) >> 1)) + m.lane);
       }
-      __syncthreads();
+#pragma unroll 1
+      for (int i = 0; i < n_iter; ++i) {
+        const int c = i - 2;
+        if (c >= 0) {
+          const int slot = c % 3, buf = c & 1;
+          const int nt = min(kValueTiles, tiles - c * kValueTiles);
+          const bool one = s->one[slot] != 0;
+          if (m.wave == 0) {
+            const f32x4* row = reinterpret_cast<const f32x4*>(s->prod[buf] + (m.lane & 15) * kProdStride);
+            acc = one ? value_chain<false>(acc, row, s->alpha[slot], nt)
+                      : value_chain<true>(acc, row, s->alpha[slot], nt);
+          } else {
+            const f32x4* row = reinterpret_cast<const f32x4*>(s->p[buf]);
+            den = one ? value_chain<false>(den, row, s->alpha[slot], nt)
+                      : value_chain<true>(den, row, s->alpha[slot], nt);
+            if (m.lane == 0) s->den = den;
+          }
+        }
+        __syncthreads();
+      }
+    } else if (m.wave == 2) {
+      uint64_t sr[kScoreRing][4];  // slot r: chunks = r mod 3
+#pragma unroll
+      for (int r = 0; r < kScoreRing; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sr[r][j] = load_s((int64_t)r * kMegaValueChunk + 4 * m.lane + j);
+      float carry = ninf;
+      auto scan = [&](auto rr, int i) {
+        constexpr int r = decltype(rr)::value;
+        if (i < nch) {
+          const int slot = i % 3;
+          const int64_t k0 = (int64_t)i * kMegaValueChunk;
+          uint64_t v[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[j] = sr[r][j];
+          unsigned spins = 0;
+          while (true) {
+            bool ready = true;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ready &= word_ready(v[j], m.tag);
+            if (ready || spin_stop(m, ++spins)) break;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (!word_ready(v[j], m.tag)) v[j] = load_s(k0 + 4 * m.lane + j);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            sr[r][j] = load_s(k0 + (int64_t)kScoreRing * kMegaValueChunk + 4 * m.lane + j);
+          f32x4 sv;
+          sv.x = bitsf((uint32_t)v[0]); sv.y = bitsf((uint32_t)v[1]);
+          sv.z = bitsf((uint32_t)v[2]); sv.w = bitsf((uint32_t)v[3]);
+          reinterpret_cast<f32x4*>(s->sc[slot])[m.lane] = sv;
+          const int64_t kl = k0 + 4 * m.lane;
+          float mt = fmaxf(fmaxf(kl < keys ? sv.x : ninf, kl + 1 < keys ? sv.y : ninf),
+                           fmaxf(kl + 2 < keys ? sv.z : ninf, kl + 3 < keys ? sv.w : ninf));
+          mt = fmaxf(mt, __shfl_xor(mt, 1, 64));  // the tile's two lanes
+          float run = mt;
+#pragma unroll
+          for (int d = 1; d < 64; d <<= 1) {
+            const float o = __shfl_up(run, d, 64);
+            if (m.lane >= d) run = fmaxf(run, o);
+          }
+          run = fmaxf(run, carry);
+          float prev = __shfl_up(run, 2, 64);
+          if (m.lane < 2) prev = i == 0 ? ninf : carry;
+          const float al = hexp(prev - run);
+          const int t = m.lane >> 1;
+          const bool valid = (m.lane & 1) == 0 && (int64_t)i * kValueTiles + t < tiles;
+          if (valid) {
+            s->mx[slot][t] = run;
+            s->alpha[slot][t] = al;
+          }
+          const uint64_t scaled = __ballot(valid && al != 1.0f);
+          if (m.lane == 0) s->one[slot] = scaled == 0ull ? 1 : 0;
+          carry = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, run), 63));
+        }
+        __syncthreads();
+      };
+      int i = 0;
+#pragma unroll 1
+      for (; i + 3 <= n_iter; i += 3) {
+        scan(R0{}, i);
+        scan(R1{}, i + 1);
+        scan(R2{}, i + 2);
+      }
+      if (i < n_iter) scan(R0{}, i);
+      if (i + 1 < n_iter) scan(R1{}, i + 1);
+    } else if (m.wave >= 4) {
+      u32x4 vr[kValueRing][2];  // slot r: chunks = r mod 3
+#pragma unroll
+      for (int r = 0; r < kValueRing; ++r)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          vr[r][q] = load_v((int64_t)r * kMegaValueChunk + (pj >> 1) + 128 * q);
+      auto produce = [&](auto rr, int i) {
+        constexpr int r = decltype(rr)::value;
+        const int c = i - 1;
+        if (c >= 0 && c < nch) {
+          const int slot = c % 3, buf = c & 1;
+          const int64_t k0 = (int64_t)c * kMegaValueChunk;
+          u32x4 vnew;
+          {
+            const uint32_t* w = s->vnew + 4 * ph;
+            vnew = u32x4{w[0], w[1], w[2], w[3]};
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const int kk = (pj >> 1) + 128 * q;
+            const int64_t k = k0 + kk;
+            if (k < padded) {
+              const float pk = k < keys ? hexp(s->sc[slot][kk] - s->mx[slot][kk >> 3]) : 0.0f;
+              const u32x4 vq = k == position ? vnew : vr[r][q];
+              float* dst = s->prod[buf] + (8 * ph) * kProdStride + kk;
+              dst[0 * kProdStride] = pk * lo2f(vq.x); dst[1 * kProdStride] = pk * hi2f(vq.x);
+              dst[2 * kProdStride] = pk * lo2f(vq.y); dst[3 * kProdStride] = pk * hi2f(vq.y);
+              dst[4 * kProdStride] = pk * lo2f(vq.z); dst[5 * kProdStride] = pk * hi2f(vq.z);
+              dst[6 * kProdStride] = pk * lo2f(vq.w); dst[7 * kProdStride] = pk * hi2f(vq.w);
+              if (ph == 0) s->p[buf][kk] = pk;
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            vr[r][q] = load_v(k0 + (int64_t)kValueRing * kMegaValueChunk + (pj >> 1) + 128 * q);
+        }
+        __syncthreads();
+      };
+      // iteration i produces chunk i - 1, whose ring slot is (i + 2) mod 3
+      int i = 0;
+#pragma unroll 1
+      for (; i + 3 <= n_iter; i += 3) {
+        produce(R2{}, i);
+        produce(R0{}, i + 1);
+        produce(R1{}, i + 2);
+      }
+      if (i < n_iter) produce(R2{}, i);
+      if (i + 1 < n_iter) produce(R0{}, i + 1);
+    } else {
+#pragma unroll 1
+      for (int i = 0; i < n_iter; ++i) __syncthreads();
     }
-    if (m.wave == 1 && m.lane == 0) s->alpha[0] = den;  // the chunks are done with alpha
-    __syncthreads();
     if (m.wave == 0) {
-      den = s->alpha[0];
+      den = s->den;
       const uint32_t gw = __shfl((int)gate_word, m.lane >> 1, 64);
       const uint16_t gb = (m.lane & 1) ? (uint16_t)(gw >> 16) : (uint16_t)(gw & 0xffffu);
       uint16_t y = 0;
@@ -1607,10 +1706,6 @@ constexpr int mega_big_bytes() {
 template <class S>
 constexpr int mega_lds_bytes() {
   return kLdsBig + mega_big_bytes<S>();
-}
-template <class S>
-constexpr int value_mx_max() {
-  return (mega_big_bytes<S>() - (int)offsetof(ValueLds, mx)) / 4;
 }
 
 template <class S>

@@ -522,20 +522,19 @@ bool shape_is(const cq35_config& c) {
 }
 
 template <class S>
-bool grid_fits(int grid, int64_t cap) {
+bool grid_fits(int grid) {
   const int64_t nw = (int64_t)grid * kMW;
   const int64_t rows_lin = S::QKV + S::VS, rows_full = 2LL * S::QS + 2LL * S::KVS;
   return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw && S::H / 2 <= (int64_t)(kMW / 2) * grid &&
          S::H / 2 <= (int64_t)DownLayout<S>::WAVES * grid &&
          S::K * S::I / 2 <= nw && S::E + 1 <= (int64_t)(kMW / 2) * grid &&
-         S::SI / 2 <= (int64_t)(kMW / 2) * grid && S::H / 2 <= nw &&
-         (cap + 7) / 8 <= value_mx_max<S>();
+         S::SI / 2 <= (int64_t)(kMW / 2) * grid && S::H / 2 <= nw;
 }
 
-int mega_kind(const cq35_config& c, int grid, int64_t cap) {
-  if (shape_is<Shape35BA3B>(c)) return grid_fits<Shape35BA3B>(grid, cap) ? kMega35B : kMegaNone;
-  if (shape_is<ShapeMiniMoE>(c)) return grid_fits<ShapeMiniMoE>(grid, cap) ? kMegaMini : kMegaNone;
-  if (shape_is<ShapeTinyMoE>(c)) return grid_fits<ShapeTinyMoE>(grid, cap) ? kMegaTiny : kMegaNone;
+int mega_kind(const cq35_config& c, int grid) {
+  if (shape_is<Shape35BA3B>(c)) return grid_fits<Shape35BA3B>(grid) ? kMega35B : kMegaNone;
+  if (shape_is<ShapeMiniMoE>(c)) return grid_fits<ShapeMiniMoE>(grid) ? kMegaMini : kMegaNone;
+  if (shape_is<ShapeTinyMoE>(c)) return grid_fits<ShapeTinyMoE>(grid) ? kMegaTiny : kMegaNone;
   return kMegaNone;
 }
 
@@ -565,7 +564,7 @@ int setup_mega(cq35_session* s) {
   const Dims& d = m.d;
   int grid = 0;
   HIP_TRY(hipDeviceGetAttribute(&grid, hipDeviceAttributeMultiprocessorCount, m.device));
-  const int kind = mega_kind(c, grid, s->capacity);
+  const int kind = mega_kind(c, grid);
   const void* kernel = mega_kernel(kind);
   if (!kernel) return CQ35_OK;
   const int lds = mega_lds(kind);
