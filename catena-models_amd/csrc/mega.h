@@ -1142,12 +1142,13 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
 struct ScoreLds {
   float rope[256];
   float normed[kMW][256];
-  uint16_t qhat[16 * 256];
+  float qhat[16 * 256];  // normalised query heads, lane-major (channel l32 + 32 j at l32 * KJ + j)
   uint16_t khat[2 * 256];
   int heads[32];  // heads this block normalises: query heads, then Q + key head
   int nheads;
 };
 static_assert(sizeof(ScoreLds) <= kLdsBigBytes, "score LDS");
+static_assert(offsetof(ScoreLds, qhat) % 16 == 0, "16-byte reads of the query heads");
 
 template <class S>
 __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
@@ -1155,7 +1156,7 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
   constexpr int HD = S::HD, Q = S::Q, KVH = S::KVH, HPK = Q / KVH, KJ = HD / 32, RH = S::R / 2;
-  static_assert(Q * HD <= 16 * 256 && KVH * HD <= 2 * 256, "score shape");
+  static_assert(Q * HD <= 16 * 256 && KVH * HD <= 2 * 256 && KJ % 2 == 0, "score shape");
   const int64_t position = (int64_t)G(a.params)[0];
   const int64_t keys = position + 1;
   const int64_t items = keys * KVH;
@@ -1165,18 +1166,34 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   // nothing to do in this phase
   const int64_t first = (int64_t)m.bid * 2 * kMW;
   if (first >= items) return;  // uniform per block
-  // prefetch the cached keys of this wave's first items
+  // item indices fit 32 bits (capacity <= 2^18, KVH <= 8): 32-bit division
+  const uint32_t ukeys = (uint32_t)keys, uitems = (uint32_t)items;
+  // score items: two per wave (32 lanes each) per round, in batches of SB
+  // rounds whose cached keys are read one batch ahead (reads of invalid
+  // rounds are clamped to key 0 and ignored); the first batch is read now
+  constexpr int SB = 4;
   const int64_t item0 = (int64_t)m.gw * 2 + half;
-  float kv0[KJ];
-  if (item0 < items) {
-    const int kvh = (int)(item0 / keys);
-    const int64_t key = item0 - (int64_t)kvh * keys;
-    if (key < position) {
-      const uint16_t* kr = a.cache + Ly.key_base + key * S::KVS + (int64_t)kvh * HD + l32;
+  const int64_t stride = 2 * (int64_t)m.nw;
+  const int rounds = item0 < items ? (int)((items - 1 - item0) / stride) + 1 : 0;
+  const int nb = (rounds + SB - 1) / SB;
+  auto load_batch = [&](uint32_t (&kv)[SB][KJ], int b) {
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) kv0[j] = bf2f(G(kr)[32 * j]);
+    for (int rr = 0; rr < SB; ++rr) {
+      const uint32_t it = (uint32_t)(item0 + (int64_t)(b * SB + rr) * stride);
+      uint32_t kvh = 0, key = 0;
+      if (it < uitems) {
+        kvh = it / ukeys;
+        key = it - kvh * ukeys;
+        if (key >= (uint32_t)position) key = 0;
+      }
+      const uint16_t* kr = a.cache + Ly.key_base + (int64_t)key * S::KVS + (int64_t)kvh * HD + l32;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) kv[rr][j] = G(kr)[32 * j];
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the batch being scored
+  };
+  uint32_t ka[SB][KJ], kb[SB][KJ];
+  if (nb > 0) load_batch(ka, 0);
   // norm weights (shared by all query heads / all key heads) and the RoPE
   // frequencies do not depend on the projection: load them first
   constexpr int VPL = HD / 64;  // values per lane
@@ -1204,10 +1221,20 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   const uint16_t* vraw = kraw + S::KVS;
   // KV groups touched by the block's items -> heads to normalise
   if (m.tid == 0) {
+    // windows of 2 kMW items start every 2 nw items from `first`; when a KV
+    // group holds at least that many items, no group between the first and
+    // the last window's is skipped
+    const uint32_t ustride = 2u * (uint32_t)m.nw, ufirst = (uint32_t)first;
+    const uint32_t ulast_start = ufirst + (uitems - 1 - ufirst) / ustride * ustride;
     unsigned mask = 0;
-    for (int64_t i0 = first; i0 < items; i0 += 2 * (int64_t)m.nw) {
-      const int64_t i1 = min<int64_t>(i0 + 2 * kMW, items) - 1;
-      for (int g = (int)(i0 / keys); g <= (int)(i1 / keys); ++g) mask |= 1u << g;
+    if (ukeys >= ustride) {
+      const uint32_t g0 = ufirst / ukeys, g1 = min(ulast_start + 2u * kMW, uitems) - 1u;
+      for (uint32_t g = g0; g <= g1 / ukeys; ++g) mask |= 1u << g;
+    } else {
+      for (uint32_t i0 = ufirst; i0 < uitems; i0 += ustride) {
+        const uint32_t i1 = min(i0 + 2u * kMW, uitems) - 1u;
+        for (uint32_t g = i0 / ukeys; g <= i1 / ukeys; ++g) mask |= 1u << g;
+      }
     }
     int n = 0;
     for (int g = 0; g < KVH; ++g)
@@ -1275,50 +1302,70 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
           result = first ? ac - bs : ac + bs;
         }
         const uint16_t rb = f2bf(result);
-        if (is_q) s->qhat[hh * HD + c] = rb;
+        // query heads lane-major: lane l32's channels l32 + 32 j contiguous
+        if (is_q) s->qhat[hh * HD + (c & 31) * KJ + (c >> 5)] = bf2f(rb);
         else s->khat[(hh - Q) * HD + c] = rb;
       }
     }
     __syncthreads();
   }
-  // score items: two per wave (32 lanes each)
-  int round = 0;
-  for (int64_t it = item0; it < items; it += 2 * (int64_t)m.nw, ++round) {
-    const int kvh = (int)(it / keys);
-    const int64_t key = it - (int64_t)kvh * keys;
-    float kv[KJ];
-    if (key == position) {
+  auto score_batch = [&](const uint32_t (&kv)[SB][KJ], int b) {
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) kv[j] = bf2f(s->khat[kvh * HD + l32 + 32 * j]);
-      // K and V of the new position into the cache, for later steps (this
-      // step's values phase takes V from the projection words)
-      uint16_t* kdst = a.cache + Ly.key_base + position * S::KVS + (int64_t)kvh * HD;
-      uint16_t* vdst = a.cache + Ly.value_base + position * S::KVS + (int64_t)kvh * HD;
+    for (int rr = 0; rr < SB; ++rr) {
+      const uint32_t it = (uint32_t)(item0 + (int64_t)(b * SB + rr) * stride);
+      if (it >= uitems) continue;
+      const int kvh = (int)(it / ukeys);
+      const int64_t key = (int64_t)(it - (uint32_t)kvh * ukeys);
+      float kf[KJ];
+      if (key == position) {
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) {
-        const int c = l32 + 32 * j;
-        G(kdst)[c] = s->khat[kvh * HD + c];
-        G(vdst)[c] = vraw[kvh * HD + c];
+        for (int j = 0; j < KJ; ++j) kf[j] = bf2f(s->khat[kvh * HD + l32 + 32 * j]);
+        // K and V of the new position into the cache, for later steps (this
+        // step's values phase takes V from the projection words)
+        uint16_t* kdst = a.cache + Ly.key_base + position * S::KVS + (int64_t)kvh * HD;
+        uint16_t* vdst = a.cache + Ly.value_base + position * S::KVS + (int64_t)kvh * HD;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) {
+          const int c = l32 + 32 * j;
+          G(kdst)[c] = s->khat[kvh * HD + c];
+          G(vdst)[c] = vraw[kvh * HD + c];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) kf[j] = bf2f((uint16_t)kv[rr][j]);
       }
-    } else if (round == 0) {
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) kv[j] = kv0[j];
-    } else {
-      const uint16_t* kr = a.cache + Ly.key_base + key * S::KVS + (int64_t)kvh * HD + l32;
+      for (int hq = 0; hq < HPK; ++hq) {
+        const int head = kvh * HPK + hq;
+        const float* qh = s->qhat + head * HD + l32 * KJ;
+        float qv[KJ];
+        if constexpr (KJ % 4 == 0) {
 #pragma unroll
-      for (int j = 0; j < KJ; ++j) kv[j] = bf2f(G(kr)[32 * j]);
+          for (int w = 0; w < KJ / 4; ++w) {
+            const f32x4 t = reinterpret_cast<const f32x4*>(qh)[w];
+            qv[4 * w] = t.x; qv[4 * w + 1] = t.y; qv[4 * w + 2] = t.z; qv[4 * w + 3] = t.w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) qv[j] = qh[j];
+        }
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KJ; ++j) acc += qv[j] * kf[j];
+        acc = tree32_lanes(acc);  // halving strides 16 .. 1 in each half wave
+        if (l32 == 0) word_store(Ly.x_scores + (size_t)head * a.cap + key, fbits(acc * a.attn_scale), m.tag);
+      }
     }
-#pragma unroll
-    for (int hq = 0; hq < HPK; ++hq) {
-      const int head = kvh * HPK + hq;
-      const uint16_t* qh = s->qhat + head * HD + l32;
-      float acc = 0.0f;
-#pragma unroll
-      for (int j = 0; j < KJ; ++j) acc += bf2f(qh[32 * j]) * kv[j];
-      acc = tree32_lanes(acc);  // halving strides 16 .. 1 in each half wave
-      if (l32 == 0) word_store(Ly.x_scores + (size_t)head * a.cap + key, fbits(acc * a.attn_scale), m.tag);
-    }
+  };
+  int b = 0;
+#pragma unroll 1
+  for (; b + 1 < nb; b += 2) {
+    load_batch(kb, b + 1);
+    score_batch(ka, b);
+    load_batch(ka, min(b + 2, nb - 1));
+    score_batch(kb, b + 1);
   }
+  if (b < nb) score_batch(ka, b);
   __syncthreads();
 }
 
