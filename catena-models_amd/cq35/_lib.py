@@ -61,6 +61,8 @@ def load():
         "cq35_session_set_graph": ([P, ctypes.c_int], ctypes.c_int),
         "cq35_session_set_persistent": ([P, ctypes.c_int], ctypes.c_int),
         "cq35_session_persistent": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+        "cq35_session_set_matrix_prefill": ([P, ctypes.c_int], ctypes.c_int),
+        "cq35_session_matrix_prefill": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "cq35_numeric_exp": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_sqrt": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_softplus": ([ctypes.c_float], ctypes.c_float),
@@ -68,6 +70,7 @@ def load():
                                  ctypes.POINTER(ctypes.c_float)], None),
         "cq35_device_numeric": ([ctypes.c_int, P, P, I64], ctypes.c_int),
         "cq35_device_gemv": ([P, P, I64, I64, ctypes.c_int, P], ctypes.c_int),
+        "cq35_device_matrix_gemm": ([P, P, I64, I64, I64, P], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(l, name)
@@ -90,6 +93,7 @@ EXPORTED = [
     "cq35_session_export_state", "cq35_session_import_state", "cq35_session_time_kernel",
     "cq35_session_kernel_time", "cq35_kernel_class_name", "cq35_kernel_class_count",
     "cq35_session_set_graph", "cq35_session_set_persistent", "cq35_session_persistent",
+    "cq35_session_set_matrix_prefill", "cq35_session_matrix_prefill",
     "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
-    "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv",
+    "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv", "cq35_device_matrix_gemm",
 ]

@@ -220,6 +220,21 @@ class Session:
         it covers; the default there) or the per-kernel launch sequence."""
         check(_lib.load().cq35_session_set_persistent(self._h, 1 if enabled else 0))
 
+    MATRIX_PROJECTIONS = 1
+    MATRIX_EXPERTS = 2
+
+    def set_matrix_prefill(self, components: int) -> None:
+        """Run these components of multi-token calls on MFMA (hardware
+        accumulation order; 0 = the exact SIMT path): MATRIX_PROJECTIONS,
+        MATRIX_EXPERTS or both (the reference's wmma_prefill scopes)."""
+        check(_lib.load().cq35_session_set_matrix_prefill(self._h, int(components)))
+
+    @property
+    def matrix_prefill(self) -> int:
+        v = ctypes.c_int()
+        check(_lib.load().cq35_session_matrix_prefill(self._h, ctypes.byref(v)))
+        return v.value
+
     @property
     def persistent(self) -> bool:
         v = ctypes.c_int()

@@ -1,0 +1,329 @@
+// Matrix-core prefill: the reference's matrix-core prompt path (wmma_prefill,
+// qwen35.rs:467-541 with the grouped-expert and projection stages of
+// qwen35_wmma_moe.hex) on CDNA4 MFMA. The products are the same as the
+// batched SIMT projections (prefill.h) but the F32 accumulation runs inside
+// v_mfma_f32_32x32x16_bf16, whose summation order is the hardware's: results
+// agree with the exact path to accumulation rounding, not bit for bit, as
+// the reference's own matrix-core path does (README.md:59-60). The exact
+// SIMT path stays the default; a session selects this one per component.
+//
+// Operand layouts of v_mfma_f32_32x32x16_bf16 (checked on the device): lane
+// l supplies A[l % 32][8 (l / 32) + i] and B[8 (l / 32) + i][l % 32] for
+// i < 8, and receives D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] in
+// accumulator register r < 16. Both prefill operands are K-contiguous
+// (activations [token][k], weights [row][k]), so every fragment is one
+// 16-byte load.
+#pragma once
+
+#include "prefill.h"
+
+namespace cq35 {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16_t mfma32(const u32x4& a, const u32x4& b, const f32x16_t& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+constexpr int kMTokens = 32;             // tokens per wave tile
+constexpr int kMRows = 64;               // weight rows per block tile (two 32-row MFMA tiles)
+constexpr int kMWaves = 4;               // waves per block, along tokens
+constexpr int kMBlockTokens = kMTokens * kMWaves;
+
+// out[t][row] = epilogue(sum_k x[t][k] w[row][k]) for t < n, row < rows;
+// cols % 16 == 0. Block (row tile bx, token tile by); wave w takes tokens
+// [128 by + 32 w, +32). k steps of 16 rotate over kParts independent partial
+// sums, added as a tree at the end: shorter F32 chains than one running
+// accumulator (closer to the reference's lane-partials-then-tree orders) and
+// independent MFMA dependency chains. The epilogues are those of k_bproject:
+// bf16(total); bf16(total) (+) res; bf16(silu(bf16 g)) (x) bf16(u) with u
+// from w2.
+template <int kMode>
+__global__ __launch_bounds__(64 * kMWaves) void k_mproject(const uint16_t* __restrict__ x, int n, int cols,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ w2, int rows,
+                                                           const uint16_t* __restrict__ res,
+                                                           uint16_t* __restrict__ out) {
+  constexpr int kParts = kMode == kBGate ? 2 : 4;
+  constexpr int kMats = kMode == kBGate ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.y * kMBlockTokens + wave * kMTokens;
+  if (t0 >= n) return;  // uniform per wave; no barriers below
+  const int r0 = blockIdx.x * kMRows;
+  const int kq = 8 * (lane >> 5);  // this lane's k offset inside a 16-wide step
+  const int tr = min(t0 + (lane & 31), n - 1);
+  const uint16_t* xa = x + (size_t)tr * cols + kq;
+  const uint16_t* wp[kMats][2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int wr = min(r0 + 32 * h + (lane & 31), rows - 1);
+    wp[0][h] = w + (size_t)wr * cols + kq;
+    if (kMode == kBGate) wp[kMats - 1][h] = w2 + (size_t)wr * cols + kq;
+  }
+  f32x16_t acc[kParts][kMats][2];
+#pragma unroll
+  for (int p = 0; p < kParts; ++p)
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi) acc[p][mi][0] = acc[p][mi][1] = f32x16_t{};
+  const int steps = cols / 16;
+  int st = 0;
+  for (; st + kParts <= steps; st += kParts) {
+    u32x4 a[kParts], b[kParts][kMats][2];
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) {
+      const int k = 16 * (st + p);
+      a[p] = *reinterpret_cast<const u32x4*>(xa + k);
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) b[p][mi][h] = *reinterpret_cast<const u32x4*>(wp[mi][h] + k);
+    }
+#pragma unroll
+    for (int p = 0; p < kParts; ++p)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[p][mi][h] = mfma32(a[p], b[p][mi][h], acc[p][mi][h]);
+  }
+  for (int p = 0; st < steps; ++st, ++p) {  // the last steps continue the rotation
+    const int k = 16 * st;
+    const u32x4 a = *reinterpret_cast<const u32x4*>(xa + k);
+#pragma unroll
+    for (int q = 0; q < kParts; ++q) {
+      if (q != p) continue;
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          acc[q][mi][h] = mfma32(a, *reinterpret_cast<const u32x4*>(wp[mi][h] + k), acc[q][mi][h]);
+    }
+  }
+  // tree over the partial sums
+#pragma unroll
+  for (int span = 1; span < kParts; span *= 2)
+#pragma unroll
+    for (int p = 0; p + span < kParts; p += 2 * span)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[p][mi][h] += acc[p + span][mi][h];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = r0 + 32 * h + (lane & 31);
+    if (row >= rows) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int t = t0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (t >= n) continue;
+      const size_t o = (size_t)t * rows + row;
+      const float v = acc[0][0][h][r];
+      uint16_t y;
+      if (kMode == kBPlain) y = f2bf(v);
+      else if (kMode == kBResidual) y = bf_add(f2bf(v), res[o]);
+      else y = bf_mul(f2bf(silu(rbf(v))), f2bf(acc[0][kMats - 1][h][r]));
+      out[o] = y;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- experts
+//
+// Grouped expert projections (the reference's grouped routed/shared expert
+// stages, qwen35_wmma_moe.hex): the chunk's (token, slot) assignments are
+// bucketed by expert, every expert's weights are streamed once per chunk
+// and applied to all of its tokens, the shared expert runs as a dense
+// product over all tokens, and the routed down products are summed per
+// token over the slots in slot order before the reference's epilogue.
+
+// One wave's 32 x 32 MFMA tile over k in [0, cols): A rows at xa, B rows at
+// w[mi] (both already offset by the lane's row and k quarter). kParts partial
+// sums over rotating k steps, added as a tree.
+template <int kParts, int kMats>
+__device__ __forceinline__ void mfma_tile(const uint16_t* xa, const uint16_t* const (&w)[kMats], int cols,
+                                          f32x16_t (&out)[kMats]) {
+  f32x16_t acc[kParts][kMats];
+#pragma unroll
+  for (int p = 0; p < kParts; ++p)
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi) acc[p][mi] = f32x16_t{};
+  const int steps = cols / 16;
+  int st = 0;
+  for (; st + kParts <= steps; st += kParts) {
+    u32x4 a[kParts], b[kParts][kMats];
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) {
+      a[p] = *reinterpret_cast<const u32x4*>(xa + 16 * (st + p));
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) b[p][mi] = *reinterpret_cast<const u32x4*>(w[mi] + 16 * (st + p));
+    }
+#pragma unroll
+    for (int p = 0; p < kParts; ++p)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) acc[p][mi] = mfma32(a[p], b[p][mi], acc[p][mi]);
+  }
+  for (int p = 0; st < steps; ++st, ++p) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(xa + 16 * st);
+#pragma unroll
+    for (int q = 0; q < kParts; ++q) {
+      if (q != p) continue;
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+        acc[q][mi] = mfma32(a, *reinterpret_cast<const u32x4*>(w[mi] + 16 * st), acc[q][mi]);
+    }
+  }
+#pragma unroll
+  for (int span = 1; span < kParts; span *= 2)
+#pragma unroll
+    for (int p = 0; p + span < kParts; p += 2 * span)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) acc[p][mi] += acc[p + span][mi];
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi) out[mi] = acc[0][mi];
+}
+
+// Buckets: eoff[e] .. eoff[e + 1] index order[], which holds assignment
+// indices t * top_k + slot. The order inside a bucket is whatever the
+// atomics give: each MFMA output element is its own dot product, unaffected
+// by the rows it shares a tile with, so results do not depend on it.
+__global__ __launch_bounds__(1024) void k_moe_bucket(const int* __restrict__ ids, int assignments, int experts,
+                                                     int* __restrict__ eoff, int* __restrict__ order) {
+  extern __shared__ int bucket_lds[];
+  int* cnt = bucket_lds;
+  int* cur = bucket_lds + experts;
+  for (int e = threadIdx.x; e < experts; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  for (int a = threadIdx.x; a < assignments; a += blockDim.x) atomicAdd(&cnt[ids[a]], 1);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < experts; ++e) {
+      cur[e] = run;
+      eoff[e] = run;
+      run += cnt[e];
+    }
+    eoff[experts] = run;
+  }
+  __syncthreads();
+  for (int a = threadIdx.x; a < assignments; a += blockDim.x) order[atomicAdd(&cur[ids[a]], 1)] = a;
+}
+
+constexpr int kXWaves = 4;                 // waves per expert block, 32 weight rows each
+constexpr int kXRows = 32 * kXWaves;       // weight rows per expert block
+
+// Gate/up of expert blockIdx.y (blockIdx.y == experts: the shared expert over
+// all n tokens) for its assignments [32 bz, +32), rows [kXRows bx, +kXRows)
+// of width `width`. Epilogues (moe.hex:254-369): routed bf16((silu(bf16 g) * bf16 u) *
+// p_slot) into act[t][slot * inter + row]; shared bf16(bf16(bf16(silu(bf16 g))
+// * bf16 u) * sigmoid(l_E)) into act[t][top_k * inter + row].
+__global__ __launch_bounds__(64 * kXWaves) void k_mmoe_gate(
+    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate,
+    const uint16_t* __restrict__ up, const uint16_t* __restrict__ sgate,
+    const uint16_t* __restrict__ sup, const int* __restrict__ eoff, const int* __restrict__ order,
+    const float* __restrict__ probs, const float* __restrict__ logits, int experts, int top_k,
+    int inter, int shared_inter, int n, uint16_t* __restrict__ act) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.y;
+  const bool shared = e == experts;
+  const int width = shared ? shared_inter : inter;
+  const int begin = shared ? 0 : eoff[e];
+  const int count = shared ? n : eoff[e + 1] - begin;
+  const int r0 = blockIdx.x * kXRows + 32 * wave;
+  if (count == 0 || r0 >= width) return;  // uniform per wave; no barriers below
+  const int kq = 8 * (lane >> 5);
+  const int wrow = min(r0 + (lane & 31), width - 1);
+  const uint16_t* w[2];
+  w[0] = (shared ? sgate : gate + (size_t)e * inter * hidden) + (size_t)wrow * hidden + kq;
+  w[1] = (shared ? sup : up + (size_t)e * inter * hidden) + (size_t)wrow * hidden + kq;
+  const int act_rows = top_k * inter + shared_inter;
+  const int row = r0 + (lane & 31);
+  {
+    const int m0 = 32 * blockIdx.z;
+    if (m0 >= count) return;
+    const int i = min(m0 + (lane & 31), count - 1);
+    const int t = shared ? i : order[begin + i] / top_k;
+    f32x16_t acc[2];
+    mfma_tile<2, 2>(x + (size_t)t * hidden + kq, w, hidden, acc);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mi = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (mi >= count || row >= width) continue;
+      const float gb = rbf(acc[0][r]), ub = rbf(acc[1][r]);
+      const float activated = silu(gb);
+      if (shared) {
+        const float shared_prob = sigmoid(logits[(size_t)mi * (experts + 1) + experts]);
+        act[(size_t)mi * act_rows + top_k * inter + row] = f2bf(rbf(rbf(activated) * ub) * shared_prob);
+      } else {
+        const int a = order[begin + mi];
+        const int ta = a / top_k, slot = a - ta * top_k;
+        act[(size_t)ta * act_rows + slot * inter + row] = f2bf((activated * ub) * probs[a]);
+      }
+    }
+  }
+}
+
+// Down of expert blockIdx.y (== experts: the shared expert) for its
+// assignments [32 bz, +32): F32 part[a][o] = sum_i act[t][slot * inter + i] down[e][o][i]
+// (shared: spart[t][o] over act[t][top_k * inter + i]), rows o in
+// [kXRows bx, +kXRows) of hidden.
+__global__ __launch_bounds__(64 * kXWaves) void k_mmoe_down(
+    const uint16_t* __restrict__ act, const uint16_t* __restrict__ down,
+    const uint16_t* __restrict__ sdown, const int* __restrict__ eoff, const int* __restrict__ order,
+    int experts, int top_k, int inter, int shared_inter, int hidden, int n, float* __restrict__ part,
+    float* __restrict__ spart) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.y;
+  const bool shared = e == experts;
+  const int width = shared ? shared_inter : inter;  // the product's k extent
+  const int begin = shared ? 0 : eoff[e];
+  const int count = shared ? n : eoff[e + 1] - begin;
+  const int o0 = blockIdx.x * kXRows + 32 * wave;
+  if (count == 0 || o0 >= hidden) return;  // uniform per wave; no barriers below
+  const int kq = 8 * (lane >> 5);
+  const int orow = min(o0 + (lane & 31), hidden - 1);
+  const uint16_t* w[1];
+  w[0] = (shared ? sdown : down + (size_t)e * hidden * inter) + (size_t)orow * width + kq;
+  const int act_rows = top_k * inter + shared_inter;
+  const int o = o0 + (lane & 31);
+  {
+    const int m0 = 32 * blockIdx.z;
+    if (m0 >= count) return;
+    const int i = min(m0 + (lane & 31), count - 1);
+    size_t arow;
+    if (shared) {
+      arow = (size_t)i * act_rows + top_k * inter;
+    } else {
+      const int a = order[begin + i];
+      const int ta = a / top_k;
+      arow = (size_t)ta * act_rows + (size_t)(a - ta * top_k) * inter;
+    }
+    f32x16_t acc[1];
+    mfma_tile<4, 1>(act + arow + kq, w, width, acc);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int mi = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      if (mi >= count || o >= hidden) continue;
+      if (shared) spart[(size_t)mi * hidden + o] = acc[0][r];
+      else part[(size_t)order[begin + mi] * hidden + o] = acc[0][r];
+    }
+  }
+}
+
+// out[t][o] = bf16(bf16(routed + res) (+) bf16(shared)) with routed summed
+// over the slots in slot order (the epilogue of moe.hex:371-471).
+__global__ __launch_bounds__(kBlock) void k_moe_combine(const float* __restrict__ part,
+                                                        const float* __restrict__ spart,
+                                                        const uint16_t* __restrict__ res, int hidden,
+                                                        int top_k, uint16_t* __restrict__ out) {
+  const int t = blockIdx.y;
+  for (int o = blockIdx.x * kBlock + threadIdx.x; o < hidden; o += gridDim.x * kBlock) {
+    const float* p = part + (size_t)t * top_k * hidden + o;
+    float routed = p[0];
+    for (int slot = 1; slot < top_k; ++slot) routed += p[(size_t)slot * hidden];
+    const size_t i = (size_t)t * hidden + o;
+    out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(spart[i]));
+  }
+}
+
+}  // namespace cq35

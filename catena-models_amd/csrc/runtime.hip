@@ -22,6 +22,7 @@
 #include "layers.h"
 #include "mega.h"
 #include "prefill.h"
+#include "mfma.h"
 
 using namespace cq35;
 
@@ -473,8 +474,11 @@ struct cq35_session {
   uint16_t *pf_a = nullptr, *pf_b = nullptr, *pf_c = nullptr, *pf_d = nullptr;
   uint16_t *pf_e = nullptr, *pf_f = nullptr, *pf_g = nullptr, *pf_act = nullptr;
   float *pf_rope = nullptr, *pf_logits = nullptr, *pf_probs = nullptr, *pf_scratch = nullptr;
+  float *pf_part = nullptr, *pf_spart = nullptr;  // matrix-core experts: routed / shared down sums
+  int *pf_eoff = nullptr, *pf_order = nullptr;    // matrix-core experts: buckets
   int* pf_ids = nullptr;
   int pf_attn_tokens = 0;  // tokens per staged-attention launch (scratch rows)
+  int matrix = 0;          // CQ35_MATRIX_* components of multi-token calls on MFMA
   // kernel timing
   int timed_class = -1;
   hipEvent_t ev[2 * kMaxTimedEvents] = {};
@@ -1046,6 +1050,10 @@ int setup_prefill(cq35_session* s) {
     check(dalloc(s, &s->pf_logits, m * (d.E + 1)));
     check(dalloc(s, &s->pf_ids, m * d.K));
     check(dalloc(s, &s->pf_probs, m * d.K));
+    check(dalloc(s, &s->pf_eoff, d.E + 2));
+    check(dalloc(s, &s->pf_order, m * d.K));
+    check(dalloc(s, &s->pf_part, m * d.K * d.H));
+    check(dalloc(s, &s->pf_spart, m * d.H));
   }
   // staged attention scratch rows, at most 64 MiB
   const int64_t per_token = d.Q * (int64_t)s->attn_stride;
@@ -1077,15 +1085,27 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
     const unsigned tiles = (unsigned)((rows_n + 4 * kBTokens - 1) / (4 * kBTokens));
     L(KC_EMBED, k_bembed, dim3(rows_n), dim3(kBlock), 0, params, first, (const uint16_t*)Wt(0), H,
       s->pf_h, c0 + rows_n == n ? s->d_best : (unsigned long long*)nullptr);
+    // matrix-core projections when selected (K a multiple of the MFMA step)
+    const bool mp = (s->matrix & CQ35_MATRIX_PROJECTIONS) != 0;
+    const unsigned mtiles = (unsigned)((rows_n + kMBlockTokens - 1) / kMBlockTokens);
+    auto mgrid = [&](int rows) { return dim3((unsigned)((rows + kMRows - 1) / kMRows), mtiles); };
     auto project = [&](const uint16_t* x, int cols, const void* w, int rows, uint16_t* out) {
-      L(KC_PREFILL_PROJECT, k_bproject<kBPlain>, dim3((unsigned)rows, tiles), dim3(kBlock), 0, x,
-        rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr,
-        out);
+      if (mp && cols % 16 == 0)
+        L(KC_PREFILL_PROJECT, k_mproject<kBPlain>, mgrid(rows), dim3(64 * kMWaves), 0, x, rows_n, cols,
+          (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr, out);
+      else
+        L(KC_PREFILL_PROJECT, k_bproject<kBPlain>, dim3((unsigned)rows, tiles), dim3(kBlock), 0, x,
+          rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr,
+          out);
     };
     auto residual_rows = [&](const uint16_t* x, int cols, const void* w, const uint16_t* res,
                              uint16_t* out) {
-      L(KC_PREFILL_PROJECT, k_bproject<kBResidual>, dim3((unsigned)H, tiles), dim3(kBlock), 0, x,
-        rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
+      if (mp && cols % 16 == 0)
+        L(KC_PREFILL_PROJECT, k_mproject<kBResidual>, mgrid(H), dim3(64 * kMWaves), 0, x, rows_n, cols,
+          (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
+      else
+        L(KC_PREFILL_PROJECT, k_bproject<kBResidual>, dim3((unsigned)H, tiles), dim3(kBlock), 0, x,
+          rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
     };
     auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
       L(KC_PROJECT, k_bnorm, dim3(rows_n), dim3(kBlock), (size_t)H * 2, x, (const float*)w, H,
@@ -1158,17 +1178,41 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         L(KC_ROUTER, k_bselect, dim3(rows_n), dim3(kBlock), (size_t)E * 4,
           (const float*)s->pf_logits, E, K, s->pf_ids, s->pf_probs);
         const int rows = K * I + SI;
-        L(KC_MOE_GATE, k_bmoe_gate, dim3((unsigned)((rows + 3) / 4), rows_n), dim3(kBlock), 0,
-          (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
-          (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
-          (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
-        L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)((H + 3) / 4), rows_n), dim3(kBlock), 0,
-          (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
-          (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, s->pf_h);
+        if ((s->matrix & CQ35_MATRIX_EXPERTS) && H % 16 == 0 && I % 16 == 0 && SI % 16 == 0) {
+          const int A = rows_n * K;
+          L(KC_ROUTER, k_moe_bucket, dim3(1), dim3(1024), (size_t)E * 2 * sizeof(int),
+            (const int*)s->pf_ids, A, E, s->pf_eoff, s->pf_order);
+          const unsigned mt = (unsigned)((rows_n + 31) / 32);  // token tiles of the busiest expert at most
+          L(KC_MOE_GATE, k_mmoe_gate, dim3((unsigned)((std::max(I, SI) + kXRows - 1) / kXRows), (unsigned)(E + 1), mt),
+            dim3(64 * kXWaves), 0, (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1),
+            (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6),
+            (const int*)s->pf_eoff, (const int*)s->pf_order, (const float*)s->pf_probs,
+            (const float*)s->pf_logits, E, K, I, SI, rows_n, s->pf_act);
+          L(KC_MOE_DOWN, k_mmoe_down, dim3((unsigned)((H + kXRows - 1) / kXRows), (unsigned)(E + 1), mt),
+            dim3(64 * kXWaves), 0, (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3),
+            (const uint16_t*)W(ffn + 7), (const int*)s->pf_eoff, (const int*)s->pf_order, E, K, I, SI, H,
+            rows_n, s->pf_part, s->pf_spart);
+          L(KC_MOE_DOWN, k_moe_combine, dim3((unsigned)((H + kBlock - 1) / kBlock), (unsigned)rows_n),
+            dim3(kBlock), 0, (const float*)s->pf_part, (const float*)s->pf_spart,
+            (const uint16_t*)s->pf_attn, H, K, s->pf_h);
+        } else {
+          L(KC_MOE_GATE, k_bmoe_gate, dim3((unsigned)((rows + 3) / 4), rows_n), dim3(kBlock), 0,
+            (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
+            (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
+            (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
+          L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)((H + 3) / 4), rows_n), dim3(kBlock), 0,
+            (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
+            (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, s->pf_h);
+        }
       } else {
-        L(KC_PREFILL_PROJECT, k_bproject<kBGate>, dim3((unsigned)d.I, tiles), dim3(kBlock), 0,
-          (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
-          (int)d.I, (const uint16_t*)nullptr, s->pf_act);
+        if (mp && H % 16 == 0)
+          L(KC_PREFILL_PROJECT, k_mproject<kBGate>, mgrid((int)d.I), dim3(64 * kMWaves), 0,
+            (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
+            (int)d.I, (const uint16_t*)nullptr, s->pf_act);
+        else
+          L(KC_PREFILL_PROJECT, k_bproject<kBGate>, dim3((unsigned)d.I, tiles), dim3(kBlock), 0,
+            (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
+            (int)d.I, (const uint16_t*)nullptr, s->pf_act);
         residual_rows(s->pf_act, (int)d.I, W(ffn + 2), s->pf_attn, s->pf_h);
       }
       base += layer_tensors(c, l);
@@ -1253,6 +1297,20 @@ extern "C" int cq35_session_set_persistent(cq35_session* s, int enabled) {
   if (enabled && !s->mega_ok)
     return fail(CQ35_EUNSUPPORTED, "this model shape or capacity is outside the persistent decode kernel");
   s->mega_on = enabled != 0;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_set_matrix_prefill(cq35_session* s, int components) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  if (components & ~(CQ35_MATRIX_PROJECTIONS | CQ35_MATRIX_EXPERTS))
+    return fail(CQ35_EINVAL, "unknown matrix-core prefill components %d", components);
+  s->matrix = components;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_matrix_prefill(const cq35_session* s, int* components) {
+  if (!s || !components) return fail(CQ35_EINVAL, "null argument");
+  *components = s->matrix;
   return CQ35_OK;
 }
 
@@ -1533,5 +1591,29 @@ extern "C" int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t ro
   if (dw) hipFree(dw);
   if (dout) hipFree(dout);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "device GEMV: %s", hipGetErrorString(e));
+  return CQ35_OK;
+}
+
+extern "C" int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, int64_t n, int64_t rows,
+                                       int64_t cols, uint16_t* out) {
+  if (!x || !w || !out || n <= 0 || rows <= 0 || cols <= 0 || cols % 16 || n > (1 << 20) ||
+      rows > (1 << 20) || cols > 65536)
+    return fail(CQ35_EINVAL, "bad matrix GEMM shape");
+  uint16_t *dx = nullptr, *dw = nullptr, *dout = nullptr;
+  hipError_t e = hipMalloc(&dx, n * cols * 2);
+  if (e == hipSuccess) e = hipMalloc(&dw, rows * cols * 2);
+  if (e == hipSuccess) e = hipMalloc(&dout, n * rows * 2);
+  if (e == hipSuccess) e = hipMemcpy(dx, x, n * cols * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dw, w, rows * cols * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    const dim3 grid((unsigned)((rows + kMRows - 1) / kMRows), (unsigned)((n + kMBlockTokens - 1) / kMBlockTokens));
+    k_mproject<kBPlain><<<grid, 64 * kMWaves>>>(dx, (int)n, (int)cols, dw, nullptr, (int)rows, nullptr, dout);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(out, dout, n * rows * 2, hipMemcpyDeviceToHost);
+  if (dx) hipFree(dx);
+  if (dw) hipFree(dw);
+  if (dout) hipFree(dout);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "device matrix GEMM: %s", hipGetErrorString(e));
   return CQ35_OK;
 }

@@ -158,6 +158,19 @@ int cq35_session_set_graph(cq35_session* session, int enabled);
 int cq35_session_set_persistent(cq35_session* session, int enabled);
 int cq35_session_persistent(const cq35_session* session, int* enabled);
 
+/* Matrix-core prefill: components of multi-token calls run on MFMA, whose
+ * F32 accumulation order is the hardware's, so results match the exact path
+ * to accumulation rounding rather than bit for bit. Replaces the reference's
+ * InferenceOptions::wmma_prefill with CATENA_WMMA_COMPONENTS (catena.rs:12-26,
+ * qwen35.rs:467-541; default off in its library API, as here). Bit 0: the
+ * dense projections (attention, DeltaNet and output projections, dense FFN);
+ * bit 1: the MoE expert projections (grouped routed experts and the shared
+ * expert). 0 keeps the exact SIMT path. Decode steps are unaffected. */
+#define CQ35_MATRIX_PROJECTIONS 1
+#define CQ35_MATRIX_EXPERTS 2
+int cq35_session_set_matrix_prefill(cq35_session* session, int components);
+int cq35_session_matrix_prefill(const cq35_session* session, int* components);
+
 /* Host-side builds of the device numerics (same source), for CPU checks. */
 float cq35_numeric_exp(float x);
 float cq35_numeric_sqrt(float x);
@@ -170,6 +183,11 @@ int cq35_device_numeric(int op, const float* input, float* output, int64_t count
  * BF16 matrix: out[r] = bf16(tree_W(x . w_r)). Host arrays. */
 int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
                      int width, uint16_t* out);
+/* Device matrix-core product of the prefill projections over host arrays:
+ * out[t][r] = bf16(sum_k x[t][k] w[r][k]) (MFMA accumulation order), x
+ * [n][cols], w [rows][cols], cols a multiple of 16. */
+int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, int64_t n, int64_t rows,
+                            int64_t cols, uint16_t* out);
 
 #ifdef __cplusplus
 }
