@@ -93,6 +93,28 @@ __device__ __forceinline__ float lane_down(float v) {
   }
 }
 
+// Halving tree over 64 reference lanes held one per physical lane
+// (strides 32 ... 1); result in lane 0.
+__device__ __forceinline__ float tree64_lanes(float v) {
+  v += lane_down<32>(v);
+  v += lane_down<16>(v);
+  v += lane_down<8>(v);
+  v += lane_down<4>(v);
+  v += lane_down<2>(v);
+  v += lane_down<1>(v);
+  return v;
+}
+// Halving tree over 32 reference lanes per half wave (strides 16 ... 1);
+// results in lanes 0 and 32.
+__device__ __forceinline__ float tree32_lanes(float v) {
+  v += lane_down<16>(v);
+  v += lane_down<8>(v);
+  v += lane_down<4>(v);
+  v += lane_down<2>(v);
+  v += lane_down<1>(v);
+  return v;
+}
+
 // Halving tree of width W = 4*LPR over the reference lanes held by the LPR
 // physical lanes of a row group (reference stride 4s = physical stride s,
 // then strides 2 and 1 inside the lane). Must be reached by every lane of

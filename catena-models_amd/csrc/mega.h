@@ -392,27 +392,6 @@ __device__ __forceinline__ void pair_acc(float& lo, float& hi, uint32_t x, uint3
   hi += hi2f(x) * hi2f(w);
 }
 
-// Halving tree over 64 reference lanes held one per physical lane
-// (strides 32 ... 1); result in lane 0.
-__device__ __forceinline__ float tree64_lanes(float v) {
-  v += lane_down<32>(v);
-  v += lane_down<16>(v);
-  v += lane_down<8>(v);
-  v += lane_down<4>(v);
-  v += lane_down<2>(v);
-  v += lane_down<1>(v);
-  return v;
-}
-// Halving tree over 32 reference lanes per half wave (strides 16 ... 1);
-// results in lanes 0 and 32.
-__device__ __forceinline__ float tree32_lanes(float v) {
-  v += lane_down<16>(v);
-  v += lane_down<8>(v);
-  v += lane_down<4>(v);
-  v += lane_down<2>(v);
-  v += lane_down<1>(v);
-  return v;
-}
 
 // -------------------------------------------------- phase: S256 projection
 

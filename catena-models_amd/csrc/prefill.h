@@ -200,68 +200,107 @@ __global__ __launch_bounds__(kBlock) void k_bhistory(const uint16_t* __restrict_
 // DeltaNet scan over the chunk's tokens with the F32 state in registers
 // (batch.scan, batch_scan.hex:1-200): per token exactly the single-step
 // arithmetic of k_delta (32 lanes per value channel, lane l owns key elements
-// l, l+32, ...; serial from 0.0, 32-wide halving tree), 8 channels per block.
-// Requires key_dim <= 256.
+// l, l+32, ...; serial from 0.0, 32-wide halving tree), 8 channels of one
+// head per block. Requires key_dim <= 256 and value_dim % 8 == 0.
+//
+// The serial chain reads only LDS: per stage of kScanTokens tokens the
+// block first stages the head's k and q rows (lane-major, lane l's elements
+// l + 32 j contiguous), its channels' values, and every token's decay and
+// rate (computed in parallel: they do not depend on the state).
+constexpr int kScanTokens = 64;
+
+__host__ __device__ constexpr size_t bscan_lds_bytes(int key_dim) {
+  return (size_t)kScanTokens * key_dim * 2 * 2 + (size_t)kScanTokens * (2 + 8) * 4;
+}
+
+template <int KJ>  // key elements per lane: key_dim / 32
 __global__ __launch_bounds__(kBlock) void k_bscan(
     const uint16_t* __restrict__ conv, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ alpha,
     const uint16_t* __restrict__ beta, const float* __restrict__ dt, const float* __restrict__ a,
     float* __restrict__ state, int m, int value_size, int value_dim, int value_heads, int key_dim,
     int key_heads, int qkv_size, float scale, uint16_t* __restrict__ out) {
-  const int c = blockIdx.x * 8 + (threadIdx.x >> 5);
-  const int lane = threadIdx.x & 31;
+  extern __shared__ __align__(16) unsigned char scan_lds[];
+  uint16_t* sk = reinterpret_cast<uint16_t*>(scan_lds);
+  uint16_t* sq = sk + kScanTokens * key_dim;
+  float* sdecay = reinterpret_cast<float*>(sq + kScanTokens * key_dim);
+  float* srate = sdecay + kScanTokens;
+  float* sval = srate + kScanTokens;  // [token][8]
+  const int c0 = blockIdx.x * 8;
+  const int ch = threadIdx.x >> 5;
+  const int c = c0 + ch;
+  const int lane = threadIdx.x & 31, half = (threadIdx.x >> 5) & 1;
   const bool valid = c < value_size;
   const int cc = valid ? c : 0;
-  const int head = cc / value_dim;
+  const int head = min(c0, value_size - 1) / value_dim;
   const int kbase = (head % key_heads) * key_dim;
   const int key_size = key_heads * key_dim;
+  constexpr int kj = KJ;
   const float dth = dt[head], ah = a[head];
-  float s[8];
+  float s[KJ];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = lane + 32 * j;
-    s[j] = i < key_dim ? state[(size_t)cc * key_dim + i] : 0.0f;
-  }
-  for (int t = 0; t < m; ++t) {
-    const uint16_t* kt = k + (size_t)t * key_size + kbase;
-    const uint16_t* qt = q + (size_t)t * key_size + kbase;
-    const float time_step = softplus(bf2f(alpha[(size_t)t * value_heads + head]) + dth);
-    const float decay = hexp(rbf(time_step * ah));
-    const float rate = rbf(sigmoid(bf2f(beta[(size_t)t * value_heads + head])));
-    float kv[8];
-    float acc = 0.0f;
+  for (int j = 0; j < KJ; ++j) s[j] = state[(size_t)cc * key_dim + lane + 32 * j];
+  for (int t0 = 0; t0 < m; t0 += kScanTokens) {
+    const int ts = min(kScanTokens, m - t0);
+    // stage: k and q rows lane-major, values, decay and rate
+    const int quads = key_dim >> 3;
+    for (int idx = threadIdx.x; idx < ts * quads; idx += blockDim.x) {
+      const int tt = idx / quads, qd = idx - tt * quads;
+      const size_t src = (size_t)(t0 + tt) * key_size + kbase + 8 * qd;
+      const u32x4 kq4 = *reinterpret_cast<const u32x4*>(k + src);
+      const u32x4 qq4 = *reinterpret_cast<const u32x4*>(q + src);
+      const uint32_t kw[4] = {kq4.x, kq4.y, kq4.z, kq4.w}, qw[4] = {qq4.x, qq4.y, qq4.z, qq4.w};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = lane + 32 * j;
-      if (i < key_dim) {
-        kv[j] = bf2f(kt[i]);
-        acc += s[j] * kv[j];
+      for (int e = 0; e < 8; ++e) {
+        const int i = 8 * qd + e;
+        const int dst = tt * key_dim + (i & 31) * kj + (i >> 5);
+        sk[dst] = (uint16_t)(kw[e >> 1] >> (16 * (e & 1)));
+        sq[dst] = (uint16_t)(qw[e >> 1] >> (16 * (e & 1)));
       }
     }
+    for (int idx = threadIdx.x; idx < ts * 8; idx += blockDim.x) {
+      const int tt = idx >> 3, cv = min(c0 + (idx & 7), value_size - 1);
+      sval[idx] = bf2f(conv[(size_t)(t0 + tt) * qkv_size + 2 * key_size + cv]);
+    }
+    if (threadIdx.x < ts) {
+      const int t = t0 + threadIdx.x;
+      const float time_step = softplus(bf2f(alpha[(size_t)t * value_heads + head]) + dth);
+      sdecay[threadIdx.x] = hexp(rbf(time_step * ah));
+      srate[threadIdx.x] = rbf(sigmoid(bf2f(beta[(size_t)t * value_heads + head])));
+    }
+    __syncthreads();
+    for (int tt = 0; tt < ts; ++tt) {
+      const uint16_t* kr = sk + tt * key_dim + lane * kj;
+      const uint16_t* qr = sq + tt * key_dim + lane * kj;
+      float kv[KJ], qv[KJ];
 #pragma unroll
-    for (int st = 16; st >= 1; st >>= 1) acc += __shfl_down(acc, st, 32);
-    const float total = __shfl(acc, 0, 32);
-    const float value = bf2f(conv[(size_t)t * qkv_size + 2 * key_size + cc]);
-    const float delta = (value - total * decay) * rate;
-    float acc2 = 0.0f;
+      for (int j = 0; j < KJ; ++j) {
+        kv[j] = bf2f(kr[j]);
+        qv[j] = bf2f(qr[j]);
+      }
+      float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = lane + 32 * j;
-      if (i < key_dim) {
+      for (int j = 0; j < KJ; ++j) acc += s[j] * kv[j];
+      acc = tree32_lanes(acc);
+      const float t_lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+      const float t_hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 32));
+      const float total = half ? t_hi : t_lo;
+      const float decay = sdecay[tt];
+      const float delta = (sval[tt * 8 + ch] - total * decay) * srate[tt];
+      float acc2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
         s[j] = s[j] * decay + kv[j] * delta;
-        acc2 += s[j] * bf2f(qt[i]);
+        acc2 += s[j] * qv[j];
       }
+      acc2 = tree32_lanes(acc2);
+      if (lane == 0 && valid) out[(size_t)(t0 + tt) * value_size + c] = f2bf(acc2 * scale);
     }
-#pragma unroll
-    for (int st = 16; st >= 1; st >>= 1) acc2 += __shfl_down(acc2, st, 32);
-    if (lane == 0 && valid) out[(size_t)t * value_size + c] = f2bf(acc2 * scale);
+    __syncthreads();
   }
   if (valid) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = lane + 32 * j;
-      if (i < key_dim) state[(size_t)c * key_dim + i] = s[j];
-    }
+    for (int j = 0; j < KJ; ++j) state[(size_t)c * key_dim + lane + 32 * j] = s[j];
   }
 }
 

@@ -1019,6 +1019,10 @@ const char* prefill_unsupported(const cq35_model& m) {
   const cq35_config& c = m.cfg;
   if (d.H % 8 || d.QS % 8 || d.VS % 8) return "hidden, query and value widths must be multiples of 8";
   if (c.key_dim > 256) return "key_dim above 256";
+  if (c.key_dim != 32 && c.key_dim != 64 && c.key_dim != 128 && c.key_dim != 256)
+    return "key_dim must be 32, 64, 128 or 256";
+  if (c.value_dim % 8) return "value_dim must be a multiple of 8 (eight channels of one head per scan block)";
+  if (bscan_lds_bytes(c.key_dim) > 65536) return "key_dim too large for the scan's LDS stage";
   if (d.I % 8) return "intermediate width must be a multiple of 8";
   if (c.moe && (d.SI % 8 || d.SI > d.K * d.I))
     return "shared-expert width must be a multiple of 8 and at most top_k * intermediate";
@@ -1159,7 +1163,11 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
           dim3(kBlock), 0, (const uint16_t*)qkv, rows_n, s->cache, conv_base, params, first,
           (int)d.QKV);
         const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
-        L(KC_DELTA, k_bscan, dim3((unsigned)((d.VS + 7) / 8)), dim3(kBlock), 0,
+        auto scan = k_bscan<4>;  // key elements per lane: key_dim / 32
+        if (c.key_dim == 32) scan = k_bscan<1>;
+        else if (c.key_dim == 64) scan = k_bscan<2>;
+        else if (c.key_dim == 256) scan = k_bscan<8>;
+        L(KC_DELTA, scan, dim3((unsigned)((d.VS + 7) / 8)), dim3(kBlock), bscan_lds_bytes(c.key_dim),
           (const uint16_t*)conv, (const uint16_t*)qn, (const uint16_t*)kn, (const uint16_t*)alpha,
           (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), s->shadow + l * d.REC,
           rows_n, (int)d.VS, c.value_dim, VH, c.key_dim, c.key_heads, (int)d.QKV, scale, core);
