@@ -248,6 +248,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=25.0)
     ap.add_argument("--prompt-per-token", action="store_true",
                     help="append the prompt one token per call instead of one batched call")
+    ap.add_argument("--no-matrix-prefill", action="store_true",
+                    help="skip the matrix-core prefill measurement")
     ap.add_argument("--long-context", type=int, default=32768,
                     help="cached positions of the long-context decode leg (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=128)
@@ -300,6 +302,23 @@ def main() -> int:
                    tokens_per_s=round(args.context / prefill_s, 1) if prefill_s > 0 else None,
                    path="batched prefill, one call" if batched_prompt else "one token per call")
     log(f"prompt of {args.context} tokens ({prefill['path']}) in {prefill_s:.3f}s")
+    if batched_prompt and not args.no_matrix_prefill:
+        # the same prompt on a second session with the matrix-core components
+        # (MFMA accumulation order; the decode below runs on the exact session)
+        ms_ = model.session(args.context + 1)
+        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS)
+        ms_.append_next_token(tokens[:args.context])  # warm the kernels
+        ms_ = model.session(args.context + 1)
+        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS)
+        device_sync()
+        t0 = time.perf_counter()
+        ms_.append_next_token(tokens[:args.context])
+        device_sync()
+        mp_s = time.perf_counter() - t0
+        del ms_
+        prefill["matrix_core"] = dict(seconds=round(mp_s, 4), tokens_per_s=round(args.context / mp_s, 1),
+                                      components="projections+experts (MFMA accumulation order)")
+        log(f"prompt of {args.context} tokens, matrix-core prefill: {mp_s:.3f}s")
     base = args.context
     nxt = tokens[base]
     for _ in range(args.warmup):
