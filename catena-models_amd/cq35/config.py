@@ -92,6 +92,13 @@ def to_c(cfg: dict) -> CConfig:
     return c
 
 
+def from_c(c: CConfig) -> dict:
+    out = {name: getattr(c, name) for name, _ in FIELDS}
+    out["eps"] = float(c.eps)
+    out["theta"] = float(c.theta)
+    return out
+
+
 def derived(cfg: dict) -> dict:
     """Derived sizes (src/spec.rs:293-362)."""
     ks = cfg["key_heads"] * cfg["key_dim"]

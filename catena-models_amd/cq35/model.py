@@ -23,7 +23,7 @@ import numpy as np
 
 from . import _lib
 from ._lib import CQ35Error, check
-from .config import CConfig, preset, to_c
+from .config import CConfig, from_c, preset, to_c
 
 
 class Model:
@@ -43,6 +43,18 @@ class Model:
         return cls(out.value, cfg)
 
     @classmethod
+    def load_gguf(cls, path: str) -> "Model":
+        """A GGUF checkpoint (one file, any shard of a set, or a directory):
+        configuration from its metadata, tensors checked against weight_specs
+        and copied into HBM (Model::load_gguf, src/model.rs:43, 81-153)."""
+        lib = _lib.load()
+        out = ctypes.c_void_p()
+        check(lib.cq35_model_load_gguf(str(path).encode(), ctypes.byref(out)))
+        m = cls(out.value, {})
+        m.cfg = m.config()
+        return m
+
+    @classmethod
     def from_arrays(cls, cfg: dict, arrays: Sequence[np.ndarray]) -> "Model":
         """Upload host tensors given in weight_specs order (src/spec.rs:443-712)."""
         lib = _lib.load()
@@ -58,6 +70,11 @@ class Model:
         if getattr(self, "_h", None) and self._h.value:
             _lib.load().cq35_model_free(self._h)
             self._h = ctypes.c_void_p()
+
+    def config(self) -> dict:
+        c = CConfig()
+        check(_lib.load().cq35_model_config(self._h, ctypes.byref(c)))
+        return from_c(c)
 
     def __del__(self):
         try:
@@ -109,6 +126,28 @@ def weight_info(cfg: dict, index: int):
     c = to_c(cfg)
     check(_lib.load().cq35_weight_info(ctypes.byref(c), index, ctypes.byref(info)))
     return info
+
+
+def gguf_config(path: str) -> dict:
+    """Model configuration from GGUF metadata (read_gguf_model_config,
+    src/checkpoint.rs:376-404); no GPU needed."""
+    c = CConfig()
+    check(_lib.load().cq35_gguf_config(str(path).encode(), ctypes.byref(c)))
+    return from_c(c)
+
+
+def gguf_validate(path: str, cfg: dict | None = None) -> None:
+    """validate_gguf_tensors (src/checkpoint.rs:406-414): raises CQ35Error
+    when the inventory, a shape, a dtype or a byte range is wrong."""
+    c = to_c(cfg) if cfg is not None else None
+    check(_lib.load().cq35_gguf_validate(str(path).encode(), ctypes.byref(c) if c is not None else None))
+
+
+def gguf_tensor_name(cfg: dict, index: int) -> str:
+    buf = ctypes.create_string_buffer(256)
+    c = to_c(cfg)
+    check(_lib.load().cq35_gguf_tensor_name(ctypes.byref(c), index, buf, 256))
+    return buf.value.decode()
 
 
 def weight_count(cfg: dict) -> int:

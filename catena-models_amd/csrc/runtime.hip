@@ -23,6 +23,7 @@
 #include "mega.h"
 #include "prefill.h"
 #include "mfma.h"
+#include "gguf.h"
 
 using namespace cq35;
 
@@ -170,6 +171,87 @@ bool describe(const cq35_config& c, int64_t index, TensorDesc* t) {
         case 5: return set(CQ35_BF16, d.SI, d.H, kMatrix);
         case 6: return set(CQ35_BF16, d.SI, d.H, kMatrix);
         case 7: return set(CQ35_BF16, d.H, d.SI, kMatrix);
+        default: return false;
+      }
+    }
+    base += n;
+  }
+  return false;
+}
+
+// GGUF name, reference shape (outermost first) and dtype of tensor `index`
+// in weight_specs order (src/spec.rs:443-712: gguf_name and shape).
+bool gguf_spec(const cq35_config& c, int64_t index, std::string* name, std::vector<uint64_t>* dims,
+               int32_t* dtype) {
+  TensorDesc t;
+  if (!describe(c, index, &t)) return false;
+  *dtype = t.dtype;
+  const Dims d = dims_of(c);
+  const int64_t total = weight_count(c);
+  auto set = [&](const std::string& n, std::vector<uint64_t> sh) {
+    *name = n;
+    *dims = std::move(sh);
+    return true;
+  };
+  const uint64_t H = d.H, V = d.V;
+  if (index == 0) return set("token_embd.weight", {V, H});
+  if (index == total - 2) return set("output_norm.weight", {H});
+  if (index == total - 1) return set(c.tied ? "token_embd.weight" : "output.weight", {V, H});
+  int64_t base = 1;
+  for (int64_t l = 0; l < c.layers; ++l) {
+    const int n = layer_tensors(c, l);
+    if (index < base + n) {
+      const int s = (int)(index - base);
+      const std::string b = "blk." + std::to_string(l) + ".";
+      if (s == 0) return set(b + "attn_norm.weight", {H});
+      int ffn;
+      if (is_full(c, l)) {
+        switch (s) {
+          case 1: return set(b + "attn_q.weight", {(uint64_t)(2 * d.QS), H});
+          case 2: return set(b + "attn_k.weight", {(uint64_t)d.KVS, H});
+          case 3: return set(b + "attn_v.weight", {(uint64_t)d.KVS, H});
+          case 4: return set(b + "attn_output.weight", {H, (uint64_t)d.QS});
+          case 5: return set(b + "attn_q_norm.weight", {(uint64_t)d.HD});
+          case 6: return set(b + "attn_k_norm.weight", {(uint64_t)d.HD});
+          case 7: return set(b + "post_attention_norm.weight", {H});
+          default: break;
+        }
+        ffn = s - 8;
+      } else {
+        const uint64_t VH = (uint64_t)c.value_heads;
+        switch (s) {
+          case 1: return set(b + "attn_qkv.weight", {(uint64_t)d.QKV, H});
+          case 2: return set(b + "attn_gate.weight", {(uint64_t)d.VS, H});
+          case 3: return set(b + "ssm_alpha.weight", {VH, H});
+          case 4: return set(b + "ssm_beta.weight", {VH, H});
+          case 5: return set(b + "ssm_dt.bias", {VH});
+          case 6: return set(b + "ssm_a", {VH});
+          case 7: return set(b + "ssm_norm.weight", {(uint64_t)c.value_dim});
+          case 8: return set(b + "ssm_out.weight", {H, (uint64_t)d.VS});
+          case 9: return set(b + "ssm_conv1d.weight", {(uint64_t)d.QKV, 4});
+          case 10: return set(b + "post_attention_norm.weight", {H});
+          default: break;
+        }
+        ffn = s - 11;
+      }
+      const uint64_t I = d.I, E = d.E, SI = d.SI;
+      if (!c.moe) {
+        switch (ffn) {
+          case 0: return set(b + "ffn_gate.weight", {I, H});
+          case 1: return set(b + "ffn_up.weight", {I, H});
+          case 2: return set(b + "ffn_down.weight", {H, I});
+          default: return false;
+        }
+      }
+      switch (ffn) {
+        case 0: return set(b + "ffn_gate_inp.weight", {E, H});
+        case 1: return set(b + "ffn_gate_exps.weight", {E, I, H});
+        case 2: return set(b + "ffn_up_exps.weight", {E, I, H});
+        case 3: return set(b + "ffn_down_exps.weight", {E, H, I});
+        case 4: return set(b + "ffn_gate_inp_shexp.weight", {1, H});
+        case 5: return set(b + "ffn_gate_shexp.weight", {SI, H});
+        case 6: return set(b + "ffn_up_shexp.weight", {SI, H});
+        case 7: return set(b + "ffn_down_shexp.weight", {H, SI});
         default: return false;
       }
     }
@@ -328,6 +410,211 @@ extern "C" int cq35_model_create(const cq35_config* cfg, const void* const* weig
   rc = finish_model(m);
   if (rc) { cq35_model_free(m); return rc; }
   *out = m;
+  return CQ35_OK;
+}
+
+namespace {
+
+// parse_gguf_model_config (checkpoint.rs:422-639) for qwen35 / qwen35moe,
+// with read_gguf_model_config's tied-output and dtype checks (376-404).
+int gguf_config_of(const gguf::Checkpoint& ck, cq35_config* out, uint64_t* nextn) {
+  if (ck.arch.empty()) return fail(CQ35_EINVAL, "GGUF is missing general.architecture");
+  if (ck.arch != "qwen35" && ck.arch != "qwen35moe")
+    return fail(CQ35_EUNSUPPORTED, "GGUF architecture \"%s\" is outside this build (qwen35, qwen35moe)",
+                ck.arch.c_str());
+  const std::string a = ck.arch;
+  int rc = CQ35_OK;
+  auto get = [&](const char* key, bool required, bool want_float) -> gguf::Scalar {
+    auto it = ck.scalars.find(key);
+    if (it == ck.scalars.end()) {
+      if (required && !rc) rc = fail(CQ35_EINVAL, "GGUF is missing %s.%s", a.c_str(), key);
+      return gguf::Scalar{};
+    }
+    if (!want_float && it->second.is_float && !rc)
+      rc = fail(CQ35_EINVAL, "GGUF %s.%s is not an integer", a.c_str(), key);
+    return it->second;
+  };
+  auto has = [&](const char* key) { return ck.scalars.count(key) != 0; };
+  auto u = [&](const char* key) { return get(key, true, false).u; };
+  auto ou = [&](const char* key, uint64_t dflt) { return has(key) ? get(key, false, false).u : dflt; };
+  auto f = [&](const char* key) {
+    const gguf::Scalar s = get(key, true, true);
+    return s.is_float ? (float)s.f : (float)s.u;
+  };
+  const bool moe = a == "qwen35moe";
+  cq35_config c{};
+  c.moe = moe ? 1 : 0;
+  const uint64_t hidden = u("embedding_length"), heads = u("attention.head_count");
+  const uint64_t blocks = u("block_count"), nn = ou("nextn_predict_layers", 0);
+  if (rc) return rc;
+  if (nn >= blocks) return fail(CQ35_EINVAL, "GGUF next-token layer count must be smaller than block count");
+  if (!has("vocab_size") && !ck.has_tokens)
+    return fail(CQ35_EINVAL, "GGUF has neither %s.vocab_size nor tokenizer tokens", a.c_str());
+  const uint64_t vocab = has("vocab_size") ? u("vocab_size") : ck.token_count;
+  const uint64_t head_dim = has("attention.key_length") ? u("attention.key_length") : (heads ? hidden / heads : 0);
+  const uint64_t inter = moe ? u("expert_feed_forward_length") : u("feed_forward_length");
+  const uint64_t kv = u("attention.head_count_kv");
+  const float eps = f("attention.layer_norm_rms_epsilon"), theta = f("rope.freq_base");
+  const uint64_t rope = ou("rope.dimension_count", head_dim);
+  const uint64_t rank = u("ssm.time_step_rank"), inner = u("ssm.inner_size");
+  const uint64_t groups = u("ssm.group_count"), state = u("ssm.state_size");
+  const uint64_t conv = u("ssm.conv_kernel"), interval = u("full_attention_interval");
+  if (rc) return rc;
+  if (conv != 4) return fail(CQ35_EINVAL, "Qwen3.5 requires four convolution taps (GGUF has %llu)", (unsigned long long)conv);
+  if (rank == 0 || inner % rank) return fail(CQ35_EINVAL, "GGUF ssm.inner_size is not a multiple of ssm.time_step_rank");
+  auto i32 = [](uint64_t v) { return v > 0x7fffffffull ? (int32_t)-1 : (int32_t)v; };
+  c.vocab = i32(vocab);
+  c.hidden = i32(hidden);
+  c.intermediate = i32(inter);
+  c.layers = i32(blocks - nn);
+  c.q_heads = i32(heads);
+  c.kv_heads = i32(kv);
+  c.head_dim = i32(head_dim);
+  c.rope_dim = i32(rope);
+  c.eps = eps;
+  c.theta = theta;
+  c.experts = i32(ou("expert_count", 0));
+  c.top_k = i32(ou("expert_used_count", 0));
+  c.shared_intermediate = i32(ou("expert_shared_feed_forward_length", 0));
+  c.full_interval = i32(interval);
+  c.key_heads = i32(groups);
+  c.key_dim = i32(state);
+  c.value_heads = i32(rank);
+  c.value_dim = i32(inner / rank);
+  c.tied = ck.tensors.count("output.weight") ? 0 : 1;
+  for (const auto& kvp : ck.tensors)
+    if (kvp.second.type == gguf::kF16)
+      return fail(CQ35_EINVAL, "language GGUF weights must be BF16/F32 (%s is F16)", kvp.first.c_str());
+  rc = cq35_config_validate(&c);
+  if (rc) return rc;
+  *out = c;
+  if (nextn) *nextn = nn;
+  return CQ35_OK;
+}
+
+// validate_files + tensor_view (checkpoint.rs:659-820): the inventory equals
+// weight_specs' names (next-token layers aside), every tensor has its
+// reference shape and dtype and lies inside its file, and no two overlap.
+int gguf_check(const gguf::Checkpoint& ck, const cq35_config& c, uint64_t nextn,
+               std::vector<const void*>* pointers) {
+  const int64_t n = weight_count(c);
+  std::set<std::string> expected;
+  std::vector<std::string> names(n);
+  std::vector<std::vector<uint64_t>> dims(n);
+  std::vector<int32_t> dtypes(n);
+  for (int64_t i = 0; i < n; ++i) {
+    if (!gguf_spec(c, i, &names[i], &dims[i], &dtypes[i]))
+      return fail(CQ35_EINVAL, "no weight spec for tensor %lld", (long long)i);
+    expected.insert(names[i]);
+  }
+  auto auxiliary = [&](const std::string& name) {
+    if (nextn == 0 || name.compare(0, 4, "blk.") != 0) return false;
+    const size_t dot = name.find('.', 4);
+    if (dot == std::string::npos) return false;
+    const std::string num = name.substr(4, dot - 4);
+    if (num.empty() || !std::all_of(num.begin(), num.end(), [](char ch) { return ch >= '0' && ch <= '9'; }))
+      return false;
+    const uint64_t layer = std::stoull(num);
+    return layer >= (uint64_t)c.layers && layer < (uint64_t)c.layers + nextn;
+  };
+  std::string missing, unexpected;
+  int nm = 0, nu = 0;
+  for (const auto& e : expected)
+    if (!ck.tensors.count(e) && nm++ < 8) missing += (missing.empty() ? "" : ", ") + e;
+  for (const auto& kvp : ck.tensors)
+    if (!expected.count(kvp.first) && !auxiliary(kvp.first) && nu++ < 8)
+      unexpected += (unexpected.empty() ? "" : ", ") + kvp.first;
+  if (nm || nu)
+    return fail(CQ35_EINVAL, "GGUF tensor inventory mismatch: %d missing (%s), %d unexpected (%s)", nm,
+                missing.c_str(), nu, unexpected.c_str());
+  std::vector<std::vector<std::pair<uint64_t, uint64_t>>> ranges(ck.files.size());
+  pointers->assign(n, nullptr);
+  for (int64_t i = 0; i < n; ++i) {
+    const gguf::Tensor& t = ck.tensors.at(names[i]);
+    if (t.dims != dims[i]) {
+      std::string got, want;
+      for (uint64_t v : t.dims) got += (got.empty() ? "" : ",") + std::to_string(v);
+      for (uint64_t v : dims[i]) want += (want.empty() ? "" : ",") + std::to_string(v);
+      return fail(CQ35_EINVAL, "GGUF tensor %s has shape [%s], expected [%s]", names[i].c_str(), got.c_str(),
+                  want.c_str());
+    }
+    const uint32_t want_type = dtypes[i] == CQ35_BF16 ? gguf::kBF16 : gguf::kF32;
+    if (t.type != want_type)
+      return fail(CQ35_EINVAL, "GGUF tensor %s has dtype %u, expected %s", names[i].c_str(), t.type,
+                  dtypes[i] == CQ35_BF16 ? "BF16" : "F32");
+    uint64_t elements = 1;
+    for (uint64_t v : t.dims) elements *= v;
+    const uint64_t bytes = elements * (t.type == gguf::kF32 ? 4 : 2);
+    const gguf::File& f = *ck.files[t.file];
+    if (t.offset > f.size || bytes > f.size - t.offset)
+      return fail(CQ35_EINVAL, "GGUF tensor %s range exceeds the length of %s", names[i].c_str(), f.path.c_str());
+    ranges[t.file].emplace_back(t.offset, t.offset + bytes);
+    (*pointers)[i] = f.base + t.offset;
+  }
+  for (size_t fi = 0; fi < ranges.size(); ++fi) {
+    auto& r = ranges[fi];
+    std::sort(r.begin(), r.end());
+    r.erase(std::unique(r.begin(), r.end()), r.end());  // the tied head names the embedding again
+    for (size_t k = 1; k < r.size(); ++k)
+      if (r[k - 1].second > r[k].first)
+        return fail(CQ35_EINVAL, "GGUF tensors overlap in %s", ck.files[fi]->path.c_str());
+  }
+  return CQ35_OK;
+}
+
+int gguf_open(const char* path, gguf::Checkpoint* ck) {
+  if (!path) return fail(CQ35_EINVAL, "null path");
+  std::string err;
+  if (!gguf::open_all(path, ck, &err)) return fail(CQ35_EINVAL, "%s", err.c_str());
+  return CQ35_OK;
+}
+
+}  // namespace
+
+extern "C" int cq35_gguf_config(const char* path, cq35_config* out) {
+  if (!out) return fail(CQ35_EINVAL, "null argument");
+  gguf::Checkpoint ck;
+  int rc = gguf_open(path, &ck);
+  return rc ? rc : gguf_config_of(ck, out, nullptr);
+}
+
+extern "C" int cq35_gguf_validate(const char* path, const cq35_config* cfg) {
+  gguf::Checkpoint ck;
+  int rc = gguf_open(path, &ck);
+  if (rc) return rc;
+  cq35_config c;
+  uint64_t nextn = 0;
+  rc = gguf_config_of(ck, &c, &nextn);
+  if (rc) return rc;
+  if (cfg && std::memcmp(cfg, &c, sizeof c) != 0)
+    return fail(CQ35_EINVAL, "the GGUF metadata describes a different configuration");
+  std::vector<const void*> pointers;
+  return gguf_check(ck, c, nextn, &pointers);
+}
+
+extern "C" int cq35_model_load_gguf(const char* path, cq35_model** out) {
+  if (!out) return fail(CQ35_EINVAL, "null argument");
+  gguf::Checkpoint ck;
+  int rc = gguf_open(path, &ck);
+  if (rc) return rc;
+  cq35_config c;
+  uint64_t nextn = 0;
+  rc = gguf_config_of(ck, &c, &nextn);
+  if (rc) return rc;
+  std::vector<const void*> pointers;
+  rc = gguf_check(ck, c, nextn, &pointers);
+  if (rc) return rc;
+  return cq35_model_create(&c, pointers.data(), 0, out);
+}
+
+extern "C" int cq35_gguf_tensor_name(const cq35_config* cfg, int64_t index, char* buf, int64_t len) {
+  if (!cfg || !buf || len <= 0) return fail(CQ35_EINVAL, "null argument");
+  std::string name;
+  std::vector<uint64_t> dims;
+  int32_t dt;
+  if (!gguf_spec(*cfg, index, &name, &dims, &dt)) return fail(CQ35_ERANGE, "tensor index %lld out of range", (long long)index);
+  if ((int64_t)name.size() + 1 > len) return fail(CQ35_EINVAL, "buffer too small for %s", name.c_str());
+  std::memcpy(buf, name.c_str(), name.size() + 1);
   return CQ35_OK;
 }
 

@@ -105,6 +105,24 @@ int cq35_model_create(const cq35_config* cfg, const void* const* weights, int on
  * No reference counterpart: for benchmarks and parity tests without a
  * checkpoint. */
 int cq35_model_create_synthetic(const cq35_config* cfg, uint64_t seed, cq35_model** out);
+
+/* GGUF checkpoints (src/checkpoint.rs): `path` is one version-3 file, any
+ * member of a standard shard set (<prefix>-NNNNN-of-MMMMM.gguf; every shard
+ * is read) or a directory of .gguf files.
+ * cq35_gguf_config: read_gguf_model_config (checkpoint.rs:376-404, 422-639)
+ *   for the qwen35 / qwen35moe architectures (others: CQ35_EUNSUPPORTED);
+ *   the output head is tied unless an output.weight tensor exists.
+ * cq35_gguf_validate: validate_gguf_tensors (checkpoint.rs:406-414, 659-733,
+ *   766-820): the tensor inventory equals weight_specs' GGUF names (tensors
+ *   of next-token layers aside), each with its shape and dtype, inside its
+ *   file, none overlapping. cfg, when given, must equal the metadata's.
+ * cq35_model_load_gguf: Model::load_gguf (model.rs:43, 81-153): the above,
+ *   then every tensor copied into HBM once (cq35_model_create).
+ * cq35_gguf_tensor_name: the GGUF name of weight_specs entry `index`. */
+int cq35_gguf_config(const char* path, cq35_config* out);
+int cq35_gguf_validate(const char* path, const cq35_config* cfg);
+int cq35_model_load_gguf(const char* path, cq35_model** out);
+int cq35_gguf_tensor_name(const cq35_config* cfg, int64_t index, char* buf, int64_t len);
 int cq35_model_free(cq35_model* model);
 int cq35_model_config(const cq35_model* model, cq35_config* out);
 /* Device bytes held by the model's weights. */
