@@ -298,6 +298,15 @@ class SessionCheckpoint:
         self.capacity = capacity
         self.position = position
 
+    def byte_len(self) -> int:
+        """Device bytes the frozen state holds (cache + F32 workspace)."""
+        total = 0
+        for which in (0, 1):
+            b = ctypes.c_int64()
+            check(_lib.load().cq35_session_state_bytes(self._h, which, ctypes.byref(b)))
+            total += b.value
+        return total
+
     def __del__(self):
         try:
             if self._h and self._h.value:

@@ -1743,6 +1743,8 @@ extern "C" int cq35_session_copy(const cq35_session* src, cq35_session** out) {
     return fail(CQ35_EDEVICE, "session copy: %s", hipGetErrorString(e));
   }
   s->graph_enabled = src->graph_enabled;
+  s->matrix = src->matrix;  // session options travel with the state
+  s->mega_on = src->mega_on && s->mega_ok;
   *out = s;
   return CQ35_OK;
 }
