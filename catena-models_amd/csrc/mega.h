@@ -1444,6 +1444,25 @@ __device__ __forceinline__ float value_chain(float acc, const f32x4* row, const 
   return acc;
 }
 
+// XCD-aware item order. Workgroups are dispatched to the 8 XCDs round-robin
+// (block b on XCD b % 8), each XCD with its own L2. For the 35B shape
+// (2 KV heads x 8 query heads x 16 chunks of 16 channels = 256 items) XCD x
+// takes KV head x / 4 and its chunks 4 (x % 4) .. +3 for all 8 query heads:
+// the 128-byte V segment of every key row is fetched from HBM by one XCD and
+// reused from its L2 by the query heads, instead of each line being fetched
+// by the four XCDs that read its 32-byte chunks. Other shapes keep the
+// natural order. A bijection on [0, ITEMS): only the placement changes.
+template <class S>
+__device__ __forceinline__ int value_item(int slot) {
+  constexpr int HPK = S::Q / S::KVH, CHUNKS = S::HD / kValueChannels;
+  if constexpr (S::KVH == 2 && HPK == 8 && CHUNKS == 16) {
+    const int x = slot & 7, s = slot >> 3;
+    return ((x >> 2) * HPK + (s >> 2)) * CHUNKS + 4 * (x & 3) + (s & 3);
+  } else {
+    return slot;
+  }
+}
+
 template <class S>
 __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
@@ -1460,7 +1479,8 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   const int pj = m.tid - 4 * 64;  // producer thread (waves 4-7)
   const int ph = pj & 1;          // channels 8 ph .. 8 ph + 7
 #pragma unroll 1
-  for (int item = m.bid; item < ITEMS; item += m.grid) {
+  for (int slot = m.bid; slot < ITEMS; slot += m.grid) {
+    const int item = value_item<S>(slot);
     const int head = item / CHUNKS, c0 = (item - head * CHUNKS) * kValueChannels;
     const uint16_t* vbase = a.cache + Ly.value_base + (int64_t)(head / HPK) * HD + c0 + 8 * ph;
     const uint64_t* sc = Ly.x_scores + (size_t)head * a.cap;
