@@ -239,31 +239,51 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
 // maximum and an adjacent-pair sum over the keys (qwen35_attention.hex:
 // 258-393), 8 interleaved context partials combined
 // ((s0+s4)+(s2+s6))+((s1+s5)+(s3+s7)) (qwen35_attention.hex:2-177) and the
-// sigmoid gate (qwen35.hex:207-222). One block per query head; blockIdx.y
-// selects token t + y of the call (the batched prefill's per-query staged
-// attention, batch_staged_attention.hex:10-47) with its own rows and scratch.
+// sigmoid gate (qwen35.hex:207-222). This kernel writes the BF16
+// probabilities into the head's scratch row; k_attention_context (below)
+// sums the context from them. One block per query head; blockIdx.y selects
+// token t + y of the call (the batched prefill's per-query staged attention,
+// batch_staged_attention.hex:10-47) with its own rows and scratch. The query
+// head is read once into LDS and the key rows as 16-byte quads; scores and
+// exponentials of up to kStagedLdsKeys keys stay in LDS, longer contexts use
+// the global scratch row.
+constexpr int kStagedLdsKeys = 2048;
+
 __global__ __launch_bounds__(kBlock) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
-    int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
-    int heads_per_kv, float scale, const uint16_t* __restrict__ qg, float* __restrict__ scratch,
-    int scratch_stride, uint16_t* __restrict__ out) {
+    const uint64_t* __restrict__ params, int t, int kvs, int head_dim, int heads_per_kv, float scale,
+    float* __restrict__ scratch, int scratch_stride) {
   __shared__ float partial[kBlock];
+  __shared__ float qf[256];
+  __shared__ float s_lds[kStagedLdsKeys];
+  __shared__ float e_lds[kStagedLdsKeys];
   const int head = blockIdx.x, tid = threadIdx.x;
   const int y = blockIdx.y;
   const size_t qs = (size_t)gridDim.x * head_dim;
   q += y * qs;
-  qg += y * 2 * qs;
-  out += y * qs;
   scratch += (size_t)y * gridDim.x * scratch_stride;
   const int64_t keys = step_position(params, t + y) + 1;
   const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
-  float* s = scratch + (size_t)head * scratch_stride;
-  float* e = s + keys;
-  uint16_t* pb = reinterpret_cast<uint16_t*>(e + keys);
+  const bool in_lds = keys <= kStagedLdsKeys;
+  float* row = scratch + (size_t)head * scratch_stride;
+  float* s = in_lds ? s_lds : row;
+  float* e = in_lds ? e_lds : row + keys;
+  uint16_t* pb = reinterpret_cast<uint16_t*>(row + 2 * keys);  // read by k_attention_context
+  if (tid < head_dim) qf[tid] = bf2f(q[head * head_dim + tid]);
+  __syncthreads();
+  // scores in the scalar order (element 0 first), 8 elements per 16-byte read
   for (int64_t kk = tid; kk < keys; kk += kBlock) {
-    const uint16_t* kr = cache + key_base + kk * kvs + off;
+    const u32x4* kr = reinterpret_cast<const u32x4*>(cache + key_base + kk * kvs + off);
     float acc = 0.0f;
-    for (int i = 0; i < head_dim; ++i) acc += bf2f(q[head * head_dim + i]) * bf2f(kr[i]);
+#pragma unroll 4
+    for (int i8 = 0; i8 < (head_dim >> 3); ++i8) {
+      const u32x4 w = kr[i8];
+      const float* qi = qf + 8 * i8;
+      acc += qi[0] * lo2f(w.x); acc += qi[1] * hi2f(w.x);
+      acc += qi[2] * lo2f(w.y); acc += qi[3] * hi2f(w.y);
+      acc += qi[4] * lo2f(w.z); acc += qi[5] * hi2f(w.z);
+      acc += qi[6] * lo2f(w.w); acc += qi[7] * hi2f(w.w);
+    }
     s[kk] = rbf(acc * scale);
   }
   __syncthreads();
@@ -285,19 +305,59 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
   const float den = e[0];
   for (int64_t kk = tid; kk < keys; kk += kBlock) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
   __syncthreads();
-  if (tid < head_dim) {
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    const uint16_t* vb = cache + value_base + off + tid;
-    for (int64_t start = 0; start < keys; start += 8) {
+}
+
+// The context of k_attention_staged's probabilities: per channel eight
+// chains over keys r, r + 8, ... (in order, the tail padded with + 0),
+// combined as ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)), then bf16(bf16(sum) *
+// sigmoid(gate)) (qwen35_attention.hex:2-177, qwen35.hex:207-222). Block
+// (head, 16-channel chunk) of grid.x = heads * head_dim / 16, blockIdx.y = token
+// t + y; thread (chain r = tid / 16, channel tid % 16), eight steps read ahead.
+constexpr int kContextChannels = 16;
+
+__global__ __launch_bounds__(128) void k_attention_context(
+    const uint16_t* __restrict__ cache, int64_t value_base, const uint64_t* __restrict__ params,
+    int t, int kvs, int head_dim, int heads, int heads_per_kv, const uint16_t* __restrict__ qg,
+    const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out) {
+  __shared__ float part[8][kContextChannels];
+  const int chunks = head_dim / kContextChannels;
+  const int head = blockIdx.x / chunks, c0 = (blockIdx.x - head * chunks) * kContextChannels;
+  const int y = blockIdx.y;
+  const int r = threadIdx.x >> 4, c = c0 + (threadIdx.x & 15);
+  const size_t qs = (size_t)heads * head_dim;
+  qg += y * 2 * qs;
+  out += y * qs;
+  const int64_t keys = step_position(params, t + y) + 1;
+  const uint16_t* pb = reinterpret_cast<const uint16_t*>(
+      scratch + (size_t)y * heads * scratch_stride + (size_t)head * scratch_stride + 2 * keys);
+  const uint16_t* vb = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c;
+  const int64_t steps = (keys + 7) >> 3;
+  float acc = 0.0f;
+  constexpr int kAhead = 8;
+  for (int64_t i0 = 0; i0 < steps; i0 += kAhead) {
+    float pv[kAhead], vv[kAhead];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int64_t kk = start + r;
-        acc[r] = acc[r] + (kk < keys ? bf2f(pb[kk]) * bf2f(vb[kk * kvs]) : 0.0f);
-      }
+    for (int j = 0; j < kAhead; ++j) {
+      const int64_t kk = 8 * (i0 + j) + r;
+      const bool ok = i0 + j < steps && kk < keys;
+      pv[j] = ok ? bf2f(pb[kk]) : 0.0f;
+      vv[j] = ok ? bf2f(vb[kk * kvs]) : 0.0f;
     }
-    const float sum = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
-    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + tid]));
-    out[head * head_dim + tid] = f2bf(rbf(sum) * gate);
+#pragma unroll
+    for (int j = 0; j < kAhead; ++j) {
+      if (i0 + j >= steps) break;
+      const int64_t kk = 8 * (i0 + j) + r;
+      acc = acc + (kk < keys ? pv[j] * vv[j] : 0.0f);
+    }
+  }
+  part[r][threadIdx.x & 15] = acc;
+  __syncthreads();
+  if (r == 0 && c < head_dim) {
+    const int x = threadIdx.x & 15;
+    const float sum = ((part[0][x] + part[4][x]) + (part[2][x] + part[6][x])) +
+                      ((part[1][x] + part[5][x]) + (part[3][x] + part[7][x]));
+    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + c]));
+    out[head * head_dim + c] = f2bf(rbf(sum) * gate);
   }
 }
 

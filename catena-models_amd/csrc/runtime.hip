@@ -1225,9 +1225,12 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->ctx);
       } else {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
-          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, value_base,
-          (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
-          (const uint16_t*)s->qg, s->attn_scratch, s->attn_stride, s->ctx);
+          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
+          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride);
+        L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(128), 0,
+          (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD,
+          (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, (const float*)s->attn_scratch,
+          s->attn_stride, s->ctx);
       }
       residual(L, s->ctx, W(4), d.H, d.QS, s->h, s->attn);
       post_norm = (const float*)W(7);
@@ -1425,10 +1428,12 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
           const int am = std::min(s->pf_attn_tokens, rows_n - a0);
           L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kBlock), 0,
-            (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base,
-            value_base, params, first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale,
-            (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS), s->pf_scratch, s->attn_stride,
-            ctx + (size_t)a0 * d.QS);
+            (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
+            first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride);
+          L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
+            dim3(128), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
+            (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
+            (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS);
         }
         residual_rows(ctx, (int)d.QS, W(4), s->pf_h, s->pf_attn);
         post_norm = W(7);
