@@ -229,6 +229,47 @@ def long_context_decode(model, cfg: dict, context: int, steps: int, seed: int) -
                 state="seeded: KV N(0,1) x 0.1, conv history N(0,1) x 0.1, DeltaNet state N(0,1)")
 
 
+def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: int) -> dict:
+    """The batch-16 configuration: `sessions` independent sessions of
+    `config`, each prefilled with its own `context`-token prompt, then
+    `steps` greedy decode rounds through cq35_step_batch, against one session
+    decoding alone over the same rounds."""
+    import cq35
+    cfg = cq35.preset(config)
+    model = cq35.Model.synthetic(cfg, seed=seed)
+    capacity = context + steps + 8
+    tokens = synthetic_tokens(sessions * context + 1, cfg["vocab"])
+    group, nxt = [], []
+    for b in range(sessions):
+        s = model.session(capacity)
+        nxt.append(s.append_next_token(tokens[b * context:(b + 1) * context]))
+        group.append(s)
+    for _ in range(2):
+        nxt = cq35.decode_batch(group, nxt)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        nxt = cq35.decode_batch(group, nxt)
+    device_sync()
+    batched = time.perf_counter() - t0
+    one = model.session(capacity)
+    x = one.append_next_token(tokens[:context])
+    for _ in range(2):
+        x = one.decode_next_token(x)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        x = one.decode_next_token(x)
+    device_sync()
+    alone = time.perf_counter() - t0
+    log(f"{sessions} {config} sessions: {sessions * steps / batched:.1f} tok/s aggregate "
+        f"({batched / steps * 1e3:.3f} ms per round); one session {steps / alone:.1f} tok/s")
+    return dict(config=config, sessions=sessions, context=context, steps=steps,
+                tokens_per_s=round(sessions * steps / batched, 1), ms_per_round=round(batched / steps * 1e3, 4),
+                single_session_tokens_per_s=round(steps / alone, 1),
+                path="cq35_step_batch: per-kernel launches of all sessions overlapped, weights read per session")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +294,10 @@ def main() -> int:
     ap.add_argument("--long-context", type=int, default=32768,
                     help="cached positions of the long-context decode leg (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=128)
+    ap.add_argument("--batch-sessions", type=int, default=16,
+                    help="sessions of the batch-16 leg (0 skips it)")
+    ap.add_argument("--batch-config", default="qwen35-2b")
+    ap.add_argument("--batch-steps", type=int, default=64)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -369,6 +414,9 @@ def main() -> int:
     if args.long_context > 0:
         del session
         long_ctx = long_context_decode(model, cfg, args.long_context, args.long_steps, args.seed)
+    batch = None
+    if args.batch_sessions > 0:
+        batch = batch_sessions(args.batch_config, args.batch_sessions, 1024, args.batch_steps, args.seed)
 
     cpu = None
     if not args.no_cpu:
@@ -404,7 +452,7 @@ def main() -> int:
         step_roofline=dict(bytes_per_token=bpt["total"], achieved_gbs=round(step_gbs, 1),
                            frac=round(step_gbs / HBM_PEAK_GBS, 4)),
         roofline=roofline, kernels=kernels, cpu_baseline=cpu,
-        prefill=prefill, long_context=long_ctx,
+        prefill=prefill, long_context=long_ctx, batch_sessions=batch,
     )
     print(json.dumps(line))
     return 0

@@ -2,13 +2,13 @@
 kernels behind a C ABI) with a host API mirroring catena-models' Model /
 Session (src/model.rs)."""
 from .config import PRESETS, bytes_per_token, derived, is_full, preset
-from .model import (Model, Session, SessionCheckpoint, gguf_config, gguf_tensor_name, gguf_validate,
+from .model import (Model, Session, SessionCheckpoint, decode_batch, gguf_config, gguf_tensor_name, gguf_validate,
                     kernel_classes, read_logits, weight_count, weight_info)
 from ._lib import CQ35Error, LIBRARY, load
 
 __all__ = [
     "PRESETS", "bytes_per_token", "derived", "is_full", "preset", "Model", "Session",
-    "SessionCheckpoint", "gguf_config", "gguf_tensor_name", "gguf_validate", "kernel_classes",
+    "SessionCheckpoint", "decode_batch", "gguf_config", "gguf_tensor_name", "gguf_validate", "kernel_classes",
     "read_logits", "weight_count", "weight_info",
     "CQ35Error", "LIBRARY", "load",
 ]

@@ -128,6 +128,36 @@ def weight_info(cfg: dict, index: int):
     return info
 
 
+def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int]) -> list:
+    """One decode step for each session (cq35_step_batch): the same next
+    tokens as stepping them one by one, with their launches overlapped."""
+    n = len(sessions)
+    if n == 0:
+        return []
+    if len(tokens) != n:
+        raise ValueError("one token per session")
+    for s in sessions:
+        if not s._alive:
+            raise RuntimeError("session state unavailable after failed execution")
+        if s.position <= 0:
+            raise ValueError("decode requires a completed prefill")
+        if s.position + 1 > s.capacity:
+            raise ValueError("token range exceeds cache capacity")
+    handles = (ctypes.c_void_p * n)(*[s._h.value for s in sessions])
+    toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint64))
+    starts = np.ascontiguousarray(np.asarray([s.position for s in sessions], dtype=np.int64))
+    out = np.zeros(n, dtype=np.uint64)
+    rc = _lib.load().cq35_step_batch(handles, toks.ctypes.data, starts.ctypes.data, n, out.ctypes.data)
+    if rc != 0:
+        if rc in (-3, -5):  # a step may have failed part-way: no session of the batch is trusted
+            for s in sessions:
+                s._alive = False
+        check(rc)
+    for s in sessions:
+        s.position += 1
+    return [int(x) for x in out]
+
+
 def gguf_config(path: str) -> dict:
     """Model configuration from GGUF metadata (read_gguf_model_config,
     src/checkpoint.rs:376-404); no GPU needed."""

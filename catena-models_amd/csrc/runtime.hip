@@ -13,6 +13,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -1547,8 +1548,18 @@ namespace {
 
 // One decode step through the persistent kernel: upload (position, token,
 // step tag), one launch, read back the argmax key and the kernel's error word.
+// The persistent step needs every CU: its blocks wait on each other, so two
+// of them sharing the device could each hold part of the CUs and stall until
+// their spin limits. Steps of different sessions on one device therefore run
+// one at a time, from launch to completion.
+std::mutex& persistent_lock(int device) {
+  static std::mutex locks[64];
+  return locks[device & 63];
+}
+
 int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* next_token,
                     uint16_t* logits) {
+  std::lock_guard<std::mutex> hold(persistent_lock(s->model->device));
   const cq35_config& c = s->model->cfg;
   if (++s->seq == 0) s->seq = 1;  // tag 0 marks never-written words
   s->h_params[0] = (uint64_t)start;
@@ -1644,37 +1655,14 @@ extern "C" int cq35_session_free(cq35_session* s) {
   return CQ35_OK;
 }
 
-extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int64_t start,
-                         int64_t capacity, uint64_t* next_token, uint16_t* logits) {
-  if (!s || !tokens || !next_token) return fail(CQ35_EINVAL, "null argument");
-  if (s->poisoned) return fail(CQ35_EPOISONED, "session state unavailable after failed execution");
+namespace {
+
+// Enqueue a validated call on the session's stream (parameter upload, the
+// launches, the token and logits readback), without waiting for it.
+int step_launch(cq35_session* s, const uint64_t* tokens, int64_t n, int64_t start, uint16_t* logits) {
   const cq35_config& c = s->model->cfg;
-  // Validation before any work (src/model.rs:267-281, 697-709).
-  if (n <= 0) return fail(CQ35_EINVAL, "the token prefix must not be empty");
-  if (capacity != s->capacity)
-    return fail(CQ35_EINVAL, "capacity %lld does not match the session's %lld", (long long)capacity,
-                (long long)s->capacity);
-  if (start < 0 || start + n > capacity)
-    return fail(CQ35_ERANGE, "token range %lld..%lld exceeds cache capacity %lld", (long long)start,
-                (long long)(start + n), (long long)capacity);
-  for (int64_t i = 0; i < n; ++i)
-    if (tokens[i] >= (uint64_t)c.vocab)
-      return fail(CQ35_ERANGE, "token prefix contains an ID outside the %d-token vocabulary", c.vocab);
-  // Multi-token calls at key_dim 128 take the batched prefill
-  // (text-dispatch, prefill.rs:623-652); smaller key dims fold token by token.
   const bool batched = n >= 2 && c.key_dim == 128;
-  if (batched) {
-    if (const char* why = prefill_unsupported(*s->model))
-      return fail(CQ35_EUNSUPPORTED, "batched prefill: %s", why);
-  }
-  hipError_t e = hipSetDevice(s->model->device);
-  if (e != hipSuccess) return fail(CQ35_EDEVICE, "hipSetDevice: %s", hipGetErrorString(e));
-  if (batched) {
-    const int rc = setup_prefill(s);
-    if (rc) return rc;
-  }
-  if (n == 1 && s->mega_on && (s->timed_class < 0 || s->timed_class == KC_DECODE_STEP))
-    return step_persistent(s, tokens[0], start, next_token, logits);
+  hipError_t e;
   s->h_params[0] = (uint64_t)start;
   for (int64_t i = 0; i < n; ++i) s->h_params[1 + i] = tokens[i];
   s->poisoned = true;  // cleared on success
@@ -1717,7 +1705,14 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
   e = hipMemcpyAsync(s->h_best, s->d_best, sizeof(unsigned long long), hipMemcpyDeviceToHost, s->stream);
   if (e == hipSuccess && logits)
     e = hipMemcpyAsync(logits, s->logits, (size_t)c.vocab * 2, hipMemcpyDeviceToHost, s->stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(s->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "step: %s", hipGetErrorString(e));
+  return CQ35_OK;
+}
+
+// Wait for a launched call and return its next token.
+int step_complete(cq35_session* s, uint64_t* next_token) {
+  const cq35_config& c = s->model->cfg;
+  hipError_t e = hipStreamSynchronize(s->stream);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "step: %s", hipGetErrorString(e));
   if (s->timed_class >= 0) {
     int rc = collect_timing(s);
@@ -1730,6 +1725,89 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
   *next_token = token;
   s->poisoned = false;
   return CQ35_OK;
+}
+
+}  // namespace
+
+extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int64_t start,
+                         int64_t capacity, uint64_t* next_token, uint16_t* logits) {
+  if (!s || !tokens || !next_token) return fail(CQ35_EINVAL, "null argument");
+  if (s->poisoned) return fail(CQ35_EPOISONED, "session state unavailable after failed execution");
+  const cq35_config& c = s->model->cfg;
+  // Validation before any work (src/model.rs:267-281, 697-709).
+  if (n <= 0) return fail(CQ35_EINVAL, "the token prefix must not be empty");
+  if (capacity != s->capacity)
+    return fail(CQ35_EINVAL, "capacity %lld does not match the session's %lld", (long long)capacity,
+                (long long)s->capacity);
+  if (start < 0 || start + n > capacity)
+    return fail(CQ35_ERANGE, "token range %lld..%lld exceeds cache capacity %lld", (long long)start,
+                (long long)(start + n), (long long)capacity);
+  for (int64_t i = 0; i < n; ++i)
+    if (tokens[i] >= (uint64_t)c.vocab)
+      return fail(CQ35_ERANGE, "token prefix contains an ID outside the %d-token vocabulary", c.vocab);
+  // Multi-token calls at key_dim 128 take the batched prefill
+  // (text-dispatch, prefill.rs:623-652); smaller key dims fold token by token.
+  const bool batched = n >= 2 && c.key_dim == 128;
+  if (batched) {
+    if (const char* why = prefill_unsupported(*s->model))
+      return fail(CQ35_EUNSUPPORTED, "batched prefill: %s", why);
+  }
+  hipError_t e = hipSetDevice(s->model->device);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "hipSetDevice: %s", hipGetErrorString(e));
+  if (batched) {
+    const int rc = setup_prefill(s);
+    if (rc) return rc;
+  }
+  if (n == 1 && s->mega_on && (s->timed_class < 0 || s->timed_class == KC_DECODE_STEP))
+    return step_persistent(s, tokens[0], start, next_token, logits);
+  const int rc = step_launch(s, tokens, n, start, logits);
+  return rc ? rc : step_complete(s, next_token);
+}
+
+extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens,
+                               const int64_t* starts, int64_t count, uint64_t* next_tokens) {
+  if (!sessions || !tokens || !starts || !next_tokens || count <= 0) return fail(CQ35_EINVAL, "null argument");
+  // every check before any work, as for one session
+  for (int64_t i = 0; i < count; ++i) {
+    cq35_session* s = sessions[i];
+    if (!s) return fail(CQ35_EINVAL, "session %lld is null", (long long)i);
+    if (s->poisoned) return fail(CQ35_EPOISONED, "session %lld state unavailable after failed execution", (long long)i);
+    for (int64_t j = 0; j < i; ++j)
+      if (sessions[j] == s) return fail(CQ35_EINVAL, "session %lld appears twice in the batch", (long long)i);
+    if (starts[i] < 0 || starts[i] + 1 > s->capacity)
+      return fail(CQ35_ERANGE, "session %lld: position %lld exceeds cache capacity %lld", (long long)i,
+                  (long long)starts[i], (long long)s->capacity);
+    if (tokens[i] >= (uint64_t)s->model->cfg.vocab)
+      return fail(CQ35_ERANGE, "session %lld: token ID outside the %d-token vocabulary", (long long)i,
+                  s->model->cfg.vocab);
+  }
+  // per-kernel sessions: launch all, then complete all (they overlap on the
+  // device); persistent sessions step one at a time (each needs every CU)
+  std::vector<int64_t> launched;
+  for (int64_t i = 0; i < count; ++i) {
+    cq35_session* s = sessions[i];
+    HIP_TRY(hipSetDevice(s->model->device));
+    int rc;
+    if (s->mega_on && s->timed_class < 0) {
+      rc = step_persistent(s, tokens[i], starts[i], &next_tokens[i], nullptr);
+    } else {
+      rc = step_launch(s, &tokens[i], 1, starts[i], nullptr);
+      if (!rc) launched.push_back(i);
+    }
+    if (rc) {
+      for (int64_t j : launched) {  // let the launched steps finish before returning
+        uint64_t unused;
+        step_complete(sessions[j], &unused);
+      }
+      return rc;
+    }
+  }
+  int first_error = CQ35_OK;
+  for (int64_t i : launched) {
+    const int rc = step_complete(sessions[i], &next_tokens[i]);
+    if (rc && !first_error) first_error = rc;
+  }
+  return first_error;
 }
 
 extern "C" int cq35_session_copy(const cq35_session* src, cq35_session** out) {

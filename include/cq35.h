@@ -144,6 +144,17 @@ int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t 
               int64_t capacity, uint64_t* next_token, uint16_t* logits);
 
 /* qwen3.copy-buffer: an independent bitwise copy of a session's state. */
+/* One decode step (one token each) for several independent sessions:
+ * tokens[i] at position starts[i] of sessions[i], next token into
+ * next_tokens[i]. Each session's result is identical to its own cq35_step.
+ * Sessions on the per-kernel path are launched back to back on their own
+ * streams and then completed, so their kernels overlap on the device;
+ * sessions on the persistent path step one at a time (each launch needs every
+ * CU). All checks precede any work. No reference counterpart: the reference
+ * steps sessions one after another (src/server/engine.rs:143-207); this is
+ * the entry point for batch-16 serving. */
+int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts,
+                    int64_t count, uint64_t* next_tokens);
 int cq35_session_copy(const cq35_session* src, cq35_session** out);
 
 /* Canonical state for parity checks, in the reference layout
