@@ -3,7 +3,8 @@
 
 Mirrors the reference's `--bench --tg K --tg-context C` protocol
 (src/main.rs:393-445): a fresh session, the C-token synthetic prompt
-(LCG ids, src/main.rs:447-457) appended one token per call, W untimed decode
+(LCG ids, src/main.rs:447-457) appended as one batched call (one token per
+call with --prompt-per-token), W untimed decode
 steps, then K timed greedy `decode_next_token` steps, each ending with the
 8-byte token readback and a stream synchronisation. Defaults are the 35B-A3B
 configuration: 512-token prompt, 512 greedy decode steps (context 512-1024). Weights are random-init BF16
