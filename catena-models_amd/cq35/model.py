@@ -264,10 +264,19 @@ class Session:
         return b.value
 
     def export_state(self, which: int = 0) -> np.ndarray:
+        """which 0: BF16 cache bits; 1: F32 DeltaNet shadow; 2 (MoE): int32
+        [layers, top_k] expert ids chosen for the last call's final token."""
         n = self.state_bytes(which)
-        a = np.empty(n // (2 if which == 0 else 4), dtype=np.uint16 if which == 0 else np.float32)
+        dtype = {0: np.uint16, 1: np.float32, 2: np.int32}[which]
+        a = np.empty(n // np.dtype(dtype).itemsize, dtype=dtype)
         check(_lib.load().cq35_session_export_state(self._h, which, a.ctypes.data, n))
+        if which == 2:
+            a = a.reshape(self.model.cfg["layers"], -1)
         return a
+
+    def router_ids(self) -> np.ndarray:
+        """Per-layer top-k expert ids (rank order) of the last call's final token."""
+        return self.export_state(2)
 
     def import_state(self, which: int, data: np.ndarray) -> None:
         a = np.ascontiguousarray(data)

@@ -553,16 +553,18 @@ __global__ __launch_bounds__(kBlock) void k_router_select(
   if (lane == 0 && row < rows)
     __hip_atomic_store(logits + row, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // The logits went out as device-coherent stores; once every wave's stores
-  // have completed, one ticket per block tells the last block it may read
-  // them all.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  // The logits went out as device-coherent stores. Every wave releases its
+  // own stores at device scope (waits until they have completed), then one
+  // ticket per block tells the last block it may read them all; that block
+  // acquires at device scope before its reads.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __syncthreads();
   if (threadIdx.x == 0)
-    last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
            gridDim.x - 1;
   __syncthreads();
   if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   float* lg = reinterpret_cast<float*>(xs);  // the staged row is no longer needed
   __shared__ int any_nan;
   if (threadIdx.x == 0) any_nan = 0;
@@ -604,7 +606,14 @@ __global__ __launch_bounds__(kBlock) void k_router_select(
       }
     }
   } else {
-    // rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}
+    // rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}. With NaNs two
+    // experts can share a rank and leave another unassigned: an unassigned
+    // rank k keeps expert k, as in the batched select and the restatement.
+    if (threadIdx.x < top_k) {
+      ids[threadIdx.x] = threadIdx.x;
+      chosen[threadIdx.x] = lg[threadIdx.x];
+    }
+    __syncthreads();
     for (int e = threadIdx.x; e < experts; e += blockDim.x) {
       const float le = lg[e];
       int rank = 0;

@@ -17,8 +17,9 @@
 // travel two per word (element 2i in the low half), F32 ones one per word.
 //
 // Every wait is bounded: a thread that polls longer than the spin limit
-// raises the block's abort flag and the global error word, after which every
-// wait of every block returns at once, so the grid always drains.
+// raises the block's abort flag and the global error word (set to the step's
+// tag), after which every wait of every block returns at once, so the grid
+// always drains.
 //
 // Code size is a first-order cost here: the layer loop runs every phase once
 // per layer, so the loop body must stay within the instruction cache. The
@@ -120,6 +121,7 @@ struct MegaArgs {
   unsigned long long* best;
   unsigned* error;
   unsigned spin_limit;
+  int* ids_out;  // [L][K]: each layer's top-k expert ids of this step
 };
 
 // LDS carve-up (bytes); the "big" area is reused by the phases that need it.
@@ -243,16 +245,17 @@ __device__ __forceinline__ volatile CQ35_LDS int* abort_flag(const Mega& m) {
 
 // Spin bookkeeping of one polling loop: true when the wait must stop. The
 // block's abort flag is checked every spin, the global error word and the
-// spin limit every 256 spins.
+// spin limit every 256 spins. The error word holds the tag of the step that
+// raised it, so an error left by an earlier step never stops a later one.
 __device__ __forceinline__ bool spin_stop(const Mega& m, unsigned spins) {
   if (*abort_flag(m)) return true;
   if ((spins & 255u) != 0) return false;
-  if (__hip_atomic_load(G(m.a.error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+  if (__hip_atomic_load(G(m.a.error), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == m.tag) {
     *abort_flag(m) = 1;
     return true;
   }
   if (spins > m.a.spin_limit) {
-    __hip_atomic_fetch_or(G(m.a.error), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(G(m.a.error), m.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *abort_flag(m) = 1;
     return true;
   }
@@ -909,6 +912,13 @@ __device__ __forceinline__ void select_experts(const Mega& m) {
   }
   __syncthreads();
   if (s->any_nan) {
+    // NaNs can make two experts share a rank and leave another unassigned:
+    // an unassigned rank k keeps expert k (as the batched select does)
+    if (m.tid < S::K) {
+      s->ids[m.tid] = m.tid;
+      s->chosen[m.tid] = s->logits[m.tid];
+    }
+    __syncthreads();
     for (int e = m.tid; e < S::E; e += kMT) {
       const float le = s->logits[e];
       int rank = 0;
@@ -983,7 +993,7 @@ __device__ __forceinline__ void issue_down(const Mega& m, const CQ35_CONST MegaL
 // Dual S256 gate/up rows of the selected experts (moe.hex:254-333):
 // bf16(silu(g) * u * p_slot), one row pair per wave.
 template <class S>
-__device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
+__device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int l) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   constexpr int H = S::H, QH = S::QH, NQ = S::NQA;
@@ -992,6 +1002,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
   poll_words<(S::E + 1 + kMT - 1) / kMT>(m, S::E + 1, Span{Ly.x_router},
                                           reinterpret_cast<uint32_t*>(m.misc->logits));
   select_experts<S>(m);
+  // every block ranks the same logits; block 0 reports the layer's choice
+  if (m.bid == 0 && m.tid < S::K) G(m.a.ids_out)[l * S::K + m.tid] = m.misc->ids[m.tid];
   const int p = m.gw;
   const bool has_pair = p < PAIRS;
   if (has_pair) {
@@ -1787,7 +1799,7 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
       phase_outproj<S, S::VS>(pa, tag, ly);
     }
     phase_router<S>(pa, tag, ly);
-    phase_gate_up<S>(pa, tag, ly);
+    phase_gate_up<S>(pa, tag, ly, l);
     phase_down<S>(pa, tag, ly, l + 1 < L ? ly + 1 : nullptr, pr);
   }
   phase_head<S>(pa, tag);

@@ -349,10 +349,12 @@ __global__ __launch_bounds__(kBlock) void k_brouter(const uint16_t* __restrict__
 // Top-k of each token's routed logits by the reference's rank,
 // rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}, and the softmax
 // weights p_j = exp(l_j - l_0) / den with den summed left to right
-// (batch.moe.select, batch_moe.hex:136-317). One block per token.
+// (batch.moe.select, batch_moe.hex:136-317). One block per token. With
+// last_ids, the last token's ids are also written there (the layer's slot of
+// the session's exported top-k).
 __global__ __launch_bounds__(kBlock) void k_bselect(const float* __restrict__ logits, int experts,
                                                      int top_k, int* __restrict__ ids,
-                                                     float* __restrict__ probs) {
+                                                     float* __restrict__ probs, int* __restrict__ last_ids) {
   extern __shared__ float bs_lg[];
   __shared__ float chosen[64];
   const int t = blockIdx.x;
@@ -385,6 +387,8 @@ __global__ __launch_bounds__(kBlock) void k_bselect(const float* __restrict__ lo
     for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
     if (lane < top_k) probs[(size_t)t * top_k + lane] = ex / den;
   }
+  if (last_ids && t == (int)gridDim.x - 1 && threadIdx.x < top_k)
+    last_ids[threadIdx.x] = ids[(size_t)t * top_k + threadIdx.x];
 }
 
 // Expert gate/up of every token (batch.moe.gate, batch_moe.hex:339-411):

@@ -968,6 +968,7 @@ int setup_mega(cq35_session* s) {
   a.logits = s->logits;
   a.best = s->d_best;
   a.error = reinterpret_cast<unsigned*>(s->d_best + 1);
+  a.ids_out = s->ids;
   a.spin_limit = 1u << 21;
   if (const char* lim = getenv("CQ35_SPIN_LIMIT")) a.spin_limit = (unsigned)strtoul(lim, nullptr, 10);
   p = nullptr;
@@ -1017,7 +1018,7 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   check(dalloc(s, &s->qr, d.QS));
   check(dalloc(s, &s->ctx, d.QS));
   check(dalloc(s, &s->router, d.E + 1));
-  check(dalloc(s, &s->ids, std::max<int64_t>(d.K, 1)));
+  check(dalloc(s, &s->ids, d.L * std::max<int64_t>(d.K, 1)));  // per layer: the last token's top-k
   check(dalloc(s, &s->probs, std::max<int64_t>(d.K, 1)));
   check(dalloc(s, &s->ticket, 1));
   check(dalloc(s, &s->active, d.K * d.I + d.SI));
@@ -1118,24 +1119,26 @@ void residual(Launcher& L, const uint16_t* x, const void* w, int64_t rows, int64
 }
 
 // MoE router + top-k selection (one launch; the last block selects).
-void router_select(Launcher& L, cq35_session* s, const uint16_t* x, const float* norm_w,
+void router_select(Launcher& L, cq35_session* s, int64_t layer, const uint16_t* x, const float* norm_w,
                    const float* w, const float* shared_w) {
   const Dims& d = s->model->d;
+  int* ids = s->ids + layer * d.K;
   const float eps = s->model->cfg.eps;
   const dim3 grid((unsigned)((d.E + 1 + 3) / 4)), block(kBlock);
   const size_t lds = router_lds_bytes((int)d.H, (int)d.E);
   switch (batch_of((d.H + 63) / 64, {8, 16, 32})) {
-    case 8: L(KC_ROUTER, k_router_select<8>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
-    case 16: L(KC_ROUTER, k_router_select<16>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
-    default: L(KC_ROUTER, k_router_select<32>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, s->ids, s->probs, s->ticket); break;
+    case 8: L(KC_ROUTER, k_router_select<8>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, ids, s->probs, s->ticket); break;
+    case 16: L(KC_ROUTER, k_router_select<16>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, ids, s->probs, s->ticket); break;
+    default: L(KC_ROUTER, k_router_select<32>, grid, block, lds, x, norm_w, eps, (int)d.H, w, shared_w, (int)d.E, (int)d.K, s->router, ids, s->probs, s->ticket); break;
   }
 }
 
 int down_batch(const Dims& d) { return batch_of(((d.K * d.I + d.SI) / 8 + 63) / 64, {4, 8, 12, 16, 24}); }
 
 // Expert down projection + residual + shared expert.
-void moe_down(Launcher& L, cq35_session* s, const void* down, const void* sdown) {
+void moe_down(Launcher& L, cq35_session* s, int64_t layer, const void* down, const void* sdown) {
   const Dims& d = s->model->d;
+  const int* ids = s->ids + layer * d.K;
   const int per_row = (int)((d.K * d.I + d.SI) / 8);
   const dim3 grid((unsigned)((d.H + kDownRows - 1) / kDownRows)), block(kBlock);
   const size_t lds = moe_down_lds_bytes(per_row);
@@ -1143,11 +1146,11 @@ void moe_down(Launcher& L, cq35_session* s, const void* down, const void* sdown)
   const uint16_t* sw = static_cast<const uint16_t*>(sdown);
   const int H = (int)d.H, K = (int)d.K, I = (int)d.I, SI = (int)d.SI;
   switch (down_batch(d)) {
-    case 4: L(KC_MOE_DOWN, k_moe_down<4>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
-    case 8: L(KC_MOE_DOWN, k_moe_down<8>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
-    case 12: L(KC_MOE_DOWN, k_moe_down<12>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
-    case 16: L(KC_MOE_DOWN, k_moe_down<16>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
-    default: L(KC_MOE_DOWN, k_moe_down<24>, grid, block, lds, (const uint16_t*)s->active, dw, sw, (const int*)s->ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 4: L(KC_MOE_DOWN, k_moe_down<4>, grid, block, lds, (const uint16_t*)s->active, dw, sw, ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 8: L(KC_MOE_DOWN, k_moe_down<8>, grid, block, lds, (const uint16_t*)s->active, dw, sw, ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 12: L(KC_MOE_DOWN, k_moe_down<12>, grid, block, lds, (const uint16_t*)s->active, dw, sw, ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    case 16: L(KC_MOE_DOWN, k_moe_down<16>, grid, block, lds, (const uint16_t*)s->active, dw, sw, ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
+    default: L(KC_MOE_DOWN, k_moe_down<24>, grid, block, lds, (const uint16_t*)s->active, dw, sw, ids, (const uint16_t*)s->attn, H, K, I, SI, s->h); break;
   }
 }
 
@@ -1265,14 +1268,14 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       ffn = 11;
     }
     if (c.moe) {
-      router_select(L, s, s->attn, post_norm, (const float*)W(ffn), (const float*)W(ffn + 4));
+      router_select(L, s, l, s->attn, post_norm, (const float*)W(ffn), (const float*)W(ffn + 4));
       const int64_t rows = d.K * d.I + d.SI;
       L(KC_MOE_GATE, k_gate_up<true>, dim3((unsigned)((rows + 4 * kRowsGate - 1) / (4 * kRowsGate))),
         dim3(kBlock), (size_t)d.H * 2, (const uint16_t*)s->attn, post_norm, c.eps, (int)d.H,
         (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
-        (const uint16_t*)W(ffn + 6), (const int*)s->ids, (const float*)s->probs,
+        (const uint16_t*)W(ffn + 6), (const int*)(s->ids + l * d.K), (const float*)s->probs,
         (const float*)s->router, (int)d.E, (int)d.K, (int)d.I, (int)d.SI, s->active);
-      moe_down(L, s, W(ffn + 3), W(ffn + 7));
+      moe_down(L, s, l, W(ffn + 3), W(ffn + 7));
     } else {
       L(KC_SWIGLU, k_gate_up<false>, dim3((unsigned)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate))),
         dim3(kBlock), (size_t)d.H * 2, (const uint16_t*)s->attn, post_norm, c.eps, (int)d.H,
@@ -1477,7 +1480,8 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
           (const uint16_t*)s->pf_x, H, (const float*)W(ffn), (const float*)W(ffn + 4), E,
           s->pf_logits);
         L(KC_ROUTER, k_bselect, dim3(rows_n), dim3(kBlock), (size_t)E * 4,
-          (const float*)s->pf_logits, E, K, s->pf_ids, s->pf_probs);
+          (const float*)s->pf_logits, E, K, s->pf_ids, s->pf_probs,
+          c0 + rows_n == n ? s->ids + l * d.K : (int*)nullptr);
         const int rows = K * I + SI;
         if ((s->matrix & CQ35_MATRIX_EXPERTS) && H % 16 == 0 && I % 16 == 0 && SI % 16 == 0) {
           const int A = rows_n * K;
@@ -1591,7 +1595,7 @@ int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* ne
     int rc = collect_timing(s);
     if (rc) return rc;
   }
-  if (s->h_best[1] != 0)
+  if ((uint32_t)s->h_best[1] == s->seq)  // the error word holds the tag of the step that raised it
     return fail(CQ35_EDEVICE, "persistent step: an exchange wait exceeded its spin limit");
   const uint64_t t = decode_key(s->h_best[0]);
   if (t >= (uint64_t)c.vocab)
@@ -1795,10 +1799,14 @@ extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* to
       if (!rc) launched.push_back(i);
     }
     if (rc) {
-      for (int64_t j : launched) {  // let the launched steps finish before returning
+      // Sessions stepped or launched before the failure have moved, and the
+      // caller cannot tell which: all of them become unusable, as the
+      // failing one is (the caller restores them from checkpoints).
+      for (int64_t j : launched) {
         uint64_t unused;
-        step_complete(sessions[j], &unused);
+        step_complete(sessions[j], &unused);  // let the launched work finish
       }
+      for (int64_t j = 0; j <= i; ++j) sessions[j]->poisoned = true;
       return rc;
     }
   }
@@ -1807,6 +1815,8 @@ extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* to
     const int rc = step_complete(sessions[i], &next_tokens[i]);
     if (rc && !first_error) first_error = rc;
   }
+  if (first_error)
+    for (int64_t i = 0; i < count; ++i) sessions[i]->poisoned = true;
   return first_error;
 }
 
@@ -1836,6 +1846,7 @@ extern "C" int cq35_session_state_bytes(const cq35_session* s, int which, int64_
   if (!s || !bytes) return fail(CQ35_EINVAL, "null argument");
   if (which == 0) *bytes = cache_elements(s->model->cfg, s->capacity) * 2;
   else if (which == 1) *bytes = s->model->d.L * s->model->d.REC * 4;
+  else if (which == 2 && s->model->cfg.moe) *bytes = s->model->d.L * s->model->d.K * 4;
   else return fail(CQ35_EINVAL, "state buffer %d does not exist", which);
   return CQ35_OK;
 }
@@ -1847,7 +1858,8 @@ extern "C" int cq35_session_export_state(const cq35_session* s, int which, void*
   if (!dst || bytes != expect) return fail(CQ35_EINVAL, "state buffer %d has %lld bytes", which, (long long)expect);
   HIP_TRY(hipSetDevice(s->model->device));
   HIP_TRY(hipStreamSynchronize(s->stream));
-  HIP_TRY(hipMemcpy(dst, which == 0 ? (void*)s->cache : (void*)s->shadow, bytes, hipMemcpyDeviceToHost));
+  const void* src = which == 0 ? (const void*)s->cache : which == 1 ? (const void*)s->shadow : (const void*)s->ids;
+  HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
   return CQ35_OK;
 }
 
@@ -1856,6 +1868,7 @@ extern "C" int cq35_session_import_state(cq35_session* s, int which, const void*
   int rc = cq35_session_state_bytes(s, which, &expect);
   if (rc) return rc;
   if (!src || bytes != expect) return fail(CQ35_EINVAL, "state buffer %d has %lld bytes", which, (long long)expect);
+  if (which == 2) return fail(CQ35_EINVAL, "state buffer 2 (router top-k) is read-only");
   HIP_TRY(hipSetDevice(s->model->device));
   HIP_TRY(hipStreamSynchronize(s->stream));
   HIP_TRY(hipMemcpy(which == 0 ? (void*)s->cache : (void*)s->shadow, src, bytes, hipMemcpyHostToDevice));

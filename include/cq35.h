@@ -143,18 +143,22 @@ int cq35_session_free(cq35_session* session);
 int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t start,
               int64_t capacity, uint64_t* next_token, uint16_t* logits);
 
-/* qwen3.copy-buffer: an independent bitwise copy of a session's state. */
 /* One decode step (one token each) for several independent sessions:
  * tokens[i] at position starts[i] of sessions[i], next token into
  * next_tokens[i]. Each session's result is identical to its own cq35_step.
  * Sessions on the per-kernel path are launched back to back on their own
  * streams and then completed, so their kernels overlap on the device;
  * sessions on the persistent path step one at a time (each launch needs every
- * CU). All checks precede any work. No reference counterpart: the reference
+ * CU). All checks precede any work. If a step fails after work was
+ * enqueued, every session of the batch is poisoned (some may have advanced a
+ * position; none reports a token). No reference counterpart: the reference
  * steps sessions one after another (src/server/engine.rs:143-207); this is
  * the entry point for batch-16 serving. */
 int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts,
                     int64_t count, uint64_t* next_tokens);
+
+/* qwen3.copy-buffer (session_copy.hex:131-135; src/model.rs:209-246): an
+ * independent bitwise copy of a session's state and options. */
 int cq35_session_copy(const cq35_session* src, cq35_session** out);
 
 /* Canonical state for parity checks, in the reference layout
@@ -162,6 +166,11 @@ int cq35_session_copy(const cq35_session* src, cq35_session** out);
  *   which = 0: BF16 cache [KV: layer, K|V, capacity, kv_heads*head_dim]
  *              [per layer: conv history 3*QKV, recurrent VH*VD*KD]
  *   which = 1: F32 DeltaNet shadow [layer, VH*VD*KD]
+ *   which = 2: (MoE only, export only) int32 [layer, top_k]: the expert ids
+ *              in rank order that the last call's final token selected at
+ *              each layer (the reference keeps the current layer's ids in
+ *              its workspace, state_layout.hex:53-87, written by
+ *              qwen35_moe.hex:86-252)
  * `bytes` must equal cq35_session_state_bytes(session, which). */
 int cq35_session_state_bytes(const cq35_session* session, int which, int64_t* bytes);
 int cq35_session_export_state(const cq35_session* session, int which, void* dst, int64_t bytes);

@@ -795,6 +795,9 @@ static void moe_route(const ox_model* m, const uint16_t* x, const float* router,
   for (int64_t e = 0; e <= E; ++e)
     logit[e] = ox_dot_width_f32w(x, e < E ? router + e * H : shared_router, H / 2, 32);
   float sel[64];
+  /* NaN logits can make two experts share a rank and leave another
+   * unassigned; an unassigned rank k keeps expert k. */
+  for (int64_t j = 0; j < K; ++j) { ids[j] = j; sel[j] = logit[j]; }
   for (int64_t e = 0; e < E; ++e) {
     int64_t rank = 0;
     for (int64_t i = 0; i < E; ++i) {
@@ -1285,6 +1288,7 @@ void ox_moe_route(const uint16_t* x, const float* router, const float* shared_ro
   for (int64_t e = 0; e <= E; ++e)
     logits[e] = ox_dot_width_f32w(x, e < E ? router + e * H : shared_router, H / 2, 32);
   float sel[64];
+  for (int64_t j = 0; j < K; ++j) { ids[j] = j; sel[j] = logits[j]; }
   for (int64_t e = 0; e < E; ++e) {
     int64_t rank = 0;
     for (int64_t i = 0; i < E; ++i) {

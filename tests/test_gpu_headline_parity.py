@@ -1,0 +1,173 @@
+"""Parity at the benchmark shapes, against the CPU restatement, through the C
+ABI on an MI355X:
+
+- qwen36-35b-a3b (the headline decode shape): a 24-token prompt as one
+  batched call, then 64 greedy decode steps, on the persistent one-launch
+  step and on the per-kernel launch sequence. At every call: the greedy
+  token, the BF16 logits and each layer's top-k expert ids (rank order,
+  qwen35_moe.hex:86-252) equal the restatement's; at the end the whole
+  session state (KV, conv history, DeltaNet state) equals it bit for bit.
+- qwen35-2b (dense): batch 1 against the restatement, and 16 sessions
+  stepped together through cq35_step_batch against the same sessions
+  stepped alone, one of them also against the restatement.
+
+The restatement's 35B weights take 69 GB of host memory; it is built once
+per module.
+"""
+import os
+import time
+
+import numpy as np
+import pytest
+
+import cq35
+import cq35.config as cc
+
+pytestmark = pytest.mark.gpu
+
+SEED = 11
+PROMPT = 24
+STEPS = 64
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def host_bytes_free() -> int:
+    try:
+        import psutil
+        return psutil.virtual_memory().available
+    except Exception:
+        return 1 << 62
+
+
+def oracle_run(oracle, cfg, prompt, steps, capacity):
+    """Restatement: batched prompt, then greedy steps; per call the token,
+    the BF16 logits and (MoE) the per-layer ids."""
+    t0 = time.time()
+    om = oracle.Model(cfg, oracle.synthetic_weights(cfg, SEED))
+    say(f"  restatement weights ready in {time.time() - t0:.1f}s")
+    s = om.session(capacity)
+    calls = []
+    tok, logits = s.step(prompt, 0)
+    ids = s.last_ids().reshape(cfg["layers"], -1) if cfg["moe"] else None
+    calls.append((tok, logits, ids))
+    pos = len(prompt)
+    for k in range(steps):
+        tok, logits = s.step([tok], pos)
+        ids = s.last_ids().reshape(cfg["layers"], -1) if cfg["moe"] else None
+        calls.append((tok, logits, ids))
+        pos += 1
+        if (k + 1) % 16 == 0:
+            say(f"  restatement step {k + 1} ({time.time() - t0:.1f}s)")
+    return calls, s.cache()
+
+
+def gpu_run(model, cfg, prompt, steps, capacity, persistent):
+    s = model.session(capacity)
+    if cfg["moe"]:
+        s.set_persistent(persistent)
+        assert s.persistent == persistent
+    calls = []
+    logits, tok = s.step_raw(prompt)
+    calls.append((tok, logits, s.router_ids() if cfg["moe"] else None))
+    for _ in range(steps):
+        logits, tok = s.step_raw([tok])
+        calls.append((tok, logits, s.router_ids() if cfg["moe"] else None))
+    return calls, s.export_state(0)
+
+
+def compare(name, got, ref):
+    for i, ((gt, gl, gi), (rt, rl, ri)) in enumerate(zip(got, ref)):
+        if gi is not None:
+            assert np.array_equal(gi, ri), f"{name}: router ids differ at call {i}"
+        assert gt == rt, f"{name}: greedy token differs at call {i}: {gt} vs {rt}"
+        assert np.array_equal(gl, rl), f"{name}: BF16 logits differ at call {i}"
+    assert len(got) == len(ref)
+
+
+@pytest.fixture(scope="module")
+def moe35(oracle):
+    cfg = cc.preset("qwen36-35b-a3b")
+    if host_bytes_free() < 80e9:
+        pytest.skip("the 35B restatement needs about 75 GB of host memory")
+    prompt = np.random.default_rng(SEED).integers(0, cfg["vocab"], PROMPT).tolist()
+    cap = PROMPT + STEPS + 1
+    say("35B restatement: prompt", PROMPT, "steps", STEPS)
+    calls, cache = oracle_run(oracle, cfg, prompt, STEPS, cap)
+    model = cq35.Model.synthetic(cfg, seed=SEED)
+    return cfg, prompt, cap, calls, cache, model
+
+
+@pytest.mark.timeout(400)
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per-kernel"])
+def test_35b_decode_matches_restatement(moe35, persistent):
+    cfg, prompt, cap, ref, ref_cache, model = moe35
+    say("35B GPU run, persistent =", persistent)
+    got, cache = gpu_run(model, cfg, prompt, STEPS, cap, persistent)
+    compare(f"35B persistent={persistent}", got, ref)
+    assert np.array_equal(cache, ref_cache), "35B: session state differs"
+
+
+def test_35b_router_ids_are_a_valid_top_k(moe35):
+    """The exported ids are distinct experts in descending logit rank: a
+    check that does not go through the restatement."""
+    cfg, prompt, cap, ref, _, model = moe35
+    s = model.session(cap)
+    s.step_raw(prompt)
+    ids = s.router_ids()
+    assert ids.shape == (cfg["layers"], cfg["top_k"])
+    for row in ids:
+        assert len(set(row.tolist())) == cfg["top_k"]
+        assert row.min() >= 0 and row.max() < cfg["experts"]
+
+
+@pytest.fixture(scope="module")
+def dense2b(oracle):
+    cfg = cc.preset("qwen35-2b")
+    model = cq35.Model.synthetic(cfg, seed=SEED)
+    return cfg, model
+
+
+@pytest.mark.timeout(300)
+def test_2b_batch1_matches_restatement(oracle, dense2b):
+    cfg, model = dense2b
+    prompt = np.random.default_rng(SEED + 1).integers(0, cfg["vocab"], 8).tolist()
+    steps = 8
+    cap = len(prompt) + steps + 1
+    say("2B restatement: prompt", len(prompt), "steps", steps)
+    ref, ref_cache = oracle_run(oracle, cfg, prompt, steps, cap)
+    got, cache = gpu_run(model, cfg, prompt, steps, cap, False)
+    compare("2B", got, ref)
+    assert np.array_equal(cache, ref_cache), "2B: session state differs"
+
+
+@pytest.mark.timeout(300)
+def test_2b_batch16_matches_sessions_alone(oracle, dense2b):
+    cfg, model = dense2b
+    B, plen, rounds = 16, 6, 6
+    rng = np.random.default_rng(SEED + 2)
+    prompts = [rng.integers(0, cfg["vocab"], plen).tolist() for _ in range(B)]
+    cap = plen + rounds + 2
+    say("2B batch of", B, "sessions,", rounds, "rounds")
+    group = [model.session(cap) for _ in range(B)]
+    nxt = [s.append_next_token(p) for s, p in zip(group, prompts)]
+    first = list(nxt)
+    history = [list(nxt)]
+    for _ in range(rounds):
+        nxt = cq35.decode_batch(group, nxt)
+        history.append(list(nxt))
+    states = [s.export_state(0) for s in group]
+    for b in range(B):
+        alone = model.session(cap)
+        t = alone.append_next_token(prompts[b])
+        assert t == first[b]
+        for r in range(rounds):
+            t = alone.decode_next_token(t)
+            assert t == history[r + 1][b], f"session {b}: token differs at round {r}"
+        assert np.array_equal(alone.export_state(0), states[b]), f"session {b}: state differs"
+    # one session of the batch against the restatement
+    ref, ref_cache = oracle_run(oracle, cfg, prompts[3], rounds, cap)
+    assert [c[0] for c in ref] == [h[3] for h in history]
+    assert np.array_equal(ref_cache, states[3])

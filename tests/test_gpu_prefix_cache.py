@@ -1,12 +1,14 @@
-"""Session checkpoints and the prompt prefix cache on the GPU, bitwise:
+"""Session checkpoints on the GPU, bitwise, as the serving loop's prompt
+prefix cache uses them through this ABI (the cache policy itself stays in the
+Rust server, src/server/prefix_cache.rs):
 - tests/session_checkpoint.rs:112-168: a checkpoint taken after a 1024-token
   block resumes exactly like the cold session, also again after a resumed
   session decoded; another model rejects it;
-- src/server/engine.rs:645-732 (serving_prefix_cache_bitwise_parity): warm
-  prefills from the stable / recent checkpoints give the cold prefill's next
-  token and logits bit for bit, a rewritten span falls back to the stable
-  slot, another capacity misses, unrelated prompts and cancelled requests
-  leave the slots alone.
+- resume equals cold at every absolute block boundary a server can hold
+  (1024 and 2048 tokens), with and without a suffix to prefill: the warm
+  prefill gives the cold prefill's next token and logits bit for bit, the
+  checkpoint stays frozen while sessions resumed from it decode, and a
+  checkpoint is only valid for its own capacity.
 On the reduced MoE shape (same code paths as 35B: batched prefill, persistent
 decode)."""
 import numpy as np
@@ -14,7 +16,6 @@ import pytest
 
 import cq35
 import cq35.config as cc
-from cq35.prefix_cache import PrefixCache, prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -66,42 +67,39 @@ def test_checkpoint_resume_is_bitwise_exact_and_independent(model):
         other.resume_checkpoint(cp)
 
 
-def test_serving_prefix_cache_bitwise_parity(model):
-    say("prefix cache parity")
-    cancel = {"now": False}
-    cancelled = lambda: cancel["now"]
-    cache = PrefixCache()
-    tokens = [100 + i % 97 for i in range(2051)]
+def test_resume_equals_cold_at_block_boundaries(model):
+    say("resume equals cold at 1024-token block boundaries")
+    tokens = [100 + (7 * i) % 97 for i in range(2051)]
 
-    def cold(toks, capacity):
-        s, nxt, _, _ = prefill(model, PrefixCache(), False, toks, capacity, 1024)
-        return nxt, bits(s.decode_logits(nxt))
+    def prefill(s, start, end):
+        """The prompt from `start` in absolute 1024-token blocks."""
+        nxt = None
+        for b in range(start, end, 1024):
+            nxt = s.append_next_token(tokens[b:min(b + 1024, end)])
+        return nxt
 
-    # both slots, including the exact-checkpoint / no-suffix path
-    for enabled, expected in [(True, 0), (True, 2048), (False, 0)]:
-        s, nxt, cached, _ = prefill(model, cache, enabled, tokens[:2048], 4096, 1024, cancelled)
-        assert cached == expected
-        logits = bits(s.decode_logits(nxt))
-        cnext, clogits = cold(tokens[:2048], 4096)
-        assert nxt == cnext and np.array_equal(logits, clogits)
-    # mutating a restored decode session above must leave the prompt frozen
-    for end, changed, capacity, expected in [(2049, False, 4096, 2048), (2051, False, 4096, 2048),
-                                             (2051, True, 4096, 1024), (2051, False, 8192, 0)]:
-        if changed:
-            tokens[1400] += 1  # rewritten earlier reasoning
-        s, nxt, cached, _ = prefill(model, cache, True, tokens[:end], capacity, 1024, cancelled)
-        assert cached == expected, (end, changed, capacity)
-        logits = bits(s.decode_logits(nxt))
-        del s
-        cnext, clogits = cold(tokens[:end], capacity)
-        assert nxt == cnext and np.array_equal(logits, clogits)
-    # unrelated short prompts and cancelled requests leave both slots intact
-    stable, recent = cache.stable, cache.recent
-    prefill(model, cache, True, [1, 2, 3], 16, 0, cancelled)
-    assert cache.stable is stable and cache.recent is recent
-    cancel["now"] = True
-    assert prefill(model, cache, True, tokens, 8192, 1024, cancelled) is None
-    cancel["now"] = False
-    cache.clear()
-    _, _, cached, _ = prefill(model, cache, True, tokens, 8192, 1024, cancelled)
-    assert cached == 0
+    base = model.session(4096)
+    after = {1024: prefill(base, 0, 1024)}  # next token of the prompt ending at the checkpoint
+    cp1024 = base.into_checkpoint()
+    s = model.resume_checkpoint(cp1024)
+    after[2048] = prefill(s, 1024, 2048)
+    cp2048 = s.into_checkpoint()
+    for end in (1024, 2048, 2049, 2051):
+        c = model.session(4096)
+        cnext = prefill(c, 0, end)
+        clogits = bits(c.decode_logits(cnext))
+        cfollow = c.decode_next_token(cnext)
+        del c
+        for cp in (cp1024, cp2048):
+            if cp.position > end:
+                continue
+            say("  prompt", end, "from checkpoint", cp.position)
+            s = model.resume_checkpoint(cp)
+            # an exact checkpoint has nothing left to prefill
+            nxt = prefill(s, cp.position, end) if end > cp.position else after[cp.position]
+            assert nxt == cnext, (end, cp.position)
+            assert np.array_equal(bits(s.decode_logits(nxt)), clogits), (end, cp.position)
+            # decoding on the resumed session leaves the checkpoint as it was
+            # (later resumes of the same checkpoint are compared again)
+            assert s.decode_next_token(nxt) == cfollow, (end, cp.position)
+            assert s.capacity == cp.capacity == 4096
