@@ -76,6 +76,7 @@ def load():
         "cq35_gguf_validate": ([ctypes.c_char_p, PC], ctypes.c_int),
         "cq35_model_load_gguf": ([ctypes.c_char_p, ctypes.POINTER(P)], ctypes.c_int),
         "cq35_gguf_tensor_name": ([PC, I64, ctypes.c_char_p, I64], ctypes.c_int),
+        "cq35_step_static": ([P, P, I64, U64, I64, P, ctypes.POINTER(U64), P], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(l, name)
@@ -102,5 +103,5 @@ EXPORTED = [
     "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
     "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv", "cq35_device_matrix_gemm",
     "cq35_gguf_config", "cq35_gguf_validate", "cq35_model_load_gguf", "cq35_gguf_tensor_name",
-    "cq35_step_batch",
+    "cq35_step_batch", "cq35_step_static",
 ]

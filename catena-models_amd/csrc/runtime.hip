@@ -2010,3 +2010,5 @@ extern "C" int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, int
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "device matrix GEMM: %s", hipGetErrorString(e));
   return CQ35_OK;
 }
+
+#include "static_step.h"

@@ -157,6 +157,23 @@ int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t 
 int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts,
                     int64_t count, uint64_t* next_tokens);
 
+/* A decode step (one token) that allocates nothing, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops
+ * and harnesses that forbid hipMalloc. No counterpart in the reference.
+ * `state` is caller-owned device memory holding the BF16 session state of
+ * `capacity` positions in the reference layout (cq35_session_state_bytes
+ * with which = 0, e.g. copied from cq35_session_export_state); it is updated
+ * in place exactly as cq35_step updates a session (same per-kernel decode
+ * sequence, same results). `stream` is a hipStream_t (NULL: the default
+ * stream); the call waits for it before returning the greedy token and, when
+ * logits != NULL, the BF16 logits to host memory. Every other buffer comes
+ * from one static device array of 16 MiB per device (held until the process
+ * ends), which bounds the capacity: about 80K positions at the 35B-A3B shape;
+ * larger capacities are rejected with CQ35_ERANGE before any work. Calls
+ * that overlap on one device share that array and race. */
+int cq35_step_static(const cq35_model* model, uint16_t* state, int64_t capacity, uint64_t token,
+                     int64_t start, void* stream, uint64_t* next_token, uint16_t* logits);
+
 /* qwen3.copy-buffer (session_copy.hex:131-135; src/model.rs:209-246): an
  * independent bitwise copy of a session's state and options. */
 int cq35_session_copy(const cq35_session* src, cq35_session** out);
