@@ -85,8 +85,42 @@ def lib():
         l.ox_step.argtypes = [P, P, I64, I64, ctypes.POINTER(U64), P]
         l.ox_step.restype = ctypes.c_int
         l.ox_set_threads.argtypes = [ctypes.c_int]
+        l.ox_set_plant.argtypes = [ctypes.c_int]
+        l.ox_k_normalize.argtypes = [P, P, I64, I64, ctypes.c_float, P]
+        l.ox_k_prepare_heads.argtypes = [P, I64, P, P, I64, P]
+        l.ox_k_rope.argtypes = [P, I64, P, I64, P]
+        l.ox_k_conv.argtypes = [P, P, I64, P, P, P]
+        l.ox_k_l2.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
+        l.ox_k_delta.argtypes = [P, P, P, P, P, P, P, P, P, P, P]
+        l.ox_k_gated_norm.argtypes = [P, P, P, P, P]
+        l.ox_k_attention.argtypes = [P, ctypes.c_int, P, P, I64, P, P]
         _lib = l
     return _lib
+
+
+# Planted mistakes (oracle.h OX_PLANT_*): switched on only by the pinning
+# tests, to show that a comparison fails for that mistake.
+PLANTS = {
+    "rope_pairing": 1, "rope_sign": 2, "rope_freq_hd": 3, "qk_norm_swap": 4,
+    "conv_tap_order": 5, "delta_scale": 6, "l2_whole": 7, "gated_sum": 8,
+    "attn_scale": 9, "gqa_map": 10, "norm_weight": 11, "key_head": 12,
+    "delta_pred_decay": 13,
+}
+
+
+class planted:
+    """Context manager: the restatement runs with one planted mistake."""
+
+    def __init__(self, name):
+        self.code = PLANTS[name] if name else 0
+
+    def __enter__(self):
+        lib().ox_set_plant(self.code)
+        return self
+
+    def __exit__(self, *exc):
+        lib().ox_set_plant(0)
+        return False
 
 
 def make_config(cfg: dict) -> OxConfig:

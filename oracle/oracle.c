@@ -21,6 +21,12 @@ static inline uint32_t fbits(float x) { uint32_t u; memcpy(&u, &x, 4); return u;
 static inline float bitsf(uint32_t u) { float x; memcpy(&x, &u, 4); return x; }
 
 /* src/weights.rs:213-221: round-to-nearest-even, NaNs quieted. */
+/* Planted mistakes (OX_PLANT_*, oracle.h): 0 in every normal use. The
+ * pinning tests switch one on to show that their comparison with an
+ * independent formulation fails for that mistake. */
+static int g_plant = 0;
+void ox_set_plant(int which) { g_plant = which; }
+
 uint16_t ox_f2bf(float x) {
   uint32_t u = fbits(x);
   if (x != x) return (uint16_t)((u >> 16) | 0x0040u);
@@ -290,7 +296,8 @@ static void normalize_rows(const uint16_t* x, const float* w, int64_t cols, int6
     float mean = sum / (float)cols;
     float inverse = 1.0f / ox_sqrt(mean + eps);
     for (int64_t c = 0; c < cols; ++c)
-      out[r * cols + c] = bf_mul(ox_f2bf(ox_bf2f(xr[c]) * inverse), ox_f2bf(w[c]));
+      out[r * cols + c] = bf_mul(ox_f2bf(ox_bf2f(xr[c]) * inverse),
+                                 ox_f2bf(g_plant == OX_PLANT_NORM_WEIGHT ? 1.0f : w[c]));
   }
 }
 
@@ -557,7 +564,9 @@ static void rope_table(const ox_model* m, int64_t position, float* table) {
   float p = (float)(uint32_t)position;
   for (int i = 0; i < half; ++i) {
     float s, c;
-    ox_sincos(p * m->freq[i], &s, &c);
+    float f = m->freq[i];
+    if (g_plant == OX_PLANT_ROPE_FREQ_HD) f = powf(m->c.theta, -((float)(2 * i) / (float)m->c.head_dim));
+    ox_sincos(p * f, &s, &c);
     table[i] = c;
     table[half + i] = s;
   }
@@ -573,9 +582,15 @@ static void rotate_head(const uint16_t* in, const float* table, int HD, int R, u
       int pair = c % half;
       int first = c < half;
       float b = ox_bf2f(in[first ? pair + half : pair]);
+      if (g_plant == OX_PLANT_ROPE_PAIRING) {  /* interleaved (2i, 2i+1) pairs */
+        pair = c / 2;
+        first = (c & 1) == 0;
+        b = ox_bf2f(in[first ? c + 1 : c - 1]);
+      }
       float ac = a * table[pair];
       float bs = b * table[pair + half];
       v = first ? ac - bs : ac + bs;
+      if (g_plant == OX_PLANT_ROPE_SIGN) v = first ? ac + bs : ac - bs;
     }
     out[c] = ox_f2bf(v);
   }
@@ -602,9 +617,9 @@ static void conv_step(const ox_model* m, uint16_t* cache, int64_t conv_base, int
       int64_t p = position + t;
       float hist = ox_bf2f(cache[conv_base + (p % 3) * QKV + ch]);
       float input = p < 3 ? 0.0f : hist;
-      taps[t] = input * weight[ch * 4 + t];
+      taps[t] = input * weight[ch * 4 + (g_plant == OX_PLANT_CONV_TAP_ORDER ? 3 - t : t)];
     }
-    float tap3 = ox_bf2f(qkv[ch]) * weight[ch * 4 + 3];
+    float tap3 = ox_bf2f(qkv[ch]) * weight[ch * 4 + (g_plant == OX_PLANT_CONV_TAP_ORDER ? 0 : 3)];
     float sum = (taps[0] + taps[2]) + (taps[1] + tap3);
     out[ch] = ox_f2bf(ox_silu(rbf(sum)));
   }
@@ -613,6 +628,7 @@ static void conv_step(const ox_model* m, uint16_t* cache, int64_t conv_base, int
 
 /* Per-head L2 norm with a serial sum (qwen35.hex:396-436; linear_prepare.hex:84-131). */
 static void l2_heads(const uint16_t* in, int heads, int dim, uint16_t* out) {
+  if (g_plant == OX_PLANT_L2_WHOLE) { dim *= heads; heads = 1; }
   for (int h = 0; h < heads; ++h) {
     float sum = 0.0f;
     for (int i = 0; i < dim; ++i) { float v = ox_bf2f(in[h * dim + i]); sum += v * v; }
@@ -629,11 +645,12 @@ static void delta_step(const ox_model* m, const uint16_t* conv, const uint16_t* 
                        uint16_t* state16, float* state32, uint16_t* out) {
   const int KD = m->c.key_dim, VD = m->c.value_dim, KH = m->c.key_heads;
   const int64_t VS = m->VS, KS = m->KS;
-  const float scale = 1.0f / sqrtf((float)KD);  /* DELTA_SCALE_BITS, qwen35.rs:703 */
+  const float scale = g_plant == OX_PLANT_DELTA_SCALE ? 1.0f : 1.0f / sqrtf((float)KD);  /* DELTA_SCALE_BITS, qwen35.rs:703 */
+  const int ratio = m->c.value_heads / KH;
 #pragma omp parallel for schedule(static)
   for (int64_t c = 0; c < VS; ++c) {
     int head = (int)(c / VD);
-    int kbase = (head % KH) * KD;
+    int kbase = (g_plant == OX_PLANT_KEY_HEAD ? head / ratio : head % KH) * KD;
     float time_step = ox_softplus(ox_bf2f(alpha[head]) + dt[head]);
     float decay = ox_exp(rbf(time_step * a[head]));
     float rate = rbf(ox_sigmoid(ox_bf2f(beta[head])));
@@ -648,7 +665,7 @@ static void delta_step(const ox_model* m, const uint16_t* conv, const uint16_t* 
     }
     float total = tree(lanes, 32);
     float value = ox_bf2f(conv[2 * KS + c]);
-    float delta = (value - total * decay) * rate;
+    float delta = (value - (g_plant == OX_PLANT_DELTA_PRED_DECAY ? total : total * decay)) * rate;
     for (int l = 0; l < 32; ++l) {
       float acc = 0.0f;
       for (int i = l; i < KD; i += 32) {
@@ -671,7 +688,7 @@ static void gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* 
   for (int h = 0; h < m->c.value_heads; ++h) {
     float sum = 0.0f;
     for (int i = 0; i < VD; ++i) { float v = ox_bf2f(core[h * VD + i]); sum += v * v; }
-    float rms = ox_sqrt(sum / (float)VD + m->c.eps);
+    float rms = ox_sqrt((g_plant == OX_PLANT_GATED_SUM ? sum : sum / (float)VD) + m->c.eps);
     for (int i = 0; i < VD; ++i) {
       float normalized = ox_bf2f(core[h * VD + i]) / rms;
       float gate = ox_silu(ox_bf2f(z[h * VD + i]));
@@ -686,10 +703,10 @@ static void attention_online(const ox_model* m, const uint16_t* q, const uint16_
                              const uint16_t* qg, uint16_t* out) {
   const int HD = m->c.head_dim, hpk = m->c.q_heads / m->c.kv_heads;
   const int64_t KVS = m->KVS;
-  const float scale = 1.0f / sqrtf((float)HD);  /* SCALE_BITS, qwen35.rs:701 */
+  const float scale = g_plant == OX_PLANT_ATTN_SCALE ? 1.0f : 1.0f / sqrtf((float)HD);  /* SCALE_BITS, qwen35.rs:701 */
 #pragma omp parallel for schedule(static)
   for (int head = 0; head < m->c.q_heads; ++head) {
-    int64_t off = (int64_t)(head / hpk) * HD;
+    int64_t off = (int64_t)(g_plant == OX_PLANT_GQA_MAP ? head % m->c.kv_heads : head / hpk) * HD;
     float maximum = bitsf(0xFF800000u), den = 0.0f;
     float* value = (float*)calloc((size_t)HD, sizeof(float));
     for (int64_t first = 0; first < keys; first += 8) {
@@ -737,12 +754,12 @@ static void attention_staged(const ox_model* m, const uint16_t* q, const uint16_
                              const uint16_t* qg, uint16_t* out) {
   const int HD = m->c.head_dim, hpk = m->c.q_heads / m->c.kv_heads;
   const int64_t KVS = m->KVS;
-  const float scale = 1.0f / sqrtf((float)HD);  /* ATTENTION_SCALE_BITS, mod.rs:361 */
+  const float scale = g_plant == OX_PLANT_ATTN_SCALE ? 1.0f : 1.0f / sqrtf((float)HD);  /* ATTENTION_SCALE_BITS, mod.rs:361 */
   float* s = (float*)malloc(sizeof(float) * (size_t)keys);
   uint16_t* p = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)keys);
   float* buf = (float*)malloc(sizeof(float) * (size_t)keys);
   for (int head = 0; head < m->c.q_heads; ++head) {
-    int64_t off = (int64_t)(head / hpk) * HD;
+    int64_t off = (int64_t)(g_plant == OX_PLANT_GQA_MAP ? head % m->c.kv_heads : head / hpk) * HD;
     for (int64_t key = 0; key < keys; ++key) {
       float acc = 0.0f;
       for (int i = 0; i < HD; ++i)
@@ -1031,8 +1048,8 @@ static int step_batch(ox_session* se, const uint64_t* tokens, int64_t n, int64_t
         uint16_t* kt = kraw + t * KVS;
         for (int hh = 0; hh < c->q_heads; ++hh)
           memcpy(qn + hh * HD, qgt + 2 * hh * HD, 2 * (size_t)HD);
-        normalize_rows(qn, WF(m, l, 5), HD, c->q_heads, c->eps, qn);
-        normalize_rows(kt, WF(m, l, 6), HD, c->kv_heads, c->eps, kt);
+        normalize_rows(qn, WF(m, l, g_plant == OX_PLANT_QK_NORM_SWAP ? 6 : 5), HD, c->q_heads, c->eps, qn);
+        normalize_rows(kt, WF(m, l, g_plant == OX_PLANT_QK_NORM_SWAP ? 5 : 6), HD, c->kv_heads, c->eps, kt);
         rope_table(m, position, rope);
         for (int hh = 0; hh < c->q_heads; ++hh)
           rotate_head(qn + hh * HD, rope, (int)HD, c->rope_dim, qr + t * QS + hh * HD);
@@ -1150,8 +1167,8 @@ int ox_step(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
         project(x, WB(m, l, 3), KVS, H, width, vraw);
         for (int hh = 0; hh < c->q_heads; ++hh)
           memcpy(qn + hh * HD, qg + 2 * hh * HD, 2 * (size_t)HD);  /* qwen35.query */
-        normalize_rows(qn, WF(m, l, 5), HD, c->q_heads, c->eps, qn);
-        normalize_rows(kraw, WF(m, l, 6), HD, c->kv_heads, c->eps, kraw);
+        normalize_rows(qn, WF(m, l, g_plant == OX_PLANT_QK_NORM_SWAP ? 6 : 5), HD, c->q_heads, c->eps, qn);
+        normalize_rows(kraw, WF(m, l, g_plant == OX_PLANT_QK_NORM_SWAP ? 5 : 6), HD, c->kv_heads, c->eps, kraw);
         for (int hh = 0; hh < c->q_heads; ++hh)
           rotate_head(qn + hh * HD, rope, (int)HD, c->rope_dim, qr + hh * HD);
         for (int hh = 0; hh < c->kv_heads; ++hh)
@@ -1302,4 +1319,61 @@ void ox_moe_route(const uint16_t* x, const float* router, const float* shared_ro
   for (int64_t j = 0; j < K; ++j) ex[j] = ox_exp(sel[j] - sel[0]);
   for (int64_t j = 0; j < K; ++j) den = den + ex[j];
   for (int64_t j = 0; j < K; ++j) probs[j] = ex[j] / den;
+}
+
+/* ------------------------------------------ kernel-level entry points */
+/* One restated function each, on explicit buffers, for the per-function
+ * pins (tests/test_oracle_pins.py); dims come from the model's config. */
+
+void ox_k_normalize(const uint16_t* x, const float* w, int64_t cols, int64_t rows, float eps,
+                    uint16_t* out) {
+  normalize_rows(x, w, cols, rows, eps, out);
+}
+
+/* Head RMS norm with weights w (full_prepare.hex:20-48) then RoPE at
+ * `position` (rope.hex:5-82), for `heads` heads of head_dim. */
+void ox_k_prepare_heads(const ox_model* m, int64_t position, const uint16_t* in, const float* w,
+                        int64_t heads, uint16_t* out) {
+  const int HD = m->c.head_dim;
+  uint16_t* tmp = (uint16_t*)malloc(2 * (size_t)(heads * HD));
+  float rope[1024];
+  normalize_rows(in, w, HD, heads, m->c.eps, tmp);
+  rope_table(m, position, rope);
+  for (int64_t h = 0; h < heads; ++h) rotate_head(tmp + h * HD, rope, HD, m->c.rope_dim, out + h * HD);
+  free(tmp);
+}
+
+/* RoPE alone on already normalised heads. */
+void ox_k_rope(const ox_model* m, int64_t position, const uint16_t* in, int64_t heads, uint16_t* out) {
+  const int HD = m->c.head_dim;
+  float rope[1024];
+  rope_table(m, position, rope);
+  for (int64_t h = 0; h < heads; ++h) rotate_head(in + h * HD, rope, HD, m->c.rope_dim, out + h * HD);
+}
+
+/* Conv over a 3-slot history [3][QKV] (updated in place). */
+void ox_k_conv(const ox_model* m, uint16_t* history, int64_t position, const float* weight,
+               const uint16_t* qkv, uint16_t* out) {
+  conv_step(m, history, 0, position, weight, qkv, out);
+}
+
+void ox_k_l2(const uint16_t* in, int heads, int dim, uint16_t* out) { l2_heads(in, heads, dim, out); }
+
+void ox_k_delta(const ox_model* m, const uint16_t* conv, const uint16_t* q, const uint16_t* k,
+                const uint16_t* alpha, const uint16_t* beta, const float* dt, const float* a,
+                uint16_t* state16, float* state32, uint16_t* out) {
+  delta_step(m, conv, q, k, alpha, beta, dt, a, state16, state32, out);
+}
+
+void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z, const float* w,
+                     uint16_t* out) {
+  gated_norm(m, core, z, w, out);
+}
+
+/* Decode attention over `keys` cached rows: kv = [keys][KVS] keys then
+ * [keys][KVS] values; online (MoE decode) or staged (dense). */
+void ox_k_attention(const ox_model* m, int online, const uint16_t* q, const uint16_t* kv, int64_t keys,
+                    const uint16_t* qg, uint16_t* out) {
+  if (online) attention_online(m, q, kv, 0, keys * m->KVS, keys, qg, out);
+  else attention_staged(m, q, kv, 0, keys * m->KVS, keys, qg, out);
 }

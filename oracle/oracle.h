@@ -23,12 +23,22 @@
  *    (129-436), plus F32 random-dot fixtures that a wrong tree width fails.
  *  - ox_moe_gate_rows: within the reference test's own 1% bar
  *    (tests/qwen35_simt.rs:309-389).
- *  - ox_step (conv, L2 norms, gated delta rule, gated RMSNorm, online and
- *    staged attention, top-k, argmax, F32 multi-token fold): against a float64
- *    textbook formulation (relative RMS of logits < 0.15, a planted
- *    key-head-mapping mistake > 0.6). The exact orders inside these (D32, AP,
- *    SER, dense-staged, CONV) are therefore pinned only to tolerance:
- *    "parity partial".
+ *  - conv, L2 norms, gated delta rule (BF16 and F32 state), gated RMSNorm,
+ *    hidden and head RMS norms, RoPE (positions to 2^17), online and staged
+ *    attention (up to 4100 keys): each function against a float64 formulation
+ *    within 1-4 BF16 unit roundoffs (relative RMS), and each with planted
+ *    mistakes (ox_set_plant: rotation pairing / sign / frequency exponent,
+ *    q/k norm swap, conv tap order, delta scale, prediction decay, key-head
+ *    map, L2 span, gated mean, attention scale, GQA map, norm weights) that
+ *    miss by 12x the tolerance or more (tests/test_oracle_pins.py).
+ *  - ox_step: every cached K/V row and DeltaNet state after a short decode,
+ *    and the logits, new rows and state of one step at position 5000 from an
+ *    imported state, against a float64 textbook model within 10-12 U, the
+ *    same planted mistakes missing by 3x or more; logits of whole prompts
+ *    within 0.15 relative RMS. The exact reduction orders inside these
+ *    functions (D32, AP, SER, dense-staged, CONV) are restated from the Hex
+ *    text and no reference-held vector fixes them: those orders are pinned
+ *    to tolerance only.
  *  - parity unpinned: stdlib.math.round_to_u32 at exact .5 ties (taken as
  *    ties away from zero), f32.max with NaN operands, bf16x2 low/high order
  *    (taken as little-endian), core.fold.bounded order (taken as ascending).
@@ -125,6 +135,26 @@ const int64_t* ox_session_last_ids(const ox_session* s);
 
 void ox_set_threads(int n);
 
+/* Planted mistakes for the pinning tests (never set in normal use): each
+ * switches one restated function to a plausible wrong variant. */
+enum {
+  OX_PLANT_NONE = 0,
+  OX_PLANT_ROPE_PAIRING = 1,     /* interleaved (2i, 2i+1) rotation pairs */
+  OX_PLANT_ROPE_SIGN = 2,        /* rotation by -angle */
+  OX_PLANT_ROPE_FREQ_HD = 3,     /* frequency exponent over head_dim, not rope_dim */
+  OX_PLANT_QK_NORM_SWAP = 4,     /* q heads normed with k_norm and vice versa */
+  OX_PLANT_CONV_TAP_ORDER = 5,   /* conv taps applied in reverse order */
+  OX_PLANT_DELTA_SCALE = 6,      /* output dot without 1/sqrt(key_dim) */
+  OX_PLANT_L2_WHOLE = 7,         /* L2 norm over all heads at once */
+  OX_PLANT_GATED_SUM = 8,        /* gated RMS from the sum, not the mean */
+  OX_PLANT_ATTN_SCALE = 9,       /* scores without 1/sqrt(head_dim) */
+  OX_PLANT_GQA_MAP = 10,         /* query head h reads KV head h % kv_heads */
+  OX_PLANT_NORM_WEIGHT = 11,     /* RMS norms without their weights */
+  OX_PLANT_KEY_HEAD = 12,        /* value head h reads key head h / (VH/KH) */
+  OX_PLANT_DELTA_PRED_DECAY = 13 /* prediction from the undecayed state */
+};
+void ox_set_plant(int which);
+
 /* Kernel-level entry points for the known-answer tests. */
 void ox_project(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols, int width,
                 uint16_t* out);
@@ -141,6 +171,23 @@ void ox_moe_down_rows(const uint16_t* active, const uint16_t* down, const uint16
                       int64_t I, int64_t SI, uint16_t* out);
 void ox_moe_route(const uint16_t* x, const float* router, const float* shared_router, int64_t H,
                   int64_t E, int64_t K, float* logits, int64_t* ids, float* probs);
+
+/* One restated function each, on explicit buffers (per-function pins). */
+void ox_k_normalize(const uint16_t* x, const float* w, int64_t cols, int64_t rows, float eps,
+                    uint16_t* out);
+void ox_k_prepare_heads(const ox_model* m, int64_t position, const uint16_t* in, const float* w,
+                        int64_t heads, uint16_t* out);
+void ox_k_rope(const ox_model* m, int64_t position, const uint16_t* in, int64_t heads, uint16_t* out);
+void ox_k_conv(const ox_model* m, uint16_t* history, int64_t position, const float* weight,
+               const uint16_t* qkv, uint16_t* out);
+void ox_k_l2(const uint16_t* in, int heads, int dim, uint16_t* out);
+void ox_k_delta(const ox_model* m, const uint16_t* conv, const uint16_t* q, const uint16_t* k,
+                const uint16_t* alpha, const uint16_t* beta, const float* dt, const float* a,
+                uint16_t* state16, float* state32, uint16_t* out);
+void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z, const float* w,
+                     uint16_t* out);
+void ox_k_attention(const ox_model* m, int online, const uint16_t* q, const uint16_t* kv, int64_t keys,
+                    const uint16_t* qg, uint16_t* out);
 
 #ifdef __cplusplus
 }

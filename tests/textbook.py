@@ -57,6 +57,25 @@ class Textbook:
         self.K = [[] for _ in range(c["layers"])]
         self.V = [[] for _ in range(c["layers"])]
 
+    def import_cache(self, cache, capacity, position):
+        """Take over a BF16 session state in the reference layout
+        (src/spec.rs:321-362): K/V rows of positions < position, the conv
+        history of positions position-3 .. position-1 (slot p mod 3) and the
+        DeltaNet state."""
+        c = self.c
+        KVS = c["kv_heads"] * c["head_dim"]
+        kv = bf(cache[:c["layers"] * 2 * capacity * KVS]).reshape(c["layers"], 2, capacity,
+                                                                    c["kv_heads"], c["head_dim"])
+        tail = bf(cache[c["layers"] * 2 * capacity * KVS:]).reshape(c["layers"], -1)
+        conv = 3 * self.QKV
+        for l in range(c["layers"]):
+            self.K[l] = [kv[l, 0, p] for p in range(position)]
+            self.V[l] = [kv[l, 1, p] for p in range(position)]
+            slots = tail[l, :conv].reshape(3, self.QKV)
+            rows = [slots[(position + t) % 3] for t in range(3) if position - 3 + t >= 0]
+            self.hist[l] = np.array(rows).reshape(-1, self.QKV)
+            self.S[l] = tail[l, conv:].reshape(c["value_heads"], c["value_dim"], c["key_dim"]).copy()
+
     def W(self, l, s, rows=None, cols=None):
         a = bf(self.w[self.base[l] + s])
         if rows is not None:
