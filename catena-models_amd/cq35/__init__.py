@@ -6,9 +6,13 @@ from .model import (Model, Session, SessionCheckpoint, decode_batch, gguf_config
                     kernel_classes, read_logits, weight_count, weight_info)
 from ._lib import CQ35Error, LIBRARY, load
 
+# decode attention over more cached keys than this runs split-K by default
+# (include/cq35.h CQ35_SPLIT_KEYS_DEFAULT)
+SPLIT_KEYS_DEFAULT = 8192
+
 __all__ = [
     "PRESETS", "bytes_per_token", "derived", "is_full", "preset", "Model", "Session",
     "SessionCheckpoint", "decode_batch", "gguf_config", "gguf_tensor_name", "gguf_validate", "kernel_classes",
     "read_logits", "weight_count", "weight_info",
-    "CQ35Error", "LIBRARY", "load",
+    "CQ35Error", "LIBRARY", "load", "SPLIT_KEYS_DEFAULT",
 ]

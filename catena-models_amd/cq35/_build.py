@@ -40,17 +40,23 @@ def hipcc() -> str:
     return path if os.path.exists(path) else "hipcc"
 
 
-def build(verbose: bool = False) -> str:
-    """Always recompile (the driver's build check relies on this)."""
-    tmp = LIBRARY + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-o", tmp, SOURCE]
+TRACE_LIBRARY = os.path.join(PKG_DIR, "libcq35_trace.so")
+
+
+def build(verbose: bool = False, trace: bool = False) -> str:
+    """Always recompile (the driver's build check relies on this). With
+    trace=True, build the phase-trace variant (-DCQ35_PHASE_TRACE) into
+    libcq35_trace.so instead."""
+    out = TRACE_LIBRARY if trace else LIBRARY
+    tmp = out + ".tmp"
+    cmd = [hipcc(), *HIPCC_FLAGS, *(["-DCQ35_PHASE_TRACE"] if trace else []), "-o", tmp, SOURCE]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError("hipcc failed:\n" + proc.stderr[-8000:])
     if verbose and proc.stderr.strip():
         print(proc.stderr[-4000:])
-    os.replace(tmp, LIBRARY)
-    return LIBRARY
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -6,7 +6,8 @@ import os
 
 from .config import CConfig
 
-LIBRARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcq35.so")
+# CQ35_LIBRARY selects another in-tree build (the phase-trace library)
+LIBRARY = os.environ.get("CQ35_LIBRARY") or os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcq35.so")
 _lib = None
 
 
@@ -77,6 +78,9 @@ def load():
         "cq35_model_load_gguf": ([ctypes.c_char_p, ctypes.POINTER(P)], ctypes.c_int),
         "cq35_gguf_tensor_name": ([PC, I64, ctypes.c_char_p, I64], ctypes.c_int),
         "cq35_step_static": ([P, P, I64, U64, I64, P, ctypes.POINTER(U64), P], ctypes.c_int),
+        "cq35_session_set_attention_split": ([P, I64], ctypes.c_int),
+        "cq35_session_attention_split": ([P, ctypes.POINTER(I64)], ctypes.c_int),
+        "cq35_session_phase_trace": ([P, P, I64, ctypes.POINTER(I64), ctypes.POINTER(I64)], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(l, name)
@@ -103,5 +107,6 @@ EXPORTED = [
     "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
     "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv", "cq35_device_matrix_gemm",
     "cq35_gguf_config", "cq35_gguf_validate", "cq35_model_load_gguf", "cq35_gguf_tensor_name",
-    "cq35_step_batch", "cq35_step_static",
+    "cq35_step_batch", "cq35_step_static", "cq35_session_set_attention_split",
+    "cq35_session_attention_split", "cq35_session_phase_trace",
 ]

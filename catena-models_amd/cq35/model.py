@@ -301,6 +301,17 @@ class Session:
     MATRIX_PROJECTIONS = 1
     MATRIX_EXPERTS = 2
 
+    def set_attention_split(self, keys: int) -> None:
+        """Decode attention over more than `keys` cached keys as four merged
+        splits (0: the reference's single chain at every length)."""
+        check(_lib.load().cq35_session_set_attention_split(self._h, keys))
+
+    @property
+    def attention_split(self) -> int:
+        k = ctypes.c_int64()
+        check(_lib.load().cq35_session_attention_split(self._h, ctypes.byref(k)))
+        return k.value
+
     def set_matrix_prefill(self, components: int) -> None:
         """Run these components of multi-token calls on MFMA (hardware
         accumulation order; 0 = the exact SIMT path): MATRIX_PROJECTIONS,

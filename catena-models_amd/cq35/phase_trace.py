@@ -1,0 +1,188 @@
+"""Per-phase critical path of the persistent decode step.
+
+    python -m cq35.phase_trace [--config qwen36-35b-a3b] [--context 512]
+                               [--long 0] [--steps 8] [--build]
+
+Uses the phase-trace build of the library (libcq35_trace.so, compiled with
+-DCQ35_PHASE_TRACE; --build or a missing file compiles it), decodes `steps`
+tokens after a `context`-token prompt (or, with --long N, from a seeded
+state of N cached positions) and prints a markdown table for the last step:
+per phase of a linear (DeltaNet) and a full-attention layer, averaged over
+the layers of that kind,
+  - critical path: the last block's completion of the phase minus the last
+    block's completion of the phase before it in the chain;
+  - inputs in: the last block's end of polling for the phase's inputs minus
+    that previous completion (exchange latency plus any wait behind the
+    phase's own loads);
+  - the HBM floor of the phase's algorithmic bytes at 8 TB/s;
+and for full layers the values phase's busy time per role. Stamps are
+s_memrealtime (100 MHz, 10 ns).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+from . import _build, _lib
+from .config import derived, is_full, preset
+
+TRACE_LAYER_SLOTS = 20  # mega.h kTraceLayerSlots
+TRACE_LAYERS = 48
+TRACE_HEAD = TRACE_LAYERS * TRACE_LAYER_SLOTS
+TRACE_START = TRACE_HEAD + 1
+TICK_US = 0.01
+HBM_GBS = 8000.0
+
+LINEAR = ["project", "delta", None, "outproj", "router + shared", "select + gate/up", "down"]
+FULL = ["project", "scores", "values", "outproj", "router + shared", "select + gate/up", "down"]
+
+
+def phase_bytes(cfg: dict, keys: int) -> dict:
+    d = derived(cfg)
+    H, VH, VD, KD = cfg["hidden"], cfg["value_heads"], cfg["value_dim"], cfg["key_dim"]
+    K, I, SI, E = cfg["top_k"], cfg["intermediate"], cfg["shared_intermediate"], cfg["experts"]
+    return {
+        ("lin", "project"): (d["qkv"] + d["value_size"] + 2 * VH) * H * 2,
+        ("full", "project"): (2 * d["query_size"] + 2 * d["kvs"]) * H * 2,
+        ("lin", "delta"): 2 * VH * VD * KD * 2 + 4 * d["qkv"] * 2,
+        ("full", "scores"): keys * d["kvs"] * 2,
+        ("full", "values"): keys * d["kvs"] * 2,
+        ("lin", "outproj"): H * d["value_size"] * 2,
+        ("full", "outproj"): H * d["query_size"] * 2,
+        ("router + shared",): (E + 1) * H * 4 + 2 * SI * H * 2,
+        ("select + gate/up",): 2 * K * I * H * 2,
+        ("down",): (K * I + SI) * H * 2,
+    }
+
+
+def floor_us(pb: dict, kind: str, name: str) -> float:
+    b = pb.get((kind, name), pb.get((name,), 0))
+    return b / (HBM_GBS * 1e3)
+
+
+def analyse(trace: np.ndarray, cfg: dict, keys: int) -> str:
+    L = cfg["layers"]
+    start = trace[:, TRACE_START][trace[:, TRACE_START] > 0].min()
+    pb = phase_bytes(cfg, keys)
+    rows = {"lin": {}, "full": {}}
+    per_layer = []
+    prev_done = start
+    roles = []
+    for l in range(L):
+        tb = l * TRACE_LAYER_SLOTS
+        kind = "full" if is_full(cfg, l) else "lin"
+        names = FULL if kind == "full" else LINEAR
+        layer_start = prev_done
+        for p, name in enumerate(names):
+            if name is None:
+                continue
+            done = trace[:, tb + 2 * p].max()
+            polled = trace[:, tb + 2 * p + 1]
+            polled = polled[polled > 0]
+            inputs = (polled.max() - prev_done) if polled.size else 0
+            r = rows[kind].setdefault(name, [0.0, 0.0, 0])
+            r[0] += (done - prev_done) * TICK_US
+            r[1] += inputs * TICK_US
+            r[2] += 1
+            prev_done = done
+        per_layer.append((l, kind, (prev_done - layer_start) * TICK_US))
+        if kind == "full":
+            busy = trace[:, tb + 14:tb + 18].astype(np.float64).mean(axis=0) * TICK_US
+            roles.append(busy)
+    head = (trace[:, TRACE_HEAD].max() - prev_done) * TICK_US
+    total = (trace[:, TRACE_HEAD].max() - start) * TICK_US
+    out = []
+    for kind, names, label in [("lin", LINEAR, "linear (DeltaNet) layer"), ("full", FULL, "full-attention layer")]:
+        n = sum(1 for _, k, _ in per_layer if k == kind)
+        if n == 0:
+            continue
+        out.append(f"\n**{label}** (mean of {n} layers)\n")
+        out.append("| phase | critical path (us) | inputs in (us) | HBM floor at 8 TB/s (us) |")
+        out.append("|---|---|---|---|")
+        tot = 0.0
+        for name in names:
+            if name is None or name not in rows[kind]:
+                continue
+            c, i, cnt = rows[kind][name]
+            tot += c / cnt
+            out.append(f"| {name} | {c / cnt:.2f} | {i / cnt:.2f} | {floor_us(pb, kind, name):.2f} |")
+        out.append(f"| **layer** | **{tot:.2f}** | | |")
+    if roles:
+        b = np.mean(roles, axis=0)
+        out.append("\n**values phase, busy time per role** (mean per block and full layer, us): "
+                   f"scan {b[0]:.2f}, products (4 waves, summed) {b[1]:.2f}, channel chains {b[2]:.2f}, "
+                   f"denominator chain {b[3]:.2f}\n")
+    out.append(f"\nhead (final norm + vocabulary + argmax): {head:.2f} us "
+               f"(HBM floor {cfg['vocab'] * cfg['hidden'] * 2 / (HBM_GBS * 1e3):.2f} us); "
+               f"step from first stamp to head end: {total:.1f} us\n")
+    return "\n".join(out)
+
+
+def seeded_state(cfg: dict, capacity: int, position: int, seed: int) -> np.ndarray:
+    """BF16 state like the long-context benchmark's: K/V rows of positions
+    below `position` ~ 0.1 N(0,1), conv history ~ 0.1 N(0,1), DeltaNet state
+    ~ N(0,1) (numpy's generator; the timing does not depend on the values)."""
+    d = derived(cfg)
+    L, kvs = cfg["layers"], d["kvs"]
+    lin = d["conv"] + d["recurrent"]
+    rng = np.random.default_rng(seed)
+    out = np.zeros(capacity * L * 2 * kvs + L * lin, dtype=np.float32)
+    kv = out[:capacity * L * 2 * kvs].reshape(L * 2, capacity, kvs)
+    for r in range(L * 2):
+        kv[r, :position] = rng.standard_normal((position, kvs), dtype=np.float32) * 0.1
+    tail = out[capacity * L * 2 * kvs:].reshape(L, lin)
+    tail[:, :d["conv"]] = rng.standard_normal((L, d["conv"]), dtype=np.float32) * 0.1
+    tail[:, d["conv"]:] = rng.standard_normal((L, lin - d["conv"]), dtype=np.float32)
+    return (out.view(np.uint32) >> 16).astype(np.uint16)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--config", default="qwen36-35b-a3b")
+    ap.add_argument("--context", type=int, default=512)
+    ap.add_argument("--long", type=int, default=0, help="decode from a seeded state of this many positions")
+    ap.add_argument("--steps", type=int, default=8)
+    ap.add_argument("--build", action="store_true")
+    args = ap.parse_args()
+    if args.build or not os.path.exists(_build.TRACE_LIBRARY):
+        _build.build(trace=True)
+    _lib.LIBRARY = _build.TRACE_LIBRARY
+    from . import model as cq
+    cfg = preset(args.config)
+    m = cq.Model.synthetic(cfg, seed=0)
+    if args.long:
+        cap = args.long + args.steps + 4
+        s = m.session(cap)
+        s.import_state(0, seeded_state(cfg, cap, args.long, 101))
+        s.position = args.long
+        nxt = 1
+    else:
+        cap = args.context + args.steps + 4
+        s = m.session(cap)
+        nxt = s.append_next_token([(7 * i) % cfg["vocab"] for i in range(args.context)])
+    if not s.persistent:
+        print("this shape has no persistent decode step", file=sys.stderr)
+        return 2
+    for _ in range(args.steps):
+        nxt = s.decode_next_token(nxt)
+    lib = _lib.load()
+    slots, blocks = ctypes.c_int64(), ctypes.c_int64()
+    _lib.check(lib.cq35_session_phase_trace(s._h, None, 0, ctypes.byref(slots), ctypes.byref(blocks)))
+    n, blocks = slots.value, blocks.value
+    buf = np.zeros(blocks * n, dtype=np.uint64)
+    _lib.check(lib.cq35_session_phase_trace(s._h, buf.ctypes.data, buf.size, ctypes.byref(slots),
+                                            ctypes.byref(ctypes.c_int64())))
+    trace = buf.reshape(blocks, n).astype(np.int64)
+    keys = (args.long or args.context) + args.steps
+    print(f"{args.config}, {blocks} blocks, {'long ' + str(args.long) if args.long else 'context ' + str(args.context)}"
+          f" + {args.steps} steps (last step traced, about {keys} keys)")
+    print(analyse(trace, cfg, keys))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

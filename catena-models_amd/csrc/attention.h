@@ -58,21 +58,31 @@ __global__ __launch_bounds__(kScoreBlock) void k_attn_scores(
 // One wave per (query head, 16-channel chunk). Keys are processed in chunks
 // of up to kValueChunk: the wave stages the chunk's V slice into LDS with
 // 16-byte loads (all in flight at once) and computes the chunk's weights,
-// then 16 lanes run the channel chains from LDS and lane 16 the denominator.
+// then the lanes run the channel and denominator chains from LDS.
+//
+// Split-K above split_keys keys (0: never): tile t belongs to split t mod 4;
+// each split runs the online recurrence over its own tiles (its own running
+// maximum, alpha, denominator and accumulators) on lanes 16s..16s+15, and the
+// splits merge at the end in a fixed tree:
+// M = max m_s, w_s = exp(m_s - M), den = (d_0 w_0 + d_1 w_1) + (d_2 w_2 + d_3 w_3),
+// acc likewise. At or below the threshold one split runs the reference's
+// single chain (the other lanes repeat it), bit for bit.
 constexpr int kValueChannels = 16;
 constexpr int kValueChunk = 1024;
+constexpr int kValueSplits = 4;
 
 __global__ __launch_bounds__(64) void k_attn_values(
     const float* __restrict__ scores, int stride, const uint16_t* __restrict__ cache,
     int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs, int head_dim,
-    int heads_per_kv, const uint16_t* __restrict__ qg, uint16_t* __restrict__ out) {
+    int heads_per_kv, const uint16_t* __restrict__ qg, int64_t split_keys, uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) float lds[];
   const int head = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
   const int64_t keys = (int64_t)params[0] + t + 1;
   const int tiles = (int)((keys + 7) >> 3);
+  const int ns = (split_keys > 0 && keys > split_keys) ? kValueSplits : 1;
   float* mx = lds;                                   // running maximum per tile (all tiles)
   float* p = mx + ((tiles + 3) & ~3);                // weights of the current key chunk
-  float* alpha = p + kValueChunk;                    // exp(m_{t-1} - m_t) of the chunk
+  float* alpha = p + kValueChunk;                    // exp(m_prev - m_t) of the chunk
   u32x4* vs = reinterpret_cast<u32x4*>(alpha + kValueChunk / 8);  // [chunk keys][16 ch] bf16
   const float* s = scores + (size_t)head * stride;
   const float ninf = bitsf(0xff800000u);
@@ -86,12 +96,17 @@ __global__ __launch_bounds__(64) void k_attn_values(
     mx[i] = m;
   }
   __syncthreads();
+  float msplit[kValueSplits] = {ninf, ninf, ninf, ninf};  // each split's final maximum (lane 0)
   if (lane == 0) {
-    float m = ninf;
-    for (int i = 0; i < tiles; ++i) { m = fmaxf(m, mx[i]); mx[i] = m; }
+    for (int i = 0; i < tiles; ++i) {
+      const int sp = i & (ns - 1);
+      msplit[sp] = fmaxf(msplit[sp], mx[i]);
+      mx[i] = msplit[sp];
+    }
   }
   __syncthreads();
   const int c0 = chunk * kValueChannels;
+  const int sp = (lane >> 4) & (ns - 1);  // this lane's split; lane & 15 its channel
   const uint16_t* vbase = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c0;
   float acc = 0.0f, den = 0.0f;
   for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kValueChunk) {
@@ -109,26 +124,37 @@ __global__ __launch_bounds__(64) void k_attn_values(
     }
     for (int i = lane; i < n / 8; i += 64) {
       const int tile = (int)(k0 / 8) + i;
-      alpha[i] = hexp((tile > 0 ? mx[tile - 1] : ninf) - mx[tile]);
+      alpha[i] = hexp((tile >= ns ? mx[tile - ns] : ninf) - mx[tile]);
     }
     __syncthreads();
-    if (lane < kValueChannels) {
-      const uint16_t* vh = reinterpret_cast<const uint16_t*>(vs) + lane;
-      for (int i = 0; i < n / 8; ++i) {
-        acc = acc * alpha[i];
+    // chunk tiles i with i mod ns == sp (k0 / 8 is a multiple of 4): the
+    // channel chain and the split's denominator chain
+    const uint16_t* vh = reinterpret_cast<const uint16_t*>(vs) + (lane & 15);
+    for (int i = sp; i < n / 8; i += ns) {
+      acc = acc * alpha[i];
+      den = den * alpha[i];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = acc + p[i * 8 + j] * bf2f(vh[(i * 8 + j) * kValueChannels]);
-      }
-    } else if (lane == kValueChannels) {
-      for (int i = 0; i < n / 8; ++i) {
-        den = den * alpha[i];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) den = den + p[i * 8 + j];
+      for (int j = 0; j < 8; ++j) {
+        acc = acc + p[i * 8 + j] * bf2f(vh[(i * 8 + j) * kValueChannels]);
+        den = den + p[i * 8 + j];
       }
     }
     __syncthreads();
   }
-  den = __shfl(den, kValueChannels, 64);
+  if (ns > 1) {
+#pragma unroll
+    for (int q = 0; q < kValueSplits; ++q) msplit[q] = __shfl(msplit[q], 0, 64);
+    const float M = fmaxf(fmaxf(msplit[0], msplit[1]), fmaxf(msplit[2], msplit[3]));
+    float w[kValueSplits], a[kValueSplits], d[kValueSplits];
+#pragma unroll
+    for (int q = 0; q < kValueSplits; ++q) {
+      w[q] = hexp(msplit[q] - M);
+      a[q] = __shfl(acc, 16 * q + (lane & 15), 64);
+      d[q] = __shfl(den, 16 * q, 64);
+    }
+    acc = (a[0] * w[0] + a[1] * w[1]) + (a[2] * w[2] + a[3] * w[3]);
+    den = (d[0] * w[0] + d[1] * w[1]) + (d[2] * w[2] + d[3] * w[3]);
+  }
   const int c = c0 + lane;
   if (lane < kValueChannels && c < head_dim) {
     const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + c]));

@@ -122,6 +122,8 @@ struct MegaArgs {
   unsigned* error;
   unsigned spin_limit;
   int* ids_out;  // [L][K]: each layer's top-k expert ids of this step
+  int64_t split_keys;  // values phase splits over more keys than this (0: never)
+  uint64_t* trace;     // phase-trace builds: [grid][kTraceSlots] s_memrealtime stamps
 };
 
 // LDS carve-up (bytes); the "big" area is reused by the phases that need it.
@@ -144,10 +146,65 @@ struct MegaMisc {
   int abort;
   int any_nan;
   int bid, grid;  // block index and grid size, re-read by every phase
+  int tslot;      // phase-trace builds: the slot the current phase's poll stamps
 };
 static_assert(sizeof(MegaMisc) <= kLdsBig - kLdsMisc, "misc LDS");
 
 extern __shared__ __align__(16) unsigned char mega_lds[];
+
+// ------------------------------------------------------------ phase trace
+//
+// Built with -DCQ35_PHASE_TRACE, every block records s_memrealtime (100 MHz)
+// stamps in LDS and copies them to MegaArgs::trace at the end of the step:
+// per layer l, for phase p (0 project, 1 delta or scores, 2 values,
+// 3 output projection, 4 router, 5 gate/up, 6 down), slot
+// l * kTraceLayerSlots + 2p holds the time its last wave finished the phase
+// and 2p + 1 the time its inputs had all arrived (end of its poll); slots
+// 14-17 hold the values phase's busy time per role (scan, products, channel
+// chains, denominator chain) in 10 ns units. Slot kTraceHead is the head's
+// end, kTraceStart the step's start. Normal builds compile all of it away.
+constexpr int kTraceLayerSlots = 20;
+constexpr int kTraceLayers = 48;
+constexpr int kTraceHead = kTraceLayers * kTraceLayerSlots;
+constexpr int kTraceStart = kTraceHead + 1;
+constexpr int kTraceSlots = kTraceHead + 4;
+
+__device__ __forceinline__ uint64_t* trace_lds();
+
+__device__ __forceinline__ void trace_max(int slot) {
+#ifdef CQ35_PHASE_TRACE
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_max(trace_lds() + slot, (uint64_t)__builtin_amdgcn_s_memrealtime(), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+#else
+  (void)slot;
+#endif
+}
+
+__device__ __forceinline__ void trace_add(int slot, uint64_t v) {
+#ifdef CQ35_PHASE_TRACE
+  if ((threadIdx.x & 63) == 0)
+    __hip_atomic_fetch_add(trace_lds() + slot, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#else
+  (void)slot;
+  (void)v;
+#endif
+}
+
+// Busy time of one role loop: paused around each barrier.
+struct RoleClock {
+  uint64_t busy = 0, t0 = 0;
+  __device__ __forceinline__ void resume() {
+#ifdef CQ35_PHASE_TRACE
+    t0 = __builtin_amdgcn_s_memrealtime();
+#endif
+  }
+  __device__ __forceinline__ void pause() {
+#ifdef CQ35_PHASE_TRACE
+    busy += __builtin_amdgcn_s_memrealtime() - t0;
+#endif
+  }
+};
 
 // Pointers read from the argument tables are generic; every HBM access goes
 // through the global address space so it compiles to global (not flat)
@@ -291,6 +348,9 @@ __device__ __forceinline__ void poll_words(const Mega& m, int n, Addr addr, uint
     if (i < n) dst[i] = (uint32_t)v[j];
   }
   __syncthreads();
+#ifdef CQ35_PHASE_TRACE
+  trace_max(m.misc->tslot);
+#endif
 }
 
 // Words i of one buffer.
@@ -1397,7 +1457,8 @@ struct ValueLds {
   float mx[3][kValueTiles];
   int one[3];
   uint32_t vnew[kValueChannels / 2];
-  float den;
+  float den[4];     // each split's denominator
+  float msplit[4];  // each split's final running maximum
 };
 static_assert(sizeof(ValueLds) <= kLdsBigBytes, "value LDS");
 static_assert(kProdStride % 4 == 0 && offsetof(ValueLds, p) % 16 == 0 && offsetof(ValueLds, sc) % 16 == 0 &&
@@ -1405,17 +1466,17 @@ static_assert(kProdStride % 4 == 0 && offsetof(ValueLds, p) % 16 == 0 && offseto
               "16-byte reads of the value stages");
 static_assert(kMegaValueChunk == 4 * 64 && kMegaValueChunk == 2 * 128, "lane mapping of the value stages");
 
-// One channel chain (or the denominator chain) over nt tiles: row holds the
-// tiles' eight addends in key order, alpha the tiles' rescale factors. Four
-// tiles make a group; two register sets alternate, so the next group's
-// addends are read while the current group is summed, with no copies on
-// the chain's wave (the last read is clamped to a valid group).
+// One channel chain (or the denominator chain) over the tiles t = s, s + ns,
+// ... below nt of a chunk: row holds the tiles' eight addends in key order,
+// alpha the tiles' rescale factors. Four tiles make a group; two register
+// sets alternate, so the next group's addends are read while the current
+// group is summed, with no copies on the chain's wave (the last read is
+// clamped to a valid group). With ns = 1 this is every tile in order.
 template <bool SCALE>
-__device__ __forceinline__ float chain_group(float acc, const f32x4 (&x)[8], const f32x4& al) {
-  const float a4[4] = {al.x, al.y, al.z, al.w};
+__device__ __forceinline__ float chain_group(float acc, const f32x4 (&x)[8], const float (&al)[4]) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    if (SCALE) acc = acc * a4[t];
+    if (SCALE) acc = acc * al[t];
     const f32x4 x0 = x[2 * t], x1 = x[2 * t + 1];
     acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
     acc = acc + x1.x; acc = acc + x1.y; acc = acc + x1.z; acc = acc + x1.w;
@@ -1424,16 +1485,22 @@ __device__ __forceinline__ float chain_group(float acc, const f32x4 (&x)[8], con
 }
 
 template <bool SCALE>
-__device__ __forceinline__ float value_chain(float acc, const f32x4* row, const float* alpha, int nt) {
-  const int groups = nt >> 2;
-  const f32x4* al4 = reinterpret_cast<const f32x4*>(alpha);
-  f32x4 xa[8], xb[8], aa, ab;
+__device__ __forceinline__ float value_chain(float acc, const f32x4* row, const float* alpha, int nt, int s,
+                                             int ns) {
+  const int count = s < nt ? (nt - 1 - s) / ns + 1 : 0;  // this split's tiles in the chunk
+  const int groups = count >> 2;
+  f32x4 xa[8], xb[8];
+  float aa[4], ab[4];
   // the scheduler would sink the reads next to their first use; the
   // barrier keeps them issued ahead of the group being summed
-  auto load = [&](f32x4 (&x)[8], f32x4& al, int g) {
+  auto load = [&](f32x4 (&x)[8], float (&al)[4], int g) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = row[8 * g + j];
-    if (SCALE) al = al4[g];
+    for (int u = 0; u < 4; ++u) {
+      const int t = s + ns * (4 * g + u);
+      x[2 * u] = row[2 * t];
+      x[2 * u + 1] = row[2 * t + 1];
+      if (SCALE) al[u] = alpha[t];
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
   if (groups > 0) load(xa, aa, 0);
@@ -1447,7 +1514,8 @@ __device__ __forceinline__ float value_chain(float acc, const f32x4* row, const 
   }
   if (g < groups) acc = chain_group<SCALE>(acc, xa, aa);
 #pragma unroll 1
-  for (int t = 4 * groups; t < nt; ++t) {
+  for (int j = 4 * groups; j < count; ++j) {
+    const int t = s + ns * j;
     if (SCALE) acc = acc * alpha[t];
     const f32x4 x0 = row[2 * t], x1 = row[2 * t + 1];
     acc = acc + x0.x; acc = acc + x0.y; acc = acc + x0.z; acc = acc + x0.w;
@@ -1476,7 +1544,7 @@ __device__ __forceinline__ int value_item(int slot) {
 }
 
 template <class S>
-__device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
+__device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int tb) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
@@ -1488,6 +1556,9 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   const int nch = (int)((padded + kMegaValueChunk - 1) / kMegaValueChunk);
   ValueLds* s = reinterpret_cast<ValueLds*>(m.big);
   const float ninf = bitsf(0xff800000u);
+  // split-K over long contexts: tile t in split t mod ns (see attention.h)
+  const int ns = (a.split_keys > 0 && keys > a.split_keys) ? 4 : 1;
+  const int sp = (m.lane >> 4) & (ns - 1);  // chain waves: this lane's split
   const int pj = m.tid - 4 * 64;  // producer thread (waves 4-7)
   const int ph = pj & 1;          // channels 8 ph .. 8 ph + 7
 #pragma unroll 1
@@ -1516,6 +1587,8 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
     using R2 = std::integral_constant<int, 2>;
     uint32_t gate_word = 0;
     float acc = 0.0f, den = 0.0f;
+    RoleClock clk;  // phase-trace builds: this role's busy time
+    clk.resume();
     if (m.wave <= 1) {
       if (m.wave == 0) {
         if (m.lane < kValueChannels / 2)
@@ -1533,16 +1606,18 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
           const bool one = s->one[slot] != 0;
           if (m.wave == 0) {
             const f32x4* row = reinterpret_cast<const f32x4*>(s->prod[buf] + (m.lane & 15) * kProdStride);
-            acc = one ? value_chain<false>(acc, row, s->alpha[slot], nt)
-                      : value_chain<true>(acc, row, s->alpha[slot], nt);
+            acc = one ? value_chain<false>(acc, row, s->alpha[slot], nt, sp, ns)
+                      : value_chain<true>(acc, row, s->alpha[slot], nt, sp, ns);
           } else {
             const f32x4* row = reinterpret_cast<const f32x4*>(s->p[buf]);
-            den = one ? value_chain<false>(den, row, s->alpha[slot], nt)
-                      : value_chain<true>(den, row, s->alpha[slot], nt);
-            if (m.lane == 0) s->den = den;
+            den = one ? value_chain<false>(den, row, s->alpha[slot], nt, sp, ns)
+                      : value_chain<true>(den, row, s->alpha[slot], nt, sp, ns);
+            if ((m.lane & 15) == 0) s->den[sp] = den;
           }
         }
+        clk.pause();
         __syncthreads();
+        clk.resume();
       }
     } else if (m.wave == 2) {
       uint64_t sr[kScoreRing][4];  // slot r: chunks = r mod 3
@@ -1580,15 +1655,16 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
           float mt = fmaxf(fmaxf(kl < keys ? sv.x : ninf, kl + 1 < keys ? sv.y : ninf),
                            fmaxf(kl + 2 < keys ? sv.z : ninf, kl + 3 < keys ? sv.w : ninf));
           mt = fmaxf(mt, __shfl_xor(mt, 1, 64));  // the tile's two lanes
+          // running maximum over the split's tiles (lanes 2 ns apart): a
+          // prefix maximum is exact in any association
           float run = mt;
-#pragma unroll
-          for (int d = 1; d < 64; d <<= 1) {
+          for (int d = 2 * ns; d < 64; d <<= 1) {
             const float o = __shfl_up(run, d, 64);
             if (m.lane >= d) run = fmaxf(run, o);
           }
           run = fmaxf(run, carry);
-          float prev = __shfl_up(run, 2, 64);
-          if (m.lane < 2) prev = i == 0 ? ninf : carry;
+          float prev = __shfl_up(run, 2 * ns, 64);
+          if (m.lane < 2 * ns) prev = i == 0 ? ninf : carry;
           const float al = hexp(prev - run);
           const int t = m.lane >> 1;
           const bool valid = (m.lane & 1) == 0 && (int64_t)i * kValueTiles + t < tiles;
@@ -1598,9 +1674,13 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
           }
           const uint64_t scaled = __ballot(valid && al != 1.0f);
           if (m.lane == 0) s->one[slot] = scaled == 0ull ? 1 : 0;
-          carry = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, run), 63));
+          // each split's running maximum at its last tile of the chunk
+          carry = __shfl(run, 64 - 2 * ns + 2 * ((m.lane >> 1) & (ns - 1)), 64);
+          if (i == nch - 1 && m.lane < 2 * ns && !(m.lane & 1)) s->msplit[m.lane >> 1] = carry;
         }
+        clk.pause();
         __syncthreads();
+        clk.resume();
       };
       int i = 0;
 #pragma unroll 1
@@ -1648,7 +1728,9 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
           for (int q = 0; q < 2; ++q)
             vr[r][q] = load_v(k0 + (int64_t)kValueRing * kMegaValueChunk + (pj >> 1) + 128 * q);
         }
+        clk.pause();
         __syncthreads();
+        clk.resume();
       };
       // iteration i produces chunk i - 1, whose ring slot is (i + 2) mod 3
       int i = 0;
@@ -1664,8 +1746,25 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
 #pragma unroll 1
       for (int i = 0; i < n_iter; ++i) __syncthreads();
     }
+    // role busy times: scan (wave 2), products (waves 4-7, summed), channel
+    // chains (wave 0), denominator chain (wave 1)
+    if (m.wave <= 2 || m.wave >= 4)
+      trace_add(tb + 14 + (m.wave == 2 ? 0 : m.wave >= 4 ? 1 : m.wave == 0 ? 2 : 3), clk.busy);
     if (m.wave == 0) {
-      den = s->den;
+      den = s->den[0];
+      if (ns > 1) {
+        // merge the splits in a fixed tree (the per-kernel path and the
+        // restatement use the same one)
+        const float M = fmaxf(fmaxf(s->msplit[0], s->msplit[1]), fmaxf(s->msplit[2], s->msplit[3]));
+        float w[4], av[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          w[q] = hexp(s->msplit[q] - M);
+          av[q] = __shfl(acc, 16 * q + (m.lane & 15), 64);
+        }
+        acc = (av[0] * w[0] + av[1] * w[1]) + (av[2] * w[2] + av[3] * w[3]);
+        den = (s->den[0] * w[0] + s->den[1] * w[1]) + (s->den[2] * w[2] + s->den[3] * w[3]);
+      }
       const uint32_t gw = __shfl((int)gate_word, m.lane >> 1, 64);
       const uint16_t gb = (m.lane & 1) ? (uint16_t)(gw >> 16) : (uint16_t)(gw & 0xffffu);
       uint16_t y = 0;
@@ -1766,6 +1865,30 @@ constexpr int mega_lds_bytes() {
   return kLdsBig + mega_big_bytes<S>();
 }
 
+// Phase-trace stamps sit after the largest shape's LDS.
+constexpr int kTraceLdsOffset = mega_lds_bytes<Shape35BA3B>();
+static_assert(mega_lds_bytes<ShapeMiniMoE>() <= kTraceLdsOffset && mega_lds_bytes<ShapeTinyMoE>() <= kTraceLdsOffset,
+              "trace offset");
+__device__ __forceinline__ uint64_t* trace_lds() { return reinterpret_cast<uint64_t*>(mega_lds + kTraceLdsOffset); }
+
+// Dynamic LDS the launch requests.
+template <class S>
+constexpr int mega_lds_request() {
+#ifdef CQ35_PHASE_TRACE
+  return kTraceLdsOffset + kTraceSlots * 8;
+#else
+  return mega_lds_bytes<S>();
+#endif
+}
+
+__device__ __forceinline__ void trace_slot(int slot) {
+#ifdef CQ35_PHASE_TRACE
+  if (threadIdx.x == 0) reinterpret_cast<MegaMisc*>(mega_lds + kLdsMisc)->tslot = slot;
+#else
+  (void)slot;
+#endif
+}
+
 template <class S>
 __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict__ pa) {
   const uint32_t tag = (uint32_t)G(pa->params)[2];
@@ -1781,6 +1904,10 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
   }
+#ifdef CQ35_PHASE_TRACE
+  for (int i = threadIdx.x; i < kTraceSlots; i += kMT) trace_lds()[i] = 0;
+  if (threadIdx.x == 0) trace_lds()[kTraceStart] = __builtin_amdgcn_s_memrealtime();
+#endif
   __syncthreads();
   const int L = pa->L;
   const MegaLayer* layers = pa->layers;
@@ -1788,21 +1915,46 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
   issue_project<S, 0, kPairsEarly>(pa, layers, pr);
   for (int l = 0; l < L; ++l) {
     const MegaLayer* ly = layers + l;
+    const int tb = l * kTraceLayerSlots;  // phase p: done at tb + 2p, inputs in at tb + 2p + 1
+    trace_slot(tb + 1);
     phase_project<S>(pa, tag, ly, l, pr);
+    trace_max(tb + 0);
     if (phase_ptr(ly)->full != 0) {
+      trace_slot(tb + 3);
       phase_scores<S>(pa, tag, ly);
-      phase_values<S>(pa, tag, ly);
+      trace_max(tb + 2);
+      trace_slot(tb + 5);
+      phase_values<S>(pa, tag, ly, tb);
+      trace_max(tb + 4);
+      trace_slot(tb + 7);
       phase_outproj<S, S::QS>(pa, tag, ly);
     } else {
+      trace_slot(tb + 3);
       phase_delta<S>(pa, tag, ly);
+      trace_max(tb + 2);
       __syncthreads();
+      trace_slot(tb + 7);
       phase_outproj<S, S::VS>(pa, tag, ly);
     }
+    trace_max(tb + 6);
+    trace_slot(tb + 9);
     phase_router<S>(pa, tag, ly);
+    trace_max(tb + 8);
+    trace_slot(tb + 11);
     phase_gate_up<S>(pa, tag, ly, l);
+    trace_max(tb + 10);
+    trace_slot(tb + 13);
     phase_down<S>(pa, tag, ly, l + 1 < L ? ly + 1 : nullptr, pr);
+    trace_max(tb + 12);
   }
+  trace_slot(kTraceHead + 2);
   phase_head<S>(pa, tag);
+  trace_max(kTraceHead);
+#ifdef CQ35_PHASE_TRACE
+  __syncthreads();
+  for (int i = threadIdx.x; i < kTraceSlots; i += kMT)
+    pa->trace[(size_t)blockIdx.x * kTraceSlots + i] = trace_lds()[i];
+#endif
 }
 
 }  // namespace cq35

@@ -767,6 +767,7 @@ struct cq35_session {
   int* pf_ids = nullptr;
   int pf_attn_tokens = 0;  // tokens per staged-attention launch (scratch rows)
   int matrix = 0;          // CQ35_MATRIX_* components of multi-token calls on MFMA
+  int64_t split_keys = CQ35_SPLIT_KEYS_DEFAULT;  // decode attention splits above this many keys
   // kernel timing
   int timed_class = -1;
   hipEvent_t ev[2 * kMaxTimedEvents] = {};
@@ -832,9 +833,9 @@ int mega_kind(const cq35_config& c, int grid) {
 
 int mega_lds(int kind) {
   switch (kind) {
-    case kMega35B: return mega_lds_bytes<Shape35BA3B>();
-    case kMegaMini: return mega_lds_bytes<ShapeMiniMoE>();
-    case kMegaTiny: return mega_lds_bytes<ShapeTinyMoE>();
+    case kMega35B: return mega_lds_request<Shape35BA3B>();
+    case kMegaMini: return mega_lds_request<ShapeMiniMoE>();
+    case kMegaTiny: return mega_lds_request<ShapeTinyMoE>();
     default: return 0;
   }
 }
@@ -969,7 +970,14 @@ int setup_mega(cq35_session* s) {
   a.best = s->d_best;
   a.error = reinterpret_cast<unsigned*>(s->d_best + 1);
   a.ids_out = s->ids;
+  a.split_keys = s->split_keys;
   a.spin_limit = 1u << 21;
+#ifdef CQ35_PHASE_TRACE
+  p = nullptr;
+  HIP_TRY(hipMalloc(&p, (size_t)grid * kTraceSlots * sizeof(uint64_t)));
+  s->allocations.push_back(p);
+  a.trace = static_cast<uint64_t*>(p);
+#endif
   if (const char* lim = getenv("CQ35_SPIN_LIMIT")) a.spin_limit = (unsigned)strtoul(lim, nullptr, 10);
   p = nullptr;
   HIP_TRY(hipMalloc(&p, sizeof(MegaArgs)));
@@ -1226,7 +1234,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           dim3((unsigned)d.Q, (unsigned)((d.HD + kValueChannels - 1) / kValueChannels)), dim3(64),
           attn_values_lds_bytes(cap), (const float*)s->attn_scratch,
           s->attn_stride, (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t,
-          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->ctx);
+          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->split_keys, s->ctx);
       } else {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
@@ -1615,6 +1623,58 @@ extern "C" int cq35_session_set_persistent(cq35_session* s, int enabled) {
   return CQ35_OK;
 }
 
+extern "C" int cq35_session_set_attention_split(cq35_session* s, int64_t keys) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  if (keys < 0) return fail(CQ35_EINVAL, "split threshold %lld is negative", (long long)keys);
+  if (keys == s->split_keys) return CQ35_OK;
+  HIP_TRY(hipSetDevice(s->model->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  s->split_keys = keys;
+  // the captured decode graph and the persistent kernel's arguments hold it
+  if (s->graph_exec) {
+    hipGraphExecDestroy(s->graph_exec);
+    s->graph_exec = nullptr;
+  }
+  if (s->graph) {
+    hipGraphDestroy(s->graph);
+    s->graph = nullptr;
+  }
+  if (s->mega_ok) {
+    s->margs.split_keys = keys;
+    HIP_TRY(hipMemcpy(s->d_margs, &s->margs, sizeof(MegaArgs), hipMemcpyHostToDevice));
+  }
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_attention_split(const cq35_session* s, int64_t* keys) {
+  if (!s || !keys) return fail(CQ35_EINVAL, "null argument");
+  *keys = s->split_keys;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_phase_trace(const cq35_session* s, uint64_t* dst, int64_t count, int64_t* slots,
+                                        int64_t* blocks) {
+  if (!s || !slots || !blocks) return fail(CQ35_EINVAL, "null argument");
+#ifdef CQ35_PHASE_TRACE
+  if (!s->mega_ok) return fail(CQ35_EUNSUPPORTED, "the session has no persistent decode step");
+  *slots = kTraceSlots;
+  *blocks = s->mega_grid;
+  const int64_t need = (int64_t)s->mega_grid * kTraceSlots;
+  if (!dst) return CQ35_OK;
+  if (count != need) return fail(CQ35_EINVAL, "the trace has %lld stamps", (long long)need);
+  HIP_TRY(hipSetDevice(s->model->device));
+  HIP_TRY(hipStreamSynchronize(s->stream));
+  HIP_TRY(hipMemcpy(dst, s->margs.trace, need * sizeof(uint64_t), hipMemcpyDeviceToHost));
+  return CQ35_OK;
+#else
+  (void)dst;
+  (void)count;
+  *slots = 0;
+  *blocks = 0;
+  return fail(CQ35_EUNSUPPORTED, "phase stamps exist only in a library built with CQ35_PHASE_TRACE");
+#endif
+}
+
 extern "C" int cq35_session_set_matrix_prefill(cq35_session* s, int components) {
   if (!s) return fail(CQ35_EINVAL, "null argument");
   if (components & ~(CQ35_MATRIX_PROJECTIONS | CQ35_MATRIX_EXPERTS))
@@ -1837,6 +1897,13 @@ extern "C" int cq35_session_copy(const cq35_session* src, cq35_session** out) {
   }
   s->graph_enabled = src->graph_enabled;
   s->matrix = src->matrix;  // session options travel with the state
+  if (src->split_keys != s->split_keys) {
+    const int r = cq35_session_set_attention_split(s, src->split_keys);
+    if (r) {
+      destroy_session(s);
+      return r;
+    }
+  }
   s->mega_on = src->mega_on && s->mega_ok;
   *out = s;
   return CQ35_OK;

@@ -202,6 +202,13 @@ int cq35_session_time_kernel(cq35_session* session, int kernel_class);
 int cq35_session_kernel_time(cq35_session* session, double* total_ms, int64_t* launches);
 const char* cq35_kernel_class_name(int kernel_class);
 int cq35_kernel_class_count(void);
+/* Phase stamps of the last persistent decode step, in a library built with
+ * -DCQ35_PHASE_TRACE (otherwise CQ35_EUNSUPPORTED): `*slots` stamps per
+ * block (s_memrealtime, 100 MHz) for each of the `*blocks` blocks of the
+ * step; with dst != NULL, count must be blocks x slots. Slot meanings:
+ * mega.h, phase trace. No reference counterpart (measurement only). */
+int cq35_session_phase_trace(const cq35_session* session, uint64_t* dst, int64_t count, int64_t* slots,
+                             int64_t* blocks);
 /* Disable (0) or enable (1, default) hipGraph replay of the decode step. */
 int cq35_session_set_graph(cq35_session* session, int enabled);
 
@@ -221,6 +228,19 @@ int cq35_session_persistent(const cq35_session* session, int* enabled);
  * dense projections (attention, DeltaNet and output projections, dense FFN);
  * bit 1: the MoE expert projections (grouped routed experts and the shared
  * expert). 0 keeps the exact SIMT path. Decode steps are unaffected. */
+/* Split-K decode attention for long contexts. Over more than `keys` cached
+ * keys (default CQ35_SPLIT_KEYS_DEFAULT; 0: never) the online softmax of each
+ * query head runs as four splits, tile t (8 keys) in split t mod 4, each the
+ * reference's recurrence over its own tiles, merged in a fixed tree
+ * (M = max m_s, w_s = exp(m_s - M), den = (d0 w0 + d1 w1) + (d2 w2 + d3 w3),
+ * likewise each channel). The reference runs one sequential chain over all
+ * tiles (qwen35_online.hex:272-331); the split changes rounding only
+ * (tolerance-level), and at or below the threshold the result is the
+ * reference's bit for bit. Both decode paths use the same split. */
+#define CQ35_SPLIT_KEYS_DEFAULT 8192
+int cq35_session_set_attention_split(cq35_session* session, int64_t keys);
+int cq35_session_attention_split(const cq35_session* session, int64_t* keys);
+
 #define CQ35_MATRIX_PROJECTIONS 1
 #define CQ35_MATRIX_EXPERTS 2
 int cq35_session_set_matrix_prefill(cq35_session* session, int components);

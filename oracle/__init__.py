@@ -93,7 +93,8 @@ def lib():
         l.ox_k_l2.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
         l.ox_k_delta.argtypes = [P, P, P, P, P, P, P, P, P, P, P]
         l.ox_k_gated_norm.argtypes = [P, P, P, P, P]
-        l.ox_k_attention.argtypes = [P, ctypes.c_int, P, P, I64, P, P]
+        l.ox_k_attention.argtypes = [P, ctypes.c_int, P, P, I64, P, I64, P]
+        l.ox_session_set_split_keys.argtypes = [P, I64]
         _lib = l
     return _lib
 
@@ -246,6 +247,11 @@ class Session:
         if src.size != n:
             raise ValueError(f"state has {src.size} elements, expected {n}")
         np.ctypeslib.as_array(lib().ox_session_cache(self._h), shape=(n,))[:] = src
+
+    def set_split_keys(self, keys: int) -> None:
+        """Decode attention over more than `keys` keys as four merged splits
+        (0: the reference's single chain at every length)."""
+        lib().ox_session_set_split_keys(self._h, keys)
 
     def last_ids(self) -> np.ndarray:
         c = self.model.cfg

@@ -502,6 +502,7 @@ struct ox_session {
   uint16_t* cache;
   float* shadow;
   int64_t* last_ids;
+  int64_t split_keys;  /* decode attention over more keys than this splits (0: never) */
 };
 
 ox_session* ox_session_create(const ox_model* m, int64_t capacity) {
@@ -511,8 +512,10 @@ ox_session* ox_session_create(const ox_model* m, int64_t capacity) {
   s->cache = (uint16_t*)calloc((size_t)ox_cache_elements(&m->c, capacity), 2);
   s->shadow = (float*)calloc((size_t)(m->REC * m->c.layers), 4);
   s->last_ids = (int64_t*)calloc((size_t)(m->c.layers * (m->c.top_k > 0 ? m->c.top_k : 1)), 8);
+  s->split_keys = OX_SPLIT_KEYS_DEFAULT;
   return s;
 }
+void ox_session_set_split_keys(ox_session* s, int64_t keys) { s->split_keys = keys; }
 void ox_session_free(ox_session* s) {
   if (!s) return;
   free(s->cache); free(s->shadow); free(s->last_ids); free(s);
@@ -697,50 +700,72 @@ static void gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* 
   }
 }
 
-/* Online decode attention, 8-key tiles (online.hex:4-331). */
+/* Online decode attention, 8-key tiles (online.hex:4-331).
+ *
+ * Split-K above split_keys keys (this build's long-context mode; the
+ * reference always runs one chain): tile t belongs to split t mod 4, and each
+ * split runs the reference's online recurrence over its own tiles in order
+ * (running maximum m_s, den_s = den_s a + p_0 + ... + p_7, acc_s = acc_s a +
+ * p_0 v_0 + ...). The splits merge in a fixed tree: M = max_s m_s,
+ * w_s = exp(m_s - M), den = (den_0 w_0 + den_1 w_1) + (den_2 w_2 + den_3 w_3),
+ * acc likewise; out = bf16(bf16(acc / den) * sigmoid(gate)). At or below
+ * split_keys (and with split_keys = 0) the single chain is the reference's. */
 static void attention_online(const ox_model* m, const uint16_t* q, const uint16_t* cache,
                              int64_t key_base, int64_t value_base, int64_t keys,
-                             const uint16_t* qg, uint16_t* out) {
+                             const uint16_t* qg, int64_t split_keys, uint16_t* out) {
   const int HD = m->c.head_dim, hpk = m->c.q_heads / m->c.kv_heads;
   const int64_t KVS = m->KVS;
+  const int NS = (split_keys > 0 && keys > split_keys) ? 4 : 1;
   const float scale = g_plant == OX_PLANT_ATTN_SCALE ? 1.0f : 1.0f / sqrtf((float)HD);  /* SCALE_BITS, qwen35.rs:701 */
 #pragma omp parallel for schedule(static)
   for (int head = 0; head < m->c.q_heads; ++head) {
     int64_t off = (int64_t)(g_plant == OX_PLANT_GQA_MAP ? head % m->c.kv_heads : head / hpk) * HD;
-    float maximum = bitsf(0xFF800000u), den = 0.0f;
-    float* value = (float*)calloc((size_t)HD, sizeof(float));
+    float maximum[4], den[4];
+    float* value = (float*)calloc((size_t)(4 * HD), sizeof(float));
+    for (int sp = 0; sp < 4; ++sp) { maximum[sp] = bitsf(0xFF800000u); den[sp] = 0.0f; }
     for (int64_t first = 0; first < keys; first += 8) {
+      const int sp = (int)((first / 8) % NS);
+      float* acc = value + sp * HD;
       float score[8], p[8];
       for (int j = 0; j < 8; ++j) {
         int64_t key = first + j;
         if (key >= keys) { score[j] = bitsf(0xFF800000u); continue; }
         float lanes[32];
         for (int l = 0; l < 32; ++l) {
-          float acc = 0.0f;
+          float a = 0.0f;
           for (int ch = l; ch < HD; ch += 32)
-            acc += ox_bf2f(q[head * HD + ch]) * ox_bf2f(cache[key_base + key * KVS + off + ch]);
-          lanes[l] = acc;
+            a += ox_bf2f(q[head * HD + ch]) * ox_bf2f(cache[key_base + key * KVS + off + ch]);
+          lanes[l] = a;
         }
         score[j] = tree(lanes, 32) * scale;
       }
-      float next_max = maximum;
+      float next_max = maximum[sp];
       for (int j = 0; j < 8; ++j) next_max = fmaxf(next_max, score[j]);
-      float alpha = ox_exp(maximum - next_max);
-      den = den * alpha;
-      for (int j = 0; j < 8; ++j) { p[j] = ox_exp(score[j] - next_max); den = den + p[j]; }
-      maximum = next_max;
+      float alpha = ox_exp(maximum[sp] - next_max);
+      den[sp] = den[sp] * alpha;
+      for (int j = 0; j < 8; ++j) { p[j] = ox_exp(score[j] - next_max); den[sp] = den[sp] + p[j]; }
+      maximum[sp] = next_max;
       for (int ch = 0; ch < HD; ++ch) {
-        float v = value[ch] * alpha;
+        float v = acc[ch] * alpha;
         for (int j = 0; j < 8; ++j) {
           int64_t key = first + j < keys ? first + j : 0;
           v = v + p[j] * ox_bf2f(cache[value_base + key * KVS + off + ch]);
         }
-        value[ch] = v;
+        acc[ch] = v;
       }
     }
+    float w[4] = {1.0f, 0.0f, 0.0f, 0.0f}, total = den[0];
+    if (NS == 4) {
+      const float M = fmaxf(fmaxf(maximum[0], maximum[1]), fmaxf(maximum[2], maximum[3]));
+      for (int sp = 0; sp < 4; ++sp) w[sp] = ox_exp(maximum[sp] - M);
+      total = (den[0] * w[0] + den[1] * w[1]) + (den[2] * w[2] + den[3] * w[3]);
+    }
     for (int ch = 0; ch < HD; ++ch) {
+      float a = value[ch];
+      if (NS == 4)
+        a = (value[ch] * w[0] + value[HD + ch] * w[1]) + (value[2 * HD + ch] * w[2] + value[3 * HD + ch] * w[3]);
       float gate = ox_sigmoid(ox_bf2f(qg[2 * (int64_t)head * HD + HD + ch]));
-      out[head * HD + ch] = ox_f2bf(rbf(value[ch] / den) * gate);
+      out[head * HD + ch] = ox_f2bf(rbf(a / total) * gate);
     }
     free(value);
   }
@@ -1176,7 +1201,7 @@ int ox_step(ox_session* se, const uint64_t* tokens, int64_t n, int64_t start,
                       se->cache + key_off + position * KVS + hh * HD);
         memcpy(se->cache + value_off + position * KVS, vraw, 2 * (size_t)KVS);
         if (c->moe)
-          attention_online(m, qr, se->cache, key_off, value_off, position + 1, qg, ctx);
+          attention_online(m, qr, se->cache, key_off, value_off, position + 1, qg, se->split_keys, ctx);
         else
           attention_staged(m, qr, se->cache, key_off, value_off, position + 1, qg, ctx);
         residual_project(ctx, WB(m, l, 4), H, QS, h, attn);
@@ -1373,7 +1398,7 @@ void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z,
 /* Decode attention over `keys` cached rows: kv = [keys][KVS] keys then
  * [keys][KVS] values; online (MoE decode) or staged (dense). */
 void ox_k_attention(const ox_model* m, int online, const uint16_t* q, const uint16_t* kv, int64_t keys,
-                    const uint16_t* qg, uint16_t* out) {
-  if (online) attention_online(m, q, kv, 0, keys * m->KVS, keys, qg, out);
+                    const uint16_t* qg, int64_t split_keys, uint16_t* out) {
+  if (online) attention_online(m, q, kv, 0, keys * m->KVS, keys, qg, split_keys, out);
   else attention_staged(m, q, kv, 0, keys * m->KVS, keys, qg, out);
 }

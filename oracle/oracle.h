@@ -130,6 +130,14 @@ float* ox_session_shadow(ox_session* s);
 int ox_step(ox_session* s, const uint64_t* tokens, int64_t n, int64_t start,
             uint64_t* next_token, uint16_t* logits);
 
+/* Decode attention (online, MoE) over more than `keys` cached keys runs as
+ * four interleaved splits merged at the end (this build's long-context
+ * mode, tolerance-level against the reference's single chain); 0 keeps the
+ * single chain at every length. Default OX_SPLIT_KEYS_DEFAULT, the GPU
+ * library's default. */
+#define OX_SPLIT_KEYS_DEFAULT 8192
+void ox_session_set_split_keys(ox_session* s, int64_t keys);
+
 /* Router diagnostics of the last MoE step: ids[layer*top_k + j]. */
 const int64_t* ox_session_last_ids(const ox_session* s);
 
@@ -187,7 +195,7 @@ void ox_k_delta(const ox_model* m, const uint16_t* conv, const uint16_t* q, cons
 void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z, const float* w,
                      uint16_t* out);
 void ox_k_attention(const ox_model* m, int online, const uint16_t* q, const uint16_t* kv, int64_t keys,
-                    const uint16_t* qg, uint16_t* out);
+                    const uint16_t* qg, int64_t split_keys, uint16_t* out);
 
 #ifdef __cplusplus
 }

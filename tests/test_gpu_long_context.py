@@ -9,7 +9,12 @@ layout is src/spec.rs:321-362).
 
 These contexts reach code the short sessions never do: several score rounds
 per wave, hundreds of value chunks through the scan/products/chain
-pipeline, and last chunks of every length."""
+pipeline, and last chunks of every length. Above 8192 cached keys the
+decode attention runs split-K by default (four interleaved splits merged in
+a fixed tree, the same in both decode paths and the restatement); the
+exact single chain stays selectable and is checked too, and the split's
+results are held to the parity bar against it (logits within 2e-2, tokens
+equal except at near-ties below 1e-3, DeltaNet state within 1e-3)."""
 import numpy as np
 import pytest
 import torch
@@ -70,8 +75,10 @@ def seeded_state(cfg, capacity, start, seed, device):
     return out.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def decode_from(model, state, capacity, start, first, steps, persistent):
+def decode_from(model, state, capacity, start, first, steps, persistent, split=None):
     s = model.session(capacity)
+    if split is not None:
+        s.set_attention_split(split)
     s.set_persistent(persistent)
     assert s.persistent == persistent
     s.import_state(0, state)
@@ -96,20 +103,23 @@ def test_persistent_covers_every_capacity(models, name):
     assert m.session(MAX_CAPACITY).persistent, f"{name}: capacity {MAX_CAPACITY} should run persistent"
 
 
-@pytest.mark.parametrize("capacity,start", [(4104, 4096), (70001, 69990)])
-def test_long_context_mini_moe_against_oracle(models, oracle, capacity, start):
+@pytest.mark.parametrize("capacity,start,split", [(4104, 4096, None), (70001, 69990, None),
+                                                  (70001, 69990, 0), (9001, 8190, 1000)])
+def test_long_context_mini_moe_against_oracle(models, oracle, capacity, start, split):
     name, steps = "mini-moe", 6
     cfg = cc.preset(name)
-    say("long context", name, "capacity", capacity, "start", start)
+    say("long context", name, "capacity", capacity, "start", start, "split", split)
     state = seeded_state(cfg, capacity, start, seed=11, device="cpu")
     m = models(name)
     first = 17
-    sa, ca = decode_from(m, state, capacity, start, first, steps, True)
+    sa, ca = decode_from(m, state, capacity, start, first, steps, True, split)
     say("  persistent done")
-    sb, cb = decode_from(m, state, capacity, start, first, steps, False)
+    sb, cb = decode_from(m, state, capacity, start, first, steps, False, split)
     say("  per-kernel done")
     om = oracle.Model(cfg, oracle.synthetic_weights(cfg, 5))
     os_ = om.session(capacity)
+    if split is not None:
+        os_.set_split_keys(split)
     os_.import_cache(state)
     co, tok = [], first
     for i in range(steps):
@@ -138,3 +148,61 @@ def test_long_context_35b_persistent_matches_per_kernel(models, capacity, start)
     say("  per-kernel done")
     same_calls(name, ca, cb)
     assert np.array_equal(sa.export_state(0), sb.export_state(0)), f"{name}: state differs"
+
+
+def recurrent_states(cfg, state, capacity):
+    kvs, conv, lin, kv, total = state_layout(cfg, capacity)
+    tail = state[kv:].reshape(cfg["layers"], lin)
+    rows = [tail[l, conv:] for l in range(cfg["layers"]) if not cc.is_full(cfg, l)]
+    return (np.concatenate(rows).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.timeout(300)
+@pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per-kernel"])
+def test_split_attention_holds_the_parity_bar(persistent):
+    """Split-K (default above 8192 keys) against the exact single chain at
+    32768 cached positions on the 35B-A3B layer shape (the same persistent
+    kernel instantiation; the layer count is a runtime argument) cut to 4
+    layers, 64 greedy steps with the exact session's tokens fed to both:
+    logits within 2e-2 absolute, the same greedy token except where the
+    exact logits' top two are within 1e-3, and the DeltaNet state within 1e-3
+    relative at the end. The one full-attention layer is the last, so the
+    logits carry the split's own effect. Random-init layers amplify any
+    change of rounding order with depth: at 8 layers the same split moves a
+    logit by 0.125 (4 BF16 steps at that magnitude), and at 40 layers the
+    reference's own two exact orders (batched and per-token prompt) differ
+    by more than half the logit spread."""
+    cfg = dict(cc.preset("qwen36-35b-a3b"), layers=4)
+    steps, start = 64, 32768
+    capacity = start + steps + 8
+    state = seeded_state(cfg, capacity, start, seed=17, device="cuda")
+    torch.cuda.empty_cache()
+    m = cq35.Model.synthetic(cfg, seed=9)
+    exact, split = m.session(capacity), m.session(capacity)
+    exact.set_attention_split(0)
+    assert exact.attention_split == 0 and split.attention_split == cq35.SPLIT_KEYS_DEFAULT
+    for s in (exact, split):
+        s.set_persistent(persistent)
+        s.import_state(0, state)
+        s.position = start
+    tok, worst, ties, changed = 4321, 0.0, 0, 0
+    for i in range(steps):
+        le, te = exact.step_raw([tok])
+        ls, ts = split.step_raw([tok])
+        fe, fs = cq35.read_logits(le).astype(np.float64), cq35.read_logits(ls).astype(np.float64)
+        worst = max(worst, float(np.max(np.abs(fe - fs))))
+        changed += int(not np.array_equal(le, ls))
+        if ts != te:
+            top2 = np.sort(fe)[-2:]
+            assert top2[1] - top2[0] < 1e-3, f"step {i}: split token {ts} vs exact {te} away from a tie"
+            ties += 1
+        tok = te
+    say(f"  split vs exact: worst logit difference {worst:.3g}, steps with any logit changed {changed}, "
+        f"near-tie token changes {ties}")
+    assert changed > 0, "the split path should change some rounding at 32768 keys"
+    assert worst <= 2e-2, worst
+    re = recurrent_states(cfg, exact.export_state(0), capacity)
+    rs = recurrent_states(cfg, split.export_state(0), capacity)
+    rel = float(np.sqrt(np.mean((re - rs) ** 2)) / np.sqrt(np.mean(re ** 2)))
+    say(f"  DeltaNet state relative difference {rel:.3g}")
+    assert rel <= 1e-3, rel

@@ -293,8 +293,8 @@ def attention_f64(cfg, q, K, V, gate):
 
 
 @pytest.mark.parametrize("name", ["tiny-moe", "mini-moe", "tiny"])
-@pytest.mark.parametrize("keys", [1, 13, 4100])
-def test_attention_pinned(oracle, name, keys):
+@pytest.mark.parametrize("keys,split", [(1, 0), (13, 0), (4100, 0), (13, 8), (4100, 1000)])
+def test_attention_pinned(oracle, name, keys, split):
     """Online 8-key-tile softmax (MoE decode) and the dense staged attention,
     over `keys` cached rows like the long-context state (K rows of a unit
     head RMS, V ~ 0.1 N(0,1))."""
@@ -310,7 +310,7 @@ def test_attention_pinned(oracle, name, keys):
     online = 1 if cfg["moe"] else 0
 
     def measure():
-        oracle.lib().ox_k_attention(m._h, online, ptr(q), ptr(kv), keys, ptr(qg), ptr(out))
+        oracle.lib().ox_k_attention(m._h, online, ptr(q), ptr(kv), keys, ptr(qg), split, ptr(out))
         ref = attention_f64(cfg, f64(oracle, q), f64(oracle, K), f64(oracle, V), f64(oracle, qg[:, 1]))
         return rel_rms(f64(oracle, out), ref)
 
@@ -322,7 +322,7 @@ def test_attention_pinned(oracle, name, keys):
     # up to U |s|, |s| <~ 4 here, averaging out over the keys), p in BF16,
     # the context in BF16, the gated output: 4U (measured 0.5-1.2U)
     tol = 2 * U if online else 4 * U
-    check(oracle, measure, tol, plants, f"attention {name} keys={keys}")
+    check(oracle, measure, tol, plants, f"attention {name} keys={keys} split={split}")
 
 
 # ------------------------------------------------- whole decode steps
