@@ -15,6 +15,16 @@ __device__ __forceinline__ int64_t step_position(const uint64_t* params, int t) 
   return (int64_t)params[0] + t;
 }
 
+// Independent sessions stepped together (one token each, same model and
+// capacity): row y of a batched launch belongs to session y, whose state is
+// its own cache at the same offsets. Device memory, rewritten per step.
+constexpr int kMaxSessions = 64;
+struct SessionRows {
+  uint16_t* cache[kMaxSessions];
+  uint64_t position[kMaxSessions];
+  uint64_t token[kMaxSessions];
+};
+
 // Embedding row gather (embedding.hex:5-14) and the F32 RoPE table
 // [cos x R/2 | sin x R/2] for this position (rope.hex:5-17); block 0 also
 // clears the argmax key of the step.
@@ -59,10 +69,17 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
     const uint16_t* __restrict__ qkv, uint16_t* __restrict__ cache, int64_t conv_base,
     const uint64_t* __restrict__ params, int t, const float* __restrict__ conv_w, int qkv_size,
     int key_dim, int key_heads, uint16_t* __restrict__ conv_out, uint16_t* __restrict__ q_out,
-    uint16_t* __restrict__ k_out) {
+    uint16_t* __restrict__ k_out, const SessionRows* __restrict__ rows) {
   __shared__ float squares[256];
   __shared__ float total;
-  const int64_t position = step_position(params, t);
+  const int y = blockIdx.y;  // session row of a batched step (0 otherwise)
+  const int key_size = key_heads * key_dim;
+  qkv += (size_t)y * qkv_size;
+  conv_out += (size_t)y * qkv_size;
+  q_out += (size_t)y * key_size;
+  k_out += (size_t)y * key_size;
+  if (rows) cache = rows->cache[y];
+  const int64_t position = rows ? (int64_t)rows->position[y] : step_position(params, t);
   const int chunk = blockIdx.x, tid = threadIdx.x;
   const int ch = chunk * key_dim + tid;
   const bool active = tid < key_dim && ch < qkv_size;
@@ -111,7 +128,17 @@ __global__ __launch_bounds__(kBlock) void k_delta(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ alpha,
     const uint16_t* __restrict__ beta, const float* __restrict__ dt, const float* __restrict__ a,
     uint16_t* __restrict__ state16, float* __restrict__ state32, int value_size, int value_dim,
-    int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out) {
+    int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out,
+    const SessionRows* __restrict__ rows, int64_t state_off) {
+  const int y = blockIdx.y;  // session row of a batched step (0 otherwise)
+  const int value_heads = value_size / value_dim;
+  conv += (size_t)y * (2 * key_size + value_size);
+  q += (size_t)y * key_size;
+  k += (size_t)y * key_size;
+  alpha += (size_t)y * value_heads;
+  beta += (size_t)y * value_heads;
+  out += (size_t)y * value_size;
+  if (rows) state16 = rows->cache[y] + state_off;
   const int c = blockIdx.x * 8 + (threadIdx.x >> 5);
   const int lane = threadIdx.x & 31;
   const bool valid = c < value_size;
@@ -164,6 +191,10 @@ __global__ __launch_bounds__(kBlock) void k_gated_norm(const uint16_t* __restric
   __shared__ float squares[256];
   __shared__ float total;
   const int h = blockIdx.x, tid = threadIdx.x;
+  const size_t row = (size_t)blockIdx.y * gridDim.x * value_dim;  // session row of a batched step
+  core += row;
+  z += row;
+  out += row;
   const float v = tid < value_dim ? bf2f(core[h * value_dim + tid]) : 0.0f;
   if (tid < value_dim) squares[tid] = v * v;
   __syncthreads();
@@ -191,7 +222,8 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
     const uint16_t* __restrict__ value, const float* __restrict__ rope,
     const float* __restrict__ qw, const float* __restrict__ kw, uint16_t* __restrict__ cache,
     int64_t key_base, int64_t value_base, const uint64_t* __restrict__ params, int t, int kvs,
-    int q_heads, int head_dim, int pad, int rope_dim, float eps, uint16_t* __restrict__ qout) {
+    int q_heads, int head_dim, int pad, int rope_dim, float eps, uint16_t* __restrict__ qout,
+    const SessionRows* __restrict__ rows) {
   __shared__ float buf[256];
   __shared__ float normed[256];
   const int head = blockIdx.x, tid = threadIdx.x;
@@ -228,7 +260,8 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
   if (is_q) {
     qout[local * head_dim + tid] = rb;
   } else {
-    const int64_t pos = step_position(params, t);
+    const int64_t pos = rows ? (int64_t)rows->position[y] : step_position(params, t);
+    if (rows) cache = rows->cache[y];
     cache[key_base + pos * kvs + local * head_dim + tid] = rb;
     cache[value_base + pos * kvs + local * head_dim + tid] = value[local * head_dim + tid];
   }
@@ -252,7 +285,7 @@ constexpr int kStagedLdsKeys = 2048;
 __global__ __launch_bounds__(kBlock) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
     const uint64_t* __restrict__ params, int t, int kvs, int head_dim, int heads_per_kv, float scale,
-    float* __restrict__ scratch, int scratch_stride) {
+    float* __restrict__ scratch, int scratch_stride, const SessionRows* __restrict__ rows) {
   __shared__ float partial[kBlock];
   __shared__ float qf[256];
   __shared__ float s_lds[kStagedLdsKeys];
@@ -262,7 +295,8 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
   const size_t qs = (size_t)gridDim.x * head_dim;
   q += y * qs;
   scratch += (size_t)y * gridDim.x * scratch_stride;
-  const int64_t keys = step_position(params, t + y) + 1;
+  const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
+  if (rows) cache = rows->cache[y];
   const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
   const bool in_lds = keys <= kStagedLdsKeys;
   float* row = scratch + (size_t)head * scratch_stride;
@@ -318,7 +352,8 @@ constexpr int kContextChannels = 16;
 __global__ __launch_bounds__(128) void k_attention_context(
     const uint16_t* __restrict__ cache, int64_t value_base, const uint64_t* __restrict__ params,
     int t, int kvs, int head_dim, int heads, int heads_per_kv, const uint16_t* __restrict__ qg,
-    const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out) {
+    const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out,
+    const SessionRows* __restrict__ rows) {
   __shared__ float part[8][kContextChannels];
   const int chunks = head_dim / kContextChannels;
   const int head = blockIdx.x / chunks, c0 = (blockIdx.x - head * chunks) * kContextChannels;
@@ -327,7 +362,8 @@ __global__ __launch_bounds__(128) void k_attention_context(
   const size_t qs = (size_t)heads * head_dim;
   qg += y * 2 * qs;
   out += y * qs;
-  const int64_t keys = step_position(params, t + y) + 1;
+  const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
+  if (rows) cache = rows->cache[y];
   const uint16_t* pb = reinterpret_cast<const uint16_t*>(
       scratch + (size_t)y * heads * scratch_stride + (size_t)head * scratch_stride + 2 * keys);
   const uint16_t* vb = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c;

@@ -25,6 +25,7 @@
 #include "prefill.h"
 #include "mfma.h"
 #include "gguf.h"
+#include "batch.h"
 
 using namespace cq35;
 
@@ -339,6 +340,11 @@ extern "C" int cq35_weight_info(const cq35_config* cfg, int64_t index, cq35_tens
 
 // ------------------------------------------------------------------ model
 
+namespace {
+struct BatchWorkspace;
+void destroy_batch(BatchWorkspace* b);
+}  // namespace
+
 struct cq35_model {
   cq35_config cfg;
   Dims d;
@@ -347,6 +353,8 @@ struct cq35_model {
   std::vector<void*> owned;   // allocations to free
   float* freq = nullptr;      // F32 theta^(-2i/R) (src/catena.rs:185-232)
   int64_t weight_bytes = 0;
+  std::mutex batch_lock;      // one weight-shared batched step at a time
+  BatchWorkspace* batch = nullptr;  // its buffers (allocated on first use)
 };
 
 namespace {
@@ -368,6 +376,7 @@ float normal_scale(double sd) { return (float)(sd / std::sqrt(1431655765.0)); }
 extern "C" int cq35_model_free(cq35_model* m) {
   if (!m) return CQ35_OK;
   hipSetDevice(m->device);
+  destroy_batch(m->batch);
   for (void* p : m->owned) hipFree(p);
   if (m->freq) hipFree(m->freq);
   delete m;
@@ -1222,7 +1231,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
         (const uint16_t*)s->qg, (const uint16_t*)s->kraw, (const uint16_t*)s->vraw,
         (const float*)s->rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
         value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd,
-        (int)d.R, c.eps, s->qr);
+        (int)d.R, c.eps, s->qr, (const SessionRows*)nullptr);
       const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
       if (c.moe) {
         L(KC_ATTENTION, k_attn_scores,
@@ -1238,11 +1247,11 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       } else {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
-          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride);
+          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr);
         L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(128), 0,
           (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD,
           (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, (const float*)s->attn_scratch,
-          s->attn_stride, s->ctx);
+          s->attn_stride, s->ctx, (const SessionRows*)nullptr);
       }
       residual(L, s->ctx, W(4), d.H, d.QS, s->h, s->attn);
       post_norm = (const float*)W(7);
@@ -1253,7 +1262,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       L(KC_PREPARE_LINEAR, k_linear_prepare, dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim)),
         dim3(kBlock), 0, (const uint16_t*)s->qkv, s->cache, conv_base, (const uint64_t*)s->d_params,
-        t, (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, s->conv, s->qn, s->kn);
+        t, (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, s->conv, s->qn, s->kn, (const SessionRows*)nullptr);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
       const dim3 dgrid((unsigned)((d.VS + 7) / 8));
       if (f32_state)
@@ -1261,13 +1270,13 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
           (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr,
           s->shadow + l * d.REC, (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale,
-          s->core);
+          s->core, (const SessionRows*)nullptr, (int64_t)0);
       else
         L(KC_DELTA, k_delta<false>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
           (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
           (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6),
           s->cache + conv_base + d.CONV, (float*)nullptr, (int)d.VS, c.value_dim, c.key_dim,
-          c.key_heads, (int)d.KS, scale, s->core);
+          c.key_heads, (int)d.KS, scale, s->core, (const SessionRows*)nullptr, (int64_t)0);
       L(KC_GATED_NORM, k_gated_norm, dim3((unsigned)c.value_heads), dim3(kBlock), 0,
         (const uint16_t*)s->core, (const uint16_t*)s->z, (const float*)W(7), c.value_dim, c.eps,
         s->gated);
@@ -1435,17 +1444,17 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         L(KC_PREPARE_FULL, k_full_prepare, dim3((unsigned)(d.Q + d.KVH), rows_n), dim3(kBlock), 0,
           (const uint16_t*)qg, (const uint16_t*)kraw, (const uint16_t*)vraw,
           (const float*)s->pf_rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
-          value_base, params, first, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, qr);
+          value_base, params, first, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, qr, (const SessionRows*)nullptr);
         const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
         for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
           const int am = std::min(s->pf_attn_tokens, rows_n - a0);
           L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kBlock), 0,
             (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
-            first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride);
+            first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
           L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
             dim3(128), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
             (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
-            (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS);
+            (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS, (const SessionRows*)nullptr);
         }
         residual_rows(ctx, (int)d.QS, W(4), s->pf_h, s->pf_attn);
         post_norm = W(7);
@@ -1828,6 +1837,265 @@ extern "C" int cq35_step(cq35_session* s, const uint64_t* tokens, int64_t n, int
   return rc ? rc : step_complete(s, next_token);
 }
 
+namespace {
+
+// ------------------------------------------------ weight-shared batched step
+
+// Buffers of the batched decode step for sessions of one capacity: every
+// activation row for up to `max_b` sessions, the session table and the
+// argmax keys, and a captured graph per batch size (the table is rewritten
+// before each replay, so a graph serves any sessions of that count).
+struct BatchWorkspace {
+  int64_t capacity = 0;
+  int max_b = 0;
+  hipStream_t stream = nullptr;
+  SessionRows* d_rows = nullptr;
+  SessionRows* h_rows = nullptr;  // pinned
+  unsigned long long* d_best = nullptr;
+  unsigned long long* h_best = nullptr;  // pinned
+  uint16_t *h = nullptr, *x = nullptr, *attn = nullptr, *qkv = nullptr, *conv = nullptr, *z = nullptr;
+  uint16_t *ab = nullptr, *qn = nullptr, *kn = nullptr, *core = nullptr, *gated = nullptr;
+  uint16_t *qg = nullptr, *kraw = nullptr, *vraw = nullptr, *qr = nullptr, *ctx = nullptr, *act = nullptr;
+  uint16_t* logits = nullptr;
+  float *rope = nullptr, *scratch = nullptr;
+  int stride = 0;
+  hipGraph_t graph[kMaxSessions + 1] = {};
+  hipGraphExec_t exec[kMaxSessions + 1] = {};
+  std::vector<void*> allocs;
+};
+
+void destroy_batch(BatchWorkspace* b) {
+  if (!b) return;
+  if (b->stream) hipStreamSynchronize(b->stream);
+  for (int i = 0; i <= kMaxSessions; ++i) {
+    if (b->exec[i]) hipGraphExecDestroy(b->exec[i]);
+    if (b->graph[i]) hipGraphDestroy(b->graph[i]);
+  }
+  for (void* p : b->allocs) hipFree(p);
+  if (b->h_rows) hipHostFree(b->h_rows);
+  if (b->h_best) hipHostFree(b->h_best);
+  if (b->stream) hipStreamDestroy(b->stream);
+  delete b;
+}
+
+int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace** out) {
+  BatchWorkspace* b = m->batch;
+  if (b && b->capacity == capacity && b->max_b >= count) {
+    *out = b;
+    return CQ35_OK;
+  }
+  destroy_batch(b);
+  m->batch = nullptr;
+  b = new (std::nothrow) BatchWorkspace();
+  if (!b) return fail(CQ35_EINVAL, "out of host memory");
+  const Dims& d = m->d;
+  const cq35_config& c = m->cfg;
+  const int B = count <= 16 ? 16 : kMaxSessions;
+  b->capacity = capacity;
+  b->max_b = B;
+  hipError_t e = hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking);
+  auto alloc = [&](auto** p, int64_t n) {
+    if (e != hipSuccess) return;
+    void* q = nullptr;
+    e = hipMalloc(&q, std::max<int64_t>(n, 1) * (int64_t)sizeof(**p));
+    if (e == hipSuccess) {
+      b->allocs.push_back(q);
+      *p = static_cast<std::remove_reference_t<decltype(*p)>>(q);
+    }
+  };
+  alloc(&b->d_rows, 1);
+  alloc(&b->d_best, B);
+  const int64_t wide = std::max({d.QKV, 2 * d.QS, d.VS, d.I, d.H});
+  for (uint16_t** p : {&b->h, &b->x, &b->attn}) alloc(p, B * d.H);
+  alloc(&b->qkv, B * d.QKV);
+  alloc(&b->conv, B * d.QKV);
+  alloc(&b->z, B * d.VS);
+  alloc(&b->ab, 2 * B * (int64_t)c.value_heads);
+  alloc(&b->qn, B * d.KS);
+  alloc(&b->kn, B * d.KS);
+  alloc(&b->core, B * d.VS);
+  alloc(&b->gated, B * d.VS);
+  alloc(&b->qg, B * 2 * d.QS);
+  alloc(&b->kraw, B * d.KVS);
+  alloc(&b->vraw, B * d.KVS);
+  alloc(&b->qr, B * d.QS);
+  alloc(&b->ctx, B * d.QS);
+  alloc(&b->act, B * std::max<int64_t>(d.I, 1));
+  alloc(&b->logits, B * d.V);
+  alloc(&b->rope, B * std::max<int64_t>(d.R, 2));
+  const int64_t tiles = (capacity + 7) / 8;
+  b->stride = (int)std::max<int64_t>(tiles * 8 + 2 * tiles + 16, 3 * capacity + 16);
+  alloc(&b->scratch, B * d.Q * (int64_t)b->stride);
+  (void)wide;
+  if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_rows, sizeof(SessionRows), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_best, B * sizeof(unsigned long long), hipHostMallocDefault);
+  if (e != hipSuccess) {
+    destroy_batch(b);
+    return fail(CQ35_EDEVICE, "batch workspace: %s", hipGetErrorString(e));
+  }
+  m->batch = b;
+  *out = b;
+  return CQ35_OK;
+}
+
+// Weight-shared GEMV launches (k_ws32 / k_ws64 / k_ws256_swiglu) over B tokens.
+void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t cols, unsigned long long* best) {
+  const int groups = (B + kBatchNB - 1) / kBatchNB;
+  const int row_blocks = (int)((seg_rows(seg) + 31) / 32);
+  const size_t lds = (size_t)kBatchNB * std::min<int64_t>(cols, kBatchChunk) * 4;
+  const dim3 grid((unsigned)batch_grid(row_blocks, groups)), block(kBlock);
+  if (best) k_ws32<true, 8><<<grid, block, lds, st>>>(x, B, groups, seg, (int)cols, best);
+  else k_ws32<false, 8><<<grid, block, lds, st>>>(x, B, groups, seg, (int)cols, best);
+}
+void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows, int64_t cols, const uint16_t* res,
+          uint16_t* out) {
+  const int groups = (B + kBatchNB - 1) / kBatchNB;
+  const int row_blocks = (int)((rows + 15) / 16);
+  const size_t lds = (size_t)kBatchNB * std::min<int64_t>(cols, kBatchChunk) * 4;
+  k_ws64<8><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), lds, st>>>(
+      x, B, groups, static_cast<const uint16_t*>(w), (int)rows, (int)cols, res, out);
+}
+
+// The batched decode step's launch sequence (dense models): every layer of
+// enqueue_token for B sessions, GEMVs weight-shared, per-session kernels with
+// one grid row per session.
+void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
+  const cq35_config& c = m->cfg;
+  const Dims& d = m->d;
+  hipStream_t st = b->stream;
+  auto Wt = [&](int64_t index) { return m->w[index]; };
+  const int64_t cap = b->capacity;
+  const SessionRows* rows = b->d_rows;
+  k_sembed<<<dim3((unsigned)grid_for((d.H + kBlock - 1) / kBlock, 64), (unsigned)B), dim3(kBlock), 0, st>>>(
+      rows, (const uint16_t*)Wt(0), (int)d.H, b->h, (const float*)m->freq, (int)(d.R / 2), b->rope, b->d_best);
+  auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
+    k_bnorm<<<dim3((unsigned)B), dim3(kBlock), (size_t)d.H * 2, st>>>(x, (const float*)w, (int)d.H, c.eps, out);
+  };
+  int64_t base = 1;
+  for (int64_t l = 0; l < d.L; ++l) {
+    auto W = [&](int slot) { return Wt(base + slot); };
+    const int64_t key_base = l * 2 * cap * d.KVS;
+    const int64_t value_base = key_base + cap * d.KVS;
+    norm(b->h, W(0), b->x);
+    int ffn;
+    const void* post_norm;
+    if (is_full(c, l)) {
+      ws32(st, b->x, B, segments({{W(1), {b->qg, 2 * d.QS}}, {W(2), {b->kraw, d.KVS}}, {W(3), {b->vraw, d.KVS}}}),
+           d.H, nullptr);
+      k_full_prepare<<<dim3((unsigned)(d.Q + d.KVH), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->qg, (const uint16_t*)b->kraw, (const uint16_t*)b->vraw, (const float*)b->rope,
+          (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
+          (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, b->qr, rows);
+      const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
+      k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
+          (int)d.HD, (int)(d.Q / d.KVH), scale, b->scratch, b->stride, rows);
+      k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(128), 0, st>>>(
+          (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
+          (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
+      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn);
+      post_norm = W(7);
+      ffn = 8;
+    } else {
+      uint16_t* alpha = b->ab;
+      uint16_t* beta = b->ab + (size_t)B * c.value_heads;
+      ws32(st, b->x, B,
+           segments({{W(1), {b->qkv, d.QKV}}, {W(2), {b->z, d.VS}}, {W(3), {alpha, c.value_heads}},
+                     {W(4), {beta, c.value_heads}}}),
+           d.H, nullptr);
+      const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
+      k_linear_prepare<<<dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->qkv, (uint16_t*)nullptr, conv_base, (const uint64_t*)nullptr, 0, (const float*)W(9),
+          (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows);
+      const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
+      k_delta<false><<<dim3((unsigned)((d.VS + 7) / 8), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const uint16_t*)alpha,
+          (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, (float*)nullptr,
+          (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
+      k_gated_norm<<<dim3((unsigned)c.value_heads, (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->core, (const uint16_t*)b->z, (const float*)W(7), c.value_dim, c.eps, b->gated);
+      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn);
+      post_norm = W(10);
+      ffn = 11;
+    }
+    norm(b->attn, post_norm, b->x);
+    {
+      const int groups = (B + kBatchNBDual - 1) / kBatchNBDual;
+      const int row_blocks = (int)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate));
+      k_ws256_swiglu<<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock),
+                       (size_t)kBatchNBDual * d.H * 4, st>>>(b->x, B, groups, (const uint16_t*)W(ffn),
+                                                             (const uint16_t*)W(ffn + 1), (int)d.I, (int)d.H,
+                                                             b->act);
+    }
+    ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h);
+    base += layer_tensors(c, l);
+  }
+  const int64_t total = weight_count(c);
+  norm(b->h, Wt(total - 2), b->x);
+  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best);
+}
+
+// One weight-shared decode step for `count` dense sessions of one model and
+// capacity (checked by the caller): tokens[i] at starts[i] of sessions[i].
+int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts, int count,
+                      uint64_t* next_tokens) {
+  cq35_model* m = sessions[0]->model;
+  std::lock_guard<std::mutex> hold(m->batch_lock);
+  HIP_TRY(hipSetDevice(m->device));
+  BatchWorkspace* b = nullptr;
+  int rc = batch_workspace(m, sessions[0]->capacity, count, &b);
+  if (rc) return rc;
+  for (int i = 0; i < count; ++i) {
+    b->h_rows->cache[i] = sessions[i]->cache;
+    b->h_rows->position[i] = (uint64_t)starts[i];
+    b->h_rows->token[i] = tokens[i];
+    sessions[i]->poisoned = true;  // cleared on success
+  }
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < count && e == hipSuccess; ++i) e = hipStreamSynchronize(sessions[i]->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(b->d_rows, b->h_rows, sizeof(SessionRows), hipMemcpyHostToDevice, b->stream);
+  if (e == hipSuccess && !b->exec[count]) {
+    e = hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+      enqueue_batch(m, b, count);
+      hipGraph_t g = nullptr;
+      e = hipStreamEndCapture(b->stream, &g);
+      if (e == hipSuccess) e = hipGraphInstantiate(&b->exec[count], g, nullptr, nullptr, 0);
+      b->graph[count] = g;
+    }
+  }
+  if (e == hipSuccess) e = hipGraphLaunch(b->exec[count], b->stream);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(b->h_best, b->d_best, count * sizeof(unsigned long long), hipMemcpyDeviceToHost, b->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "batched step: %s", hipGetErrorString(e));
+  for (int i = 0; i < count; ++i) {
+    const uint64_t t = decode_key(b->h_best[i]);
+    if (t >= (uint64_t)m->cfg.vocab)
+      return fail(CQ35_EDEVICE, "qwen3 returned next-token ID %llu outside the vocabulary", (unsigned long long)t);
+    next_tokens[i] = t;
+  }
+  for (int i = 0; i < count; ++i) sessions[i]->poisoned = false;
+  return CQ35_OK;
+}
+
+// Whether a batch can take the weight-shared step: dense sessions of one
+// model and capacity, none of them timing kernels.
+bool shared_batch_ok(cq35_session* const* sessions, int64_t count) {
+  if (count < 2 || count > kMaxSessions) return false;
+  if (const char* g = getenv("CQ35_BATCH_SHARED"))
+    if (atoi(g) == 0) return false;
+  const cq35_model* m = sessions[0]->model;
+  if (m->cfg.moe || m->cfg.hidden > kBatchChunk) return false;  // the SwiGLU stages one row chunk
+  for (int64_t i = 0; i < count; ++i)
+    if (sessions[i]->model != m || sessions[i]->capacity != sessions[0]->capacity || sessions[i]->timed_class >= 0)
+      return false;
+  return true;
+}
+
+}  // namespace
+
 extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens,
                                const int64_t* starts, int64_t count, uint64_t* next_tokens) {
   if (!sessions || !tokens || !starts || !next_tokens || count <= 0) return fail(CQ35_EINVAL, "null argument");
@@ -1844,6 +2112,12 @@ extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* to
     if (tokens[i] >= (uint64_t)s->model->cfg.vocab)
       return fail(CQ35_ERANGE, "session %lld: token ID outside the %d-token vocabulary", (long long)i,
                   s->model->cfg.vocab);
+  }
+  if (shared_batch_ok(sessions, count)) {
+    const int rc = step_batch_shared(sessions, tokens, starts, (int)count, next_tokens);
+    if (rc)
+      for (int64_t i = 0; i < count; ++i) sessions[i]->poisoned = true;
+    return rc;
   }
   // per-kernel sessions: launch all, then complete all (they overlap on the
   // device); persistent sessions step one at a time (each needs every CU)
