@@ -302,8 +302,10 @@ class Session:
     MATRIX_EXPERTS = 2
 
     def set_attention_split(self, keys: int) -> None:
-        """Decode attention over more than `keys` cached keys as four merged
-        splits (0: the reference's single chain at every length)."""
+        """Decode attention over more than `keys` cached keys as at most 128
+        ranges of equal tile counts, each an online recurrence of its own,
+        merged in ascending order (0: the reference's single chain at every
+        length)."""
         check(_lib.load().cq35_session_set_attention_split(self._h, keys))
 
     @property

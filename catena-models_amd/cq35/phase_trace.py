@@ -15,8 +15,9 @@ the layers of that kind,
     that previous completion (exchange latency plus any wait behind the
     phase's own loads);
   - the HBM floor of the phase's algorithmic bytes at 8 TB/s;
-and for full layers the values phase's busy time per role. Stamps are
-s_memrealtime (100 MHz, 10 ns).
+and for full layers the values phase's busy time per role, or, when the
+step ran split-K attention (more keys than the session's split threshold),
+the flash phase's time per stage. Stamps are s_memrealtime (100 MHz, 10 ns).
 """
 from __future__ import annotations
 
@@ -64,7 +65,7 @@ def floor_us(pb: dict, kind: str, name: str) -> float:
     return b / (HBM_GBS * 1e3)
 
 
-def analyse(trace: np.ndarray, cfg: dict, keys: int) -> str:
+def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str:
     L = cfg["layers"]
     start = trace[:, TRACE_START][trace[:, TRACE_START] > 0].min()
     pb = phase_bytes(cfg, keys)
@@ -91,7 +92,12 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int) -> str:
             prev_done = done
         per_layer.append((l, kind, (prev_done - layer_start) * TICK_US))
         if kind == "full":
-            busy = trace[:, tb + 14:tb + 18].astype(np.float64).mean(axis=0) * TICK_US
+            if flash:
+                busy = trace[:, tb + 14:tb + 19].astype(np.float64)
+                busy = np.concatenate([busy[:, :4].mean(axis=0) * TICK_US, busy[:, :4].max(axis=0) * TICK_US,
+                                       [busy[:, 4].sum()]])
+            else:
+                busy = trace[:, tb + 14:tb + 18].astype(np.float64).mean(axis=0) * TICK_US
             roles.append(busy)
     head = (trace[:, TRACE_HEAD].max() - prev_done) * TICK_US
     total = (trace[:, TRACE_HEAD].max() - start) * TICK_US
@@ -111,7 +117,12 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int) -> str:
             tot += c / cnt
             out.append(f"| {name} | {c / cnt:.2f} | {i / cnt:.2f} | {floor_us(pb, kind, name):.2f} |")
         out.append(f"| **layer** | **{tot:.2f}** | | |")
-    if roles:
+    if roles and flash:
+        b = np.mean(roles, axis=0)
+        out.append("\n**flash phase, time per stage** (per full layer, us; mean over blocks / slowest block; "
+                   f"{b[8]:.0f} items): prepare {b[0]:.2f} / {b[4]:.2f}, scores {b[1]:.2f} / {b[5]:.2f}, "
+                   f"scan {b[2]:.2f} / {b[6]:.2f}, values and partials {b[3]:.2f} / {b[7]:.2f}\n")
+    elif roles:
         b = np.mean(roles, axis=0)
         out.append("\n**values phase, busy time per role** (mean per block and full layer, us): "
                    f"scan {b[0]:.2f}, products (4 waves, summed) {b[1]:.2f}, channel chains {b[2]:.2f}, "
@@ -178,9 +189,11 @@ def main() -> int:
                                             ctypes.byref(ctypes.c_int64())))
     trace = buf.reshape(blocks, n).astype(np.int64)
     keys = (args.long or args.context) + args.steps
+    split = s.attention_split
+    flash = split > 0 and keys > split
     print(f"{args.config}, {blocks} blocks, {'long ' + str(args.long) if args.long else 'context ' + str(args.context)}"
           f" + {args.steps} steps (last step traced, about {keys} keys)")
-    print(analyse(trace, cfg, keys))
+    print(analyse(trace, cfg, keys, flash))
     return 0
 
 

@@ -58,18 +58,21 @@ __global__ __launch_bounds__(kScoreBlock) void k_attn_scores(
 // One wave per (query head, 16-channel chunk). Keys are processed in chunks
 // of up to kValueChunk: the wave stages the chunk's V slice into LDS with
 // 16-byte loads (all in flight at once) and computes the chunk's weights,
-// then the lanes run the channel and denominator chains from LDS.
+// then lanes 0-15 run the channel chains from LDS (the other lanes repeat
+// them) and every lane the denominator chain.
 //
-// Split-K above split_keys keys (0: never): tile t belongs to split t mod 4;
-// each split runs the online recurrence over its own tiles (its own running
-// maximum, alpha, denominator and accumulators) on lanes 16s..16s+15, and the
-// splits merge at the end in a fixed tree:
-// M = max m_s, w_s = exp(m_s - M), den = (d_0 w_0 + d_1 w_1) + (d_2 w_2 + d_3 w_3),
-// acc likewise. At or below the threshold one split runs the reference's
-// single chain (the other lanes repeat it), bit for bit.
+// Split-K above split_keys keys (0: never): the T tiles form at most
+// kSplitRanges ranges of ceil(T / kSplitRanges) tiles (the ranges depend on
+// the key count only) and each range runs the online recurrence from
+// scratch over its own tiles (running maximum reset at the range start, so
+// its first alpha is 0); at each range's end its accumulators join the
+// totals in ascending range order weighted by w_r = exp(m_r - M), M the
+// maximum over all scores: den = 0 + den_0 w_0 + den_1 w_1 + ..., each
+// channel likewise. At or below the threshold one chain runs over all tiles,
+// the reference's, bit for bit.
 constexpr int kValueChannels = 16;
 constexpr int kValueChunk = 1024;
-constexpr int kValueSplits = 4;
+constexpr int kSplitRanges = 128;
 
 __global__ __launch_bounds__(64) void k_attn_values(
     const float* __restrict__ scores, int stride, const uint16_t* __restrict__ cache,
@@ -79,7 +82,8 @@ __global__ __launch_bounds__(64) void k_attn_values(
   const int head = blockIdx.x, chunk = blockIdx.y, lane = threadIdx.x;
   const int64_t keys = (int64_t)params[0] + t + 1;
   const int tiles = (int)((keys + 7) >> 3);
-  const int ns = (split_keys > 0 && keys > split_keys) ? kValueSplits : 1;
+  const bool split = split_keys > 0 && keys > split_keys;
+  const int range_tiles = split ? (tiles + kSplitRanges - 1) / kSplitRanges : tiles;
   float* mx = lds;                                   // running maximum per tile (all tiles)
   float* p = mx + ((tiles + 3) & ~3);                // weights of the current key chunk
   float* alpha = p + kValueChunk;                    // exp(m_prev - m_t) of the chunk
@@ -96,19 +100,21 @@ __global__ __launch_bounds__(64) void k_attn_values(
     mx[i] = m;
   }
   __syncthreads();
-  float msplit[kValueSplits] = {ninf, ninf, ninf, ninf};  // each split's final maximum (lane 0)
+  float top = ninf;  // the maximum of all scores (lane 0)
   if (lane == 0) {
+    float m = ninf;
     for (int i = 0; i < tiles; ++i) {
-      const int sp = i & (ns - 1);
-      msplit[sp] = fmaxf(msplit[sp], mx[i]);
-      mx[i] = msplit[sp];
+      if (split && i % range_tiles == 0) m = ninf;
+      m = fmaxf(m, mx[i]);
+      mx[i] = m;
+      top = fmaxf(top, m);
     }
   }
   __syncthreads();
+  top = __shfl(top, 0, 64);
   const int c0 = chunk * kValueChannels;
-  const int sp = (lane >> 4) & (ns - 1);  // this lane's split; lane & 15 its channel
   const uint16_t* vbase = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c0;
-  float acc = 0.0f, den = 0.0f;
+  float acc = 0.0f, den = 0.0f, acc_all = 0.0f, den_all = 0.0f;
   for (int64_t k0 = 0; k0 < (int64_t)tiles * 8; k0 += kValueChunk) {
     const int n = (int)min<int64_t>(kValueChunk, (int64_t)tiles * 8 - k0);  // multiple of 8
     // stage V rows k0..k0+n (16 channels = 2 quads per key; invalid keys read key 0)
@@ -124,13 +130,12 @@ __global__ __launch_bounds__(64) void k_attn_values(
     }
     for (int i = lane; i < n / 8; i += 64) {
       const int tile = (int)(k0 / 8) + i;
-      alpha[i] = hexp((tile >= ns ? mx[tile - ns] : ninf) - mx[tile]);
+      const bool first = tile == 0 || (split && tile % range_tiles == 0);
+      alpha[i] = hexp((first ? ninf : mx[tile - 1]) - mx[tile]);
     }
     __syncthreads();
-    // chunk tiles i with i mod ns == sp (k0 / 8 is a multiple of 4): the
-    // channel chain and the split's denominator chain
     const uint16_t* vh = reinterpret_cast<const uint16_t*>(vs) + (lane & 15);
-    for (int i = sp; i < n / 8; i += ns) {
+    for (int i = 0; i < n / 8; ++i) {
       acc = acc * alpha[i];
       den = den * alpha[i];
 #pragma unroll
@@ -138,22 +143,20 @@ __global__ __launch_bounds__(64) void k_attn_values(
         acc = acc + p[i * 8 + j] * bf2f(vh[(i * 8 + j) * kValueChannels]);
         den = den + p[i * 8 + j];
       }
+      const int tile = (int)(k0 / 8) + i;
+      if (split && (tile % range_tiles == range_tiles - 1 || tile == tiles - 1)) {
+        const float w = hexp(mx[tile] - top);  // the range's running maximum at its last tile
+        acc_all = acc_all + acc * w;
+        den_all = den_all + den * w;
+        acc = 0.0f;  // the next range starts from zero
+        den = 0.0f;
+      }
     }
     __syncthreads();
   }
-  if (ns > 1) {
-#pragma unroll
-    for (int q = 0; q < kValueSplits; ++q) msplit[q] = __shfl(msplit[q], 0, 64);
-    const float M = fmaxf(fmaxf(msplit[0], msplit[1]), fmaxf(msplit[2], msplit[3]));
-    float w[kValueSplits], a[kValueSplits], d[kValueSplits];
-#pragma unroll
-    for (int q = 0; q < kValueSplits; ++q) {
-      w[q] = hexp(msplit[q] - M);
-      a[q] = __shfl(acc, 16 * q + (lane & 15), 64);
-      d[q] = __shfl(den, 16 * q, 64);
-    }
-    acc = (a[0] * w[0] + a[1] * w[1]) + (a[2] * w[2] + a[3] * w[3]);
-    den = (d[0] * w[0] + d[1] * w[1]) + (d[2] * w[2] + d[3] * w[3]);
+  if (split) {
+    acc = acc_all;
+    den = den_all;
   }
   const int c = c0 + lane;
   if (lane < kValueChannels && c < head_dim) {

@@ -107,7 +107,6 @@ __global__ __launch_bounds__(kBlock) void k_ws32(const uint16_t* __restrict__ x,
   batch_block(blockIdx.x, groups, &rb, &tg);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane & 7, g = lane >> 3;
-  const int quads = cols >> 3;
   const int total = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
   const int row = (rb * 4 + wave) * 8 + g;
   const int t0 = tg * NB;

@@ -1201,6 +1201,74 @@ struct ScoreLds {
 static_assert(sizeof(ScoreLds) <= kLdsBigBytes, "score LDS");
 static_assert(offsetof(ScoreLds, qhat) % 16 == 0, "16-byte reads of the query heads");
 
+// Head RMS norm with the adjacent-pair tree and neox RoPE on the first R
+// channels (full_prepare.hex:3-82) of the heads listed in s->heads, one wave
+// per head: a head index hh < Q is query head hh, Q + g key head g. src(hh)
+// is the head's raw BF16 row; query heads land as F32 of their BF16 results
+// in s->qhat, lane-major (channel l32 + 32 j of slot qslot(hh) at
+// (qslot * HD) + l32 * KJ + j), key heads as BF16 in s->khat[g * HD + c].
+// Needs s->rope filled and a barrier before.
+template <class S, class L, class Src, class QSlot>
+__device__ __forceinline__ void prepare_heads(const Mega& m, L* s, int nheads, const float (&qw_)[S::HD / 64],
+                                              const float (&kw_)[S::HD / 64], Src src, QSlot qslot) {
+  constexpr int HD = S::HD, Q = S::Q, KVH = S::KVH, KJ = HD / 32, RH = S::R / 2, VPL = HD / 64;
+  const CQ35_CONST MegaArgs& a = m.a;
+#pragma unroll 1
+  for (int h0 = 0; h0 < nheads; h0 += kMW) {
+    const bool live = h0 + m.wave < nheads;
+    const int hh = live ? s->heads[h0 + m.wave] : Q + KVH;
+    const bool is_q = hh < Q;
+    float x[VPL], w[VPL];
+    float t = 0.0f;
+    if (hh < Q + KVH) {
+      const uint16_t* row = src(hh);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        x[i] = bf2f(row[VPL * m.lane + i]);
+        w[i] = is_q ? qw_[i] : kw_[i];
+      }
+      // adjacent-pair tree: in-lane pairs first, then the lanes
+      if constexpr (VPL == 1) t = x[0] * x[0];
+      else if constexpr (VPL == 2) t = x[0] * x[0] + x[1] * x[1];
+      else t = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
+    }
+    t = t + lane_down<1>(t);
+    t = t + lane_down<2>(t);
+    t = t + lane_down<4>(t);
+    t = t + lane_down<8>(t);
+    t = t + lane_down<16>(t);
+    t = t + lane_down<32>(t);
+    const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
+    if (hh < Q + KVH) {
+      const float inverse = 1.0f / nsqrt(sum / (float)HD + a.eps);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+        s->normed[m.wave][VPL * m.lane + i] = bf2f(bf_mul(f2bf(x[i] * inverse), f2bf(w[i])));
+    }
+    __syncthreads();
+    if (hh < Q + KVH) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int c = m.lane + 64 * i;
+        const float nf = s->normed[m.wave][c];
+        float result = nf;
+        if (c < S::R) {
+          const int pair = c % RH;
+          const bool first = c < RH;
+          const float partner = s->normed[m.wave][first ? pair + RH : pair];
+          const float ac = nf * s->rope[pair];
+          const float bs = partner * s->rope[pair + RH];
+          result = first ? ac - bs : ac + bs;
+        }
+        const uint16_t rb = f2bf(result);
+        if (is_q) s->qhat[qslot(hh) * HD + (c & 31) * KJ + (c >> 5)] = bf2f(rb);
+        else s->khat[(hh - Q) * HD + c] = rb;
+      }
+    }
+    __syncthreads();
+  }
+}
+
 template <class S>
 __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
@@ -1304,62 +1372,9 @@ __device__ __forceinline__ void phase_scores(const MegaArgs* pa, uint32_t tag, c
   }
   __syncthreads();
   // one wave per head of the list
-  const int nheads = s->nheads;
-#pragma unroll 1
-  for (int h0 = 0; h0 < nheads; h0 += kMW) {
-    const bool live = h0 + m.wave < nheads;
-    const int hh = live ? s->heads[h0 + m.wave] : Q + KVH;
-    const bool is_q = hh < Q;
-    float x[VPL], w[VPL];
-    float t = 0.0f;
-    if (hh < Q + KVH) {
-      const uint16_t* src = is_q ? in16 + hh * HD : kraw + (hh - Q) * HD;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        x[i] = bf2f(src[VPL * m.lane + i]);
-        w[i] = is_q ? qw_[i] : kw_[i];
-      }
-      // adjacent-pair tree: in-lane pairs first, then the lanes
-      if constexpr (VPL == 1) t = x[0] * x[0];
-      else if constexpr (VPL == 2) t = x[0] * x[0] + x[1] * x[1];
-      else t = (x[0] * x[0] + x[1] * x[1]) + (x[2] * x[2] + x[3] * x[3]);
-    }
-    t = t + lane_down<1>(t);
-    t = t + lane_down<2>(t);
-    t = t + lane_down<4>(t);
-    t = t + lane_down<8>(t);
-    t = t + lane_down<16>(t);
-    t = t + lane_down<32>(t);
-    const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
-    if (hh < Q + KVH) {
-      const float inverse = 1.0f / nsqrt(sum / (float)HD + a.eps);
-#pragma unroll
-      for (int i = 0; i < VPL; ++i)
-        s->normed[m.wave][VPL * m.lane + i] = bf2f(bf_mul(f2bf(x[i] * inverse), f2bf(w[i])));
-    }
-    __syncthreads();
-    if (hh < Q + KVH) {
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int c = m.lane + 64 * i;
-        const float nf = s->normed[m.wave][c];
-        float result = nf;
-        if (c < S::R) {
-          const int pair = c % RH;
-          const bool first = c < RH;
-          const float partner = s->normed[m.wave][first ? pair + RH : pair];
-          const float ac = nf * s->rope[pair];
-          const float bs = partner * s->rope[pair + RH];
-          result = first ? ac - bs : ac + bs;
-        }
-        const uint16_t rb = f2bf(result);
-        // query heads lane-major: lane l32's channels l32 + 32 j contiguous
-        if (is_q) s->qhat[hh * HD + (c & 31) * KJ + (c >> 5)] = bf2f(rb);
-        else s->khat[(hh - Q) * HD + c] = rb;
-      }
-    }
-    __syncthreads();
-  }
+  prepare_heads<S>(m, s, s->nheads, qw_, kw_, [&](int hh) {
+    return hh < Q ? in16 + hh * HD : kraw + (hh - Q) * HD;
+  }, [&](int hh) { return hh; });
   auto score_batch = [&](const uint32_t (&kv)[SB][KJ], int b) {
 #pragma unroll
     for (int rr = 0; rr < SB; ++rr) {
@@ -1457,8 +1472,7 @@ struct ValueLds {
   float mx[3][kValueTiles];
   int one[3];
   uint32_t vnew[kValueChannels / 2];
-  float den[4];     // each split's denominator
-  float msplit[4];  // each split's final running maximum
+  float den[4];
 };
 static_assert(sizeof(ValueLds) <= kLdsBigBytes, "value LDS");
 static_assert(kProdStride % 4 == 0 && offsetof(ValueLds, p) % 16 == 0 && offsetof(ValueLds, sc) % 16 == 0 &&
@@ -1556,9 +1570,9 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
   const int nch = (int)((padded + kMegaValueChunk - 1) / kMegaValueChunk);
   ValueLds* s = reinterpret_cast<ValueLds*>(m.big);
   const float ninf = bitsf(0xff800000u);
-  // split-K over long contexts: tile t in split t mod ns (see attention.h)
-  const int ns = (a.split_keys > 0 && keys > a.split_keys) ? 4 : 1;
-  const int sp = (m.lane >> 4) & (ns - 1);  // chain waves: this lane's split
+  // one chain over every tile (split-K contexts take phase_flash instead)
+  constexpr int ns = 1;
+  constexpr int sp = 0;
   const int pj = m.tid - 4 * 64;  // producer thread (waves 4-7)
   const int ph = pj & 1;          // channels 8 ph .. 8 ph + 7
 #pragma unroll 1
@@ -1674,9 +1688,7 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
           }
           const uint64_t scaled = __ballot(valid && al != 1.0f);
           if (m.lane == 0) s->one[slot] = scaled == 0ull ? 1 : 0;
-          // each split's running maximum at its last tile of the chunk
           carry = __shfl(run, 64 - 2 * ns + 2 * ((m.lane >> 1) & (ns - 1)), 64);
-          if (i == nch - 1 && m.lane < 2 * ns && !(m.lane & 1)) s->msplit[m.lane >> 1] = carry;
         }
         clk.pause();
         __syncthreads();
@@ -1752,23 +1764,419 @@ __device__ __forceinline__ void phase_values(const MegaArgs* pa, uint32_t tag, c
       trace_add(tb + 14 + (m.wave == 2 ? 0 : m.wave >= 4 ? 1 : m.wave == 0 ? 2 : 3), clk.busy);
     if (m.wave == 0) {
       den = s->den[0];
-      if (ns > 1) {
-        // merge the splits in a fixed tree (the per-kernel path and the
-        // restatement use the same one)
-        const float M = fmaxf(fmaxf(s->msplit[0], s->msplit[1]), fmaxf(s->msplit[2], s->msplit[3]));
-        float w[4], av[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          w[q] = hexp(s->msplit[q] - M);
-          av[q] = __shfl(acc, 16 * q + (m.lane & 15), 64);
-        }
-        acc = (av[0] * w[0] + av[1] * w[1]) + (av[2] * w[2] + av[3] * w[3]);
-        den = (s->den[0] * w[0] + s->den[1] * w[1]) + (s->den[2] * w[2] + s->den[3] * w[3]);
-      }
       const uint32_t gw = __shfl((int)gate_word, m.lane >> 1, 64);
       const uint16_t gb = (m.lane & 1) ? (uint16_t)(gw >> 16) : (uint16_t)(gw & 0xffffu);
       uint16_t y = 0;
       if (m.lane < kValueChannels) y = f2bf(rbf(acc / den) * sigmoid(bf2f(gb)));
+      const uint16_t other = (uint16_t)__shfl_down((int)y, 1, 64);
+      if (m.lane < kValueChannels && (m.lane & 1) == 0)
+        word_store(Ly.x_mix + ((head * HD + c0 + m.lane) >> 1), pack_bf(y, other), m.tag);
+    }
+    __syncthreads();
+  }
+}
+
+
+// ------------------------- phases: split-K attention (long contexts only)
+
+// Above the session's split threshold a full layer's attention runs as at
+// most kSplitRanges ranges of ceil(T / kSplitRanges) 8-key tiles per KV head
+// (T tiles in all): phase_flash gives every (KV head, range) item to a block,
+// which prepares the group's query heads, scores the range's keys for all of
+// them (each key row read once), runs the reference's online recurrence over
+// the range's tiles from scratch (its running maximum, alphas, denominator
+// and per-channel accumulators, the orders of phase_scores and
+// phase_values) and publishes (m_r, den_r, acc_r[HD]) per query head as
+// tagged words. phase_merge then folds the ranges in ascending order for each
+// (query head, 16-channel) item: M = max_r m_r, w_r = exp(m_r - M),
+// den = 0 + den_0 w_0 + den_1 w_1 + ..., acc likewise,
+// out = bf16(bf16(acc / den) * sigmoid(gate)). The per-kernel path
+// (attention.h) and the restatement split the same way.
+//
+// A range is processed in sub-chunks of at most kFlashSubTiles tiles
+// (balanced, multiples of 4 tiles) carrying the running maximum,
+// denominator and accumulators, so the chain is the range's one recurrence.
+// Per sub-chunk: V rows of its first kFlashDepth passes are requested, the
+// keys are scored (query heads held in registers), each head's wave scans
+// the tile maxima, then the V passes of kFlashVKeys rows run with the next
+// kFlashDepth - 1 passes in flight (16-byte loads into a register ring).
+constexpr int kFlashSubTiles = 64;
+constexpr int kFlashVKeys = 32;  // V rows staged per pass
+constexpr int kFlashDepth = 4;   // V passes in flight
+
+struct FlashLds {
+  float rope[256];
+  float qhat[8 * 256];      // the group's query heads, lane-major
+  uint16_t khat[2 * 256];   // key heads (the new position's)
+  uint16_t vnew[256];       // the new position's value head
+  float alpha[8][kFlashSubTiles];
+  float mr[8];              // each head's running maximum (carried over sub-chunks)
+  int heads[32];
+  int nheads;
+  int pad[3];
+  union {
+    float normed[kMW][256];                 // prepare_heads only
+    float p[8][8 * kFlashSubTiles];         // scores, then weights, per query head of the group
+  };
+  uint16_t v[kFlashVKeys][256];  // V rows of the current pass
+};
+static_assert(sizeof(FlashLds) <= kLdsBigBytes, "flash LDS");
+static_assert(offsetof(FlashLds, qhat) % 16 == 0 && offsetof(FlashLds, v) % 16 == 0 &&
+                  offsetof(FlashLds, p) % 16 == 0,
+              "16-byte LDS rows");
+
+// Words per (query head, range) partial: m, den, acc[HD].
+template <class S>
+constexpr int flash_words() { return 2 + S::HD; }
+
+// Phase-trace builds: per-stage time of the flash phase (prepare, scores,
+// scan, values), added per block into the layer's slots 14-17, items in 18.
+struct FlashClock {
+#ifdef CQ35_PHASE_TRACE
+  uint64_t t = __builtin_amdgcn_s_memrealtime(), spent[4] = {0, 0, 0, 0};
+  __device__ __forceinline__ void lap(int i) {
+    const uint64_t n = __builtin_amdgcn_s_memrealtime();
+    spent[i] += n - t;
+    t = n;
+  }
+  __device__ __forceinline__ void flush(int tb, int items) {
+    if (threadIdx.x == 0) {
+      for (int i = 0; i < 4; ++i) trace_lds()[tb + 14 + i] += spent[i];
+      trace_lds()[tb + 18] += (uint64_t)items;
+    }
+  }
+#else
+  __device__ __forceinline__ void lap(int) {}
+  __device__ __forceinline__ void flush(int, int) {}
+#endif
+};
+
+template <class S>
+__device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly, int tb) {
+  const Mega m = make_mega(pa, tag);
+  const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
+  const CQ35_CONST MegaArgs& a = m.a;
+  constexpr int HD = S::HD, Q = S::Q, KVH = S::KVH, HPK = Q / KVH, KJ = HD / 32, RH = S::R / 2;
+  constexpr int VPL = HD / 64, FW = flash_words<S>();
+  static_assert(HPK <= 8 && HD <= 256 && KVH <= 2, "flash shape");
+  const int64_t position = (int64_t)G(a.params)[0];
+  const int64_t keys = position + 1;
+  const int tiles = (int)((keys + 7) >> 3);
+  const int rtiles = (tiles + kSplitRanges - 1) / kSplitRanges;  // tiles per range
+  const int nranges = (tiles + rtiles - 1) / rtiles;
+  FlashLds* s = reinterpret_cast<FlashLds*>(m.big);
+  const float ninf = bitsf(0xff800000u);
+  const int l32 = m.lane & 31, half = m.lane >> 5;
+  FlashClock clk;
+  float qw_[VPL], kw_[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    qw_[i] = G(Ly.qnorm)[VPL * m.lane + i];
+    kw_[i] = G(Ly.knorm)[VPL * m.lane + i];
+  }
+  const float freq = G(a.freq)[min(m.tid, RH - 1)];
+  int nitems = 0;
+#pragma unroll 1
+  for (int item = m.bid; item < KVH * nranges; item += m.grid) {
+    ++nitems;
+    const int g = item % KVH, r = item / KVH;
+    const int nt = min(rtiles, tiles - r * rtiles);  // tiles of the range
+    const int64_t k0 = (int64_t)r * rtiles * 8;
+    const int n = (int)min<int64_t>(8 * nt, keys - k0);  // keys of the range
+    const bool has_new = r == nranges - 1;                // the range holding the new position
+    // the group's query parts, its key and value heads (projection words)
+    constexpr int QW = HPK * (HD / 2), KW = HD / 2;
+    const uint64_t* proj = Ly.x_proj;
+    auto index = [&](int i) -> int {
+      if (i < QW) {
+        const int hq = i / (HD / 2), c = i - hq * (HD / 2);
+        return (g * HPK + hq) * HD + c;  // words of [q(HD) | gate(HD)] per head
+      }
+      if (i < QW + KW) return S::QS + g * (HD / 2) + (i - QW);               // key head g
+      return S::QS + S::KVS / 2 + g * (HD / 2) + (i - QW - KW);              // value head g
+    };
+    poll_words<(QW + 2 * KW + kMT - 1) / kMT>(m, QW + 2 * KW, [&](int i) { return proj + index(i); }, m.vec);
+    const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
+    if (m.tid == 0) {
+      int nh = 0;
+      for (int hq = 0; hq < HPK; ++hq) s->heads[nh++] = g * HPK + hq;
+      if (has_new) s->heads[nh++] = Q + g;
+      s->nheads = nh;
+    }
+    if (m.tid < HPK) s->mr[m.tid] = ninf;
+    if (m.tid < RH) {
+      float sn, cs;
+      sincos_q((float)(uint32_t)position * freq, &sn, &cs);
+      s->rope[m.tid] = cs;
+      s->rope[RH + m.tid] = sn;
+    }
+    if (has_new && m.tid < HD) s->vnew[m.tid] = in16[QW * 2 + HD + m.tid];
+    __syncthreads();
+    prepare_heads<S>(m, s, s->nheads, qw_, kw_, [&](int hh) {
+      return hh < Q ? in16 + (hh - g * HPK) * HD : in16 + QW * 2;
+    }, [&](int hh) { return hh - g * HPK; });
+    // the new position's K and V into the cache for later steps
+    if (has_new && m.tid < HD) {
+      uint16_t* kdst = a.cache + Ly.key_base + position * S::KVS + (int64_t)g * HD;
+      uint16_t* vdst = a.cache + Ly.value_base + position * S::KVS + (int64_t)g * HD;
+      G(kdst)[m.tid] = s->khat[g * HD + m.tid];
+      G(vdst)[m.tid] = s->vnew[m.tid];
+    }
+    clk.lap(0);
+    // sub-chunks: nsub of st tiles (a multiple of 4; the last may be shorter)
+    const int nsub = (nt + kFlashSubTiles - 1) / kFlashSubTiles;
+    const int st = (((nt + nsub - 1) / nsub) + 3) & ~3;
+    // channel chains: thread = channel c of CPT query heads; threads tid < HPK
+    // also run head tid's denominator chain
+    constexpr int CPT = (HPK * HD + kMT - 1) / kMT;
+    const int c = m.tid % HD, hbase = (m.tid / HD) * CPT;
+    float acc[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) acc[i] = 0.0f;
+    float den = 0.0f;
+    constexpr int VQ = kFlashVKeys * HD / 8;     // 16-byte quads per pass
+    constexpr int VPT = (VQ + kMT - 1) / kMT;    // per thread
+    u32x4 ring[kFlashDepth][VPT];
+#pragma unroll 1
+    for (int sc = 0; sc < nsub; ++sc) {
+      const int t0 = sc * st;                    // first tile of the sub-chunk (range-relative)
+      const int snt = min(st, nt - t0);          // its tiles
+      const int c0 = 8 * t0;                     // its first key (range-relative)
+      const int sn = min(8 * snt, n - c0);       // its keys
+      const int np = (snt + 3) / 4;              // its V passes
+      // V rows of pass q into ring registers (rows past the range read key
+      // 0's row; their weight is 0; the new position's row comes from LDS)
+      auto fetch = [&](u32x4 (&dst)[VPT], int q) {
+        if (q >= np) return;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+          const int idx = m.tid + kMT * i;
+          if (VQ % kMT == 0 || idx < VQ) {
+            const int kk = c0 + kFlashVKeys * q + idx / (HD / 8), qd = idx % (HD / 8);
+            const int64_t key = kk < n ? k0 + kk : 0;
+            if (key == position) dst[i] = reinterpret_cast<const u32x4*>(s->vnew)[qd];
+            else dst[i] = G(reinterpret_cast<const u32x4*>(a.cache + Ly.value_base + key * S::KVS + (int64_t)g * HD))[qd];
+          }
+        }
+      };
+      auto put = [&](const u32x4 (&src)[VPT]) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+          const int idx = m.tid + kMT * i;
+          if (VQ % kMT == 0 || idx < VQ) reinterpret_cast<u32x4*>(&s->v[idx / (HD / 8)][0])[idx % (HD / 8)] = src[i];
+        }
+      };
+#pragma unroll
+      for (int d = 0; d < kFlashDepth; ++d) fetch(ring[d], d);
+      // scores: half-wave hw takes keys hw, hw + 16, ... of the sub-chunk;
+      // lane l32 owns channels l32 + 32 j (serial from 0.0, then the 32-lane tree)
+      const int hw = 2 * m.wave + half;
+      constexpr int SB = 2;
+      auto load_keys = [&](uint32_t (&kv)[SB][KJ], int b) {
+#pragma unroll
+        for (int rr = 0; rr < SB; ++rr) {
+          const int kk = c0 + min(hw + 16 * (b * SB + rr), sn - 1);
+          const int64_t key = k0 + kk == position ? 0 : k0 + kk;
+          const uint16_t* kr = a.cache + Ly.key_base + key * S::KVS + (int64_t)g * HD + l32;
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) kv[rr][j] = G(kr)[32 * j];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      auto score_keys = [&](const uint32_t (&kv)[SB][KJ], int b) {
+        float kf[SB][KJ];
+#pragma unroll
+        for (int rr = 0; rr < SB; ++rr) {
+          const bool fresh = k0 + c0 + hw + 16 * (b * SB + rr) == position;
+#pragma unroll
+          for (int j = 0; j < KJ; ++j)
+            kf[rr][j] = bf2f(fresh ? s->khat[g * HD + l32 + 32 * j] : (uint16_t)kv[rr][j]);
+        }
+        // each query head read from LDS once per batch of SB keys
+#pragma unroll
+        for (int hq = 0; hq < HPK; ++hq) {
+          const float* qh = s->qhat + hq * HD + l32 * KJ;
+          float qv[KJ];
+#pragma unroll
+          for (int j = 0; j < KJ; ++j) qv[j] = qh[j];
+#pragma unroll
+          for (int rr = 0; rr < SB; ++rr) {
+            const int kk = hw + 16 * (b * SB + rr);  // sub-chunk relative
+            float x = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) x += qv[j] * kf[rr][j];
+            x = tree32_lanes(x);
+            if (l32 == 0 && kk < sn) s->p[hq][kk] = x * a.attn_scale;
+          }
+        }
+      };
+      const int nb = (sn + 16 * SB - 1) / (16 * SB);
+      uint32_t ka[SB][KJ], kb[SB][KJ];
+      load_keys(ka, 0);
+      int b = 0;
+#pragma unroll 1
+      for (; b + 1 < nb; b += 2) {
+        load_keys(kb, b + 1);
+        score_keys(ka, b);
+        load_keys(ka, min(b + 2, nb - 1));
+        score_keys(kb, b + 1);
+      }
+      if (b < nb) score_keys(ka, b);
+      __syncthreads();
+      clk.lap(1);
+      // per query head (wave hq), groups of 32 tiles: tile maxima, the running
+      // maximum (carried from the previous tiles of the range),
+      // alpha_t = exp(m_{t-1} - m_t) (m_{-1} = -inf), p = exp(s - m_t)
+      if (m.wave < HPK) {
+        const int hq = m.wave;
+        float carry = s->mr[hq];
+#pragma unroll 1
+        for (int tg = 0; tg < snt; tg += 32) {
+          const int t = tg + (m.lane >> 1), kb4 = 8 * t + 4 * (m.lane & 1);
+          float sv[4], mt = ninf;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            sv[j] = kb4 + j < sn ? s->p[hq][kb4 + j] : ninf;
+            mt = fmaxf(mt, sv[j]);
+          }
+          mt = fmaxf(mt, __shfl_xor(mt, 1, 64));
+          float run = mt;
+#pragma unroll
+          for (int d = 2; d < 64; d <<= 1) {
+            const float o = __shfl_up(run, d, 64);
+            if (m.lane >= d) run = fmaxf(run, o);
+          }
+          run = fmaxf(run, carry);
+          float prev = __shfl_up(run, 2, 64);
+          if (m.lane < 2) prev = carry;
+          if (t < snt) {
+            if (!(m.lane & 1)) s->alpha[hq][t] = hexp(prev - run);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s->p[hq][kb4 + j] = kb4 + j < sn ? hexp(sv[j] - run) : 0.0f;
+          }
+          const int last = min(snt - tg, 32) - 1;
+          carry = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, run), 2 * last));
+        }
+        if (m.lane == 0) s->mr[hq] = carry;
+      }
+      __syncthreads();
+      clk.lap(2);
+      // V passes: the pass's rows into LDS, the next pass requested, then the
+      // chains over the pass's tiles
+      auto consume = [&](int q) {
+        const int ta = 4 * q, tz = min(snt, ta + 4);
+        if (hbase < HPK) {
+#pragma unroll 1
+          for (int t = ta; t < tz; ++t) {
+            float vv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vv[j] = bf2f(s->v[8 * (t - ta) + j][c]);
+#pragma unroll
+            for (int i = 0; i < CPT; ++i) {
+              const int hq = hbase + i;
+              if (hq < HPK) {
+                float x = acc[i] * s->alpha[hq][t];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x = x + s->p[hq][8 * t + j] * vv[j];
+                acc[i] = x;
+              }
+            }
+          }
+        }
+        if (m.tid < HPK) {
+#pragma unroll 1
+          for (int t = ta; t < tz; ++t) {
+            den = den * s->alpha[m.tid][t];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) den = den + s->p[m.tid][8 * t + j];
+          }
+        }
+      };
+#pragma unroll 1
+      for (int q0 = 0; q0 < np; q0 += kFlashDepth) {
+#pragma unroll
+        for (int d = 0; d < kFlashDepth; ++d) {
+          const int q = q0 + d;
+          if (q < np) {
+            put(ring[d]);
+            __syncthreads();
+            fetch(ring[d], q + kFlashDepth);
+            consume(q);
+            __syncthreads();
+          }
+        }
+      }
+      clk.lap(3);
+    }
+    // partial words of each query head of the group
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int hq = hbase + i;
+      if (hq < HPK && c < HD) {
+        uint64_t* w = Ly.x_scores + ((size_t)(g * HPK + hq) * kSplitRanges + r) * FW;
+        word_store(w + 2 + c, fbits(acc[i]), m.tag);
+      }
+    }
+    if (m.tid < HPK) {
+      uint64_t* w = Ly.x_scores + ((size_t)(g * HPK + m.tid) * kSplitRanges + r) * FW;
+      word_store(w, fbits(s->mr[m.tid]), m.tag);
+      word_store(w + 1, fbits(den), m.tag);
+    }
+    __syncthreads();
+    clk.lap(3);
+  }
+  clk.flush(tb, nitems);
+}
+
+template <class S>
+__device__ __forceinline__ void phase_merge(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
+  const Mega m = make_mega(pa, tag);
+  const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
+  const CQ35_CONST MegaArgs& a = m.a;
+  constexpr int HD = S::HD, CHUNKS = HD / kValueChannels, ITEMS = S::Q * CHUNKS, FW = flash_words<S>();
+  constexpr int RW = 2 + kValueChannels;  // words of one range taken: m, den, the chunk's channels
+  const int64_t keys = (int64_t)G(a.params)[0] + 1;
+  const int tiles = (int)((keys + 7) >> 3);
+  const int rtiles = (tiles + kSplitRanges - 1) / kSplitRanges;
+  const int nranges = (tiles + rtiles - 1) / rtiles;
+  float* f = reinterpret_cast<float*>(m.big);  // [ranges][RW]
+  float* wr = f + kSplitRanges * RW;           // w_r per range
+  static_assert((kSplitRanges * (RW + 1)) * 4 <= kLdsBigBytes, "merge LDS");
+  constexpr int PW = (kSplitRanges * RW + kMT - 1) / kMT;
+  const float ninf = bitsf(0xff800000u);
+#pragma unroll 1
+  for (int slot = m.bid; slot < ITEMS; slot += m.grid) {
+    const int head = slot / CHUNKS, c0 = (slot - head * CHUNKS) * kValueChannels;
+    const uint64_t* base = Ly.x_scores + (size_t)head * kSplitRanges * FW;
+    uint32_t gate_word = 0;
+    if (m.wave == 0 && m.lane < kValueChannels / 2)
+      gate_word = poll_one(m, Ly.x_proj + ((head * 2 * HD + HD + c0) >> 1) + m.lane);
+    // every range's words at once
+    poll_words<PW>(m, nranges * RW, [&](int i) {
+      const int r = i / RW, k = i - r * RW;
+      return base + (size_t)r * FW + (k < 2 ? k : c0 + k);
+    }, reinterpret_cast<uint32_t*>(f));
+    if (m.wave == 0) {
+      float top = ninf;
+      for (int r = m.lane; r < nranges; r += 64) top = fmaxf(top, f[r * RW]);
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) top = fmaxf(top, __shfl_xor(top, d, 64));
+      for (int r = m.lane; r < nranges; r += 64) wr[r] = hexp(f[r * RW] - top);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      float A = 0.0f, D = 0.0f;
+      if (m.lane < kValueChannels) {
+        for (int i = 0; i < nranges; ++i) {
+          const float w = wr[i];
+          D = D + f[i * RW + 1] * w;
+          A = A + f[i * RW + 2 + m.lane] * w;
+        }
+      }
+      const uint32_t gw = __shfl((int)gate_word, m.lane >> 1, 64);
+      const uint16_t gb = (m.lane & 1) ? (uint16_t)(gw >> 16) : (uint16_t)(gw & 0xffffu);
+      uint16_t y = 0;
+      if (m.lane < kValueChannels) y = f2bf(rbf(A / D) * sigmoid(bf2f(gb)));
       const uint16_t other = (uint16_t)__shfl_down((int)y, 1, 64);
       if (m.lane < kValueChannels && (m.lane & 1) == 0)
         word_store(Ly.x_mix + ((head * HD + c0 + m.lane) >> 1), pack_bf(y, other), m.tag);
@@ -1920,11 +2328,15 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
     phase_project<S>(pa, tag, ly, l, pr);
     trace_max(tb + 0);
     if (phase_ptr(ly)->full != 0) {
+      const int64_t keys = (int64_t)G(phase_ptr(pa)->params)[0] + 1;
+      const int64_t split = phase_ptr(pa)->split_keys;
       trace_slot(tb + 3);
-      phase_scores<S>(pa, tag, ly);
+      if (split > 0 && keys > split) phase_flash<S>(pa, tag, ly, tb);
+      else phase_scores<S>(pa, tag, ly);
       trace_max(tb + 2);
       trace_slot(tb + 5);
-      phase_values<S>(pa, tag, ly, tb);
+      if (split > 0 && keys > split) phase_merge<S>(pa, tag, ly);
+      else phase_values<S>(pa, tag, ly, tb);
       trace_max(tb + 4);
       trace_slot(tb + 7);
       phase_outproj<S, S::QS>(pa, tag, ly);

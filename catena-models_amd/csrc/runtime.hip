@@ -883,9 +883,12 @@ int setup_mega(cq35_session* s) {
   for (int64_t l = 0; l < d.L; ++l) {
     const bool full = is_full(c, l);
     const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS;
+    // full layers: Q x capacity score words, or (split-K) per query head and
+    // range the partial words (m, den, acc[HD])
+    const int64_t scores = std::max<int64_t>(d.Q * s->capacity, d.Q * kSplitRanges * (2 + d.HD));
     const int64_t sizes[8] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
                               region(d.E + 1), region(d.K * d.I / 2),
-                              full ? region(d.Q * s->capacity) : 0, region(d.SI / 2)};
+                              full ? region(scores) : 0, region(d.SI / 2)};
     for (int64_t z : sizes) {
       offs.push_back(total);
       total += z;

@@ -229,14 +229,15 @@ int cq35_session_persistent(const cq35_session* session, int* enabled);
  * bit 1: the MoE expert projections (grouped routed experts and the shared
  * expert). 0 keeps the exact SIMT path. Decode steps are unaffected. */
 /* Split-K decode attention for long contexts. Over more than `keys` cached
- * keys (default CQ35_SPLIT_KEYS_DEFAULT; 0: never) the online softmax of each
- * query head runs as four splits, tile t (8 keys) in split t mod 4, each the
- * reference's recurrence over its own tiles, merged in a fixed tree
- * (M = max m_s, w_s = exp(m_s - M), den = (d0 w0 + d1 w1) + (d2 w2 + d3 w3),
- * likewise each channel). The reference runs one sequential chain over all
- * tiles (qwen35_online.hex:272-331); the split changes rounding only
- * (tolerance-level), and at or below the threshold the result is the
- * reference's bit for bit. Both decode paths use the same split. */
+ * keys (default CQ35_SPLIT_KEYS_DEFAULT; 0: never) the T tiles (8 keys) of
+ * each query head's online softmax form at most 128 ranges of ceil(T / 128)
+ * tiles, each the reference's recurrence over its own tiles from scratch,
+ * merged in ascending range order (M = max m_r, w_r = exp(m_r - M),
+ * den = 0 + d_0 w_0 + d_1 w_1 + ..., likewise each channel). The reference
+ * runs one sequential chain over all tiles (qwen35_online.hex:272-331); the
+ * split changes rounding only (tolerance-level), and at or below the
+ * threshold the result is the reference's bit for bit. Both decode paths use
+ * the same ranges, which depend on the key count alone. */
 #define CQ35_SPLIT_KEYS_DEFAULT 8192
 int cq35_session_set_attention_split(cq35_session* session, int64_t keys);
 int cq35_session_attention_split(const cq35_session* session, int64_t* keys);

@@ -703,71 +703,89 @@ static void gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* 
 /* Online decode attention, 8-key tiles (online.hex:4-331).
  *
  * Split-K above split_keys keys (this build's long-context mode; the
- * reference always runs one chain): tile t belongs to split t mod 4, and each
- * split runs the reference's online recurrence over its own tiles in order
- * (running maximum m_s, den_s = den_s a + p_0 + ... + p_7, acc_s = acc_s a +
- * p_0 v_0 + ...). The splits merge in a fixed tree: M = max_s m_s,
- * w_s = exp(m_s - M), den = (den_0 w_0 + den_1 w_1) + (den_2 w_2 + den_3 w_3),
+ * reference always runs one chain): the T tiles form at most 128 ranges of
+ * ceil(T / 128) tiles each (the last may be shorter), and each range runs
+ * the reference's online recurrence over its own tiles
+ * from scratch (running maximum m_r, den_r = den_r a + p_0 + ... + p_7,
+ * acc_r = acc_r a + p_0 v_0 + ...). The ranges merge in ascending order:
+ * M = max_r m_r, w_r = exp(m_r - M), den = (0 + den_0 w_0) + den_1 w_1 + ...,
  * acc likewise; out = bf16(bf16(acc / den) * sigmoid(gate)). At or below
  * split_keys (and with split_keys = 0) the single chain is the reference's. */
+#define OX_SPLIT_RANGES 128
 static void attention_online(const ox_model* m, const uint16_t* q, const uint16_t* cache,
                              int64_t key_base, int64_t value_base, int64_t keys,
                              const uint16_t* qg, int64_t split_keys, uint16_t* out) {
   const int HD = m->c.head_dim, hpk = m->c.q_heads / m->c.kv_heads;
   const int64_t KVS = m->KVS;
-  const int NS = (split_keys > 0 && keys > split_keys) ? 4 : 1;
+  const int split = split_keys > 0 && keys > split_keys;
+  const int64_t tiles = (keys + 7) / 8;
+  const int64_t range_tiles = split ? (tiles + OX_SPLIT_RANGES - 1) / OX_SPLIT_RANGES : tiles;
   const float scale = g_plant == OX_PLANT_ATTN_SCALE ? 1.0f : 1.0f / sqrtf((float)HD);  /* SCALE_BITS, qwen35.rs:701 */
 #pragma omp parallel for schedule(static)
   for (int head = 0; head < m->c.q_heads; ++head) {
     int64_t off = (int64_t)(g_plant == OX_PLANT_GQA_MAP ? head % m->c.kv_heads : head / hpk) * HD;
-    float maximum[4], den[4];
-    float* value = (float*)calloc((size_t)(4 * HD), sizeof(float));
-    for (int sp = 0; sp < 4; ++sp) { maximum[sp] = bitsf(0xFF800000u); den[sp] = 0.0f; }
-    for (int64_t first = 0; first < keys; first += 8) {
-      const int sp = (int)((first / 8) % NS);
-      float* acc = value + sp * HD;
-      float score[8], p[8];
-      for (int j = 0; j < 8; ++j) {
-        int64_t key = first + j;
-        if (key >= keys) { score[j] = bitsf(0xFF800000u); continue; }
-        float lanes[32];
-        for (int l = 0; l < 32; ++l) {
-          float a = 0.0f;
-          for (int ch = l; ch < HD; ch += 32)
-            a += ox_bf2f(q[head * HD + ch]) * ox_bf2f(cache[key_base + key * KVS + off + ch]);
-          lanes[l] = a;
-        }
-        score[j] = tree(lanes, 32) * scale;
-      }
-      float next_max = maximum[sp];
-      for (int j = 0; j < 8; ++j) next_max = fmaxf(next_max, score[j]);
-      float alpha = ox_exp(maximum[sp] - next_max);
-      den[sp] = den[sp] * alpha;
-      for (int j = 0; j < 8; ++j) { p[j] = ox_exp(score[j] - next_max); den[sp] = den[sp] + p[j]; }
-      maximum[sp] = next_max;
-      for (int ch = 0; ch < HD; ++ch) {
-        float v = acc[ch] * alpha;
+    const int64_t nranges = (tiles + range_tiles - 1) / range_tiles;
+    float* rmax = (float*)malloc(sizeof(float) * (size_t)nranges);
+    float* rden = (float*)malloc(sizeof(float) * (size_t)nranges);
+    float* racc = (float*)malloc(sizeof(float) * (size_t)(nranges * HD));
+    for (int64_t r = 0; r < nranges; ++r) {
+      float maximum = bitsf(0xFF800000u), den = 0.0f;
+      float* acc = racc + r * HD;
+      for (int ch = 0; ch < HD; ++ch) acc[ch] = 0.0f;
+      const int64_t t_end = (r + 1) * range_tiles < tiles ? (r + 1) * range_tiles : tiles;
+      for (int64_t t = r * range_tiles; t < t_end; ++t) {
+        const int64_t first = t * 8;
+        float score[8], p[8];
         for (int j = 0; j < 8; ++j) {
-          int64_t key = first + j < keys ? first + j : 0;
-          v = v + p[j] * ox_bf2f(cache[value_base + key * KVS + off + ch]);
+          int64_t key = first + j;
+          if (key >= keys) { score[j] = bitsf(0xFF800000u); continue; }
+          float lanes[32];
+          for (int l = 0; l < 32; ++l) {
+            float a = 0.0f;
+            for (int ch = l; ch < HD; ch += 32)
+              a += ox_bf2f(q[head * HD + ch]) * ox_bf2f(cache[key_base + key * KVS + off + ch]);
+            lanes[l] = a;
+          }
+          score[j] = tree(lanes, 32) * scale;
         }
-        acc[ch] = v;
+        float next_max = maximum;
+        for (int j = 0; j < 8; ++j) next_max = fmaxf(next_max, score[j]);
+        float alpha = ox_exp(maximum - next_max);
+        den = den * alpha;
+        for (int j = 0; j < 8; ++j) { p[j] = ox_exp(score[j] - next_max); den = den + p[j]; }
+        maximum = next_max;
+        for (int ch = 0; ch < HD; ++ch) {
+          float v = acc[ch] * alpha;
+          for (int j = 0; j < 8; ++j) {
+            int64_t key = first + j < keys ? first + j : 0;
+            v = v + p[j] * ox_bf2f(cache[value_base + key * KVS + off + ch]);
+          }
+          acc[ch] = v;
+        }
       }
+      rmax[r] = maximum;
+      rden[r] = den;
     }
-    float w[4] = {1.0f, 0.0f, 0.0f, 0.0f}, total = den[0];
-    if (NS == 4) {
-      const float M = fmaxf(fmaxf(maximum[0], maximum[1]), fmaxf(maximum[2], maximum[3]));
-      for (int sp = 0; sp < 4; ++sp) w[sp] = ox_exp(maximum[sp] - M);
-      total = (den[0] * w[0] + den[1] * w[1]) + (den[2] * w[2] + den[3] * w[3]);
+    float total = rden[0];
+    float* value = racc;  /* one range: the reference's single chain */
+    float* merged = NULL;
+    if (split) {
+      float M = bitsf(0xFF800000u);
+      for (int64_t r = 0; r < nranges; ++r) M = fmaxf(M, rmax[r]);
+      merged = (float*)calloc((size_t)HD, sizeof(float));
+      total = 0.0f;
+      for (int64_t r = 0; r < nranges; ++r) {
+        const float w = ox_exp(rmax[r] - M);
+        total = total + rden[r] * w;
+        for (int ch = 0; ch < HD; ++ch) merged[ch] = merged[ch] + racc[r * HD + ch] * w;
+      }
+      value = merged;
     }
     for (int ch = 0; ch < HD; ++ch) {
-      float a = value[ch];
-      if (NS == 4)
-        a = (value[ch] * w[0] + value[HD + ch] * w[1]) + (value[2 * HD + ch] * w[2] + value[3 * HD + ch] * w[3]);
       float gate = ox_sigmoid(ox_bf2f(qg[2 * (int64_t)head * HD + HD + ch]));
-      out[head * HD + ch] = ox_f2bf(rbf(a / total) * gate);
+      out[head * HD + ch] = ox_f2bf(rbf(value[ch] / total) * gate);
     }
-    free(value);
+    free(rmax); free(rden); free(racc); free(merged);
   }
 }
 

@@ -131,10 +131,10 @@ int ox_step(ox_session* s, const uint64_t* tokens, int64_t n, int64_t start,
             uint64_t* next_token, uint16_t* logits);
 
 /* Decode attention (online, MoE) over more than `keys` cached keys runs as
- * four interleaved splits merged at the end (this build's long-context
- * mode, tolerance-level against the reference's single chain); 0 keeps the
- * single chain at every length. Default OX_SPLIT_KEYS_DEFAULT, the GPU
- * library's default. */
+ * at most 128 ranges of equal tile counts, each with its own online
+ * recurrence, merged in ascending order (this build's long-context mode, tolerance-level against
+ * the reference's single chain); 0 keeps the single chain at every length.
+ * Default OX_SPLIT_KEYS_DEFAULT, the GPU library's default. */
 #define OX_SPLIT_KEYS_DEFAULT 8192
 void ox_session_set_split_keys(ox_session* s, int64_t keys);
 

@@ -10,8 +10,9 @@ layout is src/spec.rs:321-362).
 These contexts reach code the short sessions never do: several score rounds
 per wave, hundreds of value chunks through the scan/products/chain
 pipeline, and last chunks of every length. Above 8192 cached keys the
-decode attention runs split-K by default (four interleaved splits merged in
-a fixed tree, the same in both decode paths and the restatement); the
+decode attention runs split-K by default (at most 128 ranges of equal tile
+counts merged in ascending order, the same in both decode paths and the
+restatement); the
 exact single chain stays selectable and is checked too, and the split's
 results are held to the parity bar against it (logits within 2e-2, tokens
 equal except at near-ties below 1e-3, DeltaNet state within 1e-3)."""
