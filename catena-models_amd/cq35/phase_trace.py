@@ -31,7 +31,7 @@ import numpy as np
 from . import _build, _lib
 from .config import derived, is_full, preset
 
-TRACE_LAYER_SLOTS = 20  # mega.h kTraceLayerSlots
+TRACE_LAYER_SLOTS = 32  # mega.h kTraceLayerSlots
 TRACE_LAYERS = 48
 TRACE_HEAD = TRACE_LAYERS * TRACE_LAYER_SLOTS
 TRACE_START = TRACE_HEAD + 1
@@ -39,6 +39,11 @@ TICK_US = 0.01
 HBM_GBS = 8000.0
 
 LINEAR = ["project", "delta", None, "outproj", "router + shared", "select + gate/up", "down"]
+# mega.h TraceMark: (slot, phase index, label)
+MARKS = [(20, 0, "input row normalised"), (21, 1, "convolution done"), (22, 1, "L2 norms and gates done"),
+         (23, 1, "state update done"), (29, 3, "outputs computed"), (24, 4, "post-mixer row normalised"),
+         (25, 5, "experts selected"), (26, 5, "outputs stored"), (27, 6, "staged weights and inputs in"),
+         (28, 6, "outputs stored")]
 FULL = ["project", "scores", "values", "outproj", "router + shared", "select + gate/up", "down"]
 
 
@@ -70,6 +75,7 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
     start = trace[:, TRACE_START][trace[:, TRACE_START] > 0].min()
     pb = phase_bytes(cfg, keys)
     rows = {"lin": {}, "full": {}}
+    timeline = {"lin": {}, "full": {}}
     per_layer = []
     prev_done = start
     roles = []
@@ -78,6 +84,7 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
         kind = "full" if is_full(cfg, l) else "lin"
         names = FULL if kind == "full" else LINEAR
         layer_start = prev_done
+        tl = timeline[kind]
         for p, name in enumerate(names):
             if name is None:
                 continue
@@ -85,6 +92,15 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
             polled = trace[:, tb + 2 * p + 1]
             polled = polled[polled > 0]
             inputs = (polled.max() - prev_done) if polled.size else 0
+            if polled.size:
+                tl.setdefault((p, 0, name + ": inputs in"), []).append((polled.max() - layer_start) * TICK_US)
+            for slot, mp, label in MARKS:
+                if mp == p:
+                    v = trace[:, tb + slot]
+                    v = v[v > 0]
+                    if v.size:
+                        tl.setdefault((p, slot, name + ": " + label), []).append((v.max() - layer_start) * TICK_US)
+            tl.setdefault((p, 99, name + ": done"), []).append((done - layer_start) * TICK_US)
             r = rows[kind].setdefault(name, [0.0, 0.0, 0])
             r[0] += (done - prev_done) * TICK_US
             r[1] += inputs * TICK_US
@@ -117,6 +133,11 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
             tot += c / cnt
             out.append(f"| {name} | {c / cnt:.2f} | {i / cnt:.2f} | {floor_us(pb, kind, name):.2f} |")
         out.append(f"| **layer** | **{tot:.2f}** | | |")
+        out.append(f"\n*{label} timeline* (last wave to reach the point, us from the layer's start, mean)\n")
+        out.append("| point | us |")
+        out.append("|---|---|")
+        for key in sorted(timeline[kind]):
+            out.append(f"| {key[2]} | {np.mean(timeline[kind][key]):.2f} |")
     if roles and flash:
         b = np.mean(roles, axis=0)
         out.append("\n**flash phase, time per stage** (per full layer, us; mean over blocks / slowest block; "
@@ -158,10 +179,11 @@ def main() -> int:
     ap.add_argument("--long", type=int, default=0, help="decode from a seeded state of this many positions")
     ap.add_argument("--steps", type=int, default=8)
     ap.add_argument("--build", action="store_true")
+    ap.add_argument("--dump", default="", help="also save the raw [blocks][slots] stamps (numpy .npy)")
     args = ap.parse_args()
     if args.build or not os.path.exists(_build.TRACE_LIBRARY):
         _build.build(trace=True)
-    _lib.LIBRARY = _build.TRACE_LIBRARY
+    _lib.LIBRARY = os.environ.get("CQ35_LIBRARY") or _build.TRACE_LIBRARY
     from . import model as cq
     cfg = preset(args.config)
     m = cq.Model.synthetic(cfg, seed=0)
@@ -188,6 +210,8 @@ def main() -> int:
     _lib.check(lib.cq35_session_phase_trace(s._h, buf.ctypes.data, buf.size, ctypes.byref(slots),
                                             ctypes.byref(ctypes.c_int64())))
     trace = buf.reshape(blocks, n).astype(np.int64)
+    if args.dump:
+        np.save(args.dump, trace)
     keys = (args.long or args.context) + args.steps
     split = s.attention_split
     flash = split > 0 and keys > split

@@ -147,6 +147,7 @@ struct MegaMisc {
   int any_nan;
   int bid, grid;  // block index and grid size, re-read by every phase
   int tslot;      // phase-trace builds: the slot the current phase's poll stamps
+  int tbase;      // phase-trace builds: the current layer's first slot
 };
 static_assert(sizeof(MegaMisc) <= kLdsBig - kLdsMisc, "misc LDS");
 
@@ -161,9 +162,24 @@ extern __shared__ __align__(16) unsigned char mega_lds[];
 // l * kTraceLayerSlots + 2p holds the time its last wave finished the phase
 // and 2p + 1 the time its inputs had all arrived (end of its poll); slots
 // 14-17 hold the values phase's busy time per role (scan, products, channel
-// chains, denominator chain) in 10 ns units. Slot kTraceHead is the head's
-// end, kTraceStart the step's start. Normal builds compile all of it away.
-constexpr int kTraceLayerSlots = 20;
+// chains, denominator chain) in 10 ns units (split-K: the flash phase's
+// stages, 18 its items); slots 20-29 the last wave's time at points inside
+// phases (kTraceMarks). Slot kTraceHead is the head's end, kTraceStart the
+// step's start. Normal builds compile all of it away.
+constexpr int kTraceLayerSlots = 32;
+// Points inside phases (slot offsets in a layer).
+enum TraceMark {
+  kMarkProjectNormed = 20,  // project: input row polled and normalised
+  kMarkDeltaConv = 21,      // delta: convolution done
+  kMarkDeltaGates = 22,     // delta: L2 norms and gates done
+  kMarkDeltaState = 23,     // delta: state update done
+  kMarkRouterNormed = 24,   // router: post-mixer row normalised
+  kMarkSelected = 25,       // gate/up: experts selected
+  kMarkGateUpDone = 26,     // gate/up: outputs stored
+  kMarkDownStaged = 27,     // down: staged weights and inputs in
+  kMarkDownDone = 28,       // down: outputs stored
+  kMarkOutprojDone = 29,    // output projection: outputs computed
+};
 constexpr int kTraceLayers = 48;
 constexpr int kTraceHead = kTraceLayers * kTraceLayerSlots;
 constexpr int kTraceStart = kTraceHead + 1;
@@ -178,6 +194,15 @@ __device__ __forceinline__ void trace_max(int slot) {
                            __HIP_MEMORY_SCOPE_WORKGROUP);
 #else
   (void)slot;
+#endif
+}
+
+// The last wave's time at a point inside a phase of the current layer.
+__device__ __forceinline__ void trace_mark(int mark) {
+#ifdef CQ35_PHASE_TRACE
+  trace_max(reinterpret_cast<volatile int*>(mega_lds + kLdsMisc + offsetof(MegaMisc, tbase))[0] + mark);
+#else
+  (void)mark;
 #endif
 }
 
@@ -455,6 +480,35 @@ __device__ __forceinline__ void pair_acc(float& lo, float& hi, uint32_t x, uint3
   hi += hi2f(x) * hi2f(w);
 }
 
+// pair_acc over j = 0 .. NJ-1 with x[32 j] and w[32 j] in LDS, in order. The
+// reads of a batch are issued before the products of the previous one (the
+// scheduler otherwise waits out one LDS round trip per pair of reads).
+template <int NJ>
+__device__ __forceinline__ void pair_chain_lds(float& lo, float& hi, const uint32_t* x, const CQ35_LDS uint32_t* w) {
+  constexpr int B = NJ < 8 ? NJ : 8, NB = NJ / B;
+  static_assert(NJ % B == 0, "pair chain batches");
+  uint32_t xv[2][B], wv[2][B];
+#pragma unroll
+  for (int i = 0; i < B; ++i) {
+    xv[0][i] = x[32 * i];
+    wv[0][i] = w[32 * i];
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b + 1 < NB) {
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        xv[(b + 1) & 1][i] = x[32 * ((b + 1) * B + i)];
+        wv[(b + 1) & 1][i] = w[32 * ((b + 1) * B + i)];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < B; ++i) pair_acc(lo, hi, xv[b & 1][i], wv[b & 1][i]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 
 // -------------------------------------------------- phase: S256 projection
 
@@ -517,6 +571,7 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
   norm_weights<S>(m, Ly.in_norm, w0, w1);
   load_hidden<S>(m, Ly.x_h, m.xr, l == 0);
   norm_row<S>(m, m.xr, w0, w1, m.a.eps);
+  trace_mark(kMarkProjectNormed);
   // this lane's input quads, unpacked once for all its rows
   float xl[NQ][4], xh[NQ][4];
 #pragma unroll
@@ -663,6 +718,7 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     }
   }
   __syncthreads();
+  trace_mark(kMarkDeltaConv);
   // serial L2 sums (q: thread 0, k: thread 64) and the gates (thread 128)
   if (m.tid == 0 || m.tid == 64) {
     const float total = serial_sum<KD>(d->sq + (m.tid == 0 ? 0 : KD));
@@ -682,6 +738,7 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     else d->khat[m.tid - KD] = r;
   }
   __syncthreads();
+  trace_mark(kMarkDeltaGates);
   // delta step: 64 channels per pass, 8 lanes per channel; lane q holds the
   // D32 reference lanes 4q..4q+3, i.e. key elements 4q + i + 32j (i, j < 4):
   // per i a serial chain over j from 0.0, then the 32-lane halving tree
@@ -739,6 +796,7 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     if (q == 0 && valid) d->core[c] = f2bf(out * a.delta_scale);
   }
   __syncthreads();
+  trace_mark(kMarkDeltaState);
   // gated RMSNorm with a serial sum (cooperative_norm.hex:139-182)
   if (m.tid < VD) {
     const float v = bf2f(d->core[m.tid]);
@@ -804,6 +862,7 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
     o = bf_add(f2bf(v), m.xr[row]);
     if (m.lane == 0 && (m.wave & 1)) m.misc->red[4 + (m.wave >> 1)] = __builtin_bit_cast(float, (uint32_t)o);
   }
+  trace_mark(kMarkOutprojDone);
   __syncthreads();
   if (has_row && m.lane == 0 && !(m.wave & 1)) {
     const uint16_t other = (uint16_t)__builtin_bit_cast(uint32_t, m.misc->red[4 + (m.wave >> 1)]);
@@ -817,22 +876,24 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
 // for the router and the gate/up phase and keeps the raw row for the FFN
 // residual. Even waves 2i compute router row block + grid * i (rows
 // [0, E] spread one per block; moe.hex:4-84): physical lane 2r + h runs
-// reference lane r's low (h = 0) or high (h = 1) accumulator over floats
-// 64k + lane. Odd waves 2i+1 compute the shared expert's gate/up row pair
-// block + grid * i (dual S256, moe.hex:254-333) up to the routing-dependent
-// factor:
-// t = bf16(bf16(silu(bf16 g)) * bf16 u); the down phase applies
-// bf16(t * sigmoid(shared logit)), the same roundings as the reference.
+// reference lanes r's low (h = 0) or high (h = 1) accumulator over floats
+// 64k + lane. The four odd waves of block b compute the shared expert's
+// gate/up rows of pair b (dual S256, moe.hex:254-333), one row each (gate
+// 2b, up 2b, gate 2b+1, up 2b+1), and wave 1 combines them up to the
+// routing-dependent factor: t = bf16(bf16(silu(bf16 g)) * bf16 u); the down
+// phase applies bf16(t * sigmoid(shared logit)), the same roundings as the
+// reference.
 template <class S>
 __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   constexpr int H = S::H, QH = S::QH, NQ = S::NQA, ROWS = S::E + 1, NJ = (H + 63) / 64;
+  static_assert(S::SI / 2 <= 256, "shared pairs");
   float wv[NJ];
-  u32x4 gv[2][NQ], uv[2][NQ];
-  const int slot = m.bid + m.grid * (m.wave >> 1);
-  const int rrow = slot;  // router row of an even wave
-  const int sp = slot;    // shared pair of an odd wave
+  u32x4 sv[NQ];
+  const int rrow = m.bid + m.grid * (m.wave >> 1);  // router row of an even wave
+  const int sp = m.bid;                              // shared pair of the odd waves
+  const int role = m.wave >> 1;                      // odd waves: gate 2sp, up 2sp, gate 2sp+1, up 2sp+1
   const bool router_wave = !(m.wave & 1) && rrow < ROWS;
   const bool shared_wave = (m.wave & 1) && sp < S::SI / 2;
   if (router_wave) {
@@ -840,22 +901,15 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
 #pragma unroll
     for (int j = 0; j < NJ; ++j) wv[j] = ldf_at(w, (uint32_t)min(64 * j + m.lane, H - 1) * 4u);
   } else if (shared_wave) {
+    const uint16_t* w = ((role & 1) ? Ly.sup : Ly.sgate) + (size_t)(2 * sp + (role >> 1)) * H;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const uint16_t* g = Ly.sgate + (size_t)(2 * sp + r) * H;
-      const uint16_t* u = Ly.sup + (size_t)(2 * sp + r) * H;
-#pragma unroll
-      for (int j = 0; j < NQ; ++j) {
-        const uint32_t off = (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u;
-        gv[r][j] = ldq_at(g, off);
-        uv[r][j] = ldq_at(u, off);
-      }
-    }
+    for (int j = 0; j < NQ; ++j) sv[j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, QH - 1) * 16u);
   }
   f32x4 w0, w1;
   norm_weights<S>(m, Ly.post_norm, w0, w1);
   poll_words<(H / 2 + kMT - 1) / kMT>(m, H / 2, Span{Ly.x_attn}, reinterpret_cast<uint32_t*>(m.xa));
   norm_row<S>(m, m.xa, w0, w1, m.a.eps);
+  trace_mark(kMarkRouterNormed);
   if (router_wave) {
     const uint16_t* xe = reinterpret_cast<const uint16_t*>(m.xn);
     float acc = 0.0f;
@@ -870,28 +924,20 @@ __device__ __forceinline__ void phase_router(const MegaArgs* pa, uint32_t tag, c
     v += lane_down<2>(v);
     if (m.lane == 0) word_store(Ly.x_router + rrow, fbits(v), m.tag);
   } else if (shared_wave) {
+    Quad acc;
+    quad_zero(acc);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+      if (QH % 64 == 0 || m.lane + 64 * j < QH) quad_acc(acc, m.xn[m.lane + 64 * j], sv[j]);
+    const float v = rbf(quad_tree<64>(acc));
+    if (m.lane == 0) m.misc->scalars[role] = v;
+  }
+  __syncthreads();
+  if (m.wave == 1 && m.lane == 0 && sp < S::SI / 2) {
     uint16_t t[2];
-    float xl[NQ][4], xh[NQ][4];
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      const u32x4 xq = (QH % 64 == 0 || m.lane + 64 * j < QH) ? m.xn[m.lane + 64 * j] : u32x4{0u, 0u, 0u, 0u};
-      quad_unpack(xq, xl[j], xh[j]);
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      Quad ga, ua;
-      quad_zero(ga);
-      quad_zero(ua);
-#pragma unroll
-      for (int j = 0; j < NQ; ++j)
-        if (QH % 64 == 0 || m.lane + 64 * j < QH) {
-          quad_acc_f(ga, xl[j], xh[j], gv[r][j]);
-          quad_acc_f(ua, xl[j], xh[j], uv[r][j]);
-        }
-      const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
-      t[r] = f2bf(rbf(silu(gb)) * ub);
-    }
-    if (m.lane == 0) word_store(Ly.x_shared + sp, pack_bf(t[0], t[1]), m.tag);
+    for (int r = 0; r < 2; ++r) t[r] = f2bf(rbf(silu(m.misc->scalars[2 * r])) * m.misc->scalars[2 * r + 1]);
+    word_store(Ly.x_shared + sp, pack_bf(t[0], t[1]), m.tag);
   }
 }
 
@@ -1062,6 +1108,7 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
   poll_words<(S::E + 1 + kMT - 1) / kMT>(m, S::E + 1, Span{Ly.x_router},
                                           reinterpret_cast<uint32_t*>(m.misc->logits));
   select_experts<S>(m);
+  trace_mark(kMarkSelected);
   // every block ranks the same logits; block 0 reports the layer's choice
   if (m.bid == 0 && m.tid < S::K) G(m.a.ids_out)[l * S::K + m.tid] = m.misc->ids[m.tid];
   const int p = m.gw;
@@ -1107,6 +1154,7 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
     }
     if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
   }
+  trace_mark(kMarkGateUpDone);
   // the down-projection rows of the selected experts, once this wave's
   // outputs are out (issued earlier, they hold the compute above behind the
   // memory queue); they land during the exchange into the down phase
@@ -1144,6 +1192,7 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
     m.vec[RP + m.tid] = pack_bf(f2bf(lo2f(t) * gate), f2bf(hi2f(t) * gate));
   }
   __syncthreads();
+  trace_mark(kMarkDownStaged);
   const int half = m.lane >> 5, r32 = m.lane & 31;
   const int fw = m.wave;
   const int prow = m.bid + m.grid * fw;
@@ -1152,18 +1201,17 @@ __device__ __forceinline__ void phase_down(const MegaArgs* pa, uint32_t tag, con
     const CQ35_LDS uint32_t* wr = st + (half ? D::B_R : D::A_R) + r32;
     const CQ35_LDS uint32_t* ws = st + (half ? D::B_S : D::A_S) + r32;
     float lo = 0.0f, hi = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[r32 + 32 * j], wr[32 * j]);
+    pair_chain_lds<NJ>(lo, hi, m.vec + r32, wr);
     const float routed_v = tree32_lanes(lo + hi);
     float slo = 0.0f, shi = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NSJ; ++j) pair_acc(slo, shi, m.vec[RP + r32 + 32 * j], ws[32 * j]);
+    pair_chain_lds<NSJ>(slo, shi, m.vec + RP + r32, ws);
     const float shared_v = tree32_lanes(slo + shi);
     const int row = 2 * prow + half;
     const uint16_t out = bf_add(f2bf(routed_v + bf2f(m.xa[row])), f2bf(shared_v));
     const uint16_t other = (uint16_t)__shfl_down((int)out, 32, 64);
     if (m.lane == 0) word_store(Ly.x_out + prow, pack_bf(out, other), m.tag);
   }
+  trace_mark(kMarkDownDone);
   // the next layer's first projection pairs, once this block's outputs are
   // out (issuing them earlier stalls the compute above behind the memory
   // queue): they stream during the next exchange
@@ -2324,6 +2372,9 @@ __global__ __launch_bounds__(kMT) void k_decode_step(const MegaArgs* __restrict_
   for (int l = 0; l < L; ++l) {
     const MegaLayer* ly = layers + l;
     const int tb = l * kTraceLayerSlots;  // phase p: done at tb + 2p, inputs in at tb + 2p + 1
+#ifdef CQ35_PHASE_TRACE
+    if (threadIdx.x == 0) misc->tbase = tb;
+#endif
     trace_slot(tb + 1);
     phase_project<S>(pa, tag, ly, l, pr);
     trace_max(tb + 0);

@@ -830,7 +830,7 @@ bool grid_fits(int grid) {
   return S::VH <= grid && std::max(rows_lin, rows_full) / 2 <= kPairsA * nw && S::H / 2 <= (int64_t)(kMW / 2) * grid &&
          S::H / 2 <= (int64_t)DownLayout<S>::WAVES * grid &&
          S::K * S::I / 2 <= nw && S::E + 1 <= (int64_t)(kMW / 2) * grid &&
-         S::SI / 2 <= (int64_t)(kMW / 2) * grid && S::H / 2 <= nw;
+         S::SI / 2 <= grid && S::H / 2 <= nw;
 }
 
 int mega_kind(const cq35_config& c, int grid) {
