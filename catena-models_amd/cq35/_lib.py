@@ -71,7 +71,8 @@ def load():
                                  ctypes.POINTER(ctypes.c_float)], None),
         "cq35_device_numeric": ([ctypes.c_int, P, P, I64], ctypes.c_int),
         "cq35_device_gemv": ([P, P, I64, I64, ctypes.c_int, P], ctypes.c_int),
-        "cq35_device_matrix_gemm": ([P, P, I64, I64, I64, P], ctypes.c_int),
+        "cq35_device_matrix_gemm": ([P, P, P, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P],
+                                    ctypes.c_int),
         "cq35_step_batch": ([ctypes.POINTER(P), P, P, I64, P], ctypes.c_int),
         "cq35_gguf_config": ([ctypes.c_char_p, PC], ctypes.c_int),
         "cq35_gguf_validate": ([ctypes.c_char_p, PC], ctypes.c_int),

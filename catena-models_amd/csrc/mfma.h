@@ -128,6 +128,183 @@ __global__ __launch_bounds__(64 * kMWaves) void k_mproject(const uint16_t* __res
   }
 }
 
+// k_mproject's products with both operands staged through LDS, for cols a
+// multiple of 128 (an even number of 64-column steps; other widths run
+// k_mproject): block tile 128 tokens x 64 weight rows (wave w: tokens
+// [32 w, +32) x the 64 rows, as k_mproject), K staged 64 columns per step,
+// so a weight fragment is fetched
+// once per block instead of once per wave. Global loads run two steps ahead
+// of the multiplies (two register sets, three LDS buffers, one barrier per
+// step): a step's loads have two steps' MFMA work to arrive in.
+// The k steps of 16 go to the same rotating partial sums in the same order
+// (step st of the row into part st % kParts, then the same tree), so every
+// output is bit-identical to k_mproject's. LDS rows are 8 pieces of 16 bytes
+// with piece p of row r stored in slot p ^ (r & 7): the 32 rows a fragment
+// read touches spread over all banks. Blocks sharing a weight tile (all
+// token tiles of one row tile) are placed on one XCD (block b runs on XCD
+// b mod 8), so the tile is read from HBM once and from that XCD's L2 after.
+constexpr int kGBK = 64;                // columns per LDS step
+constexpr int kGPieces = kGBK / 8;      // 16-byte pieces per staged row
+constexpr int kGTokens = kMBlockTokens;  // tokens per block tile
+constexpr int kGBufs = 3;               // LDS buffers
+
+__device__ __forceinline__ int gemm_slot(int row, int piece) { return row * kGPieces + (piece ^ (row & 7)); }
+
+inline int gemm_grid(int rows, int n) {
+  const int rt = (rows + kMRows - 1) / kMRows, tt = (n + kGTokens - 1) / kGTokens;
+  return ((rt + 7) / 8) * 8 * tt;
+}
+
+template <int kMode>
+struct GemmStage {
+  static constexpr int kMats = kMode == kBGate ? 2 : 1;
+  static constexpr int AP = kGTokens * kGPieces, BP = kMRows * kGPieces;  // pieces per stage
+  static constexpr int kThreads = 64 * kMWaves;
+  static constexpr int AL = AP / kThreads, BL = BP / kThreads;  // loads per thread per stage
+  static_assert(AP % kThreads == 0 && BP % kThreads == 0, "stage loads");
+  u32x4 a[AL], b[kMats][BL];
+};
+
+// The weight rows are the concatenation of up to four segments (matrix and
+// output buffer each; row r of segment s goes to out_s[t][r]), so the
+// projections of one input run as one launch; w2 (gate) and res (residual)
+// go with a single segment.
+template <int kMode>
+__global__ __launch_bounds__(64 * kMWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_mgemm(
+    const uint16_t* __restrict__ x, int n, int cols, Segments seg, const uint16_t* __restrict__ w2,
+    const uint16_t* __restrict__ res) {
+  const int rows = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  using St = GemmStage<kMode>;
+  constexpr int kParts = kMode == kBGate ? 2 : 4;
+  constexpr int kMats = St::kMats, AP = St::AP, BP = St::BP, AL = St::AL, BL = St::BL;
+  constexpr int kThreads = St::kThreads;
+  __shared__ u32x4 sa[kGBufs][AP];
+  __shared__ u32x4 sb[kGBufs][kMats][BP];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tt = (n + kGTokens - 1) / kGTokens;
+  const int b = blockIdx.x, xcd = b & 7, r = b >> 3;
+  const int tile_t = r % tt, tile_r = (r / tt) * 8 + xcd;
+  const int r0 = tile_r * kMRows;
+  if (r0 >= rows) return;  // uniform per block
+  const int tb = tile_t * kGTokens;
+  // this thread's pieces of a stage: piece p = tid % 8 of rows tid / 8 +
+  // 32 i (clamped rows); their LDS slots are slot0 + 256 i
+  static_assert(kThreads % (8 * kGPieces) == 0, "one swizzle per thread");
+  const int p8 = threadIdx.x % kGPieces, row8 = threadIdx.x / kGPieces;
+  const int slot0 = gemm_slot(row8, p8);
+  constexpr int kRowStep = kThreads / kGPieces;
+  const uint16_t* ga[AL];
+  const uint16_t* gb[kMats][BL];
+#pragma unroll
+  for (int i = 0; i < AL; ++i) ga[i] = x + (size_t)min(tb + row8 + kRowStep * i, n - 1) * cols + 8 * p8;
+#pragma unroll
+  for (int i = 0; i < BL; ++i) {
+    int local;
+    const int sg = segment_of(seg, min(r0 + row8 + kRowStep * i, rows - 1), &local);
+    const size_t off = (size_t)local * cols + 8 * p8;
+    gb[0][i] = segment_w(seg, sg) + off;
+    if (kMode == kBGate) gb[kMats - 1][i] = w2 + off;
+  }
+  const int nstage = (cols + kGBK - 1) / kGBK;
+  // fetch and store run unconditionally (a step past the end reloads the
+  // last one into a buffer nobody reads), so the loads in flight at each
+  // store are the same on every path and the wait before it can leave the
+  // newer set outstanding
+  auto fetch = [&](int s, St& v) {
+    const int k0 = min(s, nstage - 1) * kGBK;
+#pragma unroll
+    for (int i = 0; i < AL; ++i) v.a[i] = *reinterpret_cast<const u32x4*>(ga[i] + k0);
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int i = 0; i < BL; ++i) v.b[mi][i] = *reinterpret_cast<const u32x4*>(gb[mi][i] + k0);
+  };
+  auto store = [&](int s, const St& v) {
+    const int buf = s % kGBufs;
+#pragma unroll
+    for (int i = 0; i < AL; ++i) sa[buf][slot0 + kRowStep * kGPieces * i] = v.a[i];
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int i = 0; i < BL; ++i) sb[buf][mi][slot0 + kRowStep * kGPieces * i] = v.b[mi][i];
+  };
+  f32x16_t acc[kParts][kMats][2];
+#pragma unroll
+  for (int p = 0; p < kParts; ++p)
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi) acc[p][mi][0] = acc[p][mi][1] = f32x16_t{};
+  const int arow = 32 * wave + (lane & 31), half = lane >> 5;
+  const bool active = tb + 32 * wave < n;  // uniform per wave
+  // one step: all of its fragments first, then the MFMAs (step k of the
+  // stage into part k % kParts)
+  auto compute = [&](int s) {
+    const int buf = s % kGBufs;
+    if (!active) return;
+    u32x4 av[kGBK / 16], bv[kGBK / 16][kMats][2];
+#pragma unroll
+    for (int k = 0; k < kGBK / 16; ++k) {
+      const int piece = 2 * k + half;
+      av[k] = sa[buf][gemm_slot(arow, piece)];
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) bv[k][mi][h] = sb[buf][mi][gemm_slot(32 * h + (lane & 31), piece)];
+    }
+#pragma unroll
+    for (int k = 0; k < kGBK / 16; ++k)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[k % kParts][mi][h] = mfma32(av[k], bv[k][mi][h], acc[k % kParts][mi][h]);
+  };
+  St X, Y;  // register sets: stage s + 1 in flight in one while stage s + 2 is issued into the other
+  fetch(0, X);
+  fetch(1, Y);
+  store(0, X);
+  __syncthreads();
+  for (int s = 0; s < nstage; s += 2) {  // nstage is even
+    fetch(s + 2, X);
+    compute(s);
+    store(s + 1, Y);  // buffer (s + 1) % 3 was last read at step s - 2
+    __syncthreads();
+    fetch(s + 3, Y);
+    compute(s + 1);
+    store(s + 2, X);
+    __syncthreads();
+  }
+  if (!active) return;
+#pragma unroll
+  for (int span = 1; span < kParts; span *= 2)
+#pragma unroll
+    for (int p = 0; p + span < kParts; p += 2 * span)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) acc[p][mi][h] += acc[p + span][mi][h];
+  const int t0 = tb + 32 * wave;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int row = r0 + 32 * h + (lane & 31);
+    if (row >= rows) continue;
+    int local;
+    const int sg = segment_of(seg, row, &local);
+    uint16_t* out = segment_out(seg, sg);
+    const int srows = sg == 0 ? seg.rows[0] : sg == 1 ? seg.rows[1] : sg == 2 ? seg.rows[2] : seg.rows[3];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int t = t0 + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+      if (t >= n) continue;
+      const size_t o = (size_t)t * srows + local;
+      const float v = acc[0][0][h][rr];
+      uint16_t y;
+      if (kMode == kBPlain) y = f2bf(v);
+      else if (kMode == kBResidual) y = bf_add(f2bf(v), res[o]);
+      else y = bf_mul(f2bf(silu(rbf(v))), f2bf(acc[0][kMats - 1][h][rr]));
+      out[o] = y;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- experts
 //
 // Grouped expert projections (the reference's grouped routed/shared expert

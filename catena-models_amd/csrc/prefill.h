@@ -22,6 +22,7 @@ namespace cq35 {
 
 constexpr int kBTokens = 8;   // tokens per wave sharing each weight quad
 constexpr int kBChunk = 256;  // tokens per chunk (buffer rows)
+constexpr int kMChunk = 1024;  // tokens per chunk with matrix-core components
 
 __device__ __forceinline__ void b256_acc(float (&a)[4], const u32x4& x, const u32x4& w) {
   a[0] = (a[0] + lo2f(x.x) * lo2f(w.x)) + hi2f(x.x) * hi2f(w.x);
@@ -344,6 +345,58 @@ __global__ __launch_bounds__(kBlock) void k_brouter(const uint16_t* __restrict__
   v += lane_down<4>(v);
   v += lane_down<2>(v);
   if (lane == 0 && row < rows) logits[(size_t)t * rows + row] = v;
+}
+
+// k_brouter's logits with each weight row read once per 16 tokens: wave w of
+// block (row group, token group) keeps rows 16 rg + 2 w and + 1 in registers
+// (lane l: elements l + 64 k), the group's 16 token rows are staged in LDS,
+// and every (row, token) sum runs in k_brouter's order (each lane's chain
+// over k, then the same tree), so the logits are bit-identical. cols a
+// multiple of 64, at most 2048.
+constexpr int kRouterTokens = 16;
+constexpr int kRouterRows = 16;  // 2 per wave, 8 waves
+template <int KJ>  // cols / 64
+__global__ __launch_bounds__(512) void k_brouter_shared(const uint16_t* __restrict__ x, int n,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ shared_w, int experts,
+                                                        float* __restrict__ logits) {
+  constexpr int cols = 64 * KJ;
+  __shared__ uint16_t xs[kRouterTokens][cols];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = experts + 1;
+  const int t0 = blockIdx.y * kRouterTokens;
+  const int tn = min(kRouterTokens, n - t0);
+  float wv[2][KJ];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int rc = min(blockIdx.x * kRouterRows + 2 * wave + r, rows - 1);
+    const float* wr = rc < experts ? w + (size_t)rc * cols : shared_w;
+#pragma unroll
+    for (int k = 0; k < KJ; ++k) wv[r][k] = wr[lane + 64 * k];
+  }
+  constexpr int pieces = cols / 8;
+  for (int i = threadIdx.x; i < tn * pieces; i += blockDim.x) {
+    const int t = i / pieces, p = i - t * pieces;
+    reinterpret_cast<u32x4*>(&xs[t][0])[p] = ldq(x + (size_t)(t0 + t) * cols, p);
+  }
+  __syncthreads();
+  for (int t = 0; t < tn; ++t) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KJ; ++k)
+        acc += bf2f(xs[t][lane + 64 * k]) * wv[r][k];
+      float v = acc + lane_down<1>(acc);
+      v += lane_down<32>(v);
+      v += lane_down<16>(v);
+      v += lane_down<8>(v);
+      v += lane_down<4>(v);
+      v += lane_down<2>(v);
+      const int row = blockIdx.x * kRouterRows + 2 * wave + r;
+      if (lane == 0 && row < rows) logits[(size_t)(t0 + t) * rows + row] = v;
+    }
+  }
 }
 
 // Top-k of each token's routed logits by the reference's rank,

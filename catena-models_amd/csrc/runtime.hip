@@ -775,6 +775,7 @@ struct cq35_session {
   int *pf_eoff = nullptr, *pf_order = nullptr;    // matrix-core experts: buckets
   int* pf_ids = nullptr;
   int pf_attn_tokens = 0;  // tokens per staged-attention launch (scratch rows)
+  int pf_rows = 0;         // token rows of the chunk buffers
   int matrix = 0;          // CQ35_MATRIX_* components of multi-token calls on MFMA
   int64_t split_keys = CQ35_SPLIT_KEYS_DEFAULT;  // decode attention splits above this many keys
   // kernel timing
@@ -1344,12 +1345,15 @@ const char* prefill_unsupported(const cq35_model& m) {
   return nullptr;
 }
 
-// Chunk buffers of the batched prefill (kBChunk token rows each).
+// Chunk buffers of the batched prefill: kBChunk token rows, or kMChunk when
+// the session has matrix-core components selected at its first multi-token
+// call (their expert weights are then streamed once per kMChunk tokens).
 int setup_prefill(cq35_session* s) {
   if (s->pf_ready) return CQ35_OK;
   const Dims& d = s->model->d;
   const cq35_config& c = s->model->cfg;
-  const int64_t m = kBChunk, VH = c.value_heads;
+  const int64_t m = s->matrix ? kMChunk : kBChunk, VH = c.value_heads;
+  s->pf_rows = (int)m;
   int rc = CQ35_OK;
   auto check = [&](int r) { if (r && !rc) rc = r; };
   check(dalloc(s, &s->pf_h, m * d.H));
@@ -1397,19 +1401,42 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
   const uint64_t* params = s->d_params;
   enqueue_shadow(s, true);
   int last_rows = 1;
-  for (int64_t c0 = 0; c0 < n; c0 += kBChunk) {
-    const int rows_n = (int)std::min<int64_t>(kBChunk, n - c0);
+  // The chunk size changes no result (every per-token operation is
+  // independent of the other rows, the scan carries its state in the shadow),
+  // so the matrix-core components take larger chunks when the buffers allow.
+  const int64_t chunk = s->matrix ? s->pf_rows : std::min<int64_t>(kBChunk, s->pf_rows);
+  for (int64_t c0 = 0; c0 < n; c0 += chunk) {
+    const int rows_n = (int)std::min<int64_t>(chunk, n - c0);
     const int first = (int)c0;
     const unsigned tiles = (unsigned)((rows_n + 4 * kBTokens - 1) / (4 * kBTokens));
     L(KC_EMBED, k_bembed, dim3(rows_n), dim3(kBlock), 0, params, first, (const uint16_t*)Wt(0), H,
       s->pf_h, c0 + rows_n == n ? s->d_best : (unsigned long long*)nullptr);
     // matrix-core projections when selected (K a multiple of the MFMA step)
     const bool mp = (s->matrix & CQ35_MATRIX_PROJECTIONS) != 0;
+    // matrix-core projections: LDS-staged tiles for widths of whole 128-column
+    // pairs of steps, the direct kernel (same order) for other multiples of 16
     const unsigned mtiles = (unsigned)((rows_n + kMBlockTokens - 1) / kMBlockTokens);
-    auto mgrid = [&](int rows) { return dim3((unsigned)((rows + kMRows - 1) / kMRows), mtiles); };
+    auto staged = [&](int cols) { return cols % (2 * kGBK) == 0; };
+    auto mgrid = [&](int rows, int cols) {
+      return staged(cols) ? dim3((unsigned)gemm_grid(rows, rows_n))
+                          : dim3((unsigned)((rows + kMRows - 1) / kMRows), mtiles);
+    };
+    // several projections of one input: one staged launch over their
+    // concatenated rows, else one launch each
+    auto project_all = [&](const uint16_t* x, int cols, const Segments& seg) {
+      if (mp && staged(cols)) {
+        L(KC_PREFILL_PROJECT, k_mgemm<kBPlain>, mgrid((int)seg_rows(seg), cols), dim3(64 * kMWaves), 0, x,
+          rows_n, cols, seg, (const uint16_t*)nullptr, (const uint16_t*)nullptr);
+        return true;
+      }
+      return false;
+    };
     auto project = [&](const uint16_t* x, int cols, const void* w, int rows, uint16_t* out) {
-      if (mp && cols % 16 == 0)
-        L(KC_PREFILL_PROJECT, k_mproject<kBPlain>, mgrid(rows), dim3(64 * kMWaves), 0, x, rows_n, cols,
+      if (mp && staged(cols))
+        L(KC_PREFILL_PROJECT, k_mgemm<kBPlain>, mgrid(rows, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
+          segments({{w, {out, rows}}}), (const uint16_t*)nullptr, (const uint16_t*)nullptr);
+      else if (mp && cols % 16 == 0)
+        L(KC_PREFILL_PROJECT, k_mproject<kBPlain>, mgrid(rows, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
           (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr, out);
       else
         L(KC_PREFILL_PROJECT, k_bproject<kBPlain>, dim3((unsigned)rows, tiles), dim3(kBlock), 0, x,
@@ -1418,8 +1445,11 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
     };
     auto residual_rows = [&](const uint16_t* x, int cols, const void* w, const uint16_t* res,
                              uint16_t* out) {
-      if (mp && cols % 16 == 0)
-        L(KC_PREFILL_PROJECT, k_mproject<kBResidual>, mgrid(H), dim3(64 * kMWaves), 0, x, rows_n, cols,
+      if (mp && staged(cols))
+        L(KC_PREFILL_PROJECT, k_mgemm<kBResidual>, mgrid(H, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
+          segments({{w, {out, H}}}), (const uint16_t*)nullptr, res);
+      else if (mp && cols % 16 == 0)
+        L(KC_PREFILL_PROJECT, k_mproject<kBResidual>, mgrid(H, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
           (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
       else
         L(KC_PREFILL_PROJECT, k_bproject<kBResidual>, dim3((unsigned)H, tiles), dim3(kBlock), 0, x,
@@ -1439,9 +1469,11 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
       const void* post_norm;
       if (is_full(c, l)) {
         uint16_t *qg = s->pf_a, *kraw = s->pf_b, *vraw = s->pf_c, *qr = s->pf_d, *ctx = s->pf_f;
-        project(s->pf_x, H, W(1), (int)(2 * d.QS), qg);
-        project(s->pf_x, H, W(2), (int)d.KVS, kraw);
-        project(s->pf_x, H, W(3), (int)d.KVS, vraw);
+        if (!project_all(s->pf_x, H, segments({{W(1), {qg, 2 * d.QS}}, {W(2), {kraw, d.KVS}}, {W(3), {vraw, d.KVS}}}))) {
+          project(s->pf_x, H, W(1), (int)(2 * d.QS), qg);
+          project(s->pf_x, H, W(2), (int)d.KVS, kraw);
+          project(s->pf_x, H, W(3), (int)d.KVS, vraw);
+        }
         L(KC_EMBED, k_brope, dim3(rows_n), dim3(kBlock), 0, params, first, (const float*)m.freq,
           (int)(d.R / 2), s->pf_rope);
         L(KC_PREPARE_FULL, k_full_prepare, dim3((unsigned)(d.Q + d.KVH), rows_n), dim3(kBlock), 0,
@@ -1463,13 +1495,16 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         post_norm = W(7);
         ffn = 8;
       } else {
-        uint16_t *qkv = s->pf_a, *z = s->pf_b, *alpha = s->pf_c, *beta = s->pf_c + (size_t)kBChunk * VH;
-        uint16_t *conv = s->pf_d, *qn = s->pf_e, *kn = s->pf_e + (size_t)kBChunk * d.KS;
+        uint16_t *qkv = s->pf_a, *z = s->pf_b, *alpha = s->pf_c, *beta = s->pf_c + (size_t)s->pf_rows * VH;
+        uint16_t *conv = s->pf_d, *qn = s->pf_e, *kn = s->pf_e + (size_t)s->pf_rows * d.KS;
         uint16_t *core = s->pf_f, *gated = s->pf_g;
-        project(s->pf_x, H, W(1), (int)d.QKV, qkv);
-        project(s->pf_x, H, W(2), (int)d.VS, z);
-        project(s->pf_x, H, W(3), VH, alpha);
-        project(s->pf_x, H, W(4), VH, beta);
+        if (!project_all(s->pf_x, H,
+                         segments({{W(1), {qkv, d.QKV}}, {W(2), {z, d.VS}}, {W(3), {alpha, VH}}, {W(4), {beta, VH}}}))) {
+          project(s->pf_x, H, W(1), (int)d.QKV, qkv);
+          project(s->pf_x, H, W(2), (int)d.VS, z);
+          project(s->pf_x, H, W(3), VH, alpha);
+          project(s->pf_x, H, W(4), VH, beta);
+        }
         const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
         L(KC_PREPARE_LINEAR, k_bprepare,
           dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), rows_n), dim3(kBlock), 0,
@@ -1496,9 +1531,20 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
       norm(s->pf_attn, post_norm, s->pf_x);
       if (c.moe) {
         const int E = (int)d.E, K = (int)d.K, I = (int)d.I, SI = (int)d.SI;
-        L(KC_ROUTER, k_brouter, dim3((unsigned)((E + 1 + 3) / 4), rows_n), dim3(kBlock), 0,
-          (const uint16_t*)s->pf_x, H, (const float*)W(ffn), (const float*)W(ffn + 4), E,
-          s->pf_logits);
+        const dim3 rgrid((unsigned)((E + kRouterRows) / kRouterRows),
+                         (unsigned)((rows_n + kRouterTokens - 1) / kRouterTokens));
+        auto router = [&](auto kernel) {
+          L(KC_ROUTER, kernel, rgrid, dim3(512), 0, (const uint16_t*)s->pf_x, rows_n, (const float*)W(ffn),
+            (const float*)W(ffn + 4), E, s->pf_logits);
+        };
+        if (H == 2048) router(k_brouter_shared<32>);
+        else if (H == 1024) router(k_brouter_shared<16>);
+        else if (H == 512) router(k_brouter_shared<8>);
+        else if (H == 256) router(k_brouter_shared<4>);
+        else
+          L(KC_ROUTER, k_brouter, dim3((unsigned)((E + 1 + 3) / 4), rows_n), dim3(kBlock), 0,
+            (const uint16_t*)s->pf_x, H, (const float*)W(ffn), (const float*)W(ffn + 4), E,
+            s->pf_logits);
         L(KC_ROUTER, k_bselect, dim3(rows_n), dim3(kBlock), (size_t)E * 4,
           (const float*)s->pf_logits, E, K, s->pf_ids, s->pf_probs,
           c0 + rows_n == n ? s->ids + l * d.K : (int*)nullptr);
@@ -1531,9 +1577,14 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         }
       } else {
         if (mp && H % 16 == 0)
-          L(KC_PREFILL_PROJECT, k_mproject<kBGate>, mgrid((int)d.I), dim3(64 * kMWaves), 0,
-            (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
-            (int)d.I, (const uint16_t*)nullptr, s->pf_act);
+          if (staged(H))
+            L(KC_PREFILL_PROJECT, k_mgemm<kBGate>, mgrid((int)d.I, H), dim3(64 * kMWaves), 0,
+              (const uint16_t*)s->pf_x, rows_n, H, segments({{W(ffn), {s->pf_act, d.I}}}),
+              (const uint16_t*)W(ffn + 1), (const uint16_t*)nullptr);
+          else
+            L(KC_PREFILL_PROJECT, k_mproject<kBGate>, mgrid((int)d.I, H), dim3(64 * kMWaves), 0,
+              (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
+              (int)d.I, (const uint16_t*)nullptr, s->pf_act);
         else
           L(KC_PREFILL_PROJECT, k_bproject<kBGate>, dim3((unsigned)d.I, tiles), dim3(kBlock), 0,
             (const uint16_t*)s->pf_x, rows_n, H, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1),
@@ -2331,26 +2382,47 @@ extern "C" int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t ro
   return CQ35_OK;
 }
 
-extern "C" int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, int64_t n, int64_t rows,
-                                       int64_t cols, uint16_t* out) {
+extern "C" int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, const uint16_t* w2,
+                                       const uint16_t* res, int64_t n, int64_t rows, int64_t cols, int mode,
+                                       int kernel, uint16_t* out) {
   if (!x || !w || !out || n <= 0 || rows <= 0 || cols <= 0 || cols % 16 || n > (1 << 20) ||
-      rows > (1 << 20) || cols > 65536)
+      rows > (1 << 20) || cols > 65536 || mode < kBPlain || mode > kBGate || kernel < 0 || kernel > 1 ||
+      (mode == kBGate && !w2) || (mode == kBResidual && !res))
     return fail(CQ35_EINVAL, "bad matrix GEMM shape");
-  uint16_t *dx = nullptr, *dw = nullptr, *dout = nullptr;
+  uint16_t *dx = nullptr, *dw = nullptr, *dw2 = nullptr, *dres = nullptr, *dout = nullptr;
   hipError_t e = hipMalloc(&dx, n * cols * 2);
   if (e == hipSuccess) e = hipMalloc(&dw, rows * cols * 2);
+  if (e == hipSuccess && mode == kBGate) e = hipMalloc(&dw2, rows * cols * 2);
+  if (e == hipSuccess && mode == kBResidual) e = hipMalloc(&dres, n * rows * 2);
   if (e == hipSuccess) e = hipMalloc(&dout, n * rows * 2);
   if (e == hipSuccess) e = hipMemcpy(dx, x, n * cols * 2, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(dw, w, rows * cols * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess && dw2) e = hipMemcpy(dw2, w2, rows * cols * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess && dres) e = hipMemcpy(dres, res, n * rows * 2, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    const dim3 grid((unsigned)((rows + kMRows - 1) / kMRows), (unsigned)((n + kMBlockTokens - 1) / kMBlockTokens));
-    k_mproject<kBPlain><<<grid, 64 * kMWaves>>>(dx, (int)n, (int)cols, dw, nullptr, (int)rows, nullptr, dout);
+    const int N = (int)n, R = (int)rows, C = (int)cols;
+    if (kernel == 0) {
+      const dim3 grid((unsigned)((rows + kMRows - 1) / kMRows), (unsigned)((n + kMBlockTokens - 1) / kMBlockTokens));
+      if (mode == kBPlain) k_mproject<kBPlain><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+      else if (mode == kBResidual) k_mproject<kBResidual><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+      else k_mproject<kBGate><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+    } else if (cols % (2 * kGBK) == 0) {
+      const dim3 grid((unsigned)gemm_grid(R, N));
+      const Segments one = segments({{dw, {dout, rows}}});
+      if (mode == kBPlain) k_mgemm<kBPlain><<<grid, 64 * kMWaves>>>(dx, N, C, one, dw2, dres);
+      else if (mode == kBResidual) k_mgemm<kBResidual><<<grid, 64 * kMWaves>>>(dx, N, C, one, dw2, dres);
+      else k_mgemm<kBGate><<<grid, 64 * kMWaves>>>(dx, N, C, one, dw2, dres);
+    } else {  // widths the staged tiles do not take run the direct kernel, as in the prefill
+      const dim3 grid((unsigned)((rows + kMRows - 1) / kMRows), (unsigned)((n + kMBlockTokens - 1) / kMBlockTokens));
+      if (mode == kBPlain) k_mproject<kBPlain><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+      else if (mode == kBResidual) k_mproject<kBResidual><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+      else k_mproject<kBGate><<<grid, 64 * kMWaves>>>(dx, N, C, dw, dw2, R, dres, dout);
+    }
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipMemcpy(out, dout, n * rows * 2, hipMemcpyDeviceToHost);
-  if (dx) hipFree(dx);
-  if (dw) hipFree(dw);
-  if (dout) hipFree(dout);
+  for (uint16_t* p : {dx, dw, dw2, dres, dout})
+    if (p) hipFree(p);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "device matrix GEMM: %s", hipGetErrorString(e));
   return CQ35_OK;
 }

@@ -259,11 +259,15 @@ int cq35_device_numeric(int op, const float* input, float* output, int64_t count
  * BF16 matrix: out[r] = bf16(tree_W(x . w_r)). Host arrays. */
 int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t cols,
                      int width, uint16_t* out);
-/* Device matrix-core product of the prefill projections over host arrays:
- * out[t][r] = bf16(sum_k x[t][k] w[r][k]) (MFMA accumulation order), x
- * [n][cols], w [rows][cols], cols a multiple of 16. */
-int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, int64_t n, int64_t rows,
-                            int64_t cols, uint16_t* out);
+/* Device matrix-core product of the prefill projections over host arrays,
+ * x [n][cols], w and w2 [rows][cols], res [n][rows], cols a multiple of 16:
+ * out[t][r] = epilogue(sum_k x[t][k] w[r][k]) in the MFMA accumulation order,
+ * mode 0 bf16(sum), 1 bf16(sum) (+) res, 2 bf16(silu(bf16 sum)) (x)
+ * bf16(sum over w2). kernel 0: direct fragment loads; 1: the LDS-staged
+ * tiles the prefill runs (the same order, so the same bits). */
+int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, const uint16_t* w2,
+                            const uint16_t* res, int64_t n, int64_t rows, int64_t cols, int mode,
+                            int kernel, uint16_t* out);
 
 #ifdef __cplusplus
 }

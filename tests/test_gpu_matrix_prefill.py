@@ -61,20 +61,30 @@ def shape(name):
     return cfg
 
 
+def to_bf(a):  # round to nearest even
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def device_gemm(x, w, w2, res, n, rows, cols, mode, kernel):
+    from cq35 import _lib
+    out = np.empty((n, rows), dtype=np.uint16)
+    ptr = lambda a: a.ctypes.data if a is not None else None
+    rc = _lib.load().cq35_device_matrix_gemm(ptr(x), ptr(w), ptr(w2), ptr(res), n, rows, cols, mode, kernel,
+                                             out.ctypes.data)
+    assert rc == 0
+    return out
+
+
+@pytest.mark.parametrize("kernel", [0, 1])
 @pytest.mark.parametrize("n,rows,cols", [(1, 1, 16), (37, 70, 48), (300, 130, 2048),
                                          (96, 32, 4096), (256, 1100, 512)])
-def test_matrix_gemm_against_f64(n, rows, cols):
-    from cq35 import _lib
-    say("matrix gemm", n, rows, cols)
+def test_matrix_gemm_against_f64(n, rows, cols, kernel):
+    say("matrix gemm", n, rows, cols, "kernel", kernel)
     rng = np.random.default_rng(rows + cols)
-    def to_bf(a):  # round to nearest even
-        u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
-        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     x = to_bf(rng.standard_normal((n, cols)))
     w = to_bf(rng.standard_normal((rows, cols)) * 0.05)
-    out = np.empty((n, rows), dtype=np.uint16)
-    rc = _lib.load().cq35_device_matrix_gemm(x.ctypes.data, w.ctypes.data, n, rows, cols, out.ctypes.data)
-    assert rc == 0
+    out = device_gemm(x, w, None, None, n, rows, cols, 0, kernel)
     xf = logits_f32(x).astype(np.float64).reshape(n, cols)
     wf = logits_f32(w).astype(np.float64).reshape(rows, cols)
     ref = xf @ wf.T
@@ -84,6 +94,26 @@ def test_matrix_gemm_against_f64(n, rows, cols):
     assert np.all(np.abs(y - ref) <= bound), float(np.max(np.abs(y - ref) - bound))
     rounded = logits_f32(to_bf(ref.astype(np.float32))).reshape(n, rows)
     assert np.mean(y == rounded) > 0.99
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("n,rows,cols", [(1, 1, 128), (37, 70, 256), (130, 200, 2048), (256, 64, 4224),
+                                         (300, 1100, 512), (33, 65, 48)])
+def test_staged_matrix_gemm_bit_identical(n, rows, cols, mode):
+    """The LDS-staged tiles the prefill runs (kernel 1) give the bits of the
+    direct-fragment kernel (kernel 0) in every epilogue: same k-step rotation
+    over the partial sums, same tree. Ragged token and row tails; widths that
+    are not whole 128-column pairs of steps (48) run the direct kernel in the
+    prefill too."""
+    say("staged matrix gemm", n, rows, cols, "mode", mode)
+    rng = np.random.default_rng(n * 7 + rows + cols + mode)
+    x = to_bf(rng.standard_normal((n, cols)))
+    w = to_bf(rng.standard_normal((rows, cols)) * 0.05)
+    w2 = to_bf(rng.standard_normal((rows, cols)) * 0.05) if mode == 2 else None
+    res = to_bf(rng.standard_normal((n, rows))) if mode == 1 else None
+    a = device_gemm(x, w, w2, res, n, rows, cols, mode, 0)
+    b = device_gemm(x, w, w2, res, n, rows, cols, mode, 1)
+    assert np.array_equal(a, b)
 
 
 @pytest.mark.parametrize("name,n", [("mini", 37), ("mini-moe", 37), ("mini-moe", 300)])
