@@ -322,7 +322,7 @@ def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: i
     import cq35
     cfg = cq35.preset(config)
     model = cq35.Model.synthetic(cfg, seed=seed)
-    capacity = context + steps + 8
+    capacity = context + 2 * steps + 16  # exact rounds, then as many matrix-core rounds
     tokens = synthetic_tokens(sessions * context + 1, cfg["vocab"])
     group, nxt = [], []
     for b in range(sessions):
@@ -337,6 +337,19 @@ def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: i
         nxt = cq35.decode_batch(group, nxt)
     device_sync()
     batched = time.perf_counter() - t0
+    # the same sessions with the products on MFMA (matrix-core projections
+    # selected on every session: tolerance-level, tests/test_gpu_batch_matrix.py)
+    for s in group:
+        s.set_matrix_prefill(s.MATRIX_PROJECTIONS)
+    mx_steps = steps
+    for _ in range(2):
+        nxt = cq35.decode_batch(group, nxt)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(mx_steps):
+        nxt = cq35.decode_batch(group, nxt)
+    device_sync()
+    matrix = time.perf_counter() - t0
     one = model.session(capacity)
     x = one.append_next_token(tokens[:context])
     for _ in range(2):
@@ -349,11 +362,18 @@ def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: i
     alone = time.perf_counter() - t0
     log(f"{sessions} {config} sessions: {sessions * steps / batched:.1f} tok/s aggregate "
         f"({batched / steps * 1e3:.3f} ms per round); one session {steps / alone:.1f} tok/s")
+    if mx_steps:
+        log(f"{sessions} {config} sessions, matrix-core products: {sessions * mx_steps / matrix:.1f} tok/s "
+            f"aggregate ({matrix / mx_steps * 1e3:.3f} ms per round)")
     return dict(config=config, sessions=sessions, context=context, steps=steps,
                 tokens_per_s=round(sessions * steps / batched, 1), ms_per_round=round(batched / steps * 1e3, 4),
                 single_session_tokens_per_s=round(steps / alone, 1),
                 path=("cq35_step_batch: weight-shared decode step (each layer's weights read once for all "
-                      "sessions' tokens, per-token arithmetic bit-identical to a session stepped alone)"))
+                      "sessions' tokens, per-token arithmetic bit-identical to a session stepped alone)"),
+                matrix_core=dict(steps=mx_steps,
+                                 tokens_per_s=round(sessions * mx_steps / matrix, 1) if mx_steps else None,
+                                 ms_per_round=round(matrix / mx_steps * 1e3, 4) if mx_steps else None,
+                                 path="the same step with its products on MFMA (tolerance-level)"))
 
 
 def main() -> int:

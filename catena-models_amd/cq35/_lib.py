@@ -73,7 +73,7 @@ def load():
         "cq35_device_gemv": ([P, P, I64, I64, ctypes.c_int, P], ctypes.c_int),
         "cq35_device_matrix_gemm": ([P, P, P, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P],
                                     ctypes.c_int),
-        "cq35_step_batch": ([ctypes.POINTER(P), P, P, I64, P], ctypes.c_int),
+        "cq35_step_batch": ([ctypes.POINTER(P), P, P, I64, P, P], ctypes.c_int),
         "cq35_gguf_config": ([ctypes.c_char_p, PC], ctypes.c_int),
         "cq35_gguf_validate": ([ctypes.c_char_p, PC], ctypes.c_int),
         "cq35_model_load_gguf": ([ctypes.c_char_p, ctypes.POINTER(P)], ctypes.c_int),

@@ -128,9 +128,12 @@ def weight_info(cfg: dict, index: int):
     return info
 
 
-def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int]) -> list:
+def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int], logits: bool = False):
     """One decode step for each session (cq35_step_batch): the same next
-    tokens as stepping them one by one, with their launches overlapped."""
+    tokens as stepping them one by one (dense sessions of one model and
+    capacity share each layer's weight pass; with matrix-core projections
+    selected on every session the products run on MFMA). With logits=True,
+    also returns the BF16 logits as a [sessions, vocab] uint16 array."""
     n = len(sessions)
     if n == 0:
         return []
@@ -147,7 +150,9 @@ def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int]) -> list:
     toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint64))
     starts = np.ascontiguousarray(np.asarray([s.position for s in sessions], dtype=np.int64))
     out = np.zeros(n, dtype=np.uint64)
-    rc = _lib.load().cq35_step_batch(handles, toks.ctypes.data, starts.ctypes.data, n, out.ctypes.data)
+    lg = np.empty((n, sessions[0].model.cfg["vocab"]), dtype=np.uint16) if logits else None
+    rc = _lib.load().cq35_step_batch(handles, toks.ctypes.data, starts.ctypes.data, n, out.ctypes.data,
+                                     lg.ctypes.data if logits else None)
     if rc != 0:
         if rc in (-3, -5):  # a step may have failed part-way: no session of the batch is trusted
             for s in sessions:
@@ -155,7 +160,8 @@ def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int]) -> list:
         check(rc)
     for s in sessions:
         s.position += 1
-    return [int(x) for x in out]
+    toks_out = [int(x) for x in out]
+    return (toks_out, lg) if logits else toks_out
 
 
 def gguf_config(path: str) -> dict:

@@ -305,6 +305,108 @@ __global__ __launch_bounds__(64 * kMWaves) __attribute__((amdgpu_waves_per_eu(2,
   }
 }
 
+// ------------------------------------------------- batched decode (skinny)
+//
+// The weight-shared batched decode step's products on MFMA (a session
+// option, like the prefill components): at most 32 tokens per tile, so the
+// work is a weight stream. Block = 32 weight rows x a 32-token tile; wave w
+// sums the columns [w cols/4, (w + 1) cols/4) into one accumulator, with two
+// batches of four k steps in flight (loads are unconditional: a batch past the
+// end reloads the last one, so every wait leaves the newer batch
+// outstanding); the four partial tiles are added as a tree through LDS
+// ((w0 + w1) + (w2 + w3)), then the epilogue. cols % 512 == 0.
+constexpr int kSkSplit = 4;  // waves per block
+constexpr int kSkBatch = 4;  // k steps per load batch
+enum { kSArgmax = 3 };       // mode: vocabulary head, bf16 logits and each token's (value, first index) max
+
+template <int kMode>
+__global__ __launch_bounds__(64 * kSkSplit) void k_mskinny(const uint16_t* __restrict__ x, int n, int cols,
+                                                           Segments seg, const uint16_t* __restrict__ w2,
+                                                           const uint16_t* __restrict__ res,
+                                                           unsigned long long* __restrict__ best) {
+  constexpr int kMats = kMode == kBGate ? 2 : 1;
+  __shared__ f32x16_t part[kSkSplit - 1][kMats][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  const int r0 = blockIdx.x * 32, t0 = blockIdx.y * 32;
+  const int kq = 8 * (lane >> 5);
+  const int qcols = cols / kSkSplit, c0 = wave * qcols;
+  int local;
+  const int sg = segment_of(seg, min(r0 + (lane & 31), rows - 1), &local);
+  const uint16_t* wb[kMats];
+  wb[0] = segment_w(seg, sg) + (size_t)local * cols + c0 + kq;
+  if (kMode == kBGate) wb[kMats - 1] = w2 + (size_t)local * cols + c0 + kq;
+  const uint16_t* xa = x + (size_t)min(t0 + (lane & 31), n - 1) * cols + c0 + kq;
+  const int steps = qcols / 16;  // a multiple of 2 kSkBatch
+  struct Set {
+    u32x4 a[kSkBatch], b[kMats][kSkBatch];
+  };
+  auto load = [&](int s, Set& v) {
+    const int k = 16 * min(s, steps - kSkBatch);
+#pragma unroll
+    for (int j = 0; j < kSkBatch; ++j) {
+      v.a[j] = *reinterpret_cast<const u32x4*>(xa + k + 16 * j);
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) v.b[mi][j] = *reinterpret_cast<const u32x4*>(wb[mi] + k + 16 * j);
+    }
+  };
+  f32x16_t acc[kMats];
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi) acc[mi] = f32x16_t{};
+  auto mult = [&](const Set& v) {
+#pragma unroll
+    for (int j = 0; j < kSkBatch; ++j)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) acc[mi] = mfma32(v.a[j], v.b[mi][j], acc[mi]);
+  };
+  Set P, Q;
+  load(0, P);
+  for (int s = 0; s < steps; s += 2 * kSkBatch) {
+    load(s + kSkBatch, Q);
+    mult(P);
+    load(s + 2 * kSkBatch, P);
+    mult(Q);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi) part[wave - 1][mi][lane] = acc[mi];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi) acc[mi] = (acc[mi] + part[0][mi][lane]) + (part[1][mi][lane] + part[2][mi][lane]);
+  const int row = r0 + (lane & 31);
+  int lr;
+  const int os = segment_of(seg, min(row, rows - 1), &lr);
+  uint16_t* out = segment_out(seg, os);
+  const int srows = os == 0 ? seg.rows[0] : os == 1 ? seg.rows[1] : os == 2 ? seg.rows[2] : seg.rows[3];
+#pragma unroll
+  for (int rr = 0; rr < 16; ++rr) {
+    const int t = t0 + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+    const bool ok = t < n && row < rows;
+    const size_t o = (size_t)t * srows + lr;
+    const float v = acc[0][rr];
+    uint16_t y = 0;
+    if (ok) {
+      if (kMode == kBPlain || kMode == kSArgmax) y = f2bf(v);
+      else if (kMode == kBResidual) y = bf_add(f2bf(v), res[o]);
+      else y = bf_mul(f2bf(silu(rbf(v))), f2bf(acc[kMats - 1][rr]));
+      out[o] = y;
+    }
+    if (kMode == kSArgmax) {
+      // the (value, first index) maximum of this token over the tile's 32
+      // rows (lanes of one half), then one atomic per token and tile
+      unsigned long long key = ok ? logit_key(y, (uint32_t)row) : 0ull;
+#pragma unroll
+      for (int d = 16; d >= 1; d >>= 1) {
+        const unsigned long long o2 = __shfl_xor(key, d, 64);
+        key = o2 > key ? o2 : key;
+      }
+      if ((lane & 31) == 0 && t < n && key) atomicMax(best + t, key);
+    }
+  }
+}
+
 // ---------------------------------------------------------------- experts
 //
 // Grouped expert projections (the reference's grouped routed/shared expert

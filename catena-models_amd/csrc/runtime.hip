@@ -1913,18 +1913,19 @@ struct BatchWorkspace {
   uint16_t* logits = nullptr;
   float *rope = nullptr, *scratch = nullptr;
   int stride = 0;
-  hipGraph_t graph[kMaxSessions + 1] = {};
-  hipGraphExec_t exec[kMaxSessions + 1] = {};
+  hipGraph_t graph[2][kMaxSessions + 1] = {};      // [matrix-core products][sessions]
+  hipGraphExec_t exec[2][kMaxSessions + 1] = {};
   std::vector<void*> allocs;
 };
 
 void destroy_batch(BatchWorkspace* b) {
   if (!b) return;
   if (b->stream) hipStreamSynchronize(b->stream);
-  for (int i = 0; i <= kMaxSessions; ++i) {
-    if (b->exec[i]) hipGraphExecDestroy(b->exec[i]);
-    if (b->graph[i]) hipGraphDestroy(b->graph[i]);
-  }
+  for (int k = 0; k < 2; ++k)
+    for (int i = 0; i <= kMaxSessions; ++i) {
+      if (b->exec[k][i]) hipGraphExecDestroy(b->exec[k][i]);
+      if (b->graph[k][i]) hipGraphDestroy(b->graph[k][i]);
+    }
   for (void* p : b->allocs) hipFree(p);
   if (b->h_rows) hipHostFree(b->h_rows);
   if (b->h_best) hipHostFree(b->h_best);
@@ -1992,8 +1993,21 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
   return CQ35_OK;
 }
 
-// Weight-shared GEMV launches (k_ws32 / k_ws64 / k_ws256_swiglu) over B tokens.
-void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t cols, unsigned long long* best) {
+// Matrix-core products of the batched step (k_mskinny) take widths that are
+// multiples of 512.
+bool skinny_ok(int64_t cols) { return cols % (16 * kSkSplit * 2 * kSkBatch) == 0; }
+dim3 skinny_grid(int64_t rows, int B) { return dim3((unsigned)((rows + 31) / 32), (unsigned)((B + 31) / 32)); }
+
+// Weight-shared GEMV launches (k_ws32 / k_ws64 / k_ws256_swiglu) over B
+// tokens, or with mx the matrix-core products where the width allows.
+void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t cols, unsigned long long* best,
+          bool mx = false) {
+  if (mx && skinny_ok(cols)) {
+    const dim3 grid = skinny_grid(seg_rows(seg), B), block(64 * kSkSplit);
+    if (best) k_mskinny<kSArgmax><<<grid, block, 0, st>>>(x, B, (int)cols, seg, nullptr, nullptr, best);
+    else k_mskinny<kBPlain><<<grid, block, 0, st>>>(x, B, (int)cols, seg, nullptr, nullptr, nullptr);
+    return;
+  }
   const int groups = (B + kBatchNB - 1) / kBatchNB;
   const int row_blocks = (int)((seg_rows(seg) + 31) / 32);
   const size_t lds = (size_t)kBatchNB * std::min<int64_t>(cols, kBatchChunk) * 4;
@@ -2002,7 +2016,17 @@ void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t
   else k_ws32<false, 8><<<grid, block, lds, st>>>(x, B, groups, seg, (int)cols, best);
 }
 void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows, int64_t cols, const uint16_t* res,
-          uint16_t* out) {
+          uint16_t* out, bool mx = false) {
+  if (mx && skinny_ok(cols)) {
+    const Segments one = segments({{w, {out, rows}}});
+    if (res)
+      k_mskinny<kBResidual><<<skinny_grid(rows, B), dim3(64 * kSkSplit), 0, st>>>(x, B, (int)cols, one, nullptr, res,
+                                                                                 nullptr);
+    else
+      k_mskinny<kBPlain><<<skinny_grid(rows, B), dim3(64 * kSkSplit), 0, st>>>(x, B, (int)cols, one, nullptr, nullptr,
+                                                                              nullptr);
+    return;
+  }
   const int groups = (B + kBatchNB - 1) / kBatchNB;
   const int row_blocks = (int)((rows + 15) / 16);
   const size_t lds = (size_t)kBatchNB * std::min<int64_t>(cols, kBatchChunk) * 4;
@@ -2012,8 +2036,9 @@ void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows,
 
 // The batched decode step's launch sequence (dense models): every layer of
 // enqueue_token for B sessions, GEMVs weight-shared, per-session kernels with
-// one grid row per session.
-void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
+// one grid row per session. mx: the products on MFMA (k_mskinny) where the
+// width allows.
+void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
   const cq35_config& c = m->cfg;
   const Dims& d = m->d;
   hipStream_t st = b->stream;
@@ -2035,7 +2060,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
     const void* post_norm;
     if (is_full(c, l)) {
       ws32(st, b->x, B, segments({{W(1), {b->qg, 2 * d.QS}}, {W(2), {b->kraw, d.KVS}}, {W(3), {b->vraw, d.KVS}}}),
-           d.H, nullptr);
+           d.H, nullptr, mx);
       k_full_prepare<<<dim3((unsigned)(d.Q + d.KVH), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->qg, (const uint16_t*)b->kraw, (const uint16_t*)b->vraw, (const float*)b->rope,
           (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
@@ -2047,7 +2072,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
       k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(128), 0, st>>>(
           (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
           (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
-      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn);
+      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, mx);
       post_norm = W(7);
       ffn = 8;
     } else {
@@ -2056,7 +2081,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
       ws32(st, b->x, B,
            segments({{W(1), {b->qkv, d.QKV}}, {W(2), {b->z, d.VS}}, {W(3), {alpha, c.value_heads}},
                      {W(4), {beta, c.value_heads}}}),
-           d.H, nullptr);
+           d.H, nullptr, mx);
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       k_linear_prepare<<<dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->qkv, (uint16_t*)nullptr, conv_base, (const uint64_t*)nullptr, 0, (const float*)W(9),
@@ -2068,12 +2093,15 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
           (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
       k_gated_norm<<<dim3((unsigned)c.value_heads, (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->core, (const uint16_t*)b->z, (const float*)W(7), c.value_dim, c.eps, b->gated);
-      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn);
+      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn, mx);
       post_norm = W(10);
       ffn = 11;
     }
     norm(b->attn, post_norm, b->x);
-    {
+    if (mx && skinny_ok(d.H)) {
+      k_mskinny<kBGate><<<skinny_grid(d.I, B), dim3(64 * kSkSplit), 0, st>>>(
+          b->x, B, (int)d.H, segments({{W(ffn), {b->act, d.I}}}), (const uint16_t*)W(ffn + 1), nullptr, nullptr);
+    } else {
       const int groups = (B + kBatchNBDual - 1) / kBatchNBDual;
       const int row_blocks = (int)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate));
       k_ws256_swiglu<<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock),
@@ -2081,18 +2109,18 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B) {
                                                              (const uint16_t*)W(ffn + 1), (int)d.I, (int)d.H,
                                                              b->act);
     }
-    ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h);
+    ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h, mx);
     base += layer_tensors(c, l);
   }
   const int64_t total = weight_count(c);
   norm(b->h, Wt(total - 2), b->x);
-  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best);
+  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best, mx);
 }
 
 // One weight-shared decode step for `count` dense sessions of one model and
 // capacity (checked by the caller): tokens[i] at starts[i] of sessions[i].
 int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts, int count,
-                      uint64_t* next_tokens) {
+                      uint64_t* next_tokens, uint16_t* logits) {
   cq35_model* m = sessions[0]->model;
   std::lock_guard<std::mutex> hold(m->batch_lock);
   HIP_TRY(hipSetDevice(m->device));
@@ -2105,23 +2133,29 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
     b->h_rows->token[i] = tokens[i];
     sessions[i]->poisoned = true;  // cleared on success
   }
+  // the products run on MFMA when every session selects the matrix-core
+  // projections
+  bool mx = true;
+  for (int i = 0; i < count; ++i) mx = mx && (sessions[i]->matrix & CQ35_MATRIX_PROJECTIONS) != 0;
   hipError_t e = hipSuccess;
   for (int i = 0; i < count && e == hipSuccess; ++i) e = hipStreamSynchronize(sessions[i]->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(b->d_rows, b->h_rows, sizeof(SessionRows), hipMemcpyHostToDevice, b->stream);
-  if (e == hipSuccess && !b->exec[count]) {
+  if (e == hipSuccess && !b->exec[mx][count]) {
     e = hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
-      enqueue_batch(m, b, count);
+      enqueue_batch(m, b, count, mx);
       hipGraph_t g = nullptr;
       e = hipStreamEndCapture(b->stream, &g);
-      if (e == hipSuccess) e = hipGraphInstantiate(&b->exec[count], g, nullptr, nullptr, 0);
-      b->graph[count] = g;
+      if (e == hipSuccess) e = hipGraphInstantiate(&b->exec[mx][count], g, nullptr, nullptr, 0);
+      b->graph[mx][count] = g;
     }
   }
-  if (e == hipSuccess) e = hipGraphLaunch(b->exec[count], b->stream);
+  if (e == hipSuccess) e = hipGraphLaunch(b->exec[mx][count], b->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(b->h_best, b->d_best, count * sizeof(unsigned long long), hipMemcpyDeviceToHost, b->stream);
+  if (e == hipSuccess && logits)
+    e = hipMemcpyAsync(logits, b->logits, (size_t)count * m->cfg.vocab * 2, hipMemcpyDeviceToHost, b->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "batched step: %s", hipGetErrorString(e));
   for (int i = 0; i < count; ++i) {
@@ -2151,7 +2185,7 @@ bool shared_batch_ok(cq35_session* const* sessions, int64_t count) {
 }  // namespace
 
 extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens,
-                               const int64_t* starts, int64_t count, uint64_t* next_tokens) {
+                               const int64_t* starts, int64_t count, uint64_t* next_tokens, uint16_t* logits) {
   if (!sessions || !tokens || !starts || !next_tokens || count <= 0) return fail(CQ35_EINVAL, "null argument");
   // every check before any work, as for one session
   for (int64_t i = 0; i < count; ++i) {
@@ -2168,7 +2202,7 @@ extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* to
                   s->model->cfg.vocab);
   }
   if (shared_batch_ok(sessions, count)) {
-    const int rc = step_batch_shared(sessions, tokens, starts, (int)count, next_tokens);
+    const int rc = step_batch_shared(sessions, tokens, starts, (int)count, next_tokens, logits);
     if (rc)
       for (int64_t i = 0; i < count; ++i) sessions[i]->poisoned = true;
     return rc;
@@ -2180,10 +2214,11 @@ extern "C" int cq35_step_batch(cq35_session* const* sessions, const uint64_t* to
     cq35_session* s = sessions[i];
     HIP_TRY(hipSetDevice(s->model->device));
     int rc;
+    uint16_t* li = logits ? logits + (size_t)i * s->model->cfg.vocab : nullptr;
     if (s->mega_on && s->timed_class < 0) {
-      rc = step_persistent(s, tokens[i], starts[i], &next_tokens[i], nullptr);
+      rc = step_persistent(s, tokens[i], starts[i], &next_tokens[i], li);
     } else {
-      rc = step_launch(s, &tokens[i], 1, starts[i], nullptr);
+      rc = step_launch(s, &tokens[i], 1, starts[i], li);
       if (!rc) launched.push_back(i);
     }
     if (rc) {

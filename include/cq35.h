@@ -145,17 +145,23 @@ int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t 
 
 /* One decode step (one token each) for several independent sessions:
  * tokens[i] at position starts[i] of sessions[i], next token into
- * next_tokens[i]. Each session's result is identical to its own cq35_step.
- * Sessions on the per-kernel path are launched back to back on their own
- * streams and then completed, so their kernels overlap on the device;
- * sessions on the persistent path step one at a time (each launch needs every
- * CU). All checks precede any work. If a step fails after work was
- * enqueued, every session of the batch is poisoned (some may have advanced a
- * position; none reports a token). No reference counterpart: the reference
- * steps sessions one after another (src/server/engine.rs:143-207); this is
- * the entry point for batch-16 serving. */
+ * next_tokens[i] and, when logits != NULL, session i's BF16 logits into
+ * logits[i * vocab ..]. Dense sessions of one model and capacity take one
+ * weight-shared step (each layer's weights read once for all of them); each
+ * session's result is then identical to its own cq35_step, unless every
+ * session of the batch selects the matrix-core projections
+ * (cq35_session_set_matrix_prefill), in which case the products run on MFMA
+ * (hardware accumulation order: tolerance-level, like the matrix-core
+ * prefill). Other sessions on the per-kernel path are launched back to back
+ * on their own streams and then completed, so their kernels overlap on the
+ * device; sessions on the persistent path step one at a time (each launch
+ * needs every CU). All checks precede any work. If a step fails after work
+ * was enqueued, every session of the batch is poisoned (some may have
+ * advanced a position; none reports a token). No reference counterpart: the
+ * reference steps sessions one after another (src/server/engine.rs:143-207);
+ * this is the entry point for batch-16 serving. */
 int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts,
-                    int64_t count, uint64_t* next_tokens);
+                    int64_t count, uint64_t* next_tokens, uint16_t* logits);
 
 /* A decode step (one token) that allocates nothing, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops

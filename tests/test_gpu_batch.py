@@ -56,11 +56,11 @@ def test_batch_rejects_before_any_work():
     toks = np.array([1, 1], dtype=np.uint64)
     starts = np.array([2, 2], dtype=np.int64)
     out = np.zeros(2, dtype=np.uint64)
-    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data) == -1  # twice
+    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data, None) == -1  # twice
     h = (ctypes.c_void_p * 2)(a._h.value, b._h.value)
     starts = np.array([2, 8], dtype=np.int64)
-    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data) == -2  # capacity
+    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data, None) == -2  # capacity
     toks = np.array([1, m.cfg["vocab"]], dtype=np.uint64)
     starts = np.array([2, 7], dtype=np.int64)
-    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data) == -2  # vocabulary
+    assert lib.cq35_step_batch(h, toks.ctypes.data, starts.ctypes.data, 2, out.ctypes.data, None) == -2  # vocabulary
     assert np.array_equal(a.export_state(0), state), "a rejected batch must not touch any session"
