@@ -309,55 +309,122 @@ __global__ __launch_bounds__(64 * kMWaves) __attribute__((amdgpu_waves_per_eu(2,
 //
 // The weight-shared batched decode step's products on MFMA (a session
 // option, like the prefill components): at most 32 tokens per tile, so the
-// work is a weight stream. Block = 32 weight rows x a 32-token tile; wave w
-// sums the columns [w cols/4, (w + 1) cols/4) into one accumulator, with two
-// batches of four k steps in flight (loads are unconditional: a batch past the
-// end reloads the last one, so every wait leaves the newer batch
-// outstanding); the four partial tiles are added as a tree through LDS
-// ((w0 + w1) + (w2 + w3)), then the epilogue. cols % 512 == 0.
+// work is a weight stream. Block = 32 kT weight rows (kT MFMA tiles sharing
+// each activation fragment: two for the vocabulary head) x a 32-token tile x
+// one of `kb` column ranges;
+// wave w of the block sums a quarter of that range into one accumulator per
+// tile (k permuted inside each 64-column batch so that loads are whole
+// lines), with two batches of four k steps in flight (loads are unconditional:
+// a batch past the end reloads the last one, so every wait leaves the newer
+// batch outstanding). The four wave partials are added as a tree through LDS
+// ((w0 + w1) + (w2 + w3)). With kb > 1 (launches with few row tiles: more
+// blocks keep every CU streaming) each block stores its partial tile and
+// k_mskinny_finish adds the kb partials in column-range order before the
+// epilogue; the kernel boundary orders them, so no device-scope fence (an
+// L2 write-back on a multi-XCD part) is needed. cols % (512 kb) == 0.
 constexpr int kSkSplit = 4;  // waves per block
 constexpr int kSkBatch = 4;  // k steps per load batch
 enum { kSArgmax = 3 };       // mode: vocabulary head, bf16 logits and each token's (value, first index) max
 
-template <int kMode>
+// The epilogue of a 32 kT-row x 32-token tile held by one wave (tile tx, ty).
+template <int kMode, int kMats, int kT>
+__device__ __forceinline__ void skinny_epilogue(const f32x16_t (&acc)[kMats][kT], int tx, int ty, int n,
+                                                const Segments& seg, const uint16_t* __restrict__ res,
+                                                unsigned long long* __restrict__ best) {
+  const int lane = threadIdx.x & 63;
+  const int rows = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  const int r0 = tx * 32 * kT, t0 = ty * 32;
+#pragma unroll
+  for (int h = 0; h < kT; ++h) {
+    const int row = r0 + 32 * h + (lane & 31);
+    int lr;
+    const int os = segment_of(seg, min(row, rows - 1), &lr);
+    uint16_t* out = segment_out(seg, os);
+    const int srows = os == 0 ? seg.rows[0] : os == 1 ? seg.rows[1] : os == 2 ? seg.rows[2] : seg.rows[3];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const int t = t0 + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
+      const bool ok = t < n && row < rows;
+      const size_t o = (size_t)t * srows + lr;
+      const float v = acc[0][h][rr];
+      uint16_t y = 0;
+      if (ok) {
+        if (kMode == kBPlain || kMode == kSArgmax) y = f2bf(v);
+        else if (kMode == kBResidual) y = bf_add(f2bf(v), res[o]);
+        else y = bf_mul(f2bf(silu(rbf(v))), f2bf(acc[kMats - 1][h][rr]));
+        out[o] = y;
+      }
+      if (kMode == kSArgmax) {
+        // this token's (value, first index) maximum over the 32 rows of the
+        // tile (lanes of one half), kept per tile: best[(tx kT + h) 32 + t
+        // mod 32] for k_argmax_tiles (atomics from thousands of tiles on the
+        // same few words would serialise)
+        unsigned long long key = ok ? logit_key(y, (uint32_t)row) : 0ull;
+#pragma unroll
+        for (int d = 16; d >= 1; d >>= 1) {
+          const unsigned long long o2 = __shfl_xor(key, d, 64);
+          key = o2 > key ? o2 : key;
+        }
+        if ((lane & 31) == 0) best[(size_t)((ty * gridDim.x + tx) * kT + h) * 32 + (t - t0)] = key;
+      }
+    }
+  }
+}
+
+template <int kMode, int kT>
 __global__ __launch_bounds__(64 * kSkSplit) void k_mskinny(const uint16_t* __restrict__ x, int n, int cols,
                                                            Segments seg, const uint16_t* __restrict__ w2,
                                                            const uint16_t* __restrict__ res,
-                                                           unsigned long long* __restrict__ best) {
+                                                           unsigned long long* __restrict__ best,
+                                                           f32x16_t* __restrict__ part) {
   constexpr int kMats = kMode == kBGate ? 2 : 1;
-  __shared__ f32x16_t part[kSkSplit - 1][kMats][64];
+  __shared__ f32x16_t red[kSkSplit - 1][kMats][kT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kb = gridDim.z;
   const int rows = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
-  const int r0 = blockIdx.x * 32, t0 = blockIdx.y * 32;
-  const int kq = 8 * (lane >> 5);
-  const int qcols = cols / kSkSplit, c0 = wave * qcols;
-  int local;
-  const int sg = segment_of(seg, min(r0 + (lane & 31), rows - 1), &local);
-  const uint16_t* wb[kMats];
-  wb[0] = segment_w(seg, sg) + (size_t)local * cols + c0 + kq;
-  if (kMode == kBGate) wb[kMats - 1] = w2 + (size_t)local * cols + c0 + kq;
+  const int r0 = blockIdx.x * 32 * kT, t0 = blockIdx.y * 32;
+  // a batch of four k steps covers 64 columns: lane half h holds columns
+  // [32 h, 32 h + 32) of it, 8 per step, in both operands (the same
+  // permutation of k), so each lane reads 64 contiguous bytes per row and the
+  // two halves one whole 128-byte line
+  const int kq = 32 * (lane >> 5);
+  const int span = cols / (kSkSplit * kb), c0 = (blockIdx.z * kSkSplit + wave) * span;
+  const uint16_t* wb[kMats][kT];
+#pragma unroll
+  for (int h = 0; h < kT; ++h) {
+    int local;
+    const int sg = segment_of(seg, min(r0 + 32 * h + (lane & 31), rows - 1), &local);
+    wb[0][h] = segment_w(seg, sg) + (size_t)local * cols + c0 + kq;
+    if (kMode == kBGate) wb[kMats - 1][h] = w2 + (size_t)local * cols + c0 + kq;
+  }
   const uint16_t* xa = x + (size_t)min(t0 + (lane & 31), n - 1) * cols + c0 + kq;
-  const int steps = qcols / 16;  // a multiple of 2 kSkBatch
+  const int steps = span / 16;  // a multiple of 2 kSkBatch
   struct Set {
-    u32x4 a[kSkBatch], b[kMats][kSkBatch];
+    u32x4 a[kSkBatch], b[kMats][kT][kSkBatch];
   };
   auto load = [&](int s, Set& v) {
     const int k = 16 * min(s, steps - kSkBatch);
 #pragma unroll
     for (int j = 0; j < kSkBatch; ++j) {
-      v.a[j] = *reinterpret_cast<const u32x4*>(xa + k + 16 * j);
+      v.a[j] = *reinterpret_cast<const u32x4*>(xa + k + 8 * j);
 #pragma unroll
-      for (int mi = 0; mi < kMats; ++mi) v.b[mi][j] = *reinterpret_cast<const u32x4*>(wb[mi] + k + 16 * j);
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < kT; ++h) v.b[mi][h][j] = *reinterpret_cast<const u32x4*>(wb[mi][h] + k + 8 * j);
     }
   };
-  f32x16_t acc[kMats];
+  f32x16_t acc[kMats][kT];
 #pragma unroll
-  for (int mi = 0; mi < kMats; ++mi) acc[mi] = f32x16_t{};
+  for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+    for (int h = 0; h < kT; ++h) acc[mi][h] = f32x16_t{};
   auto mult = [&](const Set& v) {
 #pragma unroll
     for (int j = 0; j < kSkBatch; ++j)
 #pragma unroll
-      for (int mi = 0; mi < kMats; ++mi) acc[mi] = mfma32(v.a[j], v.b[mi][j], acc[mi]);
+      for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+        for (int h = 0; h < kT; ++h) acc[mi][h] = mfma32(v.a[j], v.b[mi][h][j], acc[mi][h]);
   };
   Set P, Q;
   load(0, P);
@@ -369,42 +436,79 @@ __global__ __launch_bounds__(64 * kSkSplit) void k_mskinny(const uint16_t* __res
   }
   if (wave > 0) {
 #pragma unroll
-    for (int mi = 0; mi < kMats; ++mi) part[wave - 1][mi][lane] = acc[mi];
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int h = 0; h < kT; ++h) red[wave - 1][mi][h][lane] = acc[mi][h];
   }
   __syncthreads();
   if (wave > 0) return;
 #pragma unroll
-  for (int mi = 0; mi < kMats; ++mi) acc[mi] = (acc[mi] + part[0][mi][lane]) + (part[1][mi][lane] + part[2][mi][lane]);
-  const int row = r0 + (lane & 31);
-  int lr;
-  const int os = segment_of(seg, min(row, rows - 1), &lr);
-  uint16_t* out = segment_out(seg, os);
-  const int srows = os == 0 ? seg.rows[0] : os == 1 ? seg.rows[1] : os == 2 ? seg.rows[2] : seg.rows[3];
+  for (int mi = 0; mi < kMats; ++mi)
 #pragma unroll
-  for (int rr = 0; rr < 16; ++rr) {
-    const int t = t0 + 8 * (rr >> 2) + 4 * (lane >> 5) + (rr & 3);
-    const bool ok = t < n && row < rows;
-    const size_t o = (size_t)t * srows + lr;
-    const float v = acc[0][rr];
-    uint16_t y = 0;
-    if (ok) {
-      if (kMode == kBPlain || kMode == kSArgmax) y = f2bf(v);
-      else if (kMode == kBResidual) y = bf_add(f2bf(v), res[o]);
-      else y = bf_mul(f2bf(silu(rbf(v))), f2bf(acc[kMats - 1][rr]));
-      out[o] = y;
-    }
-    if (kMode == kSArgmax) {
-      // the (value, first index) maximum of this token over the tile's 32
-      // rows (lanes of one half), then one atomic per token and tile
-      unsigned long long key = ok ? logit_key(y, (uint32_t)row) : 0ull;
-#pragma unroll
-      for (int d = 16; d >= 1; d >>= 1) {
-        const unsigned long long o2 = __shfl_xor(key, d, 64);
-        key = o2 > key ? o2 : key;
-      }
-      if ((lane & 31) == 0 && t < n && key) atomicMax(best + t, key);
-    }
+    for (int h = 0; h < kT; ++h)
+      acc[mi][h] = (acc[mi][h] + red[0][mi][h][lane]) + (red[1][mi][h][lane] + red[2][mi][h][lane]);
+  if (kb == 1) {
+    skinny_epilogue<kMode, kMats, kT>(acc, blockIdx.x, blockIdx.y, n, seg, res, best);
+    return;
   }
+  const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+  f32x16_t* mine = part + (((size_t)blockIdx.z * gridDim.y * gridDim.x + tile) * kMats * kT) * 64;
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+    for (int h = 0; h < kT; ++h) mine[(mi * kT + h) * 64 + lane] = acc[mi][h];
+}
+
+// Each token's (value, first index) maximum over the per-tile maxima of a
+// kSArgmax launch (tiles x 32 keys per token tile; 0 = no candidate): one
+// block per token.
+__global__ __launch_bounds__(256) void k_argmax_tiles(const unsigned long long* __restrict__ keys, int tiles,
+                                                      int n, unsigned long long* __restrict__ best) {
+  __shared__ unsigned long long wmax[4];
+  const int t = blockIdx.x, tt = t / 32;
+  unsigned long long m = 0ull;
+  for (int i = threadIdx.x; i < tiles; i += blockDim.x) {
+    const unsigned long long k = keys[((size_t)tt * tiles + i) * 32 + (t & 31)];
+    m = k > m ? k : m;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const unsigned long long o = __shfl_xor(m, d, 64);
+    m = o > m ? o : m;
+  }
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0 && t < n) {
+    for (int i = 1; i < 4; ++i) m = wmax[i] > m ? wmax[i] : m;
+    best[t] = m;
+  }
+}
+
+// The kb column-range partials of each tile of a split k_mskinny launch,
+// added in range order, then the epilogue: one wave per (row tile, token
+// tile), all of its partials requested before the first add.
+template <int kMode, int kT>
+__global__ __launch_bounds__(64) void k_mskinny_finish(const f32x16_t* __restrict__ part, int kb, int n,
+                                                       Segments seg, const uint16_t* __restrict__ res,
+                                                       unsigned long long* __restrict__ best) {
+  constexpr int kMats = kMode == kBGate ? 2 : 1, kMaxKb = 8;
+  const int lane = threadIdx.x;
+  const size_t tiles = (size_t)gridDim.y * gridDim.x, tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+  f32x16_t acc[kMats][kT];
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+    for (int h = 0; h < kT; ++h) {
+      f32x16_t v[kMaxKb];
+#pragma unroll
+      for (int z = 0; z < kMaxKb; ++z)
+        if (z < kb) v[z] = part[(((size_t)z * tiles + tile) * kMats * kT + mi * kT + h) * 64 + lane];
+      acc[mi][h] = v[0];
+#pragma unroll
+      for (int z = 1; z < kMaxKb; ++z)
+        if (z < kb) acc[mi][h] = acc[mi][h] + v[z];
+    }
+  skinny_epilogue<kMode, kMats, kT>(acc, blockIdx.x, blockIdx.y, n, seg, res, best);
 }
 
 // ---------------------------------------------------------------- experts

@@ -1913,6 +1913,8 @@ struct BatchWorkspace {
   uint16_t* logits = nullptr;
   float *rope = nullptr, *scratch = nullptr;
   int stride = 0;
+  f32x16_t* mx_part = nullptr;  // matrix-core products: partial tiles of split column ranges
+  unsigned long long* mx_keys = nullptr;  // and the head's per-tile argmax keys [token tiles][32-row tiles][32]
   hipGraph_t graph[2][kMaxSessions + 1] = {};      // [matrix-core products][sessions]
   hipGraphExec_t exec[2][kMaxSessions + 1] = {};
   std::vector<void*> allocs;
@@ -1981,6 +1983,10 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
   const int64_t tiles = (capacity + 7) / 8;
   b->stride = (int)std::max<int64_t>(tiles * 8 + 2 * tiles + 16, 3 * capacity + 16);
   alloc(&b->scratch, B * d.Q * (int64_t)b->stride);
+  // partial tiles: kb x tiles < 1024 (split launches have < 128 tiles), each
+  // up to two matrices x two 32-row halves x 64 lanes
+  alloc(&b->mx_part, (int64_t)1024 * 2 * 2 * 64);
+  alloc(&b->mx_keys, ((B + 31) / 32) * ((d.V + 31) / 32 + 2) * 32);
   (void)wide;
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_rows, sizeof(SessionRows), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_best, B * sizeof(unsigned long long), hipHostMallocDefault);
@@ -1994,18 +2000,39 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
 }
 
 // Matrix-core products of the batched step (k_mskinny) take widths that are
-// multiples of 512.
+// multiples of 512. The vocabulary head runs two MFMA tiles per wave; launches
+// with fewer than 128 row tiles split the columns over kb blocks (a power of
+// two, at most 8) so that about 512 blocks stream.
 bool skinny_ok(int64_t cols) { return cols % (16 * kSkSplit * 2 * kSkBatch) == 0; }
-dim3 skinny_grid(int64_t rows, int B) { return dim3((unsigned)((rows + 31) / 32), (unsigned)((B + 31) / 32)); }
+template <int kMode, int kT>
+void skinny_launch(hipStream_t st, const BatchWorkspace* b, const uint16_t* x, int B, int64_t cols,
+                   const Segments& seg, const uint16_t* w2, const uint16_t* res, unsigned long long* best) {
+  const int64_t rows = seg_rows(seg), rt = (rows + 32 * kT - 1) / (32 * kT), tt = (B + 31) / 32;
+  int kb = 1;
+  if (rt * tt < 128)
+    while (kb < 8 && rt * tt * kb < 512 && cols % (512 * kb * 2) == 0) kb *= 2;
+  const dim3 grid((unsigned)rt, (unsigned)tt, (unsigned)kb);
+  // the head's per-tile maxima go to the key buffer, then one block per token
+  unsigned long long* keys = kMode == kSArgmax ? b->mx_keys : best;
+  k_mskinny<kMode, kT><<<grid, dim3(64 * kSkSplit), 0, st>>>(x, B, (int)cols, seg, w2, res, keys, b->mx_part);
+  if (kb > 1)
+    k_mskinny_finish<kMode, kT><<<dim3(grid.x, grid.y), dim3(64), 0, st>>>(b->mx_part, kb, B, seg, res, keys);
+  if (kMode == kSArgmax) k_argmax_tiles<<<dim3((unsigned)B), dim3(256), 0, st>>>(keys, (int)(rt * kT), B, best);
+}
+template <int kMode>
+void skinny(hipStream_t st, const BatchWorkspace* b, const uint16_t* x, int B, int64_t cols, const Segments& seg,
+            const uint16_t* w2, const uint16_t* res, unsigned long long* best) {
+  if (seg_rows(seg) >= 32768) skinny_launch<kMode, 2>(st, b, x, B, cols, seg, w2, res, best);
+  else skinny_launch<kMode, 1>(st, b, x, B, cols, seg, w2, res, best);
+}
 
 // Weight-shared GEMV launches (k_ws32 / k_ws64 / k_ws256_swiglu) over B
 // tokens, or with mx the matrix-core products where the width allows.
 void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t cols, unsigned long long* best,
-          bool mx = false) {
+          const BatchWorkspace* mx = nullptr) {
   if (mx && skinny_ok(cols)) {
-    const dim3 grid = skinny_grid(seg_rows(seg), B), block(64 * kSkSplit);
-    if (best) k_mskinny<kSArgmax><<<grid, block, 0, st>>>(x, B, (int)cols, seg, nullptr, nullptr, best);
-    else k_mskinny<kBPlain><<<grid, block, 0, st>>>(x, B, (int)cols, seg, nullptr, nullptr, nullptr);
+    if (best) skinny<kSArgmax>(st, mx, x, B, cols, seg, nullptr, nullptr, best);
+    else skinny<kBPlain>(st, mx, x, B, cols, seg, nullptr, nullptr, nullptr);
     return;
   }
   const int groups = (B + kBatchNB - 1) / kBatchNB;
@@ -2016,15 +2043,11 @@ void ws32(hipStream_t st, const uint16_t* x, int B, const Segments& seg, int64_t
   else k_ws32<false, 8><<<grid, block, lds, st>>>(x, B, groups, seg, (int)cols, best);
 }
 void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows, int64_t cols, const uint16_t* res,
-          uint16_t* out, bool mx = false) {
+          uint16_t* out, const BatchWorkspace* mx = nullptr) {
   if (mx && skinny_ok(cols)) {
     const Segments one = segments({{w, {out, rows}}});
-    if (res)
-      k_mskinny<kBResidual><<<skinny_grid(rows, B), dim3(64 * kSkSplit), 0, st>>>(x, B, (int)cols, one, nullptr, res,
-                                                                                 nullptr);
-    else
-      k_mskinny<kBPlain><<<skinny_grid(rows, B), dim3(64 * kSkSplit), 0, st>>>(x, B, (int)cols, one, nullptr, nullptr,
-                                                                              nullptr);
+    if (res) skinny<kBResidual>(st, mx, x, B, cols, one, nullptr, res, nullptr);
+    else skinny<kBPlain>(st, mx, x, B, cols, one, nullptr, nullptr, nullptr);
     return;
   }
   const int groups = (B + kBatchNB - 1) / kBatchNB;
@@ -2060,7 +2083,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
     const void* post_norm;
     if (is_full(c, l)) {
       ws32(st, b->x, B, segments({{W(1), {b->qg, 2 * d.QS}}, {W(2), {b->kraw, d.KVS}}, {W(3), {b->vraw, d.KVS}}}),
-           d.H, nullptr, mx);
+           d.H, nullptr, mx ? b : nullptr);
       k_full_prepare<<<dim3((unsigned)(d.Q + d.KVH), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->qg, (const uint16_t*)b->kraw, (const uint16_t*)b->vraw, (const float*)b->rope,
           (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
@@ -2072,7 +2095,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(128), 0, st>>>(
           (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
           (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
-      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, mx);
+      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, mx ? b : nullptr);
       post_norm = W(7);
       ffn = 8;
     } else {
@@ -2081,7 +2104,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       ws32(st, b->x, B,
            segments({{W(1), {b->qkv, d.QKV}}, {W(2), {b->z, d.VS}}, {W(3), {alpha, c.value_heads}},
                      {W(4), {beta, c.value_heads}}}),
-           d.H, nullptr, mx);
+           d.H, nullptr, mx ? b : nullptr);
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       k_linear_prepare<<<dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->qkv, (uint16_t*)nullptr, conv_base, (const uint64_t*)nullptr, 0, (const float*)W(9),
@@ -2093,14 +2116,14 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
           (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
       k_gated_norm<<<dim3((unsigned)c.value_heads, (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->core, (const uint16_t*)b->z, (const float*)W(7), c.value_dim, c.eps, b->gated);
-      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn, mx);
+      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn, mx ? b : nullptr);
       post_norm = W(10);
       ffn = 11;
     }
     norm(b->attn, post_norm, b->x);
     if (mx && skinny_ok(d.H)) {
-      k_mskinny<kBGate><<<skinny_grid(d.I, B), dim3(64 * kSkSplit), 0, st>>>(
-          b->x, B, (int)d.H, segments({{W(ffn), {b->act, d.I}}}), (const uint16_t*)W(ffn + 1), nullptr, nullptr);
+      skinny<kBGate>(st, b, b->x, B, d.H, segments({{W(ffn), {b->act, d.I}}}), (const uint16_t*)W(ffn + 1), nullptr,
+                     nullptr);
     } else {
       const int groups = (B + kBatchNBDual - 1) / kBatchNBDual;
       const int row_blocks = (int)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate));
@@ -2109,12 +2132,12 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
                                                              (const uint16_t*)W(ffn + 1), (int)d.I, (int)d.H,
                                                              b->act);
     }
-    ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h, mx);
+    ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h, mx ? b : nullptr);
     base += layer_tensors(c, l);
   }
   const int64_t total = weight_count(c);
   norm(b->h, Wt(total - 2), b->x);
-  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best, mx);
+  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best, mx ? b : nullptr);
 }
 
 // One weight-shared decode step for `count` dense sessions of one model and
@@ -2141,7 +2164,12 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   for (int i = 0; i < count && e == hipSuccess; ++i) e = hipStreamSynchronize(sessions[i]->stream);
   if (e == hipSuccess)
     e = hipMemcpyAsync(b->d_rows, b->h_rows, sizeof(SessionRows), hipMemcpyHostToDevice, b->stream);
-  if (e == hipSuccess && !b->exec[mx][count]) {
+  // CQ35_GRAPH=0 (as for sessions) enqueues the launches directly instead
+  // of replaying a captured graph, e.g. for kernel tracing
+  const char* graph_env = getenv("CQ35_GRAPH");
+  const bool use_graph = !(graph_env && atoi(graph_env) == 0);
+  if (e == hipSuccess && !use_graph) enqueue_batch(m, b, count, mx);
+  if (e == hipSuccess && use_graph && !b->exec[mx][count]) {
     e = hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
       enqueue_batch(m, b, count, mx);
@@ -2151,7 +2179,8 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
       b->graph[mx][count] = g;
     }
   }
-  if (e == hipSuccess) e = hipGraphLaunch(b->exec[mx][count], b->stream);
+  if (e == hipSuccess && use_graph) e = hipGraphLaunch(b->exec[mx][count], b->stream);
+  if (e == hipSuccess && !use_graph) e = hipGetLastError();
   if (e == hipSuccess)
     e = hipMemcpyAsync(b->h_best, b->d_best, count * sizeof(unsigned long long), hipMemcpyDeviceToHost, b->stream);
   if (e == hipSuccess && logits)
