@@ -2256,12 +2256,17 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
   // uniform, quad q + 8(pc*PIECE + j) of the lane's row is at byte 16q + 128(pc*PIECE + j)
   auto load_piece = [&](u32x4* buf, int t) {
     const int b = t / PIECES, pc = t - b * PIECES;
-    const uint16_t* w = a.head + (size_t)((m.gw + m.nw * b) * 8) * H + pc * PIECE * 64;
+    const int grp = steps > 0 ? m.gw + m.nw * b : 0;  // a wave without groups reads group 0 (unused)
+    const uint16_t* w = a.head + (size_t)(grp * 8) * H + pc * PIECE * 64;
 #pragma unroll
     for (int j = 0; j < PIECE; ++j) buf[j] = ldq_at(w, lane_off + (uint32_t)j * 128u);
   };
+  // Pieces past the wave's last one re-read the last (an L2 hit), so every
+  // load is unconditional: the wait before a piece's products then leaves the
+  // newer piece in flight (a conditional load makes the compiler drain them).
+  const int last = steps > 0 ? steps - 1 : 0;
   u32x4 b0[PIECE], b1[PIECE];
-  if (steps > 0) load_piece(b0, 0);
+  load_piece(b0, 0);
   f32x4 w0, w1;
   norm_weights<S>(m, a.out_norm, w0, w1);
   poll_words<(H / 2 + kMT - 1) / kMT>(m, H / 2, Span{a.x_final}, reinterpret_cast<uint32_t*>(m.xr));
@@ -2286,13 +2291,12 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
     }
   };
   for (int t = 0; t < steps; t += 2) {
-    if (t + 1 < steps) load_piece(b1, t + 1);
+    load_piece(b1, min(t + 1, last));
     consume(b0, t);
-    if (t + 1 < steps) {
-      if (t + 2 < steps) load_piece(b0, t + 2);
-      consume(b1, t + 1);
-    }
+    load_piece(b0, min(t + 2, last));
+    if (t + 1 < steps) consume(b1, t + 1);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-reads, before the wave moves on
 #pragma unroll
   for (int d = 32; d >= 8; d >>= 1) {
     const unsigned long long o = __shfl_down(mine, d, 64);
