@@ -69,7 +69,9 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
     const uint16_t* __restrict__ qkv, uint16_t* __restrict__ cache, int64_t conv_base,
     const uint64_t* __restrict__ params, int t, const float* __restrict__ conv_w, int qkv_size,
     int key_dim, int key_heads, uint16_t* __restrict__ conv_out, uint16_t* __restrict__ q_out,
-    uint16_t* __restrict__ k_out, const SessionRows* __restrict__ rows) {
+    uint16_t* __restrict__ k_out, const SessionRows* __restrict__ rows, const uint16_t* __restrict__ alpha,
+    const uint16_t* __restrict__ beta, const float* __restrict__ dt, const float* __restrict__ a,
+    int value_heads, float2* __restrict__ gates) {
   __shared__ float squares[256];
   __shared__ float total;
   const int y = blockIdx.y;  // session row of a batched step (0 otherwise)
@@ -81,6 +83,14 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
   if (rows) cache = rows->cache[y];
   const int64_t position = rows ? (int64_t)rows->position[y] : step_position(params, t);
   const int chunk = blockIdx.x, tid = threadIdx.x;
+  // the delta gates of every value head, once per token (delta_gates.hex):
+  // decay = exp(bf16(softplus(alpha + dt) * a)), rate = bf16(sigmoid(beta))
+  if (chunk == 0)
+    for (int h = tid; h < value_heads; h += blockDim.x) {
+      const float time_step = softplus(bf2f(alpha[(size_t)y * value_heads + h]) + dt[h]);
+      gates[(size_t)y * value_heads + h] =
+          float2{hexp(rbf(time_step * a[h])), rbf(sigmoid(bf2f(beta[(size_t)y * value_heads + h])))};
+    }
   const int ch = chunk * key_dim + tid;
   const bool active = tid < key_dim && ch < qkv_size;
   float value = 0.0f;
@@ -122,11 +132,11 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
 // (serial from 0.0, then a 32-wide halving tree). The state row is BF16 in
 // the cache (decode) or F32 in the shadow (inside a multi-token call); the
 // output always uses the unrounded F32 update.
+constexpr int kDeltaCh = 1;  // value channels per 32-lane group of k_delta
 template <bool kF32State>
 __global__ __launch_bounds__(kBlock) void k_delta(
     const uint16_t* __restrict__ conv, const uint16_t* __restrict__ q,
-    const uint16_t* __restrict__ k, const uint16_t* __restrict__ alpha,
-    const uint16_t* __restrict__ beta, const float* __restrict__ dt, const float* __restrict__ a,
+    const uint16_t* __restrict__ k, const float2* __restrict__ gates,
     uint16_t* __restrict__ state16, float* __restrict__ state32, int value_size, int value_dim,
     int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out,
     const SessionRows* __restrict__ rows, int64_t state_off) {
@@ -135,51 +145,66 @@ __global__ __launch_bounds__(kBlock) void k_delta(
   conv += (size_t)y * (2 * key_size + value_size);
   q += (size_t)y * key_size;
   k += (size_t)y * key_size;
-  alpha += (size_t)y * value_heads;
-  beta += (size_t)y * value_heads;
+  gates += (size_t)y * value_heads;
   out += (size_t)y * value_size;
   if (rows) state16 = rows->cache[y] + state_off;
-  const int c = blockIdx.x * 8 + (threadIdx.x >> 5);
   const int lane = threadIdx.x & 31;
-  const bool valid = c < value_size;
-  const int cc = valid ? c : 0;
-  const int head = cc / value_dim;
-  const int kbase = (head % key_heads) * key_dim;
-  const float time_step = softplus(bf2f(alpha[head]) + dt[head]);
-  const float decay = hexp(rbf(time_step * a[head]));
-  const float rate = rbf(sigmoid(bf2f(beta[head])));
-  float old[8], kv[8];
-  float acc = 0.0f;
+  // each 32-lane group runs kDeltaCh channels side by side (independent
+  // chains; one measured fastest); every input is requested up front
+  int c[kDeltaCh], cc[kDeltaCh], kbase[kDeltaCh];
+  bool valid[kDeltaCh];
+  float decay[kDeltaCh], rate[kDeltaCh], value[kDeltaCh];
+  float old[kDeltaCh][8], kv[kDeltaCh][8], qv[kDeltaCh][8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = lane + 32 * j;
-    if (i < key_dim) {
-      old[j] = kF32State ? state32[(size_t)cc * key_dim + i] : bf2f(state16[(size_t)cc * key_dim + i]);
-      kv[j] = bf2f(k[kbase + i]);
-      acc += old[j] * kv[j];
-    }
-  }
+  for (int u = 0; u < kDeltaCh; ++u) {
+    c[u] = (blockIdx.x * (kBlock / 32) + (threadIdx.x >> 5)) * kDeltaCh + u;
+    valid[u] = c[u] < value_size;
+    cc[u] = valid[u] ? c[u] : 0;
+    const int head = cc[u] / value_dim;
+    kbase[u] = (head % key_heads) * key_dim;
+    const float2 gate = gates[head];  // k_linear_prepare's (decay, rate)
+    decay[u] = gate.x;
+    rate[u] = gate.y;
+    value[u] = bf2f(conv[2 * key_size + cc[u]]);
 #pragma unroll
-  for (int s = 16; s >= 1; s >>= 1) acc += __shfl_down(acc, s, 32);
-  const float total = __shfl(acc, 0, 32);
-  const float value = bf2f(conv[2 * key_size + cc]);
-  const float delta = (value - total * decay) * rate;
-  float acc2 = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = lane + 32 * j;
-    if (i < key_dim) {
-      const float next = old[j] * decay + kv[j] * delta;
-      if (valid) {
-        if (kF32State) state32[(size_t)cc * key_dim + i] = next;
-        else state16[(size_t)cc * key_dim + i] = f2bf(next);
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + 32 * j;
+      if (i < key_dim) {
+        old[u][j] = kF32State ? state32[(size_t)cc[u] * key_dim + i] : bf2f(state16[(size_t)cc[u] * key_dim + i]);
+        kv[u][j] = bf2f(k[kbase[u] + i]);
+        qv[u][j] = bf2f(q[kbase[u] + i]);
       }
-      acc2 += next * bf2f(q[kbase + i]);
     }
   }
 #pragma unroll
-  for (int s = 16; s >= 1; s >>= 1) acc2 += __shfl_down(acc2, s, 32);
-  if (lane == 0 && valid) out[c] = f2bf(acc2 * scale);
+  for (int u = 0; u < kDeltaCh; ++u) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (lane + 32 * j < key_dim) acc += old[u][j] * kv[u][j];
+    // D32 halving tree (strides 16 .. 1) in each half wave by DPP / permlane,
+    // the sums of lanes 0 and 32 broadcast to their halves
+    acc = tree32_lanes(acc);
+    const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+    const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 32));
+    const float total = (threadIdx.x & 32) ? t1 : t0;
+    const float delta = (value[u] - total * decay[u]) * rate[u];
+    float acc2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + 32 * j;
+      if (i < key_dim) {
+        const float next = old[u][j] * decay[u] + kv[u][j] * delta;
+        if (valid[u]) {
+          if (kF32State) state32[(size_t)cc[u] * key_dim + i] = next;
+          else state16[(size_t)cc[u] * key_dim + i] = f2bf(next);
+        }
+        acc2 += next * qv[u][j];
+      }
+    }
+    acc2 = tree32_lanes(acc2);
+    if (lane == 0 && valid[u]) out[c[u]] = f2bf(acc2 * scale);
+  }
 }
 
 // Gated RMSNorm x SiLU(z) per value head with a serial sum of squares

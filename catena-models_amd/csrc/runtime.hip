@@ -737,6 +737,7 @@ struct cq35_session {
   uint16_t *h = nullptr, *attn = nullptr;
   uint16_t *qkv = nullptr, *conv = nullptr, *z = nullptr, *alpha = nullptr, *beta = nullptr;
   uint16_t *qn = nullptr, *kn = nullptr, *core = nullptr, *gated = nullptr;
+  float2* gates = nullptr;  // per value head (decay, rate) of the current token
   uint16_t *qg = nullptr, *kraw = nullptr, *vraw = nullptr, *qr = nullptr, *ctx = nullptr;
   float* router = nullptr;
   int* ids = nullptr;
@@ -1030,6 +1031,7 @@ int create_session(cq35_model* m, int64_t capacity, cq35_session** out) {
   check(dalloc(s, &s->alpha, c.value_heads));
   check(dalloc(s, &s->beta, c.value_heads));
   check(dalloc(s, &s->qn, d.KS));
+  check(dalloc(s, &s->gates, c.value_heads));
   check(dalloc(s, &s->kn, d.KS));
   check(dalloc(s, &s->core, d.VS));
   check(dalloc(s, &s->gated, d.VS));
@@ -1266,19 +1268,19 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       L(KC_PREPARE_LINEAR, k_linear_prepare, dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim)),
         dim3(kBlock), 0, (const uint16_t*)s->qkv, s->cache, conv_base, (const uint64_t*)s->d_params,
-        t, (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, s->conv, s->qn, s->kn, (const SessionRows*)nullptr);
+        t, (const float*)W(9), (int)d.QKV, c.key_dim, c.key_heads, s->conv, s->qn, s->kn, (const SessionRows*)nullptr,
+        (const uint16_t*)s->alpha, (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6), c.value_heads,
+        s->gates);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
-      const dim3 dgrid((unsigned)((d.VS + 7) / 8));
+      const dim3 dgrid((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)));
       if (f32_state)
         L(KC_DELTA, k_delta<true>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
-          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
-          (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr,
+          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const float2*)s->gates, (uint16_t*)nullptr,
           s->shadow + l * d.REC, (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale,
           s->core, (const SessionRows*)nullptr, (int64_t)0);
       else
         L(KC_DELTA, k_delta<false>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
-          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const uint16_t*)s->alpha,
-          (const uint16_t*)s->beta, (const float*)W(5), (const float*)W(6),
+          (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const float2*)s->gates,
           s->cache + conv_base + d.CONV, (float*)nullptr, (int)d.VS, c.value_dim, c.key_dim,
           c.key_heads, (int)d.KS, scale, s->core, (const SessionRows*)nullptr, (int64_t)0);
       L(KC_GATED_NORM, k_gated_norm, dim3((unsigned)c.value_heads), dim3(kBlock), 0,
@@ -1913,6 +1915,7 @@ struct BatchWorkspace {
   uint16_t* logits = nullptr;
   float *rope = nullptr, *scratch = nullptr;
   int stride = 0;
+  float2* gates = nullptr;       // per session and value head (decay, rate)
   f32x16_t* mx_part = nullptr;  // matrix-core products: partial tiles of split column ranges
   unsigned long long* mx_keys = nullptr;  // and the head's per-tile argmax keys [token tiles][32-row tiles][32]
   hipGraph_t graph[2][kMaxSessions + 1] = {};      // [matrix-core products][sessions]
@@ -1986,6 +1989,7 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
   // partial tiles: kb x tiles < 1024 (split launches have < 128 tiles), each
   // up to two matrices x two 32-row halves x 64 lanes
   alloc(&b->mx_part, (int64_t)1024 * 2 * 2 * 64);
+  alloc(&b->gates, B * (int64_t)c.value_heads);
   alloc(&b->mx_keys, ((B + 31) / 32) * ((d.V + 31) / 32 + 2) * 32);
   (void)wide;
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_rows, sizeof(SessionRows), hipHostMallocDefault);
@@ -2108,11 +2112,12 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
       k_linear_prepare<<<dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->qkv, (uint16_t*)nullptr, conv_base, (const uint64_t*)nullptr, 0, (const float*)W(9),
-          (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows);
+          (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows, (const uint16_t*)alpha,
+          (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), c.value_heads, b->gates);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
-      k_delta<false><<<dim3((unsigned)((d.VS + 7) / 8), (unsigned)B), dim3(kBlock), 0, st>>>(
-          (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const uint16_t*)alpha,
-          (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, (float*)nullptr,
+      k_delta<false><<<dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const float2*)b->gates,
+          (uint16_t*)nullptr, (float*)nullptr,
           (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
       k_gated_norm<<<dim3((unsigned)c.value_heads, (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->core, (const uint16_t*)b->z, (const float*)W(7), c.value_dim, c.eps, b->gated);

@@ -70,6 +70,7 @@ int64_t static_layout(cq35_session* s, unsigned char* base) {
   take(&s->z, d.VS);
   take(&s->alpha, c.value_heads);
   take(&s->beta, c.value_heads);
+  take(&s->gates, c.value_heads);
   take(&s->qn, d.KS);
   take(&s->kn, d.KS);
   take(&s->core, d.VS);
