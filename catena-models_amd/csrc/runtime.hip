@@ -757,6 +757,7 @@ struct cq35_session {
   // persistent decode step (MoE): tagged exchange words, layer table, args
   bool mega_ok = false;       // the shape fits the persistent kernel
   bool mega_on = false;       // n == 1 steps use it
+  bool mega_coop = false;     // launched cooperatively (co-residency of all blocks checked at launch)
   uint64_t* words = nullptr;
   MegaLayer* d_layers = nullptr;
   MegaArgs margs{};
@@ -1001,6 +1002,14 @@ int setup_mega(cq35_session* s) {
   s->mega_grid = grid;
   s->mega_kernel = kernel;
   s->mega_lds = lds;
+  // Every block waits on others' words, so all of them must be resident at
+  // once: a cooperative launch has the runtime check that (and fail the
+  // launch) instead of leaving it to the occupancy computed above.
+  // CQ35_COOPERATIVE=0 selects the ordinary launch.
+  int coop = 0;
+  hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, m.device);
+  s->mega_coop = coop != 0;
+  if (const char* cl = getenv("CQ35_COOPERATIVE")) s->mega_coop = s->mega_coop && atoi(cl) != 0;
   s->mega_ok = true;
   s->mega_on = true;
   if (const char* g = getenv("CQ35_PERSISTENT")) s->mega_on = atoi(g) != 0;
@@ -1648,7 +1657,15 @@ int step_persistent(cq35_session* s, uint64_t token, int64_t start, uint64_t* ne
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "parameter upload: %s", hipGetErrorString(e));
   const MegaArgs* args = s->d_margs;
   void* kargs[] = {(void*)&args};
-  if (s->timed_class == KC_DECODE_STEP && s->ev_used < kMaxTimedEvents) {
+  const bool timed = s->timed_class == KC_DECODE_STEP && s->ev_used < kMaxTimedEvents;
+  if (s->mega_coop) {
+    if (timed) e = hipEventRecord(s->ev[2 * s->ev_used], s->stream);
+    if (e == hipSuccess)
+      e = hipLaunchCooperativeKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs,
+                                     (unsigned)s->mega_lds, s->stream);
+    if (e == hipSuccess && timed) e = hipEventRecord(s->ev[2 * s->ev_used + 1], s->stream);
+    if (timed) ++s->ev_used;
+  } else if (timed) {
     // events stamped by the dispatch packet, as for the per-kernel classes
     e = hipExtLaunchKernel(s->mega_kernel, dim3((unsigned)s->mega_grid), dim3(kMT), kargs, (size_t)s->mega_lds,
                            s->stream, s->ev[2 * s->ev_used], s->ev[2 * s->ev_used + 1], 0);
