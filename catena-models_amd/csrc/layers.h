@@ -306,12 +306,13 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
 // exponentials of up to kStagedLdsKeys keys stay in LDS, longer contexts use
 // the global scratch row.
 constexpr int kStagedLdsKeys = 2048;
+constexpr int kStagedThreads = 1024;  // one thread per key of a 1024-key context: the score chains run at once
 
-__global__ __launch_bounds__(kBlock) void k_attention_staged(
+__global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
     const uint64_t* __restrict__ params, int t, int kvs, int head_dim, int heads_per_kv, float scale,
     float* __restrict__ scratch, int scratch_stride, const SessionRows* __restrict__ rows) {
-  __shared__ float partial[kBlock];
+  __shared__ float partial[kStagedThreads];
   __shared__ float qf[256];
   __shared__ float s_lds[kStagedLdsKeys];
   __shared__ float e_lds[kStagedLdsKeys];
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
   if (tid < head_dim) qf[tid] = bf2f(q[head * head_dim + tid]);
   __syncthreads();
   // scores in the scalar order (element 0 first), 8 elements per 16-byte read
-  for (int64_t kk = tid; kk < keys; kk += kBlock) {
+  for (int64_t kk = tid; kk < keys; kk += kStagedThreads) {
     const u32x4* kr = reinterpret_cast<const u32x4*>(cache + key_base + kk * kvs + off);
     float acc = 0.0f;
 #pragma unroll 4
@@ -347,22 +348,22 @@ __global__ __launch_bounds__(kBlock) void k_attention_staged(
   }
   __syncthreads();
   float m = bitsf(0xff800000u);
-  for (int64_t kk = tid; kk < keys; kk += kBlock) m = fmaxf(m, s[kk]);
+  for (int64_t kk = tid; kk < keys; kk += kStagedThreads) m = fmaxf(m, s[kk]);
   partial[tid] = m;
   __syncthreads();
-  for (int st = kBlock / 2; st >= 1; st >>= 1) {
+  for (int st = kStagedThreads / 2; st >= 1; st >>= 1) {
     if (tid < st) partial[tid] = fmaxf(partial[tid], partial[tid + st]);
     __syncthreads();
   }
   const float maximum = partial[0];
-  for (int64_t kk = tid; kk < keys; kk += kBlock) e[kk] = hexp(s[kk] - maximum);
+  for (int64_t kk = tid; kk < keys; kk += kStagedThreads) e[kk] = hexp(s[kk] - maximum);
   __syncthreads();
   for (int64_t d = 1; d < keys; d <<= 1) {
-    for (int64_t k2 = tid; k2 * 2 * d + d < keys; k2 += kBlock) e[k2 * 2 * d] += e[k2 * 2 * d + d];
+    for (int64_t k2 = tid; k2 * 2 * d + d < keys; k2 += kStagedThreads) e[k2 * 2 * d] += e[k2 * 2 * d + d];
     __syncthreads();
   }
   const float den = e[0];
-  for (int64_t kk = tid; kk < keys; kk += kBlock) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
+  for (int64_t kk = tid; kk < keys; kk += kStagedThreads) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
   __syncthreads();
 }
 

@@ -1260,7 +1260,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           s->attn_stride, (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t,
           (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->split_keys, s->ctx);
       } else {
-        L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kBlock), 0,
+        L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kStagedThreads), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
           (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr);
         L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(128), 0,
@@ -1494,7 +1494,7 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
         for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
           const int am = std::min(s->pf_attn_tokens, rows_n - a0);
-          L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kBlock), 0,
+          L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kStagedThreads), 0,
             (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
             first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
           L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
@@ -2110,7 +2110,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
           (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
           (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, b->qr, rows);
       const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
-      k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kBlock), 0, st>>>(
+      k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kStagedThreads), 0, st>>>(
           (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
           (int)d.HD, (int)(d.Q / d.KVH), scale, b->scratch, b->stride, rows);
       k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(128), 0, st>>>(
