@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CQ35_ABI_VERSION 1
+#define CQ35_ABI_VERSION 2  /* 2: cq35_step_batch logits, cq35_device_matrix_gemm modes */
 
 enum {
   CQ35_OK = 0,
@@ -233,7 +233,11 @@ int cq35_session_persistent(const cq35_session* session, int* enabled);
  * qwen35.rs:467-541; default off in its library API, as here). Bit 0: the
  * dense projections (attention, DeltaNet and output projections, dense FFN);
  * bit 1: the MoE expert projections (grouped routed experts and the shared
- * expert). 0 keeps the exact SIMT path. Decode steps are unaffected. */
+ * expert). 0 keeps the exact SIMT path. A session whose components are set
+ * at its first multi-token call runs multi-token calls in chunks of 1024
+ * tokens (otherwise 256; the chunk changes no result). Single-session decode
+ * steps are unaffected; the weight-shared batched step (cq35_step_batch)
+ * runs its products on MFMA when every session of the batch has bit 0. */
 /* Split-K decode attention for long contexts. Over more than `keys` cached
  * keys (default CQ35_SPLIT_KEYS_DEFAULT; 0: never) the T tiles (8 keys) of
  * each query head's online softmax form at most 128 ranges of ceil(T / 128)

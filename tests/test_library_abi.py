@@ -34,7 +34,7 @@ def test_header_symbols_exported(lib):
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.EXPORTED)
-    assert lib.cq35_abi_version() == 1
+    assert lib.cq35_abi_version() == 2
 
 
 @pytest.mark.parametrize("name", sorted(cc.PRESETS))
