@@ -37,6 +37,37 @@ def test_header_symbols_exported(lib):
     assert lib.cq35_abi_version() == 2
 
 
+def header_parameters(name):
+    text = open(os.path.join(ROOT, "include", "cq35.h")).read()
+    m = re.search(r"^(?:const )?\w+\*? ?\*?\s*" + name + r"\(([^)]*)\)", text, re.M)
+    args = [a.strip() for a in m.group(1).split(",") if a.strip() and a.strip() != "void"]
+    return len(args)
+
+
+def test_rust_binding_matches_header():
+    """The Rust FFI crate a maintainer adds to catena-models
+    (catena-models_amd/rust/catena-cq35-sys) declares only entry points of
+    include/cq35.h, each with the header's parameter count, and the same
+    constants."""
+    src = open(os.path.join(ROOT, "catena-models_amd", "rust", "catena-cq35-sys", "src", "lib.rs")).read()
+    decls = re.findall(r"pub fn (cq35_\w+)\(([^)]*)\)", src)
+    assert len(decls) >= 20
+    declared = set(declared_functions())
+    for name, params in decls:
+        assert name in declared, name
+        n = len([p for p in params.split(",") if p.strip()])
+        assert n == header_parameters(name), name
+    header = open(os.path.join(ROOT, "include", "cq35.h")).read()
+    for const in ["CQ35_ABI_VERSION", "CQ35_MATRIX_PROJECTIONS", "CQ35_MATRIX_EXPERTS", "CQ35_SPLIT_KEYS_DEFAULT"]:
+        hv = re.search(r"#define " + const + r" (\d+)", header).group(1)
+        rv = re.search(r"pub const " + const + r": \w+ = (\d+);", src).group(1)
+        assert hv == rv, const
+    # the struct's fields in the header's order
+    hfields = re.findall(r"^\s+(?:int32_t|float) (\w+);", header.split("typedef struct cq35_config")[1].split("}")[0], re.M)
+    rfields = re.findall(r"pub (\w+): (?:i32|f32),", src.split("pub struct cq35_config")[1].split("}")[0])
+    assert hfields == rfields
+
+
 @pytest.mark.parametrize("name", sorted(cc.PRESETS))
 def test_presets_validate_and_weight_abi_matches(lib, oracle, name):
     cfg = cc.preset(name)
