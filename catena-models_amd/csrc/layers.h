@@ -302,11 +302,38 @@ __global__ __launch_bounds__(kBlock) void k_full_prepare(
 // sums the context from them. One block per query head; blockIdx.y selects
 // token t + y of the call (the batched prefill's per-query staged attention,
 // batch_staged_attention.hex:10-47) with its own rows and scratch. The query
-// head is read once into LDS and the key rows as 16-byte quads; scores and
-// exponentials of up to kStagedLdsKeys keys stay in LDS, longer contexts use
-// the global scratch row.
+// head is read once into LDS and the key rows as 16-byte quads, 16 in flight
+// per thread. Up to kStagedLdsKeys keys (two per thread) the scores stay in
+// registers: the maximum is a wave reduction (max is exact in any order),
+// and the adjacent-pair sum runs its first six levels (pairs within 64
+// keys) across the lanes of a wave and the rest over the 64-key nodes in
+// one wave, the same additions as the level-by-level loop. Longer contexts
+// keep scores and exponentials in the global scratch row.
 constexpr int kStagedLdsKeys = 2048;
 constexpr int kStagedThreads = 1024;  // one thread per key of a 1024-key context: the score chains run at once
+
+// Scalar-order score of key kk: element 0 first, 8 elements per 16-byte read.
+__device__ __forceinline__ float staged_score(const uint16_t* __restrict__ krow, const float* qf, int head_dim) {
+  const u32x4* kr = reinterpret_cast<const u32x4*>(krow);
+  const int nq = head_dim >> 3;
+  float acc = 0.0f;
+  for (int i0 = 0; i0 < nq; i0 += 16) {
+    u32x4 w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = kr[min(i0 + i, nq - 1)];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i0 + i < nq) {
+        const float* qi = qf + 8 * (i0 + i);
+        acc += qi[0] * lo2f(w[i].x); acc += qi[1] * hi2f(w[i].x);
+        acc += qi[2] * lo2f(w[i].y); acc += qi[3] * hi2f(w[i].y);
+        acc += qi[4] * lo2f(w[i].z); acc += qi[5] * hi2f(w[i].z);
+        acc += qi[6] * lo2f(w[i].w); acc += qi[7] * hi2f(w[i].w);
+      }
+    }
+  }
+  return acc;
+}
 
 __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
@@ -314,9 +341,9 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
     float* __restrict__ scratch, int scratch_stride, const SessionRows* __restrict__ rows) {
   __shared__ float partial[kStagedThreads];
   __shared__ float qf[256];
-  __shared__ float s_lds[kStagedLdsKeys];
-  __shared__ float e_lds[kStagedLdsKeys];
-  const int head = blockIdx.x, tid = threadIdx.x;
+  __shared__ float nodes[kStagedLdsKeys / 64];
+  __shared__ float stat;
+  const int head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int y = blockIdx.y;
   const size_t qs = (size_t)gridDim.x * head_dim;
   q += y * qs;
@@ -324,30 +351,71 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
   const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
   if (rows) cache = rows->cache[y];
   const int64_t off = (int64_t)(head / heads_per_kv) * head_dim;
-  const bool in_lds = keys <= kStagedLdsKeys;
   float* row = scratch + (size_t)head * scratch_stride;
-  float* s = in_lds ? s_lds : row;
-  float* e = in_lds ? e_lds : row + keys;
   uint16_t* pb = reinterpret_cast<uint16_t*>(row + 2 * keys);  // read by k_attention_context
+  const float ninf = bitsf(0xff800000u);
   if (tid < head_dim) qf[tid] = bf2f(q[head * head_dim + tid]);
   __syncthreads();
-  // scores in the scalar order (element 0 first), 8 elements per 16-byte read
-  for (int64_t kk = tid; kk < keys; kk += kStagedThreads) {
-    const u32x4* kr = reinterpret_cast<const u32x4*>(cache + key_base + kk * kvs + off);
-    float acc = 0.0f;
-#pragma unroll 4
-    for (int i8 = 0; i8 < (head_dim >> 3); ++i8) {
-      const u32x4 w = kr[i8];
-      const float* qi = qf + 8 * i8;
-      acc += qi[0] * lo2f(w.x); acc += qi[1] * hi2f(w.x);
-      acc += qi[2] * lo2f(w.y); acc += qi[3] * hi2f(w.y);
-      acc += qi[4] * lo2f(w.z); acc += qi[5] * hi2f(w.z);
-      acc += qi[6] * lo2f(w.w); acc += qi[7] * hi2f(w.w);
+  if (keys <= kStagedLdsKeys) {
+    constexpr int KPT = kStagedLdsKeys / kStagedThreads;
+    float sc[KPT];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t kk = tid + (int64_t)kStagedThreads * j;
+      sc[j] = ninf;
+      if (kk < keys) sc[j] = rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
     }
-    s[kk] = rbf(acc * scale);
+    float m = sc[0];
+#pragma unroll
+    for (int j = 1; j < KPT; ++j) m = fmaxf(m, sc[j]);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+    if (lane == 0) partial[wave] = m;
+    __syncthreads();
+    float maximum = partial[0];
+    for (int w = 1; w < kStagedThreads / 64; ++w) maximum = fmaxf(maximum, partial[w]);
+    // adjacent-pair sum, levels 1..32 within each 64-key group
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t base = (int64_t)kStagedThreads * j + 64 * wave, kk = base + lane;
+      if (base < keys) {  // uniform per wave
+        float e = kk < keys ? hexp(sc[j] - maximum) : 0.0f;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float o = __shfl_down(e, d, 64);
+          if ((lane & (2 * d - 1)) == 0 && kk + d < keys) e += o;
+        }
+        if (lane == 0) nodes[base >> 6] = e;
+      }
+    }
+    __syncthreads();
+    // levels 64 and up over the 64-key nodes
+    if (wave == 0) {
+      const int nn = (int)((keys + 63) >> 6);
+      float v = lane < nn ? nodes[lane] : 0.0f;
+#pragma unroll
+      for (int d = 1; d < kStagedLdsKeys / 64; d <<= 1) {
+        const float o = __shfl_down(v, d, 64);
+        if ((lane & (2 * d - 1)) == 0 && 64 * (int64_t)(lane + d) < keys) v += o;
+      }
+      if (lane == 0) stat = v;
+    }
+    __syncthreads();
+    const float den = stat;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t kk = tid + (int64_t)kStagedThreads * j;
+      if (kk < keys) pb[kk] = f2bf(hexp(sc[j] - maximum) / den);
+    }
+    return;
   }
+  // long contexts: scores and exponentials in the scratch row
+  float* s = row;
+  float* e = row + keys;
+  for (int64_t kk = tid; kk < keys; kk += kStagedThreads)
+    s[kk] = rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
   __syncthreads();
-  float m = bitsf(0xff800000u);
+  float m = ninf;
   for (int64_t kk = tid; kk < keys; kk += kStagedThreads) m = fmaxf(m, s[kk]);
   partial[tid] = m;
   __syncthreads();
@@ -364,7 +432,6 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
   }
   const float den = e[0];
   for (int64_t kk = tid; kk < keys; kk += kStagedThreads) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
-  __syncthreads();
 }
 
 // The context of k_attention_staged's probabilities: per channel eight
@@ -372,52 +439,90 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
 // combined as ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)), then bf16(bf16(sum) *
 // sigmoid(gate)) (qwen35_attention.hex:2-177, qwen35.hex:207-222). Block
 // (head, 16-channel chunk) of grid.x = heads * head_dim / 16, blockIdx.y = token
-// t + y; thread (chain r = tid / 16, channel tid % 16), eight steps read ahead.
+// t + y. The block stages kContextKeys keys at a time in LDS (each key's
+// 32-byte channel slice as two 16-byte loads, the probabilities as 4-byte
+// pairs), the next chunk's loads in flight while threads tid < 128
+// (chain r = tid / 16, channel tid % 16) run the chains over the current one.
 constexpr int kContextChannels = 16;
+constexpr int kContextThreads = 256;
+constexpr int kContextKeys = 512;
 
-__global__ __launch_bounds__(128) void k_attention_context(
+__global__ __launch_bounds__(kContextThreads) void k_attention_context(
     const uint16_t* __restrict__ cache, int64_t value_base, const uint64_t* __restrict__ params,
     int t, int kvs, int head_dim, int heads, int heads_per_kv, const uint16_t* __restrict__ qg,
     const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out,
     const SessionRows* __restrict__ rows) {
+  __shared__ __align__(16) uint16_t vs[2][kContextKeys][kContextChannels];
+  __shared__ __align__(16) uint32_t ps[2][kContextKeys / 2];
   __shared__ float part[8][kContextChannels];
   const int chunks = head_dim / kContextChannels;
   const int head = blockIdx.x / chunks, c0 = (blockIdx.x - head * chunks) * kContextChannels;
-  const int y = blockIdx.y;
-  const int r = threadIdx.x >> 4, c = c0 + (threadIdx.x & 15);
+  const int y = blockIdx.y, tid = threadIdx.x;
+  const int r = tid >> 4, x = tid & 15;
   const size_t qs = (size_t)heads * head_dim;
   qg += y * 2 * qs;
   out += y * qs;
   const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
   if (rows) cache = rows->cache[y];
-  const uint16_t* pb = reinterpret_cast<const uint16_t*>(
+  // probabilities start 2 * keys floats into the row: 4-byte aligned pairs
+  const uint32_t* pb = reinterpret_cast<const uint32_t*>(
       scratch + (size_t)y * heads * scratch_stride + (size_t)head * scratch_stride + 2 * keys);
-  const uint16_t* vb = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c;
-  const int64_t steps = (keys + 7) >> 3;
+  const uint16_t* vb = cache + value_base + (int64_t)(head / heads_per_kv) * head_dim + c0;
+  const int64_t steps = (keys + 7) >> 3;  // chain steps; keys [0, 8 steps) are visited
+  const int nchunks = (int)((8 * steps + kContextKeys - 1) / kContextKeys);
+  constexpr int VQ = 2 * kContextKeys;  // 16-byte halves of the channel slices
+  constexpr int PW = kContextKeys / 2;  // probability pairs
+  static_assert(VQ % kContextThreads == 0 && PW <= kContextThreads, "context staging");
+  constexpr int VPT = VQ / kContextThreads;
+  u32x4 vr[VPT];
+  uint32_t pr = 0;
+  // loads of chunk ch (keys past the end read the last key; the chains skip them)
+  auto fetch = [&](int ch) {
+    const int64_t k0 = (int64_t)ch * kContextKeys;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = tid + kContextThreads * i;
+      const int64_t key = min(k0 + (idx >> 1), keys - 1);
+      vr[i] = *reinterpret_cast<const u32x4*>(vb + key * kvs + 8 * (idx & 1));
+    }
+    if (tid < PW) pr = pb[min(k0 / 2 + tid, (keys - 1) / 2)];
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = tid + kContextThreads * i;
+      reinterpret_cast<u32x4*>(&vs[buf][idx >> 1][0])[idx & 1] = vr[i];
+    }
+    if (tid < PW) ps[buf][tid] = pr;
+  };
   float acc = 0.0f;
-  constexpr int kAhead = 8;
-  for (int64_t i0 = 0; i0 < steps; i0 += kAhead) {
-    float pv[kAhead], vv[kAhead];
-#pragma unroll
-    for (int j = 0; j < kAhead; ++j) {
-      const int64_t kk = 8 * (i0 + j) + r;
-      const bool ok = i0 + j < steps && kk < keys;
-      pv[j] = ok ? bf2f(pb[kk]) : 0.0f;
-      vv[j] = ok ? bf2f(vb[kk * kvs]) : 0.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < kAhead; ++j) {
-      if (i0 + j >= steps) break;
-      const int64_t kk = 8 * (i0 + j) + r;
-      acc = acc + (kk < keys ? pv[j] * vv[j] : 0.0f);
-    }
-  }
-  part[r][threadIdx.x & 15] = acc;
+  fetch(0);
+  put(0);
   __syncthreads();
-  if (r == 0 && c < head_dim) {
-    const int x = threadIdx.x & 15;
-    const float sum = ((part[0][x] + part[4][x]) + (part[2][x] + part[6][x])) +
-                      ((part[1][x] + part[5][x]) + (part[3][x] + part[7][x]));
+#pragma unroll 1
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int buf = ch & 1;
+    if (ch + 1 < nchunks) fetch(ch + 1);
+    if (tid < 128) {
+      const int64_t k0 = (int64_t)ch * kContextKeys;
+      const int n = (int)min<int64_t>(kContextKeys / 8, steps - k0 / 8);  // chain steps in the chunk
+      const uint16_t* p16 = reinterpret_cast<const uint16_t*>(ps[buf]);
+#pragma unroll 8
+      for (int i = 0; i < n; ++i) {
+        const int local = 8 * i + r;
+        const float pv = bf2f(p16[local]), vv = bf2f(vs[buf][local][x]);
+        acc = acc + (k0 + local < keys ? pv * vv : 0.0f);
+      }
+    }
+    if (ch + 1 < nchunks) put(buf ^ 1);
+    __syncthreads();
+  }
+  if (tid < 128) part[r][x] = acc;
+  __syncthreads();
+  if (tid < kContextChannels) {
+    const int c = c0 + tid;
+    const float sum = ((part[0][tid] + part[4][tid]) + (part[2][tid] + part[6][tid])) +
+                      ((part[1][tid] + part[5][tid]) + (part[3][tid] + part[7][tid]));
     const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + c]));
     out[head * head_dim + c] = f2bf(rbf(sum) * gate);
   }

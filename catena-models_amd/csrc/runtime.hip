@@ -1263,7 +1263,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kStagedThreads), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
           (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr);
-        L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(128), 0,
+        L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(kContextThreads), 0,
           (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD,
           (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, (const float*)s->attn_scratch,
           s->attn_stride, s->ctx, (const SessionRows*)nullptr);
@@ -1498,7 +1498,7 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
             (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
             first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
           L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
-            dim3(128), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
+            dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
             (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
             (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS, (const SessionRows*)nullptr);
         }
@@ -2113,7 +2113,7 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kStagedThreads), 0, st>>>(
           (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
           (int)d.HD, (int)(d.Q / d.KVH), scale, b->scratch, b->stride, rows);
-      k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(128), 0, st>>>(
+      k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(kContextThreads), 0, st>>>(
           (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
           (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
       ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, mx ? b : nullptr);

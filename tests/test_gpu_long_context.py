@@ -104,6 +104,33 @@ def test_persistent_covers_every_capacity(models, name):
     assert m.session(MAX_CAPACITY).persistent, f"{name}: capacity {MAX_CAPACITY} should run persistent"
 
 
+@pytest.mark.parametrize("name,capacity,start,steps", [("tiny", 1100, 1020, 6), ("tiny", 2100, 2044, 6),
+                                                       ("tiny", 5000, 4600, 2), ("qwen35-0.8b", 1400, 1290, 2)])
+def test_long_context_dense_against_oracle(models, oracle, name, capacity, start, steps):
+    """Dense shapes (per-kernel staged attention) from an imported state:
+    the steps cross the staging boundaries (512-key context chunks, 1024
+    keys = two keys per score thread, 2048 keys = the register path's limit;
+    above it the scores go through the scratch row), bit-exact against the
+    restatement."""
+    cfg = cc.preset(name)
+    say("long context dense", name, "capacity", capacity, "start", start)
+    state = seeded_state(cfg, capacity, start, seed=13, device="cpu")
+    m = models(name)
+    first = 23
+    sb, cb = decode_from(m, state, capacity, start, first, steps, False)
+    say("  per-kernel done")
+    om = oracle.Model(cfg, oracle.synthetic_weights(cfg, 5))
+    os_ = om.session(capacity)
+    os_.import_cache(state)
+    co, tok = [], first
+    for i in range(steps):
+        tok, logits = os_.step([tok], start + i)
+        co.append((tok, logits))
+    say("  oracle done")
+    same_calls(name + " per-kernel/oracle", cb, co)
+    assert np.array_equal(sb.export_state(0), os_.cache()), f"{name}: per-kernel state differs"
+
+
 @pytest.mark.parametrize("capacity,start,split", [(4104, 4096, None), (70001, 69990, None),
                                                   (70001, 69990, 0), (9001, 8190, 1000)])
 def test_long_context_mini_moe_against_oracle(models, oracle, capacity, start, split):
