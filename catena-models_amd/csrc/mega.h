@@ -54,6 +54,7 @@ struct MegaShape {
   static constexpr int KS = KH * KD, VS = VH * VD, QKV = 2 * KS + VS, QS = Q * HD, KVS = KVH * HD;
   static constexpr int QH = H / 8;            // BF16 quads per hidden row
   static constexpr int NQA = (QH + 63) / 64;  // S256 quads per lane per row
+  static constexpr bool kDense = false;
   static_assert(H % 8 == 0 && H <= 2048, "hidden width");
   static_assert(KD % 32 == 0 && KD <= 128 && VD <= 128 && VD % 4 == 0, "DeltaNet head dims");
   static_assert(VH >= KH, "value heads");
@@ -102,6 +103,7 @@ struct MegaLayer {
   uint64_t* x_active;  // routed activations (K*I/2)
   uint64_t* x_shared;  // shared-expert bf16(bf16(silu(g)) * u), before the gate (SI/2)
   uint64_t* x_scores;  // Q * capacity F32 scores (full layers)
+  uint64_t* x_probs;   // dense full layers: Q x (capacity/2 + 1) BF16 probability pairs
   uint64_t* x_out;     // output hidden row (H/2) = next layer's x_h
 };
 
@@ -664,11 +666,12 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   const float dt = G(Ly.dt)[h], aa = G(Ly.a)[h];
   const float gw = m.tid < VD ? G(Ly.gnorm)[m.tid] : 0.0f;
   // alpha (wave kMW - 2) and beta (wave kMW - 1) rows of head h, on the
-  // waves that have no convolution channel
+  // waves that have no convolution channel (MoE shapes: S256 here; dense
+  // shapes: S32 rows of the projection phase)
   static_assert(NCH <= kMT - 128, "alpha/beta waves");
   constexpr int kAB = kMW - 2;
   u32x4 abw[S::NQA];
-  if (m.wave >= kAB) {
+  if (!S::kDense && m.wave >= kAB) {
     const uint16_t* w = (m.wave == kAB ? Ly.alpha_w : Ly.beta_w) + (size_t)h * S::H;
 #pragma unroll
     for (int j = 0; j < S::NQA; ++j) abw[j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
@@ -676,16 +679,24 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   // inputs: q | k | v of this head, z (projection words)
   constexpr int qw = KD / 2, vw = VD / 2;
   constexpr int zbase = S::QKV;
-  constexpr int nwords = 2 * qw + 2 * vw;
+  constexpr int nwords = 2 * qw + 2 * vw + (S::kDense ? 2 : 0);
   const uint64_t* proj = Ly.x_proj;
   auto addr = [&](int i) -> const uint64_t* {
     if (i < qw) return proj + ((kh * KD) >> 1) + i;
     if (i < 2 * qw) return proj + ((S::KS + kh * KD) >> 1) + (i - qw);
     if (i < 2 * qw + vw) return proj + ((2 * S::KS + h * VD) >> 1) + (i - 2 * qw);
-    return proj + ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
+    if (i < 2 * qw + 2 * vw) return proj + ((zbase + h * VD) >> 1) + (i - 2 * qw - vw);
+    // dense: the words holding alpha row QKV + VS + h and beta row QKV + VS + VH + h
+    return proj + ((S::QKV + S::VS + (i - 2 * qw - 2 * vw) * S::VH + h) >> 1);
   };
   poll_words<(nwords + kMT - 1) / kMT>(m, nwords, addr, m.vec);
-  if (m.wave >= kAB) {
+  if constexpr (S::kDense) {
+    static_assert(S::VH % 2 == 0, "alpha and beta rows share a word's parity");
+    if (m.tid < 2) {
+      const uint32_t w = m.vec[2 * qw + 2 * vw + m.tid];
+      d->ab[m.tid] = (uint16_t)((h & 1) ? (w >> 16) : (w & 0xffffu));
+    }
+  } else if (m.wave >= kAB) {
     Quad acc;
     quad_zero(acc);
 #pragma unroll
@@ -825,24 +836,27 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
 // then the 64-lane tree. Waves 2i and 2i+1 take rows 2p and 2p+1,
 // p = block + grid * i, and the even wave stores the word. Blocks kh < KH of a
 // linear layer also write the q and k conv history of key head kh.
-template <class S, int COLS>
+// With kDown (dense SwiGLU down projection, the same S64 order): input the
+// gate/up activations x_active (I BF16), weights sdown, residual the
+// post-mixer row, output x_out.
+template <class S, int COLS, bool kDown = false>
 __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
   constexpr int NP = COLS / 2, NJ = NP / 64;
-  static_assert(NP % 64 == 0, "output projection width");
+  static_assert(NP % 64 == 0 && NP <= 4096, "output projection width");
   const int p = m.bid + m.grid * (m.wave >> 1);
   const int row = 2 * p + (m.wave & 1);
   const bool has_row = p < S::H / 2;
   uint32_t wv[NJ];
   if (has_row) {
-    const uint16_t* w = Ly.out_w + (size_t)row * COLS;
+    const uint16_t* w = (kDown ? Ly.sdown : Ly.out_w) + (size_t)row * COLS;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) wv[j] = ldd_at(w, (uint32_t)(m.lane + 64 * j) * 4u);
   }
-  poll_words<(NP + kMT - 1) / kMT>(m, NP, Span{Ly.x_mix}, m.vec);
-  if (!Ly.full && m.bid < S::KH) {
+  poll_words<(NP + kMT - 1) / kMT>(m, NP, Span{kDown ? Ly.x_active : Ly.x_mix}, m.vec);
+  if (!kDown && !Ly.full && m.bid < S::KH) {
     // q and k history of key head kh = the block index (its raw values are
     // still in this block's LDS from the previous phase).
     const DeltaLds* d = reinterpret_cast<const DeltaLds*>(m.big);
@@ -859,14 +873,14 @@ __device__ __forceinline__ void phase_outproj(const MegaArgs* pa, uint32_t tag, 
 #pragma unroll
     for (int j = 0; j < NJ; ++j) pair_acc(lo, hi, m.vec[m.lane + 64 * j], wv[j]);
     const float v = tree64_lanes(lo + hi);
-    o = bf_add(f2bf(v), m.xr[row]);
+    o = bf_add(f2bf(v), kDown ? m.xa[row] : m.xr[row]);
     if (m.lane == 0 && (m.wave & 1)) m.misc->red[4 + (m.wave >> 1)] = __builtin_bit_cast(float, (uint32_t)o);
   }
-  trace_mark(kMarkOutprojDone);
+  if (!kDown) trace_mark(kMarkOutprojDone);
   __syncthreads();
   if (has_row && m.lane == 0 && !(m.wave & 1)) {
     const uint16_t other = (uint16_t)__builtin_bit_cast(uint32_t, m.misc->red[4 + (m.wave >> 1)]);
-    word_store(Ly.x_attn + p, pack_bf(o, other), m.tag);
+    word_store((kDown ? Ly.x_out : Ly.x_attn) + p, pack_bf(o, other), m.tag);
   }
 }
 

@@ -22,6 +22,7 @@
 #include "attention.h"
 #include "layers.h"
 #include "mega.h"
+#include "dense_step.h"
 #include "prefill.h"
 #include "mfma.h"
 #include "gguf.h"
@@ -813,10 +814,14 @@ void destroy_session(cq35_session* s) {
   delete s;
 }
 
-// Model shapes the persistent decode kernel is compiled for (mega.h) and the
-// per-grid limits of its work split; other shapes and capacities use the
-// per-kernel path. Returns the shape index (0 = none).
-enum MegaKind { kMegaNone = 0, kMega35B, kMegaMini, kMegaTiny };
+// Model shapes the persistent decode kernels are compiled for (mega.h for
+// the MoE shapes, dense_step.h for the dense ones) and the per-grid limits of
+// their work split; other shapes and capacities use the per-kernel path.
+// Returns the shape index (0 = none).
+enum MegaKind {
+  kMegaNone = 0, kMega35B, kMegaMini, kMegaTiny,
+  kDense2B, kDense08B, kDenseMini, kDenseTiny
+};
 
 template <class S>
 bool shape_is(const cq35_config& c) {
@@ -836,7 +841,25 @@ bool grid_fits(int grid) {
          S::SI / 2 <= grid && S::H / 2 <= nw;
 }
 
+template <class S>
+bool dense_shape_is(const cq35_config& c) {
+  return !c.moe && c.hidden == S::H && c.vocab == S::V && c.q_heads == S::Q && c.kv_heads == S::KVH &&
+         c.head_dim == S::HD && c.rope_dim == S::R && c.key_heads == S::KH && c.key_dim == S::KD &&
+         c.value_heads == S::VH && c.value_dim == S::VD && c.intermediate == S::I;
+}
+
+template <class S>
+bool dense_grid_fits(int grid) {
+  const int64_t nw = (int64_t)grid * kMW;
+  return S::VH <= grid && S::Q <= grid && S::H / 2 <= (int64_t)(kMW / 2) * grid &&
+         S::I <= kDenseFfnRows * nw;
+}
+
 int mega_kind(const cq35_config& c, int grid) {
+  if (dense_shape_is<ShapeDense2B>(c)) return dense_grid_fits<ShapeDense2B>(grid) ? kDense2B : kMegaNone;
+  if (dense_shape_is<ShapeDense08B>(c)) return dense_grid_fits<ShapeDense08B>(grid) ? kDense08B : kMegaNone;
+  if (dense_shape_is<ShapeDenseMini>(c)) return dense_grid_fits<ShapeDenseMini>(grid) ? kDenseMini : kMegaNone;
+  if (dense_shape_is<ShapeDenseTiny>(c)) return dense_grid_fits<ShapeDenseTiny>(grid) ? kDenseTiny : kMegaNone;
   if (shape_is<Shape35BA3B>(c)) return grid_fits<Shape35BA3B>(grid) ? kMega35B : kMegaNone;
   if (shape_is<ShapeMiniMoE>(c)) return grid_fits<ShapeMiniMoE>(grid) ? kMegaMini : kMegaNone;
   if (shape_is<ShapeTinyMoE>(c)) return grid_fits<ShapeTinyMoE>(grid) ? kMegaTiny : kMegaNone;
@@ -848,6 +871,10 @@ int mega_lds(int kind) {
     case kMega35B: return mega_lds_request<Shape35BA3B>();
     case kMegaMini: return mega_lds_request<ShapeMiniMoE>();
     case kMegaTiny: return mega_lds_request<ShapeTinyMoE>();
+    case kDense2B: return dense_lds_request<ShapeDense2B>();
+    case kDense08B: return dense_lds_request<ShapeDense08B>();
+    case kDenseMini: return dense_lds_request<ShapeDenseMini>();
+    case kDenseTiny: return dense_lds_request<ShapeDenseTiny>();
     default: return 0;
   }
 }
@@ -857,6 +884,10 @@ const void* mega_kernel(int kind) {
     case kMega35B: return (const void*)k_decode_step<Shape35BA3B>;
     case kMegaMini: return (const void*)k_decode_step<ShapeMiniMoE>;
     case kMegaTiny: return (const void*)k_decode_step<ShapeTinyMoE>;
+    case kDense2B: return (const void*)k_dense_step<ShapeDense2B>;
+    case kDense08B: return (const void*)k_dense_step<ShapeDense08B>;
+    case kDenseMini: return (const void*)k_dense_step<ShapeDenseMini>;
+    case kDenseTiny: return (const void*)k_dense_step<ShapeDenseTiny>;
     default: return nullptr;
   }
 }
@@ -872,6 +903,8 @@ int setup_mega(cq35_session* s) {
   const int kind = mega_kind(c, grid);
   const void* kernel = mega_kernel(kind);
   if (!kernel) return CQ35_OK;
+  const bool dense = !c.moe;
+  if (dense && s->capacity > kDenseKeys) return CQ35_OK;  // the softmax phase holds a head's scores in LDS
   const int lds = mega_lds(kind);
   if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
     return CQ35_OK;
@@ -881,17 +914,22 @@ int setup_mega(cq35_session* s) {
     return CQ35_OK;
   auto region = [](int64_t words) { return (words + 15) / 16 * 16; };
   const int64_t hw = region(d.H / 2);
-  std::vector<int64_t> offs;  // per layer: h, proj, mix, attn, router, active, scores, shared
+  // per layer: h, proj, mix, attn, router (dense: probabilities), active,
+  // scores, shared
+  std::vector<int64_t> offs;
   int64_t total = 0;
   for (int64_t l = 0; l < d.L; ++l) {
     const bool full = is_full(c, l);
-    const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS;
+    // dense linear layers also project alpha and beta (S32 rows)
+    const int64_t proj = full ? 2 * d.QS + 2 * d.KVS : d.QKV + d.VS + (dense ? 2 * c.value_heads : 0);
     // full layers: Q x capacity score words, or (split-K) per query head and
     // range the partial words (m, den, acc[HD])
     const int64_t scores = std::max<int64_t>(d.Q * s->capacity, d.Q * kSplitRanges * (2 + d.HD));
+    const int64_t probs = d.Q * (s->capacity / 2 + 1);
     const int64_t sizes[8] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
-                              region(d.E + 1), region(d.K * d.I / 2),
-                              full ? region(scores) : 0, region(d.SI / 2)};
+                              dense ? (full ? region(probs) : 0) : region(d.E + 1),
+                              region(dense ? d.I / 2 : d.K * d.I / 2),
+                              full ? region(scores) : 0, dense ? 0 : region(d.SI / 2)};
     for (int64_t z : sizes) {
       offs.push_back(total);
       total += z;
@@ -918,7 +956,8 @@ int setup_mega(cq35_session* s) {
     Ly.x_proj = s->words + o[1];
     Ly.x_mix = s->words + o[2];
     Ly.x_attn = s->words + o[3];
-    Ly.x_router = s->words + o[4];
+    Ly.x_router = dense ? nullptr : s->words + o[4];
+    Ly.x_probs = dense && Ly.full ? s->words + o[4] : nullptr;
     Ly.x_active = s->words + o[5];
     Ly.x_scores = s->words + o[6];
     Ly.x_shared = s->words + o[7];
@@ -938,6 +977,10 @@ int setup_mega(cq35_session* s) {
     } else {
       Ly.seg_w[0] = (const uint16_t*)W(1); Ly.seg_rows[0] = (int)d.QKV;
       Ly.seg_w[1] = (const uint16_t*)W(2); Ly.seg_rows[1] = (int)d.VS;
+      if (dense) {
+        Ly.seg_w[2] = (const uint16_t*)W(3); Ly.seg_rows[2] = c.value_heads;
+        Ly.seg_w[3] = (const uint16_t*)W(4); Ly.seg_rows[3] = c.value_heads;
+      }
       Ly.alpha_w = (const uint16_t*)W(3);
       Ly.beta_w = (const uint16_t*)W(4);
       Ly.dt = (const float*)W(5);
@@ -950,14 +993,21 @@ int setup_mega(cq35_session* s) {
       Ly.state_base = Ly.conv_base + d.CONV;
       ffn = 11;
     }
-    Ly.router = (const float*)W(ffn);
-    Ly.gate_exps = (const uint16_t*)W(ffn + 1);
-    Ly.up_exps = (const uint16_t*)W(ffn + 2);
-    Ly.down_exps = (const uint16_t*)W(ffn + 3);
-    Ly.shared_gate = (const float*)W(ffn + 4);
-    Ly.sgate = (const uint16_t*)W(ffn + 5);
-    Ly.sup = (const uint16_t*)W(ffn + 6);
-    Ly.sdown = (const uint16_t*)W(ffn + 7);
+    if (dense) {
+      // the dense SwiGLU in the shared-expert slots: gate, up, down
+      Ly.sgate = (const uint16_t*)W(ffn);
+      Ly.sup = (const uint16_t*)W(ffn + 1);
+      Ly.sdown = (const uint16_t*)W(ffn + 2);
+    } else {
+      Ly.router = (const float*)W(ffn);
+      Ly.gate_exps = (const uint16_t*)W(ffn + 1);
+      Ly.up_exps = (const uint16_t*)W(ffn + 2);
+      Ly.down_exps = (const uint16_t*)W(ffn + 3);
+      Ly.shared_gate = (const float*)W(ffn + 4);
+      Ly.sgate = (const uint16_t*)W(ffn + 5);
+      Ly.sup = (const uint16_t*)W(ffn + 6);
+      Ly.sdown = (const uint16_t*)W(ffn + 7);
+    }
     base += layer_tensors(c, l);
   }
   p = nullptr;

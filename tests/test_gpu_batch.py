@@ -27,9 +27,11 @@ def test_batch_matches_sessions_stepped_alone():
     say("batch of dense + MoE sessions")
     plan = [(dense, p) for p in prompts(dense.cfg, 4)] + [(moe, p) for p in prompts(moe.cfg, 3)]
     batch, alone, nxt_b, nxt_a = [], [], [], []
-    for m, p in plan:
+    for i, (m, p) in enumerate(plan):
         for group, nxt in ((batch, nxt_b), (alone, nxt_a)):
             s = m.session(64)
+            if i < 2:
+                s.set_persistent(False)  # two dense sessions on the per-kernel path
             nxt.append(s.append_next_token(p))
             group.append(s)
     assert nxt_b == nxt_a

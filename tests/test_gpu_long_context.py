@@ -107,11 +107,12 @@ def test_persistent_covers_every_capacity(models, name):
 @pytest.mark.parametrize("name,capacity,start,steps", [("tiny", 1100, 1020, 6), ("tiny", 2100, 2044, 6),
                                                        ("tiny", 5000, 4600, 2), ("qwen35-0.8b", 1400, 1290, 2)])
 def test_long_context_dense_against_oracle(models, oracle, name, capacity, start, steps):
-    """Dense shapes (per-kernel staged attention) from an imported state:
-    the steps cross the staging boundaries (512-key context chunks, 1024
-    keys = two keys per score thread, 2048 keys = the register path's limit;
-    above it the scores go through the scratch row), bit-exact against the
-    restatement."""
+    """Dense shapes from an imported state, bit-exact against the
+    restatement: the per-kernel staged attention across its staging
+    boundaries (512-key context chunks, 1024 keys = two keys per score
+    thread, 2048 keys = the register path's limit; above it the scores go
+    through the scratch row) and, up to its capacity bound, the persistent
+    step's score, softmax and context phases at the same contexts."""
     cfg = cc.preset(name)
     say("long context dense", name, "capacity", capacity, "start", start)
     state = seeded_state(cfg, capacity, start, seed=13, device="cpu")
@@ -119,6 +120,10 @@ def test_long_context_dense_against_oracle(models, oracle, name, capacity, start
     first = 23
     sb, cb = decode_from(m, state, capacity, start, first, steps, False)
     say("  per-kernel done")
+    persistent = capacity <= 8064  # the dense persistent step's capacity bound
+    if persistent:
+        sa, ca = decode_from(m, state, capacity, start, first, steps, True)
+        say("  persistent done")
     om = oracle.Model(cfg, oracle.synthetic_weights(cfg, 5))
     os_ = om.session(capacity)
     os_.import_cache(state)
@@ -129,6 +134,9 @@ def test_long_context_dense_against_oracle(models, oracle, name, capacity, start
     say("  oracle done")
     same_calls(name + " per-kernel/oracle", cb, co)
     assert np.array_equal(sb.export_state(0), os_.cache()), f"{name}: per-kernel state differs"
+    if persistent:
+        same_calls(name + " persistent/oracle", ca, co)
+        assert np.array_equal(sa.export_state(0), os_.cache()), f"{name}: persistent state differs"
 
 
 @pytest.mark.parametrize("capacity,start,split", [(4104, 4096, None), (70001, 69990, None),
