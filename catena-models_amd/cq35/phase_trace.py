@@ -3,6 +3,7 @@
     python -m cq35.phase_trace [--config qwen36-35b-a3b] [--context 512]
                                [--long 0] [--steps 8] [--build]
 
+Covers the MoE step (k_decode_step) and the dense step (k_dense_step).
 Uses the phase-trace build of the library (libcq35_trace.so, compiled with
 -DCQ35_PHASE_TRACE; --build or a missing file compiles it), decodes `steps`
 tokens after a `context`-token prompt (or, with --long N, from a seeded
@@ -45,12 +46,35 @@ MARKS = [(20, 0, "input row normalised"), (21, 1, "convolution done"), (22, 1, "
          (25, 5, "experts selected"), (26, 5, "outputs stored"), (27, 6, "staged weights and inputs in"),
          (28, 6, "outputs stored")]
 FULL = ["project", "scores", "values", "outproj", "router + shared", "select + gate/up", "down"]
+# dense_step.h (k_dense_step): p0 project, p1 delta or scores, p3 softmax +
+# context, p4 output projection, p5 gate/up, p6 down
+DENSE_LINEAR = ["project", "delta", None, None, "outproj", "gate/up", "down"]
+DENSE_FULL = ["project", "scores", None, "softmax + context", "outproj", "gate/up", "down"]
+DENSE_MARKS = [(20, 0, "input row normalised"), (21, 1, "convolution done"), (22, 1, "L2 norms and gates done"),
+               (23, 1, "state update done"), (29, 4, "outputs computed"), (24, 5, "post-mixer row normalised"),
+               (26, 5, "outputs stored")]
+# full layers of the dense step reuse slots 21-23 inside the attention phases
+DENSE_MARKS_FULL = [(20, 0, "input row normalised"), (21, 1, "heads prepared"), (22, 3, "softmax done"),
+                    (23, 3, "chains done"), (29, 4, "outputs computed"), (24, 5, "post-mixer row normalised"),
+                    (26, 5, "outputs stored")]
 
 
 def phase_bytes(cfg: dict, keys: int) -> dict:
     d = derived(cfg)
     H, VH, VD, KD = cfg["hidden"], cfg["value_heads"], cfg["value_dim"], cfg["key_dim"]
     K, I, SI, E = cfg["top_k"], cfg["intermediate"], cfg["shared_intermediate"], cfg["experts"]
+    if not E:
+        return {
+            ("lin", "project"): (d["qkv"] + d["value_size"] + 2 * VH) * H * 2,
+            ("full", "project"): (2 * d["query_size"] + 2 * d["kvs"]) * H * 2,
+            ("lin", "delta"): 2 * VH * VD * KD * 2 + 4 * d["qkv"] * 2,
+            ("full", "scores"): keys * d["kvs"] * 2,
+            ("full", "softmax + context"): keys * d["kvs"] * 2,
+            ("lin", "outproj"): H * d["value_size"] * 2,
+            ("full", "outproj"): H * d["query_size"] * 2,
+            ("gate/up",): 2 * I * H * 2,
+            ("down",): I * H * 2,
+        }
     return {
         ("lin", "project"): (d["qkv"] + d["value_size"] + 2 * VH) * H * 2,
         ("full", "project"): (2 * d["query_size"] + 2 * d["kvs"]) * H * 2,
@@ -79,10 +103,12 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
     per_layer = []
     prev_done = start
     roles = []
+    dense = not cfg.get("experts")
+    lin_names, full_names = (DENSE_LINEAR, DENSE_FULL) if dense else (LINEAR, FULL)
     for l in range(L):
         tb = l * TRACE_LAYER_SLOTS
         kind = "full" if is_full(cfg, l) else "lin"
-        names = FULL if kind == "full" else LINEAR
+        names = full_names if kind == "full" else lin_names
         layer_start = prev_done
         tl = timeline[kind]
         for p, name in enumerate(names):
@@ -94,7 +120,7 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
             inputs = (polled.max() - prev_done) if polled.size else 0
             if polled.size:
                 tl.setdefault((p, 0, name + ": inputs in"), []).append((polled.max() - layer_start) * TICK_US)
-            for slot, mp, label in MARKS:
+            for slot, mp, label in (MARKS if not dense else DENSE_MARKS_FULL if kind == "full" else DENSE_MARKS):
                 if mp == p:
                     v = trace[:, tb + slot]
                     v = v[v > 0]
@@ -107,7 +133,7 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
             r[2] += 1
             prev_done = done
         per_layer.append((l, kind, (prev_done - layer_start) * TICK_US))
-        if kind == "full":
+        if kind == "full" and not dense:
             if flash:
                 busy = trace[:, tb + 14:tb + 19].astype(np.float64)
                 busy = np.concatenate([busy[:, :4].mean(axis=0) * TICK_US, busy[:, :4].max(axis=0) * TICK_US,
@@ -118,7 +144,7 @@ def analyse(trace: np.ndarray, cfg: dict, keys: int, flash: bool = False) -> str
     head = (trace[:, TRACE_HEAD].max() - prev_done) * TICK_US
     total = (trace[:, TRACE_HEAD].max() - start) * TICK_US
     out = []
-    for kind, names, label in [("lin", LINEAR, "linear (DeltaNet) layer"), ("full", FULL, "full-attention layer")]:
+    for kind, names, label in [("lin", lin_names, "linear (DeltaNet) layer"), ("full", full_names, "full-attention layer")]:
         n = sum(1 for _, k, _ in per_layer if k == kind)
         if n == 0:
             continue

@@ -6,14 +6,15 @@
 //     alpha and beta included, over the input row normalised per block;
 //   * the Gated DeltaNet head step and the output projection of mega.h;
 //   * staged attention (qwen35.rs:722-790 over attention.hex:71-92 and
-//     qwen35_attention.hex:2-177, 258-393) as three phases: scalar-order
-//     scores of every (query head, key), the softmax of each head (a
-//     256-partial maximum and the adjacent-pair sum over the keys) and the
-//     context (eight interleaved chains per channel, the sigmoid gate);
+//     qwen35_attention.hex:2-177, 258-393) as two phases: scalar-order
+//     scores of every (query head, key), then per (head, channel chunk) the
+//     head's softmax (a 256-partial maximum and the adjacent-pair sum over
+//     the keys) and the context (eight interleaved chains per channel, the
+//     sigmoid gate);
 //   * the SwiGLU FFN: dual S256 gate/up (qwen3.fused.gate,
 //     simt.hex:539-646) and the S64 down projection with the residual.
-// Capacity is bounded (kDenseKeys) by the softmax phase, which holds a
-// head's scores in LDS; longer sessions use the per-kernel path.
+// Capacity is bounded (kDenseKeys) by the softmax, which holds a head's
+// scores in LDS; longer sessions use the per-kernel path.
 #pragma once
 
 #include "mega.h"
@@ -21,8 +22,8 @@
 namespace cq35 {
 
 // Largest session capacity of the dense persistent step: a head's scores
-// (F32) and 64-key nodes fit the big LDS area, and its probability words plus
-// the context item's 16 other words fit the polled-word area.
+// (F32) and 64-key nodes fit the big LDS area and its BF16 probabilities the
+// polled-word area.
 constexpr int kDenseKeys = 8064;
 constexpr int kDenseFfnRows = 3;  // SwiGLU rows per wave
 
@@ -49,9 +50,6 @@ using ShapeDense2B = DenseShape<2048, 248320, 8, 2, 256, 64, 16, 128, 32, 128, 6
 using ShapeDense08B = DenseShape<1024, 248320, 8, 2, 256, 64, 16, 128, 16, 128, 3584>;
 using ShapeDenseMini = DenseShape<512, 8192, 4, 2, 256, 64, 2, 128, 4, 128, 1408>;
 using ShapeDenseTiny = DenseShape<256, 4096, 4, 1, 64, 16, 4, 32, 8, 32, 768>;
-
-// Words of one head's probability pairs in x_probs.
-__device__ __forceinline__ int64_t dense_prob_stride(int64_t cap) { return cap / 2 + 1; }
 
 // ------------------------------------------------- phase: S32 projection
 
@@ -114,9 +112,11 @@ static_assert(offsetof(DenseScoreLds, qnat) % 16 == 0, "dense score LDS alignmen
 
 // Every block prepares all query and key heads (head RMS with the
 // adjacent-pair tree, neox RoPE; full_prepare.hex:3-82); block 0 appends the
-// new position's K and V to the cache. Then the (query head, key) items are
-// spread over all threads: score = bf16(serial chain over the head's
-// channels, element 0 first, x scale) (staged_score), one tagged word each in
+// new position's K and V to the cache. Then one (query head, 64-key chunk)
+// per wave, item i on wave i / grid of block i % grid (spread over the CUs,
+// so none streams more than a few key rows; the lanes share the query head,
+// an LDS broadcast): score = bf16(serial chain over the head's channels,
+// element 0 first, x scale) (staged_score), one tagged word each in
 // x_scores[head][key]. The new position's key row comes from LDS.
 template <class S>
 __device__ __forceinline__ void phase_dense_scores(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
@@ -169,162 +169,154 @@ __device__ __forceinline__ void phase_dense_scores(const MegaArgs* pa, uint32_t 
     G(a.cache)[Ly.value_base + position * S::KVS + m.tid] = in16[2 * QW + S::KVS + m.tid];
   }
   __syncthreads();
-  const int64_t total = (int64_t)Q * keys;
+  trace_mark(kMarkDeltaConv);  // full layers of the dense step: heads prepared
+  const int chunks = (int)((keys + 63) >> 6);
+  const int witems = Q * chunks;
 #pragma unroll 1
-  for (int64_t it = (int64_t)m.bid * kMT + m.tid; it < total; it += (int64_t)m.grid * kMT) {
-    const int hq = (int)(it / keys);
-    const int64_t key = it - (int64_t)hq * keys;
+  for (int wi = m.bid + m.grid * m.wave; wi < witems; wi += m.grid * kMW) {  // uniform per wave
+    const int hq = wi / chunks;
+    const int64_t key = (int64_t)(wi - hq * chunks) * 64 + m.lane;
     const int g = hq / HPK;
     const float* qf = s->qnat + hq * HD;
-    float acc;
-    if (key == position) {
-      acc = 0.0f;
-      for (int c = 0; c < HD; ++c) acc += qf[c] * bf2f(s->khat[g * HD + c]);
-    } else {
-      acc = staged_score(a.cache + Ly.key_base + key * S::KVS + g * HD, qf, HD);
-    }
-    word_store(Ly.x_scores + (int64_t)hq * a.cap + key, fbits(rbf(acc * a.attn_scale)), m.tag);
-  }
-}
-
-// ------------------------------------------- phase: staged attention softmax
-
-// Block b < Q: head b's scores (polled into LDS), the maximum (exact in any
-// order: wave reductions), then the adjacent-pair sum over the keys: its
-// first six levels (pairs within a 64-key group) across the lanes of a wave,
-// the rest over the 64-key nodes in LDS, the same additions as the
-// level-by-level loop; p = bf16(exp(s - max) / sum), two per tagged word.
-template <class S>
-__device__ __forceinline__ void phase_dense_softmax(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
-  const Mega m = make_mega(pa, tag);
-  const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const CQ35_CONST MegaArgs& a = m.a;
-  const int hq = m.bid;
-  if (hq >= S::Q) return;  // uniform per block
-  constexpr int KPT = (kDenseKeys + kMT - 1) / kMT;
-  const int64_t keys = (int64_t)G(a.params)[0] + 1;
-  float* sc = reinterpret_cast<float*>(m.big);
-  float* nodes = sc + kDenseKeys;
-  static_assert((kDenseKeys + kDenseKeys / 64) * 4 <= kLdsBigBytes, "dense softmax LDS");
-  poll_words<KPT>(m, (int)keys, Span{Ly.x_scores + (int64_t)hq * a.cap}, reinterpret_cast<uint32_t*>(sc));
-  const float ninf = bitsf(0xff800000u);
-  float sv[KPT];
-  float mx = ninf;
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const int64_t kk = m.tid + (int64_t)kMT * j;
-    sv[j] = kk < keys ? sc[kk] : ninf;
-    mx = fmaxf(mx, sv[j]);
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
-  if (m.lane == 0) m.misc->red[m.wave] = mx;
-  __syncthreads();
-  float maximum = m.misc->red[0];
-#pragma unroll
-  for (int w = 1; w < kMW; ++w) maximum = fmaxf(maximum, m.misc->red[w]);
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const int64_t base = (int64_t)kMT * j + 64 * m.wave, kk = base + m.lane;
-    if (base < keys) {  // uniform per wave
-      float e = kk < keys ? hexp(sv[j] - maximum) : 0.0f;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const float o = __shfl_down(e, d, 64);
-        if ((m.lane & (2 * d - 1)) == 0 && kk + d < keys) e += o;
+    if (key < keys) {
+      float acc;
+      if (key == position) {
+        acc = 0.0f;
+        for (int c = 0; c < HD; ++c) acc += qf[c] * bf2f(s->khat[g * HD + c]);
+      } else {
+        acc = staged_score(a.cache + Ly.key_base + key * S::KVS + g * HD, qf, HD);
       }
-      if (m.lane == 0) nodes[base >> 6] = e;
-    }
-  }
-  __syncthreads();
-  const int nn = (int)((keys + 63) >> 6);
-  for (int d = 1; d < nn; d <<= 1) {
-    for (int k2 = m.tid; k2 * 2 * d + d < nn; k2 += kMT) nodes[k2 * 2 * d] += nodes[k2 * 2 * d + d];
-    __syncthreads();
-  }
-  const float den = nodes[0];
-  uint64_t* out = Ly.x_probs + (int64_t)hq * dense_prob_stride(a.cap);
-#pragma unroll
-  for (int j = 0; j < KPT; ++j) {
-    const int64_t base = (int64_t)kMT * j + 64 * m.wave, kk = base + m.lane;
-    if (base < keys) {  // uniform per wave
-      const uint32_t p = kk < keys ? f2bf(hexp(sv[j] - maximum) / den) : 0u;
-      const uint32_t other = (uint32_t)__shfl_down((int)p, 1, 64);
-      if ((m.lane & 1) == 0 && kk < keys) word_store(out + (kk >> 1), pack_bf((uint16_t)p, (uint16_t)other), m.tag);
+      word_store(Ly.x_scores + (int64_t)hq * a.cap + key, fbits(rbf(acc * a.attn_scale)), m.tag);
     }
   }
 }
 
-// ------------------------------------------- phase: staged attention context
+// --------------------------------- phase: staged attention softmax + context
 
-// Item (query head, 16-channel chunk): the head's probabilities (polled into
-// LDS), its gate channels and the new position's value slice (projection
-// words); eight chains per channel over keys r, r + 8, ... in order (the
-// tail padded with + 0), combined ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)), then
-// bf16(bf16(sum) * sigmoid(gate)). Value slices (32 bytes per key) are staged
-// in LDS kContextKeys keys at a time, the next chunk's loads in flight while
-// threads tid < 128 (chain tid / 16, channel tid % 16) run the chains.
+constexpr int kAttendChannels = 8;   // channels per item
+constexpr int kAttendKeys = 1024;    // keys staged per chunk
+
+// Item (query head, 8-channel chunk), Q * HD / 8 items over the blocks. The
+// item's value slices (16 bytes per key) for its first two chunks are
+// requested first; then the block polls the head's scores into LDS and runs
+// the softmax (qwen35_attention.hex:258-393): the maximum (exact in any
+// order: wave reductions), the adjacent-pair sum over the keys (its first
+// six levels, pairs within a 64-key group, across the lanes of a wave; the
+// rest over the 64-key nodes in LDS; the same additions as the
+// level-by-level loop) and p = bf16(exp(s - max) / sum) into LDS. Then the
+// context (qwen35_attention.hex:2-177): per channel eight chains over keys
+// r, r + 8, ... in order (the tail padded with + 0) on threads tid < 64
+// (chain tid / 8, channel tid % 8), combined ((a0+a4)+(a2+a6))+
+// ((a1+a5)+(a3+a7)), then bf16(bf16(sum) * sigmoid(gate)) (qwen35.hex:
+// 207-222). Value slices are staged kAttendKeys keys at a time; the new
+// position's slice comes from the projection words. Every item of a head
+// repeats the head's softmax: it costs less than another exchange.
 template <class S>
-__device__ __forceinline__ void phase_dense_context(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
+__device__ __forceinline__ void phase_dense_attend(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
-  constexpr int HD = S::HD, Q = S::Q, HPK = Q / S::KVH, CH = kContextChannels, KC = kContextKeys;
+  constexpr int HD = S::HD, Q = S::Q, HPK = Q / S::KVH, CH = kAttendChannels, KC = kAttendKeys;
   constexpr int ITEMS = Q * HD / CH;
-  constexpr int VQ = 2 * KC, VPT = VQ / kMT;
-  static_assert(VQ % kMT == 0 && 2 * KC * CH * 2 + 8 * CH * 4 <= kLdsBigBytes, "dense context staging");
-  static_assert((kDenseKeys + 1) / 2 + CH <= 4096, "dense context words");
+  constexpr int VPT = KC / kMT;  // 16-byte slices per thread per chunk
+  constexpr int KPT = (kDenseKeys + kMT - 1) / kMT;
+  static_assert(KC % kMT == 0 && 2 * KC * CH * 2 + 8 * CH * 4 <= kLdsBigBytes, "attend staging");
+  static_assert((kDenseKeys + kDenseKeys / 64) * 4 <= kLdsBigBytes && kDenseKeys * 2 <= 4096 * 4, "attend LDS");
   const int64_t position = (int64_t)G(a.params)[0];
   const int64_t keys = position + 1;
-  const int np = (int)((keys + 1) >> 1);  // probability words
   const int64_t steps = (keys + 7) >> 3;
   const int nchunks = (int)((8 * steps + KC - 1) / KC);
-  uint16_t(*vs)[KC][CH] = reinterpret_cast<uint16_t(*)[KC][CH]>(m.big);
-  const int r = m.tid >> 4, x = m.tid & 15;
+  const float ninf = bitsf(0xff800000u);
+  const int r = m.tid >> 3, x = m.tid & 7;
 #pragma unroll 1
   for (int item = m.bid; item < ITEMS; item += m.grid) {
     const int hq = item / (HD / CH), c0 = (item - hq * (HD / CH)) * CH;
     const int g = hq / HPK;
-    const uint64_t* probs = Ly.x_probs + (int64_t)hq * dense_prob_stride(a.cap);
-    const uint64_t* gate = Ly.x_proj + ((hq * 2 * HD + HD + c0) >> 1);
-    const uint64_t* vnew = Ly.x_proj + ((2 * S::QS + S::KVS + g * HD + c0) >> 1);
     const uint16_t* vb = a.cache + Ly.value_base + (int64_t)g * HD + c0;
-    // chunk 0's value slices before the wait
-    u32x4 vr[VPT];
-    auto fetch = [&](int ch) {
+    u32x4 vr[2][VPT];
+    auto fetch = [&](u32x4 (&dst)[VPT], int ch) {
+      const int64_t k0 = (int64_t)ch * KC;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int64_t key = min(k0 + m.tid + kMT * i, position - 1 >= 0 ? position - 1 : 0);
+        dst[i] = *G(reinterpret_cast<const u32x4*>(vb + key * S::KVS));
+      }
+    };
+    fetch(vr[0], 0);
+    fetch(vr[1], min(1, nchunks - 1));
+    // the gate channels and the new position's value slice (4 words each)
+    uint32_t extra = 0;
+    if (m.tid < CH)
+      extra = poll_one(m, m.tid < CH / 2 ? Ly.x_proj + ((hq * 2 * HD + HD + c0) >> 1) + m.tid
+                                         : Ly.x_proj + ((2 * S::QS + S::KVS + g * HD + c0) >> 1) + (m.tid - CH / 2));
+    // softmax of head hq
+    float* sc = reinterpret_cast<float*>(m.big);
+    float* nodes = sc + kDenseKeys;
+    poll_words_upto<KPT>(m, (int)keys, Span{Ly.x_scores + (int64_t)hq * a.cap}, reinterpret_cast<uint32_t*>(sc));
+    uint16_t* p16 = reinterpret_cast<uint16_t*>(m.vec);
+    uint32_t* extra_lds = reinterpret_cast<uint32_t*>(m.misc->scalars);
+    if (m.tid < CH) extra_lds[m.tid] = extra;
+    float sv[KPT];
+    float mx = ninf;
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t kk = m.tid + (int64_t)kMT * j;
+      sv[j] = kk < keys ? sc[kk] : ninf;
+      mx = fmaxf(mx, sv[j]);
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+    if (m.lane == 0) m.misc->red[m.wave] = mx;
+    __syncthreads();
+    float maximum = m.misc->red[0];
+#pragma unroll
+    for (int w = 1; w < kMW; ++w) maximum = fmaxf(maximum, m.misc->red[w]);
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t base = (int64_t)kMT * j + 64 * m.wave, kk = base + m.lane;
+      if (base < keys) {  // uniform per wave
+        float e = kk < keys ? hexp(sv[j] - maximum) : 0.0f;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+          const float o = __shfl_down(e, d, 64);
+          if ((m.lane & (2 * d - 1)) == 0 && kk + d < keys) e += o;
+        }
+        if (m.lane == 0) nodes[base >> 6] = e;
+      }
+    }
+    __syncthreads();
+    const int nn = (int)((keys + 63) >> 6);
+    for (int d = 1; d < nn; d <<= 1) {
+      for (int k2 = m.tid; k2 * 2 * d + d < nn; k2 += kMT) nodes[k2 * 2 * d] += nodes[k2 * 2 * d + d];
+      __syncthreads();
+    }
+    const float den = nodes[0];
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int64_t kk = m.tid + (int64_t)kMT * j;
+      if (kk < keys) p16[kk] = f2bf(hexp(sv[j] - maximum) / den);
+    }
+    __syncthreads();  // probabilities in; the score area becomes the value staging
+    trace_mark(kMarkDeltaGates);  // full layers of the dense step: softmax done
+    uint16_t(*vs)[KC][CH] = reinterpret_cast<uint16_t(*)[KC][CH]>(m.big);
+    const uint32_t* vnw = extra_lds + CH / 2;  // the new value slice
+    auto put = [&](int buf, const u32x4 (&src)[VPT], int ch) {
       const int64_t k0 = (int64_t)ch * KC;
 #pragma unroll
       for (int i = 0; i < VPT; ++i) {
         const int idx = m.tid + kMT * i;
-        const int64_t key = min(k0 + (idx >> 1), position - 1 >= 0 ? position - 1 : 0);
-        vr[i] = *G(reinterpret_cast<const u32x4*>(vb + key * S::KVS + 8 * (idx & 1)));
+        const u32x4 v = k0 + idx == position ? u32x4{vnw[0], vnw[1], vnw[2], vnw[3]} : src[i];
+        *reinterpret_cast<u32x4*>(&vs[buf][idx][0]) = v;
       }
     };
-    fetch(0);
-    poll_words<(kDenseKeys / 2 + CH + kMT - 1) / kMT>(m, np + CH, [&](int i) {
-      return i < np ? probs + i : i < np + CH / 2 ? gate + (i - np) : vnew + (i - np - CH / 2);
-    }, m.vec);
-    const uint16_t* p16 = reinterpret_cast<const uint16_t*>(m.vec);
-    const uint32_t* vnw = m.vec + np + CH / 2;  // the new value slice (8 words, any alignment)
-    auto put = [&](int buf, int ch) {
-      const int64_t k0 = (int64_t)ch * KC;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int idx = m.tid + kMT * i;
-        // the new position's slice comes from the projection words
-        const int hw = 4 * (idx & 1);
-        const u32x4 v = k0 + (idx >> 1) == position ? u32x4{vnw[hw], vnw[hw + 1], vnw[hw + 2], vnw[hw + 3]} : vr[i];
-        reinterpret_cast<u32x4*>(&vs[buf][idx >> 1][0])[idx & 1] = v;
-      }
-    };
-    put(0, 0);
+    put(0, vr[0], 0);
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll 1
     for (int ch = 0; ch < nchunks; ++ch) {
       const int buf = ch & 1;
-      if (ch + 1 < nchunks) fetch(ch + 1);
-      if (m.tid < 128) {
+      if (ch + 1 < nchunks && ch > 0) fetch(vr[(ch + 1) & 1], ch + 1);  // chunk 1 is already in flight
+      if (m.tid < 64) {
         const int64_t k0 = (int64_t)ch * KC;
         const int n = (int)min<int64_t>(KC / 8, steps - k0 / 8);
 #pragma unroll 8
@@ -335,17 +327,19 @@ __device__ __forceinline__ void phase_dense_context(const MegaArgs* pa, uint32_t
           acc = acc + (kk < keys ? pv * vv : 0.0f);
         }
       }
-      if (ch + 1 < nchunks) put(buf ^ 1, ch + 1);
+      if (ch + 1 < nchunks) put(buf ^ 1, vr[(ch + 1) & 1], ch + 1);
       __syncthreads();
     }
+    trace_mark(kMarkDeltaState);  // full layers of the dense step: chains done
     float* part = reinterpret_cast<float*>(m.big + 2 * KC * CH * 2);
-    if (m.tid < 128) part[r * CH + x] = acc;
+    if (m.tid < 64) part[r * CH + x] = acc;
     __syncthreads();
     if (m.tid < CH) {
       const int t = m.tid;
       const float sum = ((part[0 * CH + t] + part[4 * CH + t]) + (part[2 * CH + t] + part[6 * CH + t])) +
                         ((part[1 * CH + t] + part[5 * CH + t]) + (part[3 * CH + t] + part[7 * CH + t]));
-      const uint16_t gb = p16[2 * np + t];
+      const uint32_t gw = extra_lds[t >> 1];
+      const uint16_t gb = (uint16_t)((t & 1) ? (gw >> 16) : (gw & 0xffffu));
       const uint32_t y = f2bf(rbf(sum) * sigmoid(bf2f(gb)));
       const uint32_t other = (uint32_t)__shfl_down((int)y, 1, 64);
       if ((t & 1) == 0) word_store(Ly.x_mix + ((hq * HD + c0 + t) >> 1), pack_bf((uint16_t)y, (uint16_t)other), m.tag);
@@ -435,7 +429,7 @@ constexpr int dense_lds_request() {
 }
 
 // Phase slots of the dense step's trace: p0 project, p1 delta or scores,
-// p2 softmax, p3 context, p4 output projection, p5 gate/up, p6 down.
+// p3 softmax + context, p4 output projection, p5 gate/up, p6 down.
 template <class S>
 __global__ __launch_bounds__(kMT) void k_dense_step(const MegaArgs* __restrict__ pa) {
   const uint32_t tag = (uint32_t)G(pa->params)[2];
@@ -470,12 +464,8 @@ __global__ __launch_bounds__(kMT) void k_dense_step(const MegaArgs* __restrict__
       phase_dense_scores<S>(pa, tag, ly);
       trace_max(tb + 2);
       __syncthreads();
-      trace_slot(tb + 5);
-      phase_dense_softmax<S>(pa, tag, ly);
-      trace_max(tb + 4);
-      __syncthreads();
       trace_slot(tb + 7);
-      phase_dense_context<S>(pa, tag, ly);
+      phase_dense_attend<S>(pa, tag, ly);
       trace_max(tb + 6);
       __syncthreads();
       trace_slot(tb + 9);

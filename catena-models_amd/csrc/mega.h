@@ -103,7 +103,6 @@ struct MegaLayer {
   uint64_t* x_active;  // routed activations (K*I/2)
   uint64_t* x_shared;  // shared-expert bf16(bf16(silu(g)) * u), before the gate (SI/2)
   uint64_t* x_scores;  // Q * capacity F32 scores (full layers)
-  uint64_t* x_probs;   // dense full layers: Q x (capacity/2 + 1) BF16 probability pairs
   uint64_t* x_out;     // output hidden row (H/2) = next layer's x_h
 };
 
@@ -366,6 +365,41 @@ __device__ __forceinline__ void poll_words(const Mega& m, int n, Addr addr, uint
 #pragma unroll
     for (int j = 0; j < MAXW; ++j) {
       const int i = min(m.tid + kMT * j, n - 1);
+      if (!word_ready(v[j], m.tag)) v[j] = word_load(addr(i));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+    const int i = m.tid + kMT * j;
+    if (i < n) dst[i] = (uint32_t)v[j];
+  }
+  __syncthreads();
+#ifdef CQ35_PHASE_TRACE
+  trace_max(m.misc->tslot);
+#endif
+}
+
+// poll_words for a word count far below MAXW * kMT: slots past n issue no
+// load (in poll_words they re-read word n - 1, which with many slots makes
+// every block hammer one line).
+template <int MAXW, typename Addr>
+__device__ __forceinline__ void poll_words_upto(const Mega& m, int n, Addr addr, uint32_t* dst) {
+  uint64_t v[MAXW];
+  const uint64_t done = (uint64_t)m.tag << 32;
+#pragma unroll
+  for (int j = 0; j < MAXW; ++j) {
+    const int i = m.tid + kMT * j;
+    v[j] = i < n ? word_load(addr(i)) : done;
+  }
+  unsigned spins = 0;
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) ready &= word_ready(v[j], m.tag);
+    if (ready || spin_stop(m, ++spins)) break;
+#pragma unroll
+    for (int j = 0; j < MAXW; ++j) {
+      const int i = m.tid + kMT * j;
       if (!word_ready(v[j], m.tag)) v[j] = word_load(addr(i));
     }
   }

@@ -850,9 +850,8 @@ bool dense_shape_is(const cq35_config& c) {
 
 template <class S>
 bool dense_grid_fits(int grid) {
-  const int64_t nw = (int64_t)grid * kMW;
   return S::VH <= grid && S::Q <= grid && S::H / 2 <= (int64_t)(kMW / 2) * grid &&
-         S::I <= kDenseFfnRows * nw;
+         S::I <= (int64_t)kDenseFfnRows * kMW * grid;
 }
 
 int mega_kind(const cq35_config& c, int grid) {
@@ -914,8 +913,7 @@ int setup_mega(cq35_session* s) {
     return CQ35_OK;
   auto region = [](int64_t words) { return (words + 15) / 16 * 16; };
   const int64_t hw = region(d.H / 2);
-  // per layer: h, proj, mix, attn, router (dense: probabilities), active,
-  // scores, shared
+  // per layer: h, proj, mix, attn, router, active, scores, shared
   std::vector<int64_t> offs;
   int64_t total = 0;
   for (int64_t l = 0; l < d.L; ++l) {
@@ -925,9 +923,8 @@ int setup_mega(cq35_session* s) {
     // full layers: Q x capacity score words, or (split-K) per query head and
     // range the partial words (m, den, acc[HD])
     const int64_t scores = std::max<int64_t>(d.Q * s->capacity, d.Q * kSplitRanges * (2 + d.HD));
-    const int64_t probs = d.Q * (s->capacity / 2 + 1);
     const int64_t sizes[8] = {hw, region(proj / 2), region((full ? d.QS : d.VS) / 2), hw,
-                              dense ? (full ? region(probs) : 0) : region(d.E + 1),
+                              dense ? 0 : region(d.E + 1),
                               region(dense ? d.I / 2 : d.K * d.I / 2),
                               full ? region(scores) : 0, dense ? 0 : region(d.SI / 2)};
     for (int64_t z : sizes) {
@@ -957,7 +954,6 @@ int setup_mega(cq35_session* s) {
     Ly.x_mix = s->words + o[2];
     Ly.x_attn = s->words + o[3];
     Ly.x_router = dense ? nullptr : s->words + o[4];
-    Ly.x_probs = dense && Ly.full ? s->words + o[4] : nullptr;
     Ly.x_active = s->words + o[5];
     Ly.x_scores = s->words + o[6];
     Ly.x_shared = s->words + o[7];
