@@ -146,9 +146,28 @@ __device__ __forceinline__ void phase_dense_scores(const MegaArgs* pa, uint32_t 
   };
   poll_words<(QW + 2 * KW + kMT - 1) / kMT>(m, QW + 2 * KW, [&](int i) { return proj + index(i); }, m.vec);
   const uint16_t* in16 = reinterpret_cast<const uint16_t*>(m.vec);
+  const int chunks = (int)((keys + 63) >> 6);
+  const int witems = Q * chunks;
+  // the heads this block needs: the query heads of its items, the key head
+  // of an item holding the new position (a head's last chunk) and, on block
+  // 0, every key head (the cache append)
   if (m.tid == 0) {
-    for (int hh = 0; hh < Q + KVH; ++hh) s->heads[hh] = hh;
-    s->nheads = Q + KVH;
+    int nh = 0;
+    auto add = [&](int hh) {
+      bool seen = false;
+      for (int i = 0; i < nh; ++i) seen |= s->heads[i] == hh;
+      if (!seen) s->heads[nh++] = hh;
+    };
+    for (int w = 0; w < kMW; ++w) {
+      const int wi = m.bid + m.grid * w;
+      if (wi >= witems) break;
+      const int hq = wi / chunks;
+      add(hq);
+      if (wi - hq * chunks == chunks - 1) add(Q + hq / HPK);
+    }
+    if (m.bid == 0)
+      for (int g = 0; g < KVH; ++g) add(Q + g);
+    s->nheads = nh;
   }
   if (m.tid < RH) {
     float sn, cs;
@@ -157,12 +176,13 @@ __device__ __forceinline__ void phase_dense_scores(const MegaArgs* pa, uint32_t 
     s->rope[RH + m.tid] = sn;
   }
   __syncthreads();
-  prepare_heads<S>(m, s, Q + KVH, qw_, kw_, [&](int hh) {
+  const int nheads = s->nheads;
+  prepare_heads<S>(m, s, nheads, qw_, kw_, [&](int hh) {
     return hh < Q ? in16 + hh * HD : in16 + 2 * QW + (hh - Q) * HD;
   }, [&](int hh) { return hh; });
-  for (int i = m.tid; i < Q * HD; i += kMT) {
-    const int hq = i / HD, c = i - hq * HD;
-    s->qnat[i] = s->qhat[hq * HD + (c & 31) * KJ + (c >> 5)];
+  for (int i = m.tid; i < nheads * HD; i += kMT) {
+    const int hq = s->heads[i / HD], c = i % HD;
+    if (hq < Q) s->qnat[hq * HD + c] = s->qhat[hq * HD + (c & 31) * KJ + (c >> 5)];
   }
   if (m.bid == 0 && m.tid < S::KVS) {
     G(a.cache)[Ly.key_base + position * S::KVS + m.tid] = s->khat[m.tid];
@@ -170,8 +190,6 @@ __device__ __forceinline__ void phase_dense_scores(const MegaArgs* pa, uint32_t 
   }
   __syncthreads();
   trace_mark(kMarkDeltaConv);  // full layers of the dense step: heads prepared
-  const int chunks = (int)((keys + 63) >> 6);
-  const int witems = Q * chunks;
 #pragma unroll 1
   for (int wi = m.bid + m.grid * m.wave; wi < witems; wi += m.grid * kMW) {  // uniform per wave
     const int hq = wi / chunks;
@@ -256,45 +274,65 @@ __device__ __forceinline__ void phase_dense_attend(const MegaArgs* pa, uint32_t 
     uint16_t* p16 = reinterpret_cast<uint16_t*>(m.vec);
     uint32_t* extra_lds = reinterpret_cast<uint32_t*>(m.misc->scalars);
     if (m.tid < CH) extra_lds[m.tid] = extra;
+    const int nk = (int)keys;
     float sv[KPT];
     float mx = ninf;
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int64_t kk = m.tid + (int64_t)kMT * j;
-      sv[j] = kk < keys ? sc[kk] : ninf;
+      const int kk = m.tid + kMT * j;
+      sv[j] = kk < nk ? sc[kk] : ninf;
       mx = fmaxf(mx, sv[j]);
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) mx = fmaxf(mx, __shfl_xor(mx, d, 64));
+    // wave maximum in lane 0 (its DPP reads never leave its rows)
+    mx = fmaxf(mx, lane_down<32>(mx));
+    mx = fmaxf(mx, lane_down<16>(mx));
+    mx = fmaxf(mx, lane_down<8>(mx));
+    mx = fmaxf(mx, lane_down<4>(mx));
+    mx = fmaxf(mx, lane_down<2>(mx));
+    mx = fmaxf(mx, lane_down<1>(mx));
     if (m.lane == 0) m.misc->red[m.wave] = mx;
     __syncthreads();
     float maximum = m.misc->red[0];
 #pragma unroll
     for (int w = 1; w < kMW; ++w) maximum = fmaxf(maximum, m.misc->red[w]);
+    // pair sums within each 64-key group: level d adds key k + d into key k
+    // (k a multiple of 2d) when k + d exists
+    auto group_levels = [&](float e, int kk, int limit) {
+      float o;
+      o = lane_down<1>(e);  if ((m.lane & 1) == 0 && kk + 1 < limit) e += o;
+      o = lane_down<2>(e);  if ((m.lane & 3) == 0 && kk + 2 < limit) e += o;
+      o = lane_down<4>(e);  if ((m.lane & 7) == 0 && kk + 4 < limit) e += o;
+      o = lane_down<8>(e);  if ((m.lane & 15) == 0 && kk + 8 < limit) e += o;
+      o = lane_down<16>(e); if ((m.lane & 31) == 0 && kk + 16 < limit) e += o;
+      o = lane_down<32>(e); if (m.lane == 0 && kk + 32 < limit) e += o;
+      return e;
+    };
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int64_t base = (int64_t)kMT * j + 64 * m.wave, kk = base + m.lane;
-      if (base < keys) {  // uniform per wave
-        float e = kk < keys ? hexp(sv[j] - maximum) : 0.0f;
-#pragma unroll
-        for (int d = 1; d < 64; d <<= 1) {
-          const float o = __shfl_down(e, d, 64);
-          if ((m.lane & (2 * d - 1)) == 0 && kk + d < keys) e += o;
-        }
+      const int base = kMT * j + 64 * m.wave, kk = base + m.lane;
+      if (base < nk) {  // uniform per wave
+        const float e = group_levels(kk < nk ? hexp(sv[j] - maximum) : 0.0f, kk, nk);
         if (m.lane == 0) nodes[base >> 6] = e;
       }
     }
     __syncthreads();
-    const int nn = (int)((keys + 63) >> 6);
-    for (int d = 1; d < nn; d <<= 1) {
-      for (int k2 = m.tid; k2 * 2 * d + d < nn; k2 += kMT) nodes[k2 * 2 * d] += nodes[k2 * 2 * d + d];
-      __syncthreads();
+    // levels 64 and up over the nodes (node n = keys 64n..), on wave 0: lane
+    // l holds nodes l and l + 64; the same levels, then node 0 += node 64
+    const int nn = (nk + 63) >> 6;
+    static_assert(kDenseKeys <= 128 * 64, "two nodes per lane");
+    if (m.wave == 0) {
+      float v0 = m.lane < nn ? nodes[m.lane] : 0.0f;
+      float v1 = m.lane + 64 < nn ? nodes[m.lane + 64] : 0.0f;
+      v0 = group_levels(v0, m.lane, nn);
+      v1 = group_levels(v1, m.lane + 64, nn);
+      if (m.lane == 0) m.misc->red[0] = nn > 64 ? v0 + v1 : v0;
     }
-    const float den = nodes[0];
+    __syncthreads();
+    const float den = m.misc->red[0];
 #pragma unroll
     for (int j = 0; j < KPT; ++j) {
-      const int64_t kk = m.tid + (int64_t)kMT * j;
-      if (kk < keys) p16[kk] = f2bf(hexp(sv[j] - maximum) / den);
+      const int kk = m.tid + kMT * j;
+      if (kk < nk) p16[kk] = f2bf(hexp(sv[j] - maximum) / den);
     }
     __syncthreads();  // probabilities in; the score area becomes the value staging
     trace_mark(kMarkDeltaGates);  // full layers of the dense step: softmax done
@@ -317,14 +355,19 @@ __device__ __forceinline__ void phase_dense_attend(const MegaArgs* pa, uint32_t 
       const int buf = ch & 1;
       if (ch + 1 < nchunks && ch > 0) fetch(vr[(ch + 1) & 1], ch + 1);  // chunk 1 is already in flight
       if (m.tid < 64) {
-        const int64_t k0 = (int64_t)ch * KC;
-        const int n = (int)min<int64_t>(KC / 8, steps - k0 / 8);
+        // chain r's keys k0 + 8 i + r; only the last step of all may be past the end
+        const int k0 = ch * KC;
+        const int n = min(KC / 8, (int)steps - k0 / 8);
+        const bool last = ch == nchunks - 1;
+        const int full = last ? n - 1 : n;
+        const uint16_t* pc = p16 + k0 + r;
+        const uint16_t* vc = &vs[buf][r][x];
 #pragma unroll 8
-        for (int i = 0; i < n; ++i) {
-          const int local = 8 * i + r;
-          const int64_t kk = k0 + local;
-          const float pv = bf2f(p16[kk < keys ? kk : 0]), vv = bf2f(vs[buf][local][x]);
-          acc = acc + (kk < keys ? pv * vv : 0.0f);
+        for (int i = 0; i < full; ++i) acc = acc + bf2f(pc[8 * i]) * bf2f(vc[8 * CH * i]);
+        if (last) {
+          const int kk = k0 + 8 * (n - 1) + r;
+          const float pv = bf2f(p16[kk < (int)keys ? kk : 0]), vv = bf2f(vc[8 * CH * (n - 1)]);
+          acc = acc + (kk < (int)keys ? pv * vv : 0.0f);
         }
       }
       if (ch + 1 < nchunks) put(buf ^ 1, vr[(ch + 1) & 1], ch + 1);
