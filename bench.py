@@ -376,6 +376,34 @@ def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: i
                                  path="the same step with its products on MFMA (tolerance-level)"))
 
 
+def dense_decode(config: str, context: int, steps: int, seed: int) -> dict:
+    """Batch-1 greedy decode of a dense configuration (the 0.8B and 2B
+    shapes): a `context`-token prompt in one call, two warm-up steps, then
+    `steps` timed decode steps; the roofline fraction is the algorithmic
+    bytes per token at the mean context over the step time."""
+    import cq35
+    cfg = cq35.preset(config)
+    model = cq35.Model.synthetic(cfg, seed=seed)
+    s = model.session(context + steps + 8)
+    x = s.append_next_token(synthetic_tokens(context, cfg["vocab"]))
+    for _ in range(2):
+        x = s.decode_next_token(x)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        x = s.decode_next_token(x)
+    device_sync()
+    dt = time.perf_counter() - t0
+    bpt = cq35.bytes_per_token(cfg, context + 2 + steps // 2)["total"]
+    gbs = bpt * steps / dt / 1e9
+    log(f"dense {config}: {steps / dt:.1f} tok/s batch 1 ({dt / steps * 1e3:.3f} ms/token, "
+        f"{gbs:.0f} GB/s of {bpt / 1e9:.3f} GB/token)")
+    return dict(config=config, context=context, steps=steps, tokens_per_s=round(steps / dt, 1),
+                ms_per_token=round(dt / steps * 1e3, 4), bytes_per_token=bpt, achieved_gbs=round(gbs, 1),
+                frac=round(gbs / HBM_PEAK_GBS, 4),
+                decode_path="persistent one-launch step" if s.persistent else "per-kernel launch sequence")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -412,6 +440,9 @@ def main() -> int:
                     help="sessions of the batch-16 leg (0 skips it)")
     ap.add_argument("--batch-config", default="qwen35-2b")
     ap.add_argument("--batch-steps", type=int, default=64)
+    ap.add_argument("--dense", default="qwen35-0.8b:512,qwen35-2b:1024",
+                    help="dense batch-1 decode legs, config:context pairs ('' for none)")
+    ap.add_argument("--dense-steps", type=int, default=256)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="first run one device copy of this size (counter calibration)")
     args = ap.parse_args()
@@ -554,6 +585,11 @@ def main() -> int:
     if args.batch_sessions > 0:
         batch = batch_sessions(args.batch_config, args.batch_sessions, 1024, args.batch_steps, args.seed)
 
+    dense = []
+    for item in filter(None, args.dense.split(",")):
+        name, ctx = item.split(":")
+        dense.append(dense_decode(name, int(ctx), args.dense_steps, args.seed))
+
     cpu = None
     if not args.no_cpu:
         need = model.weight_bytes()
@@ -594,6 +630,7 @@ def main() -> int:
                            frac=round(step_gbs / HBM_PEAK_GBS, 4)),
         roofline=roofline, kernels=kernels, cpu_baseline=cpu,
         prefill=prefill, long_context=long_ctx, concurrent_long_context=concurrent, batch_sessions=batch,
+        dense_decode=dense or None,
     )
     print(json.dumps(line))
     return 0
