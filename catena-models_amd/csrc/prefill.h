@@ -496,6 +496,95 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate(
   }
 }
 
+// k_bmoe_gate with the weights read once per chunk: the (token, slot)
+// assignments bucketed by expert (k_moe_bucket), block = kGRows rows of
+// expert blockIdx.y, each wave kGRowsPerWave of them with their gate and up
+// quads (lane + 64 j) held in registers, applied to the expert's tokens in
+// turn (the next token's input quads in flight). kShared: the shared expert
+// over tokens [16 blockIdx.y, +16). Per (token, row) the arithmetic is
+// k_bmoe_gate's: the B256 lane order over the quads, the tree and the
+// epilogue, so the results are the same bits.
+constexpr int kGRowsPerWave = 1;
+constexpr int kGRows = 4 * kGRowsPerWave;  // rows per block
+constexpr int kGSharedTokens = 16;
+
+template <int NQ, bool kShared>
+__global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
+    const uint16_t* __restrict__ x, int hidden, const uint16_t* __restrict__ gate,
+    const uint16_t* __restrict__ up, const int* __restrict__ eoff, const int* __restrict__ order,
+    const float* __restrict__ probs, const float* __restrict__ logits, int experts, int top_k, int inter,
+    int shared_inter, int n, uint16_t* __restrict__ active) {
+  constexpr int RW = kGRowsPerWave;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int width = kShared ? shared_inter : inter;
+  const int r0 = blockIdx.x * kGRows + RW * wave;
+  if (r0 >= width) return;  // wave-uniform
+  const int e = kShared ? 0 : blockIdx.y;
+  const int begin = kShared ? kGSharedTokens * blockIdx.y : eoff[e];
+  const int count = kShared ? min(kGSharedTokens, n - begin) : eoff[e + 1] - begin;
+  if (count <= 0) return;
+  const int quads = hidden >> 3;
+  const int rows = top_k * inter + shared_inter;
+  u32x4 gw[RW][NQ], uw[RW][NQ];
+#pragma unroll
+  for (int k = 0; k < RW; ++k) {
+    const int r = min(r0 + k, width - 1);
+    const size_t wrow = kShared ? (size_t)r : (size_t)e * inter + r;
+    const u32x4* gq = reinterpret_cast<const u32x4*>(gate + wrow * hidden);
+    const u32x4* uq = reinterpret_cast<const u32x4*>(up + wrow * hidden);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      gw[k][j] = gq[min(lane + 64 * j, quads - 1)];
+      uw[k][j] = uq[min(lane + 64 * j, quads - 1)];
+    }
+  }
+  auto token = [&](int i) { return kShared ? begin + i : order[begin + i] / top_k; };
+  auto load = [&](u32x4 (&xv)[NQ], int i) {
+    const u32x4* xq = reinterpret_cast<const u32x4*>(x + (size_t)token(min(i, count - 1)) * hidden);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) xv[j] = xq[min(lane + 64 * j, quads - 1)];
+  };
+  auto compute = [&](const u32x4 (&xv)[NQ], int i) {
+    const int a = kShared ? 0 : order[begin + i];
+    const int t = kShared ? begin + i : a / top_k;
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+      float ag[4] = {0.0f, 0.0f, 0.0f, 0.0f}, au[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int j = 0; j < NQ; ++j)
+        if (lane + 64 * j < quads) {
+          b256_acc(ag, xv[j], gw[k][j]);
+          b256_acc(au, xv[j], uw[k][j]);
+        }
+      const float g = b256_tree(ag);
+      const float u = b256_tree(au);
+      const int r = r0 + k;
+      if (lane == 0 && r < width) {
+        const float gb = rbf(g), ub = rbf(u);
+        const float activated = silu(gb);
+        if (kShared) {
+          const float shared_prob = sigmoid(logits[(size_t)t * (experts + 1) + experts]);
+          active[(size_t)t * rows + top_k * inter + r] = f2bf(rbf(rbf(activated) * ub) * shared_prob);
+        } else {
+          const int slot = a - t * top_k;
+          active[(size_t)t * rows + slot * inter + r] = f2bf((activated * ub) * probs[a]);
+        }
+      }
+    }
+  };
+  u32x4 xa[NQ], xb[NQ];
+  load(xa, 0);
+#pragma unroll 1
+  for (int i = 0; i < count; i += 2) {
+    load(xb, i + 1);
+    compute(xa, i);
+    if (i + 1 < count) {
+      load(xa, i + 2);
+      compute(xb, i + 1);
+    }
+  }
+}
+
 // Expert down of every token (batch.moe.down, batch_moe.hex:453-563): B256
 // over the K*I/2 routed pairs (pair p from expert ids[p / (I/2)], channel
 // p % (I/2)) with the shared pairs p < SI/2 accumulated in the same lanes,

@@ -1624,10 +1624,30 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
             dim3(kBlock), 0, (const float*)s->pf_part, (const float*)s->pf_spart,
             (const uint16_t*)s->pf_attn, H, K, s->pf_h);
         } else {
-          L(KC_MOE_GATE, k_bmoe_gate, dim3((unsigned)((rows + 3) / 4), rows_n), dim3(kBlock), 0,
-            (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
-            (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
-            (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
+          if (H <= 2048) {
+            // the gate/up rows read once per chunk: assignments bucketed by expert
+            L(KC_ROUTER, k_moe_bucket, dim3(1), dim3(1024), (size_t)E * 2 * sizeof(int),
+              (const int*)s->pf_ids, rows_n * K, E, s->pf_eoff, s->pf_order);
+            auto grouped = [&](auto routed, auto shared) {
+              L(KC_MOE_GATE, routed, dim3((unsigned)((I + kGRows - 1) / kGRows), (unsigned)E), dim3(kBlock), 0,
+                (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
+                (const int*)s->pf_eoff, (const int*)s->pf_order, (const float*)s->pf_probs,
+                (const float*)s->pf_logits, E, K, I, SI, rows_n, s->pf_act);
+              L(KC_MOE_GATE, shared,
+                dim3((unsigned)((SI + kGRows - 1) / kGRows), (unsigned)((rows_n + kGSharedTokens - 1) / kGSharedTokens)),
+                dim3(kBlock), 0, (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 5),
+                (const uint16_t*)W(ffn + 6), (const int*)s->pf_eoff, (const int*)s->pf_order,
+                (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, rows_n, s->pf_act);
+            };
+            if (H > 1024) grouped(k_bmoe_gate_grouped<4, false>, k_bmoe_gate_grouped<4, true>);
+            else if (H > 512) grouped(k_bmoe_gate_grouped<2, false>, k_bmoe_gate_grouped<2, true>);
+            else grouped(k_bmoe_gate_grouped<1, false>, k_bmoe_gate_grouped<1, true>);
+          } else {
+            L(KC_MOE_GATE, k_bmoe_gate, dim3((unsigned)((rows + 3) / 4), rows_n), dim3(kBlock), 0,
+              (const uint16_t*)s->pf_x, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2),
+              (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
+              (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
+          }
           L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)((H + 3) / 4), rows_n), dim3(kBlock), 0,
             (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
             (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, s->pf_h);
