@@ -275,10 +275,10 @@ def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, p
     del state
     log(f"concurrent long context: {sessions} sessions of {context} positions ready in {time.time() - t0:.1f}s")
     pre = model.session(prefill_tokens + 8)
-    pre.set_matrix_prefill(pre.MATRIX_PROJECTIONS | pre.MATRIX_EXPERTS)
+    pre.set_matrix_prefill(pre.MATRIX_PROJECTIONS | pre.MATRIX_EXPERTS | pre.MATRIX_ATTENTION)
     prompt = synthetic_tokens(prefill_tokens + 1, cfg["vocab"])[1:]
     warm = model.session(chunk + 1)  # the chunk kernels' first launch, outside the timing
-    warm.set_matrix_prefill(warm.MATRIX_PROJECTIONS | warm.MATRIX_EXPERTS)
+    warm.set_matrix_prefill(warm.MATRIX_PROJECTIONS | warm.MATRIX_EXPERTS | warm.MATRIX_ATTENTION)
     warm.append_next_token(prompt[:chunk])
     del warm
     nxt = [1000 + 17 * b for b in range(sessions)]
@@ -308,7 +308,7 @@ def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, p
                 decode_step_roofline_frac=round(bpt["total"] * sessions * steps / decode_s / 1e9 / HBM_PEAK_GBS, 4),
                 prefill=dict(tokens=prefill_tokens, chunk=chunk, seconds=round(prefill_s, 3),
                              tokens_per_s=round(prefill_tokens / prefill_s, 1),
-                             path="matrix-core prefill (MFMA projections and experts), one call per round"),
+                             path="matrix-core prefill (MFMA projections, experts and attention), one call per round"),
                 state="seeded: KV N(0,1) x 0.1, conv history N(0,1) x 0.1, DeltaNet state N(0,1); one state "
                       "imported into every session",
                 decode_path="cq35_step_batch: persistent steps one session at a time (each needs every CU)")
@@ -496,10 +496,10 @@ def main() -> int:
         # the same prompt on a second session with the matrix-core components
         # (MFMA accumulation order; the decode below runs on the exact session)
         ms_ = model.session(args.context + 1)
-        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS)
+        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS | ms_.MATRIX_ATTENTION)
         ms_.append_next_token(tokens[:args.context])  # warm the kernels
         ms_ = model.session(args.context + 1)
-        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS)
+        ms_.set_matrix_prefill(ms_.MATRIX_PROJECTIONS | ms_.MATRIX_EXPERTS | ms_.MATRIX_ATTENTION)
         device_sync()
         t0 = time.perf_counter()
         ms_.append_next_token(tokens[:args.context])
@@ -507,7 +507,7 @@ def main() -> int:
         mp_s = time.perf_counter() - t0
         del ms_
         prefill["matrix_core"] = dict(seconds=round(mp_s, 4), tokens_per_s=round(args.context / mp_s, 1),
-                                      components="projections+experts (MFMA accumulation order)")
+                                      components="projections+experts+attention (MFMA accumulation order)")
         log(f"prompt of {args.context} tokens, matrix-core prefill: {mp_s:.3f}s")
     # `runs` timed runs (the reference's --bench-runs, main.rs:459-471): each
     # a fresh session with the prompt, W untimed then K timed greedy steps;

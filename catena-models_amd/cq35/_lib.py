@@ -73,6 +73,8 @@ def load():
         "cq35_device_gemv": ([P, P, I64, I64, ctypes.c_int, P], ctypes.c_int),
         "cq35_device_matrix_gemm": ([P, P, P, P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P],
                                     ctypes.c_int),
+        "cq35_device_matrix_attention": ([P, P, P, P, I64, I64, ctypes.c_int, ctypes.c_int, ctypes.c_int, P],
+                                         ctypes.c_int),
         "cq35_step_batch": ([ctypes.POINTER(P), P, P, I64, P, P], ctypes.c_int),
         "cq35_gguf_config": ([ctypes.c_char_p, PC], ctypes.c_int),
         "cq35_gguf_validate": ([ctypes.c_char_p, PC], ctypes.c_int),
@@ -107,6 +109,7 @@ EXPORTED = [
     "cq35_session_set_matrix_prefill", "cq35_session_matrix_prefill",
     "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
     "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv", "cq35_device_matrix_gemm",
+    "cq35_device_matrix_attention",
     "cq35_gguf_config", "cq35_gguf_validate", "cq35_model_load_gguf", "cq35_gguf_tensor_name",
     "cq35_step_batch", "cq35_step_static", "cq35_session_set_attention_split",
     "cq35_session_attention_split", "cq35_session_phase_trace",

@@ -306,6 +306,7 @@ class Session:
 
     MATRIX_PROJECTIONS = 1
     MATRIX_EXPERTS = 2
+    MATRIX_ATTENTION = 4
 
     def set_attention_split(self, keys: int) -> None:
         """Decode attention over more than `keys` cached keys as at most 128
@@ -323,7 +324,8 @@ class Session:
     def set_matrix_prefill(self, components: int) -> None:
         """Run these components of multi-token calls on MFMA (hardware
         accumulation order; 0 = the exact SIMT path): MATRIX_PROJECTIONS,
-        MATRIX_EXPERTS or both (the reference's wmma_prefill scopes)."""
+        MATRIX_EXPERTS, MATRIX_ATTENTION or any combination (the reference's
+        wmma_prefill scopes)."""
         check(_lib.load().cq35_session_set_matrix_prefill(self._h, int(components)))
 
     @property

@@ -709,4 +709,235 @@ __global__ __launch_bounds__(kBlock) void k_moe_combine(const float* __restrict_
   }
 }
 
+// Matrix-core attention of the prompt path: the attention component of the
+// reference's matrix-core prefill (CATENA_WMMA_COMPONENTS "attention",
+// qwen35.rs:467-503 over qwen35_wmma_attention.hex), with its rounding
+// points: the score bf16(q.k * scale) with q.k on the matrix cores and keys
+// after the query's position at -inf (score-write, :3-22); probabilities
+// bf16(exp(s - max) / den) over the row's maximum and exponential sum
+// (softmax.write, :242-258; a masked score contributes 0); the context summed
+// on the matrix cores from those BF16 probabilities and written as
+// bf16(bf16(ctx) * sigmoid(gate)) (context-write, :503-530). The F32 sums
+// inside the products and of the denominator run in orders of their own, the
+// exponentials are the hardware's 2^x (about 1 ulp from the reference's exp)
+// and a probability is its exponential times the reciprocal of the
+// denominator (within 1 ulp of the quotient): F32-level differences under
+// the BF16 rounding points, a tolerance-level path as the reference's own
+// matrix-core path is.
+//
+// Block = (query head, 32 consecutive rows of the chunk), kAWaves waves; the
+// 32-key tiles up to the last row's position are dealt to the waves round
+// robin. Pass 1: each wave forms its tiles' scores S^T = K Q^T (A = the 32
+// key rows, B = the 32 query rows, both as 16-byte fragments along the head
+// dimension; lane l then holds 16 keys of query l % 32) and keeps a running
+// maximum and exponential sum per query; the waves' pairs are merged in wave
+// order. Pass 2 recomputes the same scores (same products, same bits), turns
+// them into BF16 probabilities, which sit in the registers as the B operand
+// of O^T = V^T P^T, and accumulates the context per 32-channel tile. V^T is
+// an LDS transpose of the tile's value rows: key pairs packed into 32-bit
+// words, positions within each 16 keys with index bits 2 and 3 swapped so
+// that a lane's 8 A elements are the 8 keys of its probability registers.
+// The waves' context partials are added in wave order through LDS.
+constexpr int kAWaves = 4;
+constexpr int kAVWords = 18;  // words per transposed value row: 16 key pairs + 2 (72 B, conflict-free stores)
+
+// e^x through the hardware's 2^x (v_exp_f32, about 1 ulp; 2^-inf = 0): the
+// probabilities' exponentials of the matrix-core attention only.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504f); }
+
+template <int HD>
+__global__ __launch_bounds__(64 * kAWaves) void k_mattention(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ qg, const uint16_t* __restrict__ cache,
+    int64_t key_base, int64_t value_base, const uint64_t* __restrict__ params, int t, int rows_n, int kvs,
+    int heads, int heads_per_kv, float scale, uint16_t* __restrict__ out) {
+  static_assert(HD % 64 == 0 && HD <= 256, "head dims of whole 64-channel pairs of tiles");
+  constexpr int KS = HD / 16;  // k steps of a score product
+  constexpr int CT = HD / 32;  // 32-channel tiles of the context
+  constexpr int PU = HD / 32;  // (key pair, 8-channel group) units of a value tile per lane
+  __shared__ __align__(16) uint32_t vt[kAWaves][HD][kAVWords];
+  __shared__ float mstat[kAWaves][32], dstat[kAWaves][32];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 31, h = lane >> 5;
+  const int head = blockIdx.x, r0 = blockIdx.y * 32;
+  const int64_t qs = (int64_t)heads * HD;
+  const int row = min(r0 + c, rows_n - 1);
+  const int64_t pos = step_position(params, t + row);
+  const int64_t last = step_position(params, t + min(r0 + 31, rows_n - 1));
+  const int tiles = (int)(last >> 5) + 1;
+  const int64_t kvoff = (int64_t)(head / heads_per_kv) * HD;
+  const float ninf = bitsf(0xff800000u);
+  u32x4 qf[KS];
+  {
+    const uint16_t* qr = q + row * qs + head * HD + 8 * h;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[s] = *reinterpret_cast<const u32x4*>(qr + 16 * s);
+  }
+  // key rows past the last row's position read that position's row (masked)
+  const uint16_t* kb = cache + key_base + kvoff + 8 * h;
+  u32x4 kf[KS];
+  auto load_keys = [&](int j) {
+    const uint16_t* kr = kb + min((int64_t)32 * j + c, last) * kvs;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kf[s] = *reinterpret_cast<const u32x4*>(kr + 16 * s);
+  };
+  // register r: key 32 j + 8 (r / 4) + 4 h + r % 4 of query row r0 + c
+  auto scores = [&](int j, f32x16_t& sc) {
+    f32x16_t acc = {};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = mfma32(kf[s], qf[s], acc);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t key = 32 * (int64_t)j + 8 * (r >> 2) + 4 * h + (r & 3);
+      sc[r] = key <= pos ? rbf(acc[r] * scale) : ninf;
+    }
+  };
+  // pass 1: running maximum and exponential sum per query
+  float m = ninf, den = 0.0f;
+  if (wave < tiles) load_keys(wave);
+#pragma unroll 1
+  for (int j = wave; j < tiles; j += kAWaves) {
+    f32x16_t sc;
+    scores(j, sc);
+    if (j + kAWaves < tiles) load_keys(j + kAWaves);
+    float tm = sc[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) tm = fmaxf(tm, sc[r]);
+    tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+    const float mn = fmaxf(m, tm);
+    float e = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) e += sc[r] == ninf ? 0.0f : fast_exp(sc[r] - mn);
+    e += __shfl_xor(e, 32, 64);  // the same sum in both halves (addition commutes)
+    den = (m == ninf ? 0.0f : den * fast_exp(m - mn)) + e;
+    m = mn;
+  }
+  if (h == 0) {
+    mstat[wave][c] = m;
+    dstat[wave][c] = den;
+  }
+  __syncthreads();
+  float M = mstat[0][c];
+#pragma unroll
+  for (int w = 1; w < kAWaves; ++w) M = fmaxf(M, mstat[w][c]);
+  float D = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kAWaves; ++w)
+    if (mstat[w][c] != ninf) D += dstat[w][c] * fast_exp(mstat[w][c] - M);
+  const float rD = 1.0f / D;
+  // pass 2: probabilities and the context
+  uint32_t* vw = &vt[wave][0][0];
+  const uint16_t* vb = cache + value_base + kvoff;
+  u32x4 vv[PU][2];
+  auto load_values = [&](int j) {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int pu = lane + 64 * u, kp = pu & 15, cg = pu >> 4;
+      const int64_t k0 = 32 * (int64_t)j + 2 * kp;
+      vv[u][0] = *reinterpret_cast<const u32x4*>(vb + min(k0, last) * kvs + 8 * cg);
+      vv[u][1] = *reinterpret_cast<const u32x4*>(vb + min(k0 + 1, last) * kvs + 8 * cg);
+    }
+  };
+  auto store_values = [&]() {
+#pragma unroll
+    for (int u = 0; u < PU; ++u) {
+      const int pu = lane + 64 * u, kp = pu & 15, cg = pu >> 4;
+      const int k = 2 * kp;
+      const int p = (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);  // bits 2 and 3 swapped
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t a = vv[u][0][i >> 1], b = vv[u][1][i >> 1];
+        const uint32_t lo = (i & 1) ? a >> 16 : a & 0xffffu;
+        const uint32_t hi = (i & 1) ? b & 0xffff0000u : b << 16;
+        vw[(8 * cg + i) * kAVWords + (p >> 1)] = lo | hi;
+      }
+    }
+  };
+  f32x16_t o[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) o[ct] = f32x16_t{};
+  if (wave < tiles) {
+    load_keys(wave);
+    load_values(wave);
+  }
+#pragma unroll 1
+  for (int j = wave; j < tiles; j += kAWaves) {
+    f32x16_t sc;
+    scores(j, sc);
+    const bool more = j + kAWaves < tiles;
+    if (more) load_keys(j + kAWaves);
+    u32x4 pb[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 8 * ks + 2 * i;
+        const uint32_t p0 = sc[r] == ninf ? 0u : f2bf(fast_exp(sc[r] - M) * rD);
+        const uint32_t p1 = sc[r + 1] == ninf ? 0u : f2bf(fast_exp(sc[r + 1] - M) * rD);
+        pb[ks][i] = p0 | (p1 << 16);
+      }
+    store_values();
+    if (more) load_values(j + kAWaves);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint32_t* src = vw + (32 * ct + c) * kAVWords + 8 * ks + 4 * h;
+        const uint2 x0 = *reinterpret_cast<const uint2*>(src), x1 = *reinterpret_cast<const uint2*>(src + 2);
+        const u32x4 a = {x0.x, x0.y, x1.x, x1.y};
+        o[ct] = mfma32(a, pb[ks], o[ct]);
+      }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // waves' partials added in wave order, one half of the channel tiles at a
+  // time (every wave's partials of a half fit the value tiles' LDS); wave w
+  // finishes tiles w, w + kAWaves, ... of the half. The half is a compile-time
+  // constant so that the accumulators stay in registers.
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&vt[0][0][0]);
+  constexpr int HT = CT / 2;
+  static_assert(kAWaves * HT * 16 * 64 * 4 <= (int)sizeof(vt), "partials fit the value tiles");
+  const int rr = r0 + c;
+  auto finish = [&](auto half_c) {
+    constexpr int half = decltype(half_c)::value;
+#pragma unroll
+    for (int i = 0; i < HT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wave * HT + i) * 16 + r) * 64 + lane] = o[half * HT + i][r];
+    __syncthreads();
+    if (rr < rows_n) {
+      const uint16_t* gate = qg + (int64_t)rr * 2 * qs + (int64_t)head * 2 * HD + HD;
+      uint16_t* dst = out + (int64_t)rr * qs + (int64_t)head * HD;
+      for (int i = wave; i < HT; i += kAWaves) {
+        const int ct = half * HT + i;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = 32 * ct + 8 * g + 4 * h;
+          const uint2 gv = *reinterpret_cast<const uint2*>(gate + ch);
+          uint32_t packed[2];
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            uint32_t two = 0;
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              const int r = 4 * g + e + x;
+              float v = red[(i * 16 + r) * 64 + lane];
+#pragma unroll
+              for (int w = 1; w < kAWaves; ++w) v += red[((w * HT + i) * 16 + r) * 64 + lane];
+              const uint32_t gw = e == 0 ? gv.x : gv.y;
+              const float gs = sigmoid(bf2f((uint16_t)(x ? gw >> 16 : gw & 0xffffu)));
+              two |= (uint32_t)f2bf(rbf(v) * gs) << (16 * x);
+            }
+            packed[e >> 1] = two;
+          }
+          *reinterpret_cast<uint2*>(dst + ch) = make_uint2(packed[0], packed[1]);
+        }
+      }
+    }
+    __syncthreads();
+  };
+  finish(std::integral_constant<int, 0>{});
+  finish(std::integral_constant<int, 1>{});
+}
+
 }  // namespace cq35

@@ -1538,15 +1538,26 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
           (const float*)s->pf_rope, (const float*)W(5), (const float*)W(6), s->cache, key_base,
           value_base, params, first, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, qr, (const SessionRows*)nullptr);
         const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
-        for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
-          const int am = std::min(s->pf_attn_tokens, rows_n - a0);
-          L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kStagedThreads), 0,
-            (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
-            first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
-          L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
-            dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
-            (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
-            (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS, (const SessionRows*)nullptr);
+        auto mattention = [&](auto kernel) {
+          L(KC_ATTENTION, kernel, dim3((unsigned)d.Q, (unsigned)((rows_n + 31) / 32)), dim3(64 * kAWaves), 0,
+            (const uint16_t*)qr, (const uint16_t*)qg, (const uint16_t*)s->cache, key_base, value_base, params,
+            first, rows_n, (int)d.KVS, (int)d.Q, (int)(d.Q / d.KVH), scale, ctx);
+        };
+        const bool ma = (s->matrix & CQ35_MATRIX_ATTENTION) != 0;
+        if (ma && d.HD == 256) mattention(k_mattention<256>);
+        else if (ma && d.HD == 128) mattention(k_mattention<128>);
+        else if (ma && d.HD == 64) mattention(k_mattention<64>);
+        else {  // the exact staged kernels
+          for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
+            const int am = std::min(s->pf_attn_tokens, rows_n - a0);
+            L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kStagedThreads), 0,
+              (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
+              first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
+            L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
+              dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
+              (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
+              (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS, (const SessionRows*)nullptr);
+          }
         }
         residual_rows(ctx, (int)d.QS, W(4), s->pf_h, s->pf_attn);
         post_norm = W(7);
@@ -1825,7 +1836,7 @@ extern "C" int cq35_session_phase_trace(const cq35_session* s, uint64_t* dst, in
 
 extern "C" int cq35_session_set_matrix_prefill(cq35_session* s, int components) {
   if (!s) return fail(CQ35_EINVAL, "null argument");
-  if (components & ~(CQ35_MATRIX_PROJECTIONS | CQ35_MATRIX_EXPERTS))
+  if (components & ~(CQ35_MATRIX_PROJECTIONS | CQ35_MATRIX_EXPERTS | CQ35_MATRIX_ATTENTION))
     return fail(CQ35_EINVAL, "unknown matrix-core prefill components %d", components);
   s->matrix = components;
   return CQ35_OK;
@@ -2576,6 +2587,49 @@ extern "C" int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, con
   for (uint16_t* p : {dx, dw, dw2, dres, dout})
     if (p) hipFree(p);
   if (e != hipSuccess) return fail(CQ35_EDEVICE, "device matrix GEMM: %s", hipGetErrorString(e));
+  return CQ35_OK;
+}
+
+extern "C" int cq35_device_matrix_attention(const uint16_t* q, const uint16_t* gate, const uint16_t* k,
+                                            const uint16_t* v, int64_t n, int64_t start, int heads,
+                                            int kv_heads, int head_dim, uint16_t* out) {
+  if (!q || !gate || !k || !v || !out || n <= 0 || start < 0 || n + start > (1 << 20) || heads <= 0 ||
+      kv_heads <= 0 || heads > 256 || heads % kv_heads || (head_dim != 64 && head_dim != 128 && head_dim != 256))
+    return fail(CQ35_EINVAL, "bad matrix attention shape");
+  const int64_t keys = start + n, qs = (int64_t)heads * head_dim, kvs = (int64_t)kv_heads * head_dim;
+  uint16_t *dq = nullptr, *dqg = nullptr, *dcache = nullptr, *dout = nullptr;
+  uint64_t* dparams = nullptr;
+  const uint64_t first_position = (uint64_t)start;
+  hipError_t e = hipMalloc(&dq, n * qs * 2);
+  if (e == hipSuccess) e = hipMalloc(&dqg, n * 2 * qs * 2);
+  if (e == hipSuccess) e = hipMalloc(&dcache, 2 * keys * kvs * 2);
+  if (e == hipSuccess) e = hipMalloc(&dout, n * qs * 2);
+  if (e == hipSuccess) e = hipMalloc(&dparams, sizeof(uint64_t));
+  if (e == hipSuccess) e = hipMemcpy(dq, q, n * qs * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemset(dqg, 0, n * 2 * qs * 2);
+  // the projection layout [row][head][q | gate]: gates into the second halves
+  if (e == hipSuccess)
+    e = hipMemcpy2D(dqg + head_dim, 2 * head_dim * 2, gate, head_dim * 2, head_dim * 2, n * heads,
+                    hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dcache, k, keys * kvs * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dcache + keys * kvs, v, keys * kvs * 2, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dparams, &first_position, sizeof(uint64_t), hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    const dim3 grid((unsigned)heads, (unsigned)((n + 31) / 32));
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    auto run = [&](auto kernel) {
+      kernel<<<grid, 64 * kAWaves>>>(dq, dqg, dcache, 0, keys * kvs, dparams, 0, (int)n, (int)kvs, heads,
+                                     heads / kv_heads, scale, dout);
+    };
+    if (head_dim == 256) run(k_mattention<256>);
+    else if (head_dim == 128) run(k_mattention<128>);
+    else run(k_mattention<64>);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpy(out, dout, n * qs * 2, hipMemcpyDeviceToHost);
+  for (void* p : {(void*)dq, (void*)dqg, (void*)dcache, (void*)dout, (void*)dparams})
+    if (p) hipFree(p);
+  if (e != hipSuccess) return fail(CQ35_EDEVICE, "device matrix attention: %s", hipGetErrorString(e));
   return CQ35_OK;
 }
 

@@ -20,6 +20,7 @@ pub const CQ35_EUNSUPPORTED: c_int = -4;
 pub const CQ35_EPOISONED: c_int = -5;
 pub const CQ35_MATRIX_PROJECTIONS: c_int = 1;
 pub const CQ35_MATRIX_EXPERTS: c_int = 2;
+pub const CQ35_MATRIX_ATTENTION: c_int = 4;
 pub const CQ35_SPLIT_KEYS_DEFAULT: i64 = 8192;
 
 /// The ModelConfig fields the token loop reads (src/spec.rs:33-62), in the

@@ -233,7 +233,10 @@ int cq35_session_persistent(const cq35_session* session, int* enabled);
  * qwen35.rs:467-541; default off in its library API, as here). Bit 0: the
  * dense projections (attention, DeltaNet and output projections, dense FFN);
  * bit 1: the MoE expert projections (grouped routed experts and the shared
- * expert). 0 keeps the exact SIMT path. A session whose components are set
+ * expert); bit 2: the full-attention layers' attention over the prompt rows
+ * (scores and context on MFMA with the reference's BF16 score, probability
+ * and context rounding, qwen35_wmma_attention.hex; head_dim 64, 128 or 256,
+ * other head dims keep the exact kernels). 0 keeps the exact SIMT path. A session whose components are set
  * at its first multi-token call runs multi-token calls in chunks of 1024
  * tokens (otherwise 256; the chunk changes no result). Single-session decode
  * steps are unaffected; the weight-shared batched step (cq35_step_batch)
@@ -254,6 +257,7 @@ int cq35_session_attention_split(const cq35_session* session, int64_t* keys);
 
 #define CQ35_MATRIX_PROJECTIONS 1
 #define CQ35_MATRIX_EXPERTS 2
+#define CQ35_MATRIX_ATTENTION 4
 int cq35_session_set_matrix_prefill(cq35_session* session, int components);
 int cq35_session_matrix_prefill(const cq35_session* session, int* components);
 
@@ -278,6 +282,17 @@ int cq35_device_gemv(const uint16_t* x, const uint16_t* w, int64_t rows, int64_t
 int cq35_device_matrix_gemm(const uint16_t* x, const uint16_t* w, const uint16_t* w2,
                             const uint16_t* res, int64_t n, int64_t rows, int64_t cols, int mode,
                             int kernel, uint16_t* out);
+/* Device matrix-core attention of the prompt path (CQ35_MATRIX_ATTENTION's
+ * kernel) over host arrays: n query rows at positions start .. start + n - 1
+ * against keys 0 .. start + n - 1. q and gate [n][heads][head_dim] (q
+ * normalised and rotated), k and v [start + n][kv_heads][head_dim], out
+ * [n][heads][head_dim] = bf16(bf16(sum_j p_j v_j) * sigmoid(gate)) with
+ * p_j = bf16(exp(s_j - max) / den) and s_j = bf16(q . k_j / sqrt(head_dim))
+ * over the keys j at or before the row's position, the products on MFMA.
+ * head_dim 64, 128 or 256; heads a multiple of kv_heads. */
+int cq35_device_matrix_attention(const uint16_t* q, const uint16_t* gate, const uint16_t* k,
+                                 const uint16_t* v, int64_t n, int64_t start, int heads, int kv_heads,
+                                 int head_dim, uint16_t* out);
 
 #ifdef __cplusplus
 }

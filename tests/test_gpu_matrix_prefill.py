@@ -139,7 +139,7 @@ def test_matrix_prefill_within_reference_gate(name, n, components):
 
 
 @pytest.mark.parametrize("layers", [4, 40])
-@pytest.mark.parametrize("components", [Session.MATRIX_PROJECTIONS, ALL])
+@pytest.mark.parametrize("components", [Session.MATRIX_PROJECTIONS, ALL, ALL | Session.MATRIX_ATTENTION])
 def test_matrix_prefill_35b_within_exact_order_spread(layers, components):
     cfg = shape(f"qwen36-35b-a3b@{layers}")
     n, steps = 96, 3
@@ -174,7 +174,7 @@ def test_matrix_prefill_switch_leaves_decode_and_exact_path(oracle):
     prompt = [5, 77, 901, 4096, 17]
     s = m.session(16)
     with pytest.raises(cq35.CQ35Error):
-        s.set_matrix_prefill(4)
+        s.set_matrix_prefill(8)
     s.set_matrix_prefill(ALL)
     s.set_matrix_prefill(0)
     logits, tok = s.step_raw(prompt)

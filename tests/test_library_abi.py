@@ -58,7 +58,8 @@ def test_rust_binding_matches_header():
         n = len([p for p in params.split(",") if p.strip()])
         assert n == header_parameters(name), name
     header = open(os.path.join(ROOT, "include", "cq35.h")).read()
-    for const in ["CQ35_ABI_VERSION", "CQ35_MATRIX_PROJECTIONS", "CQ35_MATRIX_EXPERTS", "CQ35_SPLIT_KEYS_DEFAULT"]:
+    for const in ["CQ35_ABI_VERSION", "CQ35_MATRIX_PROJECTIONS", "CQ35_MATRIX_EXPERTS", "CQ35_MATRIX_ATTENTION",
+                  "CQ35_SPLIT_KEYS_DEFAULT"]:
         hv = re.search(r"#define " + const + r" (\d+)", header).group(1)
         rv = re.search(r"pub const " + const + r": \w+ = (\d+);", src).group(1)
         assert hv == rv, const
