@@ -589,16 +589,24 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
 // over the K*I/2 routed pairs (pair p from expert ids[p / (I/2)], channel
 // p % (I/2)) with the shared pairs p < SI/2 accumulated in the same lanes,
 // then bf16(bf16(routed + residual) (+) bf16(shared)). Block (4 rows,
-// token). Requires inter % 8 == 0, shared_inter % 8 == 0 and
-// shared_inter <= top_k * inter.
+// token), numbered so that the blocks of one 4-row group, all tokens, run on
+// one XCD in sequence (block b runs on XCD b mod 8; XCD x takes the groups
+// x, x + 8, ... in ascending order): the group's rows of every expert, 4 KB
+// each, are read from HBM once into that XCD's L2 and shared by the tokens
+// routed there, instead of each token streaming its experts' whole
+// matrices. Grid: 8 * n * ceil(ceil(hidden / 4) / 8) blocks. Requires
+// inter % 8 == 0, shared_inter % 8 == 0 and shared_inter <= top_k * inter.
+inline int bmoe_down_grid(int hidden, int n) { return 8 * n * (((hidden + 3) / 4 + 7) / 8); }
+
 __global__ __launch_bounds__(kBlock) void k_bmoe_down(
     const uint16_t* __restrict__ active, const uint16_t* __restrict__ down,
     const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
-    const uint16_t* __restrict__ res, int hidden, int top_k, int inter, int shared_inter,
+    const uint16_t* __restrict__ res, int hidden, int top_k, int inter, int shared_inter, int n,
     uint16_t* __restrict__ out) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t = blockIdx.y;
-  const int o = blockIdx.x * 4 + wave;
+  const int local = (int)(blockIdx.x >> 3);
+  const int group = (int)(blockIdx.x & 7) + 8 * (local / n), t = local % n;
+  const int o = group * 4 + wave;
   if (o >= hidden) return;  // wave-uniform
   const int rows = top_k * inter + shared_inter;
   const int aq = top_k * inter / 8, iq = inter / 8, sq = shared_inter / 8;
@@ -618,6 +626,74 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_down(
   if (lane == 0) {
     const size_t i = (size_t)t * hidden + o;
     out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(shared));
+  }
+}
+
+// k_bmoe_down with each wave on kDRows consecutive output rows of one token:
+// the token's activation quads are read once into registers and used for
+// every row, each row's weight quads are read once. Block = (kDRows-row
+// group, kDTokens tokens), wave w on token 4 by + w; blocks numbered as in
+// k_bmoe_down, a group's blocks (all tokens) on one XCD in sequence. Per
+// (token, row) the products, the lane chains over qi = lane, lane + 64, ...
+// (routed and shared), the tree and the epilogue are k_bmoe_down's, so the
+// results are the same bits. NQ: quads per lane, ceil(top_k * inter / 512)
+// rounded up to a power of two.
+constexpr int kDRows = 8;
+constexpr int kDTokens = kBlock / 64;
+inline int bmoe_down_rows_grid(int hidden, int n) {
+  const int groups = (hidden + kDRows - 1) / kDRows, tiles = (n + kDTokens - 1) / kDTokens;
+  return 8 * tiles * ((groups + 7) / 8);
+}
+
+template <int NQ>
+__global__ __launch_bounds__(kBlock) void k_bmoe_down_rows(
+    const uint16_t* __restrict__ active, const uint16_t* __restrict__ down,
+    const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
+    const uint16_t* __restrict__ res, int hidden, int top_k, int inter, int shared_inter, int n,
+    uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tiles = (n + kDTokens - 1) / kDTokens;
+  const int local = (int)(blockIdx.x >> 3);
+  const int group = (int)(blockIdx.x & 7) + 8 * (local / tiles);
+  const int t = (local % tiles) * kDTokens + wave;
+  const int o0 = group * kDRows;
+  if (o0 >= hidden || t >= n) return;  // wave-uniform
+  const int rows = top_k * inter + shared_inter;
+  const int aq = top_k * inter / 8, iq = inter / 8, sq = shared_inter / 8;
+  const u32x4* xa = reinterpret_cast<const u32x4*>(active + (size_t)t * rows);
+  const int* idt = ids + (size_t)t * top_k;
+  u32x4 xv[NQ], xs[NQ];
+  size_t woff[NQ];
+#pragma unroll
+  for (int j = 0; j < NQ; ++j) {
+    const int qi = min(lane + 64 * j, aq - 1), slot = qi / iq, ch = qi - slot * iq;
+    xv[j] = xa[qi];
+    woff[j] = (size_t)idt[slot] * hidden * inter + (size_t)ch * 8;
+    if (64 * j < sq) xs[j] = xa[aq + min(lane + 64 * j, sq - 1)];
+  }
+#pragma unroll
+  for (int r = 0; r < kDRows; ++r) {
+    const int o = o0 + r;
+    if (o >= hidden) break;  // wave-uniform
+    u32x4 wv[NQ], ws[NQ];
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      wv[j] = *reinterpret_cast<const u32x4*>(down + woff[j] + (size_t)o * inter);
+      if (64 * j < sq)
+        ws[j] = reinterpret_cast<const u32x4*>(sdown + (size_t)o * shared_inter)[min(lane + 64 * j, sq - 1)];
+    }
+    float ar[4] = {0.0f, 0.0f, 0.0f, 0.0f}, as[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      if (lane + 64 * j < aq) b256_acc(ar, xv[j], wv[j]);
+      if (lane + 64 * j < sq) b256_acc(as, xs[j], ws[j]);
+    }
+    const float routed = b256_tree(ar);
+    const float shared = b256_tree(as);
+    if (lane == 0) {
+      const size_t i = (size_t)t * hidden + o;
+      out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(shared));
+    }
   }
 }
 

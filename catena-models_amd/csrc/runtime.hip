@@ -1659,9 +1659,20 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
               (const uint16_t*)W(ffn + 5), (const uint16_t*)W(ffn + 6), (const int*)s->pf_ids,
               (const float*)s->pf_probs, (const float*)s->pf_logits, E, K, I, SI, s->pf_act);
           }
-          L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)((H + 3) / 4), rows_n), dim3(kBlock), 0,
-            (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
-            (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, s->pf_h);
+          auto down_rows = [&](auto kernel) {
+            L(KC_MOE_DOWN, kernel, dim3((unsigned)bmoe_down_rows_grid(H, rows_n)), dim3(kBlock), 0,
+              (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
+              (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, rows_n, s->pf_h);
+          };
+          const int dq = (K * I / 8 + 63) / 64;  // routed quads per lane
+          if (dq <= 1) down_rows(k_bmoe_down_rows<1>);
+          else if (dq <= 2) down_rows(k_bmoe_down_rows<2>);
+          else if (dq <= 4) down_rows(k_bmoe_down_rows<4>);
+          else if (dq <= 8) down_rows(k_bmoe_down_rows<8>);
+          else
+            L(KC_MOE_DOWN, k_bmoe_down, dim3((unsigned)bmoe_down_grid(H, rows_n)), dim3(kBlock), 0,
+              (const uint16_t*)s->pf_act, (const uint16_t*)W(ffn + 3), (const uint16_t*)W(ffn + 7),
+              (const int*)s->pf_ids, (const uint16_t*)s->pf_attn, H, K, I, SI, rows_n, s->pf_h);
         }
       } else {
         if (mp && H % 16 == 0)
