@@ -45,57 +45,74 @@ enum { kBPlain = 0, kBResidual = 1, kBGate = 2 };
 
 // out[t][row] for `rows` outputs of `n` token rows of width `cols`
 // (batch.project / batch.residual / batch.gate, batch_projection.hex:30-279,
-// 280-530, 531-854). Block (row, 32-token group): wave w takes tokens
-// [32*by + 8w, +8) and shares each weight quad across them. Epilogues:
+// 280-530, 531-854). Block (bproject_rows rows, 32-token group): wave w takes
+// tokens [32*by + 8w, +8) and shares each weight quad across them. Epilogues:
 // bf16(total); bf16(bf16(total) (+) res); bf16(bf16(silu(bf16 g))) (x) bf16(u).
 // Requires cols % 8 == 0.
+// kBRows output rows per block (plain and residual modes: each wave takes
+// them all, its token quads shared by the rows; gate mode: one row).
+template <int kMode>
+constexpr int bproject_rows() { return kMode == kBGate ? 1 : 2; }
+
 template <int kMode>
 __global__ __launch_bounds__(kBlock) void k_bproject(const uint16_t* __restrict__ x, int n,
                                                      int cols, const uint16_t* __restrict__ w,
                                                      const uint16_t* __restrict__ w2, int rows,
                                                      const uint16_t* __restrict__ res,
                                                      uint16_t* __restrict__ out) {
+  constexpr int R = bproject_rows<kMode>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = blockIdx.x;
+  const int row0 = blockIdx.x * R;
   const int t0 = (blockIdx.y * 4 + wave) * kBTokens;
-  if (t0 >= n || row >= rows) return;  // wave-uniform
+  if (t0 >= n || row0 >= rows) return;  // wave-uniform
   const int quads = cols >> 3;
-  const u32x4* wr = reinterpret_cast<const u32x4*>(w + (size_t)row * cols);
-  const u32x4* wr2 = kMode == kBGate ? reinterpret_cast<const u32x4*>(w2 + (size_t)row * cols) : nullptr;
-  float acc[kBTokens][4], acc2[kMode == kBGate ? kBTokens : 1][4];
+  const u32x4* wr[R];
+#pragma unroll
+  for (int k = 0; k < R; ++k) wr[k] = reinterpret_cast<const u32x4*>(w + (size_t)min(row0 + k, rows - 1) * cols);
+  const u32x4* wr2 = kMode == kBGate ? reinterpret_cast<const u32x4*>(w2 + (size_t)row0 * cols) : nullptr;
+  float acc[R][kBTokens][4], acc2[kMode == kBGate ? kBTokens : 1][4];
 #pragma unroll
   for (int t = 0; t < kBTokens; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      acc[t][r] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < R; ++k) acc[k][t][r] = 0.0f;
       if (kMode == kBGate) acc2[t][r] = 0.0f;
     }
   for (int qi = lane; qi < quads; qi += 64) {
-    const u32x4 wq = wr[qi];
+    u32x4 wq[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) wq[k] = wr[k][qi];
     u32x4 wq2;
     if (kMode == kBGate) wq2 = wr2[qi];
 #pragma unroll
     for (int t = 0; t < kBTokens; ++t) {
       if (t0 + t < n) {
         const u32x4 xq = reinterpret_cast<const u32x4*>(x + (size_t)(t0 + t) * cols)[qi];
-        b256_acc(acc[t], xq, wq);
+#pragma unroll
+        for (int k = 0; k < R; ++k) b256_acc(acc[k][t], xq, wq[k]);
         if (kMode == kBGate) b256_acc(acc2[kMode == kBGate ? t : 0], xq, wq2);
       }
     }
   }
 #pragma unroll
-  for (int t = 0; t < kBTokens; ++t) {
-    if (t0 + t >= n) break;  // wave-uniform
-    const float total = b256_tree(acc[t]);
-    float total2 = 0.0f;
-    if (kMode == kBGate) total2 = b256_tree(acc2[kMode == kBGate ? t : 0]);
-    if (lane == 0) {
-      const size_t o = (size_t)(t0 + t) * rows + row;
-      uint16_t y;
-      if (kMode == kBPlain) y = f2bf(total);
-      else if (kMode == kBResidual) y = bf_add(f2bf(total), res[o]);
-      else y = bf_mul(f2bf(silu(rbf(total))), f2bf(total2));
-      out[o] = y;
+  for (int k = 0; k < R; ++k) {
+    const int row = row0 + k;
+    if (row >= rows) break;  // wave-uniform
+#pragma unroll
+    for (int t = 0; t < kBTokens; ++t) {
+      if (t0 + t >= n) break;  // wave-uniform
+      const float total = b256_tree(acc[k][t]);
+      float total2 = 0.0f;
+      if (kMode == kBGate) total2 = b256_tree(acc2[kMode == kBGate ? t : 0]);
+      if (lane == 0) {
+        const size_t o = (size_t)(t0 + t) * rows + row;
+        uint16_t y;
+        if (kMode == kBPlain) y = f2bf(total);
+        else if (kMode == kBResidual) y = bf_add(f2bf(total), res[o]);
+        else y = bf_mul(f2bf(silu(rbf(total))), f2bf(total2));
+        out[o] = y;
+      }
     }
   }
 }

@@ -1496,7 +1496,8 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         L(KC_PREFILL_PROJECT, k_mproject<kBPlain>, mgrid(rows, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
           (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr, out);
       else
-        L(KC_PREFILL_PROJECT, k_bproject<kBPlain>, dim3((unsigned)rows, tiles), dim3(kBlock), 0, x,
+        L(KC_PREFILL_PROJECT, k_bproject<kBPlain>,
+          dim3((unsigned)((rows + bproject_rows<kBPlain>() - 1) / bproject_rows<kBPlain>()), tiles), dim3(kBlock), 0, x,
           rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, rows, (const uint16_t*)nullptr,
           out);
     };
@@ -1509,7 +1510,8 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         L(KC_PREFILL_PROJECT, k_mproject<kBResidual>, mgrid(H, cols), dim3(64 * kMWaves), 0, x, rows_n, cols,
           (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
       else
-        L(KC_PREFILL_PROJECT, k_bproject<kBResidual>, dim3((unsigned)H, tiles), dim3(kBlock), 0, x,
+        L(KC_PREFILL_PROJECT, k_bproject<kBResidual>,
+          dim3((unsigned)((H + bproject_rows<kBResidual>() - 1) / bproject_rows<kBResidual>()), tiles), dim3(kBlock), 0, x,
           rows_n, cols, (const uint16_t*)w, (const uint16_t*)nullptr, H, res, out);
     };
     auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
