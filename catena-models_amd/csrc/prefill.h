@@ -517,7 +517,8 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate(
 // assignments bucketed by expert (k_moe_bucket), block = kGRows rows of
 // expert blockIdx.y, each wave kGRowsPerWave of them with their gate and up
 // quads (lane + 64 j) held in registers, applied to the expert's tokens in
-// turn (the next token's input quads in flight). kShared: the shared expert
+// turn (the next token's input quads in flight); the epilogues of up to 64
+// tokens run at once, one per lane. kShared: the shared expert
 // over tokens [16 blockIdx.y, +16). Per (token, row) the arithmetic is
 // k_bmoe_gate's: the B256 lane order over the quads, the tree and the
 // epilogue, so the results are the same bits.
@@ -561,9 +562,30 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
 #pragma unroll
     for (int j = 0; j < NQ; ++j) xv[j] = xq[min(lane + 64 * j, quads - 1)];
   };
-  auto compute = [&](const u32x4 (&xv)[NQ], int i) {
+  // the epilogues of up to 64 tokens at once: lane j keeps the totals of
+  // token (i & ~63) + j and applies k_bmoe_gate's epilogue to it
+  float pg[RW], pu[RW];
+  auto finish = [&](int b, int m) {
+    if (lane >= m) return;
+    const int i = b + lane;
     const int a = kShared ? 0 : order[begin + i];
     const int t = kShared ? begin + i : a / top_k;
+#pragma unroll
+    for (int k = 0; k < RW; ++k) {
+      const int r = r0 + k;
+      if (r >= width) continue;
+      const float gb = rbf(pg[k]), ub = rbf(pu[k]);
+      const float activated = silu(gb);
+      if (kShared) {
+        const float shared_prob = sigmoid(logits[(size_t)t * (experts + 1) + experts]);
+        active[(size_t)t * rows + top_k * inter + r] = f2bf(rbf(rbf(activated) * ub) * shared_prob);
+      } else {
+        const int slot = a - t * top_k;
+        active[(size_t)t * rows + slot * inter + r] = f2bf((activated * ub) * probs[a]);
+      }
+    }
+  };
+  auto compute = [&](const u32x4 (&xv)[NQ], int i) {
 #pragma unroll
     for (int k = 0; k < RW; ++k) {
       float ag[4] = {0.0f, 0.0f, 0.0f, 0.0f}, au[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -573,21 +595,14 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
           b256_acc(ag, xv[j], gw[k][j]);
           b256_acc(au, xv[j], uw[k][j]);
         }
-      const float g = b256_tree(ag);
-      const float u = b256_tree(au);
-      const int r = r0 + k;
-      if (lane == 0 && r < width) {
-        const float gb = rbf(g), ub = rbf(u);
-        const float activated = silu(gb);
-        if (kShared) {
-          const float shared_prob = sigmoid(logits[(size_t)t * (experts + 1) + experts]);
-          active[(size_t)t * rows + top_k * inter + r] = f2bf(rbf(rbf(activated) * ub) * shared_prob);
-        } else {
-          const int slot = a - t * top_k;
-          active[(size_t)t * rows + slot * inter + r] = f2bf((activated * ub) * probs[a]);
-        }
+      const float g = __shfl(b256_tree(ag), 0, 64);
+      const float u = __shfl(b256_tree(au), 0, 64);
+      if (lane == (i & 63)) {
+        pg[k] = g;
+        pu[k] = u;
       }
     }
+    if ((i & 63) == 63 || i == count - 1) finish(i & ~63, (i & 63) + 1);  // wave-uniform
   };
   u32x4 xa[NQ], xb[NQ];
   load(xa, 0);
