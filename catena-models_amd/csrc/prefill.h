@@ -41,6 +41,30 @@ __device__ __forceinline__ float b256_tree(const float (&a)[4]) {
   return v0 + v1;
 }
 
+// Two trees at once: a's total valid in lane 0, b's in lane 32. At stride
+// 128 (physical 32) each half wave receives the other half's values of one
+// tree (lanes 0-31 keep a, lanes 32-63 keep b); strides 64 ... 4 then run
+// inside each half and 2, 1 inside the lane. Every sum has the operands it
+// has in b256_tree (the two operands of a sum commute), so both totals are
+// b256_tree's bits, in fewer instructions.
+__device__ __forceinline__ float half_swap(float v) {  // v of lane ^ 32 (permlane32 swap)
+  const int b = __builtin_bit_cast(int, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? (int)r[0] : (int)r[1]);
+}
+__device__ __forceinline__ float b256_tree2(const float (&a)[4], const float (&b)[4]) {
+  const bool low = (threadIdx.x & 32) == 0;
+  float v0, v1, v2, v3;
+  v0 = (low ? a[0] : b[0]) + half_swap(low ? b[0] : a[0]);
+  v1 = (low ? a[1] : b[1]) + half_swap(low ? b[1] : a[1]);
+  v2 = (low ? a[2] : b[2]) + half_swap(low ? b[2] : a[2]);
+  v3 = (low ? a[3] : b[3]) + half_swap(low ? b[3] : a[3]);
+  tree_levels<64, 16>(v0, v1, v2, v3);
+  v0 += v2;
+  v1 += v3;
+  return v0 + v1;
+}
+
 enum { kBPlain = 0, kBResidual = 1, kBGate = 2 };
 
 // out[t][row] for `rows` outputs of `n` token rows of width `cols`
@@ -95,6 +119,25 @@ __global__ __launch_bounds__(kBlock) void k_bproject(const uint16_t* __restrict_
       }
     }
   }
+  // totals: rows in pairs (or the gate and up sums) through b256_tree2
+  float tot[R][kBTokens], tot2[kBTokens];
+#pragma unroll
+  for (int t = 0; t < kBTokens; ++t) {
+    if (t0 + t >= n) break;  // wave-uniform
+    if (kMode == kBGate) {
+      const float both = b256_tree2(acc[0][t], acc2[kMode == kBGate ? t : 0]);
+      tot[0][t] = both;
+      tot2[t] = __shfl(both, 32, 64);
+    } else {
+#pragma unroll
+      for (int k = 0; k + 1 < R; k += 2) {
+        const float both = b256_tree2(acc[k][t], acc[k + 1][t]);
+        tot[k][t] = both;
+        tot[k + 1][t] = __shfl(both, 32, 64);
+      }
+      if (R % 2) tot[R - 1][t] = b256_tree(acc[R - 1][t]);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < R; ++k) {
     const int row = row0 + k;
@@ -102,9 +145,8 @@ __global__ __launch_bounds__(kBlock) void k_bproject(const uint16_t* __restrict_
 #pragma unroll
     for (int t = 0; t < kBTokens; ++t) {
       if (t0 + t >= n) break;  // wave-uniform
-      const float total = b256_tree(acc[k][t]);
-      float total2 = 0.0f;
-      if (kMode == kBGate) total2 = b256_tree(acc2[kMode == kBGate ? t : 0]);
+      const float total = tot[k][t];
+      const float total2 = kMode == kBGate ? tot2[t] : 0.0f;
       if (lane == 0) {
         const size_t o = (size_t)(t0 + t) * rows + row;
         uint16_t y;
@@ -595,8 +637,8 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
           b256_acc(ag, xv[j], gw[k][j]);
           b256_acc(au, xv[j], uw[k][j]);
         }
-      const float g = __shfl(b256_tree(ag), 0, 64);
-      const float u = __shfl(b256_tree(au), 0, 64);
+      const float both = b256_tree2(ag, au);
+      const float g = __shfl(both, 0, 64), u = __shfl(both, 32, 64);
       if (lane == (i & 63)) {
         pg[k] = g;
         pu[k] = u;
@@ -720,8 +762,8 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_down_rows(
       if (lane + 64 * j < aq) b256_acc(ar, xv[j], wv[j]);
       if (lane + 64 * j < sq) b256_acc(as, xs[j], ws[j]);
     }
-    const float routed = b256_tree(ar);
-    const float shared = b256_tree(as);
+    const float both = b256_tree2(ar, as);
+    const float routed = both, shared = __shfl(both, 32, 64);
     if (lane == 0) {
       const size_t i = (size_t)t * hidden + o;
       out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(shared));
