@@ -260,8 +260,9 @@ def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, p
     each session then decoding from its own first token), `steps` greedy
     decode rounds through cq35_step_batch, and one `prefill_tokens`-token
     prompt on another session, appended in `chunk`-token calls on the matrix
-    cores (MFMA projections and experts), one call after each decode round
-    until it is done. Aggregate decode tok/s over the whole interleaved run."""
+    cores (MFMA projections, experts and attention), one call after each
+    decode round until it is done. Aggregate decode tok/s over the whole
+    interleaved run."""
     import cq35
     capacity = context + steps + 8
     t0 = time.time()
@@ -436,6 +437,10 @@ def main() -> int:
                     help="sessions of the concurrent long-context leg (0 skips it)")
     ap.add_argument("--concurrent-steps", type=int, default=128)
     ap.add_argument("--concurrent-prefill", type=int, default=4096)
+    # the reference's server prefills prompts in absolute 1024-token blocks
+    # (PREFILL_BLOCK, src/server/prefix_cache.rs:4; engine.rs:330)
+    ap.add_argument("--concurrent-chunk", type=int, default=1024,
+                    help="tokens per interleaved prefill call of the concurrent leg")
     ap.add_argument("--batch-sessions", type=int, default=16,
                     help="sessions of the batch-16 leg (0 skips it)")
     ap.add_argument("--batch-config", default="qwen35-2b")
@@ -580,7 +585,7 @@ def main() -> int:
     concurrent = None
     if args.concurrent > 0 and args.long_context > 0:
         concurrent = concurrent_long(model, cfg, args.concurrent, args.long_context, args.concurrent_steps,
-                                     args.concurrent_prefill, 256, args.seed)
+                                     args.concurrent_prefill, args.concurrent_chunk, args.seed)
     batch = None
     if args.batch_sessions > 0:
         batch = batch_sessions(args.batch_config, args.batch_sessions, 1024, args.batch_steps, args.seed)
