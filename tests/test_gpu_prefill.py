@@ -2,8 +2,8 @@
 text-batch, src/qwen/prefill.rs:36-653) against the CPU restatement on an
 MI355X: greedy token, BF16 logits and the whole session state bit-exact after
 the batched call and over the decode steps that follow it, for a dense and a
-MoE shape, a call spanning two 256-token chunks, and a call that starts after
-earlier tokens (convolution taps from the cache history)."""
+MoE shape, calls spanning two 256-token chunks (dense and MoE), and a call
+that starts after earlier tokens (convolution taps from the cache history)."""
 import numpy as np
 import pytest
 
@@ -81,3 +81,12 @@ def test_batched_prefill_two_chunks(oracle):
     cfg = cc.preset("mini")
     prompt = np.random.default_rng(53).integers(0, cfg["vocab"], 300).tolist()
     run(oracle, "mini", 16, [], prompt, 3)
+
+
+def test_batched_prefill_two_chunks_moe(oracle):
+    """300 MoE tokens: the first 256-token chunk routes about 64 tokens to each
+    of mini-moe's 32 experts, so the grouped gate/up runs its per-lane
+    epilogues across the 64-token boundary."""
+    cfg = cc.preset("mini-moe")
+    prompt = np.random.default_rng(54).integers(0, cfg["vocab"], 300).tolist()
+    run(oracle, "mini-moe", 17, [], prompt, 3)
