@@ -2022,13 +2022,14 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
     // sub-chunks: nsub of st tiles (a multiple of 4; the last may be shorter)
     const int nsub = (nt + kFlashSubTiles - 1) / kFlashSubTiles;
     const int st = (((nt + nsub - 1) / nsub) + 3) & ~3;
-    // channel chains: thread = channel c of CPT query heads; threads tid < HPK
-    // also run head tid's denominator chain
-    constexpr int CPT = (HPK * HD + kMT - 1) / kMT;
-    const int c = m.tid % HD, hbase = (m.tid / HD) * CPT;
-    float acc[CPT];
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) acc[i] = 0.0f;
+    // channel chains: thread = channels 2 cp, 2 cp + 1 of query heads 2 hp,
+    // 2 hp + 1 (one 4-byte V read serves both channels, each head's 8
+    // weights of a tile are two 16-byte LDS reads); threads tid < HPK also
+    // run head tid's denominator chain
+    static_assert(HPK % 2 == 0 && (HPK / 2) * (HD / 2) <= kMT, "flash chains");
+    const int cp = m.tid % (HD / 2), hp = m.tid / (HD / 2);
+    const bool chains = hp < HPK / 2;
+    float acc[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};  // [head][channel]
     float den = 0.0f;
     constexpr int VQ = kFlashVKeys * HD / 8;     // 16-byte quads per pass
     constexpr int VPT = (VQ + kMT - 1) / kMT;    // per thread
@@ -2161,21 +2162,31 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
       // chains over the pass's tiles
       auto consume = [&](int q) {
         const int ta = 4 * q, tz = min(snt, ta + 4);
-        if (hbase < HPK) {
+        if (chains) {
 #pragma unroll 1
           for (int t = ta; t < tz; ++t) {
-            float vv[8];
+            float v0[8], v1[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vv[j] = bf2f(s->v[8 * (t - ta) + j][c]);
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t pr = reinterpret_cast<const uint32_t*>(s->v[8 * (t - ta) + j])[cp];
+              v0[j] = lo2f(pr);
+              v1[j] = hi2f(pr);
+            }
 #pragma unroll
-            for (int i = 0; i < CPT; ++i) {
-              const int hq = hbase + i;
-              if (hq < HPK) {
-                float x = acc[i] * s->alpha[hq][t];
+            for (int h = 0; h < 2; ++h) {
+              const int hq = 2 * hp + h;
+              const float al = s->alpha[hq][t];
+              const f32x4 pa = *reinterpret_cast<const f32x4*>(&s->p[hq][8 * t]);
+              const f32x4 pb = *reinterpret_cast<const f32x4*>(&s->p[hq][8 * t + 4]);
+              const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+              float x0 = acc[h][0] * al, x1 = acc[h][1] * al;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x = x + s->p[hq][8 * t + j] * vv[j];
-                acc[i] = x;
+              for (int j = 0; j < 8; ++j) {
+                x0 = x0 + pv[j] * v0[j];
+                x1 = x1 + pv[j] * v1[j];
               }
+              acc[h][0] = x0;
+              acc[h][1] = x1;
             }
           }
         }
@@ -2205,12 +2216,12 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
       clk.lap(3);
     }
     // partial words of each query head of the group
+    if (chains) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int hq = hbase + i;
-      if (hq < HPK && c < HD) {
-        uint64_t* w = Ly.x_scores + ((size_t)(g * HPK + hq) * kSplitRanges + r) * FW;
-        word_store(w + 2 + c, fbits(acc[i]), m.tag);
+      for (int h = 0; h < 2; ++h) {
+        uint64_t* w = Ly.x_scores + ((size_t)(g * HPK + 2 * hp + h) * kSplitRanges + r) * FW;
+        word_store(w + 2 + 2 * cp, fbits(acc[h][0]), m.tag);
+        word_store(w + 3 + 2 * cp, fbits(acc[h][1]), m.tag);
       }
     }
     if (m.tid < HPK) {
