@@ -115,6 +115,24 @@ __device__ __forceinline__ float tree32_lanes(float v) {
   return v;
 }
 
+// Two such trees at once: a's total in lane 0 of each half wave, b's in
+// lane 16. At stride 16, lanes 0-15 of a half keep a and receive a from
+// lanes 16-31, lanes 16-31 keep b and receive b from lanes 0-15 (one
+// permlane16 swap); strides 8 ... 1 then run inside each 16-lane row. Every
+// sum has the operands it has in tree32_lanes (a sum's operands commute), so
+// both totals are its bits.
+__device__ __forceinline__ float tree32_pair(float a, float b) {
+  const bool low = (threadIdx.x & 16) == 0;
+  const int send = __builtin_bit_cast(int, low ? b : a);
+  const auto r = __builtin_amdgcn_permlane16_swap(send, send, false, false);
+  float v = (low ? a : b) + __builtin_bit_cast(float, low ? (int)r[1] : (int)r[0]);
+  v += lane_down<8>(v);
+  v += lane_down<4>(v);
+  v += lane_down<2>(v);
+  v += lane_down<1>(v);
+  return v;
+}
+
 // Halving tree of width W = 4*LPR over the reference lanes held by the LPR
 // physical lanes of a row group (reference stride 4s = physical stride s,
 // then strides 2 and 1 inside the lane). Must be reached by every lane of

@@ -2096,15 +2096,19 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
           float qv[KJ];
 #pragma unroll
           for (int j = 0; j < KJ; ++j) qv[j] = qh[j];
+          // the two keys' trees at once: key 0's total in lane 0, key 1's in
+          // lane 16 of the half wave
+          static_assert(SB == 2, "paired score trees");
+          float x[SB];
 #pragma unroll
           for (int rr = 0; rr < SB; ++rr) {
-            const int kk = hw + 16 * (b * SB + rr);  // sub-chunk relative
-            float x = 0.0f;
+            x[rr] = 0.0f;
 #pragma unroll
-            for (int j = 0; j < KJ; ++j) x += qv[j] * kf[rr][j];
-            x = tree32_lanes(x);
-            if (l32 == 0 && kk < sn) s->p[hq][kk] = x * a.attn_scale;
+            for (int j = 0; j < KJ; ++j) x[rr] += qv[j] * kf[rr][j];
           }
+          const float tot = tree32_pair(x[0], x[1]);
+          const int kk = hw + 16 * (b * SB + (l32 >> 4));  // sub-chunk relative
+          if ((l32 & 15) == 0 && kk < sn) s->p[hq][kk] = tot * a.attn_scale;
         }
       };
       const int nb = (sn + 16 * SB - 1) / (16 * SB);
