@@ -2278,7 +2278,25 @@ __device__ __forceinline__ void phase_merge(const MegaArgs* pa, uint32_t tag, co
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
       float A = 0.0f, D = 0.0f;
       if (m.lane < kValueChannels) {
-        for (int i = 0; i < nranges; ++i) {
+        // ranges in ascending order; each batch of 8 ranges' LDS reads is
+        // issued before its sums, so the chains do not wait on every read
+        int i = 0;
+#pragma unroll 1
+        for (; i + 8 <= nranges; i += 8) {
+          float w8[8], d8[8], a8[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            w8[k] = wr[i + k];
+            d8[k] = f[(i + k) * RW + 1];
+            a8[k] = f[(i + k) * RW + 2 + m.lane];
+          }
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            D = D + d8[k] * w8[k];
+            A = A + a8[k] * w8[k];
+          }
+        }
+        for (; i < nranges; ++i) {
           const float w = wr[i];
           D = D + f[i * RW + 1] * w;
           A = A + f[i * RW + 2 + m.lane] * w;
