@@ -2197,9 +2197,12 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
         if (m.tid < HPK) {
 #pragma unroll 1
           for (int t = ta; t < tz; ++t) {
-            den = den * s->alpha[m.tid][t];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) den = den + s->p[m.tid][8 * t + j];
+            const float al = s->alpha[m.tid][t];
+            const f32x4 pa = *reinterpret_cast<const f32x4*>(&s->p[m.tid][8 * t]);
+            const f32x4 pb = *reinterpret_cast<const f32x4*>(&s->p[m.tid][8 * t + 4]);
+            den = den * al;
+            den = den + pa.x; den = den + pa.y; den = den + pa.z; den = den + pa.w;
+            den = den + pb.x; den = den + pb.y; den = den + pb.z; den = den + pb.w;
           }
         }
       };
