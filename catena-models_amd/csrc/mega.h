@@ -2084,10 +2084,14 @@ __device__ __forceinline__ void phase_flash(const MegaArgs* pa, uint32_t tag, co
         float kf[SB][KJ];
 #pragma unroll
         for (int rr = 0; rr < SB; ++rr) {
-          const bool fresh = k0 + c0 + hw + 16 * (b * SB + rr) == position;
 #pragma unroll
-          for (int j = 0; j < KJ; ++j)
-            kf[rr][j] = bf2f(fresh ? s->khat[g * HD + l32 + 32 * j] : (uint16_t)kv[rr][j]);
+          for (int j = 0; j < KJ; ++j) kf[rr][j] = bf2f((uint16_t)kv[rr][j]);
+          // the new position's key row comes from LDS (one key of the whole
+          // range: a branch, so the other keys issue no LDS reads for it)
+          if (__builtin_expect(k0 + c0 + hw + 16 * (b * SB + rr) == position, 0)) {
+#pragma unroll
+            for (int j = 0; j < KJ; ++j) kf[rr][j] = bf2f(s->khat[g * HD + l32 + 32 * j]);
+          }
         }
         // each query head read from LDS once per batch of SB keys
 #pragma unroll
