@@ -2133,8 +2133,15 @@ void skinny_launch(hipStream_t st, const BatchWorkspace* b, const uint16_t* x, i
 template <int kMode>
 void skinny(hipStream_t st, const BatchWorkspace* b, const uint16_t* x, int B, int64_t cols, const Segments& seg,
             const uint16_t* w2, const uint16_t* res, unsigned long long* best) {
-  if (seg_rows(seg) >= 32768) skinny_launch<kMode, 2>(st, b, x, B, cols, seg, w2, res, best);
-  else skinny_launch<kMode, 1>(st, b, x, B, cols, seg, w2, res, best);
+  // two tiles per wave for the vocabulary head only (other launches are far
+  // narrower; instantiating the gate mode with two tiles would spill)
+  if constexpr (kMode == kSArgmax) {
+    if (seg_rows(seg) >= 32768) {
+      skinny_launch<kMode, 2>(st, b, x, B, cols, seg, w2, res, best);
+      return;
+    }
+  }
+  skinny_launch<kMode, 1>(st, b, x, B, cols, seg, w2, res, best);
 }
 
 // Weight-shared GEMV launches (k_ws32 / k_ws64 / k_ws256_swiglu) over B
