@@ -68,6 +68,44 @@ def copy_probe(megabytes: int) -> None:
     log(f"copy probe: {megabytes} MiB device-to-device")
 
 
+def copy_ceiling(mib: int = 1024, reps: int = 10) -> dict:
+    """Measured device-copy ceiling: a `mib` MiB device-to-device copy
+    (the runtime's copy kernel) timed with HIP events, `reps` times; the
+    best rate counts read + write bytes. The practical HBM ceiling next to
+    the nominal 8 TB/s."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = mib << 20
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if hip.hipMalloc(ctypes.byref(src), ctypes.c_size_t(n)) or hip.hipMalloc(ctypes.byref(dst), ctypes.c_size_t(n)):
+        raise RuntimeError("hipMalloc failed for the copy ceiling")
+    try:
+        hip.hipMemset(src, 0x3C, ctypes.c_size_t(n))
+        e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+        hip.hipEventCreate(ctypes.byref(e0))
+        hip.hipEventCreate(ctypes.byref(e1))
+        best = None
+        for i in range(reps + 1):
+            hip.hipEventRecord(e0, None)
+            if hip.hipMemcpyAsync(dst, src, ctypes.c_size_t(n), 3, None):  # hipMemcpyDeviceToDevice
+                raise RuntimeError("device copy failed")
+            hip.hipEventRecord(e1, None)
+            hip.hipEventSynchronize(e1)
+            ms = ctypes.c_float()
+            hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1)
+            if i > 0 and (best is None or ms.value < best):  # the first copy is a warm-up
+                best = ms.value
+        hip.hipEventDestroy(e0)
+        hip.hipEventDestroy(e1)
+    finally:
+        hip.hipDeviceSynchronize()
+        hip.hipFree(src)
+        hip.hipFree(dst)
+    gbs = 2 * n / (best / 1e3) / 1e9
+    log(f"copy ceiling: {mib} MiB device-to-device, {gbs:.0f} GB/s (read + write, best of {reps})")
+    return dict(gbs=round(gbs, 1), bytes=2 * n, ms=round(best, 4), reps=reps,
+                method=f"hipMemcpyAsync device-to-device of {mib} MiB, HIP events, best of {reps}")
+
+
 def kernel_bytes(cfg: dict, context: int) -> dict:
     """Algorithmic HBM bytes per launch of each streaming kernel class."""
     import cq35
@@ -338,10 +376,10 @@ def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: i
         nxt = cq35.decode_batch(group, nxt)
     device_sync()
     batched = time.perf_counter() - t0
-    # the same sessions with the products on MFMA (matrix-core projections
+    # the same sessions with the products on MFMA (matrix-core decode
     # selected on every session: tolerance-level, tests/test_gpu_batch_matrix.py)
     for s in group:
-        s.set_matrix_prefill(s.MATRIX_PROJECTIONS)
+        s.set_matrix_decode(True)
     mx_steps = steps
     for _ in range(2):
         nxt = cq35.decode_batch(group, nxt)
@@ -461,6 +499,7 @@ def main() -> int:
     cfg = cq35.preset(args.config)
     if args.copy_probe:
         copy_probe(args.copy_probe)
+    ceiling = copy_ceiling()
     t0 = time.time()
     model = cq35.Model.synthetic(cfg, seed=args.seed)
     log(f"weights: {model.weight_bytes() / 1e9:.2f} GB generated on device in {time.time() - t0:.1f}s")
@@ -573,7 +612,8 @@ def main() -> int:
         traffic = tr["fetch_bytes"] + tr["write_bytes"] if tr else None
         roofline = dict(kernel=dom, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS,
                         unit="GB/s", frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
-                        bytes_per_launch=int(by), avg_launch_us=round(kernels[dom]["avg_launch_us"], 2))
+                        bytes_per_launch=int(by), avg_launch_us=round(kernels[dom]["avg_launch_us"], 2),
+                        copy_ceiling_gbs=ceiling["gbs"], frac_of_copy_ceiling=round(achieved / ceiling["gbs"], 4))
         for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["ms_per_step"]):
             log(f"  {k:18s} {v['ms_per_step']:.3f} ms/step  {v['avg_launch_us']:.1f} us/launch"
                 + (f"  {v['gbs']:.0f} GB/s" if v["gbs"] else ""))
@@ -632,7 +672,9 @@ def main() -> int:
                     global_batch=1, seq_len=args.context, context_avg=ctx_avg, parallelism="none",
                     decode_path="persistent one-launch step" if persistent else "per-kernel launch sequence"),
         step_roofline=dict(bytes_per_token=bpt["total"], achieved_gbs=round(step_gbs, 1),
-                           frac=round(step_gbs / HBM_PEAK_GBS, 4)),
+                           frac=round(step_gbs / HBM_PEAK_GBS, 4),
+                           frac_of_copy_ceiling=round(step_gbs / ceiling["gbs"], 4)),
+        copy_ceiling=ceiling,
         roofline=roofline, kernels=kernels, cpu_baseline=cpu,
         prefill=prefill, long_context=long_ctx, concurrent_long_context=concurrent, batch_sessions=batch,
         dense_decode=dense or None,

@@ -64,6 +64,8 @@ def load():
         "cq35_session_persistent": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "cq35_session_set_matrix_prefill": ([P, ctypes.c_int], ctypes.c_int),
         "cq35_session_matrix_prefill": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
+        "cq35_session_set_matrix_decode": ([P, ctypes.c_int], ctypes.c_int),
+        "cq35_session_matrix_decode": ([P, ctypes.POINTER(ctypes.c_int)], ctypes.c_int),
         "cq35_numeric_exp": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_sqrt": ([ctypes.c_float], ctypes.c_float),
         "cq35_numeric_softplus": ([ctypes.c_float], ctypes.c_float),
@@ -107,6 +109,7 @@ EXPORTED = [
     "cq35_session_kernel_time", "cq35_kernel_class_name", "cq35_kernel_class_count",
     "cq35_session_set_graph", "cq35_session_set_persistent", "cq35_session_persistent",
     "cq35_session_set_matrix_prefill", "cq35_session_matrix_prefill",
+    "cq35_session_set_matrix_decode", "cq35_session_matrix_decode",
     "cq35_numeric_exp", "cq35_numeric_sqrt", "cq35_numeric_softplus",
     "cq35_numeric_sincos", "cq35_device_numeric", "cq35_device_gemv", "cq35_device_matrix_gemm",
     "cq35_device_matrix_attention",

@@ -130,9 +130,9 @@ def weight_info(cfg: dict, index: int):
 
 def decode_batch(sessions: Sequence["Session"], tokens: Sequence[int], logits: bool = False):
     """One decode step for each session (cq35_step_batch): the same next
-    tokens as stepping them one by one (dense sessions of one model and
-    capacity share each layer's weight pass; with matrix-core projections
-    selected on every session the products run on MFMA). With logits=True,
+    tokens as stepping them one by one (sessions of one model and capacity
+    share each layer's weight pass; with matrix-core decode selected on every
+    session the products run on MFMA). With logits=True,
     also returns the BF16 logits as a [sessions, vocab] uint16 array."""
     n = len(sessions)
     if n == 0:
@@ -333,6 +333,18 @@ class Session:
         v = ctypes.c_int()
         check(_lib.load().cq35_session_matrix_prefill(self._h, ctypes.byref(v)))
         return v.value
+
+    def set_matrix_decode(self, enabled: bool) -> None:
+        """Let cq35_step_batch run the weight-shared step's products on MFMA
+        (tolerance-level) when every session of the batch has this set; a
+        batch with any session unset takes the exact products."""
+        check(_lib.load().cq35_session_set_matrix_decode(self._h, 1 if enabled else 0))
+
+    @property
+    def matrix_decode(self) -> bool:
+        v = ctypes.c_int()
+        check(_lib.load().cq35_session_matrix_decode(self._h, ctypes.byref(v)))
+        return bool(v.value)
 
     @property
     def persistent(self) -> bool:

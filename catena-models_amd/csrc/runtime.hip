@@ -780,6 +780,7 @@ struct cq35_session {
   int pf_attn_tokens = 0;  // tokens per staged-attention launch (scratch rows)
   int pf_rows = 0;         // token rows of the chunk buffers
   int matrix = 0;          // CQ35_MATRIX_* components of multi-token calls on MFMA
+  int matrix_decode = 0;   // weight-shared batched decode products on MFMA
   int64_t split_keys = CQ35_SPLIT_KEYS_DEFAULT;  // decode attention splits above this many keys
   // kernel timing
   int timed_class = -1;
@@ -1861,6 +1862,19 @@ extern "C" int cq35_session_matrix_prefill(const cq35_session* s, int* component
   return CQ35_OK;
 }
 
+extern "C" int cq35_session_set_matrix_decode(cq35_session* s, int enabled) {
+  if (!s) return fail(CQ35_EINVAL, "null argument");
+  if (enabled != 0 && enabled != 1) return fail(CQ35_EINVAL, "matrix decode option must be 0 or 1, not %d", enabled);
+  s->matrix_decode = enabled;
+  return CQ35_OK;
+}
+
+extern "C" int cq35_session_matrix_decode(const cq35_session* s, int* enabled) {
+  if (!s || !enabled) return fail(CQ35_EINVAL, "null argument");
+  *enabled = s->matrix_decode;
+  return CQ35_OK;
+}
+
 extern "C" int cq35_session_persistent(const cq35_session* s, int* enabled) {
   if (!s || !enabled) return fail(CQ35_EINVAL, "null argument");
   *enabled = s->mega_on ? 1 : 0;
@@ -2275,10 +2289,9 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
     b->h_rows->token[i] = tokens[i];
     sessions[i]->poisoned = true;  // cleared on success
   }
-  // the products run on MFMA when every session selects the matrix-core
-  // projections
+  // the products run on MFMA when every session selects matrix-core decode
   bool mx = true;
-  for (int i = 0; i < count; ++i) mx = mx && (sessions[i]->matrix & CQ35_MATRIX_PROJECTIONS) != 0;
+  for (int i = 0; i < count; ++i) mx = mx && sessions[i]->matrix_decode != 0;
   hipError_t e = hipSuccess;
   for (int i = 0; i < count && e == hipSuccess; ++i) e = hipStreamSynchronize(sessions[i]->stream);
   if (e == hipSuccess)
@@ -2408,6 +2421,7 @@ extern "C" int cq35_session_copy(const cq35_session* src, cq35_session** out) {
   }
   s->graph_enabled = src->graph_enabled;
   s->matrix = src->matrix;  // session options travel with the state
+  s->matrix_decode = src->matrix_decode;
   if (src->split_keys != s->split_keys) {
     const int r = cq35_session_set_attention_split(s, src->split_keys);
     if (r) {

@@ -9,9 +9,13 @@
 // one file-scope device array, `scratch`, of kStaticScratchBytes; each device
 // holds its own copy for the life of the process, and its address is taken
 // once per device with hipGetSymbolAddress. Calls on one device share the
-// array, so calls that overlap on one device race; nothing but the ticket and
-// the argmax key has to start at zero, and both are cleared by a fill kernel
-// at the start of every call (no memset node, so a caller may capture it).
+// array, so each call holds that device's lock from its first launch until
+// its stream has drained: calls from several threads (or on several streams)
+// of one device run one after another instead of overwriting each other's
+// buffers. Nothing but the ticket and the argmax key has to start at zero,
+// and both are cleared by a fill kernel at the start of every call. The call
+// synchronises its stream and reads the token back before it returns, so it
+// cannot be recorded into a captured graph.
 
 namespace cq35 {
 
@@ -30,6 +34,9 @@ namespace {
 
 std::mutex g_static_lock;
 void* g_static_ptr[64] = {};
+// one lock per device, held by a call from its first launch to its final
+// stream synchronisation (the calls of one device share its scratch copy)
+std::mutex g_static_call[64];
 
 // Device address of `scratch` on the current device (taken once per device).
 int static_scratch(int device, unsigned char** out) {
@@ -134,6 +141,7 @@ extern "C" int cq35_step_static(const cq35_model* model, uint16_t* state, int64_
   int rc = static_scratch(model->device, &base);
   if (rc) return rc;
   static_layout(&view, base);
+  std::lock_guard<std::mutex> serial(g_static_call[model->device]);
   const uint64_t params[2] = {(uint64_t)start, token};
   unsigned long long key = 0;
   hipError_t e = hipSuccess;

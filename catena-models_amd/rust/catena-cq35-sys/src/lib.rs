@@ -1,4 +1,4 @@
-//! Raw declarations of `include/cq35.h` (ABI version 2) and thin owning
+//! Raw declarations of `include/cq35.h` (ABI version 3) and thin owning
 //! wrappers, for catena-models' Rust host. The host replaces its three
 //! `Artifact::exec_values` call sites for the Qwen artifact
 //! (src/model.rs:248-258 `qwen3.init`, 260-328 `qwen3`, 209-246
@@ -8,10 +8,11 @@
 #![allow(non_camel_case_types)]
 
 use std::ffi::{c_char, c_int, c_void, CStr, CString};
+use std::marker::PhantomData;
 use std::os::unix::ffi::OsStrExt;
 use std::path::Path;
 
-pub const CQ35_ABI_VERSION: c_int = 2;
+pub const CQ35_ABI_VERSION: c_int = 3;
 pub const CQ35_OK: c_int = 0;
 pub const CQ35_EINVAL: c_int = -1;
 pub const CQ35_ERANGE: c_int = -2;
@@ -98,6 +99,7 @@ extern "C" {
     pub fn cq35_session_set_persistent(session: *mut cq35_session, enabled: c_int) -> c_int;
     pub fn cq35_session_set_attention_split(session: *mut cq35_session, keys: i64) -> c_int;
     pub fn cq35_session_set_matrix_prefill(session: *mut cq35_session, components: c_int) -> c_int;
+    pub fn cq35_session_set_matrix_decode(session: *mut cq35_session, enabled: c_int) -> c_int;
 }
 
 /// `Ok(())` for CQ35_OK, else the code with the library's message for this thread.
@@ -110,10 +112,10 @@ pub fn check(rc: c_int) -> anyhow::Result<()> {
 }
 
 /// Weights placed in HBM once (the reference keeps zero-copy host views,
-/// src/checkpoint.rs:197-231).
+/// src/checkpoint.rs:197-231). `Send` but not `Sync`: the model may move to
+/// another thread, and its sessions borrow it, so it outlives them.
 pub struct Model(*mut cq35_model);
 unsafe impl Send for Model {}
-unsafe impl Sync for Model {}
 
 impl Model {
     /// `weights[i]`: host pointer of tensor i in weight_specs order (src/spec.rs:443-712).
@@ -141,11 +143,14 @@ impl Model {
         Ok(c)
     }
 
-    /// `qwen3.init(capacity)` (src/model.rs:248-258).
-    pub fn session(&self, capacity: i64) -> anyhow::Result<Session> {
+    /// `qwen3.init(capacity)` (src/model.rs:248-258). The session borrows
+    /// the model (as the reference's `Session<'a>` borrows `&'a Model`,
+    /// src/model.rs:421-427): the weights cannot be freed while it lives.
+    pub fn session(&self, capacity: i64) -> anyhow::Result<Session<'_>> {
+        let vocab = self.config()?.vocab as usize;
         let mut s = std::ptr::null_mut();
         check(unsafe { cq35_session_init(self.0, capacity, &mut s) })?;
-        Ok(Session { raw: s, capacity })
+        Ok(Session { raw: s, capacity, vocab, _model: PhantomData })
     }
 }
 
@@ -156,20 +161,26 @@ impl Drop for Model {
 }
 
 /// The opaque session state (BF16 cache, F32 workspace). One caller at a
-/// time; after a failed step the state is gone (CQ35_EPOISONED), as the
-/// reference drops its state when exec fails (src/model.rs:711-730).
-pub struct Session {
+/// time (`&mut self`); after a failed step the state is gone
+/// (CQ35_EPOISONED), as the reference drops its state when exec fails
+/// (src/model.rs:711-730). Distinct sessions may step on distinct threads.
+pub struct Session<'m> {
     raw: *mut cq35_session,
     capacity: i64,
+    vocab: usize,
+    _model: PhantomData<&'m Model>,
 }
-unsafe impl Send for Session {}
+unsafe impl Send for Session<'_> {}
 
-impl Session {
+impl<'m> Session<'m> {
     /// `qwen3(tokens, state, capacity, start, weights...)` (src/model.rs:260-328):
     /// the tokens at positions start..start+n, the greedy next token, and
     /// the last position's BF16 logits when `logits` is given (vocab entries).
     pub fn step(&mut self, tokens: &[u64], start: i64, logits: Option<&mut [u16]>) -> anyhow::Result<u64> {
         let mut next = 0u64;
+        if let Some(l) = logits.as_deref() {
+            anyhow::ensure!(l.len() >= self.vocab, "logits buffer holds {} entries, vocab is {}", l.len(), self.vocab);
+        }
         let lp = logits.map_or(std::ptr::null_mut(), |l| l.as_mut_ptr());
         check(unsafe {
             cq35_step(self.raw, tokens.as_ptr(), tokens.len() as i64, start, self.capacity, &mut next, lp)
@@ -178,10 +189,10 @@ impl Session {
     }
 
     /// `qwen3.copy-buffer(-16)` over the whole state (src/model.rs:209-246).
-    pub fn copy(&self) -> anyhow::Result<Session> {
+    pub fn copy(&self) -> anyhow::Result<Session<'m>> {
         let mut s = std::ptr::null_mut();
         check(unsafe { cq35_session_copy(self.raw, &mut s) })?;
-        Ok(Session { raw: s, capacity: self.capacity })
+        Ok(Session { raw: s, capacity: self.capacity, vocab: self.vocab, _model: PhantomData })
     }
 
     /// InferenceOptions::wmma_prefill (src/catena.rs:12-26): CQ35_MATRIX_* bits.
@@ -189,26 +200,38 @@ impl Session {
         check(unsafe { cq35_session_set_matrix_prefill(self.raw, components) })
     }
 
+    /// Matrix-core products in `step_batch` when every session of the batch
+    /// sets this (tolerance-level; no reference counterpart).
+    pub fn set_matrix_decode(&mut self, enabled: bool) -> anyhow::Result<()> {
+        check(unsafe { cq35_session_set_matrix_decode(self.raw, enabled as c_int) })
+    }
+
     pub fn raw(&self) -> *mut cq35_session {
         self.raw
     }
 }
 
-impl Drop for Session {
+impl Drop for Session<'_> {
     fn drop(&mut self) {
         unsafe { cq35_session_free(self.raw) };
     }
 }
 
 /// One decode step for each session (a serving round; the reference steps
-/// them one after another, src/server/engine.rs:143-207).
-pub fn step_batch(sessions: &mut [&mut Session], tokens: &[u64], starts: &[i64]) -> anyhow::Result<Vec<u64>> {
+/// them one after another, src/server/engine.rs:143-207). With `logits`,
+/// session i's BF16 logits land in `logits[i * vocab ..]`.
+pub fn step_batch(sessions: &mut [&mut Session<'_>], tokens: &[u64], starts: &[i64],
+                  logits: Option<&mut [u16]>) -> anyhow::Result<Vec<u64>> {
     anyhow::ensure!(sessions.len() == tokens.len() && tokens.len() == starts.len(), "one token and start per session");
+    if let Some(l) = logits.as_deref() {
+        let need = sessions.iter().map(|s| s.vocab).sum::<usize>();
+        anyhow::ensure!(sessions.iter().all(|s| s.vocab == sessions[0].vocab), "sessions of different vocabularies");
+        anyhow::ensure!(l.len() >= need, "logits buffer holds {} entries, {} sessions need {need}", l.len(),
+                        sessions.len());
+    }
     let raw: Vec<*mut cq35_session> = sessions.iter().map(|s| s.raw).collect();
     let mut next = vec![0u64; raw.len()];
-    check(unsafe {
-        cq35_step_batch(raw.as_ptr(), tokens.as_ptr(), starts.as_ptr(), raw.len() as i64, next.as_mut_ptr(),
-                        std::ptr::null_mut())
-    })?;
+    let lp = logits.map_or(std::ptr::null_mut(), |l| l.as_mut_ptr());
+    check(unsafe { cq35_step_batch(raw.as_ptr(), tokens.as_ptr(), starts.as_ptr(), raw.len() as i64, next.as_mut_ptr(), lp) })?;
     Ok(next)
 }

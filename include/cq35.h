@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define CQ35_ABI_VERSION 2  /* 2: cq35_step_batch logits, cq35_device_matrix_gemm modes */
+#define CQ35_ABI_VERSION 3  /* 3: cq35_session_set_matrix_decode; 2: cq35_step_batch logits */
 
 enum {
   CQ35_OK = 0,
@@ -149,8 +149,8 @@ int cq35_step(cq35_session* session, const uint64_t* tokens, int64_t n, int64_t 
  * logits[i * vocab ..]. Dense sessions of one model and capacity take one
  * weight-shared step (each layer's weights read once for all of them); each
  * session's result is then identical to its own cq35_step, unless every
- * session of the batch selects the matrix-core projections
- * (cq35_session_set_matrix_prefill), in which case the products run on MFMA
+ * session of the batch selects matrix-core decode
+ * (cq35_session_set_matrix_decode), in which case the products run on MFMA
  * (hardware accumulation order: tolerance-level, like the matrix-core
  * prefill). Other sessions on the per-kernel path are launched back to back
  * on their own streams and then completed, so their kernels overlap on the
@@ -164,8 +164,8 @@ int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const
                     int64_t count, uint64_t* next_tokens, uint16_t* logits);
 
 /* A decode step (one token) that allocates nothing, for callers that cannot
- * allocate device memory: code under HIP graph capture, tight serving loops
- * and harnesses that forbid hipMalloc. No counterpart in the reference.
+ * allocate device memory: tight serving loops and harnesses that forbid
+ * hipMalloc. No counterpart in the reference.
  * `state` is caller-owned device memory holding the BF16 session state of
  * `capacity` positions in the reference layout (cq35_session_state_bytes
  * with which = 0, e.g. copied from cq35_session_export_state); it is updated
@@ -175,8 +175,11 @@ int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const
  * logits != NULL, the BF16 logits to host memory. Every other buffer comes
  * from one static device array of 16 MiB per device (held until the process
  * ends), which bounds the capacity: about 80K positions at the 35B-A3B shape;
- * larger capacities are rejected with CQ35_ERANGE before any work. Calls
- * that overlap on one device share that array and race. */
+ * larger capacities are rejected with CQ35_ERANGE before any work. Calls on
+ * one device share that array: each holds a per-device lock from its first
+ * launch until its stream has drained, so calls from several threads or
+ * streams of one device run one after another. The call synchronises its
+ * stream before returning, so it cannot run under HIP graph capture. */
 int cq35_step_static(const cq35_model* model, uint16_t* state, int64_t capacity, uint64_t token,
                      int64_t start, void* stream, uint64_t* next_token, uint16_t* logits);
 
@@ -226,21 +229,6 @@ int cq35_session_set_graph(cq35_session* session, int enabled);
 int cq35_session_set_persistent(cq35_session* session, int enabled);
 int cq35_session_persistent(const cq35_session* session, int* enabled);
 
-/* Matrix-core prefill: components of multi-token calls run on MFMA, whose
- * F32 accumulation order is the hardware's, so results match the exact path
- * to accumulation rounding rather than bit for bit. Replaces the reference's
- * InferenceOptions::wmma_prefill with CATENA_WMMA_COMPONENTS (catena.rs:12-26,
- * qwen35.rs:467-541; default off in its library API, as here). Bit 0: the
- * dense projections (attention, DeltaNet and output projections, dense FFN);
- * bit 1: the MoE expert projections (grouped routed experts and the shared
- * expert); bit 2: the full-attention layers' attention over the prompt rows
- * (scores and context on MFMA with the reference's BF16 score, probability
- * and context rounding, qwen35_wmma_attention.hex; head_dim 64, 128 or 256,
- * other head dims keep the exact kernels). 0 keeps the exact SIMT path. A session whose components are set
- * at its first multi-token call runs multi-token calls in chunks of 1024
- * tokens (otherwise 256; the chunk changes no result). Single-session decode
- * steps are unaffected; the weight-shared batched step (cq35_step_batch)
- * runs its products on MFMA when every session of the batch has bit 0. */
 /* Split-K decode attention for long contexts. Over more than `keys` cached
  * keys (default CQ35_SPLIT_KEYS_DEFAULT; 0: never) the T tiles (8 keys) of
  * each query head's online softmax form at most 128 ranges of ceil(T / 128)
@@ -255,11 +243,37 @@ int cq35_session_persistent(const cq35_session* session, int* enabled);
 int cq35_session_set_attention_split(cq35_session* session, int64_t keys);
 int cq35_session_attention_split(const cq35_session* session, int64_t* keys);
 
+/* Matrix-core prefill: components of multi-token calls run on MFMA, whose
+ * F32 accumulation order is the hardware's, so results match the exact path
+ * to accumulation rounding rather than bit for bit. Replaces the reference's
+ * InferenceOptions::wmma_prefill with CATENA_WMMA_COMPONENTS (catena.rs:12-26,
+ * qwen35.rs:467-541; default off in its library API, as here). Bit 0: the
+ * dense projections (attention, DeltaNet and output projections, dense FFN);
+ * bit 1: the MoE expert projections (grouped routed experts and the shared
+ * expert); bit 2: the full-attention layers' attention over the prompt rows
+ * (scores and context on MFMA with the reference's BF16 score, probability
+ * and context rounding, qwen35_wmma_attention.hex; head_dim 64, 128 or 256,
+ * other head dims keep the exact kernels). 0 keeps the exact SIMT path. A
+ * session whose components are set at its first multi-token call runs
+ * multi-token calls in chunks of 1024 tokens (otherwise 256; the chunk
+ * changes no result). Decode steps (cq35_step with n == 1, and
+ * cq35_step_batch) are unaffected, as the reference's option affects prefill
+ * only. */
 #define CQ35_MATRIX_PROJECTIONS 1
 #define CQ35_MATRIX_EXPERTS 2
 #define CQ35_MATRIX_ATTENTION 4
 int cq35_session_set_matrix_prefill(cq35_session* session, int components);
 int cq35_session_matrix_prefill(const cq35_session* session, int* components);
+
+/* Matrix-core batched decode (no reference counterpart): 1 lets the
+ * weight-shared step of cq35_step_batch run its products on MFMA (hardware
+ * accumulation order, tolerance-level) for a batch in which EVERY session has
+ * this option set; a batch with any session at 0 (the default) takes the
+ * exact products, so each session's tokens are then identical to its own
+ * cq35_step. Single-session steps are unaffected. Copied by
+ * cq35_session_copy. */
+int cq35_session_set_matrix_decode(cq35_session* session, int enabled);
+int cq35_session_matrix_decode(const cq35_session* session, int* enabled);
 
 /* Host-side builds of the device numerics (same source), for CPU checks. */
 float cq35_numeric_exp(float x);

@@ -95,6 +95,10 @@ def lib():
         l.ox_k_gated_norm.argtypes = [P, P, P, P, P]
         l.ox_k_attention.argtypes = [P, ctypes.c_int, P, P, I64, P, I64, P]
         l.ox_session_set_split_keys.argtypes = [P, I64]
+        l.ox_k_select.argtypes = [P, I64, I64, P, P]
+        l.ox_k_argmax.argtypes = [P, I64]
+        l.ox_k_argmax.restype = U64
+        l.ox_moe_route.argtypes = [P, P, P, I64, I64, I64, P, P, P]
         _lib = l
     return _lib
 
@@ -105,7 +109,8 @@ PLANTS = {
     "rope_pairing": 1, "rope_sign": 2, "rope_freq_hd": 3, "qk_norm_swap": 4,
     "conv_tap_order": 5, "delta_scale": 6, "l2_whole": 7, "gated_sum": 8,
     "attn_scale": 9, "gqa_map": 10, "norm_weight": 11, "key_head": 12,
-    "delta_pred_decay": 13,
+    "delta_pred_decay": 13, "select_tie_high": 14, "select_ascending": 15,
+    "prob_unnormalised": 16, "softmax_all": 17, "shared_gate": 18, "argmax_last": 19,
 }
 
 
@@ -164,6 +169,21 @@ def dot_b256(x: np.ndarray, w: np.ndarray) -> float:
     x = np.ascontiguousarray(x, dtype=np.uint16)
     w = np.ascontiguousarray(w, dtype=np.uint16)
     return lib().ox_dot_b256(x.ctypes.data, w.ctypes.data, len(x) // 2)
+
+
+def select(logits: np.ndarray, k: int):
+    """Top-k ids (rank order) and routing weights over F32 router logits."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    ids = np.zeros(k, dtype=np.int64)
+    probs = np.zeros(k, dtype=np.float32)
+    lib().ox_k_select(lg.ctypes.data, lg.size, k, ids.ctypes.data, probs.ctypes.data)
+    return ids, probs
+
+
+def argmax(logits: np.ndarray) -> int:
+    """Greedy token over BF16 logit bits."""
+    lg = np.ascontiguousarray(logits, dtype=np.uint16)
+    return int(lib().ox_k_argmax(lg.ctypes.data, lg.size))
 
 
 # ------------------------------------------------------------- weights/model

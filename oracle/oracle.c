@@ -847,6 +847,35 @@ static void attention_staged(const ox_model* m, const uint16_t* q, const uint16_
  * per token, batch_moe.hex:45-96) and the top-k selection: stable rank,
  * softmax over the selected logits with a serial denominator
  * (moe.hex:86-252; batch_moe.hex:136-281). */
+/* Top-k of E router logits (moe.hex:86-252): expert e's rank is the number
+ * of experts with a larger logit plus those with an equal logit and a lower
+ * index (stable, ties toward the lower index); ids[rank] = e for rank < K;
+ * p_j = exp(l_j - l_top) / den with den summed serially in rank order. NaN
+ * logits can make two experts share a rank and leave another unassigned; an
+ * unassigned rank k keeps expert k. */
+static void select_top_k(const float* logit, int64_t E, int64_t K, int64_t* ids, float* prob) {
+  float sel[64];
+  for (int64_t j = 0; j < K; ++j) { ids[j] = j; sel[j] = logit[j]; }
+  for (int64_t e = 0; e < E; ++e) {
+    int64_t rank = 0;
+    for (int64_t i = 0; i < E; ++i) {
+      int larger = logit[i] > logit[e];
+      int smaller = logit[e] > logit[i];
+      if (g_plant == OX_PLANT_SELECT_ASCENDING) { int t = larger; larger = smaller; smaller = t; }
+      int before = g_plant == OX_PLANT_SELECT_TIE_HIGH ? i > e : i < e;
+      rank += larger ? 1 : ((before && !smaller) ? 1 : 0);
+    }
+    if (rank < K) { ids[rank] = e; sel[rank] = logit[e]; }
+  }
+  float ex[64], den = 0.0f;
+  for (int64_t j = 0; j < K; ++j) ex[j] = ox_exp(sel[j] - sel[0]);
+  if (g_plant == OX_PLANT_SOFTMAX_ALL)
+    for (int64_t e = 0; e < E; ++e) den = den + ox_exp(logit[e] - sel[0]);
+  else
+    for (int64_t j = 0; j < K; ++j) den = den + ex[j];
+  for (int64_t j = 0; j < K; ++j) prob[j] = g_plant == OX_PLANT_PROB_UNNORMALISED ? ex[j] : ex[j] / den;
+}
+
 static void moe_route(const ox_model* m, const uint16_t* x, const float* router,
                       const float* shared_router, int64_t* ids, float* prob, float* shared_prob) {
   const int64_t H = m->c.hidden, E = m->c.experts, K = m->c.top_k;
@@ -854,24 +883,8 @@ static void moe_route(const ox_model* m, const uint16_t* x, const float* router,
 #pragma omp parallel for schedule(static)
   for (int64_t e = 0; e <= E; ++e)
     logit[e] = ox_dot_width_f32w(x, e < E ? router + e * H : shared_router, H / 2, 32);
-  float sel[64];
-  /* NaN logits can make two experts share a rank and leave another
-   * unassigned; an unassigned rank k keeps expert k. */
-  for (int64_t j = 0; j < K; ++j) { ids[j] = j; sel[j] = logit[j]; }
-  for (int64_t e = 0; e < E; ++e) {
-    int64_t rank = 0;
-    for (int64_t i = 0; i < E; ++i) {
-      int larger = logit[i] > logit[e];
-      int smaller = logit[e] > logit[i];
-      rank += larger ? 1 : ((i < e && !smaller) ? 1 : 0);
-    }
-    if (rank < K) { ids[rank] = e; sel[rank] = logit[e]; }
-  }
-  float ex[64], den = 0.0f;
-  for (int64_t j = 0; j < K; ++j) ex[j] = ox_exp(sel[j] - sel[0]);
-  for (int64_t j = 0; j < K; ++j) den = den + ex[j];
-  for (int64_t j = 0; j < K; ++j) prob[j] = ex[j] / den;
-  *shared_prob = ox_sigmoid(logit[E]);
+  select_top_k(logit, E, K, ids, prob);
+  *shared_prob = g_plant == OX_PLANT_SHARED_GATE ? 1.0f : ox_sigmoid(logit[E]);
   free(logit);
 }
 
@@ -983,6 +996,7 @@ static void moe_ffn(const ox_model* m, ox_session* se, int l, int ffn, const uin
 static int argmax_bf16(const uint16_t* logits, int64_t vocab, uint64_t* token) {
   /* fused_argmax.hex: strict > from (0, -inf) over 256 contiguous chunks,
    * then a strict > reduce; the result is the first index of the maximum. */
+  const int last = g_plant == OX_PLANT_ARGMAX_LAST;
   int64_t chunk = (vocab + 255) / 256;
   uint64_t best_tok = 0;
   float best = bitsf(0xFF800000u);
@@ -992,9 +1006,9 @@ static int argmax_bf16(const uint16_t* logits, int64_t vocab, uint64_t* token) {
     float mx = bitsf(0xFF800000u);
     for (int64_t i = base; i < base + chunk && i < vocab; ++i) {
       float v = ox_bf2f(logits[i]);
-      if (v > mx) { mx = v; t = (uint64_t)i; }
+      if (v > mx || (last && v == mx)) { mx = v; t = (uint64_t)i; }
     }
-    if (mx > best) { best = mx; best_tok = t; }
+    if (mx > best || (last && mx == best && base < vocab)) { best = mx; best_tok = t; }
   }
   *token = best_tok;
   return 0;
@@ -1347,21 +1361,7 @@ void ox_moe_route(const uint16_t* x, const float* router, const float* shared_ro
                   int64_t E, int64_t K, float* logits, int64_t* ids, float* probs) {
   for (int64_t e = 0; e <= E; ++e)
     logits[e] = ox_dot_width_f32w(x, e < E ? router + e * H : shared_router, H / 2, 32);
-  float sel[64];
-  for (int64_t j = 0; j < K; ++j) { ids[j] = j; sel[j] = logits[j]; }
-  for (int64_t e = 0; e < E; ++e) {
-    int64_t rank = 0;
-    for (int64_t i = 0; i < E; ++i) {
-      int larger = logits[i] > logits[e];
-      int smaller = logits[e] > logits[i];
-      rank += larger ? 1 : ((i < e && !smaller) ? 1 : 0);
-    }
-    if (rank < K) { ids[rank] = e; sel[rank] = logits[e]; }
-  }
-  float ex[64], den = 0.0f;
-  for (int64_t j = 0; j < K; ++j) ex[j] = ox_exp(sel[j] - sel[0]);
-  for (int64_t j = 0; j < K; ++j) den = den + ex[j];
-  for (int64_t j = 0; j < K; ++j) probs[j] = ex[j] / den;
+  select_top_k(logits, E, K, ids, probs);
 }
 
 /* ------------------------------------------ kernel-level entry points */
@@ -1411,6 +1411,18 @@ void ox_k_delta(const ox_model* m, const uint16_t* conv, const uint16_t* q, cons
 void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z, const float* w,
                      uint16_t* out) {
   gated_norm(m, core, z, w, out);
+}
+
+/* Top-k selection alone, over given router logits (moe.hex:86-252). */
+void ox_k_select(const float* logits, int64_t E, int64_t K, int64_t* ids, float* probs) {
+  select_top_k(logits, E, K, ids, probs);
+}
+
+/* Greedy argmax over BF16 logits (fused_argmax.hex:1-205). */
+uint64_t ox_k_argmax(const uint16_t* logits, int64_t vocab) {
+  uint64_t t = 0;
+  argmax_bf16(logits, vocab, &t);
+  return t;
 }
 
 /* Decode attention over `keys` cached rows: kv = [keys][KVS] keys then

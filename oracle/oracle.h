@@ -159,7 +159,13 @@ enum {
   OX_PLANT_GQA_MAP = 10,         /* query head h reads KV head h % kv_heads */
   OX_PLANT_NORM_WEIGHT = 11,     /* RMS norms without their weights */
   OX_PLANT_KEY_HEAD = 12,        /* value head h reads key head h / (VH/KH) */
-  OX_PLANT_DELTA_PRED_DECAY = 13 /* prediction from the undecayed state */
+  OX_PLANT_DELTA_PRED_DECAY = 13, /* prediction from the undecayed state */
+  OX_PLANT_SELECT_TIE_HIGH = 14,  /* equal router logits ranked toward the higher index */
+  OX_PLANT_SELECT_ASCENDING = 15, /* the K smallest router logits selected */
+  OX_PLANT_PROB_UNNORMALISED = 16,/* routing weights not divided by the top-k sum */
+  OX_PLANT_SOFTMAX_ALL = 17,      /* routing softmax over all experts, not the top k */
+  OX_PLANT_SHARED_GATE = 18,      /* shared expert without its sigmoid gate */
+  OX_PLANT_ARGMAX_LAST = 19       /* argmax ties resolved to the last index */
 };
 void ox_set_plant(int which);
 
@@ -196,6 +202,8 @@ void ox_k_gated_norm(const ox_model* m, const uint16_t* core, const uint16_t* z,
                      uint16_t* out);
 void ox_k_attention(const ox_model* m, int online, const uint16_t* q, const uint16_t* kv, int64_t keys,
                     const uint16_t* qg, int64_t split_keys, uint16_t* out);
+void ox_k_select(const float* logits, int64_t E, int64_t K, int64_t* ids, float* probs);
+uint64_t ox_k_argmax(const uint16_t* logits, int64_t vocab);
 
 #ifdef __cplusplus
 }

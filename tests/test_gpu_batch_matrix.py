@@ -1,5 +1,5 @@
 """The weight-shared batched decode step with its products on MFMA
-(cq35_step_batch when every session selects the matrix-core projections):
+(cq35_step_batch when every session selects matrix-core decode):
 hardware accumulation order, so it is held to the tolerance the reference
 sets for its own matrix-core path (at most 5% relative logit RMS,
 PREFILL_BENCHMARKS.md:83, 105), against the exact weight-shared step that
@@ -52,7 +52,7 @@ def run(model, cfg, B, rounds, cap, seed):
         for t in p:
             s.step_raw([t], want_logits=False)
     for s in matrix:
-        s.set_matrix_prefill(Session.MATRIX_PROJECTIONS)
+        s.set_matrix_decode(True)
     feed = list(first)
     rows, flips = [], 0
     for r in range(rounds):
@@ -111,10 +111,10 @@ def test_matrix_batch_switch_off_is_exact():
     group = [model.session(40) for _ in prompts]
     toks = [s.append_next_token(p) for s, p in zip(group, prompts)]
     for s in group:
-        s.set_matrix_prefill(Session.MATRIX_PROJECTIONS)
+        s.set_matrix_decode(True)
     toks = cq35.decode_batch(group, toks)
     for s in group:
-        s.set_matrix_prefill(0)
+        s.set_matrix_decode(False)
     alone = []
     for src in group:
         a = model.session(40)
@@ -127,3 +127,41 @@ def test_matrix_batch_switch_off_is_exact():
         assert toks == want
     for a, s in zip(alone, group):
         assert np.array_equal(a.export_state(0), s.export_state(0))
+
+
+def test_matrix_decode_is_its_own_option():
+    """The matrix-core batched decode has an option of its own: the prefill
+    option (the reference's wmma_prefill, prefill only) leaves the batched
+    decode exact, a batch with one session without matrix-core decode is
+    exact for every session, and only an all-matrix batch takes the MFMA
+    products (its logits then differ from the exact step's, by rounding)."""
+    cfg = cc.preset("mini")
+    model = cq35.Model.synthetic(cfg, seed=23)
+    B = 4
+    prompts = [[(7 * b + 5 * i) % cfg["vocab"] for i in range(5 + b)] for b in range(B)]
+
+    def group(prefill, decode):
+        g = [model.session(40) for _ in prompts]
+        toks = [s.append_next_token(p) for s, p in zip(g, prompts)]
+        for s, pf, dc in zip(g, prefill, decode):
+            s.set_matrix_prefill(pf)
+            s.set_matrix_decode(dc)
+            assert s.matrix_prefill == pf and s.matrix_decode == dc
+        return g, toks
+
+    exact, toks = group([0] * B, [False] * B)
+    prefill_only, _ = group([Session.MATRIX_PROJECTIONS] * B, [False] * B)
+    mixed, _ = group([0] * B, [True] * (B - 1) + [False])
+    matrix, _ = group([0] * B, [True] * B)
+    te, le = cq35.decode_batch(exact, toks, logits=True)
+    for name, g in [("prefill option only", prefill_only), ("mixed batch", mixed)]:
+        t, l = cq35.decode_batch(g, toks, logits=True)
+        assert t == te and np.array_equal(l, le), f"{name}: should be the exact step"
+    tm, lm = cq35.decode_batch(matrix, toks, logits=True)
+    assert not np.array_equal(lm, le), "the all-matrix batch should take the MFMA products"
+    worst = max(rel_rms(f32(lm[b]), f32(le[b])) for b in range(B))
+    say(f"all-matrix batch vs exact: {worst:.4f}")
+    assert worst <= 0.05
+    # the option travels with a checkpoint copy
+    resumed = model.resume_checkpoint(matrix[0].into_checkpoint())
+    assert resumed.matrix_decode and resumed.matrix_prefill == 0

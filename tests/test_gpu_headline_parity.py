@@ -7,6 +7,8 @@ ABI on an MI355X:
   token, the BF16 logits and each layer's top-k expert ids (rank order,
   qwen35_moe.hex:86-252) equal the restatement's; at the end the whole
   session state (KV, conv history, DeltaNet state) equals it bit for bit.
+  The same checks from imported states at 600 and 32768 cached keys (split-K
+  on and off).
 - qwen35-2b (dense): batch 1 against the restatement, and 16 sessions
   stepped together through cq35_step_batch against the same sessions
   stepped alone, one of them also against the restatement.
@@ -19,6 +21,7 @@ import time
 
 import numpy as np
 import pytest
+import torch
 
 import cq35
 import cq35.config as cc
@@ -42,12 +45,13 @@ def host_bytes_free() -> int:
         return 1 << 62
 
 
-def oracle_run(oracle, cfg, prompt, steps, capacity):
+def oracle_run(oracle, cfg, prompt, steps, capacity, om=None):
     """Restatement: batched prompt, then greedy steps; per call the token,
     the BF16 logits and (MoE) the per-layer ids."""
     t0 = time.time()
-    om = oracle.Model(cfg, oracle.synthetic_weights(cfg, SEED))
-    say(f"  restatement weights ready in {time.time() - t0:.1f}s")
+    if om is None:
+        om = oracle.Model(cfg, oracle.synthetic_weights(cfg, SEED))
+        say(f"  restatement weights ready in {time.time() - t0:.1f}s")
     s = om.session(capacity)
     calls = []
     tok, logits = s.step(prompt, 0)
@@ -95,15 +99,19 @@ def moe35(oracle):
     prompt = np.random.default_rng(SEED).integers(0, cfg["vocab"], PROMPT).tolist()
     cap = PROMPT + STEPS + 1
     say("35B restatement: prompt", PROMPT, "steps", STEPS)
-    calls, cache = oracle_run(oracle, cfg, prompt, STEPS, cap)
+    t0 = time.time()
+    om = oracle.Model(cfg, oracle.synthetic_weights(cfg, SEED))
+    say(f"  restatement weights ready in {time.time() - t0:.1f}s")
+    calls, cache = oracle_run(oracle, cfg, prompt, STEPS, cap, om)
     model = cq35.Model.synthetic(cfg, seed=SEED)
-    return cfg, prompt, cap, calls, cache, model
+    yield cfg, prompt, cap, calls, cache, model, om
+    del om
 
 
 @pytest.mark.timeout(400)
 @pytest.mark.parametrize("persistent", [True, False], ids=["persistent", "per-kernel"])
 def test_35b_decode_matches_restatement(moe35, persistent):
-    cfg, prompt, cap, ref, ref_cache, model = moe35
+    cfg, prompt, cap, ref, ref_cache, model, _ = moe35
     say("35B GPU run, persistent =", persistent)
     got, cache = gpu_run(model, cfg, prompt, STEPS, cap, persistent)
     compare(f"35B persistent={persistent}", got, ref)
@@ -113,7 +121,7 @@ def test_35b_decode_matches_restatement(moe35, persistent):
 def test_35b_router_ids_are_a_valid_top_k(moe35):
     """The exported ids are distinct experts in descending logit rank: a
     check that does not go through the restatement."""
-    cfg, prompt, cap, ref, _, model = moe35
+    cfg, prompt, cap, ref, _, model, _ = moe35
     s = model.session(cap)
     s.step_raw(prompt)
     ids = s.router_ids()
@@ -121,6 +129,56 @@ def test_35b_router_ids_are_a_valid_top_k(moe35):
     for row in ids:
         assert len(set(row.tolist())) == cfg["top_k"]
         assert row.min() >= 0 and row.max() < cfg["experts"]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("start,split", [(600, None), (32768, None), (32768, 0)],
+                         ids=["600", "32768-split", "32768-exact"])
+def test_35b_long_context_matches_restatement(moe35, start, split):
+    """The 35B-A3B instantiation at the contexts the benchmark measures,
+    from an imported seeded state (the long-context recipe: KV N(0,1) x 0.1,
+    conv history N(0,1) x 0.1, DeltaNet state N(0,1)): around the headline
+    context (600 cached keys, the single chain) and at 32768 keys, where the
+    attention runs split-K by default (128 ranges, 8 query heads per KV head,
+    the flash and merge phases) and, with the split off, the reference's
+    single chain. Three greedy steps on both decode paths against the
+    restatement with the same split setting: tokens, BF16 logits and every
+    layer's expert ids at every step, the whole state at the end."""
+    from test_gpu_long_context import seeded_state
+    cfg, _, _, _, _, model, om = moe35
+    steps, first = 3, 4242
+    capacity = start + steps + 5
+    say("35B long context", start, "split", split)
+    state = seeded_state(cfg, capacity, start, seed=19, device="cuda")
+    torch.cuda.empty_cache()
+    t0 = time.time()
+    os_ = om.session(capacity)
+    if split is not None:
+        os_.set_split_keys(split)
+    os_.import_cache(state)
+    ref, tok = [], first
+    for i in range(steps):
+        tok, logits = os_.step([tok], start + i)
+        ref.append((tok, logits, os_.last_ids().reshape(cfg["layers"], -1)))
+    want = os_.cache()
+    del os_
+    say(f"  restatement done in {time.time() - t0:.1f}s")
+    for persistent in (True, False):
+        s = model.session(capacity)
+        if split is not None:
+            s.set_attention_split(split)
+        s.set_persistent(persistent)
+        assert s.persistent == persistent
+        s.import_state(0, state)
+        s.position = start
+        got, tok = [], first
+        for _ in range(steps):
+            logits, tok = s.step_raw([tok])
+            got.append((tok, logits, s.router_ids()))
+        compare(f"35B {start} split={split} persistent={persistent}", got, ref)
+        assert np.array_equal(s.export_state(0), want), f"35B {start}: session state differs"
+        say(f"  persistent={persistent}: equal")
+        del s
 
 
 @pytest.fixture(scope="module")

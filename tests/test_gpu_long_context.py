@@ -242,3 +242,51 @@ def test_split_attention_holds_the_parity_bar(persistent):
     rel = float(np.sqrt(np.mean((re - rs) ** 2)) / np.sqrt(np.mean(re ** 2)))
     say(f"  DeltaNet state relative difference {rel:.3g}")
     assert rel <= 1e-3, rel
+
+
+@pytest.mark.timeout(300)
+def test_split_attention_full_depth_one_step(models):
+    """The split's effect at the full 40-layer 35B-A3B shape: one decode step
+    from the same imported 32768-key state, split-K (the default) against the
+    reference's single chain, for eight different input tokens. Both runs see
+    identical inputs, so the difference is the split's rounding carried
+    through the 10 full-attention layers and the 30 layers after and between
+    them. Recorded: the largest |logit difference|, the logits' relative RMS
+    difference, the greedy tokens and the DeltaNet state's relative
+    difference. Asserted: the same greedy token except where the exact
+    logits' top two lie within the measured deviation, and the DeltaNet
+    state within the north-star bar of 1e-3 relative."""
+    name = "qwen36-35b-a3b"
+    cfg = cc.preset(name)
+    start = 32768
+    capacity = start + 8
+    state = seeded_state(cfg, capacity, start, seed=29, device="cuda")
+    torch.cuda.empty_cache()
+    m = models(name)
+    worst, worst_rel, worst_state, flips = 0.0, 0.0, 0.0, 0
+    for first in [11, 4321, 99991, 123456, 200003, 7, 65000, 248000]:
+        runs = {}
+        for split in (None, 0):
+            s = m.session(capacity)
+            if split is not None:
+                s.set_attention_split(split)
+            s.import_state(0, state)
+            s.position = start
+            logits, tok = s.step_raw([first])
+            runs[split] = (logits, tok, recurrent_states(cfg, s.export_state(0), capacity))
+            del s
+        (ls, ts, rs), (le, te, re) = runs[None], runs[0]
+        fs, fe = cq35.read_logits(ls).astype(np.float64), cq35.read_logits(le).astype(np.float64)
+        d = float(np.max(np.abs(fs - fe)))
+        rel = float(np.sqrt(np.mean((fs - fe) ** 2)) / np.sqrt(np.mean(fe ** 2)))
+        st = float(np.sqrt(np.mean((rs - re) ** 2)) / np.sqrt(np.mean(re ** 2)))
+        top2 = np.sort(fe)[-2:]
+        say(f"  token {first}: max |dlogit| {d:.4g}, logit rel RMS {rel:.3g}, state rel {st:.3g}, "
+            f"greedy {ts} vs {te} (exact top-2 gap {top2[1] - top2[0]:.4g})")
+        if ts != te:
+            assert top2[1] - top2[0] <= 2 * d, f"token {first}: split changed the greedy token away from a tie"
+            flips += 1
+        worst, worst_rel, worst_state = max(worst, d), max(worst_rel, rel), max(worst_state, st)
+    say(f"  full depth, 32768 keys, split vs exact: max |dlogit| {worst:.4g}, logit rel RMS {worst_rel:.3g}, "
+        f"DeltaNet state rel {worst_state:.3g}, near-tie token changes {flips}")
+    assert worst_state <= 1e-3, worst_state

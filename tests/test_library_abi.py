@@ -34,7 +34,7 @@ def test_header_symbols_exported(lib):
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.EXPORTED)
-    assert lib.cq35_abi_version() == 2
+    assert lib.cq35_abi_version() == 3
 
 
 def header_parameters(name):
@@ -63,6 +63,17 @@ def test_rust_binding_matches_header():
         hv = re.search(r"#define " + const + r" (\d+)", header).group(1)
         rv = re.search(r"pub const " + const + r": \w+ = (\d+);", src).group(1)
         assert hv == rv, const
+    # memory safety of the owning wrappers: a session borrows its model (the
+    # model cannot be freed under a live session), the model is not shared
+    # between threads, and host buffers are checked against the vocabulary
+    # before the library writes to them
+    assert re.search(r"pub struct Session<'m>\s*\{[^}]*_model: PhantomData<&'m Model>", src)
+    assert re.search(r"pub fn session\(&self, capacity: i64\) -> anyhow::Result<Session<'_>>", src)
+    assert "unsafe impl Sync for Model" not in src
+    step = src.split("pub fn step(&mut self")[1].split("cq35_step(")[0]
+    assert "l.len() >= self.vocab" in step
+    batch = src.split("pub fn step_batch(")[1].split("cq35_step_batch(")[0]
+    assert "l.len() >= need" in batch
     # the struct's fields in the header's order
     hfields = re.findall(r"^\s+(?:int32_t|float) (\w+);", header.split("typedef struct cq35_config")[1].split("}")[0], re.M)
     rfields = re.findall(r"pub (\w+): (?:i32|f32),", src.split("pub struct cq35_config")[1].split("}")[0])

@@ -374,8 +374,8 @@ def test_decode_state_pinned(oracle, name):
     """Six prompt tokens and three greedy steps, one token per call: every
     cached K and V row of the full-attention layers and every DeltaNet state
     against the float64 textbook (fed the restatement's tokens). Within BF16
-    activation noise; planted mistakes in the head norms, RoPE, conv taps and
-    the delta rule miss by far more."""
+    activation noise; planted mistakes in the head norms, RoPE, conv taps,
+    the delta rule and (MoE) the expert routing miss by far more."""
     from textbook import Textbook
     cfg = cc.preset(name)
     rng = np.random.default_rng(31)
@@ -404,6 +404,11 @@ def test_decode_state_pinned(oracle, name):
               "delta_pred_decay", "delta_scale", "norm_weight"]
     if cfg["value_heads"] > cfg["key_heads"]:
         plants.append("key_head")
+    if cfg["moe"]:
+        # routing semantics (moe.hex:86-252, 254-369): descending selection,
+        # weights renormalised over the top k only, the shared expert's
+        # sigmoid gate
+        plants += ["select_ascending", "prob_unnormalised", "softmax_all", "shared_gate"]
     check(oracle, measure, 12 * U, plants, f"decode state {name}")
 
 

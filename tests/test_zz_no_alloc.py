@@ -84,6 +84,61 @@ def test_static_step_matches_session_step(name):
         buf.free()
 
 
+def test_static_steps_from_two_threads_serialise():
+    """Two threads step two different caller-owned states through
+    cq35_step_static at the same time (ctypes releases the GIL during the
+    call, so the calls overlap on the host): each call holds the device's
+    lock until its stream has drained, so each thread's tokens, logits and
+    final state equal the same steps taken by cq35_step on a session."""
+    import threading
+    name, capacity, steps = "mini-moe", 64, 8
+    cfg = cc.preset(name)
+    model = model_of(name)
+    rng = np.random.default_rng(11)
+    prompts = [rng.integers(0, cfg["vocab"], 6).tolist() for _ in range(2)]
+    starts, bufs, firsts, refs = [], [], [], []
+    for p in prompts:
+        s = model.session(capacity)
+        for t in p:
+            tok = s.append_next_token([t])
+        buf = DeviceBuffer(s.state_bytes(0))
+        buf.upload(s.export_state(0))
+        bufs.append(buf)
+        firsts.append(tok)
+        starts.append(len(p))
+        calls, t = [], tok
+        for _ in range(steps):
+            lg, t = s.step_raw([t])
+            calls.append((t, lg))
+        refs.append((calls, s.export_state(0)))
+    got = [[] for _ in prompts]
+    errors = []
+    barrier = threading.Barrier(2)
+
+    def worker(i):
+        try:
+            barrier.wait()
+            t = firsts[i]
+            for k in range(steps):
+                t, lg = static_step(model, bufs[i], capacity, t, starts[i] + k)
+                got[i].append((t, lg))
+        except Exception as e:  # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for i, (calls, state) in enumerate(refs):
+        say("static step thread", i)
+        for k, ((gt, gl), (rt, rl)) in enumerate(zip(got[i], calls)):
+            assert gt == rt and np.array_equal(gl, rl), (i, k)
+        assert np.array_equal(bufs[i].download(np.uint16), state), i
+        bufs[i].free()
+
+
 def test_static_step_rejects_bad_arguments():
     cfg = cc.preset("qwen36-35b-a3b")
     model = model_of("qwen36-35b-a3b")
