@@ -18,19 +18,31 @@
 // contribute p = 0 against key 0's value), so the result is bit-identical.
 #pragma once
 
-#include "gemv.h"
+#include "layers.h"
 
 namespace cq35 {
 
 constexpr int kScoreBlock = 256;  // 8 key units of 32 lanes
 
+// rows != nullptr: grid z is the session of a batched step (its cache,
+// position, query rows [z][q_heads * head_dim] and scores [z][q_heads][stride]).
 __global__ __launch_bounds__(kScoreBlock) void k_attn_scores(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
     const uint64_t* __restrict__ params, int t, int kvs, int head_dim, int heads_per_kv,
-    float scale, float* __restrict__ scores, int stride) {
+    float scale, float* __restrict__ scores, int stride, const SessionRows* __restrict__ rows) {
   extern __shared__ float qs[];  // heads_per_kv * head_dim
   const int kvh = blockIdx.y, tid = threadIdx.x;
-  const int64_t keys = (int64_t)params[0] + t + 1;
+  int64_t keys;
+  if (rows) {
+    const int b = blockIdx.z;
+    const int q_heads = gridDim.y * heads_per_kv;
+    keys = (int64_t)rows->position[b] + 1;
+    cache = rows->cache[b];
+    q += (size_t)b * q_heads * head_dim;
+    scores += (size_t)b * q_heads * stride;
+  } else {
+    keys = (int64_t)params[0] + t + 1;
+  }
   const int nq = heads_per_kv * head_dim;
   for (int i = tid; i < nq; i += kScoreBlock) qs[i] = bf2f(q[(size_t)kvh * nq + i]);
   __syncthreads();

@@ -1,0 +1,516 @@
+// Weight-shared decode step for MoE sessions (same model and capacity, one
+// token each): the non-expert weights of every layer are read once for all
+// the sessions' tokens, the routed experts once per distinct expert of the
+// round (the union of the sessions' top-k), the shared expert once.
+//
+// The reference steps sessions one after another (src/server/engine.rs:
+// 143-207); each token's arithmetic here is exactly its single-session
+// decode step (the per-kernel kernels of gemv.h / attention.h and the
+// persistent step, bit for bit):
+//
+//  k_ws256     S256 grouped projections (qwen35.group-project) for NB tokens
+//              staged in LDS, k_project256's lane order and tree;
+//  router      F32 router rows (moe.hex:4-84) for 16 tokens per block: the
+//              batched prefill's k_brouter_shared (k_router_select's order);
+//  k_sselect   per token: stable rank top-k and the softmax weights
+//              (moe.hex:86-252), the ids also copied to the session's export
+//              row;
+//  k_bgate     per distinct routed expert (the first (token, slot) that
+//              selects it owns it) its gate/up rows applied to every token
+//              that selected it, with that token's weight; the shared expert's
+//              rows applied to every token (moe.hex:254-333);
+//  k_bdown     per (output row, token): the S32 over the token's concatenated
+//              expert rows in slot order, the shared S32 and the residual
+//              (moe.hex:371-434); the rows of experts that several tokens
+//              chose are read from HBM once and from L2 after;
+//  k_bflash /  decode attention per session over its own cache: split-K
+//  k_bmerge    ranges (one block per (KV head, range), all the group's query
+//              heads, one channel per thread) merged in ascending order, or
+//              the single chain per query head, as the session's split
+//              threshold selects; k_attn_values' arithmetic.
+#pragma once
+
+#include "attention.h"
+#include "batch.h"
+#include "prefill.h"
+
+namespace cq35 {
+
+// ------------------------------------------------ S256 grouped projection
+
+// Rows of up to four segments for NB tokens of already normalised rows
+// (cols <= kBatchChunk, staged once): token t's output row r of segment s
+// goes to seg.out[s][t * seg.rows[s] + r]. Each wave runs kRW rows, one at a
+// time, 64 lanes per row, lane l visiting quads l, l + 64, ... in order.
+template <int kRW>
+__global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x, int tokens, int groups,
+                                                  Segments seg, int cols) {
+  constexpr int NB = kBatchNB, RW = kRW, NQ = 4;
+  extern __shared__ __align__(16) float xf[];  // [NB][cols]
+  int rb, tg;
+  batch_block(blockIdx.x, groups, &rb, &tg);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quads = cols >> 3;
+  const int total = seg.rows[0] + seg.rows[1] + seg.rows[2] + seg.rows[3];
+  const int row0 = (rb * 4 + wave) * RW;
+  const int t0 = tg * NB;
+  u32x4 wv[RW][NQ];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    int local;
+    const int s = segment_of(seg, min(row0 + r, total - 1), &local);
+    const uint16_t* wr = segment_w(seg, s) + (size_t)local * cols;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) wv[r][j] = ldq(wr, min(lane + 64 * j, quads - 1));
+  }
+  stage_f32<NB>(xf, x, tokens, t0, cols, 0, cols);
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    Quad acc[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) quad_zero(acc[t]);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+      if (lane + 64 * j < quads) {
+#pragma unroll
+        for (int t = 0; t < NB; ++t) quad_acc_staged(acc[t], xf + t * cols, quads, lane + 64 * j, wv[r][j]);
+      }
+    const int row = row0 + r;
+    int local;
+    const int s = segment_of(seg, min(row, total - 1), &local);
+    const int srows = s == 0 ? seg.rows[0] : s == 1 ? seg.rows[1] : s == 2 ? seg.rows[2] : seg.rows[3];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const float v = quad_tree<64>(acc[t]);
+      if (lane == 0 && row < total && t0 + t < tokens) segment_out(seg, s)[(size_t)(t0 + t) * srows + local] = f2bf(v);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- router
+
+// The router logits come from the batched prefill's k_brouter_shared (each
+// row read once per 16 tokens, k_router_select's lane order and tree).
+//
+// Top-k of one token per block (moe.hex:86-252): rank(e) = #{i : l_i > l_e}
+// + #{i < e : !(l_e > l_i)} (the stable descending order; with NaN logits
+// an unassigned rank k keeps expert k, as in k_router_select), then
+// p_j = exp(l_j - l_0) / den with den summed left to right from 0. The ids
+// also go to row `layer` of the session's export buffer.
+__global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ logits, int experts, int top_k,
+                                                    int* __restrict__ ids, float* __restrict__ probs,
+                                                    const SessionRows* __restrict__ rows, int layer) {
+  extern __shared__ float lg[];  // experts
+  __shared__ float chosen[64];
+  __shared__ int sid[64];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const float* src = logits + (size_t)b * (experts + 1);
+  for (int e = tid; e < experts; e += blockDim.x) lg[e] = src[e];
+  if (tid < top_k) {
+    sid[tid] = tid;
+    chosen[tid] = src[tid];
+  }
+  __syncthreads();
+  for (int e = tid; e < experts; e += blockDim.x) {
+    const float le = lg[e];
+    int rank = 0;
+    for (int i = 0; i < experts; ++i) {
+      const float o = lg[i];
+      rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+    }
+    if (rank < top_k) {
+      sid[rank] = e;
+      chosen[rank] = le;
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int lane = tid;
+    const float ex = lane < top_k ? hexp(chosen[lane] - chosen[0]) : 0.0f;
+    float den = 0.0f;
+    for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
+    if (lane < top_k) {
+      probs[b * top_k + lane] = ex / den;
+      ids[b * top_k + lane] = sid[lane];
+      if (rows->ids[b]) rows->ids[b][layer * top_k + lane] = sid[lane];
+    }
+  }
+}
+
+// ----------------------------------------------------------- expert gate/up
+
+// Rows per wave and per block of k_bgate.
+constexpr int kBGateRW = 2;
+constexpr int kBGateRows = 4 * kBGateRW;
+constexpr int kBGateStage = 8;  // token rows staged per pass
+
+// Block (item, row block): items [0, tokens * top_k) are (token, slot)
+// pairs, item tokens * top_k the shared expert. A routed item runs only if
+// its (token, slot) is the first in token order to select the expert; it
+// then applies the expert's gate/up rows of its row block to every token
+// that selected the expert (dual S256, k_gate_up's order):
+// act[t][slot * I + row] = bf16(silu(bf16 g) * bf16 u * p_{t,slot}); the
+// shared item applies the shared rows to every token:
+// act[t][K * I + row] = bf16(bf16(bf16(silu(bf16 g)) * bf16 u) * sigmoid(l_E)).
+// x [tokens][cols] normalised rows, cols <= 2048.
+__global__ __launch_bounds__(kBlock) void k_bgate(
+    const uint16_t* __restrict__ x, int tokens, int cols, const uint16_t* __restrict__ gate,
+    const uint16_t* __restrict__ up, const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ sup,
+    const int* __restrict__ ids, const float* __restrict__ probs, const float* __restrict__ logits, int experts,
+    int top_k, int inter, int shared_inter, int row_blocks, uint16_t* __restrict__ act) {
+  constexpr int RW = kBGateRW, NQ = 4;
+  extern __shared__ __align__(16) u32x4 xs[];  // [kBGateStage][quads]
+  // (token, slot) pairs that chose the expert: at most one per token, more
+  // only if NaN router logits made a token's ranks collide (its slots can
+  // then repeat an expert); bounded by tokens * top_k <= kMaxSessions * 16
+  __shared__ int list_t[kMaxSessions * 16], list_k[kMaxSessions * 16];
+  __shared__ int nlist, owner;
+  const int item = blockIdx.x / row_blocks, rbk = blockIdx.x - item * row_blocks;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+  const int quads = cols >> 3;
+  const int routed_items = tokens * top_k;
+  const bool shared = item == routed_items;
+  const int nrows = shared ? shared_inter : inter;
+  const int row0 = rbk * kBGateRows + wave * RW;
+  if (rbk * kBGateRows >= nrows) return;  // block-uniform
+  const int e = shared ? 0 : ids[item];
+  // weights first: the expert's rows (or the shared rows) of this wave
+  u32x4 gv[RW][NQ], uv[RW][NQ];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int row = min(row0 + r, nrows - 1);
+    const uint16_t* g = shared ? sgate + (size_t)row * cols : gate + ((size_t)e * inter + row) * cols;
+    const uint16_t* u = shared ? sup + (size_t)row * cols : up + ((size_t)e * inter + row) * cols;
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      gv[r][j] = ldq(g, min(lane + 64 * j, quads - 1));
+      uv[r][j] = ldq(u, min(lane + 64 * j, quads - 1));
+    }
+  }
+  if (tid == 0) {
+    owner = 1;
+    nlist = 0;
+  }
+  __syncthreads();
+  if (shared) {
+    if (tid < tokens) {
+      list_t[tid] = tid;
+      list_k[tid] = -1;
+    }
+    if (tid == 0) nlist = tokens;
+  } else {
+    const int t = item / top_k;
+    // an earlier token that chose the same expert owns it
+    for (int i = tid; i < t * top_k; i += blockDim.x)
+      if (ids[i] == e) owner = 0;
+    __syncthreads();
+    if (!owner) return;  // block-uniform
+    if (tid == 0) {
+      int n = 0;
+      for (int u = t; u < tokens; ++u)
+        for (int k = 0; k < top_k; ++k)
+          if (ids[u * top_k + k] == e) {
+            list_t[n] = u;
+            list_k[n] = k;
+            ++n;
+          }
+      nlist = n;
+    }
+  }
+  __syncthreads();
+  const int n = nlist;
+  const int I = inter;
+  const int act_row = top_k * inter + shared_inter;
+  for (int base = 0; base < n; base += kBGateStage) {
+    const int m = min(kBGateStage, n - base);
+    __syncthreads();  // the previous pass's readers are done
+    for (int i = tid; i < m * quads; i += blockDim.x) {
+      const int s = i / quads, o = i - s * quads;
+      xs[s * quads + o] = ldq(x + (size_t)list_t[base + s] * cols, o);
+    }
+    __syncthreads();
+    for (int s = 0; s < m; ++s) {
+      const int t = list_t[base + s], k = list_k[base + s];
+      const u32x4* xr = xs + s * quads;
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        Quad ga, ua;
+        quad_zero(ga);
+        quad_zero(ua);
+#pragma unroll
+        for (int j = 0; j < NQ; ++j)
+          if (lane + 64 * j < quads) {
+            const u32x4 xq = xr[lane + 64 * j];
+            quad_acc(ga, xq, gv[r][j]);
+            quad_acc(ua, xq, uv[r][j]);
+          }
+        const float gsum = quad_tree<64>(ga);
+        const float usum = quad_tree<64>(ua);
+        const int row = row0 + r;
+        if (lane == 0 && row < nrows) {
+          const float gb = rbf(gsum), ub = rbf(usum);
+          const float activated = silu(gb);
+          if (!shared) {
+            const float y = (activated * ub) * probs[t * top_k + k];
+            act[(size_t)t * act_row + (size_t)k * I + row] = f2bf(y);
+          } else {
+            const float y = rbf(rbf(activated) * ub) * sigmoid(logits[(size_t)t * (experts + 1) + experts]);
+            act[(size_t)t * act_row + (size_t)top_k * I + row] = f2bf(y);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------- expert down
+
+constexpr int kBDownRows = 8;    // output rows per block
+constexpr int kBDownTokens = 4;  // tokens per block
+
+// Block (row block, token group): 32 groups of 8 lanes, group g = output row
+// row0 + (g & 7) of token t0 + (g >> 3). Lane q of a group runs reference
+// lanes 4q..4q+3 of the S32: quads q, q + 8, ... of the token's concatenated
+// routed row (slot order; expert ids[slot]'s row) and of the shared row,
+// then out = bf16(bf16(routed + residual) (+) bf16(shared)) (k_moe_down's
+// order). The group's tokens' activations are staged in LDS. Requires
+// inter % 64 == 0 and shared_inter % 64 == 0.
+__global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ act, int tokens,
+                                                  const uint16_t* __restrict__ down,
+                                                  const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
+                                                  const uint16_t* __restrict__ residual, int hidden, int top_k,
+                                                  int inter, int shared_inter, uint16_t* __restrict__ out) {
+  extern __shared__ __align__(16) u32x4 as[];  // [kBDownTokens][per_row quads]
+  const int iq = inter >> 3, sq = shared_inter >> 3, rq = top_k * iq, per_row = rq + sq;
+  const int lane = threadIdx.x & 63, tid = threadIdx.x;
+  const int g = tid >> 3, q = lane & 7;
+  const int t0 = blockIdx.y * kBDownTokens;
+  const int row = blockIdx.x * kBDownRows + (g & (kBDownRows - 1));
+  const int ti = g / kBDownRows;
+  const int t = t0 + ti;
+  const bool live = t < tokens && row < hidden;
+  const int rowc = min(row, hidden - 1), tc = min(t, tokens - 1);
+  const int ntok = min(kBDownTokens, tokens - t0);
+  for (int i = tid; i < ntok * per_row; i += blockDim.x) {
+    const int s = i / per_row, o = i - s * per_row;
+    as[i] = ldq(act + (size_t)(t0 + s) * per_row * 8, o);
+  }
+  Quad r, sh;
+  quad_zero(r);
+  quad_zero(sh);
+  // the shared row first (its loads overlap the staging)
+  const uint16_t* sw = sdown + (size_t)rowc * shared_inter;
+  constexpr int NS = 8;
+  u32x4 swv[NS];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) swv[j] = ldq(sw, min(q + 8 * j, sq - 1));
+  __syncthreads();
+  const u32x4* xr = as + (size_t)ti * per_row;
+  const int* tid_ids = ids + (size_t)tc * top_k;
+  constexpr int NW = 8;  // quads per lane per slot at inter 512
+  for (int k = 0; k < top_k; ++k) {
+    const uint16_t* wr = down + ((size_t)tid_ids[k] * hidden + rowc) * inter;
+    for (int j0 = 0; j0 < iq / 8; j0 += NW) {
+      u32x4 wv[NW];
+#pragma unroll
+      for (int j = 0; j < NW; ++j) wv[j] = ldq(wr, min(q + 8 * (j0 + j), iq - 1));
+#pragma unroll
+      for (int j = 0; j < NW; ++j)
+        if (j0 + j < iq / 8) quad_acc(r, xr[k * iq + q + 8 * (j0 + j)], wv[j]);
+    }
+  }
+  for (int j0 = 0; j0 < sq / 8; j0 += NS) {
+    if (j0 > 0) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) swv[j] = ldq(sw, min(q + 8 * (j0 + j), sq - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NS; ++j)
+      if (j0 + j < sq / 8) quad_acc(sh, xr[rq + q + 8 * (j0 + j)], swv[j]);
+  }
+  const float rv = quad_tree<8>(r);
+  const float sv = quad_tree<8>(sh);
+  if (q == 0 && live) {
+    const size_t o = (size_t)t * hidden + row;
+    out[o] = bf_add(f2bf(rv + bf2f(residual[o])), f2bf(sv));
+  }
+}
+
+inline size_t bdown_lds_bytes(int per_row_quads) { return (size_t)kBDownTokens * per_row_quads * 16; }
+
+// -------------------------------------------------------------- attention
+
+// Scores come from k_attn_scores with the session table (grid z = session).
+//
+// k_bflash: block (range, head group, session) with one thread per channel
+// and one wave for the denominators. kHPB > 1: split sessions only, the
+// group is a KV head's query heads and the tiles are range r's; kHPB == 1:
+// sessions at or below their split threshold, the group one query head and
+// the tiles all of them (range 0). Tiles run in sub-chunks of up to 64: the
+// scores of the sub-chunk staged, each head's running maximum per tile
+// (reset at the range start), alpha_t = exp(m_{t-1} - m_t), p = exp(s - m_t)
+// (invalid keys p = 0 against key 0's value), then per channel and head the
+// chain acc = acc * alpha_t + p_0 v_0 + ... + p_7 v_7 and per head
+// den = den * alpha_t + p_0 + ... + p_7 (k_attn_values' arithmetic). Split:
+// the range's (m_r, den_r, acc_r[HD]) go to part; single chain: the output
+// bf16(bf16(acc / den) * sigmoid(gate)).
+constexpr int kFlashSub = 64;  // tiles per sub-chunk
+constexpr int kFlashMaxHeads = 8;
+
+inline int flash_threads(int head_dim) { return (head_dim + 63) / 64 * 64 + 64; }
+
+template <int kHPB>
+__global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores, int stride,
+                                                const SessionRows* __restrict__ rows, int64_t value_base, int kvs,
+                                                int head_dim, int q_heads, int heads_per_kv,
+                                                const uint16_t* __restrict__ qg, float* __restrict__ part,
+                                                uint16_t* __restrict__ out) {
+  constexpr int HPB = kHPB;
+  __shared__ float p[HPB][kFlashSub * 8];
+  __shared__ float alpha[HPB][kFlashSub];
+  __shared__ float mtile[HPB][kFlashSub];
+  __shared__ float mrun[HPB], dfinal[HPB];
+  const int b = blockIdx.z, tid = threadIdx.x;
+  const int64_t keys = (int64_t)rows->position[b] + 1;
+  const int tiles = (int)((keys + 7) >> 3);
+  const int64_t sk = rows->split[b];
+  const bool split = sk > 0 && keys > sk;
+  if ((HPB > 1) != split) return;
+  const int range_tiles = split ? (tiles + kSplitRanges - 1) / kSplitRanges : tiles;
+  const int r = blockIdx.x;
+  if (r * range_tiles >= tiles) return;
+  const int t_begin = r * range_tiles, t_end = min(tiles, t_begin + range_tiles);
+  const int nh = HPB > 1 ? heads_per_kv : 1;
+  const int h0 = HPB > 1 ? blockIdx.y * heads_per_kv : blockIdx.y;
+  const int kvh = h0 / heads_per_kv;
+  const int hd_pad = (head_dim + 63) / 64 * 64;
+  const bool chan = tid < head_dim;
+  const bool den_lane = tid >= hd_pad && tid - hd_pad < nh;
+  const int dh = tid - hd_pad;
+  const float ninf = bitsf(0xff800000u);
+  const float* sb = scores + (size_t)b * q_heads * stride;
+  const uint16_t* vb = rows->cache[b] + value_base + (int64_t)kvh * head_dim + (chan ? tid : 0);
+  float acc[HPB];
+#pragma unroll
+  for (int h = 0; h < HPB; ++h) acc[h] = 0.0f;
+  float den = 0.0f;
+  if (tid < nh) mrun[tid] = ninf;
+  for (int c0 = t_begin; c0 < t_end; c0 += kFlashSub) {
+    const int nt = min(kFlashSub, t_end - c0), nk = nt * 8;
+    const int64_t k0 = (int64_t)c0 * 8;
+    __syncthreads();  // the previous sub-chunk's readers are done
+    for (int i = tid; i < nh * nk; i += blockDim.x) {
+      const int h = i / nk, kk = i - h * nk;
+      const int64_t k = k0 + kk;
+      p[h][kk] = k < keys ? sb[(size_t)(h0 + h) * stride + k] : ninf;
+    }
+    __syncthreads();
+    if (tid < nh) {
+      const int h = tid;
+      float m = mrun[h];
+      for (int i = 0; i < nt; ++i) {
+        float tm = ninf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tm = fmaxf(tm, p[h][i * 8 + j]);
+        const float prev = (c0 + i == t_begin) ? ninf : m;
+        m = fmaxf(m, tm);
+        mtile[h][i] = m;
+        alpha[h][i] = hexp(prev - m);
+      }
+      mrun[h] = m;
+    }
+    __syncthreads();
+    for (int i = tid; i < nh * nk; i += blockDim.x) {
+      const int h = i / nk, kk = i - h * nk;
+      const int64_t k = k0 + kk;
+      p[h][kk] = k < keys ? hexp(p[h][kk] - mtile[h][kk >> 3]) : 0.0f;
+    }
+    __syncthreads();
+    if (chan) {
+      float vn[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t k = k0 + j;
+        vn[j] = bf2f(vb[(k < keys ? k : 0) * kvs]);
+      }
+      for (int i = 0; i < nt; ++i) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = vn[j];
+        if (i + 1 < nt) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const int64_t k = k0 + (i + 1) * 8 + j;
+            vn[j] = bf2f(vb[(k < keys ? k : 0) * kvs]);
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < HPB; ++h) {
+          if (h < nh) {
+            float a = acc[h] * alpha[h][i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a = a + p[h][i * 8 + j] * v[j];
+            acc[h] = a;
+          }
+        }
+      }
+    } else if (den_lane) {
+      for (int i = 0; i < nt; ++i) {
+        den = den * alpha[dh][i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) den = den + p[dh][i * 8 + j];
+      }
+    }
+  }
+  if (split) {
+    for (int h = 0; h < nh; ++h) {
+      float* pr = part + (((size_t)b * q_heads + h0 + h) * kSplitRanges + r) * (2 + head_dim);
+      if (chan) pr[2 + tid] = acc[h];
+      if (den_lane && dh == h) {
+        pr[0] = mrun[h];
+        pr[1] = den;
+      }
+    }
+  } else {
+    if (den_lane) dfinal[dh] = den;
+    __syncthreads();
+    if (chan) {
+      for (int h = 0; h < nh; ++h) {
+        const int head = h0 + h;
+        const float gate = sigmoid(bf2f(qg[(size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim +
+                                           head_dim + tid]));
+        out[(size_t)b * q_heads * head_dim + head * head_dim + tid] = f2bf(rbf(acc[h] / dfinal[h]) * gate);
+      }
+    }
+  }
+}
+
+// Merge of a split session's ranges per (query head, session), one thread
+// per channel: M = max_r m_r, then in ascending range order
+// den = 0 + den_r w_r, acc = 0 + acc_r w_r with w_r = exp(m_r - M);
+// out = bf16(bf16(acc / den) * sigmoid(gate)).
+__global__ __launch_bounds__(256) void k_bmerge(const float* __restrict__ part, const SessionRows* __restrict__ rows,
+                                                int head_dim, int q_heads, const uint16_t* __restrict__ qg,
+                                                uint16_t* __restrict__ out) {
+  const int head = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
+  const int64_t keys = (int64_t)rows->position[b] + 1;
+  const int64_t sk = rows->split[b];
+  if (!(sk > 0 && keys > sk) || c >= head_dim) return;
+  const int tiles = (int)((keys + 7) >> 3);
+  const int range_tiles = (tiles + kSplitRanges - 1) / kSplitRanges;
+  const int nranges = (tiles + range_tiles - 1) / range_tiles;
+  const float* pr = part + ((size_t)b * q_heads + head) * kSplitRanges * (2 + head_dim);
+  float top = bitsf(0xff800000u);
+  for (int r = 0; r < nranges; ++r) top = fmaxf(top, pr[(size_t)r * (2 + head_dim)]);
+  float acc = 0.0f, den = 0.0f;
+  for (int r = 0; r < nranges; ++r) {
+    const float* e = pr + (size_t)r * (2 + head_dim);
+    const float w = hexp(e[0] - top);
+    acc = acc + e[2 + c] * w;
+    den = den + e[1] * w;
+  }
+  const float gate = sigmoid(bf2f(qg[(size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim + head_dim + c]));
+  out[(size_t)b * q_heads * head_dim + head * head_dim + c] = f2bf(rbf(acc / den) * gate);
+}
+
+}  // namespace cq35

@@ -23,6 +23,8 @@ struct SessionRows {
   uint16_t* cache[kMaxSessions];
   uint64_t position[kMaxSessions];
   uint64_t token[kMaxSessions];
+  int* ids[kMaxSessions];          // MoE: the session's per-layer top-k export row
+  int64_t split[kMaxSessions];     // MoE: the session's split-K threshold (0: never)
 };
 
 // Embedding row gather (embedding.hex:5-14) and the F32 RoPE table

@@ -27,6 +27,7 @@
 #include "mfma.h"
 #include "gguf.h"
 #include "batch.h"
+#include "batch_moe.h"
 
 using namespace cq35;
 
@@ -1300,7 +1301,7 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           dim3((unsigned)std::min<int64_t>((cap + 7) / 8, 512), (unsigned)d.KVH), dim3(kScoreBlock),
           (size_t)(d.Q / d.KVH) * d.HD * 4, (const uint16_t*)s->qr, (const uint16_t*)s->cache,
           key_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH),
-          scale, s->attn_scratch, s->attn_stride);
+          scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr);
         L(KC_ATTENTION_VALUES, k_attn_values,
           dim3((unsigned)d.Q, (unsigned)((d.HD + kValueChannels - 1) / kValueChannels)), dim3(64),
           attn_values_lds_bytes(cap), (const float*)s->attn_scratch,
@@ -2039,6 +2040,13 @@ struct BatchWorkspace {
   float2* gates = nullptr;       // per session and value head (decay, rate)
   f32x16_t* mx_part = nullptr;  // matrix-core products: partial tiles of split column ranges
   unsigned long long* mx_keys = nullptr;  // and the head's per-tile argmax keys [token tiles][32-row tiles][32]
+  // MoE: router logits [B][E + 1], top-k ids and weights [B][K], expert
+  // activations [B][K * I + SI], split-K range partials [B][Q][128][2 + HD]
+  float* rlogits = nullptr;
+  int* bids = nullptr;
+  float* bprobs = nullptr;
+  uint16_t* bact = nullptr;
+  float* part = nullptr;
   hipGraph_t graph[2][kMaxSessions + 1] = {};      // [matrix-core products][sessions]
   hipGraphExec_t exec[2][kMaxSessions + 1] = {};
   std::vector<void*> allocs;
@@ -2112,6 +2120,13 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
   alloc(&b->mx_part, (int64_t)1024 * 2 * 2 * 64);
   alloc(&b->gates, B * (int64_t)c.value_heads);
   alloc(&b->mx_keys, ((B + 31) / 32) * ((d.V + 31) / 32 + 2) * 32);
+  if (c.moe) {
+    alloc(&b->rlogits, B * (d.E + 1));
+    alloc(&b->bids, B * d.K);
+    alloc(&b->bprobs, B * d.K);
+    alloc(&b->bact, B * (d.K * d.I + d.SI));
+    alloc(&b->part, (int64_t)B * d.Q * kSplitRanges * (2 + d.HD));
+  }
   (void)wide;
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_rows, sizeof(SessionRows), hipHostMallocDefault);
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_best, B * sizeof(unsigned long long), hipHostMallocDefault);
@@ -2273,7 +2288,115 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
   ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best, mx ? b : nullptr);
 }
 
-// One weight-shared decode step for `count` dense sessions of one model and
+// The batched decode step's launch sequence for MoE models: every layer of
+// enqueue_token for B sessions, the non-expert products weight-shared (S256
+// projections, S64 output projections, the router, the head), the routed
+// experts once per distinct expert of the round, attention per session (split
+// ranges or the single chain, each session's own threshold).
+void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
+  const cq35_config& c = m->cfg;
+  const Dims& d = m->d;
+  hipStream_t st = b->stream;
+  auto Wt = [&](int64_t index) { return m->w[index]; };
+  const int64_t cap = b->capacity;
+  const SessionRows* rows = b->d_rows;
+  const int H = (int)d.H, E = (int)d.E, K = (int)d.K, I = (int)d.I, SI = (int)d.SI;
+  const int groups = (B + kBatchNB - 1) / kBatchNB;
+  k_sembed<<<dim3((unsigned)grid_for((d.H + kBlock - 1) / kBlock, 64), (unsigned)B), dim3(kBlock), 0, st>>>(
+      rows, (const uint16_t*)Wt(0), H, b->h, (const float*)m->freq, (int)(d.R / 2), b->rope, b->d_best);
+  auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
+    k_bnorm<<<dim3((unsigned)B), dim3(kBlock), (size_t)d.H * 2, st>>>(x, (const float*)w, H, c.eps, out);
+  };
+  auto ws256 = [&](const uint16_t* x, const Segments& seg) {
+    const int row_blocks = (int)((seg_rows(seg) + 4 * 4 - 1) / (4 * 4));
+    k_ws256<4><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), (size_t)kBatchNB * d.H * 4, st>>>(
+        x, B, groups, seg, H);
+  };
+  const int gate_blocks = (int)((std::max(d.I, d.SI) + kBGateRows - 1) / kBGateRows);
+  const int hpk = (int)(d.Q / d.KVH);
+  const int per_row = (int)((d.K * d.I + d.SI) / 8);
+  int64_t base = 1;
+  for (int64_t l = 0; l < d.L; ++l) {
+    auto W = [&](int slot) { return Wt(base + slot); };
+    const int64_t key_base = l * 2 * cap * d.KVS;
+    const int64_t value_base = key_base + cap * d.KVS;
+    norm(b->h, W(0), b->x);
+    int ffn;
+    const void* post_norm;
+    if (is_full(c, l)) {
+      ws256(b->x, segments({{W(1), {b->qg, 2 * d.QS}}, {W(2), {b->kraw, d.KVS}}, {W(3), {b->vraw, d.KVS}}}));
+      k_full_prepare<<<dim3((unsigned)(d.Q + d.KVH), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->qg, (const uint16_t*)b->kraw, (const uint16_t*)b->vraw, (const float*)b->rope,
+          (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
+          (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, b->qr, rows);
+      const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
+      k_attn_scores<<<dim3((unsigned)std::min<int64_t>((cap + 7) / 8, 512), (unsigned)d.KVH, (unsigned)B),
+                      dim3(kScoreBlock), (size_t)hpk * d.HD * 4, st>>>(
+          (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
+          (int)d.HD, hpk, scale, b->scratch, b->stride, rows);
+      const dim3 fb((unsigned)flash_threads((int)d.HD));
+      k_bflash<kFlashMaxHeads><<<dim3((unsigned)kSplitRanges, (unsigned)d.KVH, (unsigned)B), fb, 0, st>>>(
+          (const float*)b->scratch, b->stride, rows, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk,
+          (const uint16_t*)b->qg, b->part, b->ctx);
+      k_bflash<1><<<dim3(1u, (unsigned)d.Q, (unsigned)B), fb, 0, st>>>(
+          (const float*)b->scratch, b->stride, rows, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk,
+          (const uint16_t*)b->qg, b->part, b->ctx);
+      k_bmerge<<<dim3((unsigned)d.Q, (unsigned)B), dim3(256), 0, st>>>((const float*)b->part, rows, (int)d.HD,
+                                                                      (int)d.Q, (const uint16_t*)b->qg, b->ctx);
+      ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, nullptr);
+      post_norm = W(7);
+      ffn = 8;
+    } else {
+      uint16_t* alpha = b->ab;
+      uint16_t* beta = b->ab + (size_t)B * c.value_heads;
+      ws256(b->x, segments({{W(1), {b->qkv, d.QKV}}, {W(2), {b->z, d.VS}}, {W(3), {alpha, c.value_heads}},
+                            {W(4), {beta, c.value_heads}}}));
+      const int64_t conv_base = cap * d.KV_STRIDE + l * d.LIN;
+      k_linear_prepare<<<dim3((unsigned)((d.QKV + c.key_dim - 1) / c.key_dim), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->qkv, (uint16_t*)nullptr, conv_base, (const uint64_t*)nullptr, 0, (const float*)W(9),
+          (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows, (const uint16_t*)alpha,
+          (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), c.value_heads, b->gates);
+      const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
+      k_delta<false><<<dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const float2*)b->gates,
+          (uint16_t*)nullptr, (float*)nullptr,
+          (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
+      k_gated_norm<<<dim3((unsigned)c.value_heads, (unsigned)B), dim3(kBlock), 0, st>>>(
+          (const uint16_t*)b->core, (const uint16_t*)b->z, (const float*)W(7), c.value_dim, c.eps, b->gated);
+      ws64(st, b->gated, B, W(8), d.H, d.VS, b->h, b->attn, nullptr);
+      post_norm = W(10);
+      ffn = 11;
+    }
+    norm(b->attn, post_norm, b->x);
+    {
+      const dim3 rg((unsigned)((E + 1 + kRouterRows - 1) / kRouterRows),
+                    (unsigned)((B + kRouterTokens - 1) / kRouterTokens));
+      const float* rw = (const float*)W(ffn);
+      const float* srw = (const float*)W(ffn + 4);
+      switch (H) {
+        case 2048: k_brouter_shared<32><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
+        case 1024: k_brouter_shared<16><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
+        case 512: k_brouter_shared<8><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
+        default: k_brouter_shared<4><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
+      }
+    }
+    k_sselect<<<dim3((unsigned)B), dim3(kBlock), (size_t)E * 4, st>>>(b->rlogits, E, K, b->bids, b->bprobs, rows,
+                                                                      (int)l);
+    k_bgate<<<dim3((unsigned)((B * K + 1) * gate_blocks)), dim3(kBlock), (size_t)kBGateStage * d.H * 2, st>>>(
+        b->x, B, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
+        (const uint16_t*)W(ffn + 6), b->bids, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks, b->bact);
+    k_bdown<<<dim3((unsigned)((d.H + kBDownRows - 1) / kBDownRows), (unsigned)((B + kBDownTokens - 1) / kBDownTokens)),
+              dim3(kBlock), bdown_lds_bytes(per_row), st>>>(b->bact, B, (const uint16_t*)W(ffn + 3),
+                                                             (const uint16_t*)W(ffn + 7), b->bids, b->attn, H, K, I, SI,
+                                                             b->h);
+    base += layer_tensors(c, l);
+  }
+  const int64_t total = weight_count(c);
+  norm(b->h, Wt(total - 2), b->x);
+  ws32(st, b->x, B, segments({{Wt(total - 1), {b->logits, d.V}}}), d.H, b->d_best, nullptr);
+}
+
+// One weight-shared decode step for `count` sessions of one model and
 // capacity (checked by the caller): tokens[i] at starts[i] of sessions[i].
 int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, const int64_t* starts, int count,
                       uint64_t* next_tokens, uint16_t* logits) {
@@ -2283,14 +2406,18 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   BatchWorkspace* b = nullptr;
   int rc = batch_workspace(m, sessions[0]->capacity, count, &b);
   if (rc) return rc;
+  const bool moe = m->cfg.moe != 0;
   for (int i = 0; i < count; ++i) {
     b->h_rows->cache[i] = sessions[i]->cache;
     b->h_rows->position[i] = (uint64_t)starts[i];
     b->h_rows->token[i] = tokens[i];
+    b->h_rows->ids[i] = moe ? sessions[i]->ids : nullptr;
+    b->h_rows->split[i] = sessions[i]->split_keys;
     sessions[i]->poisoned = true;  // cleared on success
   }
-  // the products run on MFMA when every session selects matrix-core decode
-  bool mx = true;
+  // the products of dense models run on MFMA when every session selects
+  // matrix-core decode (the MoE step has exact products only)
+  bool mx = !moe;
   for (int i = 0; i < count; ++i) mx = mx && sessions[i]->matrix_decode != 0;
   hipError_t e = hipSuccess;
   for (int i = 0; i < count && e == hipSuccess; ++i) e = hipStreamSynchronize(sessions[i]->stream);
@@ -2300,11 +2427,15 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   // of replaying a captured graph, e.g. for kernel tracing
   const char* graph_env = getenv("CQ35_GRAPH");
   const bool use_graph = !(graph_env && atoi(graph_env) == 0);
-  if (e == hipSuccess && !use_graph) enqueue_batch(m, b, count, mx);
+  auto enqueue = [&]() {
+    if (moe) enqueue_batch_moe(m, b, count);
+    else enqueue_batch(m, b, count, mx);
+  };
+  if (e == hipSuccess && !use_graph) enqueue();
   if (e == hipSuccess && use_graph && !b->exec[mx][count]) {
     e = hipStreamBeginCapture(b->stream, hipStreamCaptureModeThreadLocal);
     if (e == hipSuccess) {
-      enqueue_batch(m, b, count, mx);
+      enqueue();
       hipGraph_t g = nullptr;
       e = hipStreamEndCapture(b->stream, &g);
       if (e == hipSuccess) e = hipGraphInstantiate(&b->exec[mx][count], g, nullptr, nullptr, 0);
@@ -2329,14 +2460,25 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   return CQ35_OK;
 }
 
-// Whether a batch can take the weight-shared step: dense sessions of one
-// model and capacity, none of them timing kernels.
+// Whether the MoE shape fits the batched MoE kernels: a hidden width the
+// shared router is instantiated for (staged once by k_ws256 and k_bgate), expert widths in whole 64-element
+// lane rounds (k_bdown), the head dim within one flash block, at most 8 query
+// heads per KV head and 16 experts selected per token.
+bool moe_batch_shape_ok(const cq35_model* m) {
+  const Dims& d = m->d;
+  return (d.H == 2048 || d.H == 1024 || d.H == 512 || d.H == 256) && d.I % 64 == 0 && d.SI % 64 == 0 && d.HD <= 256 &&
+         d.Q / d.KVH <= kFlashMaxHeads && d.K <= 16 && d.E <= 4096;
+}
+
+// Whether a batch can take the weight-shared step: sessions of one model and
+// capacity, none of them timing kernels.
 bool shared_batch_ok(cq35_session* const* sessions, int64_t count) {
   if (count < 2 || count > kMaxSessions) return false;
   if (const char* g = getenv("CQ35_BATCH_SHARED"))
     if (atoi(g) == 0) return false;
   const cq35_model* m = sessions[0]->model;
-  if (m->cfg.moe || m->cfg.hidden > kBatchChunk) return false;  // the SwiGLU stages one row chunk
+  if (m->cfg.hidden > kBatchChunk) return false;  // the SwiGLU and the S256 stage one row chunk
+  if (m->cfg.moe && !moe_batch_shape_ok(m)) return false;
   for (int64_t i = 0; i < count; ++i)
     if (sessions[i]->model != m || sessions[i]->capacity != sessions[0]->capacity || sessions[i]->timed_class >= 0)
       return false;

@@ -181,6 +181,42 @@ def test_35b_long_context_matches_restatement(moe35, start, split):
         del s
 
 
+@pytest.mark.timeout(600)
+def test_35b_batch_matches_alone_and_restatement(moe35):
+    """Eight 35B-A3B sessions stepped together through cq35_step_batch (the
+    weight-shared MoE step) equal the same sessions stepped alone: tokens,
+    BF16 logits and every layer's expert ids at every round, the state at the
+    end; one of them also against the restatement."""
+    cfg, _, _, _, _, model, om = moe35
+    B, rounds = 8, 4
+    rng = np.random.default_rng(SEED + 3)
+    prompts = [rng.integers(0, cfg["vocab"], int(rng.integers(4, 20))).tolist() for _ in range(B)]
+    cap = 24 + rounds + 2
+    group = [model.session(cap) for _ in range(B)]
+    nxt = [s.append_next_token(p) for s, p in zip(group, prompts)]
+    first = list(nxt)
+    calls = []
+    for _ in range(rounds):
+        nxt, lg = cq35.decode_batch(group, nxt, logits=True)
+        calls.append((list(nxt), lg, [s.router_ids() for s in group]))
+    say("35B batch of", B, "done")
+    for b in range(B):
+        alone = model.session(cap)
+        t = alone.append_next_token(prompts[b])
+        assert t == first[b]
+        for r in range(rounds):
+            lg, t = alone.step_raw([t])
+            assert np.array_equal(calls[r][2][b], alone.router_ids()), f"session {b}: ids differ at round {r}"
+            assert t == calls[r][0][b], f"session {b}: token differs at round {r}"
+            assert np.array_equal(calls[r][1][b], lg), f"session {b}: logits differ at round {r}"
+        assert np.array_equal(alone.export_state(0), group[b].export_state(0)), f"session {b}: state differs"
+    ref, ref_cache = oracle_run(None, cfg, prompts[5], rounds, cap, om)
+    assert [c[0] for c in ref] == [first[5]] + [calls[r][0][5] for r in range(rounds)]
+    for r in range(rounds):
+        assert np.array_equal(ref[r + 1][1], calls[r][1][5]) and np.array_equal(ref[r + 1][2], calls[r][2][5])
+    assert np.array_equal(ref_cache, group[5].export_state(0))
+
+
 @pytest.fixture(scope="module")
 def dense2b(oracle):
     cfg = cc.preset("qwen35-2b")
