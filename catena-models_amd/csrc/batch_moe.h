@@ -10,8 +10,8 @@
 //
 //  k_ws256     S256 grouped projections (qwen35.group-project) for NB tokens
 //              staged in LDS, k_project256's lane order and tree;
-//  router      F32 router rows (moe.hex:4-84) for 16 tokens per block: the
-//              batched prefill's k_brouter_shared (k_router_select's order);
+//  k_wsrouter  F32 router rows (moe.hex:4-84), every token per block,
+//              k_router_select's lane order and tree;
 //  k_sselect   per token: stable rank top-k and the softmax weights
 //              (moe.hex:86-252), the ids also copied to the session's export
 //              row;
@@ -23,18 +23,25 @@
 //              expert rows in slot order, the shared S32 and the residual
 //              (moe.hex:371-434); the rows of experts that several tokens
 //              chose are read from HBM once and from L2 after;
-//  k_bflash /  decode attention per session over its own cache: split-K
-//  k_bmerge    ranges (one block per (KV head, range), all the group's query
-//              heads, one channel per thread) merged in ascending order, or
-//              the single chain per query head, as the session's split
-//              threshold selects; k_attn_values' arithmetic.
+//  k_bscores / decode attention per session over its own cache: the scores
+//  k_bflash /  (k_attn_scores' order), then split-K ranges (one block per
+//  k_bmerge    (KV head, range), all the group's query heads, one channel
+//              per thread) merged in ascending order, or the single chain per
+//              query head, as the session's split threshold selects;
+//              k_attn_values' arithmetic.
 #pragma once
 
 #include "attention.h"
 #include "batch.h"
-#include "prefill.h"
 
 namespace cq35 {
+
+// Pointers taken from the session table are generic; loads through them are
+// made global (not flat) so that the wait counters track them alone.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
 
 // ------------------------------------------------ S256 grouped projection
 
@@ -89,43 +96,124 @@ __global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x
 
 // ---------------------------------------------------------------- router
 
-// The router logits come from the batched prefill's k_brouter_shared (each
-// row read once per 16 tokens, k_router_select's lane order and tree).
-//
-// Top-k of one token per block (moe.hex:86-252): rank(e) = #{i : l_i > l_e}
-// + #{i < e : !(l_e > l_i)} (the stable descending order; with NaN logits
-// an unassigned rank k keeps expert k, as in k_router_select), then
-// p_j = exp(l_j - l_0) / den with den summed left to right from 0. The ids
-// also go to row `layer` of the session's export buffer.
+// Router logits of every token: rows [0, E) routed, row E the shared-expert
+// gate, F32 weights; one wave per row, all tokens per block (each row read
+// once), physical lane l = 2r + h running reference lane r's low (h = 0) or
+// high (h = 1) accumulator over floats l, l + 64, ..., then lo + hi and the
+// halving tree (k_router_select's order). logits [tokens][E + 1]. The
+// tokens' rows are staged in LDS as BF16, 8 at a time.
+constexpr int kRouterStage = 8;
+__global__ __launch_bounds__(kBlock) void k_wsrouter(const uint16_t* __restrict__ x, int tokens, int cols,
+                                                     const float* __restrict__ w, const float* __restrict__ shared_w,
+                                                     int experts, float* __restrict__ logits) {
+  extern __shared__ __align__(16) uint16_t xr_s[];  // [kRouterStage][cols]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = experts + 1;
+  const int row = blockIdx.x * 4 + wave;
+  const int rc = min(row, rows - 1);
+  const float* wr = rc < experts ? w + (size_t)rc * cols : shared_w;
+  constexpr int MAXJ = 32;  // cols <= 2048
+  float wv[MAXJ];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) wv[j] = wr[min(lane + 64 * j, cols - 1)];
+  const int quads = cols >> 3;
+  for (int t0 = 0; t0 < tokens; t0 += kRouterStage) {
+    const int m = min(kRouterStage, tokens - t0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < m * quads; i += blockDim.x) {
+      const int t = i / quads, o = i - t * quads;
+      reinterpret_cast<u32x4*>(xr_s + (size_t)t * cols)[o] = ldq(x + (size_t)(t0 + t) * cols, o);
+    }
+    __syncthreads();
+    for (int t = 0; t < m; ++t) {
+      const uint16_t* xt = xr_s + (size_t)t * cols;
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < MAXJ; ++j)
+        if (lane + 64 * j < cols) acc += bf2f(xt[lane + 64 * j]) * wv[j];
+      float v = acc + lane_down<1>(acc);
+      v += lane_down<32>(v);
+      v += lane_down<16>(v);
+      v += lane_down<8>(v);
+      v += lane_down<4>(v);
+      v += lane_down<2>(v);
+      if (lane == 0 && row < rows) logits[(size_t)(t0 + t) * rows + row] = v;
+    }
+  }
+}
+
+// Top-k of one token per block (moe.hex:86-252): without NaN logits, k
+// rounds of a wave-wide maximum of (value, lowest index) keys, which is the
+// stable descending rank; with NaNs the rank formula rank(e) =
+// #{i : l_i > l_e} + #{i < e : !(l_e > l_i)} (an unassigned rank k keeps
+// expert k), as k_router_select does. Then p_j = exp(l_j - l_0) / den with
+// den summed left to right from 0. The ids also go to row `layer` of the
+// session's export buffer.
 __global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ logits, int experts, int top_k,
                                                     int* __restrict__ ids, float* __restrict__ probs,
                                                     const SessionRows* __restrict__ rows, int layer) {
   extern __shared__ float lg[];  // experts
   __shared__ float chosen[64];
   __shared__ int sid[64];
-  const int b = blockIdx.x, tid = threadIdx.x;
+  __shared__ int any_nan;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float* src = logits + (size_t)b * (experts + 1);
-  for (int e = tid; e < experts; e += blockDim.x) lg[e] = src[e];
-  if (tid < top_k) {
-    sid[tid] = tid;
-    chosen[tid] = src[tid];
-  }
+  if (tid == 0) any_nan = 0;
   __syncthreads();
   for (int e = tid; e < experts; e += blockDim.x) {
-    const float le = lg[e];
-    int rank = 0;
-    for (int i = 0; i < experts; ++i) {
-      const float o = lg[i];
-      rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+    const float le = src[e];
+    lg[e] = le;
+    if (le != le) any_nan = 1;
+  }
+  __syncthreads();
+  if (!any_nan) {
+    if (wave == 0) {
+      unsigned long long taken = 0;  // bit j: lane's j-th candidate chosen (experts <= 4096)
+      for (int k = 0; k < top_k; ++k) {
+        unsigned long long mine = 0ull;
+        for (int j = 0, e = lane; e < experts; ++j, e += 64) {
+          if ((taken >> j) & 1ull) continue;
+          const float le = lg[e];
+          const uint32_t u = le == 0.0f ? 0u : fbits(le);
+          const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+          const unsigned long long key = ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
+          mine = key > mine ? key : mine;
+        }
+        unsigned long long best = mine;
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+          const unsigned long long o = __shfl_xor(best, sh, 64);
+          best = o > best ? o : best;
+        }
+        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+        if ((e & 63) == lane) taken |= 1ull << (e >> 6);
+        if (lane == 0) {
+          sid[k] = e;
+          chosen[k] = lg[e];
+        }
+      }
     }
-    if (rank < top_k) {
-      sid[rank] = e;
-      chosen[rank] = le;
+  } else {
+    if (tid < top_k) {
+      sid[tid] = tid;
+      chosen[tid] = lg[tid];
+    }
+    __syncthreads();
+    for (int e = tid; e < experts; e += blockDim.x) {
+      const float le = lg[e];
+      int rank = 0;
+      for (int i = 0; i < experts; ++i) {
+        const float o = lg[i];
+        rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
+      }
+      if (rank < top_k) {
+        sid[rank] = e;
+        chosen[rank] = le;
+      }
     }
   }
   __syncthreads();
-  if (tid < 64) {
-    const int lane = tid;
+  if (wave == 0) {
     const float ex = lane < top_k ? hexp(chosen[lane] - chosen[0]) : 0.0f;
     float den = 0.0f;
     for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
@@ -200,22 +288,22 @@ __global__ __launch_bounds__(kBlock) void k_bgate(
     if (tid == 0) nlist = tokens;
   } else {
     const int t = item / top_k;
-    // an earlier token that chose the same expert owns it
-    for (int i = tid; i < t * top_k; i += blockDim.x)
-      if (ids[i] == e) owner = 0;
+    // an earlier token that chose the same expert owns it; the owner lists
+    // every (token, slot) from its own on that chose it (in any order: each
+    // token's rows are computed on their own)
+    for (int i = tid; i < tokens * top_k; i += blockDim.x) {
+      const int u = i / top_k;
+      if (ids[i] == e) {
+        if (u < t) owner = 0;
+        else {
+          const int at = atomicAdd(&nlist, 1);
+          list_t[at] = u;
+          list_k[at] = i - u * top_k;
+        }
+      }
+    }
     __syncthreads();
     if (!owner) return;  // block-uniform
-    if (tid == 0) {
-      int n = 0;
-      for (int u = t; u < tokens; ++u)
-        for (int k = 0; k < top_k; ++k)
-          if (ids[u * top_k + k] == e) {
-            list_t[n] = u;
-            list_k[n] = k;
-            ++n;
-          }
-      nlist = n;
-    }
   }
   __syncthreads();
   const int n = nlist;
@@ -274,13 +362,14 @@ constexpr int kBDownTokens = 4;  // tokens per block
 // routed row (slot order; expert ids[slot]'s row) and of the shared row,
 // then out = bf16(bf16(routed + residual) (+) bf16(shared)) (k_moe_down's
 // order). The group's tokens' activations are staged in LDS. Requires
-// inter % 64 == 0 and shared_inter % 64 == 0.
+// inter % 64 == 0, inter <= 512 and shared_inter % 64 == 0.
 __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ act, int tokens,
                                                   const uint16_t* __restrict__ down,
                                                   const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
                                                   const uint16_t* __restrict__ residual, int hidden, int top_k,
                                                   int inter, int shared_inter, uint16_t* __restrict__ out) {
   extern __shared__ __align__(16) u32x4 as[];  // [kBDownTokens][per_row quads]
+  __shared__ int sids[kBDownTokens * 16];
   const int iq = inter >> 3, sq = shared_inter >> 3, rq = top_k * iq, per_row = rq + sq;
   const int lane = threadIdx.x & 63, tid = threadIdx.x;
   const int g = tid >> 3, q = lane & 7;
@@ -295,6 +384,9 @@ __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ a
     const int s = i / per_row, o = i - s * per_row;
     as[i] = ldq(act + (size_t)(t0 + s) * per_row * 8, o);
   }
+  // the tokens' expert ids before any weight load: a weight address that
+  // waited on an id load would wait for every load in flight
+  if (tid < ntok * top_k) sids[tid] = ids[(size_t)t0 * top_k + tid];
   Quad r, sh;
   quad_zero(r);
   quad_zero(sh);
@@ -306,17 +398,38 @@ __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ a
   for (int j = 0; j < NS; ++j) swv[j] = ldq(sw, min(q + 8 * j, sq - 1));
   __syncthreads();
   const u32x4* xr = as + (size_t)ti * per_row;
-  const int* tid_ids = ids + (size_t)tc * top_k;
-  constexpr int NW = 8;  // quads per lane per slot at inter 512
-  for (int k = 0; k < top_k; ++k) {
-    const uint16_t* wr = down + ((size_t)tid_ids[k] * hidden + rowc) * inter;
-    for (int j0 = 0; j0 < iq / 8; j0 += NW) {
-      u32x4 wv[NW];
+  const int* tid_ids = sids + (tc - t0) * top_k;
+  // slot k + 1's rows are loaded while slot k's are summed (unconditional,
+  // clamped loads, so each wait drains only the slot it needs); a slot
+  // covers iq / 8 <= NW quads per lane
+  constexpr int NW = 8;
+  auto slot_row = [&](int k) {
+    return down + ((size_t)tid_ids[min(k, top_k - 1)] * hidden + rowc) * inter;
+  };
+  u32x4 wa[NW], wb[NW];
+  {
+    const uint16_t* wr = slot_row(0);
 #pragma unroll
-      for (int j = 0; j < NW; ++j) wv[j] = ldq(wr, min(q + 8 * (j0 + j), iq - 1));
+    for (int j = 0; j < NW; ++j) wa[j] = ldq(wr, min(q + 8 * j, iq - 1));
+  }
+  for (int k = 0; k < top_k; k += 2) {
+    {
+      const uint16_t* wr = slot_row(k + 1);
+#pragma unroll
+      for (int j = 0; j < NW; ++j) wb[j] = ldq(wr, min(q + 8 * j, iq - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < NW; ++j)
+      if (j < iq / 8) quad_acc(r, xr[k * iq + q + 8 * j], wa[j]);
+    {
+      const uint16_t* wr = slot_row(k + 2);
+#pragma unroll
+      for (int j = 0; j < NW; ++j) wa[j] = ldq(wr, min(q + 8 * j, iq - 1));
+    }
+    if (k + 1 < top_k) {
 #pragma unroll
       for (int j = 0; j < NW; ++j)
-        if (j0 + j < iq / 8) quad_acc(r, xr[k * iq + q + 8 * (j0 + j)], wv[j]);
+        if (j < iq / 8) quad_acc(r, xr[(k + 1) * iq + q + 8 * j], wb[j]);
     }
   }
   for (int j0 = 0; j0 < sq / 8; j0 += NS) {
@@ -340,33 +453,93 @@ inline size_t bdown_lds_bytes(int per_row_quads) { return (size_t)kBDownTokens *
 
 // -------------------------------------------------------------- attention
 
-// Scores come from k_attn_scores with the session table (grid z = session).
-//
-// k_bflash: block (range, head group, session) with one thread per channel
-// and one wave for the denominators. kHPB > 1: split sessions only, the
-// group is a KV head's query heads and the tiles are range r's; kHPB == 1:
-// sessions at or below their split threshold, the group one query head and
-// the tiles all of them (range 0). Tiles run in sub-chunks of up to 64: the
-// scores of the sub-chunk staged, each head's running maximum per tile
-// (reset at the range start), alpha_t = exp(m_{t-1} - m_t), p = exp(s - m_t)
-// (invalid keys p = 0 against key 0's value), then per channel and head the
-// chain acc = acc * alpha_t + p_0 v_0 + ... + p_7 v_7 and per head
-// den = den * alpha_t + p_0 + ... + p_7 (k_attn_values' arithmetic). Split:
-// the range's (m_r, den_r, acc_r[HD]) go to part; single chain: the output
-// bf16(bf16(acc / den) * sigmoid(gate)).
+// Scores of every session's keys (k_attn_scores' arithmetic: lane l of a
+// 32-lane unit owns channels l, l + 32, ..., summed serially from 0.0, then
+// the 32-wide halving tree, times 1/sqrt(HD)), with the group's HPK query
+// heads in registers, two keys per unit at a time reduced by one paired tree
+// (each total has its operands of the single tree), and the next pair's key
+// rows loaded before the current pair's products. Block (key blocks, KV head,
+// session): scores [session][q_heads][stride].
+template <int HPK, int KJ>
+__global__ __launch_bounds__(kBlock) void k_bscores(const uint16_t* __restrict__ q,
+                                                    const SessionRows* __restrict__ rows, int64_t key_base, int kvs,
+                                                    float scale, float* __restrict__ scores, int stride) {
+  constexpr int HD = 32 * KJ;
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int q_heads = gridDim.y * HPK;
+  const int l32 = threadIdx.x & 31;
+  const int unit = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
+  const int units = (gridDim.x * blockDim.x) >> 5;
+  const int64_t keys = (int64_t)rows->position[b] + 1;
+  const auto kbase = gmem(rows->cache[b] + key_base + (int64_t)kvh * HD + l32);
+  float* sb = scores + (size_t)b * q_heads * stride + (size_t)kvh * HPK * stride;
+  float qv[HPK][KJ];
+#pragma unroll
+  for (int h = 0; h < HPK; ++h)
+#pragma unroll
+    for (int j = 0; j < KJ; ++j)
+      qv[h][j] = bf2f(q[((size_t)b * q_heads + kvh * HPK + h) * HD + l32 + 32 * j]);
+  int64_t kk = 2 * (int64_t)unit;
+  uint16_t ka[KJ], kb[KJ];
+  auto load = [&](int64_t k0) {
+    const int64_t a = min<int64_t>(k0, keys - 1), c = min<int64_t>(k0 + 1, keys - 1);
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      ka[j] = kbase[a * kvs + 32 * j];
+      kb[j] = kbase[c * kvs + 32 * j];
+    }
+  };
+  if (kk < keys) load(kk);
+  for (; kk < keys; kk += 2 * (int64_t)units) {
+    float fa[KJ], fb[KJ];
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) {
+      fa[j] = bf2f(ka[j]);
+      fb[j] = bf2f(kb[j]);
+    }
+    load(kk + 2 * (int64_t)units);  // unconditional (clamped): a conditional load would drain the queue
+#pragma unroll
+    for (int h = 0; h < HPK; ++h) {
+      float a = 0.0f, c = 0.0f;
+#pragma unroll
+      for (int j = 0; j < KJ; ++j) {
+        a += qv[h][j] * fa[j];
+        c += qv[h][j] * fb[j];
+      }
+      const float v = tree32_pair(a, c);
+      if (l32 == 0) sb[(size_t)h * stride + kk] = v * scale;
+      if (l32 == 16 && kk + 1 < keys) sb[(size_t)h * stride + kk + 1] = v * scale;
+    }
+  }
+}
+
+// k_bflash: block (range, head group, session) with one thread per pair of
+// channels (c, c + 1: one 4-byte V read per key) and one wave for the
+// denominators. kSplit: split sessions only, the group is a KV head's kHPB
+// query heads (kHPB = heads per KV head) and the tiles are range r's;
+// otherwise sessions at or below their split threshold, the group one query
+// head (kHPB = 1) and the tiles all of them (range 0). Tiles run in
+// sub-chunks of up to 64: the scores of the sub-chunk staged, each head's
+// running maximum per tile (reset at the range start), alpha_t =
+// exp(m_{t-1} - m_t), p = exp(s - m_t) (invalid keys p = 0 against key 0's
+// value), then per channel and head the chain acc = acc * alpha_t +
+// p_0 v_0 + ... + p_7 v_7 and per head den = den * alpha_t + p_0 + ... + p_7
+// (k_attn_values' arithmetic), the V values kFlashRing tiles ahead of the
+// chains. Split: the range's (m_r, den_r, acc_r[HD]) go to part; single
+// chain: the output bf16(bf16(acc / den) * sigmoid(gate)).
 constexpr int kFlashSub = 64;  // tiles per sub-chunk
-constexpr int kFlashMaxHeads = 8;
+constexpr int kFlashRing = 4;  // tiles of V values in flight per thread
 
-inline int flash_threads(int head_dim) { return (head_dim + 63) / 64 * 64 + 64; }
+inline int flash_threads(int head_dim) { return (head_dim / 2 + 63) / 64 * 64 + 64; }
 
-template <int kHPB>
-__global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores, int stride,
+template <bool kSplit, int kHPB>
+__global__ __launch_bounds__(192) void k_bflash(const float* __restrict__ scores, int stride,
                                                 const SessionRows* __restrict__ rows, int64_t value_base, int kvs,
                                                 int head_dim, int q_heads, int heads_per_kv,
                                                 const uint16_t* __restrict__ qg, float* __restrict__ part,
                                                 uint16_t* __restrict__ out) {
-  constexpr int HPB = kHPB;
-  __shared__ float p[HPB][kFlashSub * 8];
+  constexpr int HPB = kHPB, D = kFlashRing;
+  __shared__ __align__(16) float p[HPB][kFlashSub * 8];
   __shared__ float alpha[HPB][kFlashSub];
   __shared__ float mtile[HPB][kFlashSub];
   __shared__ float mrun[HPB], dfinal[HPB];
@@ -375,29 +548,41 @@ __global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores
   const int tiles = (int)((keys + 7) >> 3);
   const int64_t sk = rows->split[b];
   const bool split = sk > 0 && keys > sk;
-  if ((HPB > 1) != split) return;
+  if (kSplit != split) return;
   const int range_tiles = split ? (tiles + kSplitRanges - 1) / kSplitRanges : tiles;
   const int r = blockIdx.x;
   if (r * range_tiles >= tiles) return;
   const int t_begin = r * range_tiles, t_end = min(tiles, t_begin + range_tiles);
-  const int nh = HPB > 1 ? heads_per_kv : 1;
-  const int h0 = HPB > 1 ? blockIdx.y * heads_per_kv : blockIdx.y;
+  constexpr int nh = HPB;
+  const int h0 = kSplit ? blockIdx.y * heads_per_kv : blockIdx.y;
   const int kvh = h0 / heads_per_kv;
-  const int hd_pad = (head_dim + 63) / 64 * 64;
-  const bool chan = tid < head_dim;
-  const bool den_lane = tid >= hd_pad && tid - hd_pad < nh;
-  const int dh = tid - hd_pad;
+  const int half_pad = (head_dim / 2 + 63) / 64 * 64;
+  const bool chan = tid < head_dim / 2;
+  const int c = 2 * tid;
+  const bool den_lane = tid >= half_pad && tid - half_pad < nh;
+  const int dh = tid - half_pad;
   const float ninf = bitsf(0xff800000u);
   const float* sb = scores + (size_t)b * q_heads * stride;
-  const uint16_t* vb = rows->cache[b] + value_base + (int64_t)kvh * head_dim + (chan ? tid : 0);
-  float acc[HPB];
+  const auto vb = gmem(reinterpret_cast<const uint32_t*>(rows->cache[b] + value_base + (int64_t)kvh * head_dim +
+                                                         (chan ? c : 0)));
+  const int kvw = kvs / 2;  // key stride in 4-byte words
+  auto vload = [&](int64_t k) { return vb[(k < keys ? k : 0) * kvw]; };
+  float acc[HPB][2];
 #pragma unroll
-  for (int h = 0; h < HPB; ++h) acc[h] = 0.0f;
+  for (int h = 0; h < HPB; ++h) acc[h][0] = acc[h][1] = 0.0f;
   float den = 0.0f;
   if (tid < nh) mrun[tid] = ninf;
   for (int c0 = t_begin; c0 < t_end; c0 += kFlashSub) {
     const int nt = min(kFlashSub, t_end - c0), nk = nt * 8;
     const int64_t k0 = (int64_t)c0 * 8;
+    // the first tiles' V values, in flight while the weights are computed
+    uint32_t vr[D][8];
+    if (chan) {
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) vr[d][j] = vload(k0 + 8 * d + j);
+    }
     __syncthreads();  // the previous sub-chunk's readers are done
     for (int i = tid; i < nh * nk; i += blockDim.x) {
       const int h = i / nk, kk = i - h * nk;
@@ -405,52 +590,77 @@ __global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores
       p[h][kk] = k < keys ? sb[(size_t)(h0 + h) * stride + k] : ninf;
     }
     __syncthreads();
+    // tile maxima in parallel, then each head's running maximum
+    for (int i = tid; i < nh * nt; i += blockDim.x) {
+      const int h = i / nt, ti = i - h * nt;
+      float tm = ninf;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tm = fmaxf(tm, p[h][ti * 8 + j]);
+      mtile[h][ti] = tm;
+    }
+    __syncthreads();
     if (tid < nh) {
       const int h = tid;
       float m = mrun[h];
       for (int i = 0; i < nt; ++i) {
-        float tm = ninf;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tm = fmaxf(tm, p[h][i * 8 + j]);
         const float prev = (c0 + i == t_begin) ? ninf : m;
-        m = fmaxf(m, tm);
+        m = fmaxf(m, mtile[h][i]);
         mtile[h][i] = m;
-        alpha[h][i] = hexp(prev - m);
+        alpha[h][i] = prev;  // exponentiated below
       }
       mrun[h] = m;
     }
     __syncthreads();
+    for (int i = tid; i < nh * nt; i += blockDim.x) {
+      const int h = i / nt, ti = i - h * nt;
+      alpha[h][ti] = hexp(alpha[h][ti] - mtile[h][ti]);
+    }
     for (int i = tid; i < nh * nk; i += blockDim.x) {
       const int h = i / nk, kk = i - h * nk;
       const int64_t k = k0 + kk;
       p[h][kk] = k < keys ? hexp(p[h][kk] - mtile[h][kk >> 3]) : 0.0f;
     }
+    // tiles past nt up to a whole ring group are no-ops: alpha 1 and p 0
+    // leave every chain's bits unchanged (x * 1 = x, x + (+-0) = x), so the
+    // chain loop below runs whole groups with no runtime guard
+    const int ntp = (nt + D - 1) / D * D;
+    for (int i = tid; i < nh * (ntp - nt); i += blockDim.x) {
+      const int h = i / (ntp - nt), ti = nt + i - h * (ntp - nt);
+      alpha[h][ti] = 1.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[h][ti * 8 + j] = 0.0f;
+    }
     __syncthreads();
     if (chan) {
-      float vn[8];
+      // loads are issued unconditionally (keys past the range are valid
+      // rows, keys past the end read key 0): a conditional load would make
+      // the next use wait for every load in flight
+      for (int i0 = 0; i0 < ntp; i0 += D) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t k = k0 + j;
-        vn[j] = bf2f(vb[(k < keys ? k : 0) * kvs]);
-      }
-      for (int i = 0; i < nt; ++i) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = vn[j];
-        if (i + 1 < nt) {
+        for (int d = 0; d < D; ++d) {
+          const int i = i0 + d;
+          float v0[8], v1[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const int64_t k = k0 + (i + 1) * 8 + j;
-            vn[j] = bf2f(vb[(k < keys ? k : 0) * kvs]);
+            v0[j] = lo2f(vr[d][j]);
+            v1[j] = hi2f(vr[d][j]);
           }
-        }
 #pragma unroll
-        for (int h = 0; h < HPB; ++h) {
-          if (h < nh) {
-            float a = acc[h] * alpha[h][i];
+          for (int j = 0; j < 8; ++j) vr[d][j] = vload(k0 + 8 * (i + D) + j);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a = a + p[h][i * 8 + j] * v[j];
-            acc[h] = a;
+          for (int h = 0; h < HPB; ++h) {
+            const f32x4 pa = reinterpret_cast<const f32x4*>(&p[h][i * 8])[0];
+            const f32x4 pb = reinterpret_cast<const f32x4*>(&p[h][i * 8])[1];
+            const float al = alpha[h][i];
+            const float pw[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+            float a0 = acc[h][0] * al, a1 = acc[h][1] * al;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              a0 = a0 + pw[j] * v0[j];
+              a1 = a1 + pw[j] * v1[j];
+            }
+            acc[h][0] = a0;
+            acc[h][1] = a1;
           }
         }
       }
@@ -463,9 +673,13 @@ __global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores
     }
   }
   if (split) {
+#pragma unroll
     for (int h = 0; h < nh; ++h) {
       float* pr = part + (((size_t)b * q_heads + h0 + h) * kSplitRanges + r) * (2 + head_dim);
-      if (chan) pr[2 + tid] = acc[h];
+      if (chan) {
+        pr[2 + c] = acc[h][0];
+        pr[3 + c] = acc[h][1];
+      }
       if (den_lane && dh == h) {
         pr[0] = mrun[h];
         pr[1] = den;
@@ -475,42 +689,70 @@ __global__ __launch_bounds__(320) void k_bflash(const float* __restrict__ scores
     if (den_lane) dfinal[dh] = den;
     __syncthreads();
     if (chan) {
+#pragma unroll
       for (int h = 0; h < nh; ++h) {
         const int head = h0 + h;
-        const float gate = sigmoid(bf2f(qg[(size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim +
-                                           head_dim + tid]));
-        out[(size_t)b * q_heads * head_dim + head * head_dim + tid] = f2bf(rbf(acc[h] / dfinal[h]) * gate);
+        const uint16_t* gr = qg + (size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim + head_dim + c;
+        uint16_t* o = out + (size_t)b * q_heads * head_dim + head * head_dim + c;
+        o[0] = f2bf(rbf(acc[h][0] / dfinal[h]) * sigmoid(bf2f(gr[0])));
+        o[1] = f2bf(rbf(acc[h][1] / dfinal[h]) * sigmoid(bf2f(gr[1])));
       }
     }
   }
 }
 
 // Merge of a split session's ranges per (query head, session), one thread
-// per channel: M = max_r m_r, then in ascending range order
-// den = 0 + den_r w_r, acc = 0 + acc_r w_r with w_r = exp(m_r - M);
+// per channel: M = max_r m_r, w_r = exp(m_r - M) (computed once per range),
+// then in ascending range order den = 0 + den_r w_r, acc = 0 + acc_r w_r;
 // out = bf16(bf16(acc / den) * sigmoid(gate)).
 __global__ __launch_bounds__(256) void k_bmerge(const float* __restrict__ part, const SessionRows* __restrict__ rows,
                                                 int head_dim, int q_heads, const uint16_t* __restrict__ qg,
                                                 uint16_t* __restrict__ out) {
+  __shared__ float wr[kSplitRanges], mr[kSplitRanges], dr[kSplitRanges];
+  __shared__ float top_s, den_s;
   const int head = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
   const int64_t keys = (int64_t)rows->position[b] + 1;
   const int64_t sk = rows->split[b];
-  if (!(sk > 0 && keys > sk) || c >= head_dim) return;
+  if (!(sk > 0 && keys > sk)) return;  // block-uniform
   const int tiles = (int)((keys + 7) >> 3);
   const int range_tiles = (tiles + kSplitRanges - 1) / kSplitRanges;
   const int nranges = (tiles + range_tiles - 1) / range_tiles;
   const float* pr = part + ((size_t)b * q_heads + head) * kSplitRanges * (2 + head_dim);
-  float top = bitsf(0xff800000u);
-  for (int r = 0; r < nranges; ++r) top = fmaxf(top, pr[(size_t)r * (2 + head_dim)]);
-  float acc = 0.0f, den = 0.0f;
-  for (int r = 0; r < nranges; ++r) {
-    const float* e = pr + (size_t)r * (2 + head_dim);
-    const float w = hexp(e[0] - top);
-    acc = acc + e[2 + c] * w;
-    den = den + e[1] * w;
+  if (c < nranges) {
+    mr[c] = pr[(size_t)c * (2 + head_dim)];
+    dr[c] = pr[(size_t)c * (2 + head_dim) + 1];
   }
-  const float gate = sigmoid(bf2f(qg[(size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim + head_dim + c]));
-  out[(size_t)b * q_heads * head_dim + head * head_dim + c] = f2bf(rbf(acc / den) * gate);
+  __syncthreads();
+  if (c == 0) {
+    float top = bitsf(0xff800000u);
+    for (int r = 0; r < nranges; ++r) top = fmaxf(top, mr[r]);
+    top_s = top;
+  }
+  __syncthreads();
+  if (c < nranges) wr[c] = hexp(mr[c] - top_s);
+  __syncthreads();
+  if (c == 0) {
+    float den = 0.0f;
+    for (int r = 0; r < nranges; ++r) den = den + dr[r] * wr[r];
+    den_s = den;
+  }
+  float acc = 0.0f;
+  if (c < head_dim) {
+    constexpr int G = 16;
+    for (int r0 = 0; r0 < nranges; r0 += G) {
+      float a[G];
+#pragma unroll
+      for (int g = 0; g < G; ++g) a[g] = pr[(size_t)min(r0 + g, nranges - 1) * (2 + head_dim) + 2 + c];
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (r0 + g < nranges) acc = acc + a[g] * wr[r0 + g];
+    }
+  }
+  __syncthreads();
+  if (c < head_dim) {
+    const float gate = sigmoid(bf2f(qg[(size_t)b * 2 * q_heads * head_dim + (size_t)head * 2 * head_dim + head_dim + c]));
+    out[(size_t)b * q_heads * head_dim + head * head_dim + c] = f2bf(rbf(acc / den_s) * gate);
+  }
 }
 
 }  // namespace cq35

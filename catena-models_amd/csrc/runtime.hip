@@ -2330,17 +2330,38 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
           (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
           (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, b->qr, rows);
       const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
-      k_attn_scores<<<dim3((unsigned)std::min<int64_t>((cap + 7) / 8, 512), (unsigned)d.KVH, (unsigned)B),
-                      dim3(kScoreBlock), (size_t)hpk * d.HD * 4, st>>>(
-          (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
-          (int)d.HD, hpk, scale, b->scratch, b->stride, rows);
+      {
+        // 16 keys per block per pass; about 2048 blocks over the batch
+        const int per = (int)std::max<int64_t>(1, std::min<int64_t>((cap + 15) / 16, 2048 / (d.KVH * B)));
+        const dim3 sg((unsigned)per, (unsigned)d.KVH, (unsigned)B);
+        const uint16_t* qr = b->qr;
+        if (hpk == 8 && d.HD == 256)
+          k_bscores<8, 8><<<sg, dim3(kBlock), 0, st>>>(qr, rows, key_base, (int)d.KVS, scale, b->scratch, b->stride);
+        else if (hpk == 2 && d.HD == 256)
+          k_bscores<2, 8><<<sg, dim3(kBlock), 0, st>>>(qr, rows, key_base, (int)d.KVS, scale, b->scratch, b->stride);
+        else if (hpk == 4 && d.HD == 64)
+          k_bscores<4, 2><<<sg, dim3(kBlock), 0, st>>>(qr, rows, key_base, (int)d.KVS, scale, b->scratch, b->stride);
+        else
+          k_attn_scores<<<dim3((unsigned)std::min<int64_t>((cap + 7) / 8, 512), (unsigned)d.KVH, (unsigned)B),
+                          dim3(kScoreBlock), (size_t)hpk * d.HD * 4, st>>>(
+              qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, hpk, scale,
+              b->scratch, b->stride, rows);
+      }
       const dim3 fb((unsigned)flash_threads((int)d.HD));
-      k_bflash<kFlashMaxHeads><<<dim3((unsigned)kSplitRanges, (unsigned)d.KVH, (unsigned)B), fb, 0, st>>>(
-          (const float*)b->scratch, b->stride, rows, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk,
-          (const uint16_t*)b->qg, b->part, b->ctx);
-      k_bflash<1><<<dim3(1u, (unsigned)d.Q, (unsigned)B), fb, 0, st>>>(
-          (const float*)b->scratch, b->stride, rows, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk,
-          (const uint16_t*)b->qg, b->part, b->ctx);
+      {
+        const dim3 sgrid((unsigned)kSplitRanges, (unsigned)d.KVH, (unsigned)B);
+        const float* sc = b->scratch;
+        const uint16_t* qg = b->qg;
+        const int KVS = (int)d.KVS, HD = (int)d.HD, Q = (int)d.Q;
+        switch (hpk) {
+          case 1: k_bflash<true, 1><<<sgrid, fb, 0, st>>>(sc, b->stride, rows, value_base, KVS, HD, Q, hpk, qg, b->part, b->ctx); break;
+          case 2: k_bflash<true, 2><<<sgrid, fb, 0, st>>>(sc, b->stride, rows, value_base, KVS, HD, Q, hpk, qg, b->part, b->ctx); break;
+          case 4: k_bflash<true, 4><<<sgrid, fb, 0, st>>>(sc, b->stride, rows, value_base, KVS, HD, Q, hpk, qg, b->part, b->ctx); break;
+          default: k_bflash<true, 8><<<sgrid, fb, 0, st>>>(sc, b->stride, rows, value_base, KVS, HD, Q, hpk, qg, b->part, b->ctx); break;
+        }
+        k_bflash<false, 1><<<dim3(1u, (unsigned)d.Q, (unsigned)B), fb, 0, st>>>(sc, b->stride, rows, value_base, KVS,
+                                                                                 HD, Q, hpk, qg, b->part, b->ctx);
+      }
       k_bmerge<<<dim3((unsigned)d.Q, (unsigned)B), dim3(256), 0, st>>>((const float*)b->part, rows, (int)d.HD,
                                                                       (int)d.Q, (const uint16_t*)b->qg, b->ctx);
       ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, nullptr);
@@ -2368,18 +2389,8 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
       ffn = 11;
     }
     norm(b->attn, post_norm, b->x);
-    {
-      const dim3 rg((unsigned)((E + 1 + kRouterRows - 1) / kRouterRows),
-                    (unsigned)((B + kRouterTokens - 1) / kRouterTokens));
-      const float* rw = (const float*)W(ffn);
-      const float* srw = (const float*)W(ffn + 4);
-      switch (H) {
-        case 2048: k_brouter_shared<32><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
-        case 1024: k_brouter_shared<16><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
-        case 512: k_brouter_shared<8><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
-        default: k_brouter_shared<4><<<rg, dim3(512), 0, st>>>(b->x, B, rw, srw, E, b->rlogits); break;
-      }
-    }
+    k_wsrouter<<<dim3((unsigned)((E + 1 + 3) / 4)), dim3(kBlock), (size_t)kRouterStage * d.H * 2, st>>>(
+        b->x, B, H, (const float*)W(ffn), (const float*)W(ffn + 4), E, b->rlogits);
     k_sselect<<<dim3((unsigned)B), dim3(kBlock), (size_t)E * 4, st>>>(b->rlogits, E, K, b->bids, b->bprobs, rows,
                                                                       (int)l);
     k_bgate<<<dim3((unsigned)((B * K + 1) * gate_blocks)), dim3(kBlock), (size_t)kBGateStage * d.H * 2, st>>>(
@@ -2460,14 +2471,14 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   return CQ35_OK;
 }
 
-// Whether the MoE shape fits the batched MoE kernels: a hidden width the
-// shared router is instantiated for (staged once by k_ws256 and k_bgate), expert widths in whole 64-element
-// lane rounds (k_bdown), the head dim within one flash block, at most 8 query
-// heads per KV head and 16 experts selected per token.
+// Whether the MoE shape fits the batched MoE kernels: the hidden row staged
+// once (k_ws256, k_wsrouter, k_bgate), expert widths in whole 64-element
+// lane rounds (k_bdown), the head dim within one flash block, 1, 2, 4 or 8
+// query heads per KV head and at most 16 experts selected per token.
 bool moe_batch_shape_ok(const cq35_model* m) {
   const Dims& d = m->d;
-  return (d.H == 2048 || d.H == 1024 || d.H == 512 || d.H == 256) && d.I % 64 == 0 && d.SI % 64 == 0 && d.HD <= 256 &&
-         d.Q / d.KVH <= kFlashMaxHeads && d.K <= 16 && d.E <= 4096;
+  return d.H <= kBatchChunk && d.H % 64 == 0 && d.I % 64 == 0 && d.I <= 512 && d.SI % 64 == 0 && d.HD <= 256 &&
+         (d.Q / d.KVH == 1 || d.Q / d.KVH == 2 || d.Q / d.KVH == 4 || d.Q / d.KVH == 8) && d.K <= 16 && d.E <= 4096;
 }
 
 // Whether a batch can take the weight-shared step: sessions of one model and
