@@ -14,11 +14,10 @@
 //              k_router_select's lane order and tree;
 //  k_sselect   per token: stable rank top-k and the softmax weights
 //              (moe.hex:86-252), the ids also copied to the session's export
-//              row;
-//  k_bgate     per distinct routed expert (the first (token, slot) that
-//              selects it owns it) its gate/up rows applied to every token
-//              that selected it, with that token's weight; the shared expert's
-//              rows applied to every token (moe.hex:254-333);
+//              row, each (token, slot) appended to its expert's list;
+//  k_bgate     per distinct selected expert its gate/up rows applied to every
+//              token that selected it, with that token's weight; the shared
+//              expert's rows applied to every token (moe.hex:254-333);
 //  k_bdown     per (output row, token): the S32 over the token's concatenated
 //              expert rows in slot order, the shared S32 and the residual
 //              (moe.hex:371-434); the rows of experts that several tokens
@@ -151,7 +150,9 @@ __global__ __launch_bounds__(kBlock) void k_wsrouter(const uint16_t* __restrict_
 // session's export buffer.
 __global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ logits, int experts, int top_k,
                                                     int* __restrict__ ids, float* __restrict__ probs,
-                                                    const SessionRows* __restrict__ rows, int layer) {
+                                                    const SessionRows* __restrict__ rows, int layer,
+                                                    int* __restrict__ ecount, int* __restrict__ elist, int max_tokens,
+                                                    int* __restrict__ uexp) {
   extern __shared__ float lg[];  // experts
   __shared__ float chosen[64];
   __shared__ int sid[64];
@@ -218,135 +219,99 @@ __global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ lo
     float den = 0.0f;
     for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
     if (lane < top_k) {
+      const int e = sid[lane];
       probs[b * top_k + lane] = ex / den;
-      ids[b * top_k + lane] = sid[lane];
-      if (rows->ids[b]) rows->ids[b][layer * top_k + lane] = sid[lane];
+      ids[b * top_k + lane] = e;
+      if (rows->ids[b]) rows->ids[b][layer * top_k + lane] = e;
+      // the expert's (token, slot) list for the gate/up kernel (in any
+      // order: each token's rows are computed on their own; a token's slots
+      // repeat an expert only when NaN logits made ranks collide, so a list
+      // holds at most max_tokens * top_k entries), and on its first
+      // selection a slot in the round's list of distinct experts (count at
+      // ecount[experts])
+      const int at = atomicAdd(&ecount[e], 1);
+      reinterpret_cast<int2*>(elist)[(size_t)e * max_tokens * top_k + at] =
+          int2{(b << 8) | lane, (int)fbits(ex / den)};
+      if (at == 0) uexp[atomicAdd(&ecount[experts], 1)] = e;
     }
   }
 }
 
+// Zero n ints (the experts' list counts before a round's selections).
+__global__ void k_zero_ints(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 // ----------------------------------------------------------- expert gate/up
 
-// Rows per wave and per block of k_bgate.
-constexpr int kBGateRW = 2;
-constexpr int kBGateRows = 4 * kBGateRW;
-constexpr int kBGateStage = 8;  // token rows staged per pass
+constexpr int kGateRowsPerBlock = 4;  // one row pair (gate, up) per wave
 
-// Block (item, row block): items [0, tokens * top_k) are (token, slot)
-// pairs, item tokens * top_k the shared expert. A routed item runs only if
-// its (token, slot) is the first in token order to select the expert; it
-// then applies the expert's gate/up rows of its row block to every token
-// that selected the expert (dual S256, k_gate_up's order):
-// act[t][slot * I + row] = bf16(silu(bf16 g) * bf16 u * p_{t,slot}); the
-// shared item applies the shared rows to every token:
-// act[t][K * I + row] = bf16(bf16(bf16(silu(bf16 g)) * bf16 u) * sigmoid(l_E)).
+// Block (expert slot, 4 rows): slots [0, n) are the round's distinct
+// selected experts (in selection order), slot max_slots the shared expert.
+// Each wave is on its own (no LDS, no barrier): it reads its expert, issues
+// its row pair's loads (gate and up, 8 KB), then for each (token, slot) of
+// the expert's list loads the token's normalised row (L2) and runs the dual
+// S256 (k_gate_up's order): routed act[t][slot * I + row] =
+// bf16(silu(bf16 g) * bf16 u * p_{t,slot}); shared act[t][K * I + row] =
+// bf16(bf16(bf16(silu(bf16 g)) * bf16 u) * sigmoid(l_E)). Small waves keep
+// many of them resident per CU, which is what keeps HBM busy here.
 // x [tokens][cols] normalised rows, cols <= 2048.
 __global__ __launch_bounds__(kBlock) void k_bgate(
     const uint16_t* __restrict__ x, int tokens, int cols, const uint16_t* __restrict__ gate,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ sup,
-    const int* __restrict__ ids, const float* __restrict__ probs, const float* __restrict__ logits, int experts,
-    int top_k, int inter, int shared_inter, int row_blocks, uint16_t* __restrict__ act) {
-  constexpr int RW = kBGateRW, NQ = 4;
-  extern __shared__ __align__(16) u32x4 xs[];  // [kBGateStage][quads]
-  // (token, slot) pairs that chose the expert: at most one per token, more
-  // only if NaN router logits made a token's ranks collide (its slots can
-  // then repeat an expert); bounded by tokens * top_k <= kMaxSessions * 16
-  __shared__ int list_t[kMaxSessions * 16], list_k[kMaxSessions * 16];
-  __shared__ int nlist, owner;
-  const int item = blockIdx.x / row_blocks, rbk = blockIdx.x - item * row_blocks;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, tid = threadIdx.x;
+    const int* __restrict__ ecount, const int* __restrict__ elist, const int* __restrict__ uexp,
+    const float* __restrict__ probs, const float* __restrict__ logits, int experts, int top_k, int inter,
+    int shared_inter, int row_blocks, int max_slots, int max_tokens, uint16_t* __restrict__ act) {
+  constexpr int NQ = 4;
+  const int slot = blockIdx.x / row_blocks, rb = blockIdx.x - slot * row_blocks;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quads = cols >> 3;
-  const int routed_items = tokens * top_k;
-  const bool shared = item == routed_items;
+  const bool shared = slot == max_slots;
   const int nrows = shared ? shared_inter : inter;
-  const int row0 = rbk * kBGateRows + wave * RW;
-  if (rbk * kBGateRows >= nrows) return;  // block-uniform
-  const int e = shared ? 0 : ids[item];
-  // weights first: the expert's rows (or the shared rows) of this wave
-  u32x4 gv[RW][NQ], uv[RW][NQ];
+  const int row = rb * kGateRowsPerBlock + wave;
+  if (row >= nrows) return;  // wave-uniform
+  // the distinct-expert count and this slot's expert in one round trip
+  const int n_u = ecount[experts];
+  const int e = shared ? 0 : uexp[min(slot, max_slots - 1)];
+  if (!shared && slot >= n_u) return;  // fewer distinct experts this round
+  const uint16_t* g = shared ? sgate + (size_t)row * cols : gate + ((size_t)e * inter + row) * cols;
+  const uint16_t* u = shared ? sup + (size_t)row * cols : up + ((size_t)e * inter + row) * cols;
+  u32x4 gv[NQ], uv[NQ];
 #pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int row = min(row0 + r, nrows - 1);
-    const uint16_t* g = shared ? sgate + (size_t)row * cols : gate + ((size_t)e * inter + row) * cols;
-    const uint16_t* u = shared ? sup + (size_t)row * cols : up + ((size_t)e * inter + row) * cols;
-#pragma unroll
-    for (int j = 0; j < NQ; ++j) {
-      gv[r][j] = ldq(g, min(lane + 64 * j, quads - 1));
-      uv[r][j] = ldq(u, min(lane + 64 * j, quads - 1));
-    }
+  for (int j = 0; j < NQ; ++j) {
+    gv[j] = ldq(g, min(lane + 64 * j, quads - 1));
+    uv[j] = ldq(u, min(lane + 64 * j, quads - 1));
   }
-  if (tid == 0) {
-    owner = 1;
-    nlist = 0;
-  }
-  __syncthreads();
-  if (shared) {
-    if (tid < tokens) {
-      list_t[tid] = tid;
-      list_k[tid] = -1;
-    }
-    if (tid == 0) nlist = tokens;
-  } else {
-    const int t = item / top_k;
-    // an earlier token that chose the same expert owns it; the owner lists
-    // every (token, slot) from its own on that chose it (in any order: each
-    // token's rows are computed on their own)
-    for (int i = tid; i < tokens * top_k; i += blockDim.x) {
-      const int u = i / top_k;
-      if (ids[i] == e) {
-        if (u < t) owner = 0;
-        else {
-          const int at = atomicAdd(&nlist, 1);
-          list_t[at] = u;
-          list_k[at] = i - u * top_k;
-        }
-      }
-    }
-    __syncthreads();
-    if (!owner) return;  // block-uniform
-  }
-  __syncthreads();
-  const int n = nlist;
-  const int I = inter;
+  const int n = shared ? tokens : ecount[e];
+  const int2* list = reinterpret_cast<const int2*>(elist) + (size_t)e * max_tokens * top_k;
   const int act_row = top_k * inter + shared_inter;
-  for (int base = 0; base < n; base += kBGateStage) {
-    const int m = min(kBGateStage, n - base);
-    __syncthreads();  // the previous pass's readers are done
-    for (int i = tid; i < m * quads; i += blockDim.x) {
-      const int s = i / quads, o = i - s * quads;
-      xs[s * quads + o] = ldq(x + (size_t)list_t[base + s] * cols, o);
-    }
-    __syncthreads();
-    for (int s = 0; s < m; ++s) {
-      const int t = list_t[base + s], k = list_k[base + s];
-      const u32x4* xr = xs + s * quads;
+  for (int s = 0; s < n; ++s) {
+    const int2 entry = shared ? int2{s << 8, 0} : list[s];
+    const int t = entry.x >> 8, k = entry.x & 255;
+    const float w = shared ? sigmoid(logits[(size_t)t * (experts + 1) + experts]) : bitsf((uint32_t)entry.y);
+    const uint16_t* xr = x + (size_t)t * cols;
+    u32x4 xq[NQ];
 #pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        Quad ga, ua;
-        quad_zero(ga);
-        quad_zero(ua);
+    for (int j = 0; j < NQ; ++j) xq[j] = ldq(xr, min(lane + 64 * j, quads - 1));
+    Quad ga, ua;
+    quad_zero(ga);
+    quad_zero(ua);
 #pragma unroll
-        for (int j = 0; j < NQ; ++j)
-          if (lane + 64 * j < quads) {
-            const u32x4 xq = xr[lane + 64 * j];
-            quad_acc(ga, xq, gv[r][j]);
-            quad_acc(ua, xq, uv[r][j]);
-          }
-        const float gsum = quad_tree<64>(ga);
-        const float usum = quad_tree<64>(ua);
-        const int row = row0 + r;
-        if (lane == 0 && row < nrows) {
-          const float gb = rbf(gsum), ub = rbf(usum);
-          const float activated = silu(gb);
-          if (!shared) {
-            const float y = (activated * ub) * probs[t * top_k + k];
-            act[(size_t)t * act_row + (size_t)k * I + row] = f2bf(y);
-          } else {
-            const float y = rbf(rbf(activated) * ub) * sigmoid(logits[(size_t)t * (experts + 1) + experts]);
-            act[(size_t)t * act_row + (size_t)top_k * I + row] = f2bf(y);
-          }
-        }
+    for (int j = 0; j < NQ; ++j)
+      if (lane + 64 * j < quads) {
+        quad_acc(ga, xq[j], gv[j]);
+        quad_acc(ua, xq[j], uv[j]);
       }
+    const float gsum = quad_tree<64>(ga);
+    const float usum = quad_tree<64>(ua);
+    if (lane == 0) {
+      const float gb = rbf(gsum), ub = rbf(usum);
+      const float activated = silu(gb);
+      if (!shared)
+        act[(size_t)t * act_row + (size_t)k * inter + row] = f2bf((activated * ub) * w);
+      else
+        act[(size_t)t * act_row + (size_t)top_k * inter + row] = f2bf(rbf(rbf(activated) * ub) * w);
     }
   }
 }

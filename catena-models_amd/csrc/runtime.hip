@@ -2047,6 +2047,9 @@ struct BatchWorkspace {
   float* bprobs = nullptr;
   uint16_t* bact = nullptr;
   float* part = nullptr;
+  int* ecount = nullptr;  // per layer: (token, slot) entries per expert, then the distinct-expert count
+  int* elist = nullptr;   // per layer and expert: the entries (token << 8 | slot, routing weight bits)
+  int* uexp = nullptr;    // per layer: the round's distinct selected experts
   hipGraph_t graph[2][kMaxSessions + 1] = {};      // [matrix-core products][sessions]
   hipGraphExec_t exec[2][kMaxSessions + 1] = {};
   std::vector<void*> allocs;
@@ -2126,6 +2129,9 @@ int batch_workspace(cq35_model* m, int64_t capacity, int count, BatchWorkspace**
     alloc(&b->bprobs, B * d.K);
     alloc(&b->bact, B * (d.K * d.I + d.SI));
     alloc(&b->part, (int64_t)B * d.Q * kSplitRanges * (2 + d.HD));
+    alloc(&b->ecount, d.L * (d.E + 1));
+    alloc(&b->elist, 2 * d.L * d.E * B * d.K);  // (token << 8 | slot, weight) pairs
+    alloc(&b->uexp, d.L * std::min<int64_t>(d.E, B * d.K));
   }
   (void)wide;
   if (e == hipSuccess) e = hipHostMalloc((void**)&b->h_rows, sizeof(SessionRows), hipHostMallocDefault);
@@ -2304,6 +2310,10 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
   const int groups = (B + kBatchNB - 1) / kBatchNB;
   k_sembed<<<dim3((unsigned)grid_for((d.H + kBlock - 1) / kBlock, 64), (unsigned)B), dim3(kBlock), 0, st>>>(
       rows, (const uint16_t*)Wt(0), H, b->h, (const float*)m->freq, (int)(d.R / 2), b->rope, b->d_best);
+  const int max_b = b->max_b;
+  const int max_slots = (int)std::min<int64_t>(d.E, (int64_t)max_b * d.K);
+  k_zero_ints<<<dim3((unsigned)((d.L * (E + 1) + kBlock - 1) / kBlock)), dim3(kBlock), 0, st>>>(b->ecount,
+                                                                                               (int)(d.L * (E + 1)));
   auto norm = [&](const uint16_t* x, const void* w, uint16_t* out) {
     k_bnorm<<<dim3((unsigned)B), dim3(kBlock), (size_t)d.H * 2, st>>>(x, (const float*)w, H, c.eps, out);
   };
@@ -2312,7 +2322,7 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
     k_ws256<4><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), (size_t)kBatchNB * d.H * 4, st>>>(
         x, B, groups, seg, H);
   };
-  const int gate_blocks = (int)((std::max(d.I, d.SI) + kBGateRows - 1) / kBGateRows);
+  const int gate_blocks = (int)((std::max(d.I, d.SI) + kGateRowsPerBlock - 1) / kGateRowsPerBlock);
   const int hpk = (int)(d.Q / d.KVH);
   const int per_row = (int)((d.K * d.I + d.SI) / 8);
   int64_t base = 1;
@@ -2391,11 +2401,15 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
     norm(b->attn, post_norm, b->x);
     k_wsrouter<<<dim3((unsigned)((E + 1 + 3) / 4)), dim3(kBlock), (size_t)kRouterStage * d.H * 2, st>>>(
         b->x, B, H, (const float*)W(ffn), (const float*)W(ffn + 4), E, b->rlogits);
+    int* ecount = b->ecount + l * (E + 1);
+    int* elist = b->elist + 2 * l * E * max_b * K;
+    int* uexp = b->uexp + l * max_slots;
     k_sselect<<<dim3((unsigned)B), dim3(kBlock), (size_t)E * 4, st>>>(b->rlogits, E, K, b->bids, b->bprobs, rows,
-                                                                      (int)l);
-    k_bgate<<<dim3((unsigned)((B * K + 1) * gate_blocks)), dim3(kBlock), (size_t)kBGateStage * d.H * 2, st>>>(
+                                                                      (int)l, ecount, elist, max_b, uexp);
+    k_bgate<<<dim3((unsigned)((max_slots + 1) * gate_blocks)), dim3(kBlock), 0, st>>>(
         b->x, B, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
-        (const uint16_t*)W(ffn + 6), b->bids, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks, b->bact);
+        (const uint16_t*)W(ffn + 6), ecount, elist, uexp, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks,
+        max_slots, max_b, b->bact);
     k_bdown<<<dim3((unsigned)((d.H + kBDownRows - 1) / kBDownRows), (unsigned)((B + kBDownTokens - 1) / kBDownTokens)),
               dim3(kBlock), bdown_lds_bytes(per_row), st>>>(b->bact, B, (const uint16_t*)W(ffn + 3),
                                                              (const uint16_t*)W(ffn + 7), b->bids, b->attn, H, K, I, SI,
