@@ -10,11 +10,11 @@
 //
 //  k_ws256     S256 grouped projections (qwen35.group-project) for NB tokens
 //              staged in LDS, k_project256's lane order and tree;
-//  k_wsrouter  F32 router rows (moe.hex:4-84), every token per block,
-//              k_router_select's lane order and tree;
-//  k_sselect   per token: stable rank top-k and the softmax weights
-//              (moe.hex:86-252), the ids also copied to the session's export
-//              row, each (token, slot) appended to its expert's list;
+//  k_broute   the post-mixer norm and the F32 router rows (moe.hex:4-84),
+//              every token per block, k_router_select's lane order and tree;
+//  k_sselect   per token (one wave each): stable rank top-k and the softmax
+//              weights (moe.hex:86-252), the ids also copied to the session's
+//              export row, each (token, slot) appended to its expert's list;
 //  k_bgate     per distinct selected expert its gate/up rows applied to every
 //              token that selected it, with that token's weight; the shared
 //              expert's rows applied to every token (moe.hex:254-333);
@@ -95,145 +95,205 @@ __global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x
 
 // ---------------------------------------------------------------- router
 
-// Router logits of every token: rows [0, E) routed, row E the shared-expert
-// gate, F32 weights; one wave per row, all tokens per block (each row read
-// once), physical lane l = 2r + h running reference lane r's low (h = 0) or
-// high (h = 1) accumulator over floats l, l + 64, ..., then lo + hi and the
-// halving tree (k_router_select's order). logits [tokens][E + 1]. The
-// tokens' rows are staged in LDS as BF16, 8 at a time.
-constexpr int kRouterStage = 8;
-__global__ __launch_bounds__(kBlock) void k_wsrouter(const uint16_t* __restrict__ x, int tokens, int cols,
-                                                     const float* __restrict__ w, const float* __restrict__ shared_w,
-                                                     int experts, float* __restrict__ logits) {
-  extern __shared__ __align__(16) uint16_t xr_s[];  // [kRouterStage][cols]
+// qwen35.normalize of one row by one wave, the same sums as norm_finish's
+// block-wide tree: lane l holds octets 4l .. 4l + 3 (xv, with the norm
+// weights w0/w1 of those octets), so ((o0 + o1) + (o2 + o3)) is the tree's
+// first two cross-thread levels, lane strides 1, 2, 4, 8 its next four (each
+// 16 lanes are one of its waves), and strides 16 then 32 its ((w0 + w1) +
+// (w2 + w3)). The normalised octets go to xs (LDS) and, with out, to global
+// memory. cols <= 2048.
+__device__ __forceinline__ void wave_norm_octets(const u32x4 (&xv)[4], const f32x4 (&w0)[4], const f32x4 (&w1)[4],
+                                                 int cols, float eps, u32x4* xs, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63, octs = cols >> 3;
+  float sq[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sq[q] = 4 * lane + q < octs ? octet_squares(xv[q]) : 0.0f;
+  float t = (sq[0] + sq[1]) + (sq[2] + sq[3]);
+  t = t + lane_down<1>(t);
+  t = t + lane_down<2>(t);
+  t = t + lane_down<4>(t);
+  t = t + lane_down<8>(t);
+  t = t + lane_down<16>(t);
+  t = t + lane_down<32>(t);
+  const float sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, t)));
+  const float inverse = 1.0f / nsqrt(sum / (float)cols + eps);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int o = 4 * lane + q;
+    if (o < octs) {
+      const u32x4 y = octet_scale(xv[q], inverse, w0[q], w1[q]);
+      xs[o] = y;
+      if (out) reinterpret_cast<u32x4*>(out)[o] = y;
+    }
+  }
+}
+
+// Post-mixer norm and router logits of every token: rows [0, E) routed, row
+// E the shared-expert gate, F32 weights; one wave per row, all tokens per
+// block (each row read once). Every block normalises every token's row
+// (wave w the tokens w, w + 4, ...; block 0 also writes them to xout for the
+// expert kernels) into LDS, then each wave runs its row: physical lane
+// l = 2r + h holds reference lane r's low (h = 0) or high (h = 1)
+// accumulator over floats l, l + 64, ..., then lo + hi and the halving tree
+// (k_router_select's order). logits [tokens][E + 1].
+template <int KJ>  // cols / 64
+__global__ __launch_bounds__(kBlock) void k_broute(const uint16_t* __restrict__ raw, const float* __restrict__ norm_w,
+                                                   float eps, int tokens, const float* __restrict__ w,
+                                                   const float* __restrict__ shared_w, int experts,
+                                                   uint16_t* __restrict__ xout, float* __restrict__ logits) {
+  constexpr int cols = 64 * KJ;
+  extern __shared__ __align__(16) u32x4 xsb[];  // [tokens][cols / 8] normalised rows
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = experts + 1;
   const int row = blockIdx.x * 4 + wave;
   const int rc = min(row, rows - 1);
   const float* wr = rc < experts ? w + (size_t)rc * cols : shared_w;
-  constexpr int MAXJ = 32;  // cols <= 2048
-  float wv[MAXJ];
+  float wv[KJ];
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) wv[j] = wr[min(lane + 64 * j, cols - 1)];
-  const int quads = cols >> 3;
-  for (int t0 = 0; t0 < tokens; t0 += kRouterStage) {
-    const int m = min(kRouterStage, tokens - t0);
-    __syncthreads();
-    for (int i = threadIdx.x; i < m * quads; i += blockDim.x) {
-      const int t = i / quads, o = i - t * quads;
-      reinterpret_cast<u32x4*>(xr_s + (size_t)t * cols)[o] = ldq(x + (size_t)(t0 + t) * cols, o);
-    }
-    __syncthreads();
-    for (int t = 0; t < m; ++t) {
-      const uint16_t* xt = xr_s + (size_t)t * cols;
-      float acc = 0.0f;
+  for (int j = 0; j < KJ; ++j) wv[j] = wr[lane + 64 * j];
+  constexpr int quads = cols >> 3;
+  // norm weights of this lane's octets, the same for every token
+  f32x4 w0[4], w1[4];
 #pragma unroll
-      for (int j = 0; j < MAXJ; ++j)
-        if (lane + 64 * j < cols) acc += bf2f(xt[lane + 64 * j]) * wv[j];
-      float v = acc + lane_down<1>(acc);
-      v += lane_down<32>(v);
-      v += lane_down<16>(v);
-      v += lane_down<8>(v);
-      v += lane_down<4>(v);
-      v += lane_down<2>(v);
-      if (lane == 0 && row < rows) logits[(size_t)(t0 + t) * rows + row] = v;
+  for (int q = 0; q < 4; ++q) {
+    const int o = min(4 * lane + q, quads - 1);
+    w0[q] = reinterpret_cast<const f32x4*>(norm_w)[2 * o];
+    w1[q] = reinterpret_cast<const f32x4*>(norm_w)[2 * o + 1];
+  }
+  // wave w normalises tokens w, w + 4, ..., two at a time (both rows'
+  // loads issued before either sum)
+  for (int t = wave; t < tokens; t += 8) {
+    const int t2 = min(t + 4, tokens - 1);
+    u32x4 xa[4], xb[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int o = min(4 * lane + q, quads - 1);
+      xa[q] = ldq(raw + (size_t)t * cols, o);
+      xb[q] = ldq(raw + (size_t)t2 * cols, o);
     }
+    wave_norm_octets(xa, w0, w1, cols, eps, xsb + (size_t)t * quads, blockIdx.x == 0 ? xout + (size_t)t * cols : nullptr);
+    if (t + 4 < tokens)
+      wave_norm_octets(xb, w0, w1, cols, eps, xsb + (size_t)t2 * quads,
+                       blockIdx.x == 0 ? xout + (size_t)t2 * cols : nullptr);
+  }
+  __syncthreads();
+  for (int t = 0; t < tokens; ++t) {
+    const uint16_t* xt = reinterpret_cast<const uint16_t*>(xsb + (size_t)t * quads);
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KJ; ++j) acc += bf2f(xt[lane + 64 * j]) * wv[j];
+    float v = acc + lane_down<1>(acc);
+    v += lane_down<32>(v);
+    v += lane_down<16>(v);
+    v += lane_down<8>(v);
+    v += lane_down<4>(v);
+    v += lane_down<2>(v);
+    if (lane == 0 && row < rows) logits[(size_t)t * rows + row] = v;
   }
 }
 
-// Top-k of one token per block (moe.hex:86-252): without NaN logits, k
-// rounds of a wave-wide maximum of (value, lowest index) keys, which is the
-// stable descending rank; with NaNs the rank formula rank(e) =
-// #{i : l_i > l_e} + #{i < e : !(l_e > l_i)} (an unassigned rank k keeps
-// expert k), as k_router_select does. Then p_j = exp(l_j - l_0) / den with
-// den summed left to right from 0. The ids also go to row `layer` of the
-// session's export buffer.
-__global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ logits, int experts, int top_k,
-                                                    int* __restrict__ ids, float* __restrict__ probs,
+// Orderable image of a router logit: larger logits give larger images, -0
+// equals +0, every non-NaN image is at least 0x00800000 (0 marks absent or
+// taken).
+__device__ __forceinline__ uint32_t route_order(float le) {
+  const uint32_t u = le == 0.0f ? 0u : fbits(le);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+template <int S>
+__device__ __forceinline__ uint32_t umax_lane(uint32_t v) {
+  const uint32_t o = __builtin_bit_cast(uint32_t, lane_down<S>(__builtin_bit_cast(float, v)));
+  return o > v ? o : v;
+}
+
+// Top-k of one token per wave (moe.hex:86-252): without NaN logits, k rounds
+// of a wave-wide maximum of the images (DPP) and the lowest expert index
+// holding it (ballots), which is the stable descending rank; with NaNs the
+// rank formula rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)} (an
+// unassigned rank k keeps expert k), as k_router_select does. Then
+// p_j = exp(l_j - l_0) / den with den summed left to right from 0. The ids
+// also go to row `layer` of the session's export buffer, and each
+// (token, slot) with its weight to its expert's list for the gate/up
+// kernel (in any order: each token's rows are computed on their own; a
+// token's slots repeat an expert only when NaN logits made ranks collide,
+// so a list holds at most max_tokens * top_k entries); on its first
+// selection an expert takes a slot in the round's list of distinct experts
+// (count at ecount[experts]). One block of kBlock threads per 4 tokens.
+__global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ logits, int tokens, int experts,
+                                                    int top_k, int* __restrict__ ids, float* __restrict__ probs,
                                                     const SessionRows* __restrict__ rows, int layer,
                                                     int* __restrict__ ecount, int* __restrict__ elist, int max_tokens,
                                                     int* __restrict__ uexp) {
-  extern __shared__ float lg[];  // experts
-  __shared__ float chosen[64];
-  __shared__ int sid[64];
-  __shared__ int any_nan;
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int PER = 8;  // candidates per lane: experts <= 512
+  extern __shared__ float lgs[];  // [4][experts]
+  __shared__ int sid[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x * 4 + wave;
+  if (b >= tokens) return;  // wave-uniform; no barrier below
+  float* lg = lgs + wave * experts;
   const float* src = logits + (size_t)b * (experts + 1);
-  if (tid == 0) any_nan = 0;
-  __syncthreads();
-  for (int e = tid; e < experts; e += blockDim.x) {
-    const float le = src[e];
-    lg[e] = le;
-    if (le != le) any_nan = 1;
-  }
-  __syncthreads();
-  if (!any_nan) {
-    if (wave == 0) {
-      unsigned long long taken = 0;  // bit j: lane's j-th candidate chosen (experts <= 4096)
-      for (int k = 0; k < top_k; ++k) {
-        unsigned long long mine = 0ull;
-        for (int j = 0, e = lane; e < experts; ++j, e += 64) {
-          if ((taken >> j) & 1ull) continue;
-          const float le = lg[e];
-          const uint32_t u = le == 0.0f ? 0u : fbits(le);
-          const uint32_t ordered = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-          const unsigned long long key = ((unsigned long long)ordered << 32) | (0xffffffffu - (uint32_t)e);
-          mine = key > mine ? key : mine;
-        }
-        unsigned long long best = mine;
+  uint32_t ov[PER];
+  bool nan = false;
 #pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-          const unsigned long long o = __shfl_xor(best, sh, 64);
-          best = o > best ? o : best;
-        }
-        const int e = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-        if ((e & 63) == lane) taken |= 1ull << (e >> 6);
-        if (lane == 0) {
-          sid[k] = e;
-          chosen[k] = lg[e];
-        }
+  for (int c = 0; c < PER; ++c) {
+    const int e = lane + 64 * c;
+    ov[c] = 0u;
+    if (e < experts) {
+      const float le = src[e];
+      lg[e] = le;
+      nan |= le != le;
+      ov[c] = route_order(le);
+    }
+  }
+  if (!__any(nan)) {
+    for (int k = 0; k < top_k; ++k) {
+      uint32_t best = ov[0];
+#pragma unroll
+      for (int c = 1; c < PER; ++c) best = ov[c] > best ? ov[c] : best;
+      best = umax_lane<32>(best);
+      best = umax_lane<16>(best);
+      best = umax_lane<8>(best);
+      best = umax_lane<4>(best);
+      best = umax_lane<2>(best);
+      best = umax_lane<1>(best);
+      const uint32_t win = __builtin_amdgcn_readfirstlane(best);
+      int e = experts;
+#pragma unroll
+      for (int c = PER - 1; c >= 0; --c) {
+        const unsigned long long hit = __ballot(ov[c] == win);
+        if (hit) e = 64 * c + __builtin_ctzll(hit);
       }
+#pragma unroll
+      for (int c = 0; c < PER; ++c)
+        if (64 * c + lane == e) ov[c] = 0u;  // taken
+      if (lane == 0) sid[wave][k] = e;
     }
   } else {
-    if (tid < top_k) {
-      sid[tid] = tid;
-      chosen[tid] = lg[tid];
-    }
-    __syncthreads();
-    for (int e = tid; e < experts; e += blockDim.x) {
+    if (lane < top_k) sid[wave][lane] = lane;
+    for (int e = lane; e < experts; e += 64) {
       const float le = lg[e];
       int rank = 0;
       for (int i = 0; i < experts; ++i) {
         const float o = lg[i];
         rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
       }
-      if (rank < top_k) {
-        sid[rank] = e;
-        chosen[rank] = le;
-      }
+      if (rank < top_k) sid[wave][rank] = e;
     }
   }
-  __syncthreads();
-  if (wave == 0) {
-    const float ex = lane < top_k ? hexp(chosen[lane] - chosen[0]) : 0.0f;
-    float den = 0.0f;
-    for (int j = 0; j < top_k; ++j) den = den + __shfl(ex, j, 64);
-    if (lane < top_k) {
-      const int e = sid[lane];
-      probs[b * top_k + lane] = ex / den;
-      ids[b * top_k + lane] = e;
-      if (rows->ids[b]) rows->ids[b][layer * top_k + lane] = e;
-      // the expert's (token, slot) list for the gate/up kernel (in any
-      // order: each token's rows are computed on their own; a token's slots
-      // repeat an expert only when NaN logits made ranks collide, so a list
-      // holds at most max_tokens * top_k entries), and on its first
-      // selection a slot in the round's list of distinct experts (count at
-      // ecount[experts])
-      const int at = atomicAdd(&ecount[e], 1);
-      reinterpret_cast<int2*>(elist)[(size_t)e * max_tokens * top_k + at] =
-          int2{(b << 8) | lane, (int)fbits(ex / den)};
-      if (at == 0) uexp[atomicAdd(&ecount[experts], 1)] = e;
-    }
+  const int e = lane < top_k ? sid[wave][lane] : 0;
+  const float lj = lane < top_k ? lg[e] : 0.0f;
+  const float l0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, lj)));
+  const float ex = lane < top_k ? hexp(lj - l0) : 0.0f;
+  float den = 0.0f;
+  for (int j = 0; j < top_k; ++j)
+    den = den + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), j));
+  if (lane < top_k) {
+    const float pj = ex / den;
+    probs[b * top_k + lane] = pj;
+    ids[b * top_k + lane] = e;
+    if (rows->ids[b]) rows->ids[b][layer * top_k + lane] = e;
+    const int at = atomicAdd(&ecount[e], 1);
+    reinterpret_cast<int2*>(elist)[(size_t)e * max_tokens * top_k + at] = int2{(b << 8) | lane, (int)fbits(pj)};
+    if (at == 0) uexp[atomicAdd(&ecount[experts], 1)] = e;
   }
 }
 

@@ -2398,14 +2398,22 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
       post_norm = W(10);
       ffn = 11;
     }
-    norm(b->attn, post_norm, b->x);
-    k_wsrouter<<<dim3((unsigned)((E + 1 + 3) / 4)), dim3(kBlock), (size_t)kRouterStage * d.H * 2, st>>>(
-        b->x, B, H, (const float*)W(ffn), (const float*)W(ffn + 4), E, b->rlogits);
+    {
+      const dim3 rg((unsigned)((E + 1 + 3) / 4));
+      const size_t rl = (size_t)B * d.H * 2;
+      const float *pn = (const float*)post_norm, *rw = (const float*)W(ffn), *srw = (const float*)W(ffn + 4);
+      switch (H) {
+        case 2048: k_broute<32><<<rg, dim3(kBlock), rl, st>>>(b->attn, pn, c.eps, B, rw, srw, E, b->x, b->rlogits); break;
+        case 1024: k_broute<16><<<rg, dim3(kBlock), rl, st>>>(b->attn, pn, c.eps, B, rw, srw, E, b->x, b->rlogits); break;
+        case 512: k_broute<8><<<rg, dim3(kBlock), rl, st>>>(b->attn, pn, c.eps, B, rw, srw, E, b->x, b->rlogits); break;
+        default: k_broute<4><<<rg, dim3(kBlock), rl, st>>>(b->attn, pn, c.eps, B, rw, srw, E, b->x, b->rlogits); break;
+      }
+    }
     int* ecount = b->ecount + l * (E + 1);
     int* elist = b->elist + 2 * l * E * max_b * K;
     int* uexp = b->uexp + l * max_slots;
-    k_sselect<<<dim3((unsigned)B), dim3(kBlock), (size_t)E * 4, st>>>(b->rlogits, E, K, b->bids, b->bprobs, rows,
-                                                                      (int)l, ecount, elist, max_b, uexp);
+    k_sselect<<<dim3((unsigned)((B + 3) / 4)), dim3(kBlock), (size_t)4 * E * 4, st>>>(
+        b->rlogits, B, E, K, b->bids, b->bprobs, rows, (int)l, ecount, elist, max_b, uexp);
     k_bgate<<<dim3((unsigned)((max_slots + 1) * gate_blocks)), dim3(kBlock), 0, st>>>(
         b->x, B, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
         (const uint16_t*)W(ffn + 6), ecount, elist, uexp, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks,
@@ -2485,13 +2493,13 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
   return CQ35_OK;
 }
 
-// Whether the MoE shape fits the batched MoE kernels: the hidden row staged
-// once (k_ws256, k_wsrouter, k_bgate), expert widths in whole 64-element
+// Whether the MoE shape fits the batched MoE kernels: a hidden width the
+// router is instantiated for (staged once by k_ws256 and k_broute), expert widths in whole 64-element
 // lane rounds (k_bdown), the head dim within one flash block, 1, 2, 4 or 8
 // query heads per KV head and at most 16 experts selected per token.
 bool moe_batch_shape_ok(const cq35_model* m) {
   const Dims& d = m->d;
-  return d.H <= kBatchChunk && d.H % 64 == 0 && d.I % 64 == 0 && d.I <= 512 && d.SI % 64 == 0 && d.HD <= 256 &&
+  return (d.H == 2048 || d.H == 1024 || d.H == 512 || d.H == 256) && d.I % 64 == 0 && d.I <= 512 && d.E <= 512 && d.SI % 64 == 0 && d.HD <= 256 &&
          (d.Q / d.KVH == 1 || d.Q / d.KVH == 2 || d.Q / d.KVH == 4 || d.Q / d.KVH == 8) && d.K <= 16 && d.E <= 4096;
 }
 
@@ -2504,6 +2512,8 @@ bool shared_batch_ok(cq35_session* const* sessions, int64_t count) {
   const cq35_model* m = sessions[0]->model;
   if (m->cfg.hidden > kBatchChunk) return false;  // the SwiGLU and the S256 stage one row chunk
   if (m->cfg.moe && !moe_batch_shape_ok(m)) return false;
+  // the MoE router stages every token's normalised row in LDS (64 KiB)
+  if (m->cfg.moe && count * m->cfg.hidden * 2 > 65536) return false;
   for (int64_t i = 0; i < count; ++i)
     if (sessions[i]->model != m || sessions[i]->capacity != sessions[0]->capacity || sessions[i]->timed_class >= 0)
       return false;
