@@ -307,71 +307,118 @@ __global__ void k_zero_ints(int* __restrict__ p, int n) {
 
 constexpr int kGateRowsPerBlock = 4;  // one row pair (gate, up) per wave
 
-// Block (expert slot, 4 rows): slots [0, n) are the round's distinct
-// selected experts (in selection order), slot max_slots the shared expert.
-// Each wave is on its own (no LDS, no barrier): it reads its expert, issues
-// its row pair's loads (gate and up, 8 KB), then for each (token, slot) of
-// the expert's list loads the token's normalised row (L2) and runs the dual
-// S256 (k_gate_up's order): routed act[t][slot * I + row] =
+// Block (slot, 4 rows): slot 0 is the shared expert (its waves run every
+// token, so they start first), slots 1 .. n the round's distinct selected
+// experts (in selection order). Each wave is on its own (no LDS, no
+// barrier): it reads its expert, then the head of the expert's list of
+// (token, slot) entries, issues its row pair's loads (gate and up, 8 KB) and
+// the first two entries' normalised rows (L2), and runs the dual S256
+// (k_gate_up's order) per entry, the row of the entry after next loaded
+// while an entry computes: routed act[t][slot * I + row] =
 // bf16(silu(bf16 g) * bf16 u * p_{t,slot}); shared act[t][K * I + row] =
 // bf16(bf16(bf16(silu(bf16 g)) * bf16 u) * sigmoid(l_E)). Small waves keep
-// many of them resident per CU, which is what keeps HBM busy here.
-// x [tokens][cols] normalised rows, cols <= 2048.
+// many of them resident per CU, which is what keeps HBM busy here. Loads
+// past a list's end are clamped inside the list and the token range (their
+// rows are loaded, never used).
+// x [tokens][cols] normalised rows, cols = 512 NQ (FULL) or below 512 NQ.
+template <int NQ, bool FULL>
 __global__ __launch_bounds__(kBlock) void k_bgate(
     const uint16_t* __restrict__ x, int tokens, int cols, const uint16_t* __restrict__ gate,
     const uint16_t* __restrict__ up, const uint16_t* __restrict__ sgate, const uint16_t* __restrict__ sup,
     const int* __restrict__ ecount, const int* __restrict__ elist, const int* __restrict__ uexp,
     const float* __restrict__ probs, const float* __restrict__ logits, int experts, int top_k, int inter,
     int shared_inter, int row_blocks, int max_slots, int max_tokens, uint16_t* __restrict__ act) {
-  constexpr int NQ = 4;
-  const int slot = blockIdx.x / row_blocks, rb = blockIdx.x - slot * row_blocks;
+  const int sidx = blockIdx.x / row_blocks, rb = blockIdx.x - sidx * row_blocks;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int quads = cols >> 3;
-  const bool shared = slot == max_slots;
+  const int quads = FULL ? 64 * NQ : cols >> 3;
+  const bool shared = sidx == 0;
+  const int slot = sidx - 1;
   const int nrows = shared ? shared_inter : inter;
   const int row = rb * kGateRowsPerBlock + wave;
   if (row >= nrows) return;  // wave-uniform
   // the distinct-expert count and this slot's expert in one round trip
   const int n_u = ecount[experts];
-  const int e = shared ? 0 : uexp[min(slot, max_slots - 1)];
+  const int e = shared ? 0 : uexp[max(slot, 0)];
   if (!shared && slot >= n_u) return;  // fewer distinct experts this round
+  const int cap = max_tokens * top_k;  // entries one list can hold
+  const int2* list = reinterpret_cast<const int2*>(elist) + (size_t)e * cap;
+  // count and list head first: they return ahead of the rows
+  const int n = shared ? tokens : ecount[e];
+  int2 head[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int2 v = list[min(i, cap - 1)];
+    head[i] = shared ? int2{min(i, tokens - 1) << 8, 0} : v;
+  }
   const uint16_t* g = shared ? sgate + (size_t)row * cols : gate + ((size_t)e * inter + row) * cols;
   const uint16_t* u = shared ? sup + (size_t)row * cols : up + ((size_t)e * inter + row) * cols;
   u32x4 gv[NQ], uv[NQ];
 #pragma unroll
   for (int j = 0; j < NQ; ++j) {
-    gv[j] = ldq(g, min(lane + 64 * j, quads - 1));
-    uv[j] = ldq(u, min(lane + 64 * j, quads - 1));
+    const int o = FULL ? lane + 64 * j : min(lane + 64 * j, quads - 1);
+    gv[j] = ldq(g, o);
+    uv[j] = ldq(u, o);
   }
-  const int n = shared ? tokens : ecount[e];
-  const int2* list = reinterpret_cast<const int2*>(elist) + (size_t)e * max_tokens * top_k;
-  const int act_row = top_k * inter + shared_inter;
-  for (int s = 0; s < n; ++s) {
-    const int2 entry = shared ? int2{s << 8, 0} : list[s];
-    const int t = entry.x >> 8, k = entry.x & 255;
-    const float w = shared ? sigmoid(logits[(size_t)t * (experts + 1) + experts]) : bitsf((uint32_t)entry.y);
-    const uint16_t* xr = x + (size_t)t * cols;
-    u32x4 xq[NQ];
+  // an entry past the list's end holds whatever the buffer held: its token
+  // field is clamped into [0, tokens) as an unsigned value
+  auto row_of = [&](int2 entry) {
+    return x + (size_t)min((unsigned)(entry.x >> 8), (unsigned)(tokens - 1)) * cols;
+  };
+  auto load_x = [&](u32x4 (&xq)[NQ], const uint16_t* xr) {
 #pragma unroll
-    for (int j = 0; j < NQ; ++j) xq[j] = ldq(xr, min(lane + 64 * j, quads - 1));
+    for (int j = 0; j < NQ; ++j) xq[j] = ldq(xr, FULL ? lane + 64 * j : min(lane + 64 * j, quads - 1));
+  };
+  auto entry_at = [&](int i) {
+    const int2 v = list[min(i, cap - 1)];
+    return shared ? int2{min(i, tokens - 1) << 8, 0} : v;
+  };
+  const int act_row = top_k * inter + shared_inter;
+  auto run = [&](int2 entry, const u32x4(&xq)[NQ]) {
+    // the rows stay packed across entries (unpacked per use, not hoisted)
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) asm volatile("" : "+v"(gv[j]), "+v"(uv[j]));
+    const int t = entry.x >> 8, k = entry.x & 255;
+    // the gate row's sums, then the up row's (one accumulator set live)
     Quad ga, ua;
     quad_zero(ga);
+#pragma unroll
+    for (int j = 0; j < NQ; ++j)
+      if (FULL || lane + 64 * j < quads) quad_acc(ga, xq[j], gv[j]);
+    const float gsum = quad_tree<64>(ga);
+    __builtin_amdgcn_sched_barrier(0);
     quad_zero(ua);
 #pragma unroll
     for (int j = 0; j < NQ; ++j)
-      if (lane + 64 * j < quads) {
-        quad_acc(ga, xq[j], gv[j]);
-        quad_acc(ua, xq[j], uv[j]);
-      }
-    const float gsum = quad_tree<64>(ga);
+      if (FULL || lane + 64 * j < quads) quad_acc(ua, xq[j], uv[j]);
     const float usum = quad_tree<64>(ua);
     if (lane == 0) {
       const float gb = rbf(gsum), ub = rbf(usum);
       const float activated = silu(gb);
       if (!shared)
-        act[(size_t)t * act_row + (size_t)k * inter + row] = f2bf((activated * ub) * w);
+        act[(size_t)t * act_row + (size_t)k * inter + row] = f2bf((activated * ub) * bitsf((uint32_t)entry.y));
       else
-        act[(size_t)t * act_row + (size_t)top_k * inter + row] = f2bf(rbf(rbf(activated) * ub) * w);
+        act[(size_t)t * act_row + (size_t)top_k * inter + row] =
+            f2bf(rbf(rbf(activated) * ub) * sigmoid(logits[(size_t)t * (experts + 1) + experts]));
+    }
+  };
+  // two entries in flight: A holds the even ones, B the odd ones; an
+  // entry's successor but one loads while the entry between them computes
+  u32x4 xa[NQ], xb[NQ];
+  int2 ea = head[0], eb = head[1];
+  load_x(xa, row_of(ea));
+  load_x(xb, row_of(eb));
+  for (int s = 0; s < n; s += 2) {
+    run(ea, xa);
+    if (s + 2 < n) {
+      ea = entry_at(s + 2);
+      load_x(xa, row_of(ea));
+    }
+    if (s + 1 < n) {
+      run(eb, xb);
+      if (s + 3 < n) {
+        eb = entry_at(s + 3);
+        load_x(xb, row_of(eb));
+      }
     }
   }
 }

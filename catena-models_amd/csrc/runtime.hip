@@ -2414,10 +2414,16 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
     int* uexp = b->uexp + l * max_slots;
     k_sselect<<<dim3((unsigned)((B + 3) / 4)), dim3(kBlock), (size_t)4 * E * 4, st>>>(
         b->rlogits, B, E, K, b->bids, b->bprobs, rows, (int)l, ecount, elist, max_b, uexp);
-    k_bgate<<<dim3((unsigned)((max_slots + 1) * gate_blocks)), dim3(kBlock), 0, st>>>(
-        b->x, B, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
-        (const uint16_t*)W(ffn + 6), ecount, elist, uexp, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks,
-        max_slots, max_b, b->bact);
+    {
+      auto gate_kernel = H == 2048   ? k_bgate<4, true>
+                         : H == 1024 ? k_bgate<2, true>
+                         : H == 512  ? k_bgate<1, true>
+                                     : k_bgate<1, false>;
+      gate_kernel<<<dim3((unsigned)((max_slots + 1) * gate_blocks)), dim3(kBlock), 0, st>>>(
+          b->x, B, H, (const uint16_t*)W(ffn + 1), (const uint16_t*)W(ffn + 2), (const uint16_t*)W(ffn + 5),
+          (const uint16_t*)W(ffn + 6), ecount, elist, uexp, b->bprobs, b->rlogits, E, K, I, SI, gate_blocks,
+          max_slots, max_b, b->bact);
+    }
     k_bdown<<<dim3((unsigned)((d.H + kBDownRows - 1) / kBDownRows), (unsigned)((B + kBDownTokens - 1) / kBDownTokens)),
               dim3(kBlock), bdown_lds_bytes(per_row), st>>>(b->bact, B, (const uint16_t*)W(ffn + 3),
                                                              (const uint16_t*)W(ffn + 7), b->bids, b->attn, H, K, I, SI,
