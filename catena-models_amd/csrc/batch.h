@@ -174,11 +174,11 @@ __global__ __launch_bounds__(kBlock) void k_ws32(const uint16_t* __restrict__ x,
 // quads q, q + 16, ... in order) for NB tokens:
 // out[t][r] = bf16(bf16(tree64(x_t . w_r)) (+) res[t][r]). Four waves of four
 // rows per block; the input staged in column chunks.
-template <int kNQ>
+template <int kNQ, int NB = kBatchNB>
 __global__ __launch_bounds__(kBlock) void k_ws64(const uint16_t* __restrict__ x, int tokens, int groups,
                                                  const uint16_t* __restrict__ w, int rows, int cols,
                                                  const uint16_t* __restrict__ res, uint16_t* __restrict__ out) {
-  constexpr int NB = kBatchNB, NQ = kNQ;
+  constexpr int NQ = kNQ;
   extern __shared__ __align__(16) float xf[];  // [NB][chunk]
   int rb, tg;
   batch_block(blockIdx.x, groups, &rb, &tg);

@@ -45,13 +45,14 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T* gmem(const
 // ------------------------------------------------ S256 grouped projection
 
 // Rows of up to four segments for NB tokens of already normalised rows
-// (cols <= kBatchChunk, staged once): token t's output row r of segment s
-// goes to seg.out[s][t * seg.rows[s] + r]. Each wave runs kRW rows, one at a
-// time, 64 lanes per row, lane l visiting quads l, l + 64, ... in order.
-template <int kRW>
+// (cols <= kBatchChunk, staged once as F32): token t's output row r of
+// segment s goes to seg.out[s][t * seg.rows[s] + r]. Each wave runs kRW rows,
+// one at a time, 64 lanes per row, lane l visiting quads l, l + 64, ... in
+// order.
+template <int kRW, int NB>
 __global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x, int tokens, int groups,
                                                   Segments seg, int cols) {
-  constexpr int NB = kBatchNB, RW = kRW, NQ = 4;
+  constexpr int RW = kRW, NQ = 4;
   extern __shared__ __align__(16) float xf[];  // [NB][cols]
   int rb, tg;
   batch_block(blockIdx.x, groups, &rb, &tg);

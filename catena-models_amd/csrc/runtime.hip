@@ -2203,11 +2203,18 @@ void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows,
     else skinny<kBPlain>(st, mx, x, B, cols, one, nullptr, nullptr, nullptr);
     return;
   }
-  const int groups = (B + kBatchNB - 1) / kBatchNB;
+  // two tokens per block up to 8 tokens (more blocks in flight), four above
+  const int nb = B <= 8 ? 2 : kBatchNB;
+  const int groups = (B + nb - 1) / nb;
   const int row_blocks = (int)((rows + 15) / 16);
-  const size_t lds = (size_t)kBatchNB * std::min<int64_t>(cols, kBatchChunk) * 4;
-  k_ws64<8><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), lds, st>>>(
-      x, B, groups, static_cast<const uint16_t*>(w), (int)rows, (int)cols, res, out);
+  const size_t lds = (size_t)nb * std::min<int64_t>(cols, kBatchChunk) * 4;
+  const dim3 grid((unsigned)batch_grid(row_blocks, groups));
+  if (nb == 2)
+    k_ws64<8, 2><<<grid, dim3(kBlock), lds, st>>>(x, B, groups, static_cast<const uint16_t*>(w), (int)rows,
+                                                  (int)cols, res, out);
+  else
+    k_ws64<8><<<grid, dim3(kBlock), lds, st>>>(x, B, groups, static_cast<const uint16_t*>(w), (int)rows, (int)cols,
+                                               res, out);
 }
 
 // The batched decode step's launch sequence (dense models): every layer of
@@ -2318,9 +2325,16 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
     k_bnorm<<<dim3((unsigned)B), dim3(kBlock), (size_t)d.H * 2, st>>>(x, (const float*)w, H, c.eps, out);
   };
   auto ws256 = [&](const uint16_t* x, const Segments& seg) {
-    const int row_blocks = (int)((seg_rows(seg) + 4 * 4 - 1) / (4 * 4));
-    k_ws256<4><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), (size_t)kBatchNB * d.H * 4, st>>>(
-        x, B, groups, seg, H);
+    // two rows per wave; two tokens per block up to 8 sessions (more blocks
+    // in flight, the other token groups' weight reads hit the XCD's L2),
+    // four above
+    const int row_blocks = (int)((seg_rows(seg) + 4 * 2 - 1) / (4 * 2));
+    if (B <= 8)
+      k_ws256<2, 2><<<dim3((unsigned)batch_grid(row_blocks, (B + 1) / 2)), dim3(kBlock), (size_t)2 * d.H * 4, st>>>(
+          x, B, (B + 1) / 2, seg, H);
+    else
+      k_ws256<2, 4><<<dim3((unsigned)batch_grid(row_blocks, (B + 3) / 4)), dim3(kBlock), (size_t)4 * d.H * 4, st>>>(
+          x, B, (B + 3) / 4, seg, H);
   };
   const int gate_blocks = (int)((std::max(d.I, d.SI) + kGateRowsPerBlock - 1) / kGateRowsPerBlock);
   const int hpk = (int)(d.Q / d.KVH);
