@@ -261,7 +261,8 @@ def long_context_decode(model, cfg: dict, context: int, steps: int, seed: int) -
     positions (the long-context configuration's per-session work)."""
     import cq35
     warm = 2
-    capacity = context + warm + steps
+    exact_steps = max(2, steps // 4)
+    capacity = context + warm + steps + 1 + exact_steps
     t0 = time.time()
     state = seeded_state(cfg, capacity, context, seed + 101)
     s = model.session(capacity)
@@ -282,12 +283,42 @@ def long_context_decode(model, cfg: dict, context: int, steps: int, seed: int) -
     bpt = cq35.bytes_per_token(cfg, context + warm + steps // 2)
     gbs = bpt["total"] / (ms / 1e3) / 1e9
     log(f"long context {context}: {steps / elapsed:.1f} tok/s, {ms:.3f} ms/token, {gbs:.0f} GB/s "
-        f"of {bpt['total'] / 1e9:.3f} GB/token")
+        f"of {bpt['total'] / 1e9:.3f} GB/token (split-K above {s.attention_split} keys)")
+    # the same session on the exact single chain (split off): the reference's
+    # own order, the rate that meets the logit bar at full depth
+    split = s.attention_split
+    s.set_attention_split(0)
+    nxt = s.decode_next_token(nxt)
+    device_sync()
+    t0 = time.perf_counter()
+    for _ in range(exact_steps):
+        nxt = s.decode_next_token(nxt)
+    device_sync()
+    exact_s = time.perf_counter() - t0
+    s.set_attention_split(split)
+    log(f"long context {context}, exact single chain: {exact_steps / exact_s:.1f} tok/s")
     return dict(context=context, steps=steps, warmup=warm, tokens_per_s=round(steps / elapsed, 2),
                 ms_per_token=round(ms, 4), bytes_per_token=bpt["total"], achieved_gbs=round(gbs, 1),
-                frac=round(gbs / HBM_PEAK_GBS, 4),
+                frac=round(gbs / HBM_PEAK_GBS, 4), split_keys=split,
+                exact_chain=dict(steps=exact_steps, tokens_per_s=round(exact_steps / exact_s, 2),
+                                 ms_per_token=round(exact_s / exact_steps * 1e3, 4)),
                 decode_path="persistent one-launch step" if s.persistent else "per-kernel launch sequence",
                 state="seeded: KV N(0,1) x 0.1, conv history N(0,1) x 0.1, DeltaNet state N(0,1)")
+
+
+def round_bytes(cfg: dict, sessions: int, context: int, distinct: float) -> dict:
+    """Algorithmic HBM bytes of one weight-shared batched MoE round:
+    `sessions` tokens at about `context` cached positions each, the
+    non-expert weights read once, `distinct` routed experts per layer read
+    once each, every session's KV and DeltaNet state."""
+    import cq35
+    one = cq35.bytes_per_token(cfg, context)
+    expert = 3 * cfg["intermediate"] * cfg["hidden"] * 2
+    routed_one = cfg["layers"] * cfg["top_k"] * expert
+    weights = one["weights"] - routed_one + (sessions - 1) * cfg["hidden"] * 2  # one embedding row per token
+    routed = cfg["layers"] * distinct * expert
+    return dict(weights=weights, routed_experts=routed, kv=sessions * one["kv"], state=sessions * one["state"],
+                total=weights + routed + sessions * (one["kv"] + one["state"]))
 
 
 def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, prefill_tokens: int,
@@ -301,6 +332,8 @@ def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, p
     cores (MFMA projections, experts and attention), one call after each
     decode round until it is done. Aggregate decode tok/s over the whole
     interleaved run."""
+    import numpy as np
+
     import cq35
     capacity = context + steps + 8
     t0 = time.time()
@@ -341,16 +374,33 @@ def concurrent_long(model, cfg: dict, sessions: int, context: int, steps: int, p
     log(f"{sessions} sessions x {context} positions, {steps} rounds with a {prefill_tokens}-token chunked "
         f"prefill interleaved: {agg:.1f} decode tok/s aggregate ({wall:.2f}s; decode {decode_s:.2f}s, "
         f"prefill {prefill_s:.2f}s = {prefill_tokens / prefill_s:.0f} tok/s)")
-    bpt = cq35.bytes_per_token(cfg, context + steps // 2)
+    # distinct routed experts per layer and round, from a few more rounds
+    # (outside the timing: the ids are read back per session)
+    distinct = []
+    for _ in range(4):
+        nxt = cq35.decode_batch(group, nxt)
+        ids = np.stack([s.router_ids() for s in group])  # [sessions][layers][top_k]
+        distinct += [len(np.unique(ids[:, layer, :])) for layer in range(ids.shape[1])]
+    rb = round_bytes(cfg, sessions, context + steps // 2, float(np.mean(distinct)))
+    round_s = decode_s / steps
+    log(f"  per round: {rb['total'] / 1e9:.2f} GB ({np.mean(distinct):.1f} distinct experts per layer), "
+        f"{round_s * 1e3:.2f} ms, {rb['total'] / round_s / 1e9:.0f} GB/s")
     return dict(sessions=sessions, context=context, steps=steps, wall_s=round(wall, 3),
                 decode_tokens_per_s=round(agg, 1), decode_only_tokens_per_s=round(sessions * steps / decode_s, 1),
-                decode_step_roofline_frac=round(bpt["total"] * sessions * steps / decode_s / 1e9 / HBM_PEAK_GBS, 4),
+                ms_per_round=round(round_s * 1e3, 3), bytes_per_round=int(rb["total"]),
+                bytes_per_round_parts={k: int(v) for k, v in rb.items() if k != "total"},
+                distinct_experts_per_layer=round(float(np.mean(distinct)), 2),
+                achieved_gbs=round(rb["total"] / round_s / 1e9, 1),
+                decode_step_roofline_frac=round(rb["total"] / round_s / 1e9 / HBM_PEAK_GBS, 4),
                 prefill=dict(tokens=prefill_tokens, chunk=chunk, seconds=round(prefill_s, 3),
                              tokens_per_s=round(prefill_tokens / prefill_s, 1),
                              path="matrix-core prefill (MFMA projections, experts and attention), one call per round"),
                 state="seeded: KV N(0,1) x 0.1, conv history N(0,1) x 0.1, DeltaNet state N(0,1); one state "
                       "imported into every session",
-                decode_path="cq35_step_batch: persistent steps one session at a time (each needs every CU)")
+                split_keys=group[0].attention_split,
+                decode_path="cq35_step_batch: weight-shared MoE step (projections, router, shared expert and head "
+                            "read once per round, each distinct routed expert once; per-session split-K "
+                            "attention)")
 
 
 def batch_sessions(config: str, sessions: int, context: int, steps: int, seed: int) -> dict:
