@@ -21,8 +21,8 @@
 
 namespace cq35 {
 
-constexpr int kBatchNB = 4;      // tokens per S32 / S64 GEMV block
-constexpr int kBatchNBDual = 4;  // tokens per dual S256 (SwiGLU) block
+constexpr int kBatchNB = 4;      // tokens per S32 GEMV block (S64 launches use 2)
+constexpr int kBatchNBDual = 2;  // tokens per dual S256 (SwiGLU) block
 constexpr int kBatchChunk = 2048;  // input columns staged per pass
 
 // (row block, token group) of block b for `groups` token groups.
@@ -97,10 +97,10 @@ __global__ __launch_bounds__(kBlock) void k_sembed(const SessionRows* __restrict
 // normalised rows; token t's output row r of segment s goes to
 // seg.out[s][t * seg.rows[s] + r]. kArgmax: the vocabulary head, with each
 // token's (value, lowest index) maximum into best[t].
-template <bool kArgmax, int kNQ>
+template <bool kArgmax, int kNQ, int NB = kBatchNB>
 __global__ __launch_bounds__(kBlock) void k_ws32(const uint16_t* __restrict__ x, int tokens, int groups,
                                                  Segments seg, int cols, unsigned long long* __restrict__ best) {
-  constexpr int NB = kBatchNB, NQ = kNQ;
+  constexpr int NQ = kNQ;
   extern __shared__ __align__(16) float xf[];  // [NB][chunk]
   __shared__ unsigned long long wave_best[4][NB];
   int rb, tg;
@@ -224,11 +224,12 @@ __global__ __launch_bounds__(kBlock) void k_ws64(const uint16_t* __restrict__ x,
 // quads l, l + 64, ... in order, kRowsGate rows per wave) for NB tokens of
 // already normalised rows: act[t][r] = bf16(bf16(silu(bf16 g)) * bf16(u)).
 // The input is staged once (cols <= kBatchChunk).
+template <int NB = kBatchNBDual>
 __global__ __launch_bounds__(kBlock) void k_ws256_swiglu(const uint16_t* __restrict__ x, int tokens, int groups,
                                                          const uint16_t* __restrict__ gate,
                                                          const uint16_t* __restrict__ up, int rows, int cols,
                                                          uint16_t* __restrict__ act) {
-  constexpr int NB = kBatchNBDual, RW = kRowsGate, NQ = 4;
+  constexpr int RW = kRowsGate, NQ = 4;
   extern __shared__ __align__(16) float xf[];  // [NB][cols]
   int rb, tg;
   batch_block(blockIdx.x, groups, &rb, &tg);

@@ -2203,18 +2203,14 @@ void ws64(hipStream_t st, const uint16_t* x, int B, const void* w, int64_t rows,
     else skinny<kBPlain>(st, mx, x, B, cols, one, nullptr, nullptr, nullptr);
     return;
   }
-  // two tokens per block up to 8 tokens (more blocks in flight), four above
-  const int nb = B <= 8 ? 2 : kBatchNB;
+  // two tokens per block: more blocks in flight (the other token groups'
+  // weight reads hit the XCD's L2)
+  constexpr int nb = 2;
   const int groups = (B + nb - 1) / nb;
   const int row_blocks = (int)((rows + 15) / 16);
   const size_t lds = (size_t)nb * std::min<int64_t>(cols, kBatchChunk) * 4;
-  const dim3 grid((unsigned)batch_grid(row_blocks, groups));
-  if (nb == 2)
-    k_ws64<8, 2><<<grid, dim3(kBlock), lds, st>>>(x, B, groups, static_cast<const uint16_t*>(w), (int)rows,
-                                                  (int)cols, res, out);
-  else
-    k_ws64<8><<<grid, dim3(kBlock), lds, st>>>(x, B, groups, static_cast<const uint16_t*>(w), (int)rows, (int)cols,
-                                               res, out);
+  k_ws64<8, nb><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), lds, st>>>(
+      x, B, groups, static_cast<const uint16_t*>(w), (int)rows, (int)cols, res, out);
 }
 
 // The batched decode step's launch sequence (dense models): every layer of
@@ -2286,12 +2282,12 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       skinny<kBGate>(st, b, b->x, B, d.H, segments({{W(ffn), {b->act, d.I}}}), (const uint16_t*)W(ffn + 1), nullptr,
                      nullptr);
     } else {
-      const int groups = (B + kBatchNBDual - 1) / kBatchNBDual;
+      // two tokens per block (as the S64 products): more blocks in flight
+      constexpr int nb = kBatchNBDual;
+      const int groups = (B + nb - 1) / nb;
       const int row_blocks = (int)((d.I + 4 * kRowsGate - 1) / (4 * kRowsGate));
-      k_ws256_swiglu<<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock),
-                       (size_t)kBatchNBDual * d.H * 4, st>>>(b->x, B, groups, (const uint16_t*)W(ffn),
-                                                             (const uint16_t*)W(ffn + 1), (int)d.I, (int)d.H,
-                                                             b->act);
+      k_ws256_swiglu<nb><<<dim3((unsigned)batch_grid(row_blocks, groups)), dim3(kBlock), (size_t)nb * d.H * 4, st>>>(
+          b->x, B, groups, (const uint16_t*)W(ffn), (const uint16_t*)W(ffn + 1), (int)d.I, (int)d.H, b->act);
     }
     ws64(st, b->act, B, W(ffn + 2), d.H, d.I, b->attn, b->h, mx ? b : nullptr);
     base += layer_tensors(c, l);
