@@ -427,15 +427,25 @@ __global__ __launch_bounds__(kBlock) void k_bgate(
 // ------------------------------------------------------------- expert down
 
 constexpr int kBDownRows = 8;    // output rows per block
-constexpr int kBDownTokens = 4;  // tokens per block
+constexpr int kBDownTokens = 2;  // tokens per block
 
-// Block (row block, token group): 32 groups of 8 lanes, group g = output row
-// row0 + (g & 7) of token t0 + (g >> 3). Lane q of a group runs reference
-// lanes 4q..4q+3 of the S32: quads q, q + 8, ... of the token's concatenated
-// routed row (slot order; expert ids[slot]'s row) and of the shared row,
-// then out = bf16(bf16(routed + residual) (+) bf16(shared)) (k_moe_down's
-// order). The group's tokens' activations are staged in LDS. Requires
-// inter % 64 == 0, inter <= 512 and shared_inter % 64 == 0.
+// Block (row block, token group): 16 groups of 16 lanes, group g = output
+// row row0 + (g & 7) of token t0 + (g >> 3). Lane q of a group runs
+// reference lanes 2q and 2q + 1 of the S32: the pair words 32j + 2q and
+// 32j + 2q + 1 (one 8-byte read) of the token's concatenated routed row
+// (slot order; expert ids[slot]'s row, 8 reads per slot) and of the shared
+// row, each reference lane's chain in j order, then the halving tree
+// (partners 16, 8, 4, 2 lanes away across lanes, 1 inside the lane) and
+// out = bf16(bf16(routed + residual) (+) bf16(shared)) (k_moe_down's
+// order). Two slots' rows in flight while one is summed. The group's
+// tokens' activations are staged in LDS. Requires inter % 64 == 0,
+// inter <= 512 and shared_inter % 64 == 0, shared_inter <= 512.
+__device__ __forceinline__ void pair2_acc(float (&lo)[2], float (&hi)[2], uint2 x, uint2 w) {
+  lo[0] += lo2f(x.x) * lo2f(w.x);
+  hi[0] += hi2f(x.x) * hi2f(w.x);
+  lo[1] += lo2f(x.y) * lo2f(w.y);
+  hi[1] += hi2f(x.y) * hi2f(w.y);
+}
 __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ act, int tokens,
                                                   const uint16_t* __restrict__ down,
                                                   const uint16_t* __restrict__ sdown, const int* __restrict__ ids,
@@ -445,7 +455,7 @@ __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ a
   __shared__ int sids[kBDownTokens * 16];
   const int iq = inter >> 3, sq = shared_inter >> 3, rq = top_k * iq, per_row = rq + sq;
   const int lane = threadIdx.x & 63, tid = threadIdx.x;
-  const int g = tid >> 3, q = lane & 7;
+  const int g = tid >> 4, q = lane & 15;
   const int t0 = blockIdx.y * kBDownTokens;
   const int row = blockIdx.x * kBDownRows + (g & (kBDownRows - 1));
   const int ti = g / kBDownRows;
@@ -460,62 +470,57 @@ __global__ __launch_bounds__(kBlock) void k_bdown(const uint16_t* __restrict__ a
   // the tokens' expert ids before any weight load: a weight address that
   // waited on an id load would wait for every load in flight
   if (tid < ntok * top_k) sids[tid] = ids[(size_t)t0 * top_k + tid];
-  Quad r, sh;
-  quad_zero(r);
-  quad_zero(sh);
-  // the shared row first (its loads overlap the staging)
-  const uint16_t* sw = sdown + (size_t)rowc * shared_inter;
-  constexpr int NS = 8;
-  u32x4 swv[NS];
+  float r_lo[2] = {0.0f, 0.0f}, r_hi[2] = {0.0f, 0.0f}, s_lo[2] = {0.0f, 0.0f}, s_hi[2] = {0.0f, 0.0f};
+  // the shared row first (its loads overlap the staging): pairs 32j + 2q
+  constexpr int NS = 8, NW = 8;  // 8-byte reads per lane per row (<= 512 wide)
+  const uint2* sw = reinterpret_cast<const uint2*>(sdown + (size_t)rowc * shared_inter);
+  const int sn = shared_inter >> 6, wn = inter >> 6;  // reads per lane
+  uint2 swv[NS];
 #pragma unroll
-  for (int j = 0; j < NS; ++j) swv[j] = ldq(sw, min(q + 8 * j, sq - 1));
+  for (int j = 0; j < NS; ++j) swv[j] = sw[min(q + 16 * j, 16 * sn - 1)];
   __syncthreads();
-  const u32x4* xr = as + (size_t)ti * per_row;
+  const uint2* xr = reinterpret_cast<const uint2*>(as + (size_t)ti * per_row);
   const int* tid_ids = sids + (tc - t0) * top_k;
-  // slot k + 1's rows are loaded while slot k's are summed (unconditional,
-  // clamped loads, so each wait drains only the slot it needs); a slot
-  // covers iq / 8 <= NW quads per lane
-  constexpr int NW = 8;
   auto slot_row = [&](int k) {
-    return down + ((size_t)tid_ids[min(k, top_k - 1)] * hidden + rowc) * inter;
+    return reinterpret_cast<const uint2*>(down + ((size_t)tid_ids[min(k, top_k - 1)] * hidden + rowc) * inter);
   };
-  u32x4 wa[NW], wb[NW];
+  uint2 wa[NW], wb[NW];
   {
-    const uint16_t* wr = slot_row(0);
+    const uint2* wr = slot_row(0);
 #pragma unroll
-    for (int j = 0; j < NW; ++j) wa[j] = ldq(wr, min(q + 8 * j, iq - 1));
+    for (int j = 0; j < NW; ++j) wa[j] = wr[min(q + 16 * j, 16 * wn - 1)];
   }
   for (int k = 0; k < top_k; k += 2) {
     {
-      const uint16_t* wr = slot_row(k + 1);
+      const uint2* wr = slot_row(k + 1);
 #pragma unroll
-      for (int j = 0; j < NW; ++j) wb[j] = ldq(wr, min(q + 8 * j, iq - 1));
+      for (int j = 0; j < NW; ++j) wb[j] = wr[min(q + 16 * j, 16 * wn - 1)];
     }
 #pragma unroll
     for (int j = 0; j < NW; ++j)
-      if (j < iq / 8) quad_acc(r, xr[k * iq + q + 8 * j], wa[j]);
+      if (j < wn) pair2_acc(r_lo, r_hi, xr[k * (iq * 2) + q + 16 * j], wa[j]);
     {
-      const uint16_t* wr = slot_row(k + 2);
+      const uint2* wr = slot_row(k + 2);
 #pragma unroll
-      for (int j = 0; j < NW; ++j) wa[j] = ldq(wr, min(q + 8 * j, iq - 1));
+      for (int j = 0; j < NW; ++j) wa[j] = wr[min(q + 16 * j, 16 * wn - 1)];
     }
     if (k + 1 < top_k) {
 #pragma unroll
       for (int j = 0; j < NW; ++j)
-        if (j < iq / 8) quad_acc(r, xr[(k + 1) * iq + q + 8 * j], wb[j]);
+        if (j < wn) pair2_acc(r_lo, r_hi, xr[(k + 1) * (iq * 2) + q + 16 * j], wb[j]);
     }
   }
-  for (int j0 = 0; j0 < sq / 8; j0 += NS) {
-    if (j0 > 0) {
 #pragma unroll
-      for (int j = 0; j < NS; ++j) swv[j] = ldq(sw, min(q + 8 * (j0 + j), sq - 1));
-    }
-#pragma unroll
-    for (int j = 0; j < NS; ++j)
-      if (j0 + j < sq / 8) quad_acc(sh, xr[rq + q + 8 * (j0 + j)], swv[j]);
-  }
-  const float rv = quad_tree<8>(r);
-  const float sv = quad_tree<8>(sh);
+  for (int j = 0; j < NS; ++j)
+    if (j < sn) pair2_acc(s_lo, s_hi, xr[rq * 2 + q + 16 * j], swv[j]);
+  // halving tree over the 32 reference lanes (2 per physical lane)
+  float r0 = r_lo[0] + r_hi[0], r1 = r_lo[1] + r_hi[1];
+  float h0 = s_lo[0] + s_hi[0], h1 = s_lo[1] + s_hi[1];
+  r0 += lane_down<8>(r0), r1 += lane_down<8>(r1), h0 += lane_down<8>(h0), h1 += lane_down<8>(h1);
+  r0 += lane_down<4>(r0), r1 += lane_down<4>(r1), h0 += lane_down<4>(h0), h1 += lane_down<4>(h1);
+  r0 += lane_down<2>(r0), r1 += lane_down<2>(r1), h0 += lane_down<2>(h0), h1 += lane_down<2>(h1);
+  r0 += lane_down<1>(r0), r1 += lane_down<1>(r1), h0 += lane_down<1>(h0), h1 += lane_down<1>(h1);
+  const float rv = r0 + r1, sv = h0 + h1;
   if (q == 0 && live) {
     const size_t o = (size_t)t * hidden + row;
     out[o] = bf_add(f2bf(rv + bf2f(residual[o])), f2bf(sv));

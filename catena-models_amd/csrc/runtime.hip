@@ -2510,12 +2510,13 @@ int step_batch_shared(cq35_session* const* sessions, const uint64_t* tokens, con
 }
 
 // Whether the MoE shape fits the batched MoE kernels: a hidden width the
-// router is instantiated for (staged once by k_ws256 and k_broute), expert widths in whole 64-element
-// lane rounds (k_bdown), the head dim within one flash block, 1, 2, 4 or 8
-// query heads per KV head and at most 16 experts selected per token.
+// router is instantiated for (staged once by k_ws256 and k_broute), expert
+// and shared-expert widths in whole 64-element lane rounds of at most 512
+// (k_bdown), the head dim within one flash block, 1, 2, 4 or 8 query heads
+// per KV head and at most 16 experts selected per token.
 bool moe_batch_shape_ok(const cq35_model* m) {
   const Dims& d = m->d;
-  return (d.H == 2048 || d.H == 1024 || d.H == 512 || d.H == 256) && d.I % 64 == 0 && d.I <= 512 && d.E <= 512 && d.SI % 64 == 0 && d.HD <= 256 &&
+  return (d.H == 2048 || d.H == 1024 || d.H == 512 || d.H == 256) && d.I % 64 == 0 && d.I <= 512 && d.E <= 512 && d.SI % 64 == 0 && d.SI <= 512 && d.HD <= 256 &&
          (d.Q / d.KVH == 1 || d.Q / d.KVH == 2 || d.Q / d.KVH == 4 || d.Q / d.KVH == 8) && d.K <= 16 && d.E <= 4096;
 }
 
