@@ -209,8 +209,9 @@ __device__ __forceinline__ uint32_t umax_lane(uint32_t v) {
 // Top-k of one token per wave (moe.hex:86-252): without NaN logits, k rounds
 // of a wave-wide maximum of the images (DPP) and the lowest expert index
 // holding it (ballots), which is the stable descending rank; with NaNs the
-// rank formula rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)} (an
-// unassigned rank k keeps expert k), as k_router_select does. Then
+// rank formula rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)} (the
+// largest index of a shared rank takes it, an unassigned rank k keeps
+// expert k), as k_router_select does. Then
 // p_j = exp(l_j - l_0) / den with den summed left to right from 0. The ids
 // also go to row `layer` of the session's export buffer, and each
 // (token, slot) with its weight to its expert's list for the gate/up
@@ -269,7 +270,9 @@ __global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ lo
       if (lane == 0) sid[wave][k] = e;
     }
   } else {
-    if (lane < top_k) sid[wave][lane] = lane;
+    // colliding ranks: the largest expert index takes the rank (an LDS
+    // maximum), an unassigned rank k keeps expert k
+    if (lane < top_k) sid[wave][lane] = -1;
     for (int e = lane; e < experts; e += 64) {
       const float le = lg[e];
       int rank = 0;
@@ -277,8 +280,9 @@ __global__ __launch_bounds__(kBlock) void k_sselect(const float* __restrict__ lo
         const float o = lg[i];
         rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
       }
-      if (rank < top_k) sid[wave][rank] = e;
+      if (rank < top_k) atomicMax(&sid[wave][rank], e);
     }
+    if (lane < top_k && sid[wave][lane] < 0) sid[wave][lane] = lane;
   }
   const int e = lane < top_k ? sid[wave][lane] : 0;
   const float lj = lane < top_k ? lg[e] : 0.0f;

@@ -625,12 +625,11 @@ __global__ __launch_bounds__(kBlock) void k_router_select(
     }
   } else {
     // rank(e) = #{i : l_i > l_e} + #{i < e : !(l_e > l_i)}. With NaNs two
-    // experts can share a rank and leave another unassigned: an unassigned
-    // rank k keeps expert k, as in the batched select and the restatement.
-    if (threadIdx.x < top_k) {
-      ids[threadIdx.x] = threadIdx.x;
-      chosen[threadIdx.x] = lg[threadIdx.x];
-    }
+    // experts can share a rank and leave another unassigned: the largest
+    // expert index of a shared rank takes it (the restatement's ascending
+    // scatter; an LDS maximum), an unassigned rank k keeps expert k.
+    __shared__ int won[64];
+    if (threadIdx.x < top_k) won[threadIdx.x] = -1;
     __syncthreads();
     for (int e = threadIdx.x; e < experts; e += blockDim.x) {
       const float le = lg[e];
@@ -639,10 +638,13 @@ __global__ __launch_bounds__(kBlock) void k_router_select(
         const float o = lg[i];
         rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
       }
-      if (rank < top_k) {
-        ids[rank] = e;
-        chosen[rank] = le;
-      }
+      if (rank < top_k) atomicMax(&won[rank], e);
+    }
+    __syncthreads();
+    if (threadIdx.x < top_k) {
+      const int e = won[threadIdx.x] >= 0 ? won[threadIdx.x] : threadIdx.x;
+      ids[threadIdx.x] = e;
+      chosen[threadIdx.x] = lg[e];
     }
   }
   __syncthreads();

@@ -1067,11 +1067,10 @@ __device__ __forceinline__ void select_experts(const Mega& m) {
   __syncthreads();
   if (s->any_nan) {
     // NaNs can make two experts share a rank and leave another unassigned:
-    // an unassigned rank k keeps expert k (as the batched select does)
-    if (m.tid < S::K) {
-      s->ids[m.tid] = m.tid;
-      s->chosen[m.tid] = s->logits[m.tid];
-    }
+    // the largest expert index of a shared rank takes it (the restatement's
+    // ascending scatter, deterministic here through an LDS maximum), and an
+    // unassigned rank k keeps expert k (as the batched select does)
+    if (m.tid < S::K) s->ids[m.tid] = -1;
     __syncthreads();
     for (int e = m.tid; e < S::E; e += kMT) {
       const float le = s->logits[e];
@@ -1080,10 +1079,13 @@ __device__ __forceinline__ void select_experts(const Mega& m) {
         const float o = s->logits[i];
         rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
       }
-      if (rank < S::K) {
-        s->ids[rank] = e;
-        s->chosen[rank] = le;
-      }
+      if (rank < S::K) atomicMax(&s->ids[rank], e);
+    }
+    __syncthreads();
+    if (m.tid < S::K) {
+      const int e = s->ids[m.tid] >= 0 ? s->ids[m.tid] : m.tid;
+      s->ids[m.tid] = e;
+      s->chosen[m.tid] = s->logits[e];
     }
     __syncthreads();
     if (m.wave == 0) {

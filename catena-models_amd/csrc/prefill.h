@@ -472,12 +472,12 @@ __global__ __launch_bounds__(kBlock) void k_bselect(const float* __restrict__ lo
   const int t = blockIdx.x;
   const float* lt = logits + (size_t)t * (experts + 1);
   for (int e = threadIdx.x; e < experts; e += blockDim.x) bs_lg[e] = lt[e];
-  // Every slot gets a valid expert even if NaN logits make ranks collide;
-  // without NaNs the ranks are a permutation and overwrite all of these.
-  if (threadIdx.x < top_k) {
-    ids[(size_t)t * top_k + threadIdx.x] = threadIdx.x;
-    chosen[threadIdx.x] = lt[threadIdx.x];
-  }
+  // NaN logits can make ranks collide: the largest expert index of a shared
+  // rank takes it (the restatement's ascending scatter; an LDS maximum) and
+  // an unassigned rank k keeps expert k; without NaNs the ranks are a
+  // permutation.
+  __shared__ int won[64];
+  if (threadIdx.x < top_k) won[threadIdx.x] = -1;
   __syncthreads();
   for (int e = threadIdx.x; e < experts; e += blockDim.x) {
     const float le = bs_lg[e];
@@ -486,10 +486,13 @@ __global__ __launch_bounds__(kBlock) void k_bselect(const float* __restrict__ lo
       const float o = bs_lg[i];
       rank += (o > le) ? 1 : ((i < e && !(le > o)) ? 1 : 0);
     }
-    if (rank < top_k) {
-      ids[(size_t)t * top_k + rank] = e;
-      chosen[rank] = le;
-    }
+    if (rank < top_k) atomicMax(&won[rank], e);
+  }
+  __syncthreads();
+  if (threadIdx.x < top_k) {
+    const int e = won[threadIdx.x] >= 0 ? won[threadIdx.x] : threadIdx.x;
+    ids[(size_t)t * top_k + threadIdx.x] = e;
+    chosen[threadIdx.x] = bs_lg[e];
   }
   __syncthreads();
   if (threadIdx.x < 64) {

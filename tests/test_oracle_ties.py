@@ -118,3 +118,23 @@ def test_argmax_takes_the_first_index(oracle, vocab):
     with oracle.planted("argmax_last"):
         missed = sum(oracle.argmax(bits) != first for bits, first in cases)
     assert missed == len(cases), f"last-index control caught in only {missed} of {len(cases)} cases"
+
+
+def test_selection_with_nan_logits(oracle):
+    """NaN logits under the reference's rank formula (qwen35_moe.hex:86-111):
+    comparisons with NaN are false, so NaN counts among the lower indices of
+    every expert (equal-or-unordered) and never as larger. For logits
+    [3, NaN, 5, 1] the ranks are 1, 1, 1, 3 (worked by hand: e0 has e2
+    above it; e1 has e0 below and unordered; e2 has e1 below and unordered;
+    e3 has e0 and e2 above and e1 below and unordered). With k = 2: rank 0 is
+    unassigned and keeps expert 0; rank 1 is shared by experts 0, 1 and 2
+    and the largest index, 2, takes it (the ascending scatter). The weights
+    are the softmax over the selected logits 3 and 5."""
+    ids, probs = oracle.select(np.array([3.0, np.nan, 5.0, 1.0], dtype=np.float32), 2)
+    assert ids.tolist() == [0, 2]
+    e = np.exp(np.float64(2.0))
+    assert abs(float(probs[0]) - 1.0 / (1.0 + e)) <= 2e-7
+    assert abs(float(probs[1]) - e / (1.0 + e)) <= 2e-7
+    # a NaN above every selected expert leaves the finite order untouched
+    ids, _ = oracle.select(np.array([4.0, 2.0, 9.0, np.nan], dtype=np.float32), 2)
+    assert ids.tolist() == [2, 0]
