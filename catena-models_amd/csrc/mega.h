@@ -569,11 +569,20 @@ struct ProjRegs {
   u32x4 w[kPairsA][2][S::NQA];
 };
 
+// Row pairs of the projection phase: every row of a full layer; of a
+// linear layer the q | k | v rows only (the z rows, needed only by the gated
+// norm at the end of the delta phase, are computed during that phase by the
+// blocks that have no value head: project_z).
+template <class S>
+__device__ __forceinline__ int project_pairs(const CQ35_CONST MegaLayer& Ly) {
+  return Ly.full ? (Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3]) >> 1 : S::QKV / 2;
+}
+
 template <class S, int K0, int K1>
 __device__ __forceinline__ void issue_project(const MegaArgs* pa, const MegaLayer* ly, ProjRegs<S>& r) {
   const Mega m = make_mega(pa, 0);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
-  const int pairs = (Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3]) >> 1;
+  const int pairs = project_pairs<S>(Ly);
 #pragma unroll
   for (int k = K0; k < K1; ++k) {
     const int p = m.gw + m.nw * k;
@@ -602,7 +611,7 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   constexpr int NQ = S::NQA;
-  const int pairs = (Ly.seg_rows[0] + Ly.seg_rows[1] + Ly.seg_rows[2] + Ly.seg_rows[3]) >> 1;
+  const int pairs = project_pairs<S>(Ly);
   f32x4 w0, w1;
   norm_weights<S>(m, Ly.in_norm, w0, w1);
   load_hidden<S>(m, Ly.x_h, m.xr, l == 0);
@@ -659,13 +668,69 @@ struct DeltaLds {
 };
 static_assert(sizeof(DeltaLds) <= kLdsBigBytes, "delta LDS");
 
+// The z rows of a linear layer's grouped projection (rows QKV .. QKV + VS,
+// pair words QKV/2 + zp), on the blocks that have no value head, while the
+// value-head blocks run the delta step: the same S256 rows and words as the
+// projection phase (group_projection.hex:3-97), over the normalised row the
+// block still holds from that phase. Worker wave w takes pairs w, w + W, ...
+template <class S>
+__device__ __forceinline__ void project_z(const Mega& m, const CQ35_CONST MegaLayer& Ly) {
+  constexpr int ZP = S::VS / 2, NQ = S::NQA;
+  const int workers = (m.grid - S::VH) * kMW;
+  const int w0 = (m.bid - S::VH) * kMW + m.wave;
+  float xl[NQ][4], xh[NQ][4];
+  bool unpacked = false;
+  for (int z0 = w0; z0 < ZP; z0 += 2 * workers) {
+    // two pairs' rows in flight
+    u32x4 wv[2][2][NQ];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int zp = min(z0 + k * workers, ZP - 1);
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const uint16_t* w = seg_row(Ly, S::QKV + 2 * zp + rr, S::H);
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) wv[k][rr][j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
+      }
+    }
+    if (!unpacked) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const u32x4 xq = (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) ? m.xn[m.lane + 64 * j] : u32x4{0u, 0u, 0u, 0u};
+        quad_unpack(xq, xl[j], xh[j]);
+      }
+      unpacked = true;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int zp = z0 + k * workers;
+      if (zp < ZP) {
+        float v[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          Quad acc;
+          quad_zero(acc);
+#pragma unroll
+          for (int j = 0; j < NQ; ++j)
+            if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc, xl[j], xh[j], wv[k][rr][j]);
+          v[rr] = quad_tree<64>(acc);
+        }
+        if (m.lane == 0) word_store(Ly.x_proj + S::QKV / 2 + zp, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
+      }
+    }
+  }
+}
+
 template <class S>
 __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, const MegaLayer* ly) {
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   const CQ35_CONST MegaArgs& a = m.a;
   const int h = m.bid;
-  if (h >= S::VH) return;  // uniform per block
+  if (h >= S::VH) {  // uniform per block
+    if constexpr (!S::kDense) project_z<S>(m, Ly);
+    return;
+  }
   constexpr int KD = S::KD, VD = S::VD, NCH = 2 * KD + VD;
   constexpr int KJ = KD / 32, CPP = kMT / 8, PASSES = (VD + CPP - 1) / CPP;
   static_assert(NCH <= kMT, "delta shape");
@@ -710,10 +775,11 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
 #pragma unroll
     for (int j = 0; j < S::NQA; ++j) abw[j] = ldq_at(w, (uint32_t)min(m.lane + 64 * j, S::QH - 1) * 16u);
   }
-  // inputs: q | k | v of this head, z (projection words)
+  // inputs: q | k | v of this head, z (projection words; MoE shapes: z is
+  // polled before the gated norm, its rows being computed meanwhile)
   constexpr int qw = KD / 2, vw = VD / 2;
   constexpr int zbase = S::QKV;
-  constexpr int nwords = 2 * qw + 2 * vw + (S::kDense ? 2 : 0);
+  constexpr int nwords = 2 * qw + vw + (S::kDense ? vw + 2 : 0);
   const uint64_t* proj = Ly.x_proj;
   auto addr = [&](int i) -> const uint64_t* {
     if (i < qw) return proj + ((kh * KD) >> 1) + i;
@@ -723,6 +789,7 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
     // dense: the words holding alpha row QKV + VS + h and beta row QKV + VS + VH + h
     return proj + ((S::QKV + S::VS + (i - 2 * qw - 2 * vw) * S::VH + h) >> 1);
   };
+  static_assert(S::kDense || nwords == 2 * qw + vw, "z words polled later");
   poll_words<(nwords + kMT - 1) / kMT>(m, nwords, addr, m.vec);
   if constexpr (S::kDense) {
     static_assert(S::VH % 2 == 0, "alpha and beta rows share a word's parity");
@@ -842,6 +909,10 @@ __device__ __forceinline__ void phase_delta(const MegaArgs* pa, uint32_t tag, co
   }
   __syncthreads();
   trace_mark(kMarkDeltaState);
+  if constexpr (!S::kDense) {
+    // the head's z words (computed by the blocks without a value head)
+    if (m.tid < vw) m.vec[2 * qw + vw + m.tid] = poll_one(m, addr(2 * qw + vw + m.tid));
+  }
   // gated RMSNorm with a serial sum (cooperative_norm.hex:139-182)
   if (m.tid < VD) {
     const float v = bf2f(d->core[m.tid]);
