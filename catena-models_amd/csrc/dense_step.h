@@ -55,8 +55,8 @@ using ShapeDenseTiny = DenseShape<256, 4096, 4, 1, 64, 16, 4, 32, 8, 32, 768>;
 
 // Normalised input row x the layer's projection segments in S32 order: 8
 // lanes per row (physical lane q holds reference lanes 4q..4q+3 and visits
-// quads q, q + 8, ...), 8 rows per wave per round, row 8(gw + nw k) + g for
-// lane group g; the group's tree (quad_tree<8>), rows 2p and 2p+1 packed into
+// quads q, q + 8, ...), 8 rows per wave per round, row 8(gs + nw k) + g for
+// lane group g (gs: waves interleaved across blocks); the group's tree (quad_tree<8>), rows 2p and 2p+1 packed into
 // one word by the even group. The round's weights are issued before the
 // input row is polled.
 template <class S>
@@ -70,7 +70,7 @@ __device__ __forceinline__ void phase_project32(const MegaArgs* pa, uint32_t tag
   const int rounds = (rows + 8 * m.nw - 1) / (8 * m.nw);
   u32x4 wv[NQ];
   auto issue = [&](int k) {
-    const int row = min(8 * (m.gw + m.nw * k) + g, rows - 1);
+    const int row = min(8 * (m.gs + m.nw * k) + g, rows - 1);
     const uint16_t* w = seg_row(Ly, row, S::H);
 #pragma unroll
     for (int j = 0; j < NQ; ++j) wv[j] = ldq_at(w, (uint32_t)(q + 8 * j) * 16u);
@@ -84,7 +84,7 @@ __device__ __forceinline__ void phase_project32(const MegaArgs* pa, uint32_t tag
 #pragma unroll 1
   for (int k = 0; k < rounds; ++k) {
     if (k > 0) issue(k);
-    const int row = 8 * (m.gw + m.nw * k) + g;
+    const int row = 8 * (m.gs + m.nw * k) + g;
     Quad acc;
     quad_zero(acc);
 #pragma unroll
@@ -394,8 +394,9 @@ __device__ __forceinline__ void phase_dense_attend(const MegaArgs* pa, uint32_t 
 // -------------------------------------------------- phase: SwiGLU gate/up
 
 // Every block normalises the post-mixer row (post_attention_norm) into m.xn
-// and keeps the raw row in m.xa for the down projection's residual. Wave gw
-// takes rows gw + nw k (k < kDenseFfnRows): gate and up rows in S256 order
+// and keeps the raw row in m.xa for the down projection's residual. Wave
+// slot gp takes rows gp + nw k (k < kDenseFfnRows; wave pairs interleaved
+// across blocks): gate and up rows in S256 order
 // (64 lanes, quads lane + 64 j), t = bf16(bf16(silu(bf16 g)) * bf16 u); even
 // waves hold even rows and store the word of the pair.
 template <class S>
@@ -403,10 +404,12 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
   const Mega m = make_mega(pa, tag);
   const CQ35_CONST MegaLayer& Ly = *phase_ptr(ly);
   constexpr int NQ = S::NQA, RG = kDenseFfnRows, H = S::H, QH = S::QH;
+  // wave pairs (the two rows of an output word) interleaved across blocks
+  const int gp = (((m.wave >> 1) * m.grid + m.bid) << 1) | (m.wave & 1);
   u32x4 gv[RG][NQ], uv[RG][NQ];
 #pragma unroll
   for (int k = 0; k < RG; ++k) {
-    const int row = min(m.gw + m.nw * k, S::I - 1);
+    const int row = min(gp + m.nw * k, S::I - 1);
     const uint16_t* wg = Ly.sgate + (size_t)row * H;
     const uint16_t* wu = Ly.sup + (size_t)row * H;
 #pragma unroll
@@ -424,7 +427,7 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
   uint16_t* odd = reinterpret_cast<uint16_t*>(m.big);  // [kMW / 2][RG]
 #pragma unroll
   for (int k = 0; k < RG; ++k) {
-    const int row = m.gw + m.nw * k;
+    const int row = gp + m.nw * k;
     t[k] = 0;
     if (row < S::I) {  // uniform per wave
       Quad ga, ua;
@@ -448,7 +451,7 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
   if (m.lane == 0 && !(m.wave & 1)) {
 #pragma unroll
     for (int k = 0; k < RG; ++k) {
-      const int row = m.gw + m.nw * k;
+      const int row = gp + m.nw * k;
       if (row < S::I) word_store(Ly.x_active + (row >> 1), pack_bf(t[k], odd[(m.wave >> 1) * RG + k]), m.tag);
     }
   }

@@ -269,7 +269,11 @@ __device__ __forceinline__ const CQ35_CONST T* phase_ptr(const T* p) {
 struct Mega {
   const CQ35_CONST MegaArgs& a;
   uint32_t tag;
-  int tid, lane, wave, gw, nw, bid, grid;
+  // gw: global wave index, block-major (bid * kMW + wave); gs: the same
+  // count interleaved across blocks (wave * grid + bid), so that a phase
+  // whose last round covers only part of the waves spreads that round over
+  // every CU instead of loading the first blocks with it
+  int tid, lane, wave, gw, gs, nw, bid, grid;
   u32x4* xn;
   uint16_t* xr;
   uint16_t* xa;
@@ -291,6 +295,7 @@ __device__ __forceinline__ Mega make_mega(const MegaArgs* pa, uint32_t tag) {
   const int grid = __builtin_amdgcn_readfirstlane(mm->grid);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gw = bid * kMW + wave;
+  const int gs = wave * grid + bid;
   const int nw = grid * kMW;
   return Mega{*a,
               tag,
@@ -298,6 +303,7 @@ __device__ __forceinline__ Mega make_mega(const MegaArgs* pa, uint32_t tag) {
               tid & 63,
               wave,
               gw,
+              gs,
               nw,
               bid,
               grid,
@@ -585,7 +591,7 @@ __device__ __forceinline__ void issue_project(const MegaArgs* pa, const MegaLaye
   const int pairs = project_pairs<S>(Ly);
 #pragma unroll
   for (int k = K0; k < K1; ++k) {
-    const int p = m.gw + m.nw * k;
+    const int p = m.gs + m.nw * k;
     if (p < pairs) {
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
@@ -626,7 +632,7 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
   }
 #pragma unroll
   for (int k = 0; k < kPairsA; ++k) {
-    const int p = m.gw + m.nw * k;
+    const int p = m.gs + m.nw * k;
     if (p < pairs) {
       float v[2];
 #pragma unroll
@@ -672,12 +678,13 @@ static_assert(sizeof(DeltaLds) <= kLdsBigBytes, "delta LDS");
 // pair words QKV/2 + zp), on the blocks that have no value head, while the
 // value-head blocks run the delta step: the same S256 rows and words as the
 // projection phase (group_projection.hex:3-97), over the normalised row the
-// block still holds from that phase. Worker wave w takes pairs w, w + W, ...
+// block still holds from that phase. Worker w (interleaved across the
+// worker blocks) takes pairs w, w + W, ...
 template <class S>
 __device__ __forceinline__ void project_z(const Mega& m, const CQ35_CONST MegaLayer& Ly) {
   constexpr int ZP = S::VS / 2, NQ = S::NQA;
   const int workers = (m.grid - S::VH) * kMW;
-  const int w0 = (m.bid - S::VH) * kMW + m.wave;
+  const int w0 = m.wave * (m.grid - S::VH) + (m.bid - S::VH);
   float xl[NQ][4], xh[NQ][4];
   bool unpacked = false;
   for (int z0 = w0; z0 < ZP; z0 += 2 * workers) {
@@ -2408,16 +2415,16 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
   constexpr int H = S::H, V = S::V, PER_LANE = (S::QH + 7) / 8;
   constexpr int PIECE = PER_LANE < 8 ? PER_LANE : 8, PIECES = (PER_LANE + PIECE - 1) / PIECE;
   static_assert(PIECES * PIECE == PER_LANE && S::QH % 8 == 0, "vocabulary pieces");
-  constexpr int GROUPS = V / 8;  // 8-row groups; group gw + nw*b is this wave's batch b
+  constexpr int GROUPS = V / 8;  // 8-row groups; group gs + nw*b is this wave's batch b
   const int q = m.lane & 7, g = m.lane >> 3;
-  const int nbatches = m.gw < GROUPS ? (GROUPS - 1 - m.gw) / m.nw + 1 : 0;
+  const int nbatches = m.gs < GROUPS ? (GROUPS - 1 - m.gs) / m.nw + 1 : 0;
   const int steps = nbatches * PIECES;
   const uint32_t lane_off = (uint32_t)g * (uint32_t)H * 2u + (uint32_t)q * 16u;
   // piece t = (batch t / PIECES, piece t % PIECES); the group base address is
   // uniform, quad q + 8(pc*PIECE + j) of the lane's row is at byte 16q + 128(pc*PIECE + j)
   auto load_piece = [&](u32x4* buf, int t) {
     const int b = t / PIECES, pc = t - b * PIECES;
-    const int grp = steps > 0 ? m.gw + m.nw * b : 0;  // a wave without groups reads group 0 (unused)
+    const int grp = steps > 0 ? m.gs + m.nw * b : 0;  // a wave without groups reads group 0 (unused)
     const uint16_t* w = a.head + (size_t)(grp * 8) * H + pc * PIECE * 64;
 #pragma unroll
     for (int j = 0; j < PIECE; ++j) buf[j] = ldq_at(w, lane_off + (uint32_t)j * 128u);
@@ -2442,7 +2449,7 @@ __device__ __forceinline__ void phase_head(const MegaArgs* pa, uint32_t tag) {
     if (pc == PIECES - 1) {
       const float v = quad_tree<8>(acc);
       quad_zero(acc);
-      const int row = (m.gw + m.nw * b) * 8 + g;
+      const int row = (m.gs + m.nw * b) * 8 + g;
       if (q == 0) {
         const uint16_t bb = f2bf(v);
         G(a.logits)[row] = bb;
