@@ -75,10 +75,11 @@ def phase_bytes(cfg: dict, keys: int) -> dict:
             ("gate/up",): 2 * I * H * 2,
             ("down",): I * H * 2,
         }
+    # MoE step: a linear layer's z rows are computed during the delta phase
     return {
-        ("lin", "project"): (d["qkv"] + d["value_size"] + 2 * VH) * H * 2,
+        ("lin", "project"): (d["qkv"] + 2 * VH) * H * 2,
         ("full", "project"): (2 * d["query_size"] + 2 * d["kvs"]) * H * 2,
-        ("lin", "delta"): 2 * VH * VD * KD * 2 + 4 * d["qkv"] * 2,
+        ("lin", "delta"): 2 * VH * VD * KD * 2 + 4 * d["qkv"] * 2 + d["value_size"] * H * 2,
         ("full", "scores"): keys * d["kvs"] * 2,
         ("full", "values"): keys * d["kvs"] * 2,
         ("lin", "outproj"): H * d["value_size"] * 2,
