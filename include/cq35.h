@@ -179,7 +179,10 @@ int cq35_step_batch(cq35_session* const* sessions, const uint64_t* tokens, const
  * one device share that array: each holds a per-device lock from its first
  * launch until its stream has drained, so calls from several threads or
  * streams of one device run one after another. The call synchronises its
- * stream before returning, so it cannot run under HIP graph capture. */
+ * stream before returning, so it cannot run under HIP graph capture.
+ * Decode attention splits above CQ35_SPLIT_KEYS_DEFAULT cached keys, as a
+ * new session's does (there is no per-call threshold; at the capacities
+ * this call accepts the split applies above 8192 positions). */
 int cq35_step_static(const cq35_model* model, uint16_t* state, int64_t capacity, uint64_t token,
                      int64_t start, void* stream, uint64_t* next_token, uint16_t* logits);
 
