@@ -588,7 +588,8 @@ __global__ void k_numeric(int op, const float* __restrict__ in, float* __restric
       case 3: y = softplus(x); break;
       case 4: y = nsqrt(x); break;
       case 5: sincos_q(x, &s, &c); y = s; break;
-      default: sincos_q(x, &s, &c); y = c; break;
+      case 6: sincos_q(x, &s, &c); y = c; break;
+      default: y = bitsf((uint32_t)f2bf(x) << 16); break;  // the BF16 rounding, widened back
     }
     out[i] = y;
   }

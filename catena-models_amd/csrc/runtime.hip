@@ -2703,7 +2703,7 @@ extern "C" void cq35_numeric_sincos(float angle, float* sine, float* cosine) {
 }
 
 extern "C" int cq35_device_numeric(int op, const float* input, float* output, int64_t count) {
-  if (!input || !output || count < 0 || op < 0 || op > 6) return fail(CQ35_EINVAL, "bad argument");
+  if (!input || !output || count < 0 || op < 0 || op > 7) return fail(CQ35_EINVAL, "bad argument");
   if (count == 0) return CQ35_OK;
   float *din = nullptr, *dout = nullptr;
   HIP_TRY(hipMalloc(&din, count * 4));

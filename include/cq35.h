@@ -284,7 +284,8 @@ float cq35_numeric_sqrt(float x);
 float cq35_numeric_softplus(float x);
 void cq35_numeric_sincos(float angle, float* sine, float* cosine);
 /* Device evaluation of the same numerics over an array (op 0 exp, 1 silu,
- * 2 sigmoid, 3 softplus, 4 sqrt, 5 sin, 6 cos); host in/out arrays. */
+ * 2 sigmoid, 3 softplus, 4 sqrt, 5 sin, 6 cos, 7 the F32 -> BF16 rounding
+ * widened back to F32); host in/out arrays. */
 int cq35_device_numeric(int op, const float* input, float* output, int64_t count);
 /* Device split-pair GEMV with tree width W (32, 64 or 256) over a row-major
  * BF16 matrix: out[r] = bf16(tree_W(x . w_r)). Host arrays. */
