@@ -440,8 +440,8 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
           quad_acc(ga, xq, gv[k][j]);
           quad_acc(ua, xq, uv[k][j]);
         }
-      const float gsum = quad_tree<64>(ga);
-      const float usum = quad_tree<64>(ua);
+      const float tot = quad_tree64_pair(ga, ua);  // gate total in lane 0, up total in lane 32
+      const float gsum = tot, usum = lane_value(tot, 32);
       t[k] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
       if (m.lane == 0 && (m.wave & 1)) odd[(m.wave >> 1) * RG + k] = t[k];
     }

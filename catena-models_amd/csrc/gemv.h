@@ -160,6 +160,32 @@ __device__ __forceinline__ float quad_tree(const Quad& a) {
   return v0 + v1;
 }
 
+// Two quad_tree<64> totals at once: a's valid in lane 0, b's in lane 32.
+// The first level (physical stride 32) is one permlane32 swap per value: the
+// lower half receives a's upper values, the upper half b's lower ones, so
+// lanes 0-31 continue a's tree and lanes 32-63 b's; strides 16 ... 1 then
+// run in both halves at once and 2, 1 inside the lane. Every sum has
+// quad_tree<64>'s operands (the two operands of a sum commute): the same
+// bits in about half the instructions.
+__device__ __forceinline__ float quad_tree64_pair(const Quad& a, const Quad& b) {
+  float v[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int av = __builtin_bit_cast(int, a.lo[p] + a.hi[p]);
+    const int bv = __builtin_bit_cast(int, b.lo[p] + b.hi[p]);
+    const auto r = __builtin_amdgcn_permlane32_swap(av, bv, false, false);
+    v[p] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  tree_levels<64, 16>(v[0], v[1], v[2], v[3]);
+  v[0] += v[2];
+  v[1] += v[3];
+  return v[0] + v[1];
+}
+// The value lane `lane` holds, in every lane (a scalar read).
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
 __device__ __forceinline__ u32x4 ldq(const void* base, int64_t quad) {
   return reinterpret_cast<const u32x4*>(base)[quad];
 }

@@ -634,17 +634,17 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
   for (int k = 0; k < kPairsA; ++k) {
     const int p = m.gs + m.nw * k;
     if (p < pairs) {
-      float v[2];
+      Quad acc[2];
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
-        Quad acc;
-        quad_zero(acc);
+        quad_zero(acc[rr]);
 #pragma unroll
         for (int j = 0; j < NQ; ++j)
-          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc, xl[j], xh[j], r.w[k][rr][j]);
-        v[rr] = quad_tree<64>(acc);
+          if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc[rr], xl[j], xh[j], r.w[k][rr][j]);
       }
-      if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
+      const float v = quad_tree64_pair(acc[0], acc[1]);  // row 2p in lane 0, 2p + 1 in lane 32
+      const float v1 = lane_value(v, 32);
+      if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v), f2bf(v1)), m.tag);
     }
   }
 }
@@ -712,17 +712,17 @@ __device__ __forceinline__ void project_z(const Mega& m, const CQ35_CONST MegaLa
     for (int k = 0; k < 2; ++k) {
       const int zp = z0 + k * workers;
       if (zp < ZP) {
-        float v[2];
+        Quad acc[2];
 #pragma unroll
         for (int rr = 0; rr < 2; ++rr) {
-          Quad acc;
-          quad_zero(acc);
+          quad_zero(acc[rr]);
 #pragma unroll
           for (int j = 0; j < NQ; ++j)
-            if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc, xl[j], xh[j], wv[k][rr][j]);
-          v[rr] = quad_tree<64>(acc);
+            if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc[rr], xl[j], xh[j], wv[k][rr][j]);
         }
-        if (m.lane == 0) word_store(Ly.x_proj + S::QKV / 2 + zp, pack_bf(f2bf(v[0]), f2bf(v[1])), m.tag);
+        const float v = quad_tree64_pair(acc[0], acc[1]);
+        const float v1 = lane_value(v, 32);
+        if (m.lane == 0) word_store(Ly.x_proj + S::QKV / 2 + zp, pack_bf(f2bf(v), f2bf(v1)), m.tag);
       }
     }
   }
@@ -1277,7 +1277,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
           quad_acc_f(ga, xl[j], xh[j], gv[r][j]);
           quad_acc_f(ua, xl[j], xh[j], uv[r][j]);
         }
-      const float gb = rbf(quad_tree<64>(ga)), ub = rbf(quad_tree<64>(ua));
+      const float t = quad_tree64_pair(ga, ua);  // gate total in lane 0, up total in lane 32
+      const float gb = rbf(t), ub = rbf(lane_value(t, 32));
       y[r] = f2bf((silu(gb) * ub) * m.misc->probs[(2 * p + r) / S::I]);
     }
     if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
