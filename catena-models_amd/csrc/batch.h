@@ -268,8 +268,8 @@ __global__ __launch_bounds__(kBlock) void k_ws256_swiglu(const uint16_t* __restr
     const int row = row0 + r;
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      const float gsum = quad_tree<64>(ga[t]);
-      const float usum = quad_tree<64>(ua[t]);
+      const float tot = quad_tree64_pair(ga[t], ua[t]);  // gate total in lane 0, up total in lane 32
+      const float gsum = tot, usum = lane_value(tot, 32);
       if (lane == 0 && row < rows && t0 + t < tokens)
         act[(size_t)(t0 + t) * rows + row] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
     }

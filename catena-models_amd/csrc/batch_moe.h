@@ -86,10 +86,15 @@ __global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x
     int local;
     const int s = segment_of(seg, min(row, total - 1), &local);
     const int srows = s == 0 ? seg.rows[0] : s == 1 ? seg.rows[1] : s == 2 ? seg.rows[2] : seg.rows[3];
+    static_assert(NB % 2 == 0, "token trees in pairs");
 #pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      const float v = quad_tree<64>(acc[t]);
-      if (lane == 0 && row < total && t0 + t < tokens) segment_out(seg, s)[(size_t)(t0 + t) * srows + local] = f2bf(v);
+    for (int t = 0; t < NB; t += 2) {
+      const float tot = quad_tree64_pair(acc[t], acc[t + 1]);  // token t in lane 0, t + 1 in lane 32
+      const float v1 = lane_value(tot, 32);
+      if (lane == 0 && row < total) {
+        if (t0 + t < tokens) segment_out(seg, s)[(size_t)(t0 + t) * srows + local] = f2bf(tot);
+        if (t0 + t + 1 < tokens) segment_out(seg, s)[(size_t)(t0 + t + 1) * srows + local] = f2bf(v1);
+      }
     }
   }
 }
