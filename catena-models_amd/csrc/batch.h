@@ -248,6 +248,11 @@ __global__ __launch_bounds__(kBlock) void k_ws256_swiglu(const uint16_t* __restr
     }
   }
   stage_f32<NB>(xf, x, tokens, t0, cols, 0, cols);
+  // each (row, token) total pair, wave-uniform; the epilogues run afterwards
+  // one per lane (item i = r * NB + t on lane i) instead of once per item
+  constexpr int NI = RW * NB;
+  static_assert(NI <= 64, "epilogue lanes");
+  float gs[NI], us[NI];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
     Quad ga[NB], ua[NB];
@@ -265,15 +270,24 @@ __global__ __launch_bounds__(kBlock) void k_ws256_swiglu(const uint16_t* __restr
           quad_acc_staged(ua[t], xf + t * cols, quads, lane + 64 * j, uv[r][j]);
         }
       }
-    const int row = row0 + r;
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
       const float tot = quad_tree64_pair(ga[t], ua[t]);  // gate total in lane 0, up total in lane 32
-      const float gsum = tot, usum = lane_value(tot, 32);
-      if (lane == 0 && row < rows && t0 + t < tokens)
-        act[(size_t)(t0 + t) * rows + row] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
+      gs[r * NB + t] = lane_value(tot, 0);
+      us[r * NB + t] = lane_value(tot, 32);
     }
   }
+  float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NI; ++i)
+    if (lane == i) {
+      gsum = gs[i];
+      usum = us[i];
+    }
+  const int r = lane / NB, t = lane - (lane / NB) * NB;
+  const int row = row0 + r;
+  if (lane < NI && row < rows && t0 + t < tokens)
+    act[(size_t)(t0 + t) * rows + row] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
 }
 
 }  // namespace cq35

@@ -423,12 +423,14 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
   poll_words<(H / 2 + kMT - 1) / kMT>(m, H / 2, Span{Ly.x_attn}, reinterpret_cast<uint32_t*>(m.xa));
   norm_row<S>(m, m.xa, w0, w1, m.a.eps);
   trace_mark(kMarkRouterNormed);
-  uint16_t t[RG];
   uint16_t* odd = reinterpret_cast<uint16_t*>(m.big);  // [kMW / 2][RG]
+  // the rows' total pairs (wave-uniform); the epilogues then run one per
+  // lane, lane k taking row k
+  float gs[RG], us[RG];
 #pragma unroll
   for (int k = 0; k < RG; ++k) {
     const int row = gp + m.nw * k;
-    t[k] = 0;
+    gs[k] = us[k] = 0.0f;
     if (row < S::I) {  // uniform per wave
       Quad ga, ua;
       quad_zero(ga);
@@ -441,20 +443,24 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
           quad_acc(ua, xq, uv[k][j]);
         }
       const float tot = quad_tree64_pair(ga, ua);  // gate total in lane 0, up total in lane 32
-      const float gsum = tot, usum = lane_value(tot, 32);
-      t[k] = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));
-      if (m.lane == 0 && (m.wave & 1)) odd[(m.wave >> 1) * RG + k] = t[k];
+      gs[k] = lane_value(tot, 0);
+      us[k] = lane_value(tot, 32);
     }
   }
+  float gsum = 0.0f, usum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < RG; ++k)
+    if (m.lane == k) {
+      gsum = gs[k];
+      usum = us[k];
+    }
+  const uint16_t t = bf_mul(f2bf(silu(rbf(gsum))), f2bf(usum));  // row m.lane (lanes < RG)
+  const int my_row = gp + m.nw * m.lane;
+  if (m.lane < RG && my_row < S::I && (m.wave & 1)) odd[(m.wave >> 1) * RG + m.lane] = t;
   trace_mark(kMarkGateUpDone);
   __syncthreads();
-  if (m.lane == 0 && !(m.wave & 1)) {
-#pragma unroll
-    for (int k = 0; k < RG; ++k) {
-      const int row = gp + m.nw * k;
-      if (row < S::I) word_store(Ly.x_active + (row >> 1), pack_bf(t[k], odd[(m.wave >> 1) * RG + k]), m.tag);
-    }
-  }
+  if (m.lane < RG && my_row < S::I && !(m.wave & 1))
+    word_store(Ly.x_active + (my_row >> 1), pack_bf(t, odd[(m.wave >> 1) * RG + m.lane]), m.tag);
 }
 
 // ------------------------------------------------------------- the kernel
