@@ -69,7 +69,14 @@ __device__ __forceinline__ void phase_project32(const MegaArgs* pa, uint32_t tag
   const int q = m.lane & 7, g = m.lane >> 3;
   const int rounds = (rows + 8 * m.nw - 1) / (8 * m.nw);
   u32x4 wv[NQ];
+  // a wave whose eight rows all lie past the end loads and computes nothing
+  // (uniform per wave); the wave holding the end clamps its last rows
   auto issue = [&](int k) {
+    if (8 * (m.gs + m.nw * k) >= rows) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) wv[j] = u32x4{0u, 0u, 0u, 0u};
+      return;
+    }
     const int row = min(8 * (m.gs + m.nw * k) + g, rows - 1);
     const uint16_t* w = seg_row(Ly, row, S::H);
 #pragma unroll
@@ -84,6 +91,7 @@ __device__ __forceinline__ void phase_project32(const MegaArgs* pa, uint32_t tag
 #pragma unroll 1
   for (int k = 0; k < rounds; ++k) {
     if (k > 0) issue(k);
+    if (8 * (m.gs + m.nw * k) >= rows) continue;  // uniform per wave
     const int row = 8 * (m.gs + m.nw * k) + g;
     Quad acc;
     quad_zero(acc);
@@ -409,7 +417,12 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
   u32x4 gv[RG][NQ], uv[RG][NQ];
 #pragma unroll
   for (int k = 0; k < RG; ++k) {
-    const int row = min(gp + m.nw * k, S::I - 1);
+    if (gp + m.nw * k >= S::I) {  // no row (uniform per wave): nothing to load
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) gv[k][j] = uv[k][j] = u32x4{0u, 0u, 0u, 0u};
+      continue;
+    }
+    const int row = gp + m.nw * k;
     const uint16_t* wg = Ly.sgate + (size_t)row * H;
     const uint16_t* wu = Ly.sup + (size_t)row * H;
 #pragma unroll
