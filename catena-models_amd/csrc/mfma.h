@@ -313,8 +313,9 @@ __global__ __launch_bounds__(64 * kMWaves) __attribute__((amdgpu_waves_per_eu(2,
 // each activation fragment: two for the vocabulary head) x a 32-token tile x
 // one of `kb` column ranges;
 // wave w of the block sums a quarter of that range into one accumulator per
-// tile (k permuted inside each 64-column batch so that loads are whole
-// lines), with two batches of four k steps in flight (loads are unconditional:
+// tile (k permuted inside each 64-column batch; the weight rows are loaded as
+// whole lines and handed to the MFMA operands through LDS), with two batches
+// of four k steps in flight (loads are unconditional:
 // a batch past the end reloads the last one, so every wait leaves the newer
 // batch outstanding). The four wave partials are added as a tree through LDS
 // ((w0 + w1) + (w2 + w3)). With kb > 1 (launches with few row tiles: more
@@ -385,46 +386,62 @@ __global__ __launch_bounds__(64 * kSkSplit) void k_mskinny(const uint16_t* __res
   const int r0 = blockIdx.x * 32 * kT, t0 = blockIdx.y * 32;
   // a batch of four k steps covers 64 columns: lane half h holds columns
   // [32 h, 32 h + 32) of it, 8 per step, in both operands (the same
-  // permutation of k), so each lane reads 64 contiguous bytes per row and the
-  // two halves one whole 128-byte line
+  // permutation of k), so each lane reads 64 contiguous bytes of its token
+  // row
   const int kq = 32 * (lane >> 5);
   const int span = cols / (kSkSplit * kb), c0 = (blockIdx.z * kSkSplit + wave) * span;
-  const uint16_t* wb[kMats][kT];
-#pragma unroll
-  for (int h = 0; h < kT; ++h) {
-    int local;
-    const int sg = segment_of(seg, min(r0 + 32 * h + (lane & 31), rows - 1), &local);
-    wb[0][h] = segment_w(seg, sg) + (size_t)local * cols + c0 + kq;
-    if (kMode == kBGate) wb[kMats - 1][h] = w2 + (size_t)local * cols + c0 + kq;
-  }
   const uint16_t* xa = x + (size_t)min(t0 + (lane & 31), n - 1) * cols + c0 + kq;
   const int steps = span / 16;  // a multiple of 2 kSkBatch
-  struct Set {
-    u32x4 a[kSkBatch], b[kMats][kT][kSkBatch];
-  };
-  auto load = [&](int s, Set& v) {
-    const int k = 16 * min(s, steps - kSkBatch);
-#pragma unroll
-    for (int j = 0; j < kSkBatch; ++j) {
-      v.a[j] = *reinterpret_cast<const u32x4*>(xa + k + 8 * j);
-#pragma unroll
-      for (int mi = 0; mi < kMats; ++mi)
-#pragma unroll
-        for (int h = 0; h < kT; ++h) v.b[mi][h][j] = *reinterpret_cast<const u32x4*>(wb[mi][h] + k + 8 * j);
-    }
-  };
   f32x16_t acc[kMats][kT];
 #pragma unroll
   for (int mi = 0; mi < kMats; ++mi)
 #pragma unroll
     for (int h = 0; h < kT; ++h) acc[mi][h] = f32x16_t{};
+  // Weight rows through LDS: load instruction g gives lane i the 16-byte
+  // chunk i & 7 of tile row 8 g + (i >> 3) in the 64-column batch (eight
+  // whole 128-byte lines per instruction), stored in this wave's slot with
+  // chunk c of row r at position c ^ (r & 7); the MFMA operand of lane l
+  // (row 32 h + (l & 31), chunk 4 (l >> 5) + j: the permuted k above) is
+  // then read back, the 32 rows of one chunk spread over all banks. Same
+  // operands, same products and sums as reading them directly.
+  constexpr int G = 4 * kT;  // load instructions per matrix and batch
+  __shared__ __align__(16) u32x4 wst[kSkSplit][kMats][32 * kT * 8];
+  const int cr = lane >> 3, cc = lane & 7;
+  const uint16_t* wrow[kMats][G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    int local;
+    const int sg = segment_of(seg, min(r0 + 8 * g + cr, rows - 1), &local);
+    wrow[0][g] = segment_w(seg, sg) + (size_t)local * cols + c0 + 8 * cc;
+    if (kMode == kBGate) wrow[kMats - 1][g] = w2 + (size_t)local * cols + c0 + 8 * cc;
+  }
+  struct Set {
+    u32x4 a[kSkBatch], b[kMats][G];
+  };
+  auto load = [&](int s, Set& v) {
+    const int k = 16 * min(s, steps - kSkBatch);
+#pragma unroll
+    for (int j = 0; j < kSkBatch; ++j) v.a[j] = *reinterpret_cast<const u32x4*>(xa + k + 8 * j);
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int g = 0; g < G; ++g) v.b[mi][g] = *reinterpret_cast<const u32x4*>(wrow[mi][g] + k);
+  };
   auto mult = [&](const Set& v) {
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int g = 0; g < G; ++g) wst[wave][mi][(8 * g + cr) * 8 + (cc ^ cr)] = v.b[mi][g];
 #pragma unroll
     for (int j = 0; j < kSkBatch; ++j)
 #pragma unroll
       for (int mi = 0; mi < kMats; ++mi)
 #pragma unroll
-        for (int h = 0; h < kT; ++h) acc[mi][h] = mfma32(v.a[j], v.b[mi][h][j], acc[mi][h]);
+        for (int h = 0; h < kT; ++h) {
+          const int r = 32 * h + (lane & 31);
+          const u32x4 bq = wst[wave][mi][r * 8 + ((4 * (lane >> 5) + j) ^ (lane & 7))];
+          acc[mi][h] = mfma32(v.a[j], bq, acc[mi][h]);
+        }
   };
   Set P, Q;
   load(0, P);
