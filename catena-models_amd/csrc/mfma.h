@@ -583,6 +583,70 @@ __device__ __forceinline__ void mfma_tile(const uint16_t* xa, const uint16_t* co
   for (int mi = 0; mi < kMats; ++mi) out[mi] = acc[0][mi];
 }
 
+// mfma_tile with the weight rows loaded as whole 128-byte lines: for each
+// 64-column batch (four k steps), load instruction g gives lane i the
+// 16-byte chunk i & 7 of tile row 8 g + (i >> 3) (wl[mi][g]: that row's
+// chunk at column 0), stored in the wave's LDS slot st[mi] with chunk c of
+// row r at position c ^ (r & 7); the B operand of lane l for step p (row
+// l & 31, columns 16 p + 8 (l >> 5): chunk 2 p + (l >> 5)) is read back. The
+// steps go to the same rotating partial sums in the same order, so the
+// results equal mfma_tile's. cols % 64 == 0, kParts divides 4.
+template <int kParts, int kMats>
+__device__ __forceinline__ void mfma_tile_lines(const uint16_t* xa, const uint16_t* const (&wl)[kMats][4], int cols,
+                                                u32x4 (*st)[32 * 8], f32x16_t (&out)[kMats]) {
+  static_assert(4 % kParts == 0, "parts per batch");
+  const int lane = threadIdx.x & 63, cr = lane >> 3, cc = lane & 7, r = lane & 31, h = lane >> 5;
+  f32x16_t acc[kParts][kMats];
+#pragma unroll
+  for (int p = 0; p < kParts; ++p)
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi) acc[p][mi] = f32x16_t{};
+  struct Set {
+    u32x4 a[4], b[kMats][4];
+  };
+  const int batches = cols / 64;
+  auto load = [&](int bt, Set& v) {
+    const int k = 64 * min(bt, batches - 1);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) v.a[p] = *reinterpret_cast<const u32x4*>(xa + k + 16 * p);
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) v.b[mi][g] = *reinterpret_cast<const u32x4*>(wl[mi][g] + k);
+  };
+  auto mult = [&](const Set& v) {
+#pragma unroll
+    for (int mi = 0; mi < kMats; ++mi)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) st[mi][(8 * g + cr) * 8 + (cc ^ cr)] = v.b[mi][g];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) {
+        const u32x4 bq = st[mi][r * 8 + ((2 * p + h) ^ (r & 7))];
+        acc[p % kParts][mi] = mfma32(v.a[p], bq, acc[p % kParts][mi]);
+      }
+  };
+  // two batches in flight (loads past the end repeat the last batch, which
+  // is not multiplied)
+  Set P, Q;
+  load(0, P);
+  for (int bt = 0; bt < batches; bt += 2) {
+    load(bt + 1, Q);
+    mult(P);
+    load(bt + 2, P);
+    if (bt + 1 < batches) mult(Q);  // uniform
+  }
+#pragma unroll
+  for (int span = 1; span < kParts; span *= 2)
+#pragma unroll
+    for (int p = 0; p + span < kParts; p += 2 * span)
+#pragma unroll
+      for (int mi = 0; mi < kMats; ++mi) acc[p][mi] += acc[p + span][mi];
+#pragma unroll
+  for (int mi = 0; mi < kMats; ++mi) out[mi] = acc[0][mi];
+}
+
 // Buckets: eoff[e] .. eoff[e + 1] index order[], which holds assignment
 // indices t * top_k + slot. The order inside a bucket is whatever the
 // atomics give: each MFMA output element is its own dot product, unaffected
@@ -632,10 +696,8 @@ __global__ __launch_bounds__(64 * kXWaves) void k_mmoe_gate(
   const int r0 = blockIdx.x * kXRows + 32 * wave;
   if (count == 0 || r0 >= width) return;  // uniform per wave; no barriers below
   const int kq = 8 * (lane >> 5);
-  const int wrow = min(r0 + (lane & 31), width - 1);
-  const uint16_t* w[2];
-  w[0] = (shared ? sgate : gate + (size_t)e * inter * hidden) + (size_t)wrow * hidden + kq;
-  w[1] = (shared ? sup : up + (size_t)e * inter * hidden) + (size_t)wrow * hidden + kq;
+  const uint16_t* gbase = shared ? sgate : gate + (size_t)e * inter * hidden;
+  const uint16_t* ubase = shared ? sup : up + (size_t)e * inter * hidden;
   const int act_rows = top_k * inter + shared_inter;
   const int row = r0 + (lane & 31);
   {
@@ -644,7 +706,21 @@ __global__ __launch_bounds__(64 * kXWaves) void k_mmoe_gate(
     const int i = min(m0 + (lane & 31), count - 1);
     const int t = shared ? i : order[begin + i] / top_k;
     f32x16_t acc[2];
-    mfma_tile<2, 2>(x + (size_t)t * hidden + kq, w, hidden, acc);
+    if (hidden % 64 == 0) {  // uniform
+      __shared__ __align__(16) u32x4 gst[kXWaves][2][32 * 8];
+      const uint16_t* wl[2][4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const size_t off = (size_t)min(r0 + 8 * g + (lane >> 3), width - 1) * hidden + 8 * (lane & 7);
+        wl[0][g] = gbase + off;
+        wl[1][g] = ubase + off;
+      }
+      mfma_tile_lines<2, 2>(x + (size_t)t * hidden + kq, wl, hidden, gst[wave], acc);
+    } else {
+      const int wrow = min(r0 + (lane & 31), width - 1);
+      const uint16_t* w[2] = {gbase + (size_t)wrow * hidden + kq, ubase + (size_t)wrow * hidden + kq};
+      mfma_tile<2, 2>(x + (size_t)t * hidden + kq, w, hidden, acc);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int mi = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -681,9 +757,7 @@ __global__ __launch_bounds__(64 * kXWaves) void k_mmoe_down(
   const int o0 = blockIdx.x * kXRows + 32 * wave;
   if (count == 0 || o0 >= hidden) return;  // uniform per wave; no barriers below
   const int kq = 8 * (lane >> 5);
-  const int orow = min(o0 + (lane & 31), hidden - 1);
-  const uint16_t* w[1];
-  w[0] = (shared ? sdown : down + (size_t)e * hidden * inter) + (size_t)orow * width + kq;
+  const uint16_t* dbase = shared ? sdown : down + (size_t)e * hidden * inter;
   const int act_rows = top_k * inter + shared_inter;
   const int o = o0 + (lane & 31);
   {
@@ -699,7 +773,17 @@ __global__ __launch_bounds__(64 * kXWaves) void k_mmoe_down(
       arow = (size_t)ta * act_rows + (size_t)(a - ta * top_k) * inter;
     }
     f32x16_t acc[1];
-    mfma_tile<4, 1>(act + arow + kq, w, width, acc);
+    if (width % 64 == 0) {  // uniform
+      __shared__ __align__(16) u32x4 dst_[kXWaves][1][32 * 8];
+      const uint16_t* wl[1][4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        wl[0][g] = dbase + (size_t)min(o0 + 8 * g + (lane >> 3), hidden - 1) * width + 8 * (lane & 7);
+      mfma_tile_lines<4, 1>(act + arow + kq, wl, width, dst_[wave], acc);
+    } else {
+      const uint16_t* w[1] = {dbase + (size_t)min(o0 + (lane & 31), hidden - 1) * width + kq};
+      mfma_tile<4, 1>(act + arow + kq, w, width, acc);
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int mi = m0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
