@@ -543,22 +543,26 @@ inline size_t bdown_lds_bytes(int per_row_quads) { return (size_t)kBDownTokens *
 // Scores of every session's keys (k_attn_scores' arithmetic: lane l of a
 // 32-lane unit owns channels l, l + 32, ..., summed serially from 0.0, then
 // the 32-wide halving tree, times 1/sqrt(HD)), with the group's HPK query
-// heads in registers, two keys per unit at a time reduced by one paired tree
-// (each total has its operands of the single tree), and the next pair's key
-// rows loaded before the current pair's products. Block (key blocks, KV head,
-// session): scores [session][q_heads][stride].
+// heads in registers and two keys per unit reduced by one paired tree (each
+// total has its operands of the single tree). Block (key blocks, KV head,
+// session) takes chunks of 16 consecutive keys (blockIdx.x, + gridDim.x,
+// ...): a chunk's key rows are loaded as whole lines (16-byte pieces, each
+// row's pieces on consecutive threads) into LDS, the next chunk's loads in
+// flight while unit u scores keys 2u and 2u + 1 from there. scores
+// [session][q_heads][stride].
 template <int HPK, int KJ>
 __global__ __launch_bounds__(kBlock) void k_bscores(const uint16_t* __restrict__ q,
                                                     const SessionRows* __restrict__ rows, int64_t key_base, int kvs,
                                                     float scale, float* __restrict__ scores, int stride) {
-  constexpr int HD = 32 * KJ;
+  constexpr int HD = 32 * KJ, RQ = HD / 8;      // channels, 16-byte pieces per key row
+  constexpr int CK = 2 * (kBlock / 32);         // keys per chunk: two per unit
+  constexpr int PT = (CK * RQ + kBlock - 1) / kBlock;  // pieces per thread
+  __shared__ __align__(16) uint16_t kst[2][CK * HD];
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int q_heads = gridDim.y * HPK;
-  const int l32 = threadIdx.x & 31;
-  const int unit = (blockIdx.x * blockDim.x + threadIdx.x) >> 5;
-  const int units = (gridDim.x * blockDim.x) >> 5;
+  const int l32 = threadIdx.x & 31, unit = threadIdx.x >> 5;
   const int64_t keys = (int64_t)rows->position[b] + 1;
-  const auto kbase = gmem(rows->cache[b] + key_base + (int64_t)kvh * HD + l32);
+  const auto kbase = gmem(rows->cache[b] + key_base + (int64_t)kvh * HD);
   float* sb = scores + (size_t)b * q_heads * stride + (size_t)kvh * HPK * stride;
   float qv[HPK][KJ];
 #pragma unroll
@@ -566,25 +570,43 @@ __global__ __launch_bounds__(kBlock) void k_bscores(const uint16_t* __restrict__
 #pragma unroll
     for (int j = 0; j < KJ; ++j)
       qv[h][j] = bf2f(q[((size_t)b * q_heads + kvh * HPK + h) * HD + l32 + 32 * j]);
-  int64_t kk = 2 * (int64_t)unit;
-  uint16_t ka[KJ], kb[KJ];
-  auto load = [&](int64_t k0) {
-    const int64_t a = min<int64_t>(k0, keys - 1), c = min<int64_t>(k0 + 1, keys - 1);
+  // piece i of this thread: key row (tid + kBlock i) / RQ of the chunk, its
+  // 16-byte piece (tid + kBlock i) % RQ
+  u32x4 kv[PT];
+  auto load = [&](int64_t c0) {
 #pragma unroll
-    for (int j = 0; j < KJ; ++j) {
-      ka[j] = kbase[a * kvs + 32 * j];
-      kb[j] = kbase[c * kvs + 32 * j];
+    for (int i = 0; i < PT; ++i) {
+      const int idx = threadIdx.x + kBlock * i;
+      if (CK * RQ % kBlock == 0 || idx < CK * RQ) {
+        const int64_t key = min<int64_t>(c0 + idx / RQ, keys - 1);
+        kv[i] = *reinterpret_cast<const __attribute__((address_space(1))) u32x4*>(kbase + key * kvs +
+                                                                                  8 * (idx % RQ));
+      }
     }
   };
-  if (kk < keys) load(kk);
-  for (; kk < keys; kk += 2 * (int64_t)units) {
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      const int idx = threadIdx.x + kBlock * i;
+      if (CK * RQ % kBlock == 0 || idx < CK * RQ) reinterpret_cast<u32x4*>(kst[buf])[idx] = kv[i];
+    }
+  };
+  const int64_t step = (int64_t)CK * gridDim.x;
+  int64_t c0 = (int64_t)CK * blockIdx.x;
+  if (c0 >= keys) return;  // uniform per block
+  load(c0);
+  put(0);
+  __syncthreads();
+  for (int buf = 0; c0 < keys; c0 += step, buf ^= 1) {
+    load(c0 + step);  // unconditional (clamped): a conditional load would drain the queue
+    const uint16_t* ka = kst[buf] + (2 * unit) * HD + l32;
     float fa[KJ], fb[KJ];
 #pragma unroll
     for (int j = 0; j < KJ; ++j) {
-      fa[j] = bf2f(ka[j]);
-      fb[j] = bf2f(kb[j]);
+      fa[j] = bf2f(ka[32 * j]);
+      fb[j] = bf2f(ka[HD + 32 * j]);
     }
-    load(kk + 2 * (int64_t)units);  // unconditional (clamped): a conditional load would drain the queue
+    const int64_t kk = c0 + 2 * unit;
 #pragma unroll
     for (int h = 0; h < HPK; ++h) {
       float a = 0.0f, c = 0.0f;
@@ -594,9 +616,11 @@ __global__ __launch_bounds__(kBlock) void k_bscores(const uint16_t* __restrict__
         c += qv[h][j] * fb[j];
       }
       const float v = tree32_pair(a, c);
-      if (l32 == 0) sb[(size_t)h * stride + kk] = v * scale;
+      if (l32 == 0 && kk < keys) sb[(size_t)h * stride + kk] = v * scale;
       if (l32 == 16 && kk + 1 < keys) sb[(size_t)h * stride + kk + 1] = v * scale;
     }
+    put(buf ^ 1);  // the other buffer's readers finished before the last barrier
+    __syncthreads();
   }
 }
 
