@@ -134,6 +134,13 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
 // (serial from 0.0, then a 32-wide halving tree). The state row is BF16 in
 // the cache (decode) or F32 in the shadow (inside a multi-token call); the
 // output always uses the unrounded F32 update.
+//
+// The block's 8 state rows are one contiguous run of memory, and its channels
+// share one key head when value_dim is a multiple of 8: the block then moves
+// the rows, and the head's k and q, with 16-byte loads and stores (whole
+// 128-byte lines, four rows per wave instruction) through LDS, and the lanes
+// read and write their elements there. Otherwise every lane loads and stores
+// its own elements. Same values and arithmetic either way.
 constexpr int kDeltaCh = 1;  // value channels per 32-lane group of k_delta
 template <bool kF32State>
 __global__ __launch_bounds__(kBlock) void k_delta(
@@ -142,6 +149,12 @@ __global__ __launch_bounds__(kBlock) void k_delta(
     uint16_t* __restrict__ state16, float* __restrict__ state32, int value_size, int value_dim,
     int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out,
     const SessionRows* __restrict__ rows, int64_t state_off) {
+  static_assert(kDeltaCh == 1, "one channel per 32-lane group");
+  using StateT = typename std::conditional<kF32State, float, uint16_t>::type;
+  constexpr int G = kBlock / 32;               // channels per block
+  constexpr int EPV = 16 / (int)sizeof(StateT);  // state elements per 16-byte piece
+  __shared__ __align__(16) StateT srow[G * 256];
+  __shared__ __align__(16) uint16_t kq[2][256];
   const int y = blockIdx.y;  // session row of a batched step (0 otherwise)
   const int value_heads = value_size / value_dim;
   conv += (size_t)y * (2 * key_size + value_size);
@@ -150,62 +163,88 @@ __global__ __launch_bounds__(kBlock) void k_delta(
   gates += (size_t)y * value_heads;
   out += (size_t)y * value_size;
   if (rows) state16 = rows->cache[y] + state_off;
-  const int lane = threadIdx.x & 31;
-  // each 32-lane group runs kDeltaCh channels side by side (independent
-  // chains; one measured fastest); every input is requested up front
-  int c[kDeltaCh], cc[kDeltaCh], kbase[kDeltaCh];
-  bool valid[kDeltaCh];
-  float decay[kDeltaCh], rate[kDeltaCh], value[kDeltaCh];
-  float old[kDeltaCh][8], kv[kDeltaCh][8], qv[kDeltaCh][8];
-#pragma unroll
-  for (int u = 0; u < kDeltaCh; ++u) {
-    c[u] = (blockIdx.x * (kBlock / 32) + (threadIdx.x >> 5)) * kDeltaCh + u;
-    valid[u] = c[u] < value_size;
-    cc[u] = valid[u] ? c[u] : 0;
-    const int head = cc[u] / value_dim;
-    kbase[u] = (head % key_heads) * key_dim;
-    const float2 gate = gates[head];  // k_linear_prepare's (decay, rate)
-    decay[u] = gate.x;
-    rate[u] = gate.y;
-    value[u] = bf2f(conv[2 * key_size + cc[u]]);
+  StateT* const state = kF32State ? (StateT*)state32 : (StateT*)state16;
+  const int lane = threadIdx.x & 31, g = threadIdx.x >> 5;
+  const int c0 = blockIdx.x * G;
+  const int c = c0 + g;
+  const bool valid = c < value_size;
+  const int cc = valid ? c : c0;
+  const int head = cc / value_dim;
+  const int kbase = (head % key_heads) * key_dim;
+  const int nrows = min(G, value_size - c0);
+  StateT* const run = state + (size_t)c0 * key_dim;  // the block's rows, contiguous
+  const bool staged = value_dim % G == 0 && key_dim % 8 == 0 && key_dim <= 256 &&
+                      ((uintptr_t)run & 15) == 0 && ((uintptr_t)(k + kbase) & 15) == 0 &&
+                      ((uintptr_t)(q + kbase) & 15) == 0;  // uniform over the block
+  const int pieces = nrows * key_dim / EPV;
+  if (staged) {
+    for (int p = threadIdx.x; p < pieces; p += kBlock)
+      *(u32x4*)&srow[p * EPV] = *(const u32x4*)(run + p * EPV);
+    const int t = kBlock - 1 - threadIdx.x;  // the top threads fetch k and q
+    if (t < key_dim / 4) {
+      const int which = t / (key_dim / 8), piece = t % (key_dim / 8);
+      *(u32x4*)&kq[which][8 * piece] = *(const u32x4*)((which ? q : k) + kbase + 8 * piece);
+    }
+  }
+  const float2 gate = gates[head];  // k_linear_prepare's (decay, rate)
+  const float decay = gate.x, rate = gate.y;
+  const float value = bf2f(conv[2 * key_size + cc]);
+  float old[8], kv[8], qv[8];
+  if (staged) {
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = lane + 32 * j;
       if (i < key_dim) {
-        old[u][j] = kF32State ? state32[(size_t)cc[u] * key_dim + i] : bf2f(state16[(size_t)cc[u] * key_dim + i]);
-        kv[u][j] = bf2f(k[kbase[u] + i]);
-        qv[u][j] = bf2f(q[kbase[u] + i]);
+        old[j] = kF32State ? (float)srow[g * key_dim + i] : bf2f((uint16_t)srow[g * key_dim + i]);
+        kv[j] = bf2f(kq[0][i]);
+        qv[j] = bf2f(kq[1][i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = lane + 32 * j;
+      if (i < key_dim) {
+        old[j] = kF32State ? state32[(size_t)cc * key_dim + i] : bf2f(state16[(size_t)cc * key_dim + i]);
+        kv[j] = bf2f(k[kbase + i]);
+        qv[j] = bf2f(q[kbase + i]);
       }
     }
   }
+  float acc = 0.0f;
 #pragma unroll
-  for (int u = 0; u < kDeltaCh; ++u) {
-    float acc = 0.0f;
+  for (int j = 0; j < 8; ++j)
+    if (lane + 32 * j < key_dim) acc += old[j] * kv[j];
+  // D32 halving tree (strides 16 .. 1) in each half wave by DPP / permlane,
+  // the sums of lanes 0 and 32 broadcast to their halves
+  acc = tree32_lanes(acc);
+  const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+  const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 32));
+  const float total = (threadIdx.x & 32) ? t1 : t0;
+  const float delta = (value - total * decay) * rate;
+  float acc2 = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (lane + 32 * j < key_dim) acc += old[u][j] * kv[u][j];
-    // D32 halving tree (strides 16 .. 1) in each half wave by DPP / permlane,
-    // the sums of lanes 0 and 32 broadcast to their halves
-    acc = tree32_lanes(acc);
-    const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
-    const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 32));
-    const float total = (threadIdx.x & 32) ? t1 : t0;
-    const float delta = (value[u] - total * decay[u]) * rate[u];
-    float acc2 = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = lane + 32 * j;
-      if (i < key_dim) {
-        const float next = old[u][j] * decay[u] + kv[u][j] * delta;
-        if (valid[u]) {
-          if (kF32State) state32[(size_t)cc[u] * key_dim + i] = next;
-          else state16[(size_t)cc[u] * key_dim + i] = f2bf(next);
-        }
-        acc2 += next * qv[u][j];
+  for (int j = 0; j < 8; ++j) {
+    const int i = lane + 32 * j;
+    if (i < key_dim) {
+      const float next = old[j] * decay + kv[j] * delta;
+      if (staged) {
+        if (kF32State) srow[g * key_dim + i] = next;
+        else srow[g * key_dim + i] = (StateT)f2bf(next);
+      } else if (valid) {
+        if (kF32State) state32[(size_t)cc * key_dim + i] = next;
+        else state16[(size_t)cc * key_dim + i] = f2bf(next);
       }
+      acc2 += next * qv[j];
     }
-    acc2 = tree32_lanes(acc2);
-    if (lane == 0 && valid[u]) out[c[u]] = f2bf(acc2 * scale);
+  }
+  acc2 = tree32_lanes(acc2);
+  if (lane == 0 && valid) out[c] = f2bf(acc2 * scale);
+  if (staged) {
+    __syncthreads();
+    for (int p = threadIdx.x; p < pieces; p += kBlock)
+      *(u32x4*)(run + p * EPV) = *(const u32x4*)&srow[p * EPV];
   }
 }
 
