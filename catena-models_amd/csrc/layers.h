@@ -140,9 +140,11 @@ __global__ __launch_bounds__(kBlock) void k_linear_prepare(
 // the rows, and the head's k and q, with 16-byte loads and stores (whole
 // 128-byte lines, four rows per wave instruction) through LDS, and the lanes
 // read and write their elements there. Otherwise every lane loads and stores
-// its own elements. Same values and arithmetic either way.
+// its own elements. Same values and arithmetic either way. kKD fixes
+// key_dim at compile time (128, every shipped shape: no per-element bounds
+// checks); 0 takes it from the argument (at most 256).
 constexpr int kDeltaCh = 1;  // value channels per 32-lane group of k_delta
-template <bool kF32State>
+template <bool kF32State, int kKD = 0>
 __global__ __launch_bounds__(kBlock) void k_delta(
     const uint16_t* __restrict__ conv, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const float2* __restrict__ gates,
@@ -150,11 +152,14 @@ __global__ __launch_bounds__(kBlock) void k_delta(
     int key_dim, int key_heads, int key_size, float scale, uint16_t* __restrict__ out,
     const SessionRows* __restrict__ rows, int64_t state_off) {
   static_assert(kDeltaCh == 1, "one channel per 32-lane group");
+  static_assert(kKD % 32 == 0 && kKD <= 256, "key_dim a multiple of 32, at most 256");
   using StateT = typename std::conditional<kF32State, float, uint16_t>::type;
-  constexpr int G = kBlock / 32;               // channels per block
+  constexpr int G = kBlock / 32;                 // channels per block
   constexpr int EPV = 16 / (int)sizeof(StateT);  // state elements per 16-byte piece
+  constexpr int NJ = kKD ? kKD / 32 : 8;         // key elements per lane
   __shared__ __align__(16) StateT srow[G * 256];
   __shared__ __align__(16) uint16_t kq[2][256];
+  const int KD = kKD ? kKD : key_dim;
   const int y = blockIdx.y;  // session row of a batched step (0 otherwise)
   const int value_heads = value_size / value_dim;
   conv += (size_t)y * (2 * key_size + value_size);
@@ -169,44 +174,53 @@ __global__ __launch_bounds__(kBlock) void k_delta(
   const int c = c0 + g;
   const bool valid = c < value_size;
   const int cc = valid ? c : c0;
-  const int head = cc / value_dim;
-  const int kbase = (head % key_heads) * key_dim;
   const int nrows = min(G, value_size - c0);
-  StateT* const run = state + (size_t)c0 * key_dim;  // the block's rows, contiguous
-  const bool staged = value_dim % G == 0 && key_dim % 8 == 0 && key_dim <= 256 &&
-                      ((uintptr_t)run & 15) == 0 && ((uintptr_t)(k + kbase) & 15) == 0 &&
-                      ((uintptr_t)(q + kbase) & 15) == 0;  // uniform over the block
-  const int pieces = nrows * key_dim / EPV;
+  StateT* const run = state + (size_t)c0 * KD;  // the block's rows, contiguous
+  const int head0 = c0 / value_dim;             // one division per block
+  const int kbase0 = (head0 % key_heads) * KD;
+  const bool staged = value_dim % G == 0 && KD % 8 == 0 && KD <= 256 && ((uintptr_t)run & 15) == 0 &&
+                      ((uintptr_t)(k + kbase0) & 15) == 0 &&
+                      ((uintptr_t)(q + kbase0) & 15) == 0;  // uniform over the block
+  const int pieces = nrows * KD / EPV;
+  // every channel of a staged block is in head0; otherwise per channel
+  int head, kbase;
+  if (staged) {
+    head = head0;
+    kbase = kbase0;
+  } else {
+    head = cc / value_dim;
+    kbase = (head % key_heads) * KD;
+  }
   if (staged) {
     for (int p = threadIdx.x; p < pieces; p += kBlock)
       *(u32x4*)&srow[p * EPV] = *(const u32x4*)(run + p * EPV);
     const int t = kBlock - 1 - threadIdx.x;  // the top threads fetch k and q
-    if (t < key_dim / 4) {
-      const int which = t / (key_dim / 8), piece = t % (key_dim / 8);
+    if (t < KD / 4) {
+      const int which = t / (KD / 8), piece = t % (KD / 8);
       *(u32x4*)&kq[which][8 * piece] = *(const u32x4*)((which ? q : k) + kbase + 8 * piece);
     }
   }
   const float2 gate = gates[head];  // k_linear_prepare's (decay, rate)
   const float decay = gate.x, rate = gate.y;
   const float value = bf2f(conv[2 * key_size + cc]);
-  float old[8], kv[8], qv[8];
+  float old[NJ], kv[NJ], qv[NJ];
   if (staged) {
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int i = lane + 32 * j;
-      if (i < key_dim) {
-        old[j] = kF32State ? (float)srow[g * key_dim + i] : bf2f((uint16_t)srow[g * key_dim + i]);
+      if (kKD || i < KD) {
+        old[j] = kF32State ? (float)srow[g * KD + i] : bf2f((uint16_t)srow[g * KD + i]);
         kv[j] = bf2f(kq[0][i]);
         qv[j] = bf2f(kq[1][i]);
       }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int i = lane + 32 * j;
-      if (i < key_dim) {
-        old[j] = kF32State ? state32[(size_t)cc * key_dim + i] : bf2f(state16[(size_t)cc * key_dim + i]);
+      if (kKD || i < KD) {
+        old[j] = kF32State ? state32[(size_t)cc * KD + i] : bf2f(state16[(size_t)cc * KD + i]);
         kv[j] = bf2f(k[kbase + i]);
         qv[j] = bf2f(q[kbase + i]);
       }
@@ -214,8 +228,8 @@ __global__ __launch_bounds__(kBlock) void k_delta(
   }
   float acc = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    if (lane + 32 * j < key_dim) acc += old[j] * kv[j];
+  for (int j = 0; j < NJ; ++j)
+    if (kKD || lane + 32 * j < KD) acc += old[j] * kv[j];
   // D32 halving tree (strides 16 .. 1) in each half wave by DPP / permlane,
   // the sums of lanes 0 and 32 broadcast to their halves
   acc = tree32_lanes(acc);
@@ -225,16 +239,16 @@ __global__ __launch_bounds__(kBlock) void k_delta(
   const float delta = (value - total * decay) * rate;
   float acc2 = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int i = lane + 32 * j;
-    if (i < key_dim) {
+    if (kKD || i < KD) {
       const float next = old[j] * decay + kv[j] * delta;
       if (staged) {
-        if (kF32State) srow[g * key_dim + i] = next;
-        else srow[g * key_dim + i] = (StateT)f2bf(next);
+        if (kF32State) srow[g * KD + i] = next;
+        else srow[g * KD + i] = (StateT)f2bf(next);
       } else if (valid) {
-        if (kF32State) state32[(size_t)cc * key_dim + i] = next;
-        else state16[(size_t)cc * key_dim + i] = f2bf(next);
+        if (kF32State) state32[(size_t)cc * KD + i] = next;
+        else state16[(size_t)cc * KD + i] = f2bf(next);
       }
       acc2 += next * qv[j];
     }

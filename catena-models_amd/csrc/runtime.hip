@@ -1330,13 +1330,14 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
         s->gates);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
       const dim3 dgrid((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)));
+      const bool kd128 = c.key_dim == 128;
       if (f32_state)
-        L(KC_DELTA, k_delta<true>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
+        L(KC_DELTA, kd128 ? k_delta<true, 128> : k_delta<true, 0>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
           (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const float2*)s->gates, (uint16_t*)nullptr,
           s->shadow + l * d.REC, (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale,
           s->core, (const SessionRows*)nullptr, (int64_t)0);
       else
-        L(KC_DELTA, k_delta<false>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
+        L(KC_DELTA, kd128 ? k_delta<false, 128> : k_delta<false, 0>, dgrid, dim3(kBlock), 0, (const uint16_t*)s->conv,
           (const uint16_t*)s->qn, (const uint16_t*)s->kn, (const float2*)s->gates,
           s->cache + conv_base + d.CONV, (float*)nullptr, (int)d.VS, c.value_dim, c.key_dim,
           c.key_heads, (int)d.KS, scale, s->core, (const SessionRows*)nullptr, (int64_t)0);
@@ -2267,7 +2268,8 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
           (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows, (const uint16_t*)alpha,
           (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), c.value_heads, b->gates);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
-      k_delta<false><<<dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
+      (c.key_dim == 128 ? k_delta<false, 128> : k_delta<false, 0>)<<<
+          dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const float2*)b->gates,
           (uint16_t*)nullptr, (float*)nullptr,
           (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
@@ -2398,7 +2400,8 @@ void enqueue_batch_moe(cq35_model* m, BatchWorkspace* b, int B) {
           (int)d.QKV, c.key_dim, c.key_heads, b->conv, b->qn, b->kn, rows, (const uint16_t*)alpha,
           (const uint16_t*)beta, (const float*)W(5), (const float*)W(6), c.value_heads, b->gates);
       const float scale = 1.0f / sqrtf((float)c.key_dim);  // DELTA_SCALE_BITS, qwen35.rs:703
-      k_delta<false><<<dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
+      (c.key_dim == 128 ? k_delta<false, 128> : k_delta<false, 0>)<<<
+          dim3((unsigned)((d.VS + 8 * kDeltaCh - 1) / (8 * kDeltaCh)), (unsigned)B), dim3(kBlock), 0, st>>>(
           (const uint16_t*)b->conv, (const uint16_t*)b->qn, (const uint16_t*)b->kn, (const float2*)b->gates,
           (uint16_t*)nullptr, (float*)nullptr,
           (int)d.VS, c.value_dim, c.key_dim, c.key_heads, (int)d.KS, scale, b->core, rows, conv_base + d.CONV);
