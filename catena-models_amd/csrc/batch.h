@@ -272,9 +272,9 @@ __global__ __launch_bounds__(kBlock) void k_ws256_swiglu(const uint16_t* __restr
       }
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      const float tot = quad_tree64_pair(ga[t], ua[t]);  // gate total in lane 0, up total in lane 32
-      gs[r * NB + t] = lane_value(tot, 0);
-      us[r * NB + t] = lane_value(tot, 32);
+      const float tot = quad_tree64_pair_end(ga[t], ua[t]);  // gate total in lane 31, up total in lane 63
+      gs[r * NB + t] = lane_value(tot, 31);
+      us[r * NB + t] = lane_value(tot, 63);
     }
   }
   float gsum = 0.0f, usum = 0.0f;

@@ -89,10 +89,11 @@ __global__ __launch_bounds__(kBlock) void k_ws256(const uint16_t* __restrict__ x
     static_assert(NB % 2 == 0, "token trees in pairs");
 #pragma unroll
     for (int t = 0; t < NB; t += 2) {
-      const float tot = quad_tree64_pair(acc[t], acc[t + 1]);  // token t in lane 0, t + 1 in lane 32
-      const float v1 = lane_value(tot, 32);
+      const float tot = quad_tree64_pair_end(acc[t], acc[t + 1]);  // token t in lane 31, t + 1 in lane 63
+      const float v0 = lane_value(tot, 31);
+      const float v1 = lane_value(tot, 63);
       if (lane == 0 && row < total) {
-        if (t0 + t < tokens) segment_out(seg, s)[(size_t)(t0 + t) * srows + local] = f2bf(tot);
+        if (t0 + t < tokens) segment_out(seg, s)[(size_t)(t0 + t) * srows + local] = f2bf(v0);
         if (t0 + t + 1 < tokens) segment_out(seg, s)[(size_t)(t0 + t + 1) * srows + local] = f2bf(v1);
       }
     }

@@ -181,6 +181,49 @@ __device__ __forceinline__ float quad_tree64_pair(const Quad& a, const Quad& b) 
   v[1] += v[3];
   return v[0] + v[1];
 }
+// quad_tree64_pair with the stride-16 level paired too and the levels inside
+// a 16-lane row run towards the row's last lane. After the stride-32 swap,
+// v0 and v1 (and v2 and v3) share one permlane16 swap: rows 0 and 2 go on
+// with v0's (v2's) tree, rows 1 and 3 with v1's (v3's), and no copies are
+// needed. Strides 8 ... 1 then add lane i - s into lane i (the sum of
+// reference lanes j and j + s lands in the later one, with the same two
+// operands), so each row's total ends in its last lane: v0 + v2 in lanes 15
+// and 47, v1 + v3 in lanes 31 and 63, and a row-15 broadcast adds them.
+// quad_tree<64>'s bits in fewer instructions: a's total in lane 31, b's in
+// lane 63.
+__device__ __forceinline__ float quad_tree64_pair_end(const Quad& a, const Quad& b) {
+  float v[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int av = __builtin_bit_cast(int, a.lo[p] + a.hi[p]);
+    const int bv = __builtin_bit_cast(int, b.lo[p] + b.hi[p]);
+    const auto r = __builtin_amdgcn_permlane32_swap(av, bv, false, false);
+    v[p] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+  float w[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, v[2 * q]),
+                                                    __builtin_bit_cast(int, v[2 * q + 1]), false, false);
+    w[q] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    int b = __builtin_bit_cast(int, w[q]);
+    w[q] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x118, 0xf, 0xf, true));  // row_shr:8
+    b = __builtin_bit_cast(int, w[q]);
+    w[q] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x114, 0xf, 0xf, true));  // row_shr:4
+    b = __builtin_bit_cast(int, w[q]);
+    w[q] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x112, 0xf, 0xf, true));  // row_shr:2
+    b = __builtin_bit_cast(int, w[q]);
+    w[q] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x111, 0xf, 0xf, true));  // row_shr:1
+  }
+  const float s = w[0] + w[1];
+  // row_bcast:15 (lane 15 of each row to the next row; rows 1 and 3 are the
+  // ones read)
+  return s + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x142, 0xf, 0xf, true));
+}
+
 // The value lane `lane` holds, in every lane (a scalar read).
 __device__ __forceinline__ float lane_value(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
