@@ -455,9 +455,9 @@ __device__ __forceinline__ void phase_dense_gate_up(const MegaArgs* pa, uint32_t
           quad_acc(ga, xq, gv[k][j]);
           quad_acc(ua, xq, uv[k][j]);
         }
-      const float tot = quad_tree64_pair(ga, ua);  // gate total in lane 0, up total in lane 32
-      gs[k] = lane_value(tot, 0);
-      us[k] = lane_value(tot, 32);
+      const float tot = quad_tree64_pair_end(ga, ua);  // gate total in lane 31, up total in lane 63
+      gs[k] = lane_value(tot, 31);
+      us[k] = lane_value(tot, 63);
     }
   }
   float gsum = 0.0f, usum = 0.0f;

@@ -160,37 +160,18 @@ __device__ __forceinline__ float quad_tree(const Quad& a) {
   return v0 + v1;
 }
 
-// Two quad_tree<64> totals at once: a's valid in lane 0, b's in lane 32.
-// The first level (physical stride 32) is one permlane32 swap per value: the
+// Two quad_tree<64> totals at once: a's in lane 31, b's in lane 63. The
+// first level (physical stride 32) is one permlane32 swap per value: the
 // lower half receives a's upper values, the upper half b's lower ones, so
-// lanes 0-31 continue a's tree and lanes 32-63 b's; strides 16 ... 1 then
-// run in both halves at once and 2, 1 inside the lane. Every sum has
-// quad_tree<64>'s operands (the two operands of a sum commute): the same
-// bits in about half the instructions.
-__device__ __forceinline__ float quad_tree64_pair(const Quad& a, const Quad& b) {
-  float v[4];
-#pragma unroll
-  for (int p = 0; p < 4; ++p) {
-    const int av = __builtin_bit_cast(int, a.lo[p] + a.hi[p]);
-    const int bv = __builtin_bit_cast(int, b.lo[p] + b.hi[p]);
-    const auto r = __builtin_amdgcn_permlane32_swap(av, bv, false, false);
-    v[p] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
-  }
-  tree_levels<64, 16>(v[0], v[1], v[2], v[3]);
-  v[0] += v[2];
-  v[1] += v[3];
-  return v[0] + v[1];
-}
-// quad_tree64_pair with the stride-16 level paired too and the levels inside
-// a 16-lane row run towards the row's last lane. After the stride-32 swap,
-// v0 and v1 (and v2 and v3) share one permlane16 swap: rows 0 and 2 go on
-// with v0's (v2's) tree, rows 1 and 3 with v1's (v3's), and no copies are
-// needed. Strides 8 ... 1 then add lane i - s into lane i (the sum of
-// reference lanes j and j + s lands in the later one, with the same two
-// operands), so each row's total ends in its last lane: v0 + v2 in lanes 15
-// and 47, v1 + v3 in lanes 31 and 63, and a row-15 broadcast adds them.
-// quad_tree<64>'s bits in fewer instructions: a's total in lane 31, b's in
-// lane 63.
+// lanes 0-31 continue a's tree and lanes 32-63 b's. At stride 16, v0 and v1
+// (and v2 and v3) share one permlane16 swap: rows 0 and 2 go on with v0's
+// (v2's) tree, rows 1 and 3 with v1's (v3's), no copies needed. Strides
+// 8 ... 1 then add lane i - s into lane i (the sum of reference lanes j and
+// j + s lands in the later one, with the same two operands), so each row's
+// total ends in its last lane: v0 + v2 in lanes 15 and 47, v1 + v3 in lanes
+// 31 and 63, and a row-15 broadcast adds them. Every sum has quad_tree<64>'s
+// operands (the two operands of a sum commute): the same bits in far fewer
+// instructions.
 __device__ __forceinline__ float quad_tree64_pair_end(const Quad& a, const Quad& b) {
   float v[4];
 #pragma unroll

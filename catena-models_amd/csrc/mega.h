@@ -642,9 +642,9 @@ __device__ __forceinline__ void phase_project(const MegaArgs* pa, uint32_t tag, 
         for (int j = 0; j < NQ; ++j)
           if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc[rr], xl[j], xh[j], r.w[k][rr][j]);
       }
-      const float v = quad_tree64_pair(acc[0], acc[1]);  // row 2p in lane 0, 2p + 1 in lane 32
-      const float v1 = lane_value(v, 32);
-      if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v), f2bf(v1)), m.tag);
+      const float v = quad_tree64_pair_end(acc[0], acc[1]);  // row 2p in lane 31, 2p + 1 in lane 63
+      const float v0 = lane_value(v, 31), v1 = lane_value(v, 63);
+      if (m.lane == 0) word_store(Ly.x_proj + p, pack_bf(f2bf(v0), f2bf(v1)), m.tag);
     }
   }
 }
@@ -720,9 +720,9 @@ __device__ __forceinline__ void project_z(const Mega& m, const CQ35_CONST MegaLa
           for (int j = 0; j < NQ; ++j)
             if (S::QH % 64 == 0 || m.lane + 64 * j < S::QH) quad_acc_f(acc[rr], xl[j], xh[j], wv[k][rr][j]);
         }
-        const float v = quad_tree64_pair(acc[0], acc[1]);
-        const float v1 = lane_value(v, 32);
-        if (m.lane == 0) word_store(Ly.x_proj + S::QKV / 2 + zp, pack_bf(f2bf(v), f2bf(v1)), m.tag);
+        const float v = quad_tree64_pair_end(acc[0], acc[1]);  // row 2zp in lane 31, 2zp + 1 in lane 63
+        const float v0 = lane_value(v, 31), v1 = lane_value(v, 63);
+        if (m.lane == 0) word_store(Ly.x_proj + S::QKV / 2 + zp, pack_bf(f2bf(v0), f2bf(v1)), m.tag);
       }
     }
   }
@@ -1277,8 +1277,8 @@ __device__ __forceinline__ void phase_gate_up(const MegaArgs* pa, uint32_t tag, 
           quad_acc_f(ga, xl[j], xh[j], gv[r][j]);
           quad_acc_f(ua, xl[j], xh[j], uv[r][j]);
         }
-      const float t = quad_tree64_pair(ga, ua);  // gate total in lane 0, up total in lane 32
-      const float gb = rbf(t), ub = rbf(lane_value(t, 32));
+      const float t = quad_tree64_pair_end(ga, ua);  // gate total in lane 31, up total in lane 63
+      const float gb = rbf(lane_value(t, 31)), ub = rbf(lane_value(t, 63));
       y[r] = f2bf((silu(gb) * ub) * m.misc->probs[(2 * p + r) / S::I]);
     }
     if (m.lane == 0) word_store(Ly.x_active + p, pack_bf(y[0], y[1]), m.tag);
