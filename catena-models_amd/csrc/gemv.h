@@ -116,16 +116,17 @@ __device__ __forceinline__ float tree32_lanes(float v) {
 }
 
 // Two such trees at once: a's total in lane 0 of each half wave, b's in
-// lane 16. At stride 16, lanes 0-15 of a half keep a and receive a from
-// lanes 16-31, lanes 16-31 keep b and receive b from lanes 0-15 (one
-// permlane16 swap); strides 8 ... 1 then run inside each 16-lane row. Every
-// sum has the operands it has in tree32_lanes (a sum's operands commute), so
-// both totals are its bits.
+// lane 16. At stride 16 one permlane16 swap of a with b leaves a's two rows
+// side by side in rows 0 and 2 (the first result holds a's even rows, the
+// second a's odd rows there) and b's in rows 1 and 3, so one add gives a's
+// stride-16 sums in lanes 0-15 of a half and b's in lanes 16-31; strides
+// 8 ... 1 then run inside each 16-lane row. Every sum has the operands it
+// has in tree32_lanes (a sum's operands commute), so both totals are its
+// bits.
 __device__ __forceinline__ float tree32_pair(float a, float b) {
-  const bool low = (threadIdx.x & 16) == 0;
-  const int send = __builtin_bit_cast(int, low ? b : a);
-  const auto r = __builtin_amdgcn_permlane16_swap(send, send, false, false);
-  float v = (low ? a : b) + __builtin_bit_cast(float, low ? (int)r[1] : (int)r[0]);
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false,
+                                                  false);
+  float v = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
   v += lane_down<8>(v);
   v += lane_down<4>(v);
   v += lane_down<2>(v);
