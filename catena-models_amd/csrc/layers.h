@@ -390,10 +390,12 @@ __device__ __forceinline__ float staged_score(const uint16_t* __restrict__ krow,
   return acc;
 }
 
+// scored: the scores rbf(q . k * scale) are already in the scratch rows
+// (k_bstaged_scores); the block runs the softmax only.
 __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ cache, int64_t key_base,
     const uint64_t* __restrict__ params, int t, int kvs, int head_dim, int heads_per_kv, float scale,
-    float* __restrict__ scratch, int scratch_stride, const SessionRows* __restrict__ rows) {
+    float* __restrict__ scratch, int scratch_stride, const SessionRows* __restrict__ rows, bool scored) {
   __shared__ float partial[kStagedThreads];
   __shared__ float qf[256];
   __shared__ float nodes[kStagedLdsKeys / 64];
@@ -418,7 +420,7 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
     for (int j = 0; j < KPT; ++j) {
       const int64_t kk = tid + (int64_t)kStagedThreads * j;
       sc[j] = ninf;
-      if (kk < keys) sc[j] = rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
+      if (kk < keys) sc[j] = scored ? row[kk] : rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
     }
     float m = sc[0];
 #pragma unroll
@@ -467,8 +469,9 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
   // long contexts: scores and exponentials in the scratch row
   float* s = row;
   float* e = row + keys;
-  for (int64_t kk = tid; kk < keys; kk += kStagedThreads)
-    s[kk] = rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
+  if (!scored)
+    for (int64_t kk = tid; kk < keys; kk += kStagedThreads)
+      s[kk] = rbf(staged_score(cache + key_base + kk * kvs + off, qf, head_dim) * scale);
   __syncthreads();
   float m = ninf;
   for (int64_t kk = tid; kk < keys; kk += kStagedThreads) m = fmaxf(m, s[kk]);
@@ -487,6 +490,60 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
   }
   const float den = e[0];
   for (int64_t kk = tid; kk < keys; kk += kStagedThreads) pb[kk] = f2bf(hexp(s[kk] - maximum) / den);
+}
+
+// The batched dense step's scores for k_attention_staged<scored>: block
+// (256-key chunk, group of HPT query heads of one KV head, session), thread =
+// key. The thread reads its key row once and runs the group's HPT
+// staged_score chains side by side (each head's chain in staged_score's
+// scalar order), then stores rbf(score * scale) at scratch row head, column
+// key. One block per (query head, session) left most CUs idle and read each
+// key row once per query head.
+template <int HPT>
+__global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restrict__ q,
+                                                         const SessionRows* __restrict__ rows, int64_t key_base,
+                                                         int kvs, int head_dim, int q_heads, int heads_per_kv,
+                                                         float scale, float* __restrict__ scratch, int stride) {
+  __shared__ float qf[HPT][256];
+  const int tid = threadIdx.x, y = blockIdx.z;
+  const int groups = heads_per_kv / HPT;
+  const int kvh = blockIdx.y / groups, h0 = kvh * heads_per_kv + (blockIdx.y % groups) * HPT;
+  const int64_t keys = (int64_t)rows->position[y] + 1;
+  const int64_t k0 = (int64_t)blockIdx.x * 256;
+  if (k0 >= keys) return;  // block-uniform, before the barrier
+  q += (size_t)y * q_heads * head_dim + (size_t)h0 * head_dim;
+  for (int i = tid; i < HPT * head_dim; i += 256) qf[i / head_dim][i % head_dim] = bf2f(q[i]);
+  __syncthreads();
+  const int64_t kk = k0 + tid;
+  if (kk >= keys) return;
+  const u32x4* kr = reinterpret_cast<const u32x4*>(rows->cache[y] + key_base + kk * kvs + (int64_t)kvh * head_dim);
+  const int nq = head_dim >> 3;
+  float acc[HPT];
+#pragma unroll
+  for (int h = 0; h < HPT; ++h) acc[h] = 0.0f;
+  for (int i0 = 0; i0 < nq; i0 += 16) {
+    u32x4 w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = kr[min(i0 + i, nq - 1)];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i0 + i < nq) {
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) {
+          const float* qi = qf[h] + 8 * (i0 + i);
+          float a = acc[h];
+          a += qi[0] * lo2f(w[i].x); a += qi[1] * hi2f(w[i].x);
+          a += qi[2] * lo2f(w[i].y); a += qi[3] * hi2f(w[i].y);
+          a += qi[4] * lo2f(w[i].z); a += qi[5] * hi2f(w[i].z);
+          a += qi[6] * lo2f(w[i].w); a += qi[7] * hi2f(w[i].w);
+          acc[h] = a;
+        }
+      }
+    }
+  }
+  float* sc = scratch + (size_t)y * q_heads * stride;
+#pragma unroll
+  for (int h = 0; h < HPT; ++h) sc[(size_t)(h0 + h) * stride + kk] = rbf(acc[h] * scale);
 }
 
 // The context of k_attention_staged's probabilities: per channel eight

@@ -1310,7 +1310,8 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
       } else {
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kStagedThreads), 0,
           (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
-          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr);
+          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr,
+          false);
         L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(kContextThreads), 0,
           (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD,
           (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, (const float*)s->attn_scratch,
@@ -1557,7 +1558,8 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
             const int am = std::min(s->pf_attn_tokens, rows_n - a0);
             L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kStagedThreads), 0,
               (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
-              first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr);
+              first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr,
+              false);
             L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
               dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
               (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
@@ -2246,9 +2248,24 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
           (const float*)W(5), (const float*)W(6), (uint16_t*)nullptr, key_base, value_base,
           (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.Q, (int)d.HD, d.pad_hd, (int)d.R, c.eps, b->qr, rows);
       const float scale = 1.0f / sqrtf((float)d.HD);  // SCALE_BITS, qwen35.rs:701
+      // scores over (key chunk, head pair, session), then the softmax per
+      // (head, session); one query head per thread when hpk is odd
+      const int hpk = (int)(d.Q / d.KVH);
+      const bool scored = d.HD % 8 == 0 && d.HD <= 256;
+      if (scored) {
+        const unsigned chunks = (unsigned)((cap + 255) / 256);
+        if (hpk % 2 == 0)
+          k_bstaged_scores<2><<<dim3(chunks, (unsigned)(d.KVH * hpk / 2), (unsigned)B), dim3(256), 0, st>>>(
+              (const uint16_t*)b->qr, rows, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, b->scratch,
+              b->stride);
+        else
+          k_bstaged_scores<1><<<dim3(chunks, (unsigned)(d.KVH * hpk), (unsigned)B), dim3(256), 0, st>>>(
+              (const uint16_t*)b->qr, rows, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, b->scratch,
+              b->stride);
+      }
       k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kStagedThreads), 0, st>>>(
           (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
-          (int)d.HD, (int)(d.Q / d.KVH), scale, b->scratch, b->stride, rows);
+          (int)d.HD, hpk, scale, b->scratch, b->stride, rows, scored);
       k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(kContextThreads), 0, st>>>(
           (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
           (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
