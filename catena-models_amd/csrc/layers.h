@@ -640,6 +640,112 @@ __global__ __launch_bounds__(kContextThreads) void k_attention_context(
   }
 }
 
+// k_attention_context for the batched dense step with the KV head's HPB
+// query heads in one block: block (KV head, 16-channel chunk, session); the
+// value slice of each key staged once for all of them (with each head's
+// probabilities), thread t running head group t / 128's HPB / 2 heads (HPB
+// 1: threads < 128, one head) over chain r = (t / 16) % 8, channel t % 16.
+// Every head's chains, combining tree and rounding are k_attention_context's.
+template <int HPB>
+__global__ __launch_bounds__(kContextThreads) void k_battention_context(
+    int64_t value_base, int kvs, int head_dim, int heads, const uint16_t* __restrict__ qg,
+    const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out,
+    const SessionRows* __restrict__ rows) {
+  constexpr int G = HPB >= 2 ? 2 : 1, HPT = HPB / G;  // head groups, heads per thread
+  __shared__ __align__(16) uint16_t vs[2][kContextKeys][kContextChannels];
+  __shared__ __align__(16) uint32_t ps[2][HPB][kContextKeys / 2];
+  __shared__ float part[HPB][8][kContextChannels];
+  const int chunks = head_dim / kContextChannels;
+  const int kvh = blockIdx.x / chunks, c0 = (blockIdx.x - kvh * chunks) * kContextChannels;
+  const int y = blockIdx.y, tid = threadIdx.x;
+  const int hg = tid >> 7, r = (tid >> 4) & 7, x = tid & 15;
+  const bool active = hg < G;
+  const int h0 = kvh * HPB;  // the block's first query head
+  const size_t qs = (size_t)heads * head_dim;
+  qg += y * 2 * qs;
+  out += y * qs;
+  const int64_t keys = (int64_t)rows->position[y] + 1;
+  const uint16_t* cache = rows->cache[y];
+  const float* srow = scratch + (size_t)y * heads * scratch_stride + (size_t)h0 * scratch_stride + 2 * keys;
+  const uint16_t* vb = cache + value_base + (int64_t)kvh * head_dim + c0;
+  const int64_t steps = (keys + 7) >> 3;  // chain steps; keys [0, 8 steps) are visited
+  const int nchunks = (int)((8 * steps + kContextKeys - 1) / kContextKeys);
+  constexpr int VQ = 2 * kContextKeys;  // 16-byte halves of the channel slices
+  constexpr int PW = kContextKeys / 2;  // probability pairs per head
+  static_assert(VQ % kContextThreads == 0 && (HPB * PW) % kContextThreads == 0, "context staging");
+  constexpr int VPT = VQ / kContextThreads, PPT = HPB * PW / kContextThreads;
+  u32x4 vr[VPT];
+  uint32_t pr[PPT];
+  auto fetch = [&](int ch) {
+    const int64_t k0 = (int64_t)ch * kContextKeys;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = tid + kContextThreads * i;
+      const int64_t key = min(k0 + (idx >> 1), keys - 1);
+      vr[i] = *reinterpret_cast<const u32x4*>(vb + key * kvs + 8 * (idx & 1));
+    }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int idx = tid + kContextThreads * i, h = idx / PW, w = idx - h * PW;
+      const uint32_t* pb = reinterpret_cast<const uint32_t*>(srow + (size_t)h * scratch_stride);
+      pr[i] = pb[min(k0 / 2 + w, (keys - 1) / 2)];
+    }
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      const int idx = tid + kContextThreads * i;
+      reinterpret_cast<u32x4*>(&vs[buf][idx >> 1][0])[idx & 1] = vr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int idx = tid + kContextThreads * i, h = idx / PW, w = idx - h * PW;
+      ps[buf][h][w] = pr[i];
+    }
+  };
+  float acc[HPT];
+#pragma unroll
+  for (int j = 0; j < HPT; ++j) acc[j] = 0.0f;
+  fetch(0);
+  put(0);
+  __syncthreads();
+#pragma unroll 1
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int buf = ch & 1;
+    if (ch + 1 < nchunks) fetch(ch + 1);
+    if (active) {
+      const int64_t k0 = (int64_t)ch * kContextKeys;
+      const int n = (int)min<int64_t>(kContextKeys / 8, steps - k0 / 8);  // chain steps in the chunk
+#pragma unroll 4
+      for (int i = 0; i < n; ++i) {
+        const int local = 8 * i + r;
+        const float vv = bf2f(vs[buf][local][x]);
+        const bool live = k0 + local < keys;
+#pragma unroll
+        for (int j = 0; j < HPT; ++j) {
+          const float pv = bf2f(reinterpret_cast<const uint16_t*>(ps[buf][hg * HPT + j])[local]);
+          acc[j] = acc[j] + (live ? pv * vv : 0.0f);
+        }
+      }
+    }
+    if (ch + 1 < nchunks) put(buf ^ 1);
+    __syncthreads();
+  }
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < HPT; ++j) part[hg * HPT + j][r][x] = acc[j];
+  }
+  __syncthreads();
+  if (tid < HPB * kContextChannels) {
+    const int h = tid / kContextChannels, cx = tid - h * kContextChannels;
+    const int c = c0 + cx, head = h0 + h;
+    const float sum = ((part[h][0][cx] + part[h][4][cx]) + (part[h][2][cx] + part[h][6][cx])) +
+                      ((part[h][1][cx] + part[h][5][cx]) + (part[h][3][cx] + part[h][7][cx]));
+    const float gate = sigmoid(bf2f(qg[(size_t)head * 2 * head_dim + head_dim + c]));
+    out[head * head_dim + c] = f2bf(rbf(sum) * gate);
+  }
+}
+
 // BF16 cache state <-> F32 shadow for every layer (qwen35.hex:2-141).
 __global__ void k_import(const uint16_t* __restrict__ cache, int64_t base, int64_t layer_stride,
                          int64_t conv, int64_t rec, int layers, float* __restrict__ shadow) {

@@ -2266,9 +2266,19 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kStagedThreads), 0, st>>>(
           (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
           (int)d.HD, hpk, scale, b->scratch, b->stride, rows, scored);
-      k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(kContextThreads), 0, st>>>(
-          (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
-          (int)(d.Q / d.KVH), (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
+      // the context per (KV head, channel chunk, session): each value slice
+      // staged once for the KV head's query heads
+      const dim3 cgrid((unsigned)(d.KVH * d.HD / kContextChannels), (unsigned)B);
+      switch (hpk) {
+        case 1: k_battention_context<1><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 2: k_battention_context<2><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 4: k_battention_context<4><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 8: k_battention_context<8><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        default:
+          k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(kContextThreads), 0, st>>>(
+              (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
+              hpk, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows);
+      }
       ws64(st, b->ctx, B, W(4), d.H, d.QS, b->h, b->attn, mx ? b : nullptr);
       post_norm = W(7);
       ffn = 8;
