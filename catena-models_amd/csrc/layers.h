@@ -494,18 +494,22 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
 
 // The batched dense step's scores for k_attention_staged<scored>: block
 // (256-key chunk, group of HPT query heads of one KV head, session), thread =
-// key. The thread reads its key row once and runs the group's HPT
-// staged_score chains side by side (each head's chain in staged_score's
-// scalar order), then stores rbf(score * scale) at scratch row head, column
-// key. One block per (query head, session) left most CUs idle and read each
-// key row once per query head.
+// key. Each wave stages its 64 keys' rows in LDS half a row (16 quads) at a
+// time with whole-line loads (eight lanes per 128-byte line, quad i of key r
+// at position i ^ (r & 15)); each lane then runs the group's HPT
+// staged_score chains on its key side by side (each head's chain in
+// staged_score's scalar order) and stores rbf(score * scale) at scratch row
+// head, column key. One block per (query head, session) left most CUs idle
+// and read each key row once per query head; a lane loading its own row
+// fetched a 16-byte piece of 64 lines per instruction.
 template <int HPT>
 __global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restrict__ q,
                                                          const SessionRows* __restrict__ rows, int64_t key_base,
                                                          int kvs, int head_dim, int q_heads, int heads_per_kv,
                                                          float scale, float* __restrict__ scratch, int stride) {
   __shared__ float qf[HPT][256];
-  const int tid = threadIdx.x, y = blockIdx.z;
+  __shared__ __align__(16) u32x4 kst[4][64 * 16];  // per wave: 64 keys x 16 quads
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, y = blockIdx.z;
   const int groups = heads_per_kv / HPT;
   const int kvh = blockIdx.y / groups, h0 = kvh * heads_per_kv + (blockIdx.y % groups) * HPT;
   const int64_t keys = (int64_t)rows->position[y] + 1;
@@ -514,33 +518,55 @@ __global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restri
   q += (size_t)y * q_heads * head_dim + (size_t)h0 * head_dim;
   for (int i = tid; i < HPT * head_dim; i += 256) qf[i / head_dim][i % head_dim] = bf2f(q[i]);
   __syncthreads();
-  const int64_t kk = k0 + tid;
-  if (kk >= keys) return;
-  const u32x4* kr = reinterpret_cast<const u32x4*>(rows->cache[y] + key_base + kk * kvs + (int64_t)kvh * head_dim);
-  const int nq = head_dim >> 3;
+  const int64_t kw0 = k0 + 64 * wave;  // the wave's first key
+  if (kw0 >= keys) return;             // wave-uniform; no block barrier below
+  const uint16_t* kb = rows->cache[y] + key_base + (int64_t)kvh * head_dim;
+  u32x4* st = kst[wave];
+  const int nq = head_dim >> 3;  // quads per row, at most 32
+  const int lr = lane >> 3, lc = lane & 7;
   float acc[HPT];
 #pragma unroll
   for (int h = 0; h < HPT; ++h) acc[h] = 0.0f;
-  for (int i0 = 0; i0 < nq; i0 += 16) {
-    u32x4 w[16];
+  for (int q0 = 0; q0 < nq; q0 += 16) {
+    const int hq = min(16, nq - q0);
+    u32x4 v[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) w[i] = kr[min(i0 + i, nq - 1)];
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int key = 8 * m + lr, quad = 8 * p + lc;
+        const int64_t gk = min(kw0 + key, keys - 1);
+        v[2 * m + p] = quad < hq ? *reinterpret_cast<const u32x4*>(kb + gk * kvs + 8 * (q0 + quad))
+                                 : u32x4{0u, 0u, 0u, 0u};
+      }
+    __builtin_amdgcn_wave_barrier();  // the previous part's reads are done
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int key = 8 * m + lr, quad = 8 * p + lc;
+        st[key * 16 + (quad ^ (key & 15))] = v[2 * m + p];
+      }
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      if (i0 + i < nq) {
+      if (i < hq) {
+        const u32x4 w = st[lane * 16 + (i ^ (lane & 15))];
 #pragma unroll
         for (int h = 0; h < HPT; ++h) {
-          const float* qi = qf[h] + 8 * (i0 + i);
+          const float* qi = qf[h] + 8 * (q0 + i);
           float a = acc[h];
-          a += qi[0] * lo2f(w[i].x); a += qi[1] * hi2f(w[i].x);
-          a += qi[2] * lo2f(w[i].y); a += qi[3] * hi2f(w[i].y);
-          a += qi[4] * lo2f(w[i].z); a += qi[5] * hi2f(w[i].z);
-          a += qi[6] * lo2f(w[i].w); a += qi[7] * hi2f(w[i].w);
+          a += qi[0] * lo2f(w.x); a += qi[1] * hi2f(w.x);
+          a += qi[2] * lo2f(w.y); a += qi[3] * hi2f(w.y);
+          a += qi[4] * lo2f(w.z); a += qi[5] * hi2f(w.z);
+          a += qi[6] * lo2f(w.w); a += qi[7] * hi2f(w.w);
           acc[h] = a;
         }
       }
     }
   }
+  const int64_t kk = kw0 + lane;
+  if (kk >= keys) return;
   float* sc = scratch + (size_t)y * q_heads * stride;
 #pragma unroll
   for (int h = 0; h < HPT; ++h) sc[(size_t)(h0 + h) * stride + kk] = rbf(acc[h] * scale);
