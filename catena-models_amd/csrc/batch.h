@@ -192,6 +192,27 @@ __global__ __launch_bounds__(kBlock) void k_ws64(const uint16_t* __restrict__ x,
   for (int k0 = 0; k0 < cols; k0 += kBatchChunk) {
     const int ch = min(kBatchChunk, cols - k0), cq = ch >> 3, qb = k0 >> 3;
     u32x4 wv[NQ];
+    if (cq % (16 * NQ) == 0) {
+      // whole batches (every shipped width): no clamps or per-quad guards,
+      // the same quads in the same order
+      const u32x4* wq = reinterpret_cast<const u32x4*>(wr) + qb + q;
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) wv[j] = wq[16 * j];
+      stage_f32<NB>(xf, x, tokens, t0, cols, k0, ch);
+      for (int b = 0; b * 16 * NQ < cq; ++b) {
+        if (b > 0) {
+#pragma unroll
+          for (int j = 0; j < NQ; ++j) wv[j] = wq[16 * (NQ * b + j)];
+        }
+#pragma unroll
+        for (int j = 0; j < NQ; ++j) {
+          const int o = q + 16 * (NQ * b + j);
+#pragma unroll
+          for (int t = 0; t < NB; ++t) quad_acc_staged(acc[t], xf + t * ch, cq, o, wv[j]);
+        }
+      }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < NQ; ++j) wv[j] = ldq(wr, qb + min(q + 16 * j, cq - 1));
     stage_f32<NB>(xf, x, tokens, t0, cols, k0, ch);
