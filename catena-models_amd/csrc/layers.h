@@ -501,10 +501,14 @@ __global__ __launch_bounds__(kStagedThreads) void k_attention_staged(
 // staged_score's scalar order) and stores rbf(score * scale) at scratch row
 // head, column key. One block per (query head, session) left most CUs idle
 // and read each key row once per query head; a lane loading its own row
-// fetched a 16-byte piece of 64 lines per instruction.
+// fetched a 16-byte piece of 64 lines per instruction. Grid z: the sessions
+// of a batched step (rows), or the tokens t + z of a prompt call (rows null:
+// one cache, positions from params).
 template <int HPT>
 __global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restrict__ q,
-                                                         const SessionRows* __restrict__ rows, int64_t key_base,
+                                                         const SessionRows* __restrict__ rows,
+                                                         const uint16_t* __restrict__ cache,
+                                                         const uint64_t* __restrict__ params, int t, int64_t key_base,
                                                          int kvs, int head_dim, int q_heads, int heads_per_kv,
                                                          float scale, float* __restrict__ scratch, int stride) {
   __shared__ float qf[HPT][256];
@@ -512,7 +516,7 @@ __global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restri
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, y = blockIdx.z;
   const int groups = heads_per_kv / HPT;
   const int kvh = blockIdx.y / groups, h0 = kvh * heads_per_kv + (blockIdx.y % groups) * HPT;
-  const int64_t keys = (int64_t)rows->position[y] + 1;
+  const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
   const int64_t k0 = (int64_t)blockIdx.x * 256;
   if (k0 >= keys) return;  // block-uniform, before the barrier
   q += (size_t)y * q_heads * head_dim + (size_t)h0 * head_dim;
@@ -520,7 +524,7 @@ __global__ __launch_bounds__(256) void k_bstaged_scores(const uint16_t* __restri
   __syncthreads();
   const int64_t kw0 = k0 + 64 * wave;  // the wave's first key
   if (kw0 >= keys) return;             // wave-uniform; no block barrier below
-  const uint16_t* kb = rows->cache[y] + key_base + (int64_t)kvh * head_dim;
+  const uint16_t* kb = (rows ? rows->cache[y] : cache) + key_base + (int64_t)kvh * head_dim;
   u32x4* st = kst[wave];
   const int nq = head_dim >> 3;  // quads per row, at most 32
   const int lr = lane >> 3, lc = lane & 7;
@@ -672,11 +676,12 @@ __global__ __launch_bounds__(kContextThreads) void k_attention_context(
 // probabilities), thread t running head group t / 128's HPB / 2 heads (HPB
 // 1: threads < 128, one head) over chain r = (t / 16) % 8, channel t % 16.
 // Every head's chains, combining tree and rounding are k_attention_context's.
+// Grid y: sessions (rows) or the tokens t + y of a prompt call (rows null).
 template <int HPB>
 __global__ __launch_bounds__(kContextThreads) void k_battention_context(
-    int64_t value_base, int kvs, int head_dim, int heads, const uint16_t* __restrict__ qg,
-    const float* __restrict__ scratch, int scratch_stride, uint16_t* __restrict__ out,
-    const SessionRows* __restrict__ rows) {
+    const uint16_t* __restrict__ cache_in, const uint64_t* __restrict__ params, int t, int64_t value_base, int kvs,
+    int head_dim, int heads, const uint16_t* __restrict__ qg, const float* __restrict__ scratch, int scratch_stride,
+    uint16_t* __restrict__ out, const SessionRows* __restrict__ rows) {
   constexpr int G = HPB >= 2 ? 2 : 1, HPT = HPB / G;  // head groups, heads per thread
   __shared__ __align__(16) uint16_t vs[2][kContextKeys][kContextChannels];
   __shared__ __align__(16) uint32_t ps[2][HPB][kContextKeys / 2];
@@ -690,8 +695,8 @@ __global__ __launch_bounds__(kContextThreads) void k_battention_context(
   const size_t qs = (size_t)heads * head_dim;
   qg += y * 2 * qs;
   out += y * qs;
-  const int64_t keys = (int64_t)rows->position[y] + 1;
-  const uint16_t* cache = rows->cache[y];
+  const int64_t keys = (rows ? (int64_t)rows->position[y] : step_position(params, t + y)) + 1;
+  const uint16_t* cache = rows ? rows->cache[y] : cache_in;
   const float* srow = scratch + (size_t)y * heads * scratch_stride + (size_t)h0 * scratch_stride + 2 * keys;
   const uint16_t* vb = cache + value_base + (int64_t)kvh * head_dim + c0;
   const int64_t steps = (keys + 7) >> 3;  // chain steps; keys [0, 8 steps) are visited

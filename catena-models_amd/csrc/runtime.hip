@@ -1554,16 +1554,47 @@ void enqueue_prefill(cq35_session* s, int64_t n) {
         else if (ma && d.HD == 128) mattention(k_mattention<128>);
         else if (ma && d.HD == 64) mattention(k_mattention<64>);
         else {  // the exact staged kernels
+          // regrouped as in the batched step (scores per key chunk and head
+          // pair, the softmax, the context per KV head) where the shape
+          // allows: the same chains and rounding
+          const int hpk = (int)(d.Q / d.KVH);
+          const bool regroup = d.HD % 8 == 0 && d.HD <= 256 && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8);
+          const int64_t start = (int64_t)s->h_params[0];  // the call's first position
           for (int a0 = 0; a0 < rows_n; a0 += s->pf_attn_tokens) {
             const int am = std::min(s->pf_attn_tokens, rows_n - a0);
+            const uint16_t* qa = qr + (size_t)a0 * d.QS;
+            if (regroup) {
+              const unsigned chunks = (unsigned)((start + first + a0 + am + 255) / 256);  // keys of the last token
+              if (hpk % 2 == 0)
+                L(KC_ATTENTION, k_bstaged_scores<2>, dim3(chunks, (unsigned)(d.KVH * hpk / 2), (unsigned)am), dim3(256), 0,
+                  qa, (const SessionRows*)nullptr, (const uint16_t*)s->cache, params, first + a0, key_base, (int)d.KVS,
+                  (int)d.HD, (int)d.Q, hpk, scale, s->pf_scratch, s->attn_stride);
+              else
+                L(KC_ATTENTION, k_bstaged_scores<1>, dim3(chunks, (unsigned)(d.KVH * hpk), (unsigned)am), dim3(256), 0,
+                  qa, (const SessionRows*)nullptr, (const uint16_t*)s->cache, params, first + a0, key_base, (int)d.KVS,
+                  (int)d.HD, (int)d.Q, hpk, scale, s->pf_scratch, s->attn_stride);
+            }
             L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q, (unsigned)am), dim3(kStagedThreads), 0,
-              (const uint16_t*)(qr + (size_t)a0 * d.QS), (const uint16_t*)s->cache, key_base, params,
-              first + a0, (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr,
-              false);
-            L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
-              dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS, (int)d.HD,
-              (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)(qg + (size_t)a0 * 2 * d.QS),
-              (const float*)s->pf_scratch, s->attn_stride, ctx + (size_t)a0 * d.QS, (const SessionRows*)nullptr);
+              qa, (const uint16_t*)s->cache, key_base, params,
+              first + a0, (int)d.KVS, (int)d.HD, hpk, scale, s->pf_scratch, s->attn_stride, (const SessionRows*)nullptr,
+              regroup);
+            const uint16_t* qga = qg + (size_t)a0 * 2 * d.QS;
+            uint16_t* ca = ctx + (size_t)a0 * d.QS;
+            const dim3 cgrid((unsigned)(d.KVH * d.HD / kContextChannels), (unsigned)am);
+            auto grouped = [&](auto kernel) {
+              L(KC_ATTENTION, kernel, cgrid, dim3(kContextThreads), 0, (const uint16_t*)s->cache, params, first + a0,
+                value_base, (int)d.KVS, (int)d.HD, (int)d.Q, qga, (const float*)s->pf_scratch, s->attn_stride, ca,
+                (const SessionRows*)nullptr);
+            };
+            if (regroup && hpk == 1) grouped(k_battention_context<1>);
+            else if (regroup && hpk == 2) grouped(k_battention_context<2>);
+            else if (regroup && hpk == 4) grouped(k_battention_context<4>);
+            else if (regroup && hpk == 8) grouped(k_battention_context<8>);
+            else
+              L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)am),
+                dim3(kContextThreads), 0, (const uint16_t*)s->cache, value_base, params, first + a0, (int)d.KVS,
+                (int)d.HD, (int)d.Q, hpk, qga, (const float*)s->pf_scratch, s->attn_stride, ca,
+                (const SessionRows*)nullptr);
           }
         }
         residual_rows(ctx, (int)d.QS, W(4), s->pf_h, s->pf_attn);
@@ -2256,12 +2287,12 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
         const unsigned chunks = (unsigned)((cap + 255) / 256);
         if (hpk % 2 == 0)
           k_bstaged_scores<2><<<dim3(chunks, (unsigned)(d.KVH * hpk / 2), (unsigned)B), dim3(256), 0, st>>>(
-              (const uint16_t*)b->qr, rows, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, b->scratch,
-              b->stride);
+              (const uint16_t*)b->qr, rows, nullptr, nullptr, 0, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale,
+              b->scratch, b->stride);
         else
           k_bstaged_scores<1><<<dim3(chunks, (unsigned)(d.KVH * hpk), (unsigned)B), dim3(256), 0, st>>>(
-              (const uint16_t*)b->qr, rows, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, b->scratch,
-              b->stride);
+              (const uint16_t*)b->qr, rows, nullptr, nullptr, 0, key_base, (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale,
+              b->scratch, b->stride);
       }
       k_attention_staged<<<dim3((unsigned)d.Q, (unsigned)B), dim3(kStagedThreads), 0, st>>>(
           (const uint16_t*)b->qr, (const uint16_t*)nullptr, key_base, (const uint64_t*)nullptr, 0, (int)d.KVS,
@@ -2270,10 +2301,10 @@ void enqueue_batch(cq35_model* m, BatchWorkspace* b, int B, bool mx) {
       // staged once for the KV head's query heads
       const dim3 cgrid((unsigned)(d.KVH * d.HD / kContextChannels), (unsigned)B);
       switch (hpk) {
-        case 1: k_battention_context<1><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
-        case 2: k_battention_context<2><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
-        case 4: k_battention_context<4><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
-        case 8: k_battention_context<8><<<cgrid, dim3(kContextThreads), 0, st>>>(value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 1: k_battention_context<1><<<cgrid, dim3(kContextThreads), 0, st>>>(nullptr, nullptr, 0, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 2: k_battention_context<2><<<cgrid, dim3(kContextThreads), 0, st>>>(nullptr, nullptr, 0, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 4: k_battention_context<4><<<cgrid, dim3(kContextThreads), 0, st>>>(nullptr, nullptr, 0, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
+        case 8: k_battention_context<8><<<cgrid, dim3(kContextThreads), 0, st>>>(nullptr, nullptr, 0, value_base, (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)b->qg, (const float*)b->scratch, b->stride, b->ctx, rows); break;
         default:
           k_attention_context<<<dim3((unsigned)(d.Q * d.HD / kContextChannels), (unsigned)B), dim3(kContextThreads), 0, st>>>(
               (const uint16_t*)nullptr, value_base, (const uint64_t*)nullptr, 0, (int)d.KVS, (int)d.HD, (int)d.Q,
