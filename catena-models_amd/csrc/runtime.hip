@@ -1308,14 +1308,41 @@ void enqueue_token(cq35_session* s, int t, bool last, bool f32_state) {
           s->attn_stride, (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t,
           (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, s->split_keys, s->ctx);
       } else {
+        // regrouped (scores per key chunk and head pair, the softmax, the
+        // context per KV head) where the shape allows; the scores grid covers
+        // the capacity, since a captured graph replays at later positions
+        const int hpk = (int)(d.Q / d.KVH);
+        const bool regroup = d.HD % 8 == 0 && d.HD <= 256 && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8);
+        const uint64_t* params = (const uint64_t*)s->d_params;
+        if (regroup) {
+          const unsigned chunks = (unsigned)((cap + 255) / 256);
+          if (hpk % 2 == 0)
+            L(KC_ATTENTION, k_bstaged_scores<2>, dim3(chunks, (unsigned)(d.KVH * hpk / 2)), dim3(256), 0,
+              (const uint16_t*)s->qr, (const SessionRows*)nullptr, (const uint16_t*)s->cache, params, t, key_base,
+              (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, s->attn_scratch, s->attn_stride);
+          else
+            L(KC_ATTENTION, k_bstaged_scores<1>, dim3(chunks, (unsigned)(d.KVH * hpk)), dim3(256), 0,
+              (const uint16_t*)s->qr, (const SessionRows*)nullptr, (const uint16_t*)s->cache, params, t, key_base,
+              (int)d.KVS, (int)d.HD, (int)d.Q, hpk, scale, s->attn_scratch, s->attn_stride);
+        }
         L(KC_ATTENTION, k_attention_staged, dim3((unsigned)d.Q), dim3(kStagedThreads), 0,
-          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, (const uint64_t*)s->d_params, t,
-          (int)d.KVS, (int)d.HD, (int)(d.Q / d.KVH), scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr,
-          false);
-        L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(kContextThreads), 0,
-          (const uint16_t*)s->cache, value_base, (const uint64_t*)s->d_params, t, (int)d.KVS, (int)d.HD,
-          (int)d.Q, (int)(d.Q / d.KVH), (const uint16_t*)s->qg, (const float*)s->attn_scratch,
-          s->attn_stride, s->ctx, (const SessionRows*)nullptr);
+          (const uint16_t*)s->qr, (const uint16_t*)s->cache, key_base, params, t,
+          (int)d.KVS, (int)d.HD, hpk, scale, s->attn_scratch, s->attn_stride, (const SessionRows*)nullptr,
+          regroup);
+        const dim3 cgrid((unsigned)(d.KVH * d.HD / kContextChannels));
+        auto grouped = [&](auto kernel) {
+          L(KC_ATTENTION, kernel, cgrid, dim3(kContextThreads), 0, (const uint16_t*)s->cache, params, t, value_base,
+            (int)d.KVS, (int)d.HD, (int)d.Q, (const uint16_t*)s->qg, (const float*)s->attn_scratch, s->attn_stride,
+            s->ctx, (const SessionRows*)nullptr);
+        };
+        if (regroup && hpk == 1) grouped(k_battention_context<1>);
+        else if (regroup && hpk == 2) grouped(k_battention_context<2>);
+        else if (regroup && hpk == 4) grouped(k_battention_context<4>);
+        else if (regroup && hpk == 8) grouped(k_battention_context<8>);
+        else
+          L(KC_ATTENTION, k_attention_context, dim3((unsigned)(d.Q * d.HD / kContextChannels)), dim3(kContextThreads),
+            0, (const uint16_t*)s->cache, value_base, params, t, (int)d.KVS, (int)d.HD, (int)d.Q, hpk,
+            (const uint16_t*)s->qg, (const float*)s->attn_scratch, s->attn_stride, s->ctx, (const SessionRows*)nullptr);
       }
       residual(L, s->ctx, W(4), d.H, d.QS, s->h, s->attn);
       post_norm = (const float*)W(7);
