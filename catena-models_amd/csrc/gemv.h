@@ -173,13 +173,14 @@ __device__ __forceinline__ float quad_tree(const Quad& a) {
 // 31 and 63, and a row-15 broadcast adds them. Every sum has quad_tree<64>'s
 // operands (the two operands of a sum commute): the same bits in far fewer
 // instructions.
-__device__ __forceinline__ float quad_tree64_pair_end(const Quad& a, const Quad& b) {
+// The same tree over four values per lane held directly (the B256 order's
+// per-lane sums): a's total in lane 31, b's in lane 63.
+__device__ __forceinline__ float tree64_pair4_end(const float (&a)[4], const float (&b)[4]) {
   float v[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const int av = __builtin_bit_cast(int, a.lo[p] + a.hi[p]);
-    const int bv = __builtin_bit_cast(int, b.lo[p] + b.hi[p]);
-    const auto r = __builtin_amdgcn_permlane32_swap(av, bv, false, false);
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a[p]), __builtin_bit_cast(int, b[p]), false,
+                                                    false);
     v[p] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
   }
   float w[2];
@@ -204,6 +205,11 @@ __device__ __forceinline__ float quad_tree64_pair_end(const Quad& a, const Quad&
   // row_bcast:15 (lane 15 of each row to the next row; rows 1 and 3 are the
   // ones read)
   return s + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x142, 0xf, 0xf, true));
+}
+__device__ __forceinline__ float quad_tree64_pair_end(const Quad& a, const Quad& b) {
+  const float av[4] = {a.lo[0] + a.hi[0], a.lo[1] + a.hi[1], a.lo[2] + a.hi[2], a.lo[3] + a.hi[3]};
+  const float bv[4] = {b.lo[0] + b.hi[0], b.lo[1] + b.hi[1], b.lo[2] + b.hi[2], b.lo[3] + b.hi[3]};
+  return tree64_pair4_end(av, bv);
 }
 
 // The value lane `lane` holds, in every lane (a scalar read).

@@ -41,28 +41,10 @@ __device__ __forceinline__ float b256_tree(const float (&a)[4]) {
   return v0 + v1;
 }
 
-// Two trees at once: a's total valid in lane 0, b's in lane 32. At stride
-// 128 (physical 32) each half wave receives the other half's values of one
-// tree (lanes 0-31 keep a, lanes 32-63 keep b); strides 64 ... 4 then run
-// inside each half and 2, 1 inside the lane. Every sum has the operands it
-// has in b256_tree (the two operands of a sum commute), so both totals are
-// b256_tree's bits, in fewer instructions.
-__device__ __forceinline__ float half_swap(float v) {  // v of lane ^ 32 (permlane32 swap)
-  const int b = __builtin_bit_cast(int, v);
-  const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
-  return __builtin_bit_cast(float, (threadIdx.x & 32) ? (int)r[0] : (int)r[1]);
-}
+// Two B256 trees at once (tree64_pair4_end: every sum with b256_tree's
+// operands): a's total in lane 31, b's in lane 63.
 __device__ __forceinline__ float b256_tree2(const float (&a)[4], const float (&b)[4]) {
-  const bool low = (threadIdx.x & 32) == 0;
-  float v0, v1, v2, v3;
-  v0 = (low ? a[0] : b[0]) + half_swap(low ? b[0] : a[0]);
-  v1 = (low ? a[1] : b[1]) + half_swap(low ? b[1] : a[1]);
-  v2 = (low ? a[2] : b[2]) + half_swap(low ? b[2] : a[2]);
-  v3 = (low ? a[3] : b[3]) + half_swap(low ? b[3] : a[3]);
-  tree_levels<64, 16>(v0, v1, v2, v3);
-  v0 += v2;
-  v1 += v3;
-  return v0 + v1;
+  return tree64_pair4_end(a, b);
 }
 
 enum { kBPlain = 0, kBResidual = 1, kBGate = 2 };
@@ -126,14 +108,14 @@ __global__ __launch_bounds__(kBlock) void k_bproject(const uint16_t* __restrict_
     if (t0 + t >= n) break;  // wave-uniform
     if (kMode == kBGate) {
       const float both = b256_tree2(acc[0][t], acc2[kMode == kBGate ? t : 0]);
-      tot[0][t] = both;
-      tot2[t] = __shfl(both, 32, 64);
+      tot[0][t] = lane_value(both, 31);
+      tot2[t] = lane_value(both, 63);
     } else {
 #pragma unroll
       for (int k = 0; k + 1 < R; k += 2) {
         const float both = b256_tree2(acc[k][t], acc[k + 1][t]);
-        tot[k][t] = both;
-        tot[k + 1][t] = __shfl(both, 32, 64);
+        tot[k][t] = lane_value(both, 31);
+        tot[k + 1][t] = lane_value(both, 63);
       }
       if (R % 2) tot[R - 1][t] = b256_tree(acc[R - 1][t]);
     }
@@ -542,8 +524,8 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate(
     b256_acc(ag, xv, gq[qi]);
     b256_acc(au, xv, uq[qi]);
   }
-  const float g = b256_tree(ag);
-  const float u = b256_tree(au);
+  const float both = b256_tree2(ag, au);
+  const float g = lane_value(both, 31), u = lane_value(both, 63);
   if (lane == 0) {
     const float gb = rbf(g), ub = rbf(u);
     const float activated = silu(gb);
@@ -641,7 +623,7 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_gate_grouped(
           b256_acc(au, xv[j], uw[k][j]);
         }
       const float both = b256_tree2(ag, au);
-      const float g = __shfl(both, 0, 64), u = __shfl(both, 32, 64);
+      const float g = lane_value(both, 31), u = lane_value(both, 63);
       if (lane == (i & 63)) {
         pg[k] = g;
         pu[k] = u;
@@ -698,8 +680,8 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_down(
     b256_acc(ar, xa[qi], wr[ch]);
     if (qi < sq) b256_acc(as, xa[aq + qi], sw[qi]);
   }
-  const float routed = b256_tree(ar);
-  const float shared = b256_tree(as);
+  const float both = b256_tree2(ar, as);
+  const float routed = lane_value(both, 31), shared = lane_value(both, 63);
   if (lane == 0) {
     const size_t i = (size_t)t * hidden + o;
     out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(shared));
@@ -766,7 +748,7 @@ __global__ __launch_bounds__(kBlock) void k_bmoe_down_rows(
       if (lane + 64 * j < sq) b256_acc(as, xs[j], ws[j]);
     }
     const float both = b256_tree2(ar, as);
-    const float routed = both, shared = __shfl(both, 32, 64);
+    const float routed = lane_value(both, 31), shared = lane_value(both, 63);
     if (lane == 0) {
       const size_t i = (size_t)t * hidden + o;
       out[i] = bf_add(f2bf(routed + bf2f(res[i])), f2bf(shared));
